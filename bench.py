@@ -1,0 +1,224 @@
+"""Benchmark of the retrieval hot path on one MI355X.
+
+Workload (N=1M, D=768, K=10): the seeded episode corpus (4 IMAGE / 3 TEXT /
+3 AUDIO per 10-node episode, decay lambda 0.1/s, query time 600 s), NSN graph
+= intra-episode pairs + 8-NN, queries = IMAGE node embeddings resident in HBM.
+A step is one Q=1 query. Timed: K global queries (fused scan + decay + top-K
++ depth-2 BFS, fp32 corpus), K episode-scoped queries, K global queries over
+the fp16 corpus; each query is one C-ABI call whose host wall latency is taken
+inside the library (steady_clock), p99 = sorted[floor(0.99 (n-1))].
+
+One JSON line on stdout; progress on stderr.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "p99 query latency µs @N=1M D=768 K=10 (episode & global); HBM GB/s % peak"
+HBM_PEAK_GBS = 8000.0
+
+
+def log(*a):
+    print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+def pctl(v, p):
+    v = np.sort(np.asarray(v, np.float64))
+    return float(v[int(p * (len(v) - 1))]) if len(v) else 0.0
+
+
+def knn_gpu(emb: np.ndarray, k: int):
+    """8-NN of the corpus for the benchmark graph (setup, outside the timed region)."""
+    import torch
+    E = torch.from_numpy(emb).to("cuda:0")
+    n = E.shape[0]
+    out = np.empty((n, k), np.int32)
+    step = 2048
+    for s in range(0, n, step):
+        e = min(n, s + step)
+        S = E[s:e] @ E.T
+        r = torch.arange(e - s, device=S.device)
+        S[r, s + r] = -float("inf")
+        _, idx = torch.topk(S, k, dim=1)
+        out[s:e] = idx.to(torch.int32).cpu().numpy()
+        del S
+    del E
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return out
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10000)
+    ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--n", type=int, default=1_000_000)
+    ap.add_argument("--dim", type=int, default=768)
+    ap.add_argument("--seed", type=int, default=2026)
+    ap.add_argument("--query-seed", type=int, default=77)
+    ap.add_argument("--cpu-queries", type=int, default=40)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--profile-only", action="store_true", help="only the global fp32 pass (for rocprofv3)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py: this build measures one GPU; --gpus above 1 is not supported here "
+              "(the path would shard by node range, see DESIGN.md)", file=sys.stderr)
+        return 2
+
+    import torch
+    import mars_amd
+    from mars_amd import RetrievalConfig, RetrievalScope, corpus
+    from mars_amd._lib import RetrievalConfigC, check, lib
+
+    mars_amd.init(0)
+    N, D, K = args.n, args.dim, 10
+    t = time.time()
+    c = corpus.make_corpus(N, D, seed=args.seed)
+    log(f"corpus N={N} D={D} seed={args.seed}: {time.time() - t:.1f}s")
+    t = time.time()
+    knn = knn_gpu(c.embeddings, corpus.KNN_K) if N > 20000 else corpus.knn_cpu(c.embeddings, corpus.KNN_K)[0]
+    corpus.nsn_graph(c, knn)
+    log(f"NSN graph: {len(c.col_indices)} directed edges, avg degree {len(c.col_indices) / N:.1f}: "
+        f"{time.time() - t:.1f}s")
+    g = mars_amd.MemoryGraph(N, D, c.row_offsets, c.col_indices, c.embeddings, c.modalities, c.timestamps)
+    dg = mars_amd.upload_to_device(g)
+    mars_amd.upload_episode_ids(dg, c.episode_ids)
+    csr = mars_amd.build_episode_csr(c.episode_ids, N)
+    mars_amd.upload_episode_csr(dg, csr)
+    mars_amd.upload_fp16_embeddings(dg)
+    ctx = mars_amd.create_query_context(N, D, 64, flags=mars_amd.MARS_CTX_TIMING)
+
+    nq = args.steps + args.warmup
+    qnodes = corpus.pick_queries(c.modalities, nq, seed=args.query_seed)
+    dq = torch.from_numpy(c.embeddings[qnodes]).to("cuda:0").contiguous()
+    torch.cuda.synchronize()
+
+    gcfg = RetrievalConfig(top_k=K, bfs_max_hops=2, time_decay_lambda=corpus.DECAY_LAMBDA, bfs_score_decay=0.5)
+    off = csr.ep_csr_offsets
+
+    def ep_cfgs(nodes):
+        arr = (RetrievalConfigC * len(nodes))()
+        for i, node in enumerate(nodes):
+            ep = int(c.episode_ids[node])
+            arr[i] = RetrievalConfig(top_k=K, time_decay_lambda=corpus.DECAY_LAMBDA,
+                                     retrieval_scope=RetrievalScope.EpisodeScoped, query_episode_id=ep,
+                                     query_episode_member_begin=int(off[ep]),
+                                     query_episode_member_count=int(off[ep + 1] - off[ep])).to_c()
+        return arr
+
+    def run(first, count, cfgs, n_cfg):
+        lat = np.zeros(count, np.float64)
+        kern = np.zeros(count, np.float32)
+        bfs = np.zeros(count, np.float32)
+        nres = np.zeros(count, np.int32)
+        ptr = dq.data_ptr() + first * D * 4
+        torch.cuda.synchronize()
+        check(lib.mars_bench_queries(dg.handle, ctx.handle, C.c_void_p(ptr), D, count,
+                                     C.c_float(corpus.QUERY_TIME), cfgs, n_cfg, C.c_void_p(lat.ctypes.data),
+                                     C.c_void_p(kern.ctypes.data), C.c_void_p(bfs.ctypes.data),
+                                     C.c_void_p(nres.ctypes.data)), "mars_bench_queries")
+        torch.cuda.synchronize()
+        assert np.all(nres == K), "every query must return K results"
+        return lat, kern, bfs
+
+    W, S = args.warmup, args.steps
+    g1 = gcfg.to_c()
+    out = {}
+    # ---- global fp32
+    ctx.use_fp16 = False
+    run(0, W, C.pointer(g1), 1)
+    t0 = time.time()
+    lat_g, kern_g, bfs_g = run(W, S, C.pointer(g1), 1)
+    wall_g = time.time() - t0
+    log(f"global fp32: p50 {pctl(lat_g, .5):.1f} us p99 {pctl(lat_g, .99):.1f} us; scan kernel mean "
+        f"{kern_g.mean():.1f} us; finalize mean {bfs_g.mean():.1f} us; {S / wall_g:.0f} q/s")
+    bytes_f32 = N * D * 4 + 4 * N
+    if not args.profile_only:
+        # ---- episode-scoped
+        ec = ep_cfgs(qnodes)
+        run(0, W, ec, W) if W else None
+        ec_t = ep_cfgs(qnodes[W:W + S])
+        t0 = time.time()
+        lat_e, kern_e, _ = run(W, S, ec_t, S)
+        wall_e = time.time() - t0
+        log(f"episode: p50 {pctl(lat_e, .5):.1f} us p99 {pctl(lat_e, .99):.1f} us; kernel mean {kern_e.mean():.1f} us;"
+            f" {S / wall_e:.0f} q/s")
+        # ---- global fp16
+        ctx.use_fp16 = True
+        run(0, W, C.pointer(g1), 1)
+        t0 = time.time()
+        lat_h, kern_h, bfs_h = run(W, S, C.pointer(g1), 1)
+        wall_h = time.time() - t0
+        ctx.use_fp16 = False
+        bytes_f16 = N * D * 2 + 4 * N
+        log(f"global fp16: p50 {pctl(lat_h, .5):.1f} us p99 {pctl(lat_h, .99):.1f} us; scan kernel mean "
+            f"{kern_h.mean():.1f} us ({bytes_f16 / kern_h.mean() / 1e3:.0f} GB/s)")
+        out["episode"] = dict(p50_us=pctl(lat_e, .5), p99_us=pctl(lat_e, .99), qps=S / wall_e,
+                              kernel_mean_us=float(kern_e.mean()))
+        out["global_fp16"] = dict(p50_us=pctl(lat_h, .5), p99_us=pctl(lat_h, .99), qps=S / wall_h,
+                                  scan_kernel_mean_us=float(kern_h.mean()),
+                                  scan_gbs=bytes_f16 / float(kern_h.mean()) / 1e3,
+                                  scan_frac=bytes_f16 / float(kern_h.mean()) / 1e3 / HBM_PEAK_GBS)
+
+    achieved = bytes_f32 / float(kern_g.mean()) / 1e3       # GB/s
+    res = {
+        "metric": METRIC,
+        "value": round(pctl(lat_g, .99), 2),
+        "unit": "us",
+        "n_gpus": 1,
+        "steps": S,
+        "warmup": W,
+        "ms_per_step": round(float(lat_g.mean()) / 1e3, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "global Q=1 decay+top-K+depth-2 BFS over N=1M D=768 fp32, K=10 (episode-scoped and "
+                               "fp16 global reported alongside)",
+                   "num_nodes": N, "dim": D, "top_k": K, "bfs_hops": 2, "decay_lambda": corpus.DECAY_LAMBDA,
+                   "corpus_seed": args.seed, "query_seed": args.query_seed, "num_edges": int(len(c.col_indices))},
+        "global_fp32": dict(p50_us=pctl(lat_g, .5), p99_us=pctl(lat_g, .99), qps=S / wall_g,
+                            scan_kernel_mean_us=float(kern_g.mean()), finalize_kernel_mean_us=float(bfs_g.mean())),
+        **out,
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "k_scan<float,QF32<12>>", "bytes_per_launch": bytes_f32},
+    }
+
+    if not args.no_cpu and not args.profile_only:
+        import oracle
+        og = oracle.make_graph(c.embeddings, c.modalities, c.timestamps, c.row_offsets, c.col_indices)
+        ocfg = oracle.config(K, 2, corpus.DECAY_LAMBDA, 0.5)
+        cl = []
+        nc = min(args.cpu_queries, S)
+        for node in qnodes[W:W + nc]:
+            t0 = time.perf_counter()
+            oracle.query(og, c.embeddings[node], corpus.QUERY_TIME, ocfg)
+            cl.append((time.perf_counter() - t0) * 1e6)
+        res["cpu_baseline"] = {"value": round(pctl(cl, .99), 1), "unit": "us", "cores": oracle.lib.oracle_num_threads(),
+                               "kind": "port",
+                               "sample": f"first {nc} of the timed global queries (same corpus, graph and query "
+                                         f"vectors), fp64 C++ oracle with OpenMP over rows; p99 of {nc}",
+                               "p50_us": round(pctl(cl, .5), 1)}
+        log(f"cpu oracle ({res['cpu_baseline']['cores']} threads): p50 {pctl(cl, .5):.0f} us p99 {pctl(cl, .99):.0f} us")
+    mars_amd.destroy_query_context(ctx)
+    mars_amd.free_device(dg)
+    print(json.dumps(res), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,208 @@
+/*
+ * mars_amd.h — C ABI of the MI355X (gfx950) retrieval hot path.
+ *
+ * Plain C, plain pointers and sizes. Every entry point returns an int status
+ * (MARS_OK == 0, negative on error) and never exits the process; the text of
+ * the last error on the calling thread is available from mars_last_error().
+ *
+ * Object model (mirrors the reference's DeviceMemoryGraph / QueryContext split):
+ *   mars_graph  — device-resident corpus: embeddings (fp32, optional fp16 copy),
+ *                 timestamps, modalities, NSN CSR, optional episode ids / CSR.
+ *   mars_ctx    — per-thread query context: stream, scratch, pinned staging.
+ *                 One context serves one thread at a time (same contract as
+ *                 the reference's QueryContext).
+ *
+ * Reference interfaces replaced (paths relative to the MARS source tree):
+ *   include/memory_cuda.cuh:63-97    DeviceMemoryGraph, upload_to_device, free_device,
+ *                                    upload_episode_ids, upload_episode_csr,
+ *                                    upload_fp16_embeddings, free_fp16_embeddings
+ *   include/memory_cuda.cuh:100-137  QueryResult, RetrievalConfig, RetrievalStats
+ *   include/memory_cuda.cuh:141-231  query_memory, QueryContext, create_query_context,
+ *                                    destroy_query_context, query_memory_fast
+ *   include/memory_graph.h:70-81     HostEpisodeCSR, build_episode_csr, RetrievalScope
+ */
+#ifndef MARS_AMD_H
+#define MARS_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MARS_ABI_VERSION 1
+
+/* ---- status codes -------------------------------------------------------- */
+#define MARS_OK              0
+#define MARS_ERR_INVALID    -1   /* bad argument / inconsistent input          */
+#define MARS_ERR_HIP        -2   /* a HIP runtime call failed                  */
+#define MARS_ERR_NOMEM      -3   /* device or host allocation failed           */
+#define MARS_ERR_CAPACITY   -4   /* input larger than the object was sized for */
+#define MARS_ERR_UNSUPPORTED -5  /* valid request this build does not serve    */
+#define MARS_ERR_NODEVICE   -6   /* no usable gfx950 device                    */
+
+/* ---- modality tags (memory_graph.h:17-22) --------------------------------- */
+#define MARS_MOD_TEXT  0
+#define MARS_MOD_AUDIO 1
+#define MARS_MOD_IMAGE 2
+
+/* ---- retrieval scope (memory_graph.h:79-81, enum class RetrievalScope) ---- */
+#define MARS_SCOPE_GLOBAL          0
+#define MARS_SCOPE_EPISODE_SCOPED  1
+
+/* Result record, 16 bytes: same field order as QueryResult (memory_cuda.cuh:100-105). */
+typedef struct mars_query_result {
+    int32_t node_id;
+    float   score;
+    int32_t modality;
+    int32_t hops_from_seed;   /* 0 = seed, 1+ = reached by BFS */
+} mars_query_result;
+
+/* RetrievalConfig (memory_cuda.cuh:107-127) with bool / enum class as int32_t.
+ * Field order and defaults are the reference's; see mars_config_default(). */
+typedef struct mars_retrieval_config {
+    int32_t top_k;                     /* default 10                                 */
+    int32_t bfs_max_hops;              /* default 2                                  */
+    float   time_decay_lambda;         /* default 1e-8 (per second)                  */
+    float   bfs_score_decay;           /* default 0.5 (per-hop multiplier)           */
+    int32_t modality_filter;           /* default -1 (any)                           */
+    int32_t use_importance;            /* accepted, never read (as in the reference) */
+    int32_t max_results_returned;      /* default -1 (= K)                           */
+    int32_t retrieval_scope;           /* MARS_SCOPE_*                               */
+    int32_t query_episode_id;          /* default -1                                 */
+    int32_t query_episode_member_begin;
+    int32_t query_episode_member_count;
+    float   episode_same_boost;        /* default 0 (off)                            */
+} mars_retrieval_config;
+
+/* RetrievalStats (memory_cuda.cuh:129-137) plus fields the reference lacks. */
+typedef struct mars_stats {
+    float   gpu_ms_similarity;
+    float   gpu_ms_topk;
+    float   gpu_ms_bfs;
+    float   gpu_ms_rerank;
+    float   gpu_ms_total;
+    int32_t nodes_scanned;
+    int32_t bfs_waves;          /* reference semantics: cfg.bfs_max_hops (global), 0 (scoped) */
+    /* extensions */
+    int32_t scope_fallback;     /* 1 if EpisodeScoped was requested but inactive -> Global */
+    int32_t visited;            /* number of nodes reached (seeds + BFS)                  */
+    int32_t bfs_levels_run;     /* BFS levels actually expanded                           */
+    int32_t used_fp16;          /* 1 if the fp16 corpus was scanned                       */
+    double  wall_us;            /* host wall time of the call                             */
+} mars_stats;
+
+/* Graph descriptor for mars_graph_create. Pointers are host memory unless
+ * flags has MARS_DESC_DEVICE_POINTERS, in which case the graph adopts copies
+ * made device-to-device (the caller keeps ownership of its buffers). */
+#define MARS_DESC_DEVICE_POINTERS 0x1u
+typedef struct mars_graph_desc {
+    int32_t        num_nodes;
+    int32_t        num_edges;        /* length of col_indices (both directions) */
+    int32_t        embedding_dim;
+    const int32_t* row_offsets;      /* num_nodes + 1 (may be NULL if num_edges == 0) */
+    const int32_t* col_indices;      /* num_edges; no duplicate id inside a row       */
+    const float*   embeddings;       /* num_nodes * embedding_dim, row-major, unit L2 */
+    const int32_t* modalities;       /* num_nodes                                     */
+    const float*   timestamps;       /* num_nodes (seconds)                           */
+    int32_t        capacity_nodes;   /* >= num_nodes; room for streaming append (0 = num_nodes) */
+    int64_t        capacity_edges;   /* >= num_edges (0 = num_edges + growth default)           */
+    uint32_t       flags;
+} mars_graph_desc;
+
+typedef struct mars_graph mars_graph;
+typedef struct mars_ctx   mars_ctx;
+
+/* Read-only view of a graph's device arrays (DeviceMemoryGraph fields). */
+typedef struct mars_graph_view {
+    int32_t  num_nodes;
+    int32_t  num_edges;
+    int32_t  embedding_dim;
+    int32_t  episode_num_episodes;
+    int32_t  episode_csr_member_total;
+    int32_t  has_fp16;
+    void*    d_row_offsets;
+    void*    d_col_indices;
+    void*    d_embeddings;
+    void*    d_embeddings_fp16;
+    void*    d_modalities;
+    void*    d_timestamps;
+    void*    d_episode_ids;
+    void*    d_ep_csr_offsets;
+    void*    d_ep_csr_members;
+} mars_graph_view;
+
+/* ---- library ------------------------------------------------------------- */
+const char* mars_last_error(void);
+int         mars_abi_version(void);
+/* Initialise HIP on `device`; fails with MARS_ERR_NODEVICE if it is not gfx950. */
+int         mars_init(int32_t device);
+void        mars_config_default(mars_retrieval_config* cfg);
+
+/* ---- graph (memory_cuda.cuh:87-97) ------------------------------------------ */
+/* upload_to_device */
+int mars_graph_create(const mars_graph_desc* desc, mars_graph** out);
+/* free_device */
+int mars_graph_destroy(mars_graph* g);
+/* upload_episode_ids: n must equal num_nodes; NULL/n<=0 clears (reference: silent no-op). */
+int mars_graph_set_episode_ids(mars_graph* g, const int32_t* episode_ids, int32_t n);
+/* upload_episode_csr: offsets has num_episodes+1 entries, members has offsets[num_episodes]. */
+int mars_graph_set_episode_csr(mars_graph* g, int32_t num_episodes,
+                               const int32_t* offsets, const int32_t* members,
+                               int32_t member_total);
+/* upload_fp16_embeddings / free_fp16_embeddings (RNE fp32->fp16, 64-bit indexing). */
+int mars_graph_enable_fp16(mars_graph* g);
+int mars_graph_disable_fp16(mars_graph* g);
+int mars_graph_get_view(const mars_graph* g, mars_graph_view* out);
+/* Copy device arrays back to host (any pointer may be NULL to skip). */
+int mars_graph_download(const mars_graph* g, int32_t* row_offsets, int32_t* col_indices,
+                        int32_t* ep_offsets, int32_t* ep_members);
+
+/* ---- query context (memory_cuda.cuh:141-231) --------------------------------- */
+#define MARS_CTX_USE_FP16    0x1u   /* scan the fp16 copy when present (ctx.use_fp16)      */
+#define MARS_CTX_USE_GRAPH   0x2u   /* replay the query pipeline as a hipGraph             */
+#define MARS_CTX_TIMING      0x4u   /* fill per-stage gpu_ms_* with hipEvents              */
+/* create_query_context(max_nodes, embedding_dim, max_k): max_k clamps to 64. */
+int mars_ctx_create(int32_t max_nodes, int32_t embedding_dim, int32_t max_k,
+                    uint32_t flags, mars_ctx** out);
+int mars_ctx_destroy(mars_ctx* ctx);
+int mars_ctx_set_flags(mars_ctx* ctx, uint32_t flags);
+int mars_ctx_get_flags(const mars_ctx* ctx, uint32_t* flags);
+
+/* query_memory_fast: one query from a host vector (embedding_dim floats).
+ * Writes min(cap, n) results sorted by (score desc, node_id asc) and sets
+ * *n_out = n, the number of results the query produced (n <= cap is the
+ * caller's check). stats may be NULL. */
+int mars_query(const mars_graph* g, mars_ctx* ctx, const float* h_query, float t_q,
+               const mars_retrieval_config* cfg, mars_query_result* out, int32_t cap,
+               int32_t* n_out, mars_stats* stats);
+/* Same, with the query vector already in device memory (d_query: embedding_dim floats). */
+int mars_query_device(const mars_graph* g, mars_ctx* ctx, const float* d_query, float t_q,
+                      const mars_retrieval_config* cfg, mars_query_result* out,
+                      int32_t cap, int32_t* n_out, mars_stats* stats);
+
+/* Debug / parity hooks: copy the last query's per-node fp32 scores (N floats) and
+ * its seed list (top-K ids and scores, K entries) to host memory. */
+int mars_ctx_last_scores(mars_ctx* ctx, float* h_scores, int64_t n);
+int mars_ctx_last_seeds(mars_ctx* ctx, int32_t* h_idx, float* h_val, int32_t k, int32_t* k_out);
+/* The last global query's visit list in discovery order (seeds first, then BFS
+ * level by level): node ids, hop levels and BFS scores; *n_out = nodes visited. */
+int mars_ctx_last_visited(mars_ctx* ctx, int32_t* h_ids, int32_t* h_hops, float* h_scores,
+                          int32_t cap, int32_t* n_out);
+
+/* ---- benchmark loop (harness semantics of src/latency_bench.cu:355-393) ------------ */
+/* Runs n single queries back to back, query i reading the device vector
+ * d_queries + i*stride with configuration cfgs[n_cfg == 1 ? 0 : i]. lat_us[i]
+ * receives the host wall latency of the whole call (steady_clock, measured here,
+ * not through any binding layer); with MARS_CTX_TIMING set, kern_us[i] (may be NULL)
+ * receives the GPU time of the scan / episode kernel and bfs_us[i] (may be NULL)
+ * that of the finalize kernel. n_res[i] (may be NULL) gets the result count. */
+int mars_bench_queries(const mars_graph* g, mars_ctx* ctx, const float* d_queries, int64_t stride,
+                       int32_t n, float t_q, const mars_retrieval_config* cfgs, int32_t n_cfg,
+                       double* lat_us, float* kern_us, float* bfs_us, int32_t* n_res);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MARS_AMD_H */

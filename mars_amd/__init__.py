@@ -1,0 +1,326 @@
+"""mars_amd — MI355X (gfx950) retrieval hot path of MARS behind a C ABI.
+
+Python mirror of the reference's query API (include/memory_cuda.cuh and
+include/memory_graph.h of MARS), calling libmars_amd.so through ctypes:
+
+    dg  = upload_to_device(graph)                  # memory_cuda.cuh:87
+    upload_episode_ids(dg, episode_ids)            # :89-91
+    upload_episode_csr(dg, build_episode_csr(ids, n))   # :92-93, memory_graph.h:77-78
+    upload_fp16_embeddings(dg)                     # :96
+    ctx = create_query_context(n, 768, max_k=64)   # :212-213
+    res = query_memory_fast(dg, ctx, q, t, cfg, stats)  # :216-222
+    destroy_query_context(ctx); free_device(dg)
+
+Every query runs the HIP kernels of libmars_amd.so; there is no CPU path.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import enum
+from dataclasses import dataclass, field
+from typing import List, Optional
+
+import numpy as np
+
+from . import _lib
+from ._lib import (MARS_CTX_TIMING, MARS_CTX_USE_FP16, MARS_CTX_USE_GRAPH, MARS_DESC_DEVICE_POINTERS,
+                   MarsError, check, lib)
+
+__all__ = [
+    "Modality", "RetrievalScope", "RetrievalConfig", "RetrievalStats", "QueryResult", "MemoryGraph",
+    "HostEpisodeCSR", "DeviceMemoryGraph", "QueryContext", "build_episode_csr", "upload_to_device",
+    "upload_episode_ids", "upload_episode_csr", "upload_fp16_embeddings", "free_fp16_embeddings",
+    "free_device", "create_query_context", "destroy_query_context", "query_memory_fast",
+    "query_memory_fast_device", "init", "MarsError", "corpus",
+]
+
+MOD_TEXT, MOD_AUDIO, MOD_IMAGE = 0, 1, 2
+
+
+class Modality(enum.IntEnum):                      # memory_graph.h:17-22
+    TEXT = 0
+    AUDIO = 1
+    IMAGE = 2
+
+
+class RetrievalScope(enum.IntEnum):                # memory_graph.h:79-81
+    Global = 0
+    EpisodeScoped = 1
+
+
+@dataclass
+class RetrievalConfig:                             # memory_cuda.cuh:107-127 (same defaults)
+    top_k: int = 10
+    bfs_max_hops: int = 2
+    time_decay_lambda: float = 1e-8
+    bfs_score_decay: float = 0.5
+    modality_filter: int = -1
+    use_importance: bool = False
+    max_results_returned: int = -1
+    retrieval_scope: RetrievalScope = RetrievalScope.Global
+    query_episode_id: int = -1
+    query_episode_member_begin: int = 0
+    query_episode_member_count: int = 0
+    episode_same_boost: float = 0.0
+
+    def to_c(self) -> _lib.RetrievalConfigC:
+        return _lib.RetrievalConfigC(
+            int(self.top_k), int(self.bfs_max_hops), float(self.time_decay_lambda),
+            float(self.bfs_score_decay), int(self.modality_filter), int(bool(self.use_importance)),
+            int(self.max_results_returned), int(self.retrieval_scope), int(self.query_episode_id),
+            int(self.query_episode_member_begin), int(self.query_episode_member_count),
+            float(self.episode_same_boost))
+
+
+@dataclass
+class RetrievalStats:                              # memory_cuda.cuh:129-137 (+ extensions)
+    gpu_ms_similarity: float = 0.0
+    gpu_ms_topk: float = 0.0
+    gpu_ms_bfs: float = 0.0
+    gpu_ms_rerank: float = 0.0
+    gpu_ms_total: float = 0.0
+    nodes_scanned: int = 0
+    bfs_waves: int = 0
+    scope_fallback: int = 0
+    visited: int = 0
+    bfs_levels_run: int = 0
+    used_fp16: int = 0
+    wall_us: float = 0.0
+
+    def _fill(self, s: _lib.StatsC) -> None:
+        for name, _ in _lib.StatsC._fields_:
+            setattr(self, name, getattr(s, name))
+
+
+@dataclass(frozen=True)
+class QueryResult:                                 # memory_cuda.cuh:100-105
+    node_id: int
+    score: float
+    modality: int
+    hops_from_seed: int
+
+
+@dataclass
+class MemoryGraph:                                 # memory_graph.h:25-60 (host arrays)
+    num_nodes: int
+    embedding_dim: int
+    row_offsets: np.ndarray
+    col_indices: np.ndarray
+    embeddings: np.ndarray
+    modalities: np.ndarray
+    timestamps: np.ndarray
+
+    @property
+    def num_edges(self) -> int:
+        return int(len(self.col_indices))
+
+
+@dataclass
+class HostEpisodeCSR:                              # memory_graph.h:70-75
+    num_episodes: int = 0
+    ep_csr_offsets: np.ndarray = field(default_factory=lambda: np.zeros(0, np.int32))
+    ep_csr_members: np.ndarray = field(default_factory=lambda: np.zeros(0, np.int32))
+
+
+def _ptr(a: Optional[np.ndarray]):
+    return None if a is None else C.c_void_p(a.ctypes.data)
+
+
+def _i32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.int32)
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def init(device: int = 0) -> None:
+    check(lib.mars_init(device), "mars_init")
+
+
+def build_episode_csr(episode_ids, num_nodes: int) -> HostEpisodeCSR:
+    """memory_graph.cpp:12-44 — counting sort of node ids by episode id."""
+    ids = _i32(episode_ids)
+    if num_nodes <= 0 or len(ids) != num_nodes:
+        return HostEpisodeCSR()
+    ne = C.c_int32(0)
+    check(lib.mars_build_episode_csr(_ptr(ids), num_nodes, C.byref(ne), None, None), "build_episode_csr")
+    off = np.zeros(ne.value + 1, np.int32)
+    mem = np.zeros(num_nodes, np.int32)
+    check(lib.mars_build_episode_csr(_ptr(ids), num_nodes, C.byref(ne), _ptr(off), _ptr(mem)),
+          "build_episode_csr")
+    return HostEpisodeCSR(ne.value, off, mem)
+
+
+class DeviceMemoryGraph:
+    """Handle of a device-resident graph (memory_cuda.cuh:63-85)."""
+
+    def __init__(self, handle: C.c_void_p, num_nodes: int, num_edges: int, dim: int):
+        self.handle = handle
+        self.num_nodes = num_nodes
+        self.num_edges = num_edges
+        self.embedding_dim = dim
+
+    def view(self) -> _lib.GraphViewC:
+        v = _lib.GraphViewC()
+        check(lib.mars_graph_get_view(self.handle, C.byref(v)), "mars_graph_get_view")
+        return v
+
+    @property
+    def episode_num_episodes(self) -> int:
+        return self.view().episode_num_episodes
+
+    @property
+    def episode_csr_member_total(self) -> int:
+        return self.view().episode_csr_member_total
+
+    def download_csr(self):
+        row = np.zeros(self.num_nodes + 1, np.int32)
+        col = np.zeros(max(self.num_edges, 1), np.int32)
+        check(lib.mars_graph_download(self.handle, _ptr(row), _ptr(col), None, None), "mars_graph_download")
+        return row, col[: self.num_edges]
+
+    def download_episode_csr(self):
+        v = self.view()
+        off = np.zeros(v.episode_num_episodes + 1, np.int32)
+        mem = np.zeros(max(v.episode_csr_member_total, 1), np.int32)
+        check(lib.mars_graph_download(self.handle, None, None, _ptr(off), _ptr(mem)), "mars_graph_download")
+        return off, mem[: v.episode_csr_member_total]
+
+
+def upload_to_device(g: MemoryGraph, capacity_nodes: int = 0, capacity_edges: int = 0) -> DeviceMemoryGraph:
+    """upload_to_device (memory_cuda.cu:776-799)."""
+    emb = _f32(g.embeddings).reshape(-1)
+    mods, ts = _i32(g.modalities), _f32(g.timestamps)
+    row = _i32(g.row_offsets) if g.row_offsets is not None else None
+    col = _i32(g.col_indices) if g.col_indices is not None else None
+    ne = 0 if col is None else int(len(col))
+    desc = _lib.GraphDescC(int(g.num_nodes), ne, int(g.embedding_dim), _ptr(row).value if row is not None else None,
+                           _ptr(col).value if col is not None and ne else None, emb.ctypes.data, mods.ctypes.data,
+                           ts.ctypes.data, int(capacity_nodes), int(capacity_edges), 0)
+    h = C.c_void_p()
+    check(lib.mars_graph_create(C.byref(desc), C.byref(h)), "upload_to_device")
+    return DeviceMemoryGraph(h, int(g.num_nodes), ne, int(g.embedding_dim))
+
+
+def upload_episode_ids(dg: DeviceMemoryGraph, episode_ids) -> None:
+    ids = _i32(episode_ids)
+    check(lib.mars_graph_set_episode_ids(dg.handle, _ptr(ids), len(ids)), "upload_episode_ids")
+
+
+def upload_episode_csr(dg: DeviceMemoryGraph, csr: HostEpisodeCSR) -> None:
+    off, mem = _i32(csr.ep_csr_offsets), _i32(csr.ep_csr_members)
+    tail = int(off[csr.num_episodes]) if csr.num_episodes > 0 else 0
+    check(lib.mars_graph_set_episode_csr(dg.handle, int(csr.num_episodes), _ptr(off), _ptr(mem), tail),
+          "upload_episode_csr")
+
+
+def upload_fp16_embeddings(dg: DeviceMemoryGraph) -> None:
+    check(lib.mars_graph_enable_fp16(dg.handle), "upload_fp16_embeddings")
+
+
+def free_fp16_embeddings(dg: DeviceMemoryGraph) -> None:
+    check(lib.mars_graph_disable_fp16(dg.handle), "free_fp16_embeddings")
+
+
+def free_device(dg: DeviceMemoryGraph) -> None:
+    if dg.handle:
+        check(lib.mars_graph_destroy(dg.handle), "free_device")
+        dg.handle = C.c_void_p()
+
+
+class QueryContext:
+    """Pre-allocated query context (memory_cuda.cuh:141-209): one per thread."""
+
+    def __init__(self, handle: C.c_void_p, max_nodes: int, dim: int, max_k: int):
+        self.handle = handle
+        self.max_nodes = max_nodes
+        self.embedding_dim = dim
+        self.max_k = min(max_k, 64)
+        self._out = (_lib.QueryResultC * 8192)()
+
+    def _flag(self, bit: int) -> bool:
+        f = C.c_uint32()
+        check(lib.mars_ctx_get_flags(self.handle, C.byref(f)), "mars_ctx_get_flags")
+        return bool(f.value & bit)
+
+    def _set(self, bit: int, on: bool) -> None:
+        f = C.c_uint32()
+        check(lib.mars_ctx_get_flags(self.handle, C.byref(f)), "mars_ctx_get_flags")
+        v = (f.value | bit) if on else (f.value & ~bit)
+        check(lib.mars_ctx_set_flags(self.handle, v), "mars_ctx_set_flags")
+
+    use_fp16 = property(lambda s: s._flag(MARS_CTX_USE_FP16), lambda s, v: s._set(MARS_CTX_USE_FP16, v))
+    use_cuda_graph = property(lambda s: s._flag(MARS_CTX_USE_GRAPH), lambda s, v: s._set(MARS_CTX_USE_GRAPH, v))
+    timing = property(lambda s: s._flag(MARS_CTX_TIMING), lambda s, v: s._set(MARS_CTX_TIMING, v))
+
+    def last_scores(self, n: int) -> np.ndarray:
+        out = np.zeros(n, np.float32)
+        check(lib.mars_ctx_last_scores(self.handle, _ptr(out), n), "mars_ctx_last_scores")
+        return out
+
+    def last_seeds(self):
+        idx = np.zeros(64, np.int32)
+        val = np.zeros(64, np.float32)
+        k = C.c_int32()
+        check(lib.mars_ctx_last_seeds(self.handle, _ptr(idx), _ptr(val), 64, C.byref(k)), "mars_ctx_last_seeds")
+        return idx[: k.value].copy(), val[: k.value].copy()
+
+    def last_visited(self):
+        n = C.c_int32()
+        check(lib.mars_ctx_last_visited(self.handle, None, None, None, 0, C.byref(n)), "mars_ctx_last_visited")
+        ids = np.zeros(max(n.value, 1), np.int32)
+        hops = np.zeros(max(n.value, 1), np.int32)
+        sc = np.zeros(max(n.value, 1), np.float32)
+        check(lib.mars_ctx_last_visited(self.handle, _ptr(ids), _ptr(hops), _ptr(sc), n.value, C.byref(n)),
+              "mars_ctx_last_visited")
+        return ids[: n.value], hops[: n.value], sc[: n.value]
+
+
+def create_query_context(max_nodes: int, embedding_dim: int, max_k: int = 64, flags: int = MARS_CTX_TIMING) -> QueryContext:
+    h = C.c_void_p()
+    check(lib.mars_ctx_create(max_nodes, embedding_dim, max_k, flags, C.byref(h)), "create_query_context")
+    return QueryContext(h, max_nodes, embedding_dim, max_k)
+
+
+def destroy_query_context(ctx: QueryContext) -> None:
+    if ctx.handle:
+        check(lib.mars_ctx_destroy(ctx.handle), "destroy_query_context")
+        ctx.handle = C.c_void_p()
+
+
+def _results(ctx: QueryContext, n: int) -> List[QueryResult]:
+    o = ctx._out
+    return [QueryResult(o[i].node_id, o[i].score, o[i].modality, o[i].hops_from_seed) for i in range(min(n, 8192))]
+
+
+def query_memory_fast(dg: DeviceMemoryGraph, ctx: QueryContext, h_query, query_timestamp: float,
+                      cfg: RetrievalConfig, stats: Optional[RetrievalStats] = None) -> List[QueryResult]:
+    """query_memory_fast (memory_cuda.cu:1351-1464): results sorted by (score desc, id asc)."""
+    q = _f32(h_query)
+    if q.size != dg.embedding_dim:
+        raise ValueError(f"query has {q.size} values, graph dim is {dg.embedding_dim}")
+    n = C.c_int32()
+    st = _lib.StatsC()
+    c = cfg.to_c()
+    check(lib.mars_query(dg.handle, ctx.handle, _ptr(q), float(query_timestamp), C.byref(c), ctx._out, 8192,
+                         C.byref(n), C.byref(st)), "query_memory_fast")
+    if stats is not None:
+        stats._fill(st)
+    return _results(ctx, n.value)
+
+
+def query_memory_fast_device(dg: DeviceMemoryGraph, ctx: QueryContext, d_query_ptr: int, query_timestamp: float,
+                             cfg: RetrievalConfig, stats: Optional[RetrievalStats] = None) -> List[QueryResult]:
+    """Same as query_memory_fast with the query vector already in device memory."""
+    n = C.c_int32()
+    st = _lib.StatsC()
+    c = cfg.to_c()
+    check(lib.mars_query_device(dg.handle, ctx.handle, C.c_void_p(d_query_ptr), float(query_timestamp),
+                                C.byref(c), ctx._out, 8192, C.byref(n), C.byref(st)), "query_memory_fast_device")
+    if stats is not None:
+        stats._fill(st)
+    return _results(ctx, n.value)
+
+
+from . import corpus  # noqa: E402  (needs lib)

@@ -1,0 +1,94 @@
+"""Seeded benchmark corpus (include/mars_corpus.h) as numpy arrays.
+
+``make_corpus(n, dim, seed)`` returns embeddings, modalities, timestamps and
+episode ids; ``nsn_graph`` adds the NSN CSR (intra-episode pairs + k-NN,
+symmetrised); ``pick_queries`` draws IMAGE query nodes.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+from typing import Optional
+
+import numpy as np
+
+from ._lib import CorpusParamsC, check, lib
+
+QUERY_TIME = 600.0          # seconds: every timestamp of the corpus is <= 600
+DECAY_LAMBDA = 0.1          # per second
+KNN_K = 8
+
+
+@dataclass
+class Corpus:
+    embeddings: np.ndarray   # (n, dim) float32, unit rows
+    modalities: np.ndarray   # (n,) int32
+    timestamps: np.ndarray   # (n,) float32
+    episode_ids: np.ndarray  # (n,) int32
+    seed: int
+    row_offsets: Optional[np.ndarray] = None
+    col_indices: Optional[np.ndarray] = None
+
+    @property
+    def num_nodes(self) -> int:
+        return int(self.embeddings.shape[0])
+
+    @property
+    def dim(self) -> int:
+        return int(self.embeddings.shape[1])
+
+
+def _p(a: np.ndarray):
+    return C.c_void_p(a.ctypes.data)
+
+
+def make_corpus(n: int, dim: int = 768, seed: int = 2026, threads: int = 0, embeddings: bool = True) -> Corpus:
+    p = CorpusParamsC()
+    lib.mars_corpus_default(C.byref(p), int(n), int(dim), int(seed))
+    emb = np.empty((n, dim) if embeddings else (0, dim), np.float32)
+    mods = np.empty(n, np.int32)
+    ts = np.empty(n, np.float32)
+    ep = np.empty(n, np.int32)
+    check(lib.mars_corpus_generate(C.byref(p), _p(emb) if embeddings else None, _p(mods), _p(ts), _p(ep),
+                                   int(threads)), "mars_corpus_generate")
+    return Corpus(emb, mods, ts, ep, seed)
+
+
+def knn_cpu(emb: np.ndarray, k: int = KNN_K, threads: int = 0):
+    emb = np.ascontiguousarray(emb, np.float32)
+    n, d = emb.shape
+    nb = np.empty((n, k), np.int32)
+    sims = np.empty((n, k), np.float32)
+    check(lib.mars_knn_cpu(_p(emb), n, d, k, _p(nb), _p(sims), int(threads)), "mars_knn_cpu")
+    return nb, sims
+
+
+def build_nsn_csr(episode_ids: np.ndarray, knn: np.ndarray, threads: int = 0):
+    ep = np.ascontiguousarray(episode_ids, np.int32)
+    knn = np.ascontiguousarray(knn, np.int32)
+    n = len(ep)
+    k = knn.shape[1] if knn.ndim == 2 else 0
+    row = np.empty(n + 1, np.int32)
+    ne = C.c_int64()
+    check(lib.mars_build_nsn_csr(n, _p(ep), _p(knn), k, _p(row), None, C.byref(ne), int(threads)),
+          "mars_build_nsn_csr")
+    col = np.empty(max(ne.value, 1), np.int32)
+    check(lib.mars_build_nsn_csr(n, _p(ep), _p(knn), k, _p(row), _p(col), C.byref(ne), int(threads)),
+          "mars_build_nsn_csr")
+    return row, col[: ne.value]
+
+
+def nsn_graph(c: Corpus, knn: Optional[np.ndarray] = None, threads: int = 0) -> Corpus:
+    """Attach the NSN CSR: intra-episode pairs + k-NN (CPU exact k-NN unless given)."""
+    if knn is None:
+        knn, _ = knn_cpu(c.embeddings, KNN_K, threads)
+    c.row_offsets, c.col_indices = build_nsn_csr(c.episode_ids, knn, threads)
+    return c
+
+
+def pick_queries(modalities: np.ndarray, n_queries: int, seed: int, modality: int = 2) -> np.ndarray:
+    mods = np.ascontiguousarray(modalities, np.int32)
+    out = np.empty(n_queries, np.int32)
+    check(lib.mars_corpus_pick_queries(_p(mods), len(mods), modality, n_queries, int(seed), _p(out)),
+          "mars_corpus_pick_queries")
+    return out

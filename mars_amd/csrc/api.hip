@@ -1,0 +1,549 @@
+// ============================================================================
+//  api.hip — C ABI of libmars_amd: graph residency, query contexts and the
+//  query pipeline (declared in include/mars_amd.h).
+//
+//  Global query:   [H2D q] -> k_scan (fused score + per-workgroup top-K)
+//                          -> k_finalize (seeds, BFS, sorted results -> pinned host)
+//  Episode query:  [H2D q] -> k_episode (member range only -> pinned host)
+//  One stream synchronisation per query and no device->host copy: the last
+//  kernel writes the result records into mapped pinned memory.
+// ============================================================================
+#include "internal.hpp"
+
+#include <algorithm>
+#include <chrono>
+#include <cstdarg>
+#include <cstring>
+#include <vector>
+
+struct mars_graph { mars::Graph g; };
+struct mars_ctx { mars::Ctx c; };
+
+namespace mars {
+
+namespace {
+thread_local char g_err[1024] = "";
+constexpr int32_t kMaxWg = 4096;     // upper bound of scan workgroups (partials buffer)
+constexpr int32_t kTargetWg = 2048;  // scan workgroups aimed for (8 per CU on 256 CUs)
+
+int ensure_device(int* dev) {
+    int d = 0;
+    MARS_HIP(hipGetDevice(&d));
+    hipDeviceProp_t prop;
+    MARS_HIP(hipGetDeviceProperties(&prop, d));
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return set_error(MARS_ERR_NODEVICE, "device %d is %s, this build targets gfx950 only", d,
+                         prop.gcnArchName);
+    if (dev) *dev = d;
+    return MARS_OK;
+}
+
+int use_device(int dev) {
+    int cur = -1;
+    MARS_HIP(hipGetDevice(&cur));
+    if (cur != dev) MARS_HIP(hipSetDevice(dev));
+    return MARS_OK;
+}
+
+template <typename T>
+int dmalloc(T** p, size_t count) {
+    *p = nullptr;
+    if (count == 0) count = 1;
+    hipError_t e = hipMalloc(reinterpret_cast<void**>(p), count * sizeof(T));
+    if (e != hipSuccess)
+        return set_error(MARS_ERR_NOMEM, "hipMalloc(%zu bytes): %s", count * sizeof(T), hipGetErrorString(e));
+    return MARS_OK;
+}
+
+template <typename T>
+void dfree(T*& p) {
+    if (p) (void)hipFree(p);
+    p = nullptr;
+}
+
+#define MARS_TRY(expr)                  \
+    do {                                \
+        int rc__ = (expr);              \
+        if (rc__ != MARS_OK) return rc__; \
+    } while (0)
+
+// CSR checks done on host input: offsets start at 0, non-decreasing, end at E;
+// neighbour ids in range; no id twice in one row (the BFS claim relies on it).
+int validate_csr(int32_t n, int32_t e, const int32_t* row, const int32_t* col) {
+    if (e == 0 && row == nullptr) return MARS_OK;
+    MARS_CHECK(row != nullptr && (e == 0 || col != nullptr), MARS_ERR_INVALID,
+               "row_offsets/col_indices missing");
+    MARS_CHECK(row[0] == 0, MARS_ERR_INVALID, "row_offsets[0] = %d, expected 0", row[0]);
+    MARS_CHECK(row[n] == e, MARS_ERR_INVALID, "row_offsets[N] = %d, expected num_edges %d", row[n], e);
+    std::vector<int32_t> tmp;
+    for (int32_t i = 0; i < n; ++i) {
+        const int32_t b = row[i], t = row[i + 1];
+        MARS_CHECK(b <= t, MARS_ERR_INVALID, "row_offsets decrease at row %d", i);
+        bool ascending = true;
+        for (int32_t j = b; j < t; ++j) {
+            MARS_CHECK(col[j] >= 0 && col[j] < n, MARS_ERR_INVALID, "col_indices[%d] = %d out of range", j,
+                       col[j]);
+            if (j > b && col[j] <= col[j - 1]) ascending = false;
+        }
+        if (!ascending) {
+            tmp.assign(col + b, col + t);
+            std::sort(tmp.begin(), tmp.end());
+            MARS_CHECK(std::adjacent_find(tmp.begin(), tmp.end()) == tmp.end(), MARS_ERR_INVALID,
+                       "row %d lists a neighbour twice", i);
+        }
+    }
+    return MARS_OK;
+}
+
+bool episode_scoped_active(const Graph& g, const mars_retrieval_config& c) {
+    // memory_cuda.cu:1163-1171
+    return c.retrieval_scope == MARS_SCOPE_EPISODE_SCOPED && g.ep_off != nullptr && g.ep_mem != nullptr &&
+           c.query_episode_id >= 0 && c.query_episode_id < g.num_eps && c.query_episode_member_count > 0 &&
+           c.query_episode_member_begin >= 0 &&
+           int64_t(c.query_episode_member_begin) + c.query_episode_member_count <= g.member_total;
+}
+
+}  // namespace
+
+int set_error(int code, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    std::vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+namespace {
+
+int graph_free(Graph& g) {
+    (void)use_device(g.device);
+    dfree(g.emb); dfree(g.emb16); dfree(g.mods); dfree(g.ts); dfree(g.row); dfree(g.col);
+    dfree(g.ep_ids); dfree(g.ep_off); dfree(g.ep_mem);
+    g = Graph{};
+    return MARS_OK;
+}
+
+int ctx_free(Ctx& c) {
+    (void)use_device(c.device);
+    if (c.stream) (void)hipStreamSynchronize(c.stream);
+    dfree(c.query); dfree(c.fin); dfree(c.part); dfree(c.vis); dfree(c.claim); dfree(c.vlist);
+    dfree(c.vhop); dfree(c.vscore); dfree(c.sortbuf); dfree(c.seed_idx); dfree(c.seed_val);
+    if (c.h_query) (void)hipHostFree(c.h_query);
+    if (c.h_res) (void)hipHostFree(c.h_res);
+    for (auto& e : c.ev) if (e) (void)hipEventDestroy(e);
+    if (c.stream) (void)hipStreamDestroy(c.stream);
+    c = Ctx{};
+    return MARS_OK;
+}
+
+int query_impl(const mars_graph* gh, mars_ctx* ch, const float* h_q, const float* d_q, float t_q,
+               const mars_retrieval_config* cfg, mars_query_result* out, int32_t cap, int32_t* n_out,
+               mars_stats* stats) {
+    const auto t0 = std::chrono::steady_clock::now();
+    MARS_CHECK(gh && ch && cfg && n_out && (h_q || d_q), MARS_ERR_INVALID, "null argument");
+    MARS_CHECK(cap >= 0 && (cap == 0 || out), MARS_ERR_INVALID, "bad output buffer");
+    const Graph& g = gh->g;
+    Ctx& c = ch->c;
+    MARS_CHECK(g.d == c.d, MARS_ERR_INVALID, "graph dim %d != context dim %d", g.d, c.d);
+    MARS_CHECK(g.n <= c.max_nodes, MARS_ERR_CAPACITY, "graph has %d nodes, context sized for %d", g.n,
+               c.max_nodes);
+    MARS_CHECK(g.n > 0, MARS_ERR_INVALID, "empty graph");
+    MARS_CHECK(cfg->top_k > 0, MARS_ERR_INVALID, "top_k = %d", cfg->top_k);
+    const int32_t K = std::min(cfg->top_k, c.max_k);                      // memory_cuda.cu:1361
+    const bool scoped = episode_scoped_active(g, *cfg);
+    const int32_t hops = scoped ? 0 : std::max(0, cfg->bfs_max_hops);     // :1189
+    const int32_t rcap = cfg->max_results_returned > 0 ? cfg->max_results_returned : K;
+    MARS_CHECK(rcap <= c.res_cap, MARS_ERR_UNSUPPORTED, "max_results_returned %d exceeds %d", rcap,
+               c.res_cap);
+    MARS_TRY(use_device(c.device));
+    hipStream_t s = c.stream;
+    const bool timing = (c.flags & MARS_CTX_TIMING) != 0;
+    const bool fp16 = !scoped && (c.flags & MARS_CTX_USE_FP16) && g.emb16 != nullptr;
+
+    const float* q = d_q;
+    if (!q) {
+        std::memcpy(c.h_query, h_q, size_t(g.d) * sizeof(float));
+        MARS_HIP(hipMemcpyAsync(c.query, c.h_query, size_t(g.d) * sizeof(float), hipMemcpyHostToDevice, s));
+        q = c.query;
+    }
+    if (timing) MARS_HIP(hipEventRecord(c.ev[0], s));
+    if (scoped) {
+        EpisodeArgs a{};
+        a.emb = g.emb; a.d = g.d; a.n = g.n; a.q = q; a.ts = g.ts; a.mods = g.mods;
+        a.members = g.ep_mem + cfg->query_episode_member_begin;
+        a.m = cfg->query_episode_member_count;
+        a.t_q = t_q; a.lambda = cfg->time_decay_lambda; a.mod_filter = cfg->modality_filter;
+        a.k = K; a.rcap = rcap; a.keybuf = c.sortbuf;
+        a.seed_idx = c.seed_idx; a.seed_val = c.seed_val; a.res = c.d_res; a.rec = c.d_rec;
+        MARS_TRY(launch_episode(a, s));
+        if (timing) MARS_HIP(hipEventRecord(c.ev[1], s));
+    } else {
+        int32_t rpw = 0, nwg = 0;
+        scan_grid(g.n, kTargetWg, &rpw, &nwg);
+        ScanArgs a{};
+        a.emb = fp16 ? static_cast<const void*>(g.emb16) : static_cast<const void*>(g.emb);
+        a.fp16 = fp16 ? 1 : 0; a.n = g.n; a.d = g.d; a.q = q; a.ts = g.ts; a.mods = g.mods;
+        a.ep_ids = g.ep_ids; a.t_q = t_q; a.lambda = cfg->time_decay_lambda;
+        a.mod_filter = cfg->modality_filter; a.query_ep = cfg->query_episode_id;
+        a.boost = (g.ep_ids && cfg->query_episode_id >= 0) ? cfg->episode_same_boost : 0.0f;
+        a.k = K; a.fin = c.fin; a.part = c.part; a.rows_per_wg = rpw; a.num_wg = nwg;
+        MARS_TRY(launch_scan(a, s));
+        if (timing) MARS_HIP(hipEventRecord(c.ev[1], s));
+        // visit stamps / claim generations: no O(N) reset per query
+        if (c.epoch == 0xFFFFFFFFu) {
+            MARS_HIP(hipMemsetAsync(c.vis, 0, size_t(c.max_nodes) * sizeof(uint32_t), s));
+            c.epoch = 0;
+        }
+        const uint32_t epoch = ++c.epoch;
+        const uint32_t span = uint32_t(std::max(hops, 1));
+        if (uint64_t(c.gen) + span >= 0xFFFFFFF0ull) {
+            MARS_HIP(hipMemsetAsync(c.claim, 0xFF, size_t(c.max_nodes) * sizeof(uint64_t), s));
+            c.gen = 0;
+        }
+        const uint32_t gen_base = c.gen;
+        c.gen += span;
+        FinalizeArgs f{};
+        f.part = c.part; f.n_part = nwg * K; f.k = K; f.row = g.row; f.col = g.col; f.fin = c.fin;
+        f.mods = g.mods; f.hops = hops; f.hop_decay = cfg->bfs_score_decay; f.epoch = epoch;
+        f.gen_base = gen_base; f.vis = c.vis; f.claim = c.claim; f.vlist = c.vlist; f.vhop = c.vhop;
+        f.vscore = c.vscore; f.sortbuf = c.sortbuf; f.cap_visit = c.max_nodes; f.rcap = rcap;
+        f.seed_idx = c.seed_idx; f.seed_val = c.seed_val; f.res = c.d_res; f.rec = c.d_rec;
+        MARS_TRY(launch_finalize(f, s));
+        c.last_n = g.n;
+    }
+    if (timing) MARS_HIP(hipEventRecord(c.ev[2], s));
+    MARS_HIP(hipStreamSynchronize(s));
+    const ResultHeader h = *c.h_res;
+    const int32_t nw = std::min(h.count, cap);
+    if (nw > 0) std::memcpy(out, c.h_rec, size_t(nw) * sizeof(mars_query_result));
+    *n_out = h.count;
+    c.last_k = h.n_seeds;
+    c.last_visited = scoped ? 0 : h.visited;
+    if (stats) {
+        mars_stats st{};
+        if (timing) {
+            float ms = 0.0f;
+            MARS_HIP(hipEventElapsedTime(&ms, c.ev[0], c.ev[1]));
+            st.gpu_ms_similarity = ms;
+            MARS_HIP(hipEventElapsedTime(&ms, c.ev[1], c.ev[2]));
+            st.gpu_ms_bfs = ms;
+            MARS_HIP(hipEventElapsedTime(&ms, c.ev[0], c.ev[2]));
+            st.gpu_ms_total = ms;
+        }
+        // rerank / top-K are fused into the scan: their time is inside gpu_ms_similarity
+        st.nodes_scanned = scoped ? cfg->query_episode_member_count : g.n;
+        st.bfs_waves = scoped ? 0 : cfg->bfs_max_hops;                     // :1680-1686 semantics
+        st.scope_fallback = (cfg->retrieval_scope == MARS_SCOPE_EPISODE_SCOPED && !scoped) ? 1 : 0;
+        st.visited = h.visited;
+        st.bfs_levels_run = h.levels;
+        st.used_fp16 = fp16 ? 1 : 0;
+        st.wall_us = std::chrono::duration<double, std::micro>(std::chrono::steady_clock::now() - t0).count();
+        *stats = st;
+    }
+    return MARS_OK;
+}
+
+}  // namespace
+}  // namespace mars
+
+using namespace mars;
+
+extern "C" {
+
+const char* mars_last_error(void) { return g_err; }
+int mars_abi_version(void) { return MARS_ABI_VERSION; }
+
+int mars_init(int32_t device) {
+    int count = 0;
+    hipError_t e = hipGetDeviceCount(&count);
+    if (e != hipSuccess || count <= 0) return set_error(MARS_ERR_NODEVICE, "no HIP device");
+    MARS_CHECK(device >= 0 && device < count, MARS_ERR_INVALID, "device %d of %d", device, count);
+    MARS_HIP(hipSetDevice(device));
+    return ensure_device(nullptr);
+}
+
+void mars_config_default(mars_retrieval_config* c) {
+    // RetrievalConfig defaults, memory_cuda.cuh:107-127
+    c->top_k = 10;
+    c->bfs_max_hops = 2;
+    c->time_decay_lambda = 1e-8f;
+    c->bfs_score_decay = 0.5f;
+    c->modality_filter = -1;
+    c->use_importance = 0;
+    c->max_results_returned = -1;
+    c->retrieval_scope = MARS_SCOPE_GLOBAL;
+    c->query_episode_id = -1;
+    c->query_episode_member_begin = 0;
+    c->query_episode_member_count = 0;
+    c->episode_same_boost = 0.0f;
+}
+
+int mars_graph_create(const mars_graph_desc* d, mars_graph** out) {
+    MARS_CHECK(d && out, MARS_ERR_INVALID, "null argument");
+    *out = nullptr;
+    MARS_CHECK(d->num_nodes > 0 && d->embedding_dim > 0 && d->num_edges >= 0, MARS_ERR_INVALID,
+               "num_nodes %d, embedding_dim %d, num_edges %d", d->num_nodes, d->embedding_dim, d->num_edges);
+    MARS_CHECK(d->embeddings && d->modalities && d->timestamps, MARS_ERR_INVALID,
+               "embeddings, modalities and timestamps are required");
+    const bool dev = (d->flags & MARS_DESC_DEVICE_POINTERS) != 0;
+    if (!dev) MARS_TRY(validate_csr(d->num_nodes, d->num_edges, d->row_offsets, d->col_indices));
+    else MARS_CHECK(d->num_edges == 0 || (d->row_offsets && d->col_indices), MARS_ERR_INVALID, "CSR missing");
+    int devid = 0;
+    MARS_TRY(ensure_device(&devid));
+    auto* gh = new mars_graph();
+    Graph& g = gh->g;
+    g.device = devid;
+    g.n = d->num_nodes; g.e = d->num_edges; g.d = d->embedding_dim;
+    g.cap_n = std::max(d->capacity_nodes, d->num_nodes);
+    g.cap_e = std::max<int64_t>(d->capacity_edges, d->num_edges);
+    const size_t N = size_t(g.n), D = size_t(g.d), CN = size_t(g.cap_n);
+    int rc = MARS_OK;
+    auto fail = [&](int r) { graph_free(g); delete gh; return r; };
+    if ((rc = dmalloc(&g.emb, CN * D)) || (rc = dmalloc(&g.mods, CN)) || (rc = dmalloc(&g.ts, CN)) ||
+        (rc = dmalloc(&g.row, CN + 1)) || (rc = dmalloc(&g.col, size_t(g.cap_e))))
+        return fail(rc);
+    const hipMemcpyKind kind = dev ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice;
+    hipError_t e = hipSuccess;
+    if (e == hipSuccess) e = hipMemcpy(g.emb, d->embeddings, N * D * sizeof(float), kind);
+    if (e == hipSuccess) e = hipMemcpy(g.mods, d->modalities, N * sizeof(int32_t), kind);
+    if (e == hipSuccess) e = hipMemcpy(g.ts, d->timestamps, N * sizeof(float), kind);
+    if (e == hipSuccess) {
+        if (d->row_offsets) e = hipMemcpy(g.row, d->row_offsets, (N + 1) * sizeof(int32_t), kind);
+        else e = hipMemset(g.row, 0, (N + 1) * sizeof(int32_t));
+    }
+    if (e == hipSuccess && g.e > 0) e = hipMemcpy(g.col, d->col_indices, size_t(g.e) * sizeof(int32_t), kind);
+    if (e != hipSuccess) return fail(set_error(MARS_ERR_HIP, "graph upload: %s", hipGetErrorString(e)));
+    *out = gh;
+    return MARS_OK;
+}
+
+int mars_graph_destroy(mars_graph* gh) {
+    if (!gh) return MARS_OK;
+    graph_free(gh->g);
+    delete gh;
+    return MARS_OK;
+}
+
+int mars_graph_set_episode_ids(mars_graph* gh, const int32_t* ids, int32_t n) {
+    MARS_CHECK(gh, MARS_ERR_INVALID, "null graph");
+    Graph& g = gh->g;
+    MARS_TRY(use_device(g.device));
+    dfree(g.ep_ids);                                      // memory_cuda.cu:814-826
+    if (!ids || n <= 0) return MARS_OK;                   // cleared
+    MARS_CHECK(n == g.n, MARS_ERR_INVALID, "episode ids: %d entries for %d nodes", n, g.n);
+    MARS_TRY(dmalloc(&g.ep_ids, size_t(g.cap_n)));
+    MARS_HIP(hipMemcpy(g.ep_ids, ids, size_t(n) * sizeof(int32_t), hipMemcpyHostToDevice));
+    return MARS_OK;
+}
+
+int mars_graph_set_episode_csr(mars_graph* gh, int32_t num_eps, const int32_t* off, const int32_t* mem,
+                               int32_t member_total) {
+    MARS_CHECK(gh, MARS_ERR_INVALID, "null graph");
+    Graph& g = gh->g;
+    MARS_TRY(use_device(g.device));
+    dfree(g.ep_off); dfree(g.ep_mem);                     // memory_cuda.cu:828-855
+    g.num_eps = 0;
+    g.member_total = 0;
+    if (num_eps <= 0) return MARS_OK;
+    MARS_CHECK(off && (member_total == 0 || mem), MARS_ERR_INVALID, "episode CSR arrays missing");
+    MARS_CHECK(off[num_eps] == member_total && member_total >= 0, MARS_ERR_INVALID,
+               "episode CSR tail %d != member_total %d", off[num_eps], member_total);
+    MARS_CHECK(off[0] == 0, MARS_ERR_INVALID, "episode CSR offsets[0] = %d", off[0]);
+    for (int32_t e = 0; e < num_eps; ++e)
+        MARS_CHECK(off[e] <= off[e + 1], MARS_ERR_INVALID, "episode CSR offsets decrease at %d", e);
+    for (int32_t j = 0; j < member_total; ++j)
+        MARS_CHECK(mem[j] >= 0 && mem[j] < g.n, MARS_ERR_INVALID, "episode member %d = %d out of range", j,
+                   mem[j]);
+    MARS_TRY(dmalloc(&g.ep_off, size_t(num_eps) + 1));
+    MARS_TRY(dmalloc(&g.ep_mem, size_t(std::max(member_total, g.cap_n))));
+    MARS_HIP(hipMemcpy(g.ep_off, off, (size_t(num_eps) + 1) * sizeof(int32_t), hipMemcpyHostToDevice));
+    if (member_total > 0)
+        MARS_HIP(hipMemcpy(g.ep_mem, mem, size_t(member_total) * sizeof(int32_t), hipMemcpyHostToDevice));
+    g.num_eps = num_eps;
+    g.member_total = member_total;
+    return MARS_OK;
+}
+
+int mars_graph_enable_fp16(mars_graph* gh) {
+    MARS_CHECK(gh, MARS_ERR_INVALID, "null graph");
+    Graph& g = gh->g;
+    MARS_TRY(use_device(g.device));
+    if (!g.emb16) MARS_TRY(dmalloc(&g.emb16, size_t(g.cap_n) * size_t(g.d)));
+    MARS_TRY(launch_convert_f16(g.emb, g.emb16, int64_t(g.n) * g.d, nullptr));
+    MARS_HIP(hipStreamSynchronize(nullptr));
+    return MARS_OK;
+}
+
+int mars_graph_disable_fp16(mars_graph* gh) {
+    MARS_CHECK(gh, MARS_ERR_INVALID, "null graph");
+    MARS_TRY(use_device(gh->g.device));
+    dfree(gh->g.emb16);
+    return MARS_OK;
+}
+
+int mars_graph_get_view(const mars_graph* gh, mars_graph_view* v) {
+    MARS_CHECK(gh && v, MARS_ERR_INVALID, "null argument");
+    const Graph& g = gh->g;
+    v->num_nodes = g.n; v->num_edges = g.e; v->embedding_dim = g.d;
+    v->episode_num_episodes = g.num_eps; v->episode_csr_member_total = g.member_total;
+    v->has_fp16 = g.emb16 ? 1 : 0;
+    v->d_row_offsets = g.row; v->d_col_indices = g.col; v->d_embeddings = g.emb;
+    v->d_embeddings_fp16 = g.emb16; v->d_modalities = g.mods; v->d_timestamps = g.ts;
+    v->d_episode_ids = g.ep_ids; v->d_ep_csr_offsets = g.ep_off; v->d_ep_csr_members = g.ep_mem;
+    return MARS_OK;
+}
+
+int mars_graph_download(const mars_graph* gh, int32_t* row, int32_t* col, int32_t* ep_off, int32_t* ep_mem) {
+    MARS_CHECK(gh, MARS_ERR_INVALID, "null graph");
+    const Graph& g = gh->g;
+    MARS_TRY(use_device(g.device));
+    if (row) MARS_HIP(hipMemcpy(row, g.row, (size_t(g.n) + 1) * sizeof(int32_t), hipMemcpyDeviceToHost));
+    if (col && g.e > 0) MARS_HIP(hipMemcpy(col, g.col, size_t(g.e) * sizeof(int32_t), hipMemcpyDeviceToHost));
+    if (ep_off && g.ep_off)
+        MARS_HIP(hipMemcpy(ep_off, g.ep_off, (size_t(g.num_eps) + 1) * sizeof(int32_t), hipMemcpyDeviceToHost));
+    if (ep_mem && g.ep_mem && g.member_total > 0)
+        MARS_HIP(hipMemcpy(ep_mem, g.ep_mem, size_t(g.member_total) * sizeof(int32_t), hipMemcpyDeviceToHost));
+    return MARS_OK;
+}
+
+int mars_ctx_create(int32_t max_nodes, int32_t dim, int32_t max_k, uint32_t flags, mars_ctx** out) {
+    MARS_CHECK(out, MARS_ERR_INVALID, "null argument");
+    *out = nullptr;
+    MARS_CHECK(max_nodes > 0 && dim > 0 && max_k > 0, MARS_ERR_INVALID, "max_nodes %d, dim %d, max_k %d",
+               max_nodes, dim, max_k);
+    int devid = 0;
+    MARS_TRY(ensure_device(&devid));
+    auto* ch = new mars_ctx();
+    Ctx& c = ch->c;
+    c.device = devid;
+    c.max_nodes = max_nodes;
+    c.d = dim;
+    c.max_k = std::min(max_k, kMaxK);                       // memory_cuda.cu:1036
+    c.flags = flags;
+    c.max_wg = kMaxWg;
+    c.res_cap = kSortCap;
+    const size_t N = size_t(max_nodes);
+    int rc = MARS_OK;
+    auto fail = [&](int r) { ctx_free(c); delete ch; return r; };
+    hipError_t e = hipStreamCreateWithFlags(&c.stream, hipStreamNonBlocking);
+    if (e != hipSuccess) return fail(set_error(MARS_ERR_HIP, "stream: %s", hipGetErrorString(e)));
+    if ((rc = dmalloc(&c.query, size_t(dim))) || (rc = dmalloc(&c.fin, N)) ||
+        (rc = dmalloc(&c.part, size_t(kMaxWg) * kMaxK)) || (rc = dmalloc(&c.vis, N)) ||
+        (rc = dmalloc(&c.claim, N)) || (rc = dmalloc(&c.vlist, N)) || (rc = dmalloc(&c.vhop, N)) ||
+        (rc = dmalloc(&c.vscore, N)) || (rc = dmalloc(&c.sortbuf, 2 * size_t(kSortCap))) ||
+        (rc = dmalloc(&c.seed_idx, size_t(kMaxK))) || (rc = dmalloc(&c.seed_val, size_t(kMaxK))))
+        return fail(rc);
+    e = hipMemset(c.vis, 0, N * sizeof(uint32_t));
+    if (e == hipSuccess) e = hipMemset(c.claim, 0xFF, N * sizeof(uint64_t));
+    if (e == hipSuccess) e = hipHostMalloc(reinterpret_cast<void**>(&c.h_query), size_t(dim) * sizeof(float));
+    const size_t res_bytes = sizeof(ResultHeader) + size_t(kSortCap) * sizeof(mars_query_result);
+    if (e == hipSuccess)
+        e = hipHostMalloc(reinterpret_cast<void**>(&c.h_res), res_bytes, hipHostMallocMapped);
+    void* dres = nullptr;
+    if (e == hipSuccess) e = hipHostGetDevicePointer(&dres, c.h_res, 0);
+    if (e != hipSuccess) return fail(set_error(MARS_ERR_NOMEM, "context setup: %s", hipGetErrorString(e)));
+    std::memset(c.h_res, 0, res_bytes);
+    c.h_rec = reinterpret_cast<mars_query_result*>(c.h_res + 1);
+    c.d_res = static_cast<ResultHeader*>(dres);
+    c.d_rec = reinterpret_cast<mars_query_result*>(c.d_res + 1);
+    for (auto& ev : c.ev) {
+        e = hipEventCreate(&ev);
+        if (e != hipSuccess) return fail(set_error(MARS_ERR_HIP, "event: %s", hipGetErrorString(e)));
+    }
+    *out = ch;
+    return MARS_OK;
+}
+
+int mars_ctx_destroy(mars_ctx* ch) {
+    if (!ch) return MARS_OK;
+    ctx_free(ch->c);
+    delete ch;
+    return MARS_OK;
+}
+
+int mars_ctx_set_flags(mars_ctx* ch, uint32_t flags) {
+    MARS_CHECK(ch, MARS_ERR_INVALID, "null context");
+    ch->c.flags = flags;
+    return MARS_OK;
+}
+
+int mars_ctx_get_flags(const mars_ctx* ch, uint32_t* flags) {
+    MARS_CHECK(ch && flags, MARS_ERR_INVALID, "null argument");
+    *flags = ch->c.flags;
+    return MARS_OK;
+}
+
+int mars_query(const mars_graph* g, mars_ctx* c, const float* h_query, float t_q,
+               const mars_retrieval_config* cfg, mars_query_result* out, int32_t cap, int32_t* n_out,
+               mars_stats* stats) {
+    MARS_CHECK(h_query, MARS_ERR_INVALID, "null query");
+    return query_impl(g, c, h_query, nullptr, t_q, cfg, out, cap, n_out, stats);
+}
+
+int mars_query_device(const mars_graph* g, mars_ctx* c, const float* d_query, float t_q,
+                      const mars_retrieval_config* cfg, mars_query_result* out, int32_t cap, int32_t* n_out,
+                      mars_stats* stats) {
+    MARS_CHECK(d_query, MARS_ERR_INVALID, "null query");
+    return query_impl(g, c, nullptr, d_query, t_q, cfg, out, cap, n_out, stats);
+}
+
+int mars_bench_queries(const mars_graph* g, mars_ctx* c, const float* dq, int64_t stride, int32_t n, float t_q,
+                       const mars_retrieval_config* cfgs, int32_t n_cfg, double* lat_us, float* kern_us,
+                       float* bfs_us, int32_t* n_res) {
+    MARS_CHECK(g && c && dq && cfgs && lat_us && n >= 0 && (n_cfg == 1 || n_cfg == n) && stride >= g->g.d,
+               MARS_ERR_INVALID, "bad benchmark arguments");
+    mars_query_result out[64];
+    for (int32_t i = 0; i < n; ++i) {
+        mars_stats st{};
+        int32_t nr = 0;
+        const auto t0 = std::chrono::steady_clock::now();
+        const int rc = query_impl(g, c, nullptr, dq + int64_t(i) * stride, t_q, &cfgs[n_cfg == 1 ? 0 : i], out, 64,
+                                  &nr, &st);
+        const auto t1 = std::chrono::steady_clock::now();
+        if (rc != MARS_OK) return rc;
+        lat_us[i] = std::chrono::duration<double, std::micro>(t1 - t0).count();
+        if (kern_us) kern_us[i] = st.gpu_ms_similarity * 1000.0f;
+        if (bfs_us) bfs_us[i] = st.gpu_ms_bfs * 1000.0f;
+        if (n_res) n_res[i] = nr;
+    }
+    return MARS_OK;
+}
+
+int mars_ctx_last_scores(mars_ctx* ch, float* h, int64_t n) {
+    MARS_CHECK(ch && h, MARS_ERR_INVALID, "null argument");
+    Ctx& c = ch->c;
+    MARS_CHECK(n <= c.last_n && n >= 0, MARS_ERR_INVALID, "asked %lld scores, last global query had %d",
+               (long long)n, c.last_n);
+    MARS_TRY(use_device(c.device));
+    MARS_HIP(hipMemcpy(h, c.fin, size_t(n) * sizeof(float), hipMemcpyDeviceToHost));
+    return MARS_OK;
+}
+
+int mars_ctx_last_seeds(mars_ctx* ch, int32_t* idx, float* val, int32_t k, int32_t* k_out) {
+    MARS_CHECK(ch && idx && val && k_out, MARS_ERR_INVALID, "null argument");
+    Ctx& c = ch->c;
+    MARS_TRY(use_device(c.device));
+    const int32_t n = std::min(k, c.last_k);
+    if (n > 0) {
+        MARS_HIP(hipMemcpy(idx, c.seed_idx, size_t(n) * sizeof(int32_t), hipMemcpyDeviceToHost));
+        MARS_HIP(hipMemcpy(val, c.seed_val, size_t(n) * sizeof(float), hipMemcpyDeviceToHost));
+    }
+    *k_out = c.last_k;
+    return MARS_OK;
+}
+
+int mars_ctx_last_visited(mars_ctx* ch, int32_t* ids, int32_t* hops, float* scores, int32_t cap, int32_t* n_out) {
+    MARS_CHECK(ch && n_out && cap >= 0, MARS_ERR_INVALID, "null argument");
+    Ctx& c = ch->c;
+    MARS_TRY(use_device(c.device));
+    const int32_t n = std::min(cap, c.last_visited);
+    if (n > 0) {
+        if (ids) MARS_HIP(hipMemcpy(ids, c.vlist, size_t(n) * sizeof(int32_t), hipMemcpyDeviceToHost));
+        if (hops) MARS_HIP(hipMemcpy(hops, c.vhop, size_t(n) * sizeof(int32_t), hipMemcpyDeviceToHost));
+        if (scores) MARS_HIP(hipMemcpy(scores, c.vscore, size_t(n) * sizeof(float), hipMemcpyDeviceToHost));
+    }
+    *n_out = c.last_visited;
+    return MARS_OK;
+}
+
+}  // extern "C"

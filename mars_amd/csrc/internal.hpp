@@ -1,0 +1,206 @@
+// ============================================================================
+//  internal.hpp — shared internals of libmars_amd (gfx950 only).
+//
+//  Score keys. Every selection in the library (per-wave top-K, seed merge,
+//  final result order) compares 64-bit keys
+//        key = (desc32(score) << 32) | node_id
+//  where desc32 is an order-reversing bijection of fp32 (larger score ->
+//  smaller key, -0.0 folded onto +0.0). Ascending keys are therefore
+//  (score desc, node id asc): the order of a stable ascending radix sort of
+//  negated scores (reference: src/memory_cuda.cu:1254-1283) and a total order,
+//  so top-K and final results are deterministic.
+// ============================================================================
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "mars_amd.h"
+
+namespace mars {
+
+// ---- error reporting ---------------------------------------------------------
+int set_error(int code, const char* fmt, ...);
+#define MARS_HIP(call)                                                               \
+    do {                                                                             \
+        hipError_t e__ = (call);                                                     \
+        if (e__ != hipSuccess)                                                       \
+            return ::mars::set_error(MARS_ERR_HIP, "%s:%d %s -> %s", __FILE__, __LINE__, \
+                                     #call, hipGetErrorString(e__));                 \
+    } while (0)
+#define MARS_CHECK(cond, code, ...)                                                  \
+    do {                                                                             \
+        if (!(cond)) return ::mars::set_error((code), __VA_ARGS__);                  \
+    } while (0)
+
+constexpr int kMaxK = 64;              // seeds per query (wave-held list), as MAX_TOP_K
+constexpr int kSortCap = 8192;         // results sorted in LDS by the finalize kernel
+constexpr int kFrontierChunk = 4096;   // frontier nodes per BFS chunk (LDS)
+constexpr uint64_t kEmptyKey = ~0ull;
+
+// ---- score keys ----------------------------------------------------------------
+__host__ __device__ inline uint32_t desc32(float s) {
+    s = s + 0.0f;                                   // -0.0 -> +0.0
+    uint32_t u;
+    __builtin_memcpy(&u, &s, 4);
+    const uint32_t asc = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ~asc;
+}
+__host__ __device__ inline float desc32_inv(uint32_t k) {
+    const uint32_t asc = ~k;
+    const uint32_t u = (asc & 0x80000000u) ? (asc & 0x7fffffffu) : ~asc;
+    float s;
+    __builtin_memcpy(&s, &u, 4);
+    return s;
+}
+__host__ __device__ inline uint64_t make_key(float s, uint32_t id) {
+    return (uint64_t(desc32(s)) << 32) | id;
+}
+__host__ __device__ inline float key_score(uint64_t k) { return desc32_inv(uint32_t(k >> 32)); }
+__host__ __device__ inline int32_t key_id(uint64_t k) { return int32_t(uint32_t(k)); }
+
+// ---- device objects ---------------------------------------------------------------
+struct Graph {
+    int device = 0;
+    int32_t n = 0;            // live nodes
+    int32_t e = 0;            // live edges (col entries)
+    int32_t d = 0;
+    int32_t cap_n = 0;
+    int64_t cap_e = 0;
+    float* emb = nullptr;
+    __half* emb16 = nullptr;
+    int32_t* mods = nullptr;
+    float* ts = nullptr;
+    int32_t* row = nullptr;   // cap_n + 1
+    int32_t* col = nullptr;   // cap_e
+    int32_t* ep_ids = nullptr;
+    int32_t* ep_off = nullptr;
+    int32_t* ep_mem = nullptr;
+    int32_t num_eps = 0;
+    int32_t member_total = 0;
+};
+
+// Result staging written by the finalize / episode kernels straight into
+// pinned host memory (one PCIe write burst, no D2H copy).
+struct ResultHeader {
+    int32_t count;        // results written (<= requested cap)
+    int32_t visited;      // nodes reached (seeds + BFS)
+    int32_t levels;       // BFS levels expanded
+    int32_t n_seeds;      // seeds selected
+};
+
+struct Ctx {
+    int device = 0;
+    int32_t max_nodes = 0;
+    int32_t d = 0;
+    int32_t max_k = 0;
+    uint32_t flags = 0;
+    hipStream_t stream = nullptr;
+    // device scratch
+    float* query = nullptr;        // d
+    float* fin = nullptr;          // max_nodes: fused score of the last global query
+    uint64_t* part = nullptr;      // max_wg * kMaxK partial top-K keys
+    int32_t max_wg = 0;
+    uint32_t* vis = nullptr;       // max_nodes visit stamps (epoch)
+    uint64_t* claim = nullptr;     // max_nodes BFS claim keys
+    int32_t* vlist = nullptr;      // max_nodes visit order (node ids)
+    int32_t* vhop = nullptr;       // max_nodes
+    float* vscore = nullptr;       // max_nodes
+    uint64_t* sortbuf = nullptr;   // max_nodes keys (large-result fallback)
+    int32_t* seed_idx = nullptr;   // kMaxK
+    float* seed_val = nullptr;     // kMaxK
+    // pinned host staging
+    float* h_query = nullptr;      // d
+    ResultHeader* h_res = nullptr; // header + results
+    mars_query_result* h_rec = nullptr;
+    ResultHeader* d_res = nullptr; // device alias of h_res
+    mars_query_result* d_rec = nullptr;
+    int32_t res_cap = 0;
+    uint32_t epoch = 0;            // last visit stamp used
+    uint32_t gen = 0;              // next BFS claim generation
+    hipEvent_t ev[4] = {nullptr, nullptr, nullptr, nullptr};
+    int32_t last_n = 0;            // node count of the last global query
+    int32_t last_k = 0;
+    int32_t last_visited = 0;      // visit-list length of the last global query
+};
+
+// ---- launch helpers (defined in kernels.hip) --------------------------------------
+struct ScanArgs {
+    const void* emb;     // fp32 or fp16 rows
+    int32_t fp16;
+    int64_t n;
+    int32_t d;
+    const float* q;
+    const float* ts;
+    const int32_t* mods;
+    const int32_t* ep_ids;
+    float t_q;
+    float lambda;
+    int32_t mod_filter;
+    int32_t query_ep;
+    float boost;         // > 0 and ep_ids != null: same-episode boost
+    int32_t k;
+    float* fin;
+    uint64_t* part;
+    int32_t rows_per_wg;
+    int32_t num_wg;
+};
+int launch_scan(const ScanArgs& a, hipStream_t s);
+void scan_grid(int64_t n, int32_t max_wg, int32_t* rows_per_wg, int32_t* num_wg);
+
+struct FinalizeArgs {
+    const uint64_t* part;
+    int32_t n_part;          // partial keys (num_wg * k)
+    int32_t k;
+    const int32_t* row;
+    const int32_t* col;
+    const float* fin;
+    const int32_t* mods;
+    int32_t hops;
+    float hop_decay;
+    uint32_t epoch;          // visit stamp of this query (vis[i] == epoch: visited)
+    uint32_t gen_base;       // claim generation of BFS level 0 (level h uses gen_base + h)
+    uint32_t* vis;
+    uint64_t* claim;
+    int32_t* vlist;
+    int32_t* vhop;
+    float* vscore;
+    uint64_t* sortbuf;
+    int32_t cap_visit;
+    int32_t rcap;            // results requested (max_results or K)
+    int32_t* seed_idx;
+    float* seed_val;
+    ResultHeader* res;
+    mars_query_result* rec;
+};
+int launch_finalize(const FinalizeArgs& a, hipStream_t s);
+
+struct EpisodeArgs {
+    const float* emb;
+    int32_t d;
+    int64_t n;
+    const float* q;
+    const float* ts;
+    const int32_t* mods;
+    const int32_t* members;  // ep_csr_members + begin
+    int32_t m;
+    float t_q;
+    float lambda;
+    int32_t mod_filter;
+    int32_t k;
+    int32_t rcap;
+    uint64_t* keybuf;        // >= m keys scratch
+    int32_t* seed_idx;
+    float* seed_val;
+    ResultHeader* res;
+    mars_query_result* rec;
+};
+int launch_episode(const EpisodeArgs& a, hipStream_t s);
+
+int launch_convert_f16(const float* in, __half* out, int64_t count, hipStream_t s);
+
+}  // namespace mars

@@ -1,0 +1,672 @@
+// ============================================================================
+//  kernels.hip — retrieval hot-path kernels for gfx950 (wave64).
+//
+//  k_scan       Q=1 global scan. Rows are read by 16-lane groups (a DPP row):
+//               lane s of a group reads 16-byte pieces s, s+16, s+32, ... of the
+//               row, so one wave load instruction covers four rows with four
+//               fully used 256-byte segments. The dot product is finished with a
+//               4-step in-row reduction; temporal decay, modality filter and the
+//               same-episode boost are applied in registers; the fused score is
+//               written once (4 bytes/row) and offered to a wave-held top-K list
+//               (lane i holds the i-th smallest key). Each workgroup writes its
+//               K best keys. Replaces cublasSgemv + temporal_rerank_kernel +
+//               episode_same_boost_kernel + negate/iota/CUB sort/extract
+//               (reference src/memory_cuda.cu:1207-1283, :400-440, :737-771).
+//  k_finalize   One workgroup: merges the per-workgroup keys into the K seeds,
+//               runs the deterministic level-synchronous BFS (first discoverer in
+//               (frontier position, CSR slot) order wins, via a 64-bit atomicMin
+//               claim and an in-order compaction), then sorts the visited set by
+//               (score desc, id asc) and writes the results straight into pinned
+//               host memory. Replaces bfs_init_seeds / bfs_expand_device_driven /
+//               compact_results and the host std::sort (src/memory_cuda.cu:633-732,
+//               :1300-1345, :1421-1447).
+//  k_episode    Episode-scoped query in one launch: dot + decay over the member
+//               range only, top-K, reference padding, results. Replaces
+//               fill_neg_inf_final + cosine_episode_subset_fused + the O(N) sort /
+//               compaction (src/memory_cuda.cu:421-424, :443-493, :1194-1206).
+//  k_convert_f16  RNE fp32 -> fp16 copy with 64-bit indexing (convert_f32_to_f16,
+//               src/memory_cuda.cu:207-211 and :858-868, which overflows int32).
+// ============================================================================
+#include "internal.hpp"
+
+#include <cfloat>
+#include <type_traits>
+
+namespace mars {
+namespace {
+
+__device__ inline int lane_id() { return int(threadIdx.x & 63u); }
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Loads of data written earlier in the same kernel by other threads: served by
+// L2 (agent-coherent), never by a stale L1 line.
+template <typename T>
+__device__ inline T ld_coherent(const T* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Insert key x into the wave-held ascending list (lane i = i-th smallest; lanes
+// >= k hold kEmptyKey). Caller guarantees x < list[k-1].
+__device__ inline void list_insert(uint64_t& list, uint64_t x, int lane, int k) {
+    const uint64_t below = __ballot(list < x);
+    const int pos = __popcll(below);
+    const uint64_t up = __shfl_up(list, 1u);
+    uint64_t v = (lane < pos) ? list : ((lane == pos) ? x : up);
+    list = (lane < k) ? v : kEmptyKey;
+}
+
+// Offer one candidate key per lane where `offer` holds; keeps thr = list[k-1].
+__device__ inline void list_offer(uint64_t& list, uint64_t& thr, uint64_t key, bool offer,
+                                  int lane, int k) {
+    uint64_t m = __ballot(offer && key < thr);
+    while (m) {
+        const int src = __ffsll((unsigned long long)m) - 1;
+        m &= m - 1;
+        const uint64_t x = __shfl(key, src);
+        if (x < thr) {
+            list_insert(list, x, lane, k);
+            thr = __shfl(list, k - 1);
+        }
+    }
+}
+
+// Sum over the 16 lanes of a DPP row; every lane of the row gets the total.
+__device__ inline float row16_sum(float v) {
+    v += __shfl_xor(v, 8, 16);
+    v += __shfl_xor(v, 4, 16);
+    v += __shfl_xor(v, 2, 16);
+    v += __shfl_xor(v, 1, 16);
+    return v;
+}
+
+// ---- per-row dot products -------------------------------------------------------
+// fp32 rows: chunk c covers floats [64c, 64c+64); lane s holds 4 of them.
+template <int NCH>
+struct QF32 {
+    float v[NCH][4];
+    __device__ void load(const float* q, int sub) {
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+            const float4 x = reinterpret_cast<const float4*>(q + c * 64)[sub];
+            v[c][0] = x.x; v[c][1] = x.y; v[c][2] = x.z; v[c][3] = x.w;
+        }
+    }
+    __device__ float dot(const float* row, int sub) const {
+        const f32x4* r = reinterpret_cast<const f32x4*>(row) + sub;
+        f32x4 x[NCH];
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) x[c] = __builtin_nontemporal_load(r + c * 16);
+        float acc = 0.0f;
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+            acc = fmaf(x[c].x, v[c][0], acc);
+            acc = fmaf(x[c].y, v[c][1], acc);
+            acc = fmaf(x[c].z, v[c][2], acc);
+            acc = fmaf(x[c].w, v[c][3], acc);
+        }
+        return acc;
+    }
+};
+
+// fp16 rows: chunk c covers halves [128c, 128c+128); lane s holds 8 of them.
+template <int NCH>
+struct QF16 {
+    float v[NCH][8];
+    __device__ void load(const float* q, int sub) {
+#pragma unroll
+        for (int c = 0; c < NCH; ++c)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[c][j] = q[c * 128 + sub * 8 + j];
+    }
+    __device__ float dot(const __half* row, int sub) const {
+        const u32x4* r = reinterpret_cast<const u32x4*>(row) + sub;
+        u32x4 x[NCH];
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) x[c] = __builtin_nontemporal_load(r + c * 16);
+        float acc = 0.0f;
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+            const uint32_t w[4] = {x[c].x, x[c].y, x[c].z, x[c].w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const __half2 h2 = *reinterpret_cast<const __half2*>(&w[j]);
+                const float2 f = __half22float2(h2);
+                acc = fmaf(f.x, v[c][2 * j], acc);
+                acc = fmaf(f.y, v[c][2 * j + 1], acc);
+            }
+        }
+        return acc;
+    }
+};
+
+// Any D: lane s of the group takes elements s, s+16, ... (q read through cache).
+struct QGeneric {
+    const float* q;
+    int d;
+    __device__ void load(const float* q_, int) { q = q_; }
+    __device__ float dot(const float* row, int sub) const {
+        float acc = 0.0f;
+        for (int i = sub; i < d; i += 16) acc = fmaf(row[i], q[i], acc);
+        return acc;
+    }
+    __device__ float dot(const __half* row, int sub) const {
+        float acc = 0.0f;
+        for (int i = sub; i < d; i += 16) acc = fmaf(__half2float(row[i]), q[i], acc);
+        return acc;
+    }
+};
+
+// fused stage-1/2 epilogue (reference order of fp32 operations: dot * w, then
+// * (1 + boost); filtered rows are -FLT_MAX and not decayed).
+__device__ inline float fuse_score(float dot, float ts, int32_t mod, int32_t ep,
+                                   const ScanArgs& a) {
+    if (a.mod_filter >= 0 && mod != a.mod_filter) return -FLT_MAX;
+    const float age = fmaxf(0.0f, a.t_q - ts);
+    float s = dot * expf(-a.lambda * age);
+    if (a.boost > 0.0f && ep == a.query_ep && s > -FLT_MAX * 0.5f) s = s * (1.0f + a.boost);
+    return s;
+}
+
+template <typename T, typename QF>
+__global__ __launch_bounds__(256) void k_scan(ScanArgs a) {
+    __shared__ uint64_t s_lists[4][64];
+    const int lane = lane_id(), wave = int(threadIdx.x >> 6);
+    const int sub = lane & 15, grp = lane >> 4;
+    const int k = a.k;
+    QF qf;
+    if constexpr (std::is_same_v<QF, QGeneric>) qf.d = a.d;
+    qf.load(a.q, sub);
+    const T* emb = static_cast<const T*>(a.emb);
+    const int64_t r0 = int64_t(blockIdx.x) * a.rows_per_wg;
+    const int64_t r1 = (a.n < r0 + a.rows_per_wg) ? a.n : r0 + a.rows_per_wg;
+    const bool use_boost = a.boost > 0.0f && a.ep_ids != nullptr;
+    uint64_t list = kEmptyKey, thr = kEmptyKey;
+    for (int64_t base = r0 + 4 * wave; base < r1; base += 16) {
+        const int64_t r = base + grp;
+        const bool valid = r < r1;
+        const int64_t rr = valid ? r : r1 - 1;
+        const float ts = a.ts[rr];
+        const int32_t mod = (a.mod_filter >= 0) ? a.mods[rr] : 0;
+        const int32_t ep = use_boost ? a.ep_ids[rr] : -1;
+        const float dot = row16_sum(qf.dot(emb + rr * a.d, sub));
+        const float s = fuse_score(dot, ts, mod, ep, a);
+        if (valid && sub == 0) a.fin[r] = s;
+        const uint64_t key = valid ? make_key(s, uint32_t(r)) : kEmptyKey;
+        list_offer(list, thr, key, sub == 0, lane, k);
+    }
+    s_lists[wave][lane] = list;
+    __syncthreads();
+    if (wave == 0) {
+        for (int w = 1; w < 4; ++w) list_offer(list, thr, s_lists[w][lane], true, lane, k);
+        if (lane < k) a.part[int64_t(blockIdx.x) * k + lane] = list;
+    }
+}
+
+// ---- block-wide helpers (1024 threads) --------------------------------------------
+constexpr int kFinThreads = 1024;
+constexpr int kFinWaves = kFinThreads / 64;
+
+// Exclusive prefix sum across the block; *total gets the block sum.
+__device__ inline int block_excl_scan(int v, int* s_wave, int* total) {
+    const int lane = lane_id(), wave = int(threadIdx.x >> 6);
+    int incl = v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(incl, unsigned(o));
+        if (lane >= o) incl += y;
+    }
+    if (lane == 63) s_wave[wave] = incl;
+    __syncthreads();
+    int off = 0, tot = 0;
+#pragma unroll
+    for (int w = 0; w < kFinWaves; ++w) {
+        const int x = s_wave[w];
+        off += (w < wave) ? x : 0;
+        tot += x;
+    }
+    __syncthreads();
+    *total = tot;
+    return off + incl - v;
+}
+
+// largest p in [0, cn) with eoff[p] <= t (eoff[0] == 0 <= t)
+__device__ inline int owner_of(const int32_t* eoff, int cn, int t) {
+    int lo = 0, hi = cn;
+    while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (eoff[mid] <= t) lo = mid; else hi = mid;
+    }
+    return lo;
+}
+
+// Bitonic sort of n (power of two, <= kSortCap) keys with 16-bit payloads in LDS.
+__device__ inline void block_bitonic(uint64_t* key, uint16_t* pay, int n) {
+    for (int size = 2; size <= n; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            for (int i = int(threadIdx.x); i < (n >> 1); i += kFinThreads) {
+                const int lo = 2 * i - (i & (stride - 1));
+                const int hi = lo + stride;
+                const bool up = (lo & size) == 0;
+                const uint64_t a = key[lo], b = key[hi];
+                if ((a > b) == up) {
+                    key[lo] = b; key[hi] = a;
+                    const uint16_t t = pay[lo]; pay[lo] = pay[hi]; pay[hi] = t;
+                }
+            }
+            __syncthreads();
+        }
+    }
+}
+
+struct FinShared {
+    union {
+        struct {
+            uint64_t key[kSortCap];
+            uint16_t pay[kSortCap];
+        } sort;
+        struct {
+            int32_t rstart[kFrontierChunk];
+            int32_t eoff[kFrontierChunk + 1];
+        } bfs;
+        uint64_t lists[kFinWaves][64];
+        uint32_t hist[256];
+    } u;
+    int s_wave[kFinWaves];
+    int s_misc[4];
+};
+
+__global__ __launch_bounds__(kFinThreads) void k_finalize(FinalizeArgs a) {
+    __shared__ FinShared sh;
+    const int tid = int(threadIdx.x), lane = lane_id(), wave = tid >> 6;
+    const int k = a.k;
+
+    // ---- A. merge per-workgroup keys into the K seeds -------------------------
+    uint64_t list = kEmptyKey, thr = kEmptyKey;
+    for (int base = wave * 64; base < a.n_part; base += kFinThreads) {
+        const int i = base + lane;
+        const uint64_t x = (i < a.n_part) ? a.part[i] : kEmptyKey;
+        list_offer(list, thr, x, true, lane, k);
+    }
+    sh.u.lists[wave][lane] = list;
+    __syncthreads();
+    if (wave == 0) {
+        for (int w = 1; w < kFinWaves; ++w) list_offer(list, thr, sh.u.lists[w][lane], true, lane, k);
+        const int ns = __popcll(__ballot(lane < k && list != kEmptyKey));
+        if (lane < ns) {
+            const int32_t id = key_id(list);
+            const float sc = key_score(list);
+            a.seed_idx[lane] = id;
+            a.seed_val[lane] = sc;
+            a.vlist[lane] = id;
+            a.vhop[lane] = 0;
+            a.vscore[lane] = sc;
+            a.vis[id] = a.epoch;
+        }
+        if (lane == 0) sh.s_misc[0] = ns;
+    }
+    __threadfence();
+    __syncthreads();
+    const int ns = sh.s_misc[0];
+
+    // ---- B. deterministic BFS ------------------------------------------------
+    int fs = 0, fe = ns, levels = 0;
+    for (int h = 0; h < a.hops && fs < fe; ++h) {
+        const uint32_t gen = a.gen_base + uint32_t(h);
+        const uint64_t hi = uint64_t(0xFFFFFFFFu - gen) << 32;
+        int out = fe;
+        for (int c0 = fs; c0 < fe; c0 += kFrontierChunk) {
+            const int cn = min(kFrontierChunk, fe - c0);
+            // degrees of this chunk, 4 consecutive frontier slots per thread
+            int deg[4], rs[4], local = 0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int i = tid * 4 + j;
+                deg[j] = 0; rs[j] = 0;
+                if (i < cn) {
+                    const int32_t v = ld_coherent(a.vlist + c0 + i);
+                    rs[j] = a.row[v];
+                    deg[j] = a.row[v + 1] - rs[j];
+                }
+                local += deg[j];
+            }
+            int total = 0;
+            int off = block_excl_scan(local, sh.s_wave, &total);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int i = tid * 4 + j;
+                if (i < cn) { sh.u.bfs.eoff[i] = off; sh.u.bfs.rstart[i] = rs[j]; }
+                off += deg[j];
+            }
+            __syncthreads();
+            const int T = total;
+            // claim: smallest (frontier position) wins each undiscovered neighbour
+            for (int t = tid; t < T; t += kFinThreads) {
+                const int p = owner_of(sh.u.bfs.eoff, cn, t);
+                const int32_t nb = a.col[sh.u.bfs.rstart[p] + (t - sh.u.bfs.eoff[p])];
+                if (ld_coherent(a.vis + nb) != a.epoch)
+                    atomicMin(reinterpret_cast<unsigned long long*>(a.claim + nb),
+                              (unsigned long long)(hi | uint32_t(c0 + p)));
+            }
+            __threadfence();
+            __syncthreads();
+            // emit winners in (frontier position, CSR slot) order
+            for (int r0 = 0; r0 < T; r0 += kFinThreads) {
+                const int t = r0 + tid;
+                bool won = false;
+                int p = 0;
+                int32_t nb = 0;
+                if (t < T) {
+                    p = owner_of(sh.u.bfs.eoff, cn, t);
+                    nb = a.col[sh.u.bfs.rstart[p] + (t - sh.u.bfs.eoff[p])];
+                    won = ld_coherent(a.claim + nb) == (hi | uint32_t(c0 + p));
+                }
+                const uint64_t m = __ballot(won);
+                if (lane == 0) sh.s_wave[wave] = __popcll(m);
+                __syncthreads();
+                int woff = 0, wtot = 0;
+#pragma unroll
+                for (int w = 0; w < kFinWaves; ++w) {
+                    const int x = sh.s_wave[w];
+                    woff += (w < wave) ? x : 0;
+                    wtot += x;
+                }
+                if (won) {
+                    const int pos = out + woff + __popcll(m & ((1ull << lane) - 1ull));
+                    const float ps = ld_coherent(a.vscore + c0 + p);
+                    a.vlist[pos] = nb;
+                    a.vhop[pos] = h + 1;
+                    a.vscore[pos] = fmaxf(ps * a.hop_decay, a.fin[nb] * 0.8f);
+                    a.vis[nb] = a.epoch;
+                }
+                out += wtot;
+                __threadfence();
+                __syncthreads();
+            }
+        }
+        fs = fe;
+        fe = out;
+        ++levels;
+    }
+
+    // ---- C. results: (score desc, id asc), first rcap ----------------------------
+    const int V = fe;
+    const int rc = min(a.rcap, V);
+    if (V <= kSortCap) {
+        int n2 = 1;
+        while (n2 < V) n2 <<= 1;
+        for (int i = tid; i < n2; i += kFinThreads) {
+            if (i < V) {
+                sh.u.sort.key[i] = make_key(ld_coherent(a.vscore + i), uint32_t(ld_coherent(a.vlist + i)));
+                sh.u.sort.pay[i] = uint16_t(i);
+            } else {
+                sh.u.sort.key[i] = kEmptyKey;
+                sh.u.sort.pay[i] = 0;
+            }
+        }
+        __syncthreads();
+        block_bitonic(sh.u.sort.key, sh.u.sort.pay, n2);
+        for (int j = tid; j < rc; j += kFinThreads) {
+            const uint64_t key = sh.u.sort.key[j];
+            const int pos = sh.u.sort.pay[j];
+            const int32_t id = key_id(key);
+            mars_query_result r;
+            r.node_id = id;
+            r.score = key_score(key);
+            r.modality = a.mods[id];
+            r.hops_from_seed = ld_coherent(a.vhop + pos);
+            a.rec[j] = r;
+        }
+    } else {
+        // radix-select the key of rank rc (keys are unique), then sort the rc
+        // smallest (rc <= kSortCap is enforced by the host).
+        uint64_t prefix = 0, mask = 0;
+        int need = rc;
+        for (int shift = 56; shift >= 0; shift -= 8) {
+            for (int i = tid; i < 256; i += kFinThreads) sh.u.hist[i] = 0;
+            __syncthreads();
+            for (int i = tid; i < V; i += kFinThreads) {
+                const uint64_t key = make_key(ld_coherent(a.vscore + i), uint32_t(ld_coherent(a.vlist + i)));
+                if ((key & mask) == prefix) atomicAdd(&sh.u.hist[(key >> shift) & 255u], 1u);
+            }
+            __syncthreads();
+            if (tid == 0) {
+                int cum = 0, dg = 255;
+                for (int b = 0; b < 256; ++b) {
+                    if (cum + int(sh.u.hist[b]) >= need) { dg = b; break; }
+                    cum += int(sh.u.hist[b]);
+                }
+                sh.s_misc[1] = dg;
+                sh.s_misc[2] = need - cum;
+            }
+            __syncthreads();
+            prefix |= uint64_t(sh.s_misc[1]) << shift;
+            mask |= uint64_t(0xFF) << shift;
+            need = sh.s_misc[2];
+            __syncthreads();
+        }
+        // gather the rc keys <= prefix (with their visit positions) into sortbuf
+        int base = 0;
+        for (int r0 = 0; r0 < V; r0 += kFinThreads) {
+            const int i = r0 + tid;
+            uint64_t key = kEmptyKey;
+            bool take = false;
+            if (i < V) {
+                key = make_key(ld_coherent(a.vscore + i), uint32_t(ld_coherent(a.vlist + i)));
+                take = key <= prefix;
+            }
+            int tot = 0;
+            const int o = block_excl_scan(take ? 1 : 0, sh.s_wave, &tot);
+            if (take) { a.sortbuf[2 * (base + o)] = key; a.sortbuf[2 * (base + o) + 1] = uint64_t(i); }
+            base += tot;
+        }
+        __threadfence();
+        __syncthreads();
+        int n2 = 1;
+        while (n2 < rc) n2 <<= 1;
+        // positions can exceed 16 bits here: sort (key, slot) and look the position up
+        for (int i = tid; i < n2; i += kFinThreads) {
+            sh.u.sort.key[i] = (i < rc) ? ld_coherent(a.sortbuf + 2 * i) : kEmptyKey;
+            sh.u.sort.pay[i] = uint16_t(i < rc ? i : 0);
+        }
+        __syncthreads();
+        block_bitonic(sh.u.sort.key, sh.u.sort.pay, n2);
+        for (int j = tid; j < rc; j += kFinThreads) {
+            const uint64_t key = sh.u.sort.key[j];
+            const int slot = sh.u.sort.pay[j];
+            const int pos = int(ld_coherent(a.sortbuf + 2 * slot + 1));
+            const int32_t id = key_id(key);
+            mars_query_result r;
+            r.node_id = id;
+            r.score = key_score(key);
+            r.modality = a.mods[id];
+            r.hops_from_seed = ld_coherent(a.vhop + pos);
+            a.rec[j] = r;
+        }
+    }
+    if (tid == 0) {
+        ResultHeader h;
+        h.count = rc;
+        h.visited = V;
+        h.levels = levels;
+        h.n_seeds = ns;
+        *a.res = h;
+    }
+}
+
+// ---- episode-scoped query ------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_episode(EpisodeArgs a) {
+    __shared__ uint64_t s_lists[4][64];
+    __shared__ int32_t s_ids[64];
+    __shared__ uint64_t s_out[64];
+    __shared__ int s_cnt[2];
+    const int lane = lane_id(), wave = int(threadIdx.x >> 6);
+    const int sub = lane & 15, grp = lane >> 4;
+    const int k = a.k;
+    uint64_t list = kEmptyKey, thr = kEmptyKey;
+    for (int base = 4 * wave; base < a.m; base += 16) {
+        const int j = base + grp;
+        const bool valid = j < a.m;
+        const int32_t node = a.members[valid ? j : a.m - 1];
+        float acc = 0.0f;
+        const float* row = a.emb + int64_t(node) * a.d;
+        if ((a.d & 3) == 0) {
+            const float4* r4 = reinterpret_cast<const float4*>(row);
+            const float4* q4 = reinterpret_cast<const float4*>(a.q);
+            for (int i = sub; i < (a.d >> 2); i += 16) {
+                const float4 x = r4[i], y = q4[i];
+                acc = fmaf(x.x, y.x, acc); acc = fmaf(x.y, y.y, acc);
+                acc = fmaf(x.z, y.z, acc); acc = fmaf(x.w, y.w, acc);
+            }
+        } else {
+            for (int i = sub; i < a.d; i += 16) acc = fmaf(row[i], a.q[i], acc);
+        }
+        const float dot = row16_sum(acc);
+        const bool filtered = a.mod_filter >= 0 && a.mods[node] != a.mod_filter;
+        const float age = fmaxf(0.0f, a.t_q - a.ts[node]);
+        const float s = dot * expf(-a.lambda * age);
+        // filtered members score -FLT_MAX exactly like non-members (padding pool)
+        const uint64_t key = (valid && !filtered) ? make_key(s, uint32_t(node)) : kEmptyKey;
+        list_offer(list, thr, key, sub == 0, lane, k);
+    }
+    s_lists[wave][lane] = list;
+    __syncthreads();
+    if (wave == 0) {
+        for (int w = 1; w < 4; ++w) list_offer(list, thr, s_lists[w][lane], true, lane, k);
+        const int u = __popcll(__ballot(lane < k && list != kEmptyKey));
+        s_out[lane] = list;
+        if (lane < u) s_ids[lane] = key_id(list);
+        if (lane == 0) s_cnt[0] = u;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const int u = s_cnt[0];
+        const int kk = int(a.n < k ? a.n : k);          // seeds = min(K, N)
+        // fewer unfiltered members than seeds: pad with the lowest ids whose
+        // score is -FLT_MAX (everything but the unfiltered members), as the
+        // reference's stable sort over the -FLT_MAX-filled score array does.
+        if (u < kk) {
+            for (int i = 1; i < u; ++i) {                 // sort member ids ascending
+                const int32_t x = s_ids[i];
+                int j = i - 1;
+                while (j >= 0 && s_ids[j] > x) { s_ids[j + 1] = s_ids[j]; --j; }
+                s_ids[j + 1] = x;
+            }
+            int need = kk - u, jm = 0, w = u;
+            for (int32_t cand = 0; need > 0; ++cand) {
+                if (jm < u && s_ids[jm] == cand) { ++jm; continue; }
+                s_out[w++] = make_key(-FLT_MAX, uint32_t(cand));
+                --need;
+            }
+        }
+        s_cnt[1] = kk;
+    }
+    __syncthreads();
+    const int kk = s_cnt[1];
+    const int rc = min(a.rcap, kk);
+    if (threadIdx.x < unsigned(kk)) {
+        const uint64_t key = s_out[threadIdx.x];
+        const int32_t id = key_id(key);
+        a.seed_idx[threadIdx.x] = id;
+        a.seed_val[threadIdx.x] = key_score(key);
+        if (int(threadIdx.x) < rc) {
+            mars_query_result r;
+            r.node_id = id;
+            r.score = key_score(key);
+            r.modality = a.mods[id];
+            r.hops_from_seed = 0;
+            a.rec[threadIdx.x] = r;
+        }
+    }
+    if (threadIdx.x == 0) {
+        ResultHeader h;
+        h.count = rc;
+        h.visited = kk;
+        h.levels = 0;
+        h.n_seeds = kk;
+        *a.res = h;
+    }
+}
+
+__global__ void k_convert_f16(const float* __restrict__ in, __half* __restrict__ out, int64_t count) {
+    const int64_t n8 = count >> 3;
+    const int64_t stride = int64_t(gridDim.x) * blockDim.x;
+    for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n8; i += stride) {
+        const float4 a = reinterpret_cast<const float4*>(in)[2 * i];
+        const float4 b = reinterpret_cast<const float4*>(in)[2 * i + 1];
+        __half2 h[4] = {__floats2half2_rn(a.x, a.y), __floats2half2_rn(a.z, a.w),
+                        __floats2half2_rn(b.x, b.y), __floats2half2_rn(b.z, b.w)};
+        reinterpret_cast<uint4*>(out)[i] = *reinterpret_cast<const uint4*>(h);
+    }
+    for (int64_t i = (n8 << 3) + int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < count; i += stride)
+        out[i] = __float2half_rn(in[i]);
+}
+
+template <typename T, typename QF>
+int launch_scan_t(const ScanArgs& a, hipStream_t s) {
+    hipLaunchKernelGGL((k_scan<T, QF>), dim3(unsigned(a.num_wg)), dim3(256), 0, s, a);
+    MARS_HIP(hipGetLastError());
+    return MARS_OK;
+}
+
+}  // namespace
+
+void scan_grid(int64_t n, int32_t max_wg, int32_t* rows_per_wg, int32_t* num_wg) {
+    // ~8 workgroups per CU on 256 CUs, at least 64 rows each, multiple of 16 rows
+    const int64_t target = max_wg;
+    int64_t rpw = (n + target - 1) / target;
+    if (rpw < 64) rpw = 64;
+    rpw = (rpw + 15) / 16 * 16;
+    *rows_per_wg = int32_t(rpw);
+    *num_wg = int32_t((n + rpw - 1) / rpw);
+}
+
+int launch_scan(const ScanArgs& a, hipStream_t s) {
+    const bool f16 = a.fp16 != 0;
+    if (!f16 && a.d % 64 == 0) {
+        switch (a.d / 64) {
+            case 4: return launch_scan_t<float, QF32<4>>(a, s);
+            case 6: return launch_scan_t<float, QF32<6>>(a, s);
+            case 8: return launch_scan_t<float, QF32<8>>(a, s);
+            case 12: return launch_scan_t<float, QF32<12>>(a, s);
+            case 16: return launch_scan_t<float, QF32<16>>(a, s);
+            default: break;
+        }
+    }
+    if (f16 && a.d % 128 == 0) {
+        switch (a.d / 128) {
+            case 2: return launch_scan_t<__half, QF16<2>>(a, s);
+            case 3: return launch_scan_t<__half, QF16<3>>(a, s);
+            case 4: return launch_scan_t<__half, QF16<4>>(a, s);
+            case 6: return launch_scan_t<__half, QF16<6>>(a, s);
+            case 8: return launch_scan_t<__half, QF16<8>>(a, s);
+            default: break;
+        }
+    }
+    if (f16) return launch_scan_t<__half, QGeneric>(a, s);
+    return launch_scan_t<float, QGeneric>(a, s);
+}
+
+int launch_finalize(const FinalizeArgs& a, hipStream_t s) {
+    hipLaunchKernelGGL(k_finalize, dim3(1), dim3(kFinThreads), 0, s, a);
+    MARS_HIP(hipGetLastError());
+    return MARS_OK;
+}
+
+int launch_episode(const EpisodeArgs& a, hipStream_t s) {
+    hipLaunchKernelGGL(k_episode, dim3(1), dim3(256), 0, s, a);
+    MARS_HIP(hipGetLastError());
+    return MARS_OK;
+}
+
+int launch_convert_f16(const float* in, __half* out, int64_t count, hipStream_t s) {
+    int64_t blocks = (count / 8 + 255) / 256;
+    if (blocks < 1) blocks = 1;
+    if (blocks > 65536) blocks = 65536;
+    hipLaunchKernelGGL(k_convert_f16, dim3(unsigned(blocks)), dim3(256), 0, s, in, out, count);
+    MARS_HIP(hipGetLastError());
+    return MARS_OK;
+}
+
+}  // namespace mars

@@ -1,0 +1,331 @@
+"""GPU parity: the HIP path (through the C ABI) against the CPU oracle on the
+same seeded inputs.
+
+Bars (written here as the tests apply them):
+  * fused scores:  |gpu - oracle| <= 1e-5 * max(|oracle|, w * sum|e q|)  (fp32; fp16 rows
+                   against the oracle on the same RNE-rounded rows), and <= 2e-3 of the
+                   same scale for the fp16 path against the fp32 oracle;
+  * seeds / results: identical id sets except ids whose oracle score lies within
+                   that tolerance of the cut;
+  * BFS given the GPU's seeds: visit order (ids), hop levels and visited count
+                   bit-exact; BFS scores within the score tolerance;
+  * episode CSR / episode-scoped results: ids and hops exact.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import mars_amd
+import oracle
+from mars_amd import RetrievalConfig, RetrievalScope, corpus
+
+from conftest import RTOL_F16_VS_F32, RTOL_F32
+
+pytestmark = pytest.mark.gpu
+FLT_MAX = float(np.finfo(np.float32).max)
+T_Q = corpus.QUERY_TIME
+LAM = corpus.DECAY_LAMBDA
+
+
+class Dev:
+    def __init__(self, emb, mods, ts, row, col, ep=None, max_k=64, fp16=False):
+        self.n, self.d = emb.shape
+        g = mars_amd.MemoryGraph(self.n, self.d, row, col, emb, mods, ts)
+        self.dg = mars_amd.upload_to_device(g)
+        self.csr = None
+        if ep is not None:
+            mars_amd.upload_episode_ids(self.dg, ep)
+            self.csr = mars_amd.build_episode_csr(ep, self.n)
+            mars_amd.upload_episode_csr(self.dg, self.csr)
+        if fp16:
+            mars_amd.upload_fp16_embeddings(self.dg)
+        self.ctx = mars_amd.create_query_context(self.n, self.d, max_k)
+        self.og = oracle.make_graph(emb, mods, ts, row, col, ep)
+
+    def close(self):
+        mars_amd.destroy_query_context(self.ctx)
+        mars_amd.free_device(self.dg)
+
+    def query(self, q, cfg, t_q=T_Q):
+        st = mars_amd.RetrievalStats()
+        res = mars_amd.query_memory_fast(self.dg, self.ctx, q, t_q, cfg, st)
+        return res, st
+
+
+def ocfg(cfg: RetrievalConfig):
+    return oracle.config(cfg.top_k, cfg.bfs_max_hops, cfg.time_decay_lambda, cfg.bfs_score_decay,
+                         cfg.modality_filter, cfg.max_results_returned, int(cfg.retrieval_scope),
+                         cfg.query_episode_id, cfg.query_episode_member_begin, cfg.query_episode_member_count,
+                         cfg.episode_same_boost)
+
+
+def check_scores(gpu, ref, scale, rtol):
+    bound = rtol * np.maximum(np.abs(ref), scale) + 1e-30
+    filt = ref == -FLT_MAX
+    assert np.all(gpu[filt] == np.float32(-FLT_MAX))
+    err = np.abs(gpu[~filt].astype(np.float64) - ref[~filt])
+    worst = np.max(err / bound[~filt]) if err.size else 0.0
+    assert worst <= 1.0, f"score error {worst:.3f}x the bound"
+
+
+def check_global(dev: Dev, q, cfg: RetrievalConfig, emb16=None, rtol=RTOL_F32):
+    """Full global-query parity for one query; returns the GPU results."""
+    res, st = dev.query(q, cfg)
+    assert st.scope_fallback == 0 or cfg.retrieval_scope == RetrievalScope.EpisodeScoped
+    og = dev.og
+    if emb16 is not None:
+        og = oracle.Graph(og.embeddings, og.modalities, og.timestamps, og.row_offsets, og.col_indices,
+                          og.episode_ids, og.ep_offsets, og.ep_members, emb16)
+    ref = oracle.query(og, q, T_Q, ocfg(cfg))
+    fin_ref = ref["final"]
+    _, scale = oracle.scores(og, q, T_Q, cfg.time_decay_lambda, cfg.modality_filter)
+    tol = rtol * np.maximum(np.abs(fin_ref), scale)
+    # 1) fused scores over all N
+    fin_gpu = dev.ctx.last_scores(dev.n)
+    if cfg.episode_same_boost > 0:
+        scale = scale * (1.0 + cfg.episode_same_boost)
+    check_scores(fin_gpu, fin_ref, scale, rtol)
+    # 2) seeds: same set up to near-ties at the K-th score
+    seeds, seed_vals = dev.ctx.last_seeds()
+    k = ref["k"]
+    assert len(seeds) == min(k, dev.n)
+    kth = fin_ref[ref["seeds"][-1]]
+    diff = set(seeds.tolist()) ^ set(ref["seeds"].tolist())
+    assert all(abs(fin_ref[i] - kth) <= 2 * tol[i] + 2 * tol[ref["seeds"][-1]] for i in diff), diff
+    np.testing.assert_array_equal(seed_vals, fin_gpu[seeds])
+    # seeds come out in (score desc, id asc) order of the GPU's own scores
+    order = np.lexsort((seeds, -seed_vals.astype(np.float64)))
+    np.testing.assert_array_equal(order, np.arange(len(seeds)))
+    # 3) BFS from the GPU's seeds: visit order / hops exact, scores in tolerance
+    ids, hops, vsc = dev.ctx.last_visited()
+    b = oracle.bfs(og.row_offsets, og.col_indices, fin_ref, seeds, fin_ref[seeds],
+                   max(0, cfg.bfs_max_hops), cfg.bfs_score_decay)
+    np.testing.assert_array_equal(ids, b["ids"])
+    np.testing.assert_array_equal(hops, b["hops"])
+    vtol = rtol * np.maximum(np.abs(b["scores"]), np.max(scale)) + 1e-30
+    assert np.all(np.abs(vsc - b["scores"]) <= vtol)
+    assert st.visited == len(ids)
+    # 4) final results: oracle given the same seeds
+    r2 = oracle.query(og, q, T_Q, ocfg(cfg), seeds_in=seeds)
+    want = r2["results"]
+    assert len(res) == len(want) == r2["n_results"]
+    vis_score = dict(zip(b["ids"].tolist(), b["scores"].tolist()))
+    vis_hop = dict(zip(b["ids"].tolist(), b["hops"].tolist()))
+    for j, (r, w) in enumerate(zip(res, want)):
+        if r.node_id != w[0]:
+            assert abs(vis_score[r.node_id] - w[1]) <= 2 * RTOL_F32 * max(abs(w[1]), 1.0), (j, r, w)
+        assert r.hops_from_seed == vis_hop[r.node_id]
+        assert r.modality == int(dev.og.modalities[r.node_id])
+        assert abs(r.score - vis_score[r.node_id]) <= rtol * max(abs(vis_score[r.node_id]), 1.0)
+    return res
+
+
+# ---------------------------------------------------------------- corpus N=10K (CPU plumbing size)
+@pytest.fixture(scope="module")
+def dev10k(corpus_10k):
+    c = corpus_10k
+    d = Dev(c.embeddings, c.modalities, c.timestamps, c.row_offsets, c.col_indices, c.episode_ids, fp16=True)
+    yield d
+    d.close()
+
+
+def test_episode_csr_on_device_matches(dev10k, corpus_10k):
+    off, mem = dev10k.dg.download_episode_csr()
+    want_off, want_mem = oracle.episode_csr(corpus_10k.episode_ids)
+    np.testing.assert_array_equal(off, want_off)
+    np.testing.assert_array_equal(mem, want_mem)
+
+
+def test_global_parity_10k(dev10k, corpus_10k):
+    qs = corpus.pick_queries(corpus_10k.modalities, 60, seed=101)
+    cfg = RetrievalConfig(top_k=10, bfs_max_hops=2, time_decay_lambda=LAM, bfs_score_decay=0.5,
+                          max_results_returned=15)
+    dev10k.ctx.use_fp16 = False
+    for node in qs:
+        check_global(dev10k, corpus_10k.embeddings[node], cfg)
+
+
+def test_global_parity_variants_10k(dev10k, corpus_10k):
+    dev10k.ctx.use_fp16 = False
+    q = corpus_10k.embeddings[corpus.pick_queries(corpus_10k.modalities, 1, seed=7)[0]]
+    for cfg in [
+        RetrievalConfig(top_k=64, bfs_max_hops=2, time_decay_lambda=LAM, max_results_returned=2000),
+        RetrievalConfig(top_k=1, bfs_max_hops=3, time_decay_lambda=LAM),
+        RetrievalConfig(top_k=10, bfs_max_hops=0, time_decay_lambda=LAM),
+        RetrievalConfig(top_k=10, bfs_max_hops=2, time_decay_lambda=1e-8, modality_filter=0),
+        RetrievalConfig(top_k=10, bfs_max_hops=2, time_decay_lambda=LAM, query_episode_id=17,
+                        episode_same_boost=0.5),
+        RetrievalConfig(top_k=200, bfs_max_hops=1, time_decay_lambda=LAM, bfs_score_decay=0.85),
+    ]:
+        check_global(dev10k, q, cfg)
+
+
+def test_episode_parity_10k(dev10k, corpus_10k):
+    qs = corpus.pick_queries(corpus_10k.modalities, 100, seed=202)
+    off = dev10k.csr.ep_csr_offsets
+    for i, node in enumerate(qs):
+        ep = int(corpus_10k.episode_ids[node])
+        k = 15 if i % 2 else 10          # K > M=10 exercises the reference padding
+        cfg = RetrievalConfig(top_k=k, time_decay_lambda=LAM, max_results_returned=15,
+                              retrieval_scope=RetrievalScope.EpisodeScoped, query_episode_id=ep,
+                              query_episode_member_begin=int(off[ep]),
+                              query_episode_member_count=int(off[ep + 1] - off[ep]))
+        res, st = dev10k.query(corpus_10k.embeddings[node], cfg)
+        assert st.scope_fallback == 0 and st.nodes_scanned == 10 and st.bfs_waves == 0
+        ref = oracle.query(dev10k.og, corpus_10k.embeddings[node], T_Q, ocfg(cfg))
+        assert ref["scoped"]
+        assert [r.node_id for r in res] == [w[0] for w in ref["results"]]
+        assert all(r.hops_from_seed == 0 for r in res)
+        for r, w in zip(res, ref["results"]):
+            if w[1] == -FLT_MAX:
+                assert r.score == np.float32(-FLT_MAX)
+            else:
+                assert abs(r.score - w[1]) <= RTOL_F32 * max(abs(w[1]), 1.0)
+        # published outcome: episode-scoped retrieval returns the episode's TEXT and AUDIO
+        mods = {r.modality for r in res if corpus_10k.episode_ids[r.node_id] == ep}
+        assert {0, 1} <= mods
+
+
+def test_episode_invalid_range_falls_back(dev10k, corpus_10k):
+    cfg = RetrievalConfig(top_k=10, time_decay_lambda=LAM, retrieval_scope=RetrievalScope.EpisodeScoped,
+                          query_episode_id=3, query_episode_member_begin=9990, query_episode_member_count=50)
+    res, st = dev10k.query(corpus_10k.embeddings[30], cfg)
+    assert st.scope_fallback == 1 and st.nodes_scanned == 10000 and len(res) == 10
+
+
+def test_fp16_parity_10k(dev10k, corpus_10k):
+    emb16 = oracle.to_f16_bits(corpus_10k.embeddings)
+    dev10k.ctx.use_fp16 = True
+    try:
+        cfg = RetrievalConfig(top_k=10, bfs_max_hops=2, time_decay_lambda=LAM, max_results_returned=15)
+        for node in corpus.pick_queries(corpus_10k.modalities, 20, seed=303):
+            q = corpus_10k.embeddings[node]
+            check_global(dev10k, q, cfg, emb16=emb16)
+            res, st = dev10k.query(q, cfg)
+            assert st.used_fp16 == 1
+            # fp16 path against the fp32 oracle
+            fin32, scale = oracle.scores(dev10k.og, q, T_Q, LAM)
+            check_scores(dev10k.ctx.last_scores(dev10k.n), fin32, scale, RTOL_F16_VS_F32)
+    finally:
+        dev10k.ctx.use_fp16 = False
+
+
+def test_repeat_query_is_stable(dev10k, corpus_10k):
+    cfg = RetrievalConfig(top_k=10, time_decay_lambda=LAM, max_results_returned=50)
+    a, _ = dev10k.query(corpus_10k.embeddings[40], cfg)
+    b, _ = dev10k.query(corpus_10k.embeddings[1240], cfg)
+    c, _ = dev10k.query(corpus_10k.embeddings[40], cfg)
+    assert a == c and a != b
+
+
+def test_device_query_pointer(dev10k, corpus_10k):
+    import torch
+    q = corpus_10k.embeddings[1234]
+    cfg = RetrievalConfig(top_k=10, time_decay_lambda=LAM, max_results_returned=15)
+    host, _ = dev10k.query(q, cfg)
+    t = torch.from_numpy(q.copy()).to("cuda:0")
+    torch.cuda.synchronize()
+    dev_res = mars_amd.query_memory_fast_device(dev10k.dg, dev10k.ctx, t.data_ptr(), T_Q, cfg)
+    assert host == dev_res
+
+
+def test_unsupported_result_count(dev10k, corpus_10k):
+    cfg = RetrievalConfig(top_k=10, max_results_returned=9000)
+    with pytest.raises(mars_amd.MarsError, match="MARS_ERR_UNSUPPORTED"):
+        dev10k.query(corpus_10k.embeddings[0], cfg)
+
+
+# ---------------------------------------------------------------- the reference's own corpus
+def test_reference_kids_corpus(golden):
+    z = np.load(golden / "kids_small.npz")
+    dev = Dev(z["emb"], z["mods"], z["ts"], z["row"], z["col"], z["ep"])
+    try:
+        img = np.nonzero(z["mods"] == 2)[0]
+        off = dev.csr.ep_csr_offsets
+        for node in img[:30]:
+            q, t = z["emb"][node], float(z["ts"][node])
+            ep = int(z["ep"][node])
+            cfg = RetrievalConfig(top_k=15, time_decay_lambda=8e-6, bfs_score_decay=0.55,
+                                  max_results_returned=15)
+            res, st = dev.query(q, cfg, t_q=t)
+            ref = oracle.query(dev.og, q, t, ocfg(cfg), seeds_in=dev.ctx.last_seeds()[0])
+            ids, hops, _ = dev.ctx.last_visited()
+            assert st.visited == ref["visited"] == len(ids)
+            cfg_s = RetrievalConfig(top_k=15, time_decay_lambda=8e-6, max_results_returned=15,
+                                    retrieval_scope=RetrievalScope.EpisodeScoped, query_episode_id=ep,
+                                    query_episode_member_begin=int(off[ep]),
+                                    query_episode_member_count=int(off[ep + 1] - off[ep]))
+            res, st = dev.query(q, cfg_s, t_q=t)
+            ref = oracle.query(dev.og, q, t, ocfg(cfg_s))
+            assert [r.node_id for r in res] == [w[0] for w in ref["results"]]
+            mods = {r.modality for r in res if z["ep"][r.node_id] == ep}
+            assert {0, 1} <= mods                           # published episode hit@15 = 1.0
+    finally:
+        dev.close()
+
+
+# ---------------------------------------------------------------- shapes and edge cases
+def _random_graph(rng, n, d, deg=6, n_ep=None):
+    emb = rng.standard_normal((n, d)).astype(np.float32)
+    emb /= np.linalg.norm(emb, axis=1, keepdims=True)
+    mods = rng.integers(0, 3, size=n).astype(np.int32)
+    ts = rng.uniform(0, 600, size=n).astype(np.float32)
+    ep = (np.arange(n) // 10).astype(np.int32) if n_ep is None else np.sort(rng.integers(0, n_ep, n)).astype(np.int32)
+    knn = rng.integers(0, n, size=(n, deg)).astype(np.int32)
+    row, col = corpus.build_nsn_csr(ep, knn)
+    return emb, mods, ts, row, col, ep
+
+
+@pytest.mark.parametrize("n,d", [(5, 768), (300, 100), (3000, 384), (2000, 1024), (777, 256), (1500, 64)])
+def test_shapes(n, d, rng):
+    emb, mods, ts, row, col, ep = _random_graph(rng, n, d)
+    dev = Dev(emb, mods, ts, row, col, ep, fp16=True)
+    try:
+        for node in (0, n // 2, n - 1):
+            check_global(dev, emb[node], RetrievalConfig(top_k=10, time_decay_lambda=LAM, max_results_returned=20))
+        dev.ctx.use_fp16 = True
+        e16 = oracle.to_f16_bits(emb)
+        check_global(dev, emb[1], RetrievalConfig(top_k=10, time_decay_lambda=LAM), emb16=e16)
+    finally:
+        dev.close()
+
+
+def test_no_edges_graph(rng):
+    n, d = 500, 128
+    emb = rng.standard_normal((n, d)).astype(np.float32)
+    emb /= np.linalg.norm(emb, axis=1, keepdims=True)
+    dev = Dev(emb, np.zeros(n, np.int32), np.zeros(n, np.float32), None, None)
+    try:
+        res = check_global(dev, emb[3], RetrievalConfig(top_k=10, time_decay_lambda=LAM, max_results_returned=30))
+        assert len(res) == 10 and res[0].node_id == 3 and all(r.hops_from_seed == 0 for r in res)
+    finally:
+        dev.close()
+
+
+def test_large_frontier_and_visited(rng):
+    """Hubs: the level-1 frontier exceeds one LDS chunk (4096) and the visited set
+    exceeds the LDS sort (8192), exercising the chunked BFS and radix-select path."""
+    n, d = 60000, 64
+    emb = rng.standard_normal((n, d)).astype(np.float32)
+    emb /= np.linalg.norm(emb, axis=1, keepdims=True)
+    q = emb[0]
+    hubs = np.argsort(-(emb @ q))[:10]
+    edges = [(int(h), int(t)) for h in hubs for t in rng.choice(n, 800, replace=False)]
+    edges += [(int(a), int(b)) for a, b in rng.integers(0, n, size=(60000, 2))]
+    adj = [set() for _ in range(n)]
+    for a, b in edges:
+        if a != b:
+            adj[a].add(b)
+            adj[b].add(a)
+    row = np.zeros(n + 1, np.int32)
+    row[1:] = np.cumsum([len(s) for s in adj])
+    col = np.concatenate([np.array(sorted(s), np.int32) for s in adj])
+    dev = Dev(emb, rng.integers(0, 3, n).astype(np.int32), rng.uniform(0, 600, n).astype(np.float32), row, col)
+    try:
+        cfg = RetrievalConfig(top_k=10, bfs_max_hops=2, time_decay_lambda=LAM, max_results_returned=5000)
+        check_global(dev, q, cfg)
+        _, st = dev.query(q, cfg)
+        assert st.visited > 8192
+    finally:
+        dev.close()
