@@ -38,27 +38,6 @@ def pctl(v, p):
     return float(v[int(p * (len(v) - 1))]) if len(v) else 0.0
 
 
-def knn_gpu(emb: np.ndarray, k: int):
-    """8-NN of the corpus for the benchmark graph (setup, outside the timed region)."""
-    import torch
-    E = torch.from_numpy(emb).to("cuda:0")
-    n = E.shape[0]
-    out = np.empty((n, k), np.int32)
-    step = 2048
-    for s in range(0, n, step):
-        e = min(n, s + step)
-        S = E[s:e] @ E.T
-        r = torch.arange(e - s, device=S.device)
-        S[r, s + r] = -float("inf")
-        _, idx = torch.topk(S, k, dim=1)
-        out[s:e] = idx.to(torch.int32).cpu().numpy()
-        del S
-    del E
-    torch.cuda.synchronize()
-    torch.cuda.empty_cache()
-    return out
-
-
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -77,7 +56,6 @@ def main() -> int:
               "(the path would shard by node range, see DESIGN.md)", file=sys.stderr)
         return 2
 
-    import torch
     import mars_amd
     from mars_amd import RetrievalConfig, RetrievalScope, corpus
     from mars_amd._lib import RetrievalConfigC, check, lib
@@ -88,7 +66,7 @@ def main() -> int:
     c = corpus.make_corpus(N, D, seed=args.seed)
     log(f"corpus N={N} D={D} seed={args.seed}: {time.time() - t:.1f}s")
     t = time.time()
-    knn = knn_gpu(c.embeddings, corpus.KNN_K) if N > 20000 else corpus.knn_cpu(c.embeddings, corpus.KNN_K)[0]
+    knn = corpus.knn(c.embeddings, corpus.KNN_K)
     corpus.nsn_graph(c, knn)
     log(f"NSN graph: {len(c.col_indices)} directed edges, avg degree {len(c.col_indices) / N:.1f}: "
         f"{time.time() - t:.1f}s")
@@ -102,8 +80,7 @@ def main() -> int:
 
     nq = args.steps + args.warmup
     qnodes = corpus.pick_queries(c.modalities, nq, seed=args.query_seed)
-    dq = torch.from_numpy(c.embeddings[qnodes]).to("cuda:0").contiguous()
-    torch.cuda.synchronize()
+    dq = mars_amd.DeviceBuffer.from_array(c.embeddings[qnodes])
 
     gcfg = RetrievalConfig(top_k=K, bfs_max_hops=2, time_decay_lambda=corpus.DECAY_LAMBDA, bfs_score_decay=0.5)
     off = csr.ep_csr_offsets
@@ -123,13 +100,11 @@ def main() -> int:
         kern = np.zeros(count, np.float32)
         bfs = np.zeros(count, np.float32)
         nres = np.zeros(count, np.int32)
-        ptr = dq.data_ptr() + first * D * 4
-        torch.cuda.synchronize()
+        ptr = dq.ptr + first * D * 4
         check(lib.mars_bench_queries(dg.handle, ctx.handle, C.c_void_p(ptr), D, count,
                                      C.c_float(corpus.QUERY_TIME), cfgs, n_cfg, C.c_void_p(lat.ctypes.data),
                                      C.c_void_p(kern.ctypes.data), C.c_void_p(bfs.ctypes.data),
                                      C.c_void_p(nres.ctypes.data)), "mars_bench_queries")
-        torch.cuda.synchronize()
         assert np.all(nres == K), "every query must return K results"
         return lat, kern, bfs
 
@@ -214,6 +189,7 @@ def main() -> int:
                                          f"vectors), fp64 C++ oracle with OpenMP over rows; p99 of {nc}",
                                "p50_us": round(pctl(cl, .5), 1)}
         log(f"cpu oracle ({res['cpu_baseline']['cores']} threads): p50 {pctl(cl, .5):.0f} us p99 {pctl(cl, .99):.0f} us")
+    dq.free()
     mars_amd.destroy_query_context(ctx)
     mars_amd.free_device(dg)
     print(json.dumps(res), flush=True)

@@ -191,6 +191,15 @@ int mars_ctx_last_seeds(mars_ctx* ctx, int32_t* h_idx, float* h_val, int32_t k, 
 int mars_ctx_last_visited(mars_ctx* ctx, int32_t* h_ids, int32_t* h_hops, float* h_scores,
                           int32_t cap, int32_t* n_out);
 
+/* ---- device memory helpers ----------------------------------------------------------
+ * Device buffers for callers that hold no HIP runtime of their own (e.g. the ctypes
+ * benchmark; a second HIP runtime in the same process, such as the one bundled with
+ * a Python framework, must not be mixed with this library's). */
+int mars_device_alloc(size_t bytes, void** ptr);
+int mars_device_free(void* ptr);
+int mars_copy_to_device(void* dst, const void* src, size_t bytes);
+int mars_copy_to_host(void* dst, const void* src, size_t bytes);
+
 /* ---- benchmark loop (harness semantics of src/latency_bench.cu:355-393) ------------ */
 /* Runs n single queries back to back, query i reading the device vector
  * d_queries + i*stride with configuration cfgs[n_cfg == 1 ? 0 : i]. lat_us[i]

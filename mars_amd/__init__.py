@@ -31,7 +31,7 @@ __all__ = [
     "HostEpisodeCSR", "DeviceMemoryGraph", "QueryContext", "build_episode_csr", "upload_to_device",
     "upload_episode_ids", "upload_episode_csr", "upload_fp16_embeddings", "free_fp16_embeddings",
     "free_device", "create_query_context", "destroy_query_context", "query_memory_fast",
-    "query_memory_fast_device", "init", "MarsError", "corpus",
+    "query_memory_fast_device", "init", "MarsError", "corpus", "DeviceBuffer",
 ]
 
 MOD_TEXT, MOD_AUDIO, MOD_IMAGE = 0, 1, 2
@@ -321,6 +321,39 @@ def query_memory_fast_device(dg: DeviceMemoryGraph, ctx: QueryContext, d_query_p
     if stats is not None:
         stats._fill(st)
     return _results(ctx, n.value)
+
+
+class DeviceBuffer:
+    """Device memory owned by libmars_amd's HIP runtime (holds e.g. query vectors)."""
+
+    def __init__(self, nbytes: int):
+        p = C.c_void_p()
+        check(lib.mars_device_alloc(int(nbytes), C.byref(p)), "mars_device_alloc")
+        self.ptr = p.value
+        self.nbytes = int(nbytes)
+
+    @classmethod
+    def from_array(cls, a: np.ndarray) -> "DeviceBuffer":
+        a = np.ascontiguousarray(a)
+        b = cls(a.nbytes)
+        check(lib.mars_copy_to_device(C.c_void_p(b.ptr), C.c_void_p(a.ctypes.data), a.nbytes), "mars_copy_to_device")
+        return b
+
+    def to_array(self, dtype, count: int) -> np.ndarray:
+        out = np.empty(count, dtype)
+        check(lib.mars_copy_to_host(C.c_void_p(out.ctypes.data), C.c_void_p(self.ptr), out.nbytes), "mars_copy_to_host")
+        return out
+
+    def free(self) -> None:
+        if self.ptr:
+            check(lib.mars_device_free(C.c_void_p(self.ptr)), "mars_device_free")
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
 
 
 from . import corpus  # noqa: E402  (needs lib)

@@ -63,6 +63,11 @@ def knn_cpu(emb: np.ndarray, k: int = KNN_K, threads: int = 0):
     return nb, sims
 
 
+def knn(emb: np.ndarray, k: int = KNN_K, threads: int = 0) -> np.ndarray:
+    """k-NN ids of every row: exact CPU k-NN (the GPU builder takes over where available)."""
+    return knn_cpu(emb, k, threads)[0]
+
+
 def build_nsn_csr(episode_ids: np.ndarray, knn: np.ndarray, threads: int = 0):
     ep = np.ascontiguousarray(episode_ids, np.int32)
     knn = np.ascontiguousarray(knn, np.int32)

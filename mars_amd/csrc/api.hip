@@ -487,6 +487,32 @@ int mars_query_device(const mars_graph* g, mars_ctx* c, const float* d_query, fl
     return query_impl(g, c, nullptr, d_query, t_q, cfg, out, cap, n_out, stats);
 }
 
+int mars_device_alloc(size_t bytes, void** ptr) {
+    MARS_CHECK(ptr, MARS_ERR_INVALID, "null argument");
+    *ptr = nullptr;
+    MARS_TRY(ensure_device(nullptr));
+    hipError_t e = hipMalloc(ptr, bytes ? bytes : 1);
+    if (e != hipSuccess) return set_error(MARS_ERR_NOMEM, "hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
+    return MARS_OK;
+}
+
+int mars_device_free(void* ptr) {
+    if (ptr) MARS_HIP(hipFree(ptr));
+    return MARS_OK;
+}
+
+int mars_copy_to_device(void* dst, const void* src, size_t bytes) {
+    MARS_CHECK(dst && src, MARS_ERR_INVALID, "null argument");
+    MARS_HIP(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
+    return MARS_OK;
+}
+
+int mars_copy_to_host(void* dst, const void* src, size_t bytes) {
+    MARS_CHECK(dst && src, MARS_ERR_INVALID, "null argument");
+    MARS_HIP(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
+    return MARS_OK;
+}
+
 int mars_bench_queries(const mars_graph* g, mars_ctx* c, const float* dq, int64_t stride, int32_t n, float t_q,
                        const mars_retrieval_config* cfgs, int32_t n_cfg, double* lat_us, float* kern_us,
                        float* bfs_us, int32_t* n_res) {

@@ -172,8 +172,8 @@ def topk(fin: np.ndarray, k: int):
 
 
 def bfs(row, col, fin, seeds, seed_vals, hops: int, decay: float):
-    row = np.ascontiguousarray(row, np.int32)
-    col = np.ascontiguousarray(col, np.int32)
+    row = None if row is None else np.ascontiguousarray(row, np.int32)
+    col = None if col is None else np.ascontiguousarray(col, np.int32)
     fin = np.ascontiguousarray(fin, np.float64)
     seeds = np.ascontiguousarray(seeds, np.int32)
     seed_vals = np.ascontiguousarray(seed_vals, np.float64)

@@ -220,13 +220,13 @@ def test_repeat_query_is_stable(dev10k, corpus_10k):
 
 
 def test_device_query_pointer(dev10k, corpus_10k):
-    import torch
     q = corpus_10k.embeddings[1234]
     cfg = RetrievalConfig(top_k=10, time_decay_lambda=LAM, max_results_returned=15)
     host, _ = dev10k.query(q, cfg)
-    t = torch.from_numpy(q.copy()).to("cuda:0")
-    torch.cuda.synchronize()
-    dev_res = mars_amd.query_memory_fast_device(dev10k.dg, dev10k.ctx, t.data_ptr(), T_Q, cfg)
+    buf = mars_amd.DeviceBuffer.from_array(q)
+    np.testing.assert_array_equal(buf.to_array(np.float32, q.size), q)
+    dev_res = mars_amd.query_memory_fast_device(dev10k.dg, dev10k.ctx, buf.ptr, T_Q, cfg)
+    buf.free()
     assert host == dev_res
 
 
@@ -321,7 +321,8 @@ def test_large_frontier_and_visited(rng):
     row = np.zeros(n + 1, np.int32)
     row[1:] = np.cumsum([len(s) for s in adj])
     col = np.concatenate([np.array(sorted(s), np.int32) for s in adj])
-    dev = Dev(emb, rng.integers(0, 3, n).astype(np.int32), rng.uniform(0, 600, n).astype(np.float32), row, col)
+    # every memory at the query time: no decay, so the seeds are exactly the hubs
+    dev = Dev(emb, rng.integers(0, 3, n).astype(np.int32), np.full(n, T_Q, np.float32), row, col)
     try:
         cfg = RetrievalConfig(top_k=10, bfs_max_hops=2, time_decay_lambda=LAM, max_results_returned=5000)
         check_global(dev, q, cfg)
