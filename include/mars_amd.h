@@ -155,6 +155,15 @@ int mars_graph_set_episode_csr(mars_graph* g, int32_t num_episodes,
 int mars_graph_enable_fp16(mars_graph* g);
 int mars_graph_disable_fp16(mars_graph* g);
 int mars_graph_get_view(const mars_graph* g, mars_graph_view* out);
+/* Replace the NSN CSR of a graph (host arrays, validated like mars_graph_create). */
+int mars_graph_set_csr(mars_graph* g, int32_t num_edges, const int32_t* row_offsets,
+                       const int32_t* col_indices);
+/* k nearest neighbours of every node by cosine (the node itself excluded, ties: lower
+ * id): an fp16 MFMA scan keeps 16 candidates per node, exact fp32 rescoring keeps
+ * k <= 16. Needs the fp16 copy. nbrs: host, num_nodes * k ids. Builds the k-NN part
+ * of the NSN graph at corpus sizes a CPU cannot (analogue of the tiled kNN build of
+ * src/cmng_build.cu:135-245). */
+int mars_graph_knn(mars_graph* g, int32_t k, int32_t* nbrs);
 /* Copy device arrays back to host (any pointer may be NULL to skip). */
 int mars_graph_download(const mars_graph* g, int32_t* row_offsets, int32_t* col_indices,
                         int32_t* ep_offsets, int32_t* ep_members);
@@ -181,6 +190,17 @@ int mars_query(const mars_graph* g, mars_ctx* ctx, const float* h_query, float t
 int mars_query_device(const mars_graph* g, mars_ctx* ctx, const float* d_query, float t_q,
                       const mars_retrieval_config* cfg, mars_query_result* out,
                       int32_t cap, int32_t* n_out, mars_stats* stats);
+
+/* Batched global scoring: Q query vectors in device memory (row-major Q x embedding_dim
+ * fp32), query i at time t_q[i] (host array), decay / modality filter from cfg, top-K
+ * (cfg->top_k <= 16) per query over the fp16 corpus (mars_graph_enable_fp16) on MFMA
+ * fp16 tiles with fp32 accumulation. No BFS, no episode scope: each row of the
+ * output is the seed list the Q=1 global path would select (scores within the fp16
+ * tolerance). out_ids / out_scores: host, Q x top_k, each row sorted (score desc,
+ * id asc). Reference analogue: none (wmma_similarity.cu:55-138 scores one query). */
+int mars_query_batch(const mars_graph* g, mars_ctx* ctx, const float* d_queries, int32_t Q,
+                     const float* t_q, const mars_retrieval_config* cfg, int32_t* out_ids,
+                     float* out_scores, mars_stats* stats);
 
 /* Debug / parity hooks: copy the last query's per-node fp32 scores (N floats) and
  * its seed list (top-K ids and scores, K entries) to host memory. */

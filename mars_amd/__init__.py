@@ -31,7 +31,7 @@ __all__ = [
     "HostEpisodeCSR", "DeviceMemoryGraph", "QueryContext", "build_episode_csr", "upload_to_device",
     "upload_episode_ids", "upload_episode_csr", "upload_fp16_embeddings", "free_fp16_embeddings",
     "free_device", "create_query_context", "destroy_query_context", "query_memory_fast",
-    "query_memory_fast_device", "init", "MarsError", "corpus", "DeviceBuffer",
+    "query_memory_fast_device", "init", "MarsError", "corpus", "DeviceBuffer", "query_batch", "graph_knn", "set_csr",
 ]
 
 MOD_TEXT, MOD_AUDIO, MOD_IMAGE = 0, 1, 2
@@ -203,6 +203,13 @@ def upload_to_device(g: MemoryGraph, capacity_nodes: int = 0, capacity_edges: in
     return DeviceMemoryGraph(h, int(g.num_nodes), ne, int(g.embedding_dim))
 
 
+def set_csr(dg: DeviceMemoryGraph, row_offsets, col_indices) -> None:
+    """Replace the graph's NSN CSR (validated)."""
+    row, col = _i32(row_offsets), _i32(col_indices)
+    check(lib.mars_graph_set_csr(dg.handle, len(col), _ptr(row), _ptr(col) if len(col) else None), "mars_graph_set_csr")
+    dg.num_edges = len(col)
+
+
 def upload_episode_ids(dg: DeviceMemoryGraph, episode_ids) -> None:
     ids = _i32(episode_ids)
     check(lib.mars_graph_set_episode_ids(dg.handle, _ptr(ids), len(ids)), "upload_episode_ids")
@@ -321,6 +328,28 @@ def query_memory_fast_device(dg: DeviceMemoryGraph, ctx: QueryContext, d_query_p
     if stats is not None:
         stats._fill(st)
     return _results(ctx, n.value)
+
+
+def query_batch(dg: DeviceMemoryGraph, ctx: QueryContext, d_queries_ptr: int, n_queries: int, t_q,
+                cfg: RetrievalConfig, stats: Optional[RetrievalStats] = None):
+    """Batched global scoring (fp16 MFMA): returns (ids, scores), each (Q, top_k)."""
+    tq = np.ascontiguousarray(np.broadcast_to(np.asarray(t_q, np.float32), (n_queries,)))
+    ids = np.empty((n_queries, cfg.top_k), np.int32)
+    sc = np.empty((n_queries, cfg.top_k), np.float32)
+    st = _lib.StatsC()
+    c = cfg.to_c()
+    check(lib.mars_query_batch(dg.handle, ctx.handle, C.c_void_p(d_queries_ptr), int(n_queries), _ptr(tq), C.byref(c),
+                               _ptr(ids), _ptr(sc), C.byref(st)), "mars_query_batch")
+    if stats is not None:
+        stats._fill(st)
+    return ids, sc
+
+
+def graph_knn(dg: DeviceMemoryGraph, k: int = 8) -> np.ndarray:
+    """k nearest neighbours of every node (fp16 MFMA candidates + exact fp32 rescoring)."""
+    out = np.empty((dg.num_nodes, k), np.int32)
+    check(lib.mars_graph_knn(dg.handle, int(k), _ptr(out)), "mars_graph_knn")
+    return out
 
 
 class DeviceBuffer:

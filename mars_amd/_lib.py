@@ -144,6 +144,9 @@ SIGNATURES = {
     "mars_query_device": (C.c_int, [VP, VP, VP, C.c_float, C.POINTER(RetrievalConfigC), VP, I32, PI32,
                                     C.POINTER(StatsC)]),
     "mars_ctx_last_scores": (C.c_int, [VP, VP, I64]),
+    "mars_query_batch": (C.c_int, [VP, VP, VP, I32, VP, C.POINTER(RetrievalConfigC), VP, VP, C.POINTER(StatsC)]),
+    "mars_graph_knn": (C.c_int, [VP, I32, VP]),
+    "mars_graph_set_csr": (C.c_int, [VP, I32, VP, VP]),
     "mars_ctx_last_seeds": (C.c_int, [VP, VP, VP, I32, PI32]),
     "mars_ctx_last_visited": (C.c_int, [VP, VP, VP, VP, I32, PI32]),
     "mars_device_alloc": (C.c_int, [C.c_size_t, C.POINTER(VP)]),

@@ -11,6 +11,7 @@
 #include "internal.hpp"
 
 #include <algorithm>
+#include <cfloat>
 #include <chrono>
 #include <cstdarg>
 #include <cstring>
@@ -128,6 +129,7 @@ int ctx_free(Ctx& c) {
     if (c.stream) (void)hipStreamSynchronize(c.stream);
     dfree(c.query); dfree(c.fin); dfree(c.part); dfree(c.vis); dfree(c.claim); dfree(c.vlist);
     dfree(c.vhop); dfree(c.vscore); dfree(c.sortbuf); dfree(c.seed_idx); dfree(c.seed_val);
+    dfree(c.bq); dfree(c.btq); dfree(c.bpart); dfree(c.bout);
     if (c.h_query) (void)hipHostFree(c.h_query);
     if (c.h_res) (void)hipHostFree(c.h_res);
     for (auto& e : c.ev) if (e) (void)hipEventDestroy(e);
@@ -243,6 +245,37 @@ int query_impl(const mars_graph* gh, mars_ctx* ch, const float* h_q, const float
     return MARS_OK;
 }
 
+// Row ranges x query blocks for the batched scan: one 512-thread workgroup per CU
+// (256 CUs), all query blocks of a row range on one XCD.
+void batch_grid(int64_t n, int32_t q, int32_t* n_rranges, int32_t* n_qblocks, int64_t* rows_per_range) {
+    const int32_t qblocks = (q + 63) / 64;
+    int32_t rr = std::max(8, (256 / std::max(qblocks, 1)) / 8 * 8);
+    const int64_t max_rr = std::max<int64_t>(1, (n + 15) / 16);      // at least one tile per range
+    if (rr > max_rr) rr = int32_t(max_rr);
+    *n_rranges = rr;
+    *n_qblocks = qblocks;
+    *rows_per_range = ((n + rr - 1) / rr + 15) / 16 * 16;
+    *n_rranges = int32_t((n + *rows_per_range - 1) / *rows_per_range);
+}
+
+int ensure_batch_scratch(Ctx& c, int32_t q, int64_t part_keys) {
+    if (q > c.bcap_q) {
+        dfree(c.bq); dfree(c.btq); dfree(c.bout);
+        c.bcap_q = 0;
+        MARS_TRY(dmalloc(&c.bq, size_t(q) * size_t(c.d)));
+        MARS_TRY(dmalloc(&c.btq, size_t(q)));
+        MARS_TRY(dmalloc(&c.bout, size_t(q) * 16));
+        c.bcap_q = q;
+    }
+    if (part_keys > c.bcap_part) {
+        dfree(c.bpart);
+        c.bcap_part = 0;
+        MARS_TRY(dmalloc(&c.bpart, size_t(part_keys)));
+        c.bcap_part = part_keys;
+    }
+    return MARS_OK;
+}
+
 }  // namespace
 }  // namespace mars
 
@@ -321,6 +354,25 @@ int mars_graph_destroy(mars_graph* gh) {
     if (!gh) return MARS_OK;
     graph_free(gh->g);
     delete gh;
+    return MARS_OK;
+}
+
+int mars_graph_set_csr(mars_graph* gh, int32_t ne, const int32_t* row, const int32_t* col) {
+    MARS_CHECK(gh && ne >= 0, MARS_ERR_INVALID, "bad arguments");
+    Graph& g = gh->g;
+    MARS_TRY(validate_csr(g.n, ne, row, col));
+    MARS_TRY(use_device(g.device));
+    if (int64_t(ne) > g.cap_e) {
+        int32_t* ncol = nullptr;
+        MARS_TRY(dmalloc(&ncol, size_t(ne)));
+        dfree(g.col);
+        g.col = ncol;
+        g.cap_e = ne;
+    }
+    if (row) MARS_HIP(hipMemcpy(g.row, row, (size_t(g.n) + 1) * sizeof(int32_t), hipMemcpyHostToDevice));
+    else MARS_HIP(hipMemset(g.row, 0, (size_t(g.n) + 1) * sizeof(int32_t)));
+    if (ne > 0) MARS_HIP(hipMemcpy(g.col, col, size_t(ne) * sizeof(int32_t), hipMemcpyHostToDevice));
+    g.e = ne;
     return MARS_OK;
 }
 
@@ -533,6 +585,105 @@ int mars_bench_queries(const mars_graph* g, mars_ctx* c, const float* dq, int64_
         if (n_res) n_res[i] = nr;
     }
     return MARS_OK;
+}
+
+int mars_query_batch(const mars_graph* gh, mars_ctx* ch, const float* dq, int32_t Q, const float* h_tq,
+                     const mars_retrieval_config* cfg, int32_t* out_ids, float* out_scores, mars_stats* stats) {
+    const auto t0 = std::chrono::steady_clock::now();
+    MARS_CHECK(gh && ch && dq && h_tq && cfg && out_ids && out_scores && Q > 0, MARS_ERR_INVALID, "bad arguments");
+    const Graph& g = gh->g;
+    Ctx& c = ch->c;
+    MARS_CHECK(g.d == c.d, MARS_ERR_INVALID, "graph dim %d != context dim %d", g.d, c.d);
+    MARS_CHECK(g.emb16 != nullptr, MARS_ERR_UNSUPPORTED, "batched scoring reads the fp16 corpus: enable it first");
+    MARS_CHECK(batch_dim_supported(g.d), MARS_ERR_UNSUPPORTED, "batched scoring: embedding_dim %d unsupported", g.d);
+    MARS_CHECK(cfg->top_k >= 1 && cfg->top_k <= 16, MARS_ERR_UNSUPPORTED, "batched top_k %d not in [1, 16]",
+               cfg->top_k);
+    MARS_TRY(use_device(c.device));
+    const int32_t K = cfg->top_k;
+    int32_t nrr = 0, nqb = 0;
+    int64_t rpr = 0;
+    batch_grid(g.n, Q, &nrr, &nqb, &rpr);
+    const int32_t kp = batch_kpart(K);
+    MARS_TRY(ensure_batch_scratch(c, Q, int64_t(nqb) * nrr * 64 * kp));
+    hipStream_t s = c.stream;
+    MARS_HIP(hipMemcpyAsync(c.btq, h_tq, size_t(Q) * sizeof(float), hipMemcpyHostToDevice, s));
+    MARS_TRY(launch_f32_to_f16_rows(dq, c.bq, int64_t(Q) * g.d, s));
+    const bool timing = (c.flags & MARS_CTX_TIMING) != 0;
+    if (timing) MARS_HIP(hipEventRecord(c.ev[0], s));
+    BatchArgs a{};
+    a.emb16 = g.emb16; a.n = g.n; a.d = g.d; a.qh = c.bq; a.q = Q; a.tq = c.btq; a.ts = g.ts; a.mods = g.mods;
+    a.lambda = cfg->time_decay_lambda; a.mod_filter = cfg->modality_filter; a.k = K; a.self_base = -1;
+    a.part = c.bpart; a.rows_per_range = rpr; a.n_rranges = nrr; a.n_qblocks = nqb;
+    MARS_TRY(launch_batch_scan(a, s));
+    if (timing) MARS_HIP(hipEventRecord(c.ev[1], s));
+    MARS_TRY(launch_batch_merge(c.bpart, nrr, kp, Q, K, c.bout, s));
+    if (timing) MARS_HIP(hipEventRecord(c.ev[2], s));
+    std::vector<uint64_t> keys(size_t(Q) * K);
+    MARS_HIP(hipMemcpyAsync(keys.data(), c.bout, keys.size() * sizeof(uint64_t), hipMemcpyDeviceToHost, s));
+    MARS_HIP(hipStreamSynchronize(s));
+    for (size_t i = 0; i < keys.size(); ++i) {
+        out_ids[i] = keys[i] == kEmptyKey ? -1 : key_id(keys[i]);
+        out_scores[i] = keys[i] == kEmptyKey ? -FLT_MAX : key_score(keys[i]);
+    }
+    if (stats) {
+        mars_stats st{};
+        if (timing) {
+            float ms = 0.0f;
+            MARS_HIP(hipEventElapsedTime(&ms, c.ev[0], c.ev[1]));
+            st.gpu_ms_similarity = ms;
+            MARS_HIP(hipEventElapsedTime(&ms, c.ev[1], c.ev[2]));
+            st.gpu_ms_topk = ms;
+            MARS_HIP(hipEventElapsedTime(&ms, c.ev[0], c.ev[2]));
+            st.gpu_ms_total = ms;
+        }
+        st.nodes_scanned = g.n;
+        st.used_fp16 = 1;
+        st.wall_us = std::chrono::duration<double, std::micro>(std::chrono::steady_clock::now() - t0).count();
+        *stats = st;
+    }
+    return MARS_OK;
+}
+
+int mars_graph_knn(mars_graph* gh, int32_t k, int32_t* nbrs) {
+    MARS_CHECK(gh && nbrs && k >= 1 && k <= 16, MARS_ERR_INVALID, "k-NN: bad arguments (k=%d)", k);
+    Graph& g = gh->g;
+    MARS_CHECK(g.emb16 != nullptr, MARS_ERR_UNSUPPORTED, "k-NN reads the fp16 corpus: enable it first");
+    MARS_CHECK(batch_dim_supported(g.d), MARS_ERR_UNSUPPORTED, "k-NN: embedding_dim %d unsupported", g.d);
+    MARS_TRY(use_device(g.device));
+    constexpr int32_t kChunk = 1024;                 // queries per launch (16 query blocks)
+    constexpr int32_t kCand = 16;
+    int32_t nrr = 0, nqb = 0;
+    int64_t rpr = 0;
+    batch_grid(g.n, kChunk, &nrr, &nqb, &rpr);
+    float* tq = nullptr; uint64_t* part = nullptr; uint64_t* cand = nullptr; int32_t* dn = nullptr;
+    hipStream_t s = nullptr;
+    int rc = MARS_OK;
+    auto cleanup = [&]() { dfree(tq); dfree(part); dfree(cand); dfree(dn); if (s) (void)hipStreamDestroy(s); };
+    if ((rc = dmalloc(&tq, kChunk)) || (rc = dmalloc(&part, size_t(nqb) * nrr * 64 * kCand)) ||
+        (rc = dmalloc(&cand, size_t(kChunk) * kCand)) || (rc = dmalloc(&dn, size_t(g.n) * k))) {
+        cleanup();
+        return rc;
+    }
+    hipError_t e = hipStreamCreateWithFlags(&s, hipStreamNonBlocking);
+    if (e == hipSuccess) e = hipMemsetAsync(tq, 0, kChunk * sizeof(float), s);
+    if (e != hipSuccess) { cleanup(); return set_error(MARS_ERR_HIP, "k-NN setup: %s", hipGetErrorString(e)); }
+    for (int64_t q0 = 0; q0 < g.n && rc == MARS_OK; q0 += kChunk) {
+        const int32_t q = int32_t(std::min<int64_t>(kChunk, g.n - q0));
+        BatchArgs a{};
+        a.emb16 = g.emb16; a.n = g.n; a.d = g.d; a.qh = g.emb16 + q0 * g.d; a.q = q; a.tq = tq; a.ts = g.ts;
+        a.mods = g.mods; a.lambda = 0.0f; a.mod_filter = -1; a.k = kCand; a.self_base = q0; a.part = part;
+        a.rows_per_range = rpr; a.n_rranges = nrr; a.n_qblocks = (q + 63) / 64;
+        rc = launch_batch_scan(a, s);
+        if (rc == MARS_OK) rc = launch_batch_merge(part, nrr, kCand, q, kCand, cand, s);
+        if (rc == MARS_OK) rc = launch_knn_rerank(g.emb, q0, q, g.d, cand, kCand, k, dn + q0 * k, s);
+    }
+    if (rc == MARS_OK) {
+        e = hipStreamSynchronize(s);
+        if (e == hipSuccess) e = hipMemcpy(nbrs, dn, size_t(g.n) * k * sizeof(int32_t), hipMemcpyDeviceToHost);
+        if (e != hipSuccess) rc = set_error(MARS_ERR_HIP, "k-NN: %s", hipGetErrorString(e));
+    }
+    cleanup();
+    return rc;
 }
 
 int mars_ctx_last_scores(mars_ctx* ch, float* h, int64_t n) {

@@ -1,0 +1,302 @@
+// ============================================================================
+//  batch.hip — batched scoring on MFMA (gfx950 v_mfma_f32_16x16x32_f16) with
+//  fused temporal decay and per-query top-K; the k-NN graph builder on top.
+//
+//  k_batch_scan  C[q][row] = <Qh_q, E16_row> for 64 queries x 16-row tiles.
+//                Queries live in LDS in MFMA A-fragment order (one 16-byte LDS
+//                read per lane per fragment, conflict free); corpus fragments are
+//                16-byte global loads straight into registers (the B operand is
+//                K-contiguous, like the A operand, so no transpose is needed).
+//                The 16x64 score tile goes through a per-wave LDS stage, after
+//                which lane j owns query j: it applies the decay / filter and
+//                keeps a sorted register list of the K best keys (score desc,
+//                id asc). Workgroup (row range r, query block b) writes K keys per
+//                query; the workgroup index puts all query blocks of a row range
+//                on the same XCD (id % 8 == r % 8) so they share its L2.
+//  k_batch_merge One wave per query merges the per-row-range keys.
+//  k_knn_rerank  Exact fp32 rescoring of k-NN candidates (16-lane group per node).
+//
+//  Reference analogue: wmma_mma_similarity_kernel / wmma_similarity_kernel
+//  (src/wmma_similarity.cu:55-138), which score one query and are never called.
+// ============================================================================
+#include "internal.hpp"
+
+#include <cfloat>
+
+namespace mars {
+namespace {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kBQ = 64;        // queries per workgroup (4 MFMA row tiles of 16)
+constexpr int kBWaves = 8;     // waves per workgroup
+constexpr int kTile = 16;      // corpus rows per MFMA tile
+
+// Orders this wave's LDS writes before its later LDS reads (the staging buffers
+// are private to one wave; waves run different trip counts, so no block barrier).
+__device__ inline void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+template <int K>
+__device__ inline void reg_insert(uint64_t (&list)[K], uint64_t x) {
+    // list ascending; x < list[K-1] is checked by the caller
+    uint64_t v = x;
+#pragma unroll
+    for (int j = 0; j < K; ++j) {
+        const uint64_t lo = list[j] < v ? list[j] : v;
+        const uint64_t hi = list[j] < v ? v : list[j];
+        list[j] = lo;
+        v = hi;
+    }
+}
+
+template <int KCH, int K>
+struct BatchLds {
+    static constexpr size_t kQBytes = size_t(4) * KCH * 64 * 16;
+    static constexpr size_t kListBytes = size_t(kBWaves) * 64 * K * 8;
+    static constexpr size_t kBytes = kQBytes > kListBytes ? kQBytes : kListBytes;
+};
+
+template <int KCH, int K>
+__global__ __launch_bounds__(kBWaves * 64) void k_batch_scan(BatchArgs a) {
+    // query A-fragments [4][KCH][64] (16 B each); after the scan, the per-wave lists
+    __shared__ __attribute__((aligned(16))) unsigned char s_raw[BatchLds<KCH, K>::kBytes];
+    u32x4 (*s_q)[KCH][64] = reinterpret_cast<u32x4 (*)[KCH][64]>(s_raw);
+    __shared__ float s_stage[kBWaves][kTile][kBQ + 1];  // per-wave score tile (+1: bank spread)
+    __shared__ float s_ts[kBWaves][kTile];
+    __shared__ int32_t s_mod[kBWaves][kTile];
+    const int lane = int(threadIdx.x & 63u), wave = int(threadIdx.x >> 6);
+    const int m = lane & 15, kg = lane >> 4;
+    const int r_id = int(blockIdx.x) % a.n_rranges;
+    const int qb = int(blockIdx.x) / a.n_rranges;
+    const int d = KCH * 32;
+
+    // stage this block's 64 queries (zero rows past the batch)
+    for (int idx = int(threadIdx.x); idx < 4 * KCH * 64; idx += kBWaves * 64) {
+        const int l = idx & 63, ks = (idx >> 6) % KCH, qt = idx / (64 * KCH);
+        const int qrow = qb * kBQ + qt * 16 + (l & 15);
+        u32x4 v = {0u, 0u, 0u, 0u};
+        if (qrow < a.q)
+            v = *reinterpret_cast<const u32x4*>(a.qh + int64_t(qrow) * d + ks * 32 + (l >> 4) * 8);
+        s_q[qt][ks][l] = v;
+    }
+    __syncthreads();
+
+    // lane j owns query (qb*64 + j)
+    const int myq = qb * kBQ + lane;
+    const bool qvalid = myq < a.q;
+    const float tq = qvalid ? a.tq[myq] : 0.0f;
+    const int64_t self_id = (a.self_base >= 0 && qvalid) ? a.self_base + myq : -1;
+    uint64_t list[K];
+#pragma unroll
+    for (int j = 0; j < K; ++j) list[j] = kEmptyKey;
+
+    const int64_t r0 = int64_t(r_id) * a.rows_per_range;
+    const int64_t r1 = (a.n < r0 + a.rows_per_range) ? a.n : r0 + a.rows_per_range;
+    for (int64_t t0 = r0 + int64_t(wave) * kTile; t0 < r1; t0 += int64_t(kBWaves) * kTile) {
+        const int64_t row = t0 + m;
+        const int64_t rr = row < r1 ? row : r1 - 1;
+        const u32x4* bp = reinterpret_cast<const u32x4*>(a.emb16 + rr * d + kg * 8);
+        u32x4 b[KCH];
+#pragma unroll
+        for (int ks = 0; ks < KCH; ++ks) b[ks] = __builtin_nontemporal_load(bp + ks * 4);
+        if (lane < kTile) {
+            const int64_t rl = (t0 + lane < r1) ? t0 + lane : r1 - 1;
+            s_ts[wave][lane] = a.ts[rl];
+            s_mod[wave][lane] = (a.mod_filter >= 0) ? a.mods[rl] : 0;
+        }
+        f32x4 acc[4];
+#pragma unroll
+        for (int qt = 0; qt < 4; ++qt) acc[qt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int ks = 0; ks < KCH; ++ks) {
+            const f16x8 bf = __builtin_bit_cast(f16x8, b[ks]);
+#pragma unroll
+            for (int qt = 0; qt < 4; ++qt) {
+                const f16x8 af = __builtin_bit_cast(f16x8, s_q[qt][ks][lane]);
+                acc[qt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf, acc[qt], 0, 0, 0);
+            }
+        }
+        // C[query = qt*16 + 4*kg + i][row = m]
+#pragma unroll
+        for (int qt = 0; qt < 4; ++qt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) s_stage[wave][m][qt * 16 + 4 * kg + i] = acc[qt][i];
+        wave_lds_sync();
+        if (qvalid) {
+            const int nr = int((r1 - t0) < kTile ? (r1 - t0) : kTile);
+            for (int rr2 = 0; rr2 < nr; ++rr2) {
+                const int64_t id = t0 + rr2;
+                if (id == self_id) continue;
+                float s;
+                if (a.mod_filter >= 0 && s_mod[wave][rr2] != a.mod_filter) {
+                    s = -FLT_MAX;
+                } else if (a.lambda != 0.0f) {
+                    const float age = fmaxf(0.0f, tq - s_ts[wave][rr2]);
+                    s = s_stage[wave][rr2][lane] * expf(-a.lambda * age);
+                } else {
+                    s = s_stage[wave][rr2][lane];
+                }
+                const uint64_t key = make_key(s, uint32_t(id));
+                if (key < list[K - 1]) reg_insert<K>(list, key);
+            }
+        }
+        wave_lds_sync();
+    }
+
+    // merge the 8 waves' lists of each query (the query LDS is reused as staging)
+    __syncthreads();
+    uint64_t* s_lists = reinterpret_cast<uint64_t*>(s_raw);   // [kBWaves][64][K]
+#pragma unroll
+    for (int j = 0; j < K; ++j) s_lists[(wave * 64 + lane) * K + j] = list[j];
+    __syncthreads();
+    if (wave == 0 && qvalid) {
+        for (int w = 1; w < kBWaves; ++w)
+#pragma unroll
+            for (int j = 0; j < K; ++j) {
+                const uint64_t x = s_lists[(w * 64 + lane) * K + j];
+                if (x < list[K - 1]) reg_insert<K>(list, x);
+            }
+        uint64_t* out = a.part + ((int64_t(qb) * a.n_rranges + r_id) * kBQ + lane) * K;
+#pragma unroll
+        for (int j = 0; j < K; ++j) out[j] = list[j];
+    }
+}
+
+// One wave per query: merge n_rranges lists of K keys into the best k_out.
+__global__ __launch_bounds__(64) void k_batch_merge(const uint64_t* __restrict__ part, int32_t n_rranges,
+                                                    int32_t kpart, int32_t q, int32_t k_out,
+                                                    uint64_t* __restrict__ out) {
+    const int lane = int(threadIdx.x);
+    const int qi = int(blockIdx.x);
+    if (qi >= q) return;
+    const int qb = qi / kBQ, j = qi % kBQ;
+    uint64_t list = kEmptyKey, thr = kEmptyKey;
+    const int total = n_rranges * kpart;
+    for (int base = 0; base < total; base += 64) {
+        const int t = base + lane;
+        uint64_t x = kEmptyKey;
+        if (t < total) {
+            const int r = t / kpart, s = t % kpart;
+            x = part[((int64_t(qb) * n_rranges + r) * kBQ + j) * kpart + s];
+        }
+        uint64_t msk = __ballot(x < thr);
+        while (msk) {
+            const int src = __ffsll((unsigned long long)msk) - 1;
+            msk &= msk - 1;
+            const uint64_t y = __shfl(x, src);
+            if (y < thr) {
+                const uint64_t below = __ballot(list < y);
+                const int pos = __popcll(below);
+                const uint64_t up = __shfl_up(list, 1u);
+                const uint64_t v = (lane < pos) ? list : ((lane == pos) ? y : up);
+                list = (lane < k_out) ? v : kEmptyKey;
+                thr = __shfl(list, k_out - 1);
+            }
+        }
+    }
+    if (lane < k_out) out[int64_t(qi) * k_out + lane] = list;
+}
+
+// Exact fp32 rescoring of kc candidates per node; keeps k_out by (score desc, id asc).
+// Nodes q0 .. q0+nq-1; cand / nbrs are indexed from q0.
+__global__ __launch_bounds__(256) void k_knn_rerank(const float* __restrict__ emb, int64_t q0, int64_t nq,
+                                                    int32_t d, const uint64_t* __restrict__ cand, int32_t kc,
+                                                    int32_t k_out, int32_t* __restrict__ nbrs) {
+    const int lane = int(threadIdx.x & 63u);
+    const int sub = lane & 15;
+    const int64_t node = (int64_t(blockIdx.x) * blockDim.x + threadIdx.x) >> 4;
+    if (node >= nq) return;                     // whole 16-lane group exits together
+    const float* x = emb + (q0 + node) * d;
+    uint64_t keys[16];
+    for (int c = 0; c < 16; ++c) keys[c] = kEmptyKey;
+    for (int c = 0; c < kc && c < 16; ++c) {
+        const uint64_t ck = cand[node * kc + c];
+        const int32_t id = key_id(ck);
+        float acc = 0.0f;
+        if (ck != kEmptyKey) {
+            const float* y = emb + int64_t(id) * d;
+            for (int i = sub; i < d; i += 16) acc = fmaf(x[i], y[i], acc);
+        }
+        acc += __shfl_xor(acc, 8, 16);
+        acc += __shfl_xor(acc, 4, 16);
+        acc += __shfl_xor(acc, 2, 16);
+        acc += __shfl_xor(acc, 1, 16);
+        keys[c] = (ck != kEmptyKey) ? make_key(acc, uint32_t(id)) : kEmptyKey;
+    }
+    if (sub == 0) {
+        for (int i = 1; i < 16; ++i) {           // insertion sort of 16 keys
+            const uint64_t v = keys[i];
+            int j = i - 1;
+            while (j >= 0 && keys[j] > v) { keys[j + 1] = keys[j]; --j; }
+            keys[j + 1] = v;
+        }
+        for (int c = 0; c < k_out; ++c) nbrs[node * k_out + c] = (keys[c] != kEmptyKey) ? key_id(keys[c]) : -1;
+    }
+}
+
+__global__ void k_f32_to_f16_rows(const float* __restrict__ in, __half* __restrict__ out, int64_t count) {
+    for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < count; i += int64_t(gridDim.x) * blockDim.x)
+        out[i] = __float2half_rn(in[i]);
+}
+
+template <int KCH, int K>
+int launch_batch_t(const BatchArgs& a, hipStream_t s) {
+    const unsigned grid = unsigned(a.n_rranges * a.n_qblocks);
+    hipLaunchKernelGGL((k_batch_scan<KCH, K>), dim3(grid), dim3(kBWaves * 64), 0, s, a);
+    MARS_HIP(hipGetLastError());
+    return MARS_OK;
+}
+
+template <int K>
+int launch_batch_k(const BatchArgs& a, hipStream_t s) {
+    switch (a.d / 32) {
+        case 8: return launch_batch_t<8, K>(a, s);
+        case 12: return launch_batch_t<12, K>(a, s);
+        case 16: return launch_batch_t<16, K>(a, s);
+        case 24: return launch_batch_t<24, K>(a, s);
+        default: return set_error(MARS_ERR_UNSUPPORTED, "batched scoring: embedding_dim %d not in {256,384,512,768}", a.d);
+    }
+}
+
+}  // namespace
+
+bool batch_dim_supported(int32_t d) { return d == 256 || d == 384 || d == 512 || d == 768; }
+int batch_kpart(int32_t k) { return k <= 8 ? 8 : 16; }
+
+int launch_batch_scan(const BatchArgs& a, hipStream_t s) {
+    MARS_CHECK(a.k >= 1 && a.k <= 16, MARS_ERR_UNSUPPORTED, "batched scoring keeps at most 16 per query (asked %d)",
+               a.k);
+    return a.k <= 8 ? launch_batch_k<8>(a, s) : launch_batch_k<16>(a, s);
+}
+
+int launch_batch_merge(const uint64_t* part, int32_t n_rranges, int32_t kpart, int32_t q, int32_t k_out,
+                       uint64_t* out, hipStream_t s) {
+    hipLaunchKernelGGL(k_batch_merge, dim3(unsigned(q)), dim3(64), 0, s, part, n_rranges, kpart, q, k_out, out);
+    MARS_HIP(hipGetLastError());
+    return MARS_OK;
+}
+
+int launch_knn_rerank(const float* emb, int64_t q0, int64_t nq, int32_t d, const uint64_t* cand, int32_t kc,
+                      int32_t k_out, int32_t* nbrs, hipStream_t s) {
+    const int64_t threads = nq * 16;
+    hipLaunchKernelGGL(k_knn_rerank, dim3(unsigned((threads + 255) / 256)), dim3(256), 0, s, emb, q0, nq, d, cand, kc,
+                       k_out, nbrs);
+    MARS_HIP(hipGetLastError());
+    return MARS_OK;
+}
+
+int launch_f32_to_f16_rows(const float* in, __half* out, int64_t count, hipStream_t s) {
+    int64_t blocks = (count + 255) / 256;
+    if (blocks > 4096) blocks = 4096;
+    hipLaunchKernelGGL(k_f32_to_f16_rows, dim3(unsigned(blocks)), dim3(256), 0, s, in, out, count);
+    MARS_HIP(hipGetLastError());
+    return MARS_OK;
+}
+
+}  // namespace mars

@@ -126,6 +126,13 @@ struct Ctx {
     int32_t last_n = 0;            // node count of the last global query
     int32_t last_k = 0;
     int32_t last_visited = 0;      // visit-list length of the last global query
+    // batched scoring scratch (grown on demand)
+    __half* bq = nullptr;          // queries in fp16
+    float* btq = nullptr;          // query times
+    uint64_t* bpart = nullptr;     // per-(query, row range) keys
+    uint64_t* bout = nullptr;      // merged keys per query
+    int32_t bcap_q = 0;
+    int64_t bcap_part = 0;
 };
 
 // ---- launch helpers (defined in kernels.hip) --------------------------------------
@@ -202,5 +209,33 @@ struct EpisodeArgs {
 int launch_episode(const EpisodeArgs& a, hipStream_t s);
 
 int launch_convert_f16(const float* in, __half* out, int64_t count, hipStream_t s);
+
+// ---- batched MFMA scoring (defined in batch.hip) ---------------------------------------
+struct BatchArgs {
+    const __half* emb16;     // corpus rows, fp16
+    int64_t n;
+    int32_t d;
+    const __half* qh;        // queries, fp16, row-major q x d
+    int32_t q;
+    const float* tq;         // q query times
+    const float* ts;
+    const int32_t* mods;
+    float lambda;
+    int32_t mod_filter;
+    int32_t k;               // <= 16 kept per query
+    int64_t self_base;       // >= 0: query j is node self_base + j and never its own neighbour
+    uint64_t* part;          // [n_qblocks][n_rranges][64][K] keys
+    int64_t rows_per_range;
+    int32_t n_rranges;
+    int32_t n_qblocks;
+};
+bool batch_dim_supported(int32_t d);
+int batch_kpart(int32_t k);  // keys per (query, row range) the scan writes
+int launch_batch_scan(const BatchArgs& a, hipStream_t s);
+int launch_batch_merge(const uint64_t* part, int32_t n_rranges, int32_t kpart, int32_t q, int32_t k_out,
+                       uint64_t* out, hipStream_t s);
+int launch_knn_rerank(const float* emb, int64_t q0, int64_t nq, int32_t d, const uint64_t* cand, int32_t kc,
+                      int32_t k_out, int32_t* nbrs, hipStream_t s);
+int launch_f32_to_f16_rows(const float* in, __half* out, int64_t count, hipStream_t s);
 
 }  // namespace mars

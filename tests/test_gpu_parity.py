@@ -330,3 +330,79 @@ def test_large_frontier_and_visited(rng):
         assert st.visited > 8192
     finally:
         dev.close()
+
+
+# ---------------------------------------------------------------- batched MFMA scoring
+def _batch_check(dev: Dev, qnodes, cfg, t_q, emb):
+    qs = emb[qnodes]
+    buf = mars_amd.DeviceBuffer.from_array(qs)
+    try:
+        ids, sc = mars_amd.query_batch(dev.dg, dev.ctx, buf.ptr, len(qnodes), t_q, cfg)
+    finally:
+        buf.free()
+    tq = np.broadcast_to(np.asarray(t_q, np.float32), (len(qnodes),))
+    k = cfg.top_k
+    for i in range(len(qnodes)):
+        fin, scale = oracle.scores(dev.og, qs[i], float(tq[i]), cfg.time_decay_lambda, cfg.modality_filter)
+        want, _ = oracle.topk(fin, k)
+        tol = RTOL_F16_VS_F32 * np.maximum(np.abs(fin), scale)
+        got = ids[i][ids[i] >= 0]
+        assert len(got) == min(k, dev.n)
+        ok = fin[got] != -FLT_MAX
+        assert np.all(np.abs(sc[i][: len(got)][ok] - fin[got][ok]) <= tol[got][ok])
+        kth = fin[want[-1]]
+        for j in set(got.tolist()) ^ set(want.tolist()):
+            assert abs(fin[j] - kth) <= 2 * (tol[j] + tol[want[-1]]), (i, j)
+        assert np.all(np.diff(sc[i][: len(got)].astype(np.float64)) <= 0)      # sorted desc
+    return ids, sc
+
+
+def test_batch_parity_q64(dev10k, corpus_10k):
+    qn = corpus.pick_queries(corpus_10k.modalities, 64, seed=404)
+    _batch_check(dev10k, qn, RetrievalConfig(top_k=10, time_decay_lambda=LAM), T_Q, corpus_10k.embeddings)
+
+
+@pytest.mark.parametrize("q,k,filt", [(1, 10, -1), (200, 16, -1), (130, 5, 1), (64, 16, 2)])
+def test_batch_parity_shapes(dev10k, corpus_10k, q, k, filt, rng):
+    qn = corpus.pick_queries(corpus_10k.modalities, q, seed=q)
+    tq = rng.uniform(400, 600, size=q).astype(np.float32)             # per-query times
+    _batch_check(dev10k, qn, RetrievalConfig(top_k=k, time_decay_lambda=LAM, modality_filter=filt), tq,
+                 corpus_10k.embeddings)
+
+
+def test_batch_matches_single_query_seeds(dev10k, corpus_10k):
+    """The batched seeds agree with the Q=1 fp16 path's seeds up to fp16 near-ties."""
+    qn = corpus.pick_queries(corpus_10k.modalities, 32, seed=505)
+    cfg = RetrievalConfig(top_k=10, time_decay_lambda=LAM)
+    ids, _ = _batch_check(dev10k, qn, cfg, T_Q, corpus_10k.embeddings)
+    dev10k.ctx.use_fp16 = True
+    try:
+        agree = 0
+        for i, node in enumerate(qn):
+            dev10k.query(corpus_10k.embeddings[node], cfg)
+            seeds, _ = dev10k.ctx.last_seeds()
+            agree += len(set(seeds.tolist()) & set(ids[i].tolist()))
+        assert agree >= 0.98 * 10 * len(qn)
+    finally:
+        dev10k.ctx.use_fp16 = False
+
+
+def test_gpu_knn_matches_cpu_exact():
+    c = corpus.make_corpus(6000, 768, seed=31)
+    dev = Dev(c.embeddings, c.modalities, c.timestamps, None, None, fp16=True)
+    try:
+        got = mars_amd.graph_knn(dev.dg, 8)
+        want, sims = corpus.knn_cpu(c.embeddings, 8)
+        s = c.embeddings @ c.embeddings.T
+        np.fill_diagonal(s, -np.inf)
+        mism = 0
+        for i in range(c.num_nodes):
+            if not np.array_equal(got[i], want[i]):
+                mism += 1
+                # every differing neighbour is a near-tie with the 8th exact score
+                for j in set(got[i].tolist()) ^ set(want[i].tolist()):
+                    assert abs(s[i, j] - sims[i, 7]) <= 1e-5, (i, j)
+        assert mism <= 0.01 * c.num_nodes
+        assert np.all(got != np.arange(c.num_nodes)[:, None])
+    finally:
+        dev.close()
