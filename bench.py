@@ -115,6 +115,13 @@ def main() -> int:
 
     W, S = args.warmup, args.steps
     g1 = gcfg.to_c()
+    if args.profile_only:
+        # a plain 1 GiB device copy: the HBM counters of a known byte count, used to
+        # scale FETCH_SIZE / WRITE_SIZE of the scan kernel
+        src, dst = mars_amd.DeviceBuffer(1 << 30), mars_amd.DeviceBuffer(1 << 30)
+        check(lib.mars_copy_device(C.c_void_p(dst.ptr), C.c_void_p(src.ptr), 1 << 30), "mars_copy_device")
+        src.free()
+        dst.free()
     out = {}
     # ---- global fp32
     ctx.use_fp16 = False
@@ -125,6 +132,14 @@ def main() -> int:
     log(f"global fp32: p50 {pctl(lat_g, .5):.1f} us p99 {pctl(lat_g, .99):.1f} us; scan kernel mean "
         f"{kern_g.mean():.1f} us; finalize mean {bfs_g.mean():.1f} us; {S / wall_g:.0f} q/s")
     bytes_f32 = N * D * 4 + 4 * N
+    # finalize phase breakdown (seed merge, BFS, selection) from the GPU realtime counter
+    ph = []
+    for node in qnodes[W:W + 200]:
+        mars_amd.query_memory_fast(dg, ctx, c.embeddings[node], corpus.QUERY_TIME, gcfg)
+        ph.append(ctx.last_phases())
+    ph = np.array(ph)
+    log(f"finalize phases (us, mean): seeds {ph[:, 0].mean():.1f}  bfs {ph[:, 1].mean():.1f}  "
+        f"select {ph[:, 2].mean():.1f}")
     if not args.profile_only:
         # ---- episode-scoped
         ec = ep_cfgs(qnodes)
@@ -189,7 +204,9 @@ def main() -> int:
                    "num_nodes": N, "dim": D, "top_k": K, "bfs_hops": 2, "decay_lambda": corpus.DECAY_LAMBDA,
                    "corpus_seed": args.seed, "query_seed": args.query_seed, "num_edges": int(len(c.col_indices))},
         "global_fp32": dict(p50_us=pctl(lat_g, .5), p99_us=pctl(lat_g, .99), qps=S / wall_g,
-                            scan_kernel_mean_us=float(kern_g.mean()), finalize_kernel_mean_us=float(bfs_g.mean())),
+                            scan_kernel_mean_us=float(kern_g.mean()), finalize_kernel_mean_us=float(bfs_g.mean()),
+                            finalize_phases_us=dict(seed_merge=float(ph[:, 0].mean()), bfs=float(ph[:, 1].mean()),
+                                                    select=float(ph[:, 2].mean()))),
         **out,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,

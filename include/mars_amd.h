@@ -206,6 +206,9 @@ int mars_query_batch(const mars_graph* g, mars_ctx* ctx, const float* d_queries,
  * its seed list (top-K ids and scores, K entries) to host memory. */
 int mars_ctx_last_scores(mars_ctx* ctx, float* h_scores, int64_t n);
 int mars_ctx_last_seeds(mars_ctx* ctx, int32_t* h_idx, float* h_val, int32_t k, int32_t* k_out);
+/* Durations (us) of the last global query's finalize phases: seed merge, BFS,
+ * result selection (n <= 3), from the GPU's 100 MHz realtime counter. */
+int mars_ctx_last_phases(mars_ctx* ctx, double* us, int32_t n);
 /* The last global query's visit list in discovery order (seeds first, then BFS
  * level by level): node ids, hop levels and BFS scores; *n_out = nodes visited. */
 int mars_ctx_last_visited(mars_ctx* ctx, int32_t* h_ids, int32_t* h_hops, float* h_scores,
@@ -219,6 +222,7 @@ int mars_device_alloc(size_t bytes, void** ptr);
 int mars_device_free(void* ptr);
 int mars_copy_to_device(void* dst, const void* src, size_t bytes);
 int mars_copy_to_host(void* dst, const void* src, size_t bytes);
+int mars_copy_device(void* dst, const void* src, size_t bytes);   /* device to device */
 
 /* ---- benchmark loop (harness semantics of src/latency_bench.cu:355-393) ------------ */
 /* Runs n single queries back to back, query i reading the device vector

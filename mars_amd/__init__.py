@@ -273,6 +273,11 @@ class QueryContext:
         check(lib.mars_ctx_last_seeds(self.handle, _ptr(idx), _ptr(val), 64, C.byref(k)), "mars_ctx_last_seeds")
         return idx[: k.value].copy(), val[: k.value].copy()
 
+    def last_phases(self):
+        us = np.zeros(3, np.float64)
+        check(lib.mars_ctx_last_phases(self.handle, _ptr(us), 3), "mars_ctx_last_phases")
+        return us
+
     def last_visited(self):
         n = C.c_int32()
         check(lib.mars_ctx_last_visited(self.handle, None, None, None, 0, C.byref(n)), "mars_ctx_last_visited")

@@ -149,10 +149,12 @@ SIGNATURES = {
     "mars_graph_set_csr": (C.c_int, [VP, I32, VP, VP]),
     "mars_ctx_last_seeds": (C.c_int, [VP, VP, VP, I32, PI32]),
     "mars_ctx_last_visited": (C.c_int, [VP, VP, VP, VP, I32, PI32]),
+    "mars_ctx_last_phases": (C.c_int, [VP, VP, I32]),
     "mars_device_alloc": (C.c_int, [C.c_size_t, C.POINTER(VP)]),
     "mars_device_free": (C.c_int, [VP]),
     "mars_copy_to_device": (C.c_int, [VP, VP, C.c_size_t]),
     "mars_copy_to_host": (C.c_int, [VP, VP, C.c_size_t]),
+    "mars_copy_device": (C.c_int, [VP, VP, C.c_size_t]),
     "mars_bench_queries": (C.c_int, [VP, VP, VP, I64, I32, C.c_float, C.POINTER(RetrievalConfigC), I32, VP, VP,
                                      VP, VP]),
     # mars_corpus.h

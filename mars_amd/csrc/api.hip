@@ -25,7 +25,7 @@ namespace mars {
 namespace {
 thread_local char g_err[1024] = "";
 constexpr int32_t kMaxWg = 4096;     // upper bound of scan workgroups (partials buffer)
-constexpr int32_t kTargetWg = 2048;  // scan workgroups aimed for (8 per CU on 256 CUs)
+constexpr int32_t kTargetWg = 1024;  // scan workgroups aimed for (4 per CU on 256 CUs: all resident)
 
 int ensure_device(int* dev) {
     int d = 0;
@@ -128,7 +128,8 @@ int ctx_free(Ctx& c) {
     (void)use_device(c.device);
     if (c.stream) (void)hipStreamSynchronize(c.stream);
     dfree(c.query); dfree(c.fin); dfree(c.part); dfree(c.vis); dfree(c.claim); dfree(c.vlist);
-    dfree(c.vhop); dfree(c.vscore); dfree(c.sortbuf); dfree(c.seed_idx); dfree(c.seed_val);
+    dfree(c.vhop); dfree(c.vscore); dfree(c.vro); dfree(c.sortbuf); dfree(c.seed_idx); dfree(c.seed_val); dfree(c.stamps);
+    dfree(c.gthr); dfree(c.gcnt);
     dfree(c.bq); dfree(c.btq); dfree(c.bpart); dfree(c.bout);
     if (c.h_query) (void)hipHostFree(c.h_query);
     if (c.h_res) (void)hipHostFree(c.h_res);
@@ -188,7 +189,8 @@ int query_impl(const mars_graph* gh, mars_ctx* ch, const float* h_q, const float
         a.ep_ids = g.ep_ids; a.t_q = t_q; a.lambda = cfg->time_decay_lambda;
         a.mod_filter = cfg->modality_filter; a.query_ep = cfg->query_episode_id;
         a.boost = (g.ep_ids && cfg->query_episode_id >= 0) ? cfg->episode_same_boost : 0.0f;
-        a.k = K; a.fin = c.fin; a.part = c.part; a.rows_per_wg = rpw; a.num_wg = nwg;
+        a.k = K; a.fin = c.fin; a.part = c.part; a.gthr = c.gthr; a.gcnt = c.gcnt; a.rows_per_wg = rpw;
+        a.num_wg = nwg;
         MARS_TRY(launch_scan(a, s));
         if (timing) MARS_HIP(hipEventRecord(c.ev[1], s));
         // visit stamps / claim generations: no O(N) reset per query
@@ -205,12 +207,19 @@ int query_impl(const mars_graph* gh, mars_ctx* ch, const float* h_q, const float
         const uint32_t gen_base = c.gen;
         c.gen += span;
         FinalizeArgs f{};
-        f.part = c.part; f.n_part = nwg * K; f.k = K; f.row = g.row; f.col = g.col; f.fin = c.fin;
+        f.part = c.part; f.gcnt = c.gcnt; f.gthr = c.gthr; f.k = K; f.row = g.row; f.col = g.col; f.fin = c.fin;
         f.mods = g.mods; f.hops = hops; f.hop_decay = cfg->bfs_score_decay; f.epoch = epoch;
         f.gen_base = gen_base; f.vis = c.vis; f.claim = c.claim; f.vlist = c.vlist; f.vhop = c.vhop;
-        f.vscore = c.vscore; f.sortbuf = c.sortbuf; f.cap_visit = c.max_nodes; f.rcap = rcap;
+        f.vscore = c.vscore; f.vro = c.vro; f.sortbuf = c.sortbuf; f.cap_visit = c.max_nodes; f.rcap = rcap;
         f.seed_idx = c.seed_idx; f.seed_val = c.seed_val; f.res = c.d_res; f.rec = c.d_rec;
-        MARS_TRY(launch_finalize(f, s));
+        f.stamps = c.stamps;
+        if (launch_finalize(f, s) != MARS_OK) {
+            // the scan already appended candidates: clear them for the next query
+            (void)hipMemsetAsync(c.gcnt, 0, sizeof(uint32_t), s);
+            (void)hipMemsetAsync(c.gthr, 0xFF, sizeof(uint64_t), s);
+            (void)hipStreamSynchronize(s);
+            return set_error(MARS_ERR_HIP, "finalize launch failed");
+        }
         c.last_n = g.n;
     }
     if (timing) MARS_HIP(hipEventRecord(c.ev[2], s));
@@ -482,10 +491,13 @@ int mars_ctx_create(int32_t max_nodes, int32_t dim, int32_t max_k, uint32_t flag
     if ((rc = dmalloc(&c.query, size_t(dim))) || (rc = dmalloc(&c.fin, N)) ||
         (rc = dmalloc(&c.part, size_t(kMaxWg) * kMaxK)) || (rc = dmalloc(&c.vis, N)) ||
         (rc = dmalloc(&c.claim, N)) || (rc = dmalloc(&c.vlist, N)) || (rc = dmalloc(&c.vhop, N)) ||
-        (rc = dmalloc(&c.vscore, N)) || (rc = dmalloc(&c.sortbuf, 2 * size_t(kSortCap))) ||
-        (rc = dmalloc(&c.seed_idx, size_t(kMaxK))) || (rc = dmalloc(&c.seed_val, size_t(kMaxK))))
+        (rc = dmalloc(&c.vscore, N)) || (rc = dmalloc(&c.vro, 2 * N)) || (rc = dmalloc(&c.sortbuf, 2 * size_t(kSortCap))) ||
+        (rc = dmalloc(&c.seed_idx, size_t(kMaxK))) || (rc = dmalloc(&c.seed_val, size_t(kMaxK))) ||
+        (rc = dmalloc(&c.stamps, 4)) || (rc = dmalloc(&c.gthr, 1)) || (rc = dmalloc(&c.gcnt, 1)))
         return fail(rc);
     e = hipMemset(c.vis, 0, N * sizeof(uint32_t));
+    if (e == hipSuccess) e = hipMemset(c.gthr, 0xFF, sizeof(uint64_t));
+    if (e == hipSuccess) e = hipMemset(c.gcnt, 0, sizeof(uint32_t));
     if (e == hipSuccess) e = hipMemset(c.claim, 0xFF, N * sizeof(uint64_t));
     if (e == hipSuccess) e = hipHostMalloc(reinterpret_cast<void**>(&c.h_query), size_t(dim) * sizeof(float));
     const size_t res_bytes = sizeof(ResultHeader) + size_t(kSortCap) * sizeof(mars_query_result);
@@ -562,6 +574,12 @@ int mars_copy_to_device(void* dst, const void* src, size_t bytes) {
 int mars_copy_to_host(void* dst, const void* src, size_t bytes) {
     MARS_CHECK(dst && src, MARS_ERR_INVALID, "null argument");
     MARS_HIP(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
+    return MARS_OK;
+}
+
+int mars_copy_device(void* dst, const void* src, size_t bytes) {
+    MARS_CHECK(dst && src, MARS_ERR_INVALID, "null argument");
+    MARS_HIP(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToDevice));
     return MARS_OK;
 }
 
@@ -706,6 +724,15 @@ int mars_ctx_last_seeds(mars_ctx* ch, int32_t* idx, float* val, int32_t k, int32
         MARS_HIP(hipMemcpy(val, c.seed_val, size_t(n) * sizeof(float), hipMemcpyDeviceToHost));
     }
     *k_out = c.last_k;
+    return MARS_OK;
+}
+
+int mars_ctx_last_phases(mars_ctx* ch, double* us, int32_t n) {
+    MARS_CHECK(ch && us && n >= 0 && n <= 3, MARS_ERR_INVALID, "bad arguments");
+    MARS_TRY(use_device(ch->c.device));
+    uint64_t t[4] = {0, 0, 0, 0};
+    MARS_HIP(hipMemcpy(t, ch->c.stamps, sizeof(t), hipMemcpyDeviceToHost));
+    for (int32_t i = 0; i < n; ++i) us[i] = double(t[i + 1] - t[i]) * 0.01;   // 100 MHz counter
     return MARS_OK;
 }
 

@@ -103,15 +103,19 @@ struct Ctx {
     // device scratch
     float* query = nullptr;        // d
     float* fin = nullptr;          // max_nodes: fused score of the last global query
-    uint64_t* part = nullptr;      // max_wg * kMaxK partial top-K keys
+    uint64_t* part = nullptr;      // max_wg * kMaxK candidate keys
+    uint64_t* gthr = nullptr;      // scan's running K-th key bound (reset by finalize)
+    uint32_t* gcnt = nullptr;      // candidate count (reset by finalize)
     int32_t max_wg = 0;
     uint32_t* vis = nullptr;       // max_nodes visit stamps (epoch)
     uint64_t* claim = nullptr;     // max_nodes BFS claim keys
     int32_t* vlist = nullptr;      // max_nodes visit order (node ids)
     int32_t* vhop = nullptr;       // max_nodes
     float* vscore = nullptr;       // max_nodes
+    int32_t* vro = nullptr;        // 2 * max_nodes: row offsets of each visited node
     uint64_t* sortbuf = nullptr;   // max_nodes keys (large-result fallback)
     int32_t* seed_idx = nullptr;   // kMaxK
+    uint64_t* stamps = nullptr;    // finalize phase stamps (100 MHz realtime counter)
     float* seed_val = nullptr;     // kMaxK
     // pinned host staging
     float* h_query = nullptr;      // d
@@ -152,7 +156,9 @@ struct ScanArgs {
     float boost;         // > 0 and ep_ids != null: same-episode boost
     int32_t k;
     float* fin;
-    uint64_t* part;
+    uint64_t* part;          // candidate keys appended by the workgroups
+    uint64_t* gthr;          // running bound on the K-th best key (atomicMin)
+    uint32_t* gcnt;          // number of candidate keys appended (atomicAdd)
     int32_t rows_per_wg;
     int32_t num_wg;
 };
@@ -160,8 +166,9 @@ int launch_scan(const ScanArgs& a, hipStream_t s);
 void scan_grid(int64_t n, int32_t max_wg, int32_t* rows_per_wg, int32_t* num_wg);
 
 struct FinalizeArgs {
-    const uint64_t* part;
-    int32_t n_part;          // partial keys (num_wg * k)
+    const uint64_t* part;    // candidate keys from the scan
+    uint32_t* gcnt;          // their count; reset to 0 here for the next query
+    uint64_t* gthr;          // scan's running bound; reset to kEmptyKey here
     int32_t k;
     const int32_t* row;
     const int32_t* col;
@@ -176,6 +183,7 @@ struct FinalizeArgs {
     int32_t* vlist;
     int32_t* vhop;
     float* vscore;
+    int32_t* vro;            // 2 per visit position: row_offsets[v], row_offsets[v+1]
     uint64_t* sortbuf;
     int32_t cap_visit;
     int32_t rcap;            // results requested (max_results or K)
@@ -183,6 +191,7 @@ struct FinalizeArgs {
     float* seed_val;
     ResultHeader* res;
     mars_query_result* rec;
+    uint64_t* stamps;        // 4 realtime stamps (start, seeds, BFS done, end) or null
 };
 int launch_finalize(const FinalizeArgs& a, hipStream_t s);
 

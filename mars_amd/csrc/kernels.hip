@@ -47,6 +47,30 @@ __device__ inline T ld_coherent(const T* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// ---- lane exchanges: value of lane (lane ^ J) -----------------------------------
+// J = 1, 2: DPP quad_perm; J = 4: DPP row_shl/row_shr; J = 8: DPP row_ror:8 (within a
+// 16-lane row i^8 == i+-8); J = 16: ds_swizzle (xor within 32 lanes); J = 32: bpermute.
+template <int J>
+__device__ inline uint32_t xor_lane(uint32_t v) {
+    if constexpr (J == 1) return uint32_t(__builtin_amdgcn_mov_dpp(int(v), 0xB1, 0xF, 0xF, false));
+    else if constexpr (J == 2) return uint32_t(__builtin_amdgcn_mov_dpp(int(v), 0x4E, 0xF, 0xF, false));
+    else if constexpr (J == 4) {
+        const uint32_t up = uint32_t(__builtin_amdgcn_mov_dpp(int(v), 0x104, 0xF, 0xF, false));   // lane + 4
+        const uint32_t dn = uint32_t(__builtin_amdgcn_mov_dpp(int(v), 0x114, 0xF, 0xF, false));   // lane - 4
+        return (threadIdx.x & 4u) ? dn : up;
+    } else if constexpr (J == 8) return uint32_t(__builtin_amdgcn_mov_dpp(int(v), 0x128, 0xF, 0xF, false));
+    else if constexpr (J == 16) return uint32_t(__builtin_amdgcn_ds_swizzle(int(v), 0x401F));
+    else return uint32_t(__shfl_xor(int(v), J));
+}
+template <int J>
+__device__ inline uint64_t xor_lane64(uint64_t v) {
+    return (uint64_t(xor_lane<J>(uint32_t(v >> 32))) << 32) | xor_lane<J>(uint32_t(v));
+}
+template <int J>
+__device__ inline float xor_lanef(float v) {
+    return __uint_as_float(xor_lane<J>(__float_as_uint(v)));
+}
+
 // Insert key x into the wave-held ascending list (lane i = i-th smallest; lanes
 // >= k hold kEmptyKey). Caller guarantees x < list[k-1].
 __device__ inline void list_insert(uint64_t& list, uint64_t x, int lane, int k) {
@@ -72,12 +96,74 @@ __device__ inline void list_offer(uint64_t& list, uint64_t& thr, uint64_t key, b
     }
 }
 
+template <int J>
+__device__ inline uint64_t cmpx(uint64_t x, int lane, bool ascending_block) {
+    const uint64_t y = xor_lane64<J>(x);
+    const bool lower = (lane & J) == 0;
+    const uint64_t lo = x < y ? x : y, hi = x < y ? y : x;
+    return (lower == ascending_block) ? lo : hi;
+}
+
+// Ascending bitonic sort of one key per lane across the wave.
+__device__ inline uint64_t wave_sort64(uint64_t x, int lane) {
+    x = cmpx<1>(x, lane, (lane & 2) == 0);
+    x = cmpx<2>(x, lane, (lane & 4) == 0);
+    x = cmpx<1>(x, lane, (lane & 4) == 0);
+    x = cmpx<4>(x, lane, (lane & 8) == 0);
+    x = cmpx<2>(x, lane, (lane & 8) == 0);
+    x = cmpx<1>(x, lane, (lane & 8) == 0);
+    x = cmpx<8>(x, lane, (lane & 16) == 0);
+    x = cmpx<4>(x, lane, (lane & 16) == 0);
+    x = cmpx<2>(x, lane, (lane & 16) == 0);
+    x = cmpx<1>(x, lane, (lane & 16) == 0);
+    x = cmpx<16>(x, lane, (lane & 32) == 0);
+    x = cmpx<8>(x, lane, (lane & 32) == 0);
+    x = cmpx<4>(x, lane, (lane & 32) == 0);
+    x = cmpx<2>(x, lane, (lane & 32) == 0);
+    x = cmpx<1>(x, lane, (lane & 32) == 0);
+    x = cmpx<32>(x, lane, true);
+    x = cmpx<16>(x, lane, true);
+    x = cmpx<8>(x, lane, true);
+    x = cmpx<4>(x, lane, true);
+    x = cmpx<2>(x, lane, true);
+    x = cmpx<1>(x, lane, true);
+    return x;
+}
+
+// Smallest k of two ascending wave lists (lanes >= k of the result hold kEmptyKey):
+// min(a[i], b[63-i]) is bitonic and holds the 64 smallest; six half-cleaners sort it.
+__device__ inline uint64_t wave_merge64(uint64_t a, uint64_t b, int lane, int k) {
+    const uint64_t r = __shfl(b, 63 - lane);
+    uint64_t c = a < r ? a : r;
+    c = cmpx<32>(c, lane, true);
+    c = cmpx<16>(c, lane, true);
+    c = cmpx<8>(c, lane, true);
+    c = cmpx<4>(c, lane, true);
+    c = cmpx<2>(c, lane, true);
+    c = cmpx<1>(c, lane, true);
+    return lane < k ? c : kEmptyKey;
+}
+
+// Offer one key per lane: few winners are inserted one by one, many are sorted
+// and merged in registers.
+__device__ inline void wave_offer(uint64_t& list, uint64_t& thr, uint64_t key, int lane, int k) {
+    const uint64_t m = __ballot(key < thr);
+    if (m == 0) return;
+    if (__popcll(m) <= 2) {
+        list_offer(list, thr, key, true, lane, k);
+        return;
+    }
+    const uint64_t xs = wave_sort64(key < thr ? key : kEmptyKey, lane);
+    list = wave_merge64(list, xs, lane, k);
+    thr = __shfl(list, k - 1);
+}
+
 // Sum over the 16 lanes of a DPP row; every lane of the row gets the total.
 __device__ inline float row16_sum(float v) {
-    v += __shfl_xor(v, 8, 16);
-    v += __shfl_xor(v, 4, 16);
-    v += __shfl_xor(v, 2, 16);
-    v += __shfl_xor(v, 1, 16);
+    v += xor_lanef<8>(v);
+    v += xor_lanef<4>(v);
+    v += xor_lanef<2>(v);
+    v += xor_lanef<1>(v);
     return v;
 }
 
@@ -199,8 +285,26 @@ __global__ __launch_bounds__(256) void k_scan(ScanArgs a) {
     s_lists[wave][lane] = list;
     __syncthreads();
     if (wave == 0) {
-        for (int w = 1; w < 4; ++w) list_offer(list, thr, s_lists[w][lane], true, lane, k);
-        if (lane < k) a.part[int64_t(blockIdx.x) * k + lane] = list;
+        list = wave_merge64(list, s_lists[1][lane], lane, k);
+        list = wave_merge64(list, wave_merge64(s_lists[2][lane], s_lists[3][lane], lane, k), lane, k);
+        // Every key of the global top-K is <= the global K-th key <= any
+        // workgroup's K-th key, so keys above the running minimum of those are
+        // dropped here without changing the result.
+        // The bound is read first; only a workgroup that lowers it issues the
+        // atomicMin (about ln(#workgroups) of them), and only one with keys under
+        // it appends.
+        const uint64_t kth = __shfl(list, k - 1);
+        uint64_t cur = kEmptyKey;
+        if (lane == 0) cur = ld_coherent(a.gthr);
+        cur = __shfl(cur, 0);
+        if (kth < cur && lane == 0) atomicMin(reinterpret_cast<unsigned long long*>(a.gthr), (unsigned long long)kth);
+        const uint64_t bound = cur < kth ? cur : kth;
+        const bool pass = lane < k && list != kEmptyKey && list <= bound;
+        const uint64_t m = __ballot(pass);
+        uint32_t base = 0;
+        if (lane == 0 && m) base = atomicAdd(a.gcnt, uint32_t(__popcll(m)));
+        base = __shfl(base, 0);
+        if (pass) a.part[base + uint32_t(__popcll(m & ((1ull << lane) - 1ull)))] = list;
     }
 }
 
@@ -260,6 +364,10 @@ __device__ inline void block_bitonic(uint64_t* key, uint16_t* pay, int n) {
     }
 }
 
+constexpr int kHashCap = 8192;              // LDS hash slots (power of two)
+constexpr int kHashLimit = 6144;            // more distinct nodes: use the global arrays instead
+constexpr uint32_t kClaimHop = 0xFFu;       // hop field of a claimed, not yet visited node
+
 struct FinShared {
     union {
         struct {
@@ -269,48 +377,194 @@ struct FinShared {
         struct {
             int32_t rstart[kFrontierChunk];
             int32_t eoff[kFrontierChunk + 1];
+            uint32_t hkey[kHashCap];        // node id + 1 (0 = empty slot)
+            uint32_t hval[kHashCap];        // (hop << 16) | visit position
         } bfs;
-        uint64_t lists[kFinWaves][64];
         uint32_t hist[256];
     } u;
+    uint64_t lists[kFinWaves][64];
     int s_wave[kFinWaves];
-    int s_misc[4];
+    int s_misc[8];
 };
 
-__global__ __launch_bounds__(kFinThreads) void k_finalize(FinalizeArgs a) {
-    __shared__ FinShared sh;
-    const int tid = int(threadIdx.x), lane = lane_id(), wave = tid >> 6;
-    const int k = a.k;
+__device__ inline uint32_t hash_slot0(int32_t v) { return (uint32_t(v) * 2654435761u) >> (32 - 13); }
 
-    // ---- A. merge per-workgroup keys into the K seeds -------------------------
-    uint64_t list = kEmptyKey, thr = kEmptyKey;
-    for (int base = wave * 64; base < a.n_part; base += kFinThreads) {
-        const int i = base + lane;
-        const uint64_t x = (i < a.n_part) ? a.part[i] : kEmptyKey;
-        list_offer(list, thr, x, true, lane, k);
-    }
-    sh.u.lists[wave][lane] = list;
-    __syncthreads();
-    if (wave == 0) {
-        for (int w = 1; w < kFinWaves; ++w) list_offer(list, thr, sh.u.lists[w][lane], true, lane, k);
-        const int ns = __popcll(__ballot(lane < k && list != kEmptyKey));
-        if (lane < ns) {
-            const int32_t id = key_id(list);
-            const float sc = key_score(list);
-            a.seed_idx[lane] = id;
-            a.seed_val[lane] = sc;
-            a.vlist[lane] = id;
-            a.vhop[lane] = 0;
-            a.vscore[lane] = sc;
-            a.vis[id] = a.epoch;
+// Find (or insert) node v in the LDS hash; -1 when the table is full.
+// At most kHashLimit + blockDim inserts ever land (later ones bail out on the
+// overflow flag), so the table never fills and every probe sequence ends.
+__device__ inline int hash_find_or_insert(FinShared& sh, int32_t v) {
+    if (sh.s_misc[5]) return -1;
+    const uint32_t k = uint32_t(v) + 1u;
+    uint32_t s = hash_slot0(v);
+    for (int probe = 0; probe < kHashCap; ++probe) {
+        const uint32_t cur = sh.u.bfs.hkey[s];
+        if (cur == k) return int(s);
+        if (cur == 0u) {
+            const uint32_t old = atomicCAS(&sh.u.bfs.hkey[s], 0u, k);
+            if (old == 0u) {
+                if (atomicAdd(&sh.s_misc[4], 1) >= kHashLimit) sh.s_misc[5] = 1;   // overflow
+                return int(s);
+            }
+            if (old == k) return int(s);
         }
-        if (lane == 0) sh.s_misc[0] = ns;
+        s = (s + 1u) & uint32_t(kHashCap - 1);
     }
+    sh.s_misc[5] = 1;
+    return -1;
+}
+
+__device__ inline int hash_find(const FinShared& sh, int32_t v) {
+    const uint32_t k = uint32_t(v) + 1u;
+    uint32_t s = hash_slot0(v);
+    for (int probe = 0; probe < kHashCap; ++probe) {
+        const uint32_t cur = sh.u.bfs.hkey[s];
+        if (cur == k) return int(s);
+        if (cur == 0u) return -1;
+        s = (s + 1u) & uint32_t(kHashCap - 1);
+    }
+    return -1;
+}
+
+// Degrees of frontier slots [c0, c0+cn) -> sh.u.bfs.eoff / rstart; returns the edge count.
+// CACHED: the row offsets of each visited node were stored in a.vro when it was
+// visited (one dependent HBM load less per level).
+template <bool CACHED>
+__device__ inline int frontier_edges(FinShared& sh, const FinalizeArgs& a, int c0, int cn) {
+    const int tid = int(threadIdx.x);
+    int deg[4], rs[4], local = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int i = tid * 4 + j;
+        deg[j] = 0; rs[j] = 0;
+        if (i < cn) {
+            if constexpr (CACHED) {
+                const int64_t ro = ld_coherent(reinterpret_cast<const int64_t*>(a.vro) + c0 + i);
+                rs[j] = int32_t(ro);
+                deg[j] = int32_t(ro >> 32) - rs[j];
+            } else {
+                const int32_t v = ld_coherent(a.vlist + c0 + i);
+                rs[j] = a.row[v];
+                deg[j] = a.row[v + 1] - rs[j];
+            }
+        }
+        local += deg[j];
+    }
+    int total = 0;
+    int off = block_excl_scan(local, sh.s_wave, &total);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int i = tid * 4 + j;
+        if (i < cn) { sh.u.bfs.eoff[i] = off; sh.u.bfs.rstart[i] = rs[j]; }
+        off += deg[j];
+    }
+    __syncthreads();
+    return total;
+}
+
+// In-order compaction of one 1024-edge round: returns the number of winners and
+// gives each winner its rank.
+__device__ inline int round_rank(FinShared& sh, bool won, int* rank) {
+    const int lane = lane_id(), wave = int(threadIdx.x >> 6);
+    const uint64_t m = __ballot(won);
+    if (lane == 0) sh.s_wave[wave] = __popcll(m);
+    __syncthreads();
+    int woff = 0, wtot = 0;
+#pragma unroll
+    for (int w = 0; w < kFinWaves; ++w) {
+        const int x = sh.s_wave[w];
+        woff += (w < wave) ? x : 0;
+        wtot += x;
+    }
+    *rank = woff + __popcll(m & ((1ull << lane) - 1ull));
+    return wtot;
+}
+
+// BFS with the visited / claim state in the LDS hash. Returns the visit count,
+// or -1 if the visit set outgrew the table (nothing global but the visit lists
+// was touched, so the caller can run the global-array BFS instead).
+__device__ int bfs_lds(FinShared& sh, const FinalizeArgs& a, int ns, int* levels_out) {
+    constexpr int R = 4;                       // 1024-edge rounds cached in registers
+    const int tid = int(threadIdx.x);
+    for (int i = tid; i < kHashCap; i += kFinThreads) { sh.u.bfs.hkey[i] = 0u; sh.u.bfs.hval[i] = 0xFFFFFFFFu; }
+    if (tid == 0) { sh.s_misc[4] = 0; sh.s_misc[5] = 0; }
+    __syncthreads();
+    if (tid < ns) {
+        const int slot = hash_find_or_insert(sh, ld_coherent(a.vlist + tid));
+        if (slot >= 0) sh.u.bfs.hval[slot] = uint32_t(tid);          // hop 0, position tid
+    }
+    __syncthreads();
+    int fs = 0, fe = ns, levels = 0;
+    for (int h = 0; h < a.hops && fs < fe; ++h) {
+        int out = fe;
+        for (int c0 = fs; c0 < fe; c0 += kFrontierChunk) {
+            const int cn = min(kFrontierChunk, fe - c0);
+            const int T = frontier_edges<true>(sh, a, c0, cn);
+            for (int s0 = 0; s0 < T; s0 += R * kFinThreads) {
+                // claim: the smallest parent position wins; visited nodes keep their
+                // smaller (hop < 0xFF) value under the atomicMin. The edge, its slot
+                // and the two scores the emit needs stay in registers.
+                int32_t nb[R], pp[R], slot[R], rb[R], re[R];
+                float fv[R], ps[R];
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    const int t = s0 + r * kFinThreads + tid;
+                    slot[r] = -1; nb[r] = 0; pp[r] = 0; fv[r] = 0.0f; ps[r] = 0.0f; rb[r] = 0; re[r] = 0;
+                    if (t < T) {
+                        const int p = owner_of(sh.u.bfs.eoff, cn, t);
+                        pp[r] = c0 + p;
+                        nb[r] = a.col[sh.u.bfs.rstart[p] + (t - sh.u.bfs.eoff[p])];
+                    }
+                }
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    if (s0 + r * kFinThreads + tid < T) {
+                        fv[r] = a.fin[nb[r]];
+                        rb[r] = a.row[nb[r]];
+                        re[r] = a.row[nb[r] + 1];
+                        ps[r] = ld_coherent(a.vscore + pp[r]);
+                        slot[r] = hash_find_or_insert(sh, nb[r]);
+                        if (slot[r] >= 0) atomicMin(&sh.u.bfs.hval[slot[r]], (kClaimHop << 16) | uint32_t(pp[r]));
+                    }
+                }
+                __syncthreads();
+                if (sh.s_misc[5]) return -1;
+                // emit winners in (frontier position, CSR slot) order
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    if (s0 + r * kFinThreads >= T) break;                  // block-uniform
+                    const bool won = slot[r] >= 0 &&
+                                     sh.u.bfs.hval[slot[r]] == ((kClaimHop << 16) | uint32_t(pp[r]));
+                    int rank = 0;
+                    const int wtot = round_rank(sh, won, &rank);
+                    if (won) {
+                        const int pos = out + rank;
+                        a.vlist[pos] = nb[r];
+                        a.vhop[pos] = h + 1;
+                        a.vscore[pos] = fmaxf(ps[r] * a.hop_decay, fv[r] * 0.8f);
+                        reinterpret_cast<int64_t*>(a.vro)[pos] = (int64_t(re[r]) << 32) | uint32_t(rb[r]);
+                        sh.u.bfs.hval[slot[r]] = (uint32_t(h + 1) << 16) | uint32_t(pos);
+                    }
+                    out += wtot;
+                    __syncthreads();
+                }
+                __threadfence_block();
+            }
+            __syncthreads();
+        }
+        fs = fe;
+        fe = out;
+        ++levels;
+    }
+    *levels_out = levels;
+    return fe;
+}
+
+// BFS with the visited / claim state in global memory (any visit-set size).
+__device__ int bfs_global(FinShared& sh, const FinalizeArgs& a, int ns, int* levels_out) {
+    const int tid = int(threadIdx.x);
+    if (tid < ns) a.vis[ld_coherent(a.vlist + tid)] = a.epoch;
     __threadfence();
     __syncthreads();
-    const int ns = sh.s_misc[0];
-
-    // ---- B. deterministic BFS ------------------------------------------------
     int fs = 0, fe = ns, levels = 0;
     for (int h = 0; h < a.hops && fs < fe; ++h) {
         const uint32_t gen = a.gen_base + uint32_t(h);
@@ -318,30 +572,7 @@ __global__ __launch_bounds__(kFinThreads) void k_finalize(FinalizeArgs a) {
         int out = fe;
         for (int c0 = fs; c0 < fe; c0 += kFrontierChunk) {
             const int cn = min(kFrontierChunk, fe - c0);
-            // degrees of this chunk, 4 consecutive frontier slots per thread
-            int deg[4], rs[4], local = 0;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int i = tid * 4 + j;
-                deg[j] = 0; rs[j] = 0;
-                if (i < cn) {
-                    const int32_t v = ld_coherent(a.vlist + c0 + i);
-                    rs[j] = a.row[v];
-                    deg[j] = a.row[v + 1] - rs[j];
-                }
-                local += deg[j];
-            }
-            int total = 0;
-            int off = block_excl_scan(local, sh.s_wave, &total);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int i = tid * 4 + j;
-                if (i < cn) { sh.u.bfs.eoff[i] = off; sh.u.bfs.rstart[i] = rs[j]; }
-                off += deg[j];
-            }
-            __syncthreads();
-            const int T = total;
-            // claim: smallest (frontier position) wins each undiscovered neighbour
+            const int T = frontier_edges<false>(sh, a, c0, cn);
             for (int t = tid; t < T; t += kFinThreads) {
                 const int p = owner_of(sh.u.bfs.eoff, cn, t);
                 const int32_t nb = a.col[sh.u.bfs.rstart[p] + (t - sh.u.bfs.eoff[p])];
@@ -351,7 +582,6 @@ __global__ __launch_bounds__(kFinThreads) void k_finalize(FinalizeArgs a) {
             }
             __threadfence();
             __syncthreads();
-            // emit winners in (frontier position, CSR slot) order
             for (int r0 = 0; r0 < T; r0 += kFinThreads) {
                 const int t = r0 + tid;
                 bool won = false;
@@ -362,18 +592,10 @@ __global__ __launch_bounds__(kFinThreads) void k_finalize(FinalizeArgs a) {
                     nb = a.col[sh.u.bfs.rstart[p] + (t - sh.u.bfs.eoff[p])];
                     won = ld_coherent(a.claim + nb) == (hi | uint32_t(c0 + p));
                 }
-                const uint64_t m = __ballot(won);
-                if (lane == 0) sh.s_wave[wave] = __popcll(m);
-                __syncthreads();
-                int woff = 0, wtot = 0;
-#pragma unroll
-                for (int w = 0; w < kFinWaves; ++w) {
-                    const int x = sh.s_wave[w];
-                    woff += (w < wave) ? x : 0;
-                    wtot += x;
-                }
+                int rank = 0;
+                const int wtot = round_rank(sh, won, &rank);
                 if (won) {
-                    const int pos = out + woff + __popcll(m & ((1ull << lane) - 1ull));
+                    const int pos = out + rank;
                     const float ps = ld_coherent(a.vscore + c0 + p);
                     a.vlist[pos] = nb;
                     a.vhop[pos] = h + 1;
@@ -389,10 +611,23 @@ __global__ __launch_bounds__(kFinThreads) void k_finalize(FinalizeArgs a) {
         fe = out;
         ++levels;
     }
+    *levels_out = levels;
+    return fe;
+}
 
-    // ---- C. results: (score desc, id asc), first rcap ----------------------------
-    const int V = fe;
-    const int rc = min(a.rcap, V);
+__device__ inline void write_result(const FinalizeArgs& a, int j, uint64_t key, int32_t hop) {
+    const int32_t id = key_id(key);
+    mars_query_result r;
+    r.node_id = id;
+    r.score = key_score(key);
+    r.modality = a.mods[id];
+    r.hops_from_seed = hop;
+    a.rec[j] = r;
+}
+
+// Results by full sort of the visit set (bitonic in LDS, radix select beyond).
+__device__ void select_sorted(FinShared& sh, const FinalizeArgs& a, int V, int rc) {
+    const int tid = int(threadIdx.x);
     if (V <= kSortCap) {
         int n2 = 1;
         while (n2 < V) n2 <<= 1;
@@ -407,83 +642,153 @@ __global__ __launch_bounds__(kFinThreads) void k_finalize(FinalizeArgs a) {
         }
         __syncthreads();
         block_bitonic(sh.u.sort.key, sh.u.sort.pay, n2);
-        for (int j = tid; j < rc; j += kFinThreads) {
-            const uint64_t key = sh.u.sort.key[j];
-            const int pos = sh.u.sort.pay[j];
-            const int32_t id = key_id(key);
-            mars_query_result r;
-            r.node_id = id;
-            r.score = key_score(key);
-            r.modality = a.mods[id];
-            r.hops_from_seed = ld_coherent(a.vhop + pos);
-            a.rec[j] = r;
+        for (int j = tid; j < rc; j += kFinThreads)
+            write_result(a, j, sh.u.sort.key[j], ld_coherent(a.vhop + sh.u.sort.pay[j]));
+        return;
+    }
+    // radix-select the key of rank rc (keys are unique), then sort the rc smallest
+    // (rc <= kSortCap is enforced by the host)
+    uint64_t prefix = 0, mask = 0;
+    int need = rc;
+    for (int shift = 56; shift >= 0; shift -= 8) {
+        for (int i = tid; i < 256; i += kFinThreads) sh.u.hist[i] = 0;
+        __syncthreads();
+        for (int i = tid; i < V; i += kFinThreads) {
+            const uint64_t key = make_key(ld_coherent(a.vscore + i), uint32_t(ld_coherent(a.vlist + i)));
+            if ((key & mask) == prefix) atomicAdd(&sh.u.hist[(key >> shift) & 255u], 1u);
+        }
+        __syncthreads();
+        if (tid == 0) {
+            int cum = 0, dg = 255;
+            for (int b = 0; b < 256; ++b) {
+                if (cum + int(sh.u.hist[b]) >= need) { dg = b; break; }
+                cum += int(sh.u.hist[b]);
+            }
+            sh.s_misc[1] = dg;
+            sh.s_misc[2] = need - cum;
+        }
+        __syncthreads();
+        prefix |= uint64_t(sh.s_misc[1]) << shift;
+        mask |= uint64_t(0xFF) << shift;
+        need = sh.s_misc[2];
+        __syncthreads();
+    }
+    int base = 0;
+    for (int r0 = 0; r0 < V; r0 += kFinThreads) {
+        const int i = r0 + tid;
+        uint64_t key = kEmptyKey;
+        bool take = false;
+        if (i < V) {
+            key = make_key(ld_coherent(a.vscore + i), uint32_t(ld_coherent(a.vlist + i)));
+            take = key <= prefix;
+        }
+        int tot = 0;
+        const int o = block_excl_scan(take ? 1 : 0, sh.s_wave, &tot);
+        if (take) { a.sortbuf[2 * (base + o)] = key; a.sortbuf[2 * (base + o) + 1] = uint64_t(i); }
+        base += tot;
+    }
+    __threadfence();
+    __syncthreads();
+    int n2 = 1;
+    while (n2 < rc) n2 <<= 1;
+    for (int i = tid; i < n2; i += kFinThreads) {
+        sh.u.sort.key[i] = (i < rc) ? ld_coherent(a.sortbuf + 2 * i) : kEmptyKey;
+        sh.u.sort.pay[i] = uint16_t(i < rc ? i : 0);
+    }
+    __syncthreads();
+    block_bitonic(sh.u.sort.key, sh.u.sort.pay, n2);
+    for (int j = tid; j < rc; j += kFinThreads) {
+        const int pos = int(ld_coherent(a.sortbuf + 2 * sh.u.sort.pay[j] + 1));
+        write_result(a, j, sh.u.sort.key[j], ld_coherent(a.vhop + pos));
+    }
+}
+
+// Merge the 16 waves' lists pairwise in LDS; wave 0 returns the result.
+__device__ inline uint64_t tree_merge(FinShared& sh, uint64_t list, int k) {
+    const int lane = lane_id(), wave = int(threadIdx.x >> 6);
+    for (int half = kFinWaves / 2; half > 0; half >>= 1) {
+        if (wave >= half && wave < 2 * half) sh.lists[wave][lane] = list;
+        __syncthreads();
+        if (wave < half) list = wave_merge64(list, sh.lists[wave + half][lane], lane, k);
+        __syncthreads();
+    }
+    return list;
+}
+
+__device__ inline void stamp(const FinalizeArgs& a, int i) {
+    if (threadIdx.x == 0 && a.stamps) a.stamps[i] = __builtin_amdgcn_s_memrealtime();
+}
+
+__global__ __launch_bounds__(kFinThreads) void k_finalize(FinalizeArgs a) {
+    __shared__ FinShared sh;
+    const int tid = int(threadIdx.x), lane = lane_id(), wave = tid >> 6;
+    const int k = a.k;
+    stamp(a, 0);
+
+    // ---- A. merge the scan's candidate keys into the K seeds (8 loads in flight per lane)
+    const int n_part = int(*a.gcnt);
+    uint64_t list = kEmptyKey, thr = kEmptyKey;
+    for (int base = wave * 64; base < n_part; base += kFinThreads * 8) {
+        uint64_t x[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int i = base + j * kFinThreads + lane;
+            x[j] = (i < n_part) ? a.part[i] : kEmptyKey;
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) wave_offer(list, thr, x[j], lane, k);
+    }
+    list = tree_merge(sh, list, k);
+    if (wave == 0) {
+        const int ns = __popcll(__ballot(lane < k && list != kEmptyKey));
+        if (lane < ns) {
+            const int32_t id = key_id(list);
+            const float sc = key_score(list);
+            a.seed_idx[lane] = id;
+            a.seed_val[lane] = sc;
+            a.vlist[lane] = id;
+            a.vhop[lane] = 0;
+            a.vscore[lane] = sc;
+            reinterpret_cast<int64_t*>(a.vro)[lane] = (int64_t(a.row[id + 1]) << 32) | uint32_t(a.row[id]);
+        }
+        if (lane == 0) sh.s_misc[0] = ns;
+    }
+    __threadfence();
+    __syncthreads();
+    const int ns = sh.s_misc[0];
+    stamp(a, 1);
+
+    // ---- B. deterministic BFS: LDS hash first, global arrays if it outgrows it
+    int levels = 0;
+    int V = (a.hops < int(kClaimHop)) ? bfs_lds(sh, a, ns, &levels) : -1;   // hop must fit below the claim mark
+    const bool in_lds = V >= 0;
+    if (!in_lds) {
+        __syncthreads();
+        V = bfs_global(sh, a, ns, &levels);
+    }
+
+    stamp(a, 2);
+    // ---- C. results: (score desc, id asc), first rcap
+    const int rc = min(a.rcap, V);
+    if (in_lds && rc <= 64) {
+        // wave-held lists over the visit set, hop looked up in the LDS hash
+        uint64_t best = kEmptyKey, bthr = kEmptyKey;
+        for (int base = wave * 64; base < V; base += kFinThreads) {
+            const int i = base + lane;
+            const uint64_t key = (i < V) ? make_key(ld_coherent(a.vscore + i), uint32_t(ld_coherent(a.vlist + i)))
+                                         : kEmptyKey;
+            wave_offer(best, bthr, key, lane, rc > 0 ? rc : 1);
+        }
+        best = tree_merge(sh, best, rc > 0 ? rc : 1);
+        if (wave == 0) {
+            if (lane < rc) {
+                const int slot = hash_find(sh, key_id(best));
+                write_result(a, lane, best, int32_t(sh.u.bfs.hval[slot] >> 16));
+            }
         }
     } else {
-        // radix-select the key of rank rc (keys are unique), then sort the rc
-        // smallest (rc <= kSortCap is enforced by the host).
-        uint64_t prefix = 0, mask = 0;
-        int need = rc;
-        for (int shift = 56; shift >= 0; shift -= 8) {
-            for (int i = tid; i < 256; i += kFinThreads) sh.u.hist[i] = 0;
-            __syncthreads();
-            for (int i = tid; i < V; i += kFinThreads) {
-                const uint64_t key = make_key(ld_coherent(a.vscore + i), uint32_t(ld_coherent(a.vlist + i)));
-                if ((key & mask) == prefix) atomicAdd(&sh.u.hist[(key >> shift) & 255u], 1u);
-            }
-            __syncthreads();
-            if (tid == 0) {
-                int cum = 0, dg = 255;
-                for (int b = 0; b < 256; ++b) {
-                    if (cum + int(sh.u.hist[b]) >= need) { dg = b; break; }
-                    cum += int(sh.u.hist[b]);
-                }
-                sh.s_misc[1] = dg;
-                sh.s_misc[2] = need - cum;
-            }
-            __syncthreads();
-            prefix |= uint64_t(sh.s_misc[1]) << shift;
-            mask |= uint64_t(0xFF) << shift;
-            need = sh.s_misc[2];
-            __syncthreads();
-        }
-        // gather the rc keys <= prefix (with their visit positions) into sortbuf
-        int base = 0;
-        for (int r0 = 0; r0 < V; r0 += kFinThreads) {
-            const int i = r0 + tid;
-            uint64_t key = kEmptyKey;
-            bool take = false;
-            if (i < V) {
-                key = make_key(ld_coherent(a.vscore + i), uint32_t(ld_coherent(a.vlist + i)));
-                take = key <= prefix;
-            }
-            int tot = 0;
-            const int o = block_excl_scan(take ? 1 : 0, sh.s_wave, &tot);
-            if (take) { a.sortbuf[2 * (base + o)] = key; a.sortbuf[2 * (base + o) + 1] = uint64_t(i); }
-            base += tot;
-        }
-        __threadfence();
         __syncthreads();
-        int n2 = 1;
-        while (n2 < rc) n2 <<= 1;
-        // positions can exceed 16 bits here: sort (key, slot) and look the position up
-        for (int i = tid; i < n2; i += kFinThreads) {
-            sh.u.sort.key[i] = (i < rc) ? ld_coherent(a.sortbuf + 2 * i) : kEmptyKey;
-            sh.u.sort.pay[i] = uint16_t(i < rc ? i : 0);
-        }
-        __syncthreads();
-        block_bitonic(sh.u.sort.key, sh.u.sort.pay, n2);
-        for (int j = tid; j < rc; j += kFinThreads) {
-            const uint64_t key = sh.u.sort.key[j];
-            const int slot = sh.u.sort.pay[j];
-            const int pos = int(ld_coherent(a.sortbuf + 2 * slot + 1));
-            const int32_t id = key_id(key);
-            mars_query_result r;
-            r.node_id = id;
-            r.score = key_score(key);
-            r.modality = a.mods[id];
-            r.hops_from_seed = ld_coherent(a.vhop + pos);
-            a.rec[j] = r;
-        }
+        select_sorted(sh, a, V, rc);
     }
     if (tid == 0) {
         ResultHeader h;
@@ -492,7 +797,10 @@ __global__ __launch_bounds__(kFinThreads) void k_finalize(FinalizeArgs a) {
         h.levels = levels;
         h.n_seeds = ns;
         *a.res = h;
+        *a.gcnt = 0u;                 // ready for the next query's scan
+        *a.gthr = kEmptyKey;
     }
+    stamp(a, 3);
 }
 
 // ---- episode-scoped query ------------------------------------------------------------
