@@ -81,7 +81,7 @@ def main() -> int:
     mars_amd.upload_episode_ids(dg, c.episode_ids)
     csr = mars_amd.build_episode_csr(c.episode_ids, N)
     mars_amd.upload_episode_csr(dg, csr)
-    ctx = mars_amd.create_query_context(N, D, 64, flags=mars_amd.MARS_CTX_TIMING)
+    ctx = mars_amd.create_query_context(N, D, 64, flags=0)
 
     nq = args.steps + args.warmup
     qnodes = corpus.pick_queries(c.modalities, nq, seed=args.query_seed)
@@ -114,6 +114,7 @@ def main() -> int:
         return lat, kern, bfs
 
     W, S = args.warmup, args.steps
+    KT = min(S, 2000)          # queries of the kernel-timing passes (HIP events on the query stream)
     g1 = gcfg.to_c()
     if args.profile_only:
         # a plain 1 GiB device copy: the HBM counters of a known byte count, used to
@@ -123,16 +124,24 @@ def main() -> int:
         src.free()
         dst.free()
     out = {}
-    # ---- global fp32
+    bytes_f32 = N * D * 4 + 4 * N
+    bytes_f16 = N * D * 2 + 4 * N
+
+    def timed(first, count, cfgs, n_cfg, events):
+        ctx.timing = events
+        t0 = time.time()
+        r = run(first, count, cfgs, n_cfg)
+        return r, time.time() - t0
+
+    # ---- global fp32: latency pass (no events), then a kernel-timing pass
     ctx.use_fp16 = False
     run(0, W, C.pointer(g1), 1)
-    t0 = time.time()
-    lat_g, kern_g, bfs_g = run(W, S, C.pointer(g1), 1)
-    wall_g = time.time() - t0
-    log(f"global fp32: p50 {pctl(lat_g, .5):.1f} us p99 {pctl(lat_g, .99):.1f} us; scan kernel mean "
-        f"{kern_g.mean():.1f} us; finalize mean {bfs_g.mean():.1f} us; {S / wall_g:.0f} q/s")
-    bytes_f32 = N * D * 4 + 4 * N
+    (lat_g, _, _), wall_g = timed(W, S, C.pointer(g1), 1, False)
+    (lat_gk, kern_g, bfs_g), _ = timed(W, KT, C.pointer(g1), 1, True)
+    log(f"global fp32: p50 {pctl(lat_g, .5):.1f} us p99 {pctl(lat_g, .99):.1f} us; {S / wall_g:.0f} q/s; scan kernel "
+        f"mean {kern_g.mean():.1f} us ({bytes_f32 / kern_g.mean() / 1e3:.0f} GB/s); finalize mean {bfs_g.mean():.1f} us")
     # finalize phase breakdown (seed merge, BFS, selection) from the GPU realtime counter
+    ctx.timing = False
     ph = []
     for node in qnodes[W:W + 200]:
         mars_amd.query_memory_fast(dg, ctx, c.embeddings[node], corpus.QUERY_TIME, gcfg)
@@ -142,25 +151,23 @@ def main() -> int:
         f"select {ph[:, 2].mean():.1f}")
     if not args.profile_only:
         # ---- episode-scoped
-        ec = ep_cfgs(qnodes)
+        ec = ep_cfgs(qnodes[:W + S])
         run(0, W, ec, W) if W else None
-        ec_t = ep_cfgs(qnodes[W:W + S])
-        t0 = time.time()
-        lat_e, kern_e, _ = run(W, S, ec_t, S)
-        wall_e = time.time() - t0
-        log(f"episode: p50 {pctl(lat_e, .5):.1f} us p99 {pctl(lat_e, .99):.1f} us; kernel mean {kern_e.mean():.1f} us;"
-            f" {S / wall_e:.0f} q/s")
+        ec_t = (RetrievalConfigC * S).from_buffer(ec, W * C.sizeof(RetrievalConfigC))
+        (lat_e, _, _), wall_e = timed(W, S, ec_t, S, False)
+        (_, kern_e, _), _ = timed(W, KT, ec_t, KT, True)
+        log(f"episode: p50 {pctl(lat_e, .5):.1f} us p99 {pctl(lat_e, .99):.1f} us; {S / wall_e:.0f} q/s; kernel mean "
+            f"{kern_e.mean():.1f} us")
         # ---- global fp16
         ctx.use_fp16 = True
         run(0, W, C.pointer(g1), 1)
-        t0 = time.time()
-        lat_h, kern_h, bfs_h = run(W, S, C.pointer(g1), 1)
-        wall_h = time.time() - t0
+        (lat_h, _, _), wall_h = timed(W, S, C.pointer(g1), 1, False)
+        (_, kern_h, bfs_h), _ = timed(W, KT, C.pointer(g1), 1, True)
         ctx.use_fp16 = False
-        bytes_f16 = N * D * 2 + 4 * N
         log(f"global fp16: p50 {pctl(lat_h, .5):.1f} us p99 {pctl(lat_h, .99):.1f} us; scan kernel mean "
             f"{kern_h.mean():.1f} us ({bytes_f16 / kern_h.mean() / 1e3:.0f} GB/s)")
         # ---- batched Q=64 global scoring on MFMA fp16 tiles
+        ctx.timing = True
         B, reps = 64, 30
         bl, bk = [], []
         for r in range(reps + 3):
@@ -170,6 +177,7 @@ def main() -> int:
             if r >= 3:
                 bl.append(st.wall_us)
                 bk.append(st.gpu_ms_similarity * 1e3)
+        ctx.timing = False
         bkm = float(np.mean(bk))
         flops = 2.0 * B * N * D
         out["batch_q64_fp16"] = dict(p50_us=pctl(bl, .5), p99_us=pctl(bl, .99), queries_per_s=B / (pctl(bl, .5) / 1e6),
@@ -204,6 +212,7 @@ def main() -> int:
                    "num_nodes": N, "dim": D, "top_k": K, "bfs_hops": 2, "decay_lambda": corpus.DECAY_LAMBDA,
                    "corpus_seed": args.seed, "query_seed": args.query_seed, "num_edges": int(len(c.col_indices))},
         "global_fp32": dict(p50_us=pctl(lat_g, .5), p99_us=pctl(lat_g, .99), qps=S / wall_g,
+                            p99_us_with_events=pctl(lat_gk, .99),
                             scan_kernel_mean_us=float(kern_g.mean()), finalize_kernel_mean_us=float(bfs_g.mean()),
                             finalize_phases_us=dict(seed_merge=float(ph[:, 0].mean()), bfs=float(ph[:, 1].mean()),
                                                     select=float(ph[:, 2].mean()))),

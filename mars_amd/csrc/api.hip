@@ -25,7 +25,7 @@ namespace mars {
 namespace {
 thread_local char g_err[1024] = "";
 constexpr int32_t kMaxWg = 4096;     // upper bound of scan workgroups (partials buffer)
-constexpr int32_t kTargetWg = 1024;  // scan workgroups aimed for (4 per CU on 256 CUs: all resident)
+constexpr int32_t kTargetWg = 2048;  // scan workgroups (grid-stride; 8 per CU on 256 CUs)
 
 int ensure_device(int* dev) {
     int d = 0;

@@ -159,7 +159,7 @@ struct ScanArgs {
     uint64_t* part;          // candidate keys appended by the workgroups
     uint64_t* gthr;          // running bound on the K-th best key (atomicMin)
     uint32_t* gcnt;          // number of candidate keys appended (atomicAdd)
-    int32_t rows_per_wg;
+    int32_t rows_per_wg;     // unused (grid-stride scan)
     int32_t num_wg;
 };
 int launch_scan(const ScanArgs& a, hipStream_t s);

@@ -255,6 +255,12 @@ __device__ inline float fuse_score(float dot, float ts, int32_t mod, int32_t ep,
     return s;
 }
 
+// Row groups of 4 rows (one per 16-lane group) are dealt out grid-stride: wave w of
+// workgroup b takes groups (it * gridDim.x * 4 + b * 4 + w) * kUnroll + u, so at any
+// moment the grid sweeps one contiguous window of the corpus; kUnroll groups per
+// step keep 2 x 4 rows of loads in flight per wave.
+constexpr int kScanUnroll = 2;
+
 template <typename T, typename QF>
 __global__ __launch_bounds__(256) void k_scan(ScanArgs a) {
     __shared__ uint64_t s_lists[4][64];
@@ -265,22 +271,31 @@ __global__ __launch_bounds__(256) void k_scan(ScanArgs a) {
     if constexpr (std::is_same_v<QF, QGeneric>) qf.d = a.d;
     qf.load(a.q, sub);
     const T* emb = static_cast<const T*>(a.emb);
-    const int64_t r0 = int64_t(blockIdx.x) * a.rows_per_wg;
-    const int64_t r1 = (a.n < r0 + a.rows_per_wg) ? a.n : r0 + a.rows_per_wg;
     const bool use_boost = a.boost > 0.0f && a.ep_ids != nullptr;
     uint64_t list = kEmptyKey, thr = kEmptyKey;
-    for (int64_t base = r0 + 4 * wave; base < r1; base += 16) {
-        const int64_t r = base + grp;
-        const bool valid = r < r1;
-        const int64_t rr = valid ? r : r1 - 1;
-        const float ts = a.ts[rr];
-        const int32_t mod = (a.mod_filter >= 0) ? a.mods[rr] : 0;
-        const int32_t ep = use_boost ? a.ep_ids[rr] : -1;
-        const float dot = row16_sum(qf.dot(emb + rr * a.d, sub));
-        const float s = fuse_score(dot, ts, mod, ep, a);
-        if (valid && sub == 0) a.fin[r] = s;
-        const uint64_t key = valid ? make_key(s, uint32_t(r)) : kEmptyKey;
-        list_offer(list, thr, key, sub == 0, lane, k);
+    const int64_t ngroups = (a.n + 3) / 4;
+    const int64_t gstride = int64_t(gridDim.x) * 4 * kScanUnroll;
+    for (int64_t g0 = (int64_t(blockIdx.x) * 4 + wave) * kScanUnroll; g0 < ngroups; g0 += gstride) {
+        float dot[kScanUnroll], ts[kScanUnroll];
+        int32_t mod[kScanUnroll], ep[kScanUnroll];
+#pragma unroll
+        for (int u = 0; u < kScanUnroll; ++u) {
+            int64_t rr = (g0 + u) * 4 + grp;
+            rr = rr < a.n ? rr : a.n - 1;
+            ts[u] = a.ts[rr];
+            mod[u] = (a.mod_filter >= 0) ? a.mods[rr] : 0;
+            ep[u] = use_boost ? a.ep_ids[rr] : -1;
+            dot[u] = qf.dot(emb + rr * a.d, sub);
+        }
+#pragma unroll
+        for (int u = 0; u < kScanUnroll; ++u) {
+            const int64_t r = (g0 + u) * 4 + grp;
+            const bool valid = r < a.n;
+            const float s = fuse_score(row16_sum(dot[u]), ts[u], mod[u], ep[u], a);
+            if (valid && sub == 0) a.fin[r] = s;
+            const uint64_t key = valid ? make_key(s, uint32_t(r)) : kEmptyKey;
+            list_offer(list, thr, key, sub == 0, lane, k);
+        }
     }
     s_lists[wave][lane] = list;
     __syncthreads();
@@ -482,7 +497,10 @@ __device__ inline int round_rank(FinShared& sh, bool won, int* rank) {
 // BFS with the visited / claim state in the LDS hash. Returns the visit count,
 // or -1 if the visit set outgrew the table (nothing global but the visit lists
 // was touched, so the caller can run the global-array BFS instead).
-__device__ int bfs_lds(FinShared& sh, const FinalizeArgs& a, int ns, int* levels_out) {
+// With rk > 0 every wave also keeps the rk best (score, id) keys it emits in
+// `best` (wave 0 starts from the seeds), so the results need only a tree merge.
+__device__ int bfs_lds(FinShared& sh, const FinalizeArgs& a, int ns, int* levels_out, uint64_t& best,
+                       uint64_t& bthr, int rk) {
     constexpr int R = 4;                       // 1024-edge rounds cached in registers
     const int tid = int(threadIdx.x);
     for (int i = tid; i < kHashCap; i += kFinThreads) { sh.u.bfs.hkey[i] = 0u; sh.u.bfs.hval[i] = 0xFFFFFFFFu; }
@@ -536,14 +554,16 @@ __device__ int bfs_lds(FinShared& sh, const FinalizeArgs& a, int ns, int* levels
                                      sh.u.bfs.hval[slot[r]] == ((kClaimHop << 16) | uint32_t(pp[r]));
                     int rank = 0;
                     const int wtot = round_rank(sh, won, &rank);
+                    const float sc = fmaxf(ps[r] * a.hop_decay, fv[r] * 0.8f);
                     if (won) {
                         const int pos = out + rank;
                         a.vlist[pos] = nb[r];
                         a.vhop[pos] = h + 1;
-                        a.vscore[pos] = fmaxf(ps[r] * a.hop_decay, fv[r] * 0.8f);
+                        a.vscore[pos] = sc;
                         reinterpret_cast<int64_t*>(a.vro)[pos] = (int64_t(re[r]) << 32) | uint32_t(rb[r]);
                         sh.u.bfs.hval[slot[r]] = (uint32_t(h + 1) << 16) | uint32_t(pos);
                     }
+                    if (rk > 0) wave_offer(best, bthr, won ? make_key(sc, uint32_t(nb[r])) : kEmptyKey, lane_id(), rk);
                     out += wtot;
                     __syncthreads();
                 }
@@ -703,10 +723,13 @@ __device__ void select_sorted(FinShared& sh, const FinalizeArgs& a, int V, int r
     }
 }
 
-// Merge the 16 waves' lists pairwise in LDS; wave 0 returns the result.
-__device__ inline uint64_t tree_merge(FinShared& sh, uint64_t list, int k) {
+// Merge the lists of waves [0, active) pairwise in LDS (waves >= active hold
+// empty lists); wave 0 returns the result. `active` is block-uniform.
+__device__ inline uint64_t tree_merge(FinShared& sh, uint64_t list, int k, int active = kFinWaves) {
     const int lane = lane_id(), wave = int(threadIdx.x >> 6);
-    for (int half = kFinWaves / 2; half > 0; half >>= 1) {
+    int span = 1;
+    while (span < active) span <<= 1;
+    for (int half = span / 2; half > 0; half >>= 1) {
         if (wave >= half && wave < 2 * half) sh.lists[wave][lane] = list;
         __syncthreads();
         if (wave < half) list = wave_merge64(list, sh.lists[wave + half][lane], lane, k);
@@ -726,9 +749,19 @@ __global__ __launch_bounds__(kFinThreads) void k_finalize(FinalizeArgs a) {
     stamp(a, 0);
 
     // ---- A. merge the scan's candidate keys into the K seeds (8 loads in flight per lane)
-    const int n_part = int(*a.gcnt);
+    // the count and the first 8192 keys are loaded together; slots past the count
+    // (left from earlier queries) are masked afterwards
     uint64_t list = kEmptyKey, thr = kEmptyKey;
-    for (int base = wave * 64; base < n_part; base += kFinThreads * 8) {
+    const int n_part = int(*a.gcnt);
+    {
+        uint64_t x[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) x[j] = a.part[wave * 64 + j * kFinThreads + lane];
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            wave_offer(list, thr, (wave * 64 + j * kFinThreads + lane < n_part) ? x[j] : kEmptyKey, lane, k);
+    }
+    for (int base = kFinThreads * 8 + wave * 64; base < n_part; base += kFinThreads * 8) {
         uint64_t x[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
@@ -738,7 +771,7 @@ __global__ __launch_bounds__(kFinThreads) void k_finalize(FinalizeArgs a) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) wave_offer(list, thr, x[j], lane, k);
     }
-    list = tree_merge(sh, list, k);
+    list = tree_merge(sh, list, k, n_part <= kFinThreads ? (n_part + 63) / 64 : kFinWaves);
     if (wave == 0) {
         const int ns = __popcll(__ballot(lane < k && list != kEmptyKey));
         if (lane < ns) {
@@ -753,14 +786,17 @@ __global__ __launch_bounds__(kFinThreads) void k_finalize(FinalizeArgs a) {
         }
         if (lane == 0) sh.s_misc[0] = ns;
     }
-    __threadfence();
+    __threadfence_block();        // one workgroup: readers use L2-coherent loads
     __syncthreads();
     const int ns = sh.s_misc[0];
     stamp(a, 1);
 
     // ---- B. deterministic BFS: LDS hash first, global arrays if it outgrows it
+    const int rk = a.rcap <= 64 ? a.rcap : 0;       // results tracked during the BFS
+    uint64_t best = (wave == 0 && lane < rk) ? list : kEmptyKey;
+    uint64_t bthr = rk > 0 ? __shfl(best, rk - 1) : kEmptyKey;
     int levels = 0;
-    int V = (a.hops < int(kClaimHop)) ? bfs_lds(sh, a, ns, &levels) : -1;   // hop must fit below the claim mark
+    int V = (a.hops < int(kClaimHop)) ? bfs_lds(sh, a, ns, &levels, best, bthr, rk) : -1;   // hop below the claim mark
     const bool in_lds = V >= 0;
     if (!in_lds) {
         __syncthreads();
@@ -770,16 +806,9 @@ __global__ __launch_bounds__(kFinThreads) void k_finalize(FinalizeArgs a) {
     stamp(a, 2);
     // ---- C. results: (score desc, id asc), first rcap
     const int rc = min(a.rcap, V);
-    if (in_lds && rc <= 64) {
-        // wave-held lists over the visit set, hop looked up in the LDS hash
-        uint64_t best = kEmptyKey, bthr = kEmptyKey;
-        for (int base = wave * 64; base < V; base += kFinThreads) {
-            const int i = base + lane;
-            const uint64_t key = (i < V) ? make_key(ld_coherent(a.vscore + i), uint32_t(ld_coherent(a.vlist + i)))
-                                         : kEmptyKey;
-            wave_offer(best, bthr, key, lane, rc > 0 ? rc : 1);
-        }
-        best = tree_merge(sh, best, rc > 0 ? rc : 1);
+    if (in_lds && rk > 0) {
+        // each wave's best emitted keys, merged; hop looked up in the LDS hash
+        best = tree_merge(sh, best, rk);
         if (wave == 0) {
             if (lane < rc) {
                 const int slot = hash_find(sh, key_id(best));
@@ -921,13 +950,13 @@ int launch_scan_t(const ScanArgs& a, hipStream_t s) {
 }  // namespace
 
 void scan_grid(int64_t n, int32_t max_wg, int32_t* rows_per_wg, int32_t* num_wg) {
-    // ~8 workgroups per CU on 256 CUs, at least 64 rows each, multiple of 16 rows
-    const int64_t target = max_wg;
-    int64_t rpw = (n + target - 1) / target;
-    if (rpw < 64) rpw = 64;
-    rpw = (rpw + 15) / 16 * 16;
-    *rows_per_wg = int32_t(rpw);
-    *num_wg = int32_t((n + rpw - 1) / rpw);
+    // grid-stride scan: up to max_wg workgroups, each with at least one step of
+    // 4 waves x kScanUnroll row groups of 4 rows
+    const int64_t per_wg = int64_t(4) * 4 * kScanUnroll;
+    int64_t wg = (n + per_wg - 1) / per_wg;
+    if (wg > max_wg) wg = max_wg;
+    *rows_per_wg = 0;
+    *num_wg = int32_t(wg < 1 ? 1 : wg);
 }
 
 int launch_scan(const ScanArgs& a, hipStream_t s) {
