@@ -1,0 +1,113 @@
+// ============================================================================
+//  mars/memory_cuda.cuh — the reference's query API (include/memory_cuda.cuh of
+//  MARS, lines 63-231) served by libmars_amd on MI355X. Plain C++17: no CUDA or
+//  HIP header is included; code that includes "memory_cuda.cuh" and calls
+//  upload_to_device / create_query_context / query_memory_fast compiles against
+//  this header and links against libmars_amd.so.
+//
+//  Same names, members and semantics as the reference, with these differences:
+//    * device pointers are opaque (void* / typed where HIP-free); `handle` carries
+//      the library objects;
+//    * QueryContext::use_cublas / use_cub_topk / use_wmma are accepted and have no
+//      effect (scoring and selection always run the fused HIP kernels);
+//    * results are sorted by (score desc, node_id asc) and the BFS is the
+//      deterministic first-discoverer BFS (no frontier cap, no compaction cap);
+//    * library errors print a message and exit, as CUDA_CHECK does (lines 52-60);
+//      malformed episode inputs are silent no-ops and an inactive episode scope
+//      falls back to Global, as in the reference (memory_cuda.cu:814-855, 1163-1171).
+//  The importance / novelty / graph-maintenance entry points (lines 234-272) are
+//  not part of this API (no driver calls them).
+// ============================================================================
+#ifndef MEMORY_CUDA_CUH
+#define MEMORY_CUDA_CUH
+
+#include <cstdint>
+#include <vector>
+
+#include "memory_graph.h"
+
+struct mars_graph;
+struct mars_ctx;
+
+struct DeviceMemoryGraph {
+    int32_t num_nodes = 0;
+    int32_t num_edges = 0;
+    int32_t embedding_dim = 0;
+    int32_t* d_row_offsets = nullptr;
+    int32_t* d_col_indices = nullptr;
+    float* d_embeddings = nullptr;
+    void* d_embeddings_fp16 = nullptr;     // binary16 rows
+    int32_t* d_modalities = nullptr;
+    float* d_timestamps = nullptr;
+    int32_t* d_episode_ids = nullptr;
+    int32_t* d_ep_csr_offsets = nullptr;
+    int32_t* d_ep_csr_members = nullptr;
+    int32_t episode_num_episodes = 0;
+    int32_t episode_csr_member_total = 0;
+    float* d_importance = nullptr;         // never allocated here
+    int32_t* d_edge_hits = nullptr;        // never allocated here
+    mars_graph* handle = nullptr;
+};
+
+DeviceMemoryGraph upload_to_device(const MemoryGraph& h);
+void free_device(DeviceMemoryGraph& d);
+void upload_episode_ids(DeviceMemoryGraph& dg, const int32_t* host_episode_ids, int32_t num_ids);
+void upload_episode_csr(DeviceMemoryGraph& dg, const HostEpisodeCSR& csr);
+void upload_fp16_embeddings(DeviceMemoryGraph& dg);
+void free_fp16_embeddings(DeviceMemoryGraph& dg);
+
+struct QueryResult {
+    int32_t node_id;
+    float score;
+    int32_t modality;
+    int32_t hops_from_seed;
+};
+
+struct RetrievalConfig {
+    int32_t top_k = 10;
+    int32_t bfs_max_hops = 2;
+    float time_decay_lambda = 1e-8f;
+    float bfs_score_decay = 0.5f;
+    int32_t modality_filter = -1;
+    bool use_importance = false;
+    int32_t max_results_returned = -1;
+    RetrievalScope retrieval_scope = RetrievalScope::Global;
+    int32_t query_episode_id = -1;
+    int32_t query_episode_member_begin = 0;
+    int32_t query_episode_member_count = 0;
+    float episode_same_boost = 0.0f;
+};
+
+struct RetrievalStats {
+    float gpu_ms_similarity = 0.0f;
+    float gpu_ms_topk = 0.0f;
+    float gpu_ms_bfs = 0.0f;
+    float gpu_ms_rerank = 0.0f;
+    float gpu_ms_total = 0.0f;
+    int32_t nodes_scanned = 0;
+    int32_t bfs_waves = 0;
+};
+
+std::vector<QueryResult> query_memory(const DeviceMemoryGraph& dg, const float* h_query, float query_timestamp,
+                                      const RetrievalConfig& cfg, RetrievalStats& stats);
+
+struct QueryContext {
+    int32_t max_nodes = 0;
+    int32_t embedding_dim = 0;
+    int32_t max_k = 0;
+    bool valid = false;
+    bool use_cuda_graph = false;
+    bool use_fp16 = false;
+    bool use_cublas = true;       // accepted, no effect
+    bool use_cub_topk = true;     // accepted, no effect
+    bool use_wmma = false;        // accepted, no effect
+    mars_ctx* handle = nullptr;
+};
+
+QueryContext create_query_context(int32_t max_nodes, int32_t embedding_dim, int32_t max_k = 64);
+void destroy_query_context(QueryContext& ctx);
+
+std::vector<QueryResult> query_memory_fast(const DeviceMemoryGraph& dg, QueryContext& ctx, const float* h_query,
+                                           float query_timestamp, const RetrievalConfig& cfg, RetrievalStats& stats);
+
+#endif  // MEMORY_CUDA_CUH

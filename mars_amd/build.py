@@ -25,7 +25,9 @@ ARCH = "gfx950"
 # hipcc ignores the feature with a warning).
 NO_PK_FP32 = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 COMMON = ["-std=c++17", "-O3", "-fPIC", f"-I{ROOT / 'include'}", f"-I{CSRC}"]
-SOURCES = ["api.hip", "kernels.hip", "batch.hip", "corpus.cpp"]
+SOURCES = ["api.hip", "kernels.hip", "batch.hip", "corpus.cpp", "shim.cpp"]
+DRIVER_SRC = ROOT / "tests" / "cpp" / "shim_driver.cpp"
+DRIVER = ROOT / "tests" / "cpp" / "shim_driver"
 
 
 def _compile(src: str) -> Path:
@@ -52,8 +54,14 @@ def build_library(verbose: bool = False) -> Path:
     if r.returncode != 0:
         raise RuntimeError(f"link failed: {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
     os.replace(tmp, LIB)
+    # the C++ driver of the reference-API shim (tests run it)
+    cmd = [CXX, "-std=c++17", "-O2", f"-I{ROOT / 'include'}", str(DRIVER_SRC), "-o", str(DRIVER),
+           f"-L{PKG}", "-lmars_amd", f"-Wl,-rpath,{PKG}", "-Wl,-rpath,$ORIGIN/../../mars_amd"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"driver build failed: {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
     if verbose:
-        print(f"built {LIB}")
+        print(f"built {LIB} and {DRIVER}")
     return LIB
 
 

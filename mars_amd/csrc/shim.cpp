@@ -1,0 +1,178 @@
+// ============================================================================
+//  shim.cpp — the reference's C++ query API (include/mars/memory_cuda.cuh,
+//  include/mars/memory_graph.h) over the C ABI of libmars_amd.
+//
+//  Error behaviour mirrors the reference: a failing library call prints the
+//  library's message and exits (CUDA_CHECK, memory_cuda.cuh:52-60); malformed
+//  episode inputs are silent no-ops (memory_cuda.cu:814-855).
+// ============================================================================
+#include "mars/memory_cuda.cuh"
+#include "mars/memory_graph.h"
+#include "mars_amd.h"
+#include "mars_corpus.h"
+
+#include <algorithm>
+#include <cstdio>
+#include <cstdlib>
+
+namespace {
+
+void die_on(int rc, const char* what) {
+    if (rc == MARS_OK) return;
+    std::fprintf(stderr, "libmars_amd error in %s (%d): %s\n", what, rc, mars_last_error());
+    std::exit(EXIT_FAILURE);
+}
+
+void refresh_view(DeviceMemoryGraph& d) {
+    mars_graph_view v{};
+    die_on(mars_graph_get_view(d.handle, &v), "mars_graph_get_view");
+    d.num_nodes = v.num_nodes;
+    d.num_edges = v.num_edges;
+    d.embedding_dim = v.embedding_dim;
+    d.d_row_offsets = static_cast<int32_t*>(v.d_row_offsets);
+    d.d_col_indices = static_cast<int32_t*>(v.d_col_indices);
+    d.d_embeddings = static_cast<float*>(v.d_embeddings);
+    d.d_embeddings_fp16 = v.d_embeddings_fp16;
+    d.d_modalities = static_cast<int32_t*>(v.d_modalities);
+    d.d_timestamps = static_cast<float*>(v.d_timestamps);
+    d.d_episode_ids = static_cast<int32_t*>(v.d_episode_ids);
+    d.d_ep_csr_offsets = static_cast<int32_t*>(v.d_ep_csr_offsets);
+    d.d_ep_csr_members = static_cast<int32_t*>(v.d_ep_csr_members);
+    d.episode_num_episodes = v.episode_num_episodes;
+    d.episode_csr_member_total = v.episode_csr_member_total;
+}
+
+mars_retrieval_config to_c(const RetrievalConfig& c) {
+    mars_retrieval_config r;
+    r.top_k = c.top_k;
+    r.bfs_max_hops = c.bfs_max_hops;
+    r.time_decay_lambda = c.time_decay_lambda;
+    r.bfs_score_decay = c.bfs_score_decay;
+    r.modality_filter = c.modality_filter;
+    r.use_importance = c.use_importance ? 1 : 0;
+    r.max_results_returned = c.max_results_returned;
+    r.retrieval_scope = static_cast<int32_t>(c.retrieval_scope);
+    r.query_episode_id = c.query_episode_id;
+    r.query_episode_member_begin = c.query_episode_member_begin;
+    r.query_episode_member_count = c.query_episode_member_count;
+    r.episode_same_boost = c.episode_same_boost;
+    return r;
+}
+
+}  // namespace
+
+HostEpisodeCSR build_episode_csr(const std::vector<int32_t>& episode_ids, int32_t num_nodes) {
+    HostEpisodeCSR out;
+    if (num_nodes <= 0 || int32_t(episode_ids.size()) != num_nodes) return out;      // memory_graph.cpp:15-16
+    int32_t ne = 0;
+    if (mars_build_episode_csr(episode_ids.data(), num_nodes, &ne, nullptr, nullptr) != MARS_OK) return out;
+    out.num_episodes = ne;
+    out.ep_csr_offsets.resize(size_t(ne) + 1);
+    out.ep_csr_members.resize(size_t(num_nodes));
+    mars_build_episode_csr(episode_ids.data(), num_nodes, &ne, out.ep_csr_offsets.data(), out.ep_csr_members.data());
+    return out;
+}
+
+DeviceMemoryGraph upload_to_device(const MemoryGraph& h) {
+    mars_graph_desc desc{};
+    desc.num_nodes = h.num_nodes;
+    desc.num_edges = int32_t(h.col_indices.size());
+    desc.embedding_dim = h.embedding_dim;
+    desc.row_offsets = h.row_offsets.empty() ? nullptr : h.row_offsets.data();
+    desc.col_indices = h.col_indices.empty() ? nullptr : h.col_indices.data();
+    desc.embeddings = h.embeddings.data();
+    desc.modalities = h.modalities.data();
+    desc.timestamps = h.timestamps.data();
+    DeviceMemoryGraph d;
+    die_on(mars_graph_create(&desc, &d.handle), "upload_to_device");
+    refresh_view(d);
+    return d;
+}
+
+void free_device(DeviceMemoryGraph& d) {
+    if (d.handle) mars_graph_destroy(d.handle);
+    d = DeviceMemoryGraph{};
+}
+
+void upload_episode_ids(DeviceMemoryGraph& dg, const int32_t* ids, int32_t n) {
+    if (!dg.handle) return;
+    (void)mars_graph_set_episode_ids(dg.handle, ids, n);          // bad input: cleared, no error
+    refresh_view(dg);
+}
+
+void upload_episode_csr(DeviceMemoryGraph& dg, const HostEpisodeCSR& csr) {
+    if (!dg.handle) return;
+    const bool shaped = csr.num_episodes > 0 && int32_t(csr.ep_csr_offsets.size()) == csr.num_episodes + 1 &&
+                        int32_t(csr.ep_csr_members.size()) == csr.ep_csr_offsets.back();
+    if (shaped)
+        (void)mars_graph_set_episode_csr(dg.handle, csr.num_episodes, csr.ep_csr_offsets.data(),
+                                         csr.ep_csr_members.data(), int32_t(csr.ep_csr_members.size()));
+    else
+        (void)mars_graph_set_episode_csr(dg.handle, 0, nullptr, nullptr, 0);   // cleared, as the reference
+    refresh_view(dg);
+}
+
+void upload_fp16_embeddings(DeviceMemoryGraph& dg) {
+    if (!dg.handle) return;
+    die_on(mars_graph_enable_fp16(dg.handle), "upload_fp16_embeddings");
+    refresh_view(dg);
+}
+
+void free_fp16_embeddings(DeviceMemoryGraph& dg) {
+    if (!dg.handle) return;
+    die_on(mars_graph_disable_fp16(dg.handle), "free_fp16_embeddings");
+    refresh_view(dg);
+}
+
+QueryContext create_query_context(int32_t max_nodes, int32_t embedding_dim, int32_t max_k) {
+    QueryContext ctx;
+    die_on(mars_ctx_create(max_nodes, embedding_dim, max_k, MARS_CTX_TIMING, &ctx.handle), "create_query_context");
+    ctx.max_nodes = max_nodes;
+    ctx.embedding_dim = embedding_dim;
+    ctx.max_k = std::min(max_k, 64);
+    ctx.valid = true;
+    return ctx;
+}
+
+void destroy_query_context(QueryContext& ctx) {
+    if (!ctx.valid) return;
+    mars_ctx_destroy(ctx.handle);
+    ctx = QueryContext{};
+}
+
+std::vector<QueryResult> query_memory_fast(const DeviceMemoryGraph& dg, QueryContext& ctx, const float* h_query,
+                                           float query_timestamp, const RetrievalConfig& cfg, RetrievalStats& stats) {
+    uint32_t flags = MARS_CTX_TIMING;                         // stats are always filled, as the reference
+    if (ctx.use_fp16) flags |= MARS_CTX_USE_FP16;
+    if (ctx.use_cuda_graph) flags |= MARS_CTX_USE_GRAPH;
+    die_on(mars_ctx_set_flags(ctx.handle, flags), "query_memory_fast");
+    const mars_retrieval_config c = to_c(cfg);
+    std::vector<mars_query_result> buf(size_t(std::max(1, cfg.max_results_returned > 0 ? cfg.max_results_returned
+                                                                                      : std::min(cfg.top_k, 64))));
+    int32_t n = 0;
+    mars_stats st{};
+    die_on(mars_query(dg.handle, ctx.handle, h_query, query_timestamp, &c, buf.data(), int32_t(buf.size()), &n, &st),
+           "query_memory_fast");
+    std::vector<QueryResult> out;
+    out.reserve(size_t(n));
+    for (int32_t i = 0; i < std::min<int32_t>(n, int32_t(buf.size())); ++i)
+        out.push_back({buf[size_t(i)].node_id, buf[size_t(i)].score, buf[size_t(i)].modality,
+                       buf[size_t(i)].hops_from_seed});
+    stats.gpu_ms_similarity = st.gpu_ms_similarity;
+    stats.gpu_ms_topk = st.gpu_ms_topk;
+    stats.gpu_ms_bfs = st.gpu_ms_bfs;
+    stats.gpu_ms_rerank = st.gpu_ms_rerank;
+    stats.gpu_ms_total = st.gpu_ms_total;
+    stats.nodes_scanned = st.nodes_scanned;
+    stats.bfs_waves = st.bfs_waves;
+    return out;
+}
+
+std::vector<QueryResult> query_memory(const DeviceMemoryGraph& dg, const float* h_query, float query_timestamp,
+                                      const RetrievalConfig& cfg, RetrievalStats& stats) {
+    // the reference allocates per call (memory_cuda.cu:881-1026); so does this one
+    QueryContext ctx = create_query_context(dg.num_nodes, dg.embedding_dim, 64);
+    std::vector<QueryResult> r = query_memory_fast(dg, ctx, h_query, query_timestamp, cfg, stats);
+    destroy_query_context(ctx);
+    return r;
+}
