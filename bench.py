@@ -140,6 +140,12 @@ def main() -> int:
     (lat_gk, kern_g, bfs_g), _ = timed(W, KT, C.pointer(g1), 1, True)
     log(f"global fp32: p50 {pctl(lat_g, .5):.1f} us p99 {pctl(lat_g, .99):.1f} us; {S / wall_g:.0f} q/s; scan kernel "
         f"mean {kern_g.mean():.1f} us ({bytes_f32 / kern_g.mean() / 1e3:.0f} GB/s); finalize mean {bfs_g.mean():.1f} us")
+    # the same queries replayed as a hipGraph (kernel-node arguments rewritten per query)
+    ctx.use_cuda_graph = True
+    run(0, W, C.pointer(g1), 1)
+    (lat_gg, _, _), wall_gg = timed(W, S, C.pointer(g1), 1, False)
+    ctx.use_cuda_graph = False
+    log(f"global fp32 (graph replay): p50 {pctl(lat_gg, .5):.1f} us p99 {pctl(lat_gg, .99):.1f} us")
     # finalize phase breakdown (seed merge, BFS, selection) from the GPU realtime counter
     ctx.timing = False
     ph = []
@@ -158,6 +164,11 @@ def main() -> int:
         (_, kern_e, _), _ = timed(W, KT, ec_t, KT, True)
         log(f"episode: p50 {pctl(lat_e, .5):.1f} us p99 {pctl(lat_e, .99):.1f} us; {S / wall_e:.0f} q/s; kernel mean "
             f"{kern_e.mean():.1f} us")
+        ctx.use_cuda_graph = True
+        run(0, W, ec, W) if W else None
+        (lat_eg, _, _), _ = timed(W, S, ec_t, S, False)
+        ctx.use_cuda_graph = False
+        log(f"episode (graph replay): p50 {pctl(lat_eg, .5):.1f} us p99 {pctl(lat_eg, .99):.1f} us")
         # ---- global fp16
         ctx.use_fp16 = True
         run(0, W, C.pointer(g1), 1)
@@ -187,7 +198,8 @@ def main() -> int:
         log(f"batch Q=64: p50 {pctl(bl, .5):.0f} us; scan {bkm:.0f} us = {flops / bkm / 1e6:.0f} TFLOP/s "
             f"({flops / bkm / 1e6 / 25:.1f}% of 2.5 PF), {bytes_f16 / bkm / 1e3:.0f} GB/s")
         out["episode"] = dict(p50_us=pctl(lat_e, .5), p99_us=pctl(lat_e, .99), qps=S / wall_e,
-                              kernel_mean_us=float(kern_e.mean()))
+                              kernel_mean_us=float(kern_e.mean()),
+                              graph_replay=dict(p50_us=pctl(lat_eg, .5), p99_us=pctl(lat_eg, .99)))
         out["global_fp16"] = dict(p50_us=pctl(lat_h, .5), p99_us=pctl(lat_h, .99), qps=S / wall_h,
                                   scan_kernel_mean_us=float(kern_h.mean()),
                                   scan_gbs=bytes_f16 / float(kern_h.mean()) / 1e3,
@@ -213,6 +225,7 @@ def main() -> int:
                    "corpus_seed": args.seed, "query_seed": args.query_seed, "num_edges": int(len(c.col_indices))},
         "global_fp32": dict(p50_us=pctl(lat_g, .5), p99_us=pctl(lat_g, .99), qps=S / wall_g,
                             p99_us_with_events=pctl(lat_gk, .99),
+                            graph_replay=dict(p50_us=pctl(lat_gg, .5), p99_us=pctl(lat_gg, .99)),
                             scan_kernel_mean_us=float(kern_g.mean()), finalize_kernel_mean_us=float(bfs_g.mean()),
                             finalize_phases_us=dict(seed_merge=float(ph[:, 0].mean()), bfs=float(ph[:, 1].mean()),
                                                     select=float(ph[:, 2].mean()))),

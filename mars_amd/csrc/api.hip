@@ -124,6 +124,8 @@ int graph_free(Graph& g) {
     return MARS_OK;
 }
 
+void graph_slot_free(Ctx::GraphSlot& g);
+
 int ctx_free(Ctx& c) {
     (void)use_device(c.device);
     if (c.stream) (void)hipStreamSynchronize(c.stream);
@@ -134,8 +136,46 @@ int ctx_free(Ctx& c) {
     if (c.h_query) (void)hipHostFree(c.h_query);
     if (c.h_res) (void)hipHostFree(c.h_res);
     for (auto& e : c.ev) if (e) (void)hipEventDestroy(e);
+    graph_slot_free(c.g_global);
+    graph_slot_free(c.g_episode);
     if (c.stream) (void)hipStreamDestroy(c.stream);
     c = Ctx{};
+    return MARS_OK;
+}
+
+void graph_slot_free(Ctx::GraphSlot& g) {
+    if (g.exec) (void)hipGraphExecDestroy(g.exec);
+    if (g.graph) (void)hipGraphDestroy(g.graph);
+    g = Ctx::GraphSlot{};
+}
+
+// Launch 1 or 2 dependent kernels as a replayed graph: the graph is built once per
+// (kernel, grid) shape and each query only rewrites the kernel-node arguments, so no
+// per-query value (query time, epoch, ...) is frozen into it.
+int graph_launch(Ctx::GraphSlot& g, int n, const KernelLaunch* l, void* const* args, hipStream_t s) {
+    hipKernelNodeParams p[2];
+    for (int i = 0; i < n; ++i) {
+        p[i] = hipKernelNodeParams{};
+        p[i].func = const_cast<void*>(l[i].fn);
+        p[i].gridDim = l[i].grid;
+        p[i].blockDim = l[i].block;
+        p[i].sharedMemBytes = 0;
+        p[i].kernelParams = const_cast<void**>(&args[i]);
+        p[i].extra = nullptr;
+    }
+    const bool same = g.exec && g.fn[0] == l[0].fn && (n < 2 || g.fn[1] == l[1].fn) && g.grid0 == l[0].grid.x;
+    if (!same) {
+        graph_slot_free(g);
+        MARS_HIP(hipGraphCreate(&g.graph, 0));
+        for (int i = 0; i < n; ++i)
+            MARS_HIP(hipGraphAddKernelNode(&g.node[i], g.graph, i ? &g.node[i - 1] : nullptr, i ? 1 : 0, &p[i]));
+        MARS_HIP(hipGraphInstantiate(&g.exec, g.graph, nullptr, nullptr, 0));
+        for (int i = 0; i < n; ++i) g.fn[i] = l[i].fn;
+        g.grid0 = l[0].grid.x;
+    } else {
+        for (int i = 0; i < n; ++i) MARS_HIP(hipGraphExecKernelNodeSetParams(g.exec, g.node[i], &p[i]));
+    }
+    MARS_HIP(hipGraphLaunch(g.exec, s));
     return MARS_OK;
 }
 
@@ -162,6 +202,7 @@ int query_impl(const mars_graph* gh, mars_ctx* ch, const float* h_q, const float
     hipStream_t s = c.stream;
     const bool timing = (c.flags & MARS_CTX_TIMING) != 0;
     const bool fp16 = !scoped && (c.flags & MARS_CTX_USE_FP16) && g.emb16 != nullptr;
+    const bool use_graph = (c.flags & MARS_CTX_USE_GRAPH) != 0;
 
     const float* q = d_q;
     if (!q) {
@@ -178,7 +219,13 @@ int query_impl(const mars_graph* gh, mars_ctx* ch, const float* h_q, const float
         a.t_q = t_q; a.lambda = cfg->time_decay_lambda; a.mod_filter = cfg->modality_filter;
         a.k = K; a.rcap = rcap; a.keybuf = c.sortbuf;
         a.seed_idx = c.seed_idx; a.seed_val = c.seed_val; a.res = c.d_res; a.rec = c.d_rec;
-        MARS_TRY(launch_episode(a, s));
+        if (use_graph) {
+            const KernelLaunch l = episode_launch();
+            void* args[1] = {&a};
+            MARS_TRY(graph_launch(c.g_episode, 1, &l, args, s));
+        } else {
+            MARS_TRY(launch_episode(a, s));
+        }
         if (timing) MARS_HIP(hipEventRecord(c.ev[1], s));
     } else {
         int32_t rpw = 0, nwg = 0;
@@ -191,8 +238,6 @@ int query_impl(const mars_graph* gh, mars_ctx* ch, const float* h_q, const float
         a.boost = (g.ep_ids && cfg->query_episode_id >= 0) ? cfg->episode_same_boost : 0.0f;
         a.k = K; a.fin = c.fin; a.part = c.part; a.gthr = c.gthr; a.gcnt = c.gcnt; a.rows_per_wg = rpw;
         a.num_wg = nwg;
-        MARS_TRY(launch_scan(a, s));
-        if (timing) MARS_HIP(hipEventRecord(c.ev[1], s));
         // visit stamps / claim generations: no O(N) reset per query
         if (c.epoch == 0xFFFFFFFFu) {
             MARS_HIP(hipMemsetAsync(c.vis, 0, size_t(c.max_nodes) * sizeof(uint32_t), s));
@@ -213,7 +258,17 @@ int query_impl(const mars_graph* gh, mars_ctx* ch, const float* h_q, const float
         f.vscore = c.vscore; f.vro = c.vro; f.sortbuf = c.sortbuf; f.cap_visit = c.max_nodes; f.rcap = rcap;
         f.seed_idx = c.seed_idx; f.seed_val = c.seed_val; f.res = c.d_res; f.rec = c.d_rec;
         f.stamps = c.stamps;
-        if (launch_finalize(f, s) != MARS_OK) {
+        if (use_graph) {
+            // one replayed graph for both kernels (the per-stage split is not timed)
+            const KernelLaunch l[2] = {scan_launch(a), finalize_launch()};
+            void* args[2] = {&a, &f};
+            MARS_TRY(graph_launch(c.g_global, 2, l, args, s));
+            if (timing) MARS_HIP(hipEventRecord(c.ev[1], s));
+        } else {
+            MARS_TRY(launch_scan(a, s));
+            if (timing) MARS_HIP(hipEventRecord(c.ev[1], s));
+        }
+        if (!use_graph && launch_finalize(f, s) != MARS_OK) {
             // the scan already appended candidates: clear them for the next query
             (void)hipMemsetAsync(c.gcnt, 0, sizeof(uint32_t), s);
             (void)hipMemsetAsync(c.gthr, 0xFF, sizeof(uint64_t), s);

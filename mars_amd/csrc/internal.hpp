@@ -137,6 +137,15 @@ struct Ctx {
     uint64_t* bout = nullptr;      // merged keys per query
     int32_t bcap_q = 0;
     int64_t bcap_part = 0;
+    // replayed query graphs (kernel nodes updated per query)
+    struct GraphSlot {
+        hipGraph_t graph = nullptr;
+        hipGraphExec_t exec = nullptr;
+        hipGraphNode_t node[2] = {nullptr, nullptr};
+        const void* fn[2] = {nullptr, nullptr};
+        unsigned grid0 = 0;
+    };
+    GraphSlot g_global, g_episode;
 };
 
 // ---- launch helpers (defined in kernels.hip) --------------------------------------
@@ -162,7 +171,16 @@ struct ScanArgs {
     int32_t rows_per_wg;     // unused (grid-stride scan)
     int32_t num_wg;
 };
+// Kernel entry point + launch shape of one launch (for graph kernel nodes).
+struct KernelLaunch {
+    const void* fn = nullptr;
+    dim3 grid;
+    dim3 block;
+};
 int launch_scan(const ScanArgs& a, hipStream_t s);
+KernelLaunch scan_launch(const ScanArgs& a);
+KernelLaunch finalize_launch();
+KernelLaunch episode_launch();
 void scan_grid(int64_t n, int32_t max_wg, int32_t* rows_per_wg, int32_t* num_wg);
 
 struct FinalizeArgs {

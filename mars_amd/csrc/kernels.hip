@@ -941,10 +941,12 @@ __global__ void k_convert_f16(const float* __restrict__ in, __half* __restrict__
 }
 
 template <typename T, typename QF>
-int launch_scan_t(const ScanArgs& a, hipStream_t s) {
-    hipLaunchKernelGGL((k_scan<T, QF>), dim3(unsigned(a.num_wg)), dim3(256), 0, s, a);
-    MARS_HIP(hipGetLastError());
-    return MARS_OK;
+KernelLaunch scan_launch_t(const ScanArgs& a) {
+    KernelLaunch l;
+    l.fn = reinterpret_cast<const void*>(&k_scan<T, QF>);
+    l.grid = dim3(unsigned(a.num_wg));
+    l.block = dim3(256);
+    return l;
 }
 
 }  // namespace
@@ -959,30 +961,53 @@ void scan_grid(int64_t n, int32_t max_wg, int32_t* rows_per_wg, int32_t* num_wg)
     *num_wg = int32_t(wg < 1 ? 1 : wg);
 }
 
-int launch_scan(const ScanArgs& a, hipStream_t s) {
+KernelLaunch scan_launch(const ScanArgs& a) {
     const bool f16 = a.fp16 != 0;
     if (!f16 && a.d % 64 == 0) {
         switch (a.d / 64) {
-            case 4: return launch_scan_t<float, QF32<4>>(a, s);
-            case 6: return launch_scan_t<float, QF32<6>>(a, s);
-            case 8: return launch_scan_t<float, QF32<8>>(a, s);
-            case 12: return launch_scan_t<float, QF32<12>>(a, s);
-            case 16: return launch_scan_t<float, QF32<16>>(a, s);
+            case 4: return scan_launch_t<float, QF32<4>>(a);
+            case 6: return scan_launch_t<float, QF32<6>>(a);
+            case 8: return scan_launch_t<float, QF32<8>>(a);
+            case 12: return scan_launch_t<float, QF32<12>>(a);
+            case 16: return scan_launch_t<float, QF32<16>>(a);
             default: break;
         }
     }
     if (f16 && a.d % 128 == 0) {
         switch (a.d / 128) {
-            case 2: return launch_scan_t<__half, QF16<2>>(a, s);
-            case 3: return launch_scan_t<__half, QF16<3>>(a, s);
-            case 4: return launch_scan_t<__half, QF16<4>>(a, s);
-            case 6: return launch_scan_t<__half, QF16<6>>(a, s);
-            case 8: return launch_scan_t<__half, QF16<8>>(a, s);
+            case 2: return scan_launch_t<__half, QF16<2>>(a);
+            case 3: return scan_launch_t<__half, QF16<3>>(a);
+            case 4: return scan_launch_t<__half, QF16<4>>(a);
+            case 6: return scan_launch_t<__half, QF16<6>>(a);
+            case 8: return scan_launch_t<__half, QF16<8>>(a);
             default: break;
         }
     }
-    if (f16) return launch_scan_t<__half, QGeneric>(a, s);
-    return launch_scan_t<float, QGeneric>(a, s);
+    if (f16) return scan_launch_t<__half, QGeneric>(a);
+    return scan_launch_t<float, QGeneric>(a);
+}
+
+KernelLaunch finalize_launch() {
+    KernelLaunch l;
+    l.fn = reinterpret_cast<const void*>(&k_finalize);
+    l.grid = dim3(1);
+    l.block = dim3(kFinThreads);
+    return l;
+}
+
+KernelLaunch episode_launch() {
+    KernelLaunch l;
+    l.fn = reinterpret_cast<const void*>(&k_episode);
+    l.grid = dim3(1);
+    l.block = dim3(256);
+    return l;
+}
+
+int launch_scan(const ScanArgs& a, hipStream_t s) {
+    const KernelLaunch l = scan_launch(a);
+    void* args[] = {const_cast<ScanArgs*>(&a)};
+    MARS_HIP(hipLaunchKernel(l.fn, l.grid, l.block, args, 0, s));
+    return MARS_OK;
 }
 
 int launch_finalize(const FinalizeArgs& a, hipStream_t s) {

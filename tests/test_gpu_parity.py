@@ -406,3 +406,32 @@ def test_gpu_knn_matches_cpu_exact():
         assert np.all(got != np.arange(c.num_nodes)[:, None])
     finally:
         dev.close()
+
+
+# ---------------------------------------------------------------- replayed query graphs
+def test_graph_replay_matches_eager(dev10k, corpus_10k):
+    """Replays of the query graph (arguments rewritten per query) interleaved with
+    eager queries: every replay returns exactly the eager result."""
+    qs = corpus.pick_queries(corpus_10k.modalities, 24, seed=606)
+    off = dev10k.csr.ep_csr_offsets
+    try:
+        for fp16 in (False, True):
+            dev10k.ctx.use_fp16 = fp16
+            for i, node in enumerate(qs):
+                ep = int(corpus_10k.episode_ids[node])
+                cfgs = [RetrievalConfig(top_k=10, time_decay_lambda=LAM, max_results_returned=15),
+                        RetrievalConfig(top_k=10, time_decay_lambda=LAM, max_results_returned=15,
+                                        retrieval_scope=RetrievalScope.EpisodeScoped, query_episode_id=ep,
+                                        query_episode_member_begin=int(off[ep]),
+                                        query_episode_member_count=int(off[ep + 1] - off[ep]))]
+                for cfg in cfgs:
+                    t = T_Q - 5.0 * (i % 3)                   # the query time changes between replays
+                    dev10k.ctx.use_cuda_graph = False
+                    eager, _ = dev10k.query(corpus_10k.embeddings[node], cfg, t_q=t)
+                    dev10k.ctx.use_cuda_graph = True
+                    replay, _ = dev10k.query(corpus_10k.embeddings[node], cfg, t_q=t)
+                    replay2, _ = dev10k.query(corpus_10k.embeddings[node], cfg, t_q=t)
+                    assert replay == eager and replay2 == eager, (fp16, i, cfg.retrieval_scope)
+    finally:
+        dev10k.ctx.use_cuda_graph = False
+        dev10k.ctx.use_fp16 = False
