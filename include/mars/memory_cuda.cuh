@@ -33,7 +33,7 @@ struct DeviceMemoryGraph {
     int32_t num_nodes = 0;
     int32_t num_edges = 0;
     int32_t embedding_dim = 0;
-    int32_t* d_row_offsets = nullptr;
+    int32_t* d_row_offsets = nullptr;      // not kept on the device (see d_row_words)
     int32_t* d_col_indices = nullptr;
     float* d_embeddings = nullptr;
     void* d_embeddings_fp16 = nullptr;     // binary16 rows
@@ -46,6 +46,7 @@ struct DeviceMemoryGraph {
     int32_t episode_csr_member_total = 0;
     float* d_importance = nullptr;         // never allocated here
     int32_t* d_edge_hits = nullptr;        // never allocated here
+    int64_t* d_row_words = nullptr;        // per node: (row length << 32) | row start in col
     mars_graph* handle = nullptr;
 };
 

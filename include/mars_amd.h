@@ -122,7 +122,7 @@ typedef struct mars_graph_view {
     int32_t  episode_num_episodes;
     int32_t  episode_csr_member_total;
     int32_t  has_fp16;
-    void*    d_row_offsets;
+    void*    d_row_words;      /* int64 per node: (row length << 32) | row start in col */
     void*    d_col_indices;
     void*    d_embeddings;
     void*    d_embeddings_fp16;
@@ -164,7 +164,8 @@ int mars_graph_set_csr(mars_graph* g, int32_t num_edges, const int32_t* row_offs
  * of the NSN graph at corpus sizes a CPU cannot (analogue of the tiled kNN build of
  * src/cmng_build.cu:135-245). */
 int mars_graph_knn(mars_graph* g, int32_t k, int32_t* nbrs);
-/* Copy device arrays back to host (any pointer may be NULL to skip). */
+/* Copy device arrays back to host (any pointer may be NULL to skip): the NSN graph as
+ * a packed CSR (row_offsets: num_nodes + 1, col_indices: num_edges) and the episode CSR. */
 int mars_graph_download(const mars_graph* g, int32_t* row_offsets, int32_t* col_indices,
                         int32_t* ep_offsets, int32_t* ep_members);
 

@@ -91,7 +91,7 @@ class GraphViewC(C.Structure):
         ("episode_num_episodes", C.c_int32),
         ("episode_csr_member_total", C.c_int32),
         ("has_fp16", C.c_int32),
-        ("d_row_offsets", C.c_void_p),
+        ("d_row_words", C.c_void_p),
         ("d_col_indices", C.c_void_p),
         ("d_embeddings", C.c_void_p),
         ("d_embeddings_fp16", C.c_void_p),

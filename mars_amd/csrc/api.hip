@@ -17,8 +17,6 @@
 #include <cstring>
 #include <vector>
 
-struct mars_graph { mars::Graph g; };
-struct mars_ctx { mars::Ctx c; };
 
 namespace mars {
 
@@ -118,9 +116,35 @@ namespace {
 
 int graph_free(Graph& g) {
     (void)use_device(g.device);
-    dfree(g.emb); dfree(g.emb16); dfree(g.mods); dfree(g.ts); dfree(g.row); dfree(g.col);
+    if (g.ins_stream) (void)hipStreamSynchronize(g.ins_stream);
+    dfree(g.emb); dfree(g.emb16); dfree(g.mods); dfree(g.ts); dfree(g.ro); dfree(g.rcap); dfree(g.col);
     dfree(g.ep_ids); dfree(g.ep_off); dfree(g.ep_mem);
+    if (g.ins_stream) (void)hipStreamDestroy(g.ins_stream);
     g = Graph{};
+    return MARS_OK;
+}
+
+// Row words from a host CSR (rows packed back to back, no slack) and their upload.
+int load_csr(Graph& g, int32_t n, int32_t e, const int32_t* row, const int32_t* col, hipMemcpyKind kind) {
+    g.ro_h.assign(size_t(g.cap_n), 0);
+    g.rcap_h.assign(size_t(g.cap_n), 0);
+    std::vector<int32_t> hrow;
+    const int32_t* r = row;
+    if (row && kind == hipMemcpyDeviceToDevice) {
+        hrow.resize(size_t(n) + 1);
+        MARS_HIP(hipMemcpy(hrow.data(), row, hrow.size() * sizeof(int32_t), hipMemcpyDeviceToHost));
+        r = hrow.data();
+    }
+    for (int32_t i = 0; i < n; ++i) {
+        const int32_t b = r ? r[i] : 0, len = r ? r[i + 1] - r[i] : 0;
+        g.ro_h[size_t(i)] = (int64_t(len) << 32) | uint32_t(b);
+        g.rcap_h[size_t(i)] = len;
+    }
+    MARS_HIP(hipMemcpy(g.ro, g.ro_h.data(), size_t(g.cap_n) * sizeof(int64_t), hipMemcpyHostToDevice));
+    MARS_HIP(hipMemcpy(g.rcap, g.rcap_h.data(), size_t(g.cap_n) * sizeof(int32_t), hipMemcpyHostToDevice));
+    if (e > 0) MARS_HIP(hipMemcpy(g.col, col, size_t(e) * sizeof(int32_t), kind));
+    g.e = e;
+    g.e_used = e;
     return MARS_OK;
 }
 
@@ -188,11 +212,12 @@ int query_impl(const mars_graph* gh, mars_ctx* ch, const float* h_q, const float
     const Graph& g = gh->g;
     Ctx& c = ch->c;
     MARS_CHECK(g.d == c.d, MARS_ERR_INVALID, "graph dim %d != context dim %d", g.d, c.d);
-    MARS_CHECK(g.n <= c.max_nodes, MARS_ERR_CAPACITY, "graph has %d nodes, context sized for %d", g.n,
-               c.max_nodes);
+    MARS_CHECK(__atomic_load_n(&g.n, __ATOMIC_ACQUIRE) <= c.max_nodes, MARS_ERR_CAPACITY,
+               "graph has %d nodes, context sized for %d", g.n, c.max_nodes);
     MARS_CHECK(g.n > 0, MARS_ERR_INVALID, "empty graph");
     MARS_CHECK(cfg->top_k > 0, MARS_ERR_INVALID, "top_k = %d", cfg->top_k);
     const int32_t K = std::min(cfg->top_k, c.max_k);                      // memory_cuda.cu:1361
+    const int32_t n_live = __atomic_load_n(&g.n, __ATOMIC_ACQUIRE);       // nodes published so far
     const bool scoped = episode_scoped_active(g, *cfg);
     const int32_t hops = scoped ? 0 : std::max(0, cfg->bfs_max_hops);     // :1189
     const int32_t rcap = cfg->max_results_returned > 0 ? cfg->max_results_returned : K;
@@ -213,7 +238,7 @@ int query_impl(const mars_graph* gh, mars_ctx* ch, const float* h_q, const float
     if (timing) MARS_HIP(hipEventRecord(c.ev[0], s));
     if (scoped) {
         EpisodeArgs a{};
-        a.emb = g.emb; a.d = g.d; a.n = g.n; a.q = q; a.ts = g.ts; a.mods = g.mods;
+        a.emb = g.emb; a.d = g.d; a.n = n_live; a.q = q; a.ts = g.ts; a.mods = g.mods;
         a.members = g.ep_mem + cfg->query_episode_member_begin;
         a.m = cfg->query_episode_member_count;
         a.t_q = t_q; a.lambda = cfg->time_decay_lambda; a.mod_filter = cfg->modality_filter;
@@ -229,10 +254,10 @@ int query_impl(const mars_graph* gh, mars_ctx* ch, const float* h_q, const float
         if (timing) MARS_HIP(hipEventRecord(c.ev[1], s));
     } else {
         int32_t rpw = 0, nwg = 0;
-        scan_grid(g.n, kTargetWg, &rpw, &nwg);
+        scan_grid(n_live, kTargetWg, &rpw, &nwg);
         ScanArgs a{};
         a.emb = fp16 ? static_cast<const void*>(g.emb16) : static_cast<const void*>(g.emb);
-        a.fp16 = fp16 ? 1 : 0; a.n = g.n; a.d = g.d; a.q = q; a.ts = g.ts; a.mods = g.mods;
+        a.fp16 = fp16 ? 1 : 0; a.n = n_live; a.d = g.d; a.q = q; a.ts = g.ts; a.mods = g.mods;
         a.ep_ids = g.ep_ids; a.t_q = t_q; a.lambda = cfg->time_decay_lambda;
         a.mod_filter = cfg->modality_filter; a.query_ep = cfg->query_episode_id;
         a.boost = (g.ep_ids && cfg->query_episode_id >= 0) ? cfg->episode_same_boost : 0.0f;
@@ -252,7 +277,7 @@ int query_impl(const mars_graph* gh, mars_ctx* ch, const float* h_q, const float
         const uint32_t gen_base = c.gen;
         c.gen += span;
         FinalizeArgs f{};
-        f.part = c.part; f.gcnt = c.gcnt; f.gthr = c.gthr; f.k = K; f.row = g.row; f.col = g.col; f.fin = c.fin;
+        f.part = c.part; f.gcnt = c.gcnt; f.gthr = c.gthr; f.k = K; f.ro = g.ro; f.col = g.col; f.n_live = n_live; f.fin = c.fin;
         f.mods = g.mods; f.hops = hops; f.hop_decay = cfg->bfs_score_decay; f.epoch = epoch;
         f.gen_base = gen_base; f.vis = c.vis; f.claim = c.claim; f.vlist = c.vlist; f.vhop = c.vhop;
         f.vscore = c.vscore; f.vro = c.vro; f.sortbuf = c.sortbuf; f.cap_visit = c.max_nodes; f.rcap = rcap;
@@ -275,7 +300,7 @@ int query_impl(const mars_graph* gh, mars_ctx* ch, const float* h_q, const float
             (void)hipStreamSynchronize(s);
             return set_error(MARS_ERR_HIP, "finalize launch failed");
         }
-        c.last_n = g.n;
+        c.last_n = n_live;
     }
     if (timing) MARS_HIP(hipEventRecord(c.ev[2], s));
     MARS_HIP(hipStreamSynchronize(s));
@@ -297,7 +322,7 @@ int query_impl(const mars_graph* gh, mars_ctx* ch, const float* h_q, const float
             st.gpu_ms_total = ms;
         }
         // rerank / top-K are fused into the scan: their time is inside gpu_ms_similarity
-        st.nodes_scanned = scoped ? cfg->query_episode_member_count : g.n;
+        st.nodes_scanned = scoped ? cfg->query_episode_member_count : n_live;
         st.bfs_waves = scoped ? 0 : cfg->bfs_max_hops;                     // :1680-1686 semantics
         st.scope_fallback = (cfg->retrieval_scope == MARS_SCOPE_EPISODE_SCOPED && !scoped) ? 1 : 0;
         st.visited = h.visited;
@@ -397,19 +422,16 @@ int mars_graph_create(const mars_graph_desc* d, mars_graph** out) {
     int rc = MARS_OK;
     auto fail = [&](int r) { graph_free(g); delete gh; return r; };
     if ((rc = dmalloc(&g.emb, CN * D)) || (rc = dmalloc(&g.mods, CN)) || (rc = dmalloc(&g.ts, CN)) ||
-        (rc = dmalloc(&g.row, CN + 1)) || (rc = dmalloc(&g.col, size_t(g.cap_e))))
+        (rc = dmalloc(&g.ro, CN)) || (rc = dmalloc(&g.rcap, CN)) || (rc = dmalloc(&g.col, size_t(g.cap_e))))
         return fail(rc);
     const hipMemcpyKind kind = dev ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice;
     hipError_t e = hipSuccess;
     if (e == hipSuccess) e = hipMemcpy(g.emb, d->embeddings, N * D * sizeof(float), kind);
     if (e == hipSuccess) e = hipMemcpy(g.mods, d->modalities, N * sizeof(int32_t), kind);
     if (e == hipSuccess) e = hipMemcpy(g.ts, d->timestamps, N * sizeof(float), kind);
-    if (e == hipSuccess) {
-        if (d->row_offsets) e = hipMemcpy(g.row, d->row_offsets, (N + 1) * sizeof(int32_t), kind);
-        else e = hipMemset(g.row, 0, (N + 1) * sizeof(int32_t));
-    }
-    if (e == hipSuccess && g.e > 0) e = hipMemcpy(g.col, d->col_indices, size_t(g.e) * sizeof(int32_t), kind);
+    if (e == hipSuccess) e = hipStreamCreateWithFlags(&g.ins_stream, hipStreamNonBlocking);
     if (e != hipSuccess) return fail(set_error(MARS_ERR_HIP, "graph upload: %s", hipGetErrorString(e)));
+    if ((rc = load_csr(g, g.n, g.e, d->row_offsets, d->col_indices, kind)) != MARS_OK) return fail(rc);
     *out = gh;
     return MARS_OK;
 }
@@ -423,9 +445,11 @@ int mars_graph_destroy(mars_graph* gh) {
 
 int mars_graph_set_csr(mars_graph* gh, int32_t ne, const int32_t* row, const int32_t* col) {
     MARS_CHECK(gh && ne >= 0, MARS_ERR_INVALID, "bad arguments");
+    std::lock_guard<std::mutex> lock(gh->mu);
     Graph& g = gh->g;
     MARS_TRY(validate_csr(g.n, ne, row, col));
     MARS_TRY(use_device(g.device));
+    MARS_HIP(hipStreamSynchronize(g.ins_stream));
     if (int64_t(ne) > g.cap_e) {
         int32_t* ncol = nullptr;
         MARS_TRY(dmalloc(&ncol, size_t(ne)));
@@ -433,15 +457,12 @@ int mars_graph_set_csr(mars_graph* gh, int32_t ne, const int32_t* row, const int
         g.col = ncol;
         g.cap_e = ne;
     }
-    if (row) MARS_HIP(hipMemcpy(g.row, row, (size_t(g.n) + 1) * sizeof(int32_t), hipMemcpyHostToDevice));
-    else MARS_HIP(hipMemset(g.row, 0, (size_t(g.n) + 1) * sizeof(int32_t)));
-    if (ne > 0) MARS_HIP(hipMemcpy(g.col, col, size_t(ne) * sizeof(int32_t), hipMemcpyHostToDevice));
-    g.e = ne;
-    return MARS_OK;
+    return load_csr(g, g.n, ne, row, col, hipMemcpyHostToDevice);
 }
 
 int mars_graph_set_episode_ids(mars_graph* gh, const int32_t* ids, int32_t n) {
     MARS_CHECK(gh, MARS_ERR_INVALID, "null graph");
+    std::lock_guard<std::mutex> lock(gh->mu);
     Graph& g = gh->g;
     MARS_TRY(use_device(g.device));
     dfree(g.ep_ids);                                      // memory_cuda.cu:814-826
@@ -455,6 +476,7 @@ int mars_graph_set_episode_ids(mars_graph* gh, const int32_t* ids, int32_t n) {
 int mars_graph_set_episode_csr(mars_graph* gh, int32_t num_eps, const int32_t* off, const int32_t* mem,
                                int32_t member_total) {
     MARS_CHECK(gh, MARS_ERR_INVALID, "null graph");
+    std::lock_guard<std::mutex> lock(gh->mu);
     Graph& g = gh->g;
     MARS_TRY(use_device(g.device));
     dfree(g.ep_off); dfree(g.ep_mem);                     // memory_cuda.cu:828-855
@@ -470,7 +492,8 @@ int mars_graph_set_episode_csr(mars_graph* gh, int32_t num_eps, const int32_t* o
     for (int32_t j = 0; j < member_total; ++j)
         MARS_CHECK(mem[j] >= 0 && mem[j] < g.n, MARS_ERR_INVALID, "episode member %d = %d out of range", j,
                    mem[j]);
-    MARS_TRY(dmalloc(&g.ep_off, size_t(num_eps) + 1));
+    // capacity for episodes appended by streaming inserts (at most one per node)
+    MARS_TRY(dmalloc(&g.ep_off, size_t(std::max(num_eps, g.cap_n)) + 1));
     MARS_TRY(dmalloc(&g.ep_mem, size_t(std::max(member_total, g.cap_n))));
     MARS_HIP(hipMemcpy(g.ep_off, off, (size_t(num_eps) + 1) * sizeof(int32_t), hipMemcpyHostToDevice));
     if (member_total > 0)
@@ -503,7 +526,7 @@ int mars_graph_get_view(const mars_graph* gh, mars_graph_view* v) {
     v->num_nodes = g.n; v->num_edges = g.e; v->embedding_dim = g.d;
     v->episode_num_episodes = g.num_eps; v->episode_csr_member_total = g.member_total;
     v->has_fp16 = g.emb16 ? 1 : 0;
-    v->d_row_offsets = g.row; v->d_col_indices = g.col; v->d_embeddings = g.emb;
+    v->d_row_words = g.ro; v->d_col_indices = g.col; v->d_embeddings = g.emb;
     v->d_embeddings_fp16 = g.emb16; v->d_modalities = g.mods; v->d_timestamps = g.ts;
     v->d_episode_ids = g.ep_ids; v->d_ep_csr_offsets = g.ep_off; v->d_ep_csr_members = g.ep_mem;
     return MARS_OK;
@@ -513,8 +536,21 @@ int mars_graph_download(const mars_graph* gh, int32_t* row, int32_t* col, int32_
     MARS_CHECK(gh, MARS_ERR_INVALID, "null graph");
     const Graph& g = gh->g;
     MARS_TRY(use_device(g.device));
-    if (row) MARS_HIP(hipMemcpy(row, g.row, (size_t(g.n) + 1) * sizeof(int32_t), hipMemcpyDeviceToHost));
-    if (col && g.e > 0) MARS_HIP(hipMemcpy(col, g.col, size_t(g.e) * sizeof(int32_t), hipMemcpyDeviceToHost));
+    if (row || col) {
+        // rows are (start, length) segments of col: rebuild the packed CSR
+        std::vector<int32_t> dcol(size_t(std::max<int64_t>(g.e_used, 1)));
+        if (g.e_used > 0)
+            MARS_HIP(hipMemcpy(dcol.data(), g.col, size_t(g.e_used) * sizeof(int32_t), hipMemcpyDeviceToHost));
+        int64_t pos = 0;
+        if (row) row[0] = 0;
+        for (int32_t i = 0; i < g.n; ++i) {
+            const int64_t w = g.ro_h[size_t(i)];
+            const int32_t b = int32_t(uint32_t(w)), len = int32_t(w >> 32);
+            if (col) std::memcpy(col + pos, dcol.data() + b, size_t(len) * sizeof(int32_t));
+            pos += len;
+            if (row) row[i + 1] = int32_t(pos);
+        }
+    }
     if (ep_off && g.ep_off)
         MARS_HIP(hipMemcpy(ep_off, g.ep_off, (size_t(g.num_eps) + 1) * sizeof(int32_t), hipMemcpyDeviceToHost));
     if (ep_mem && g.ep_mem && g.member_total > 0)

@@ -17,7 +17,9 @@
 
 #include <cstdint>
 #include <cstdio>
+#include <mutex>
 #include <string>
+#include <vector>
 
 #include "mars_amd.h"
 
@@ -66,7 +68,7 @@ __host__ __device__ inline int32_t key_id(uint64_t k) { return int32_t(uint32_t(
 // ---- device objects ---------------------------------------------------------------
 struct Graph {
     int device = 0;
-    int32_t n = 0;            // live nodes
+    int32_t n = 0;            // live nodes (published with __atomic_store_n; queries load it once)
     int32_t e = 0;            // live edges (col entries)
     int32_t d = 0;
     int32_t cap_n = 0;
@@ -75,13 +77,31 @@ struct Graph {
     __half* emb16 = nullptr;
     int32_t* mods = nullptr;
     float* ts = nullptr;
-    int32_t* row = nullptr;   // cap_n + 1
+    int64_t* ro = nullptr;    // cap_n: (row length << 32) | row start in col
+    int32_t* rcap = nullptr;  // cap_n: slots reserved for the row in col (>= length)
     int32_t* col = nullptr;   // cap_e
     int32_t* ep_ids = nullptr;
     int32_t* ep_off = nullptr;
     int32_t* ep_mem = nullptr;
     int32_t num_eps = 0;
     int32_t member_total = 0;
+    // host mirrors of the row words / capacities and the used part of col
+    std::vector<int64_t> ro_h;
+    std::vector<int32_t> rcap_h;
+    int64_t e_used = 0;
+    hipStream_t ins_stream = nullptr;    // side stream of streaming inserts
+    // insert scratch (grown on demand)
+    void* ins_pinned = nullptr;          // pinned staging of rows / patches
+    size_t ins_pinned_bytes = 0;
+    void* ins_dev = nullptr;             // device copy of patches
+    size_t ins_dev_bytes = 0;
+    uint64_t* ins_part = nullptr;        // batched-scan keys
+    uint64_t* ins_cand = nullptr;        // merged candidates
+    int32_t* ins_nbrs = nullptr;         // rescored neighbours
+    float* ins_tq = nullptr;             // zero query times (no decay)
+    __half* ins_qh = nullptr;            // unused slot kept for symmetry with the context
+    int32_t ins_cap_q = 0;
+    hipEvent_t ins_ev[4] = {nullptr, nullptr, nullptr, nullptr};
 };
 
 // Result staging written by the finalize / episode kernels straight into
@@ -112,7 +132,7 @@ struct Ctx {
     int32_t* vlist = nullptr;      // max_nodes visit order (node ids)
     int32_t* vhop = nullptr;       // max_nodes
     float* vscore = nullptr;       // max_nodes
-    int32_t* vro = nullptr;        // 2 * max_nodes: row offsets of each visited node
+    int64_t* vro = nullptr;        // max_nodes: row (len << 32 | start) of each visited node
     uint64_t* sortbuf = nullptr;   // max_nodes keys (large-result fallback)
     int32_t* seed_idx = nullptr;   // kMaxK
     uint64_t* stamps = nullptr;    // finalize phase stamps (100 MHz realtime counter)
@@ -147,6 +167,23 @@ struct Ctx {
     };
     GraphSlot g_global, g_episode;
 };
+
+// ---- streaming insert kernels (defined in stream.hip) --------------------------------
+struct PatchArgs {
+    int32_t* col;
+    int64_t* ro;
+    int32_t* rcap;
+    const int64_t* reloc;      // n_reloc x {src_start, len, dst_start}
+    int32_t n_reloc;
+    const int32_t* tail;       // values for col[tail_base ..); -1 marks a relocated slot
+    int64_t tail_base;
+    int32_t n_tail;
+    const int64_t* app;        // n_app x {offset, value}: appends inside existing row slack
+    int32_t n_app;
+    const int64_t* rows;       // n_rows x {node, row word, capacity}
+    int32_t n_rows;
+};
+int launch_patch(const PatchArgs& a, hipStream_t s);
 
 // ---- launch helpers (defined in kernels.hip) --------------------------------------
 struct ScanArgs {
@@ -188,8 +225,9 @@ struct FinalizeArgs {
     uint32_t* gcnt;          // their count; reset to 0 here for the next query
     uint64_t* gthr;          // scan's running bound; reset to kEmptyKey here
     int32_t k;
-    const int32_t* row;
+    const int64_t* ro;       // per node: (row length << 32) | row start in col
     const int32_t* col;
+    int32_t n_live;          // nodes this query sees; neighbours >= n_live are skipped
     const float* fin;
     const int32_t* mods;
     int32_t hops;
@@ -201,7 +239,7 @@ struct FinalizeArgs {
     int32_t* vlist;
     int32_t* vhop;
     float* vscore;
-    int32_t* vro;            // 2 per visit position: row_offsets[v], row_offsets[v+1]
+    int64_t* vro;            // per visit position: the node's (len << 32) | start
     uint64_t* sortbuf;
     int32_t cap_visit;
     int32_t rcap;            // results requested (max_results or K)
@@ -266,3 +304,9 @@ int launch_knn_rerank(const float* emb, int64_t q0, int64_t nq, int32_t d, const
 int launch_f32_to_f16_rows(const float* in, __half* out, int64_t count, hipStream_t s);
 
 }  // namespace mars
+
+struct mars_graph {
+    mars::Graph g;
+    std::mutex mu;      // serialises inserts / CSR and episode replacement
+};
+struct mars_ctx { mars::Ctx c; };

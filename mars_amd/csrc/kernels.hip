@@ -441,7 +441,7 @@ __device__ inline int hash_find(const FinShared& sh, int32_t v) {
 }
 
 // Degrees of frontier slots [c0, c0+cn) -> sh.u.bfs.eoff / rstart; returns the edge count.
-// CACHED: the row offsets of each visited node were stored in a.vro when it was
+// CACHED: the row word of each visited node was stored in a.vro when it was
 // visited (one dependent HBM load less per level).
 template <bool CACHED>
 __device__ inline int frontier_edges(FinShared& sh, const FinalizeArgs& a, int c0, int cn) {
@@ -452,15 +452,11 @@ __device__ inline int frontier_edges(FinShared& sh, const FinalizeArgs& a, int c
         const int i = tid * 4 + j;
         deg[j] = 0; rs[j] = 0;
         if (i < cn) {
-            if constexpr (CACHED) {
-                const int64_t ro = ld_coherent(reinterpret_cast<const int64_t*>(a.vro) + c0 + i);
-                rs[j] = int32_t(ro);
-                deg[j] = int32_t(ro >> 32) - rs[j];
-            } else {
-                const int32_t v = ld_coherent(a.vlist + c0 + i);
-                rs[j] = a.row[v];
-                deg[j] = a.row[v + 1] - rs[j];
-            }
+            int64_t ro;
+            if constexpr (CACHED) ro = ld_coherent(a.vro + c0 + i);
+            else ro = a.ro[ld_coherent(a.vlist + c0 + i)];
+            rs[j] = int32_t(uint32_t(ro));
+            deg[j] = int32_t(ro >> 32);
         }
         local += deg[j];
     }
@@ -521,12 +517,13 @@ __device__ int bfs_lds(FinShared& sh, const FinalizeArgs& a, int ns, int* levels
                 // claim: the smallest parent position wins; visited nodes keep their
                 // smaller (hop < 0xFF) value under the atomicMin. The edge, its slot
                 // and the two scores the emit needs stay in registers.
-                int32_t nb[R], pp[R], slot[R], rb[R], re[R];
+                int32_t nb[R], pp[R], slot[R];
+                int64_t rw[R];
                 float fv[R], ps[R];
 #pragma unroll
                 for (int r = 0; r < R; ++r) {
                     const int t = s0 + r * kFinThreads + tid;
-                    slot[r] = -1; nb[r] = 0; pp[r] = 0; fv[r] = 0.0f; ps[r] = 0.0f; rb[r] = 0; re[r] = 0;
+                    slot[r] = -1; nb[r] = -1; pp[r] = 0; fv[r] = 0.0f; ps[r] = 0.0f; rw[r] = 0;
                     if (t < T) {
                         const int p = owner_of(sh.u.bfs.eoff, cn, t);
                         pp[r] = c0 + p;
@@ -535,10 +532,9 @@ __device__ int bfs_lds(FinShared& sh, const FinalizeArgs& a, int ns, int* levels
                 }
 #pragma unroll
                 for (int r = 0; r < R; ++r) {
-                    if (s0 + r * kFinThreads + tid < T) {
+                    if (s0 + r * kFinThreads + tid < T && nb[r] < a.n_live) {
                         fv[r] = a.fin[nb[r]];
-                        rb[r] = a.row[nb[r]];
-                        re[r] = a.row[nb[r] + 1];
+                        rw[r] = a.ro[nb[r]];
                         ps[r] = ld_coherent(a.vscore + pp[r]);
                         slot[r] = hash_find_or_insert(sh, nb[r]);
                         if (slot[r] >= 0) atomicMin(&sh.u.bfs.hval[slot[r]], (kClaimHop << 16) | uint32_t(pp[r]));
@@ -560,7 +556,7 @@ __device__ int bfs_lds(FinShared& sh, const FinalizeArgs& a, int ns, int* levels
                         a.vlist[pos] = nb[r];
                         a.vhop[pos] = h + 1;
                         a.vscore[pos] = sc;
-                        reinterpret_cast<int64_t*>(a.vro)[pos] = (int64_t(re[r]) << 32) | uint32_t(rb[r]);
+                        a.vro[pos] = rw[r];
                         sh.u.bfs.hval[slot[r]] = (uint32_t(h + 1) << 16) | uint32_t(pos);
                     }
                     if (rk > 0) wave_offer(best, bthr, won ? make_key(sc, uint32_t(nb[r])) : kEmptyKey, lane_id(), rk);
@@ -596,7 +592,7 @@ __device__ int bfs_global(FinShared& sh, const FinalizeArgs& a, int ns, int* lev
             for (int t = tid; t < T; t += kFinThreads) {
                 const int p = owner_of(sh.u.bfs.eoff, cn, t);
                 const int32_t nb = a.col[sh.u.bfs.rstart[p] + (t - sh.u.bfs.eoff[p])];
-                if (ld_coherent(a.vis + nb) != a.epoch)
+                if (nb < a.n_live && ld_coherent(a.vis + nb) != a.epoch)
                     atomicMin(reinterpret_cast<unsigned long long*>(a.claim + nb),
                               (unsigned long long)(hi | uint32_t(c0 + p)));
             }
@@ -610,7 +606,7 @@ __device__ int bfs_global(FinShared& sh, const FinalizeArgs& a, int ns, int* lev
                 if (t < T) {
                     p = owner_of(sh.u.bfs.eoff, cn, t);
                     nb = a.col[sh.u.bfs.rstart[p] + (t - sh.u.bfs.eoff[p])];
-                    won = ld_coherent(a.claim + nb) == (hi | uint32_t(c0 + p));
+                    won = nb < a.n_live && ld_coherent(a.claim + nb) == (hi | uint32_t(c0 + p));
                 }
                 int rank = 0;
                 const int wtot = round_rank(sh, won, &rank);
@@ -782,7 +778,7 @@ __global__ __launch_bounds__(kFinThreads) void k_finalize(FinalizeArgs a) {
             a.vlist[lane] = id;
             a.vhop[lane] = 0;
             a.vscore[lane] = sc;
-            reinterpret_cast<int64_t*>(a.vro)[lane] = (int64_t(a.row[id + 1]) << 32) | uint32_t(a.row[id]);
+            a.vro[lane] = a.ro[id];
         }
         if (lane == 0) sh.s_misc[0] = ns;
     }

@@ -29,7 +29,8 @@ void refresh_view(DeviceMemoryGraph& d) {
     d.num_nodes = v.num_nodes;
     d.num_edges = v.num_edges;
     d.embedding_dim = v.embedding_dim;
-    d.d_row_offsets = static_cast<int32_t*>(v.d_row_offsets);
+    d.d_row_offsets = nullptr;                       // rows are (start, length) words: d_row_words
+    d.d_row_words = static_cast<int64_t*>(v.d_row_words);
     d.d_col_indices = static_cast<int32_t*>(v.d_col_indices);
     d.d_embeddings = static_cast<float*>(v.d_embeddings);
     d.d_embeddings_fp16 = v.d_embeddings_fp16;
