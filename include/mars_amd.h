@@ -107,7 +107,7 @@ typedef struct mars_graph_desc {
     const int32_t* modalities;       /* num_nodes                                     */
     const float*   timestamps;       /* num_nodes (seconds)                           */
     int32_t        capacity_nodes;   /* >= num_nodes; room for streaming append (0 = num_nodes) */
-    int64_t        capacity_edges;   /* >= num_edges (0 = num_edges + growth default)           */
+    int64_t        capacity_edges;   /* col slots for streaming append; 0 = num_edges + 256 per spare node */
     uint32_t       flags;
 } mars_graph_desc;
 
@@ -168,6 +168,36 @@ int mars_graph_knn(mars_graph* g, int32_t k, int32_t* nbrs);
  * a packed CSR (row_offsets: num_nodes + 1, col_indices: num_edges) and the episode CSR. */
 int mars_graph_download(const mars_graph* g, int32_t* row_offsets, int32_t* col_indices,
                         int32_t* ep_offsets, int32_t* ep_members);
+
+/* ---- streaming insert (streaming.cpp:35-163, engine_server.cu:154-213) ------- */
+typedef struct mars_insert_stats {
+    int32_t first_node;       /* id of the first inserted node (ids are consecutive)   */
+    int32_t nodes_added;
+    int64_t edges_added;      /* CSR entries added (each edge in both directions)      */
+    int32_t rows_relocated;   /* old rows moved to a tail region of col                */
+    int32_t rows_appended;    /* old rows extended in place                            */
+    double  queryable_us;     /* call -> nodes visible to scans and episode scope       */
+    double  linked_us;        /* call -> NSN edges visible to the BFS (call returns)    */
+    double  knn_us;           /* device time of the neighbour search                   */
+} mars_insert_stats;
+
+/* Append n_new nodes (host arrays: rows n_new * embedding_dim, modalities, timestamps)
+ * on the graph's side stream; queries on other threads / contexts keep running.
+ * Replaces StreamingBuffer::insert + flush (streaming.cpp:13-80) and its
+ * add_incremental_edges_ (:97-163), which rebuild the whole CSR on the host before a
+ * re-upload. Edge rule: intra-episode pairs among the new nodes plus each new node's
+ * knn_k nearest neighbours by cosine over all nodes (fp16 MFMA candidates, exact fp32
+ * order, ties by lower id), stored in both directions, rows ascending.
+ * episode_ids: required iff the graph has episode ids; each must open a new episode
+ * (>= every episode id already present); the episode CSR, when present, is appended.
+ * knn_k in [0, 16]; knn_k > 0 needs the fp16 copy. out_knn (nullable): n_new * knn_k
+ * neighbour ids found (-1: none). Nodes become visible to scans first (queryable_us),
+ * then their edges (linked_us); a query that runs meanwhile sees each row either as
+ * before or as after the insert. MARS_ERR_CAPACITY when capacity_nodes /
+ * capacity_edges (mars_graph_desc) cannot hold the insert: nothing is changed then. */
+int mars_graph_insert(mars_graph* g, int32_t n_new, const float* embeddings, const int32_t* modalities,
+                      const float* timestamps, const int32_t* episode_ids, int32_t knn_k,
+                      int32_t* out_knn, mars_insert_stats* stats);
 
 /* ---- query context (memory_cuda.cuh:141-231) --------------------------------- */
 #define MARS_CTX_USE_FP16    0x1u   /* scan the fp16 copy when present (ctx.use_fp16)      */

@@ -174,7 +174,13 @@ class DeviceMemoryGraph:
     def episode_csr_member_total(self) -> int:
         return self.view().episode_csr_member_total
 
+    def refresh(self) -> None:
+        """Node / edge counts as published (they grow under streaming inserts)."""
+        v = self.view()
+        self.num_nodes, self.num_edges = int(v.num_nodes), int(v.num_edges)
+
     def download_csr(self):
+        self.refresh()
         row = np.zeros(self.num_nodes + 1, np.int32)
         col = np.zeros(max(self.num_edges, 1), np.int32)
         check(lib.mars_graph_download(self.handle, _ptr(row), _ptr(col), None, None), "mars_graph_download")
@@ -355,6 +361,42 @@ def graph_knn(dg: DeviceMemoryGraph, k: int = 8) -> np.ndarray:
     out = np.empty((dg.num_nodes, k), np.int32)
     check(lib.mars_graph_knn(dg.handle, int(k), _ptr(out)), "mars_graph_knn")
     return out
+
+
+@dataclass
+class InsertStats:
+    first_node: int
+    nodes_added: int
+    edges_added: int
+    rows_relocated: int
+    rows_appended: int
+    queryable_us: float
+    linked_us: float
+    knn_us: float
+
+
+def insert_nodes(dg: DeviceMemoryGraph, embeddings, modalities, timestamps, episode_ids=None, knn_k: int = 8,
+                 return_knn: bool = False):
+    """Streaming insert (replaces StreamingBuffer::insert + flush, src/streaming.cpp:13-163):
+    appends the rows on the graph's side stream, links each new node to its episode's
+    new nodes and its knn_k nearest neighbours (both directions). Returns InsertStats
+    (and the (n_new, knn_k) neighbour ids when return_knn)."""
+    emb = _f32(embeddings).reshape(-1)
+    mods, ts = _i32(modalities), _f32(timestamps)
+    n_new = len(mods)
+    if len(ts) != n_new or emb.size != n_new * dg.embedding_dim:
+        raise ValueError("insert_nodes: rows / modalities / timestamps disagree in length")
+    ep = _i32(episode_ids) if episode_ids is not None else None
+    if ep is not None and len(ep) != n_new:
+        raise ValueError("insert_nodes: one episode id per new node")
+    knn = np.full((n_new, max(knn_k, 1)), -1, np.int32)
+    st = _lib.InsertStatsC()
+    check(lib.mars_graph_insert(dg.handle, n_new, _ptr(emb), _ptr(mods), _ptr(ts), _ptr(ep), int(knn_k),
+                                _ptr(knn) if knn_k > 0 else None, C.byref(st)), "mars_graph_insert")
+    dg.refresh()
+    out = InsertStats(st.first_node, st.nodes_added, st.edges_added, st.rows_relocated, st.rows_appended,
+                      st.queryable_us, st.linked_us, st.knn_us)
+    return (out, knn[:, :knn_k]) if return_knn else out
 
 
 class DeviceBuffer:

@@ -103,6 +103,19 @@ class GraphViewC(C.Structure):
     ]
 
 
+class InsertStatsC(C.Structure):
+    _fields_ = [
+        ("first_node", C.c_int32),
+        ("nodes_added", C.c_int32),
+        ("edges_added", C.c_int64),
+        ("rows_relocated", C.c_int32),
+        ("rows_appended", C.c_int32),
+        ("queryable_us", C.c_double),
+        ("linked_us", C.c_double),
+        ("knn_us", C.c_double),
+    ]
+
+
 class CorpusParamsC(C.Structure):
     _fields_ = [
         ("num_nodes", C.c_int64),
@@ -147,6 +160,7 @@ SIGNATURES = {
     "mars_query_batch": (C.c_int, [VP, VP, VP, I32, VP, C.POINTER(RetrievalConfigC), VP, VP, C.POINTER(StatsC)]),
     "mars_graph_knn": (C.c_int, [VP, I32, VP]),
     "mars_graph_set_csr": (C.c_int, [VP, I32, VP, VP]),
+    "mars_graph_insert": (C.c_int, [VP, I32, VP, VP, VP, VP, I32, VP, C.POINTER(InsertStatsC)]),
     "mars_ctx_last_seeds": (C.c_int, [VP, VP, VP, I32, PI32]),
     "mars_ctx_last_visited": (C.c_int, [VP, VP, VP, VP, I32, PI32]),
     "mars_ctx_last_phases": (C.c_int, [VP, VP, I32]),

@@ -37,35 +37,6 @@ int ensure_device(int* dev) {
     return MARS_OK;
 }
 
-int use_device(int dev) {
-    int cur = -1;
-    MARS_HIP(hipGetDevice(&cur));
-    if (cur != dev) MARS_HIP(hipSetDevice(dev));
-    return MARS_OK;
-}
-
-template <typename T>
-int dmalloc(T** p, size_t count) {
-    *p = nullptr;
-    if (count == 0) count = 1;
-    hipError_t e = hipMalloc(reinterpret_cast<void**>(p), count * sizeof(T));
-    if (e != hipSuccess)
-        return set_error(MARS_ERR_NOMEM, "hipMalloc(%zu bytes): %s", count * sizeof(T), hipGetErrorString(e));
-    return MARS_OK;
-}
-
-template <typename T>
-void dfree(T*& p) {
-    if (p) (void)hipFree(p);
-    p = nullptr;
-}
-
-#define MARS_TRY(expr)                  \
-    do {                                \
-        int rc__ = (expr);              \
-        if (rc__ != MARS_OK) return rc__; \
-    } while (0)
-
 // CSR checks done on host input: offsets start at 0, non-decreasing, end at E;
 // neighbour ids in range; no id twice in one row (the BFS claim relies on it).
 int validate_csr(int32_t n, int32_t e, const int32_t* row, const int32_t* col) {
@@ -96,10 +67,12 @@ int validate_csr(int32_t n, int32_t e, const int32_t* row, const int32_t* col) {
 
 bool episode_scoped_active(const Graph& g, const mars_retrieval_config& c) {
     // memory_cuda.cu:1163-1171
+    // (episode count and member total grow under streaming inserts: read once each)
     return c.retrieval_scope == MARS_SCOPE_EPISODE_SCOPED && g.ep_off != nullptr && g.ep_mem != nullptr &&
-           c.query_episode_id >= 0 && c.query_episode_id < g.num_eps && c.query_episode_member_count > 0 &&
-           c.query_episode_member_begin >= 0 &&
-           int64_t(c.query_episode_member_begin) + c.query_episode_member_count <= g.member_total;
+           c.query_episode_id >= 0 && c.query_episode_id < __atomic_load_n(&g.num_eps, __ATOMIC_ACQUIRE) &&
+           c.query_episode_member_count > 0 && c.query_episode_member_begin >= 0 &&
+           int64_t(c.query_episode_member_begin) + c.query_episode_member_count <=
+               __atomic_load_n(&g.member_total, __ATOMIC_ACQUIRE);
 }
 
 }  // namespace
@@ -119,6 +92,7 @@ int graph_free(Graph& g) {
     if (g.ins_stream) (void)hipStreamSynchronize(g.ins_stream);
     dfree(g.emb); dfree(g.emb16); dfree(g.mods); dfree(g.ts); dfree(g.ro); dfree(g.rcap); dfree(g.col);
     dfree(g.ep_ids); dfree(g.ep_off); dfree(g.ep_mem);
+    graph_insert_free(g);
     if (g.ins_stream) (void)hipStreamDestroy(g.ins_stream);
     g = Graph{};
     return MARS_OK;
@@ -135,10 +109,12 @@ int load_csr(Graph& g, int32_t n, int32_t e, const int32_t* row, const int32_t* 
         MARS_HIP(hipMemcpy(hrow.data(), row, hrow.size() * sizeof(int32_t), hipMemcpyDeviceToHost));
         r = hrow.data();
     }
+    g.max_deg = 0;
     for (int32_t i = 0; i < n; ++i) {
         const int32_t b = r ? r[i] : 0, len = r ? r[i + 1] - r[i] : 0;
         g.ro_h[size_t(i)] = (int64_t(len) << 32) | uint32_t(b);
         g.rcap_h[size_t(i)] = len;
+        g.max_deg = std::max(g.max_deg, len);
     }
     MARS_HIP(hipMemcpy(g.ro, g.ro_h.data(), size_t(g.cap_n) * sizeof(int64_t), hipMemcpyHostToDevice));
     MARS_HIP(hipMemcpy(g.rcap, g.rcap_h.data(), size_t(g.cap_n) * sizeof(int32_t), hipMemcpyHostToDevice));
@@ -212,12 +188,13 @@ int query_impl(const mars_graph* gh, mars_ctx* ch, const float* h_q, const float
     const Graph& g = gh->g;
     Ctx& c = ch->c;
     MARS_CHECK(g.d == c.d, MARS_ERR_INVALID, "graph dim %d != context dim %d", g.d, c.d);
-    MARS_CHECK(__atomic_load_n(&g.n, __ATOMIC_ACQUIRE) <= c.max_nodes, MARS_ERR_CAPACITY,
-               "graph has %d nodes, context sized for %d", g.n, c.max_nodes);
-    MARS_CHECK(g.n > 0, MARS_ERR_INVALID, "empty graph");
+    // nodes published so far: loaded once, every kernel of this query is bounded by it
+    const int32_t n_live = __atomic_load_n(&g.n, __ATOMIC_ACQUIRE);
+    MARS_CHECK(n_live <= c.max_nodes, MARS_ERR_CAPACITY, "graph has %d nodes, context sized for %d", n_live,
+               c.max_nodes);
+    MARS_CHECK(n_live > 0, MARS_ERR_INVALID, "empty graph");
     MARS_CHECK(cfg->top_k > 0, MARS_ERR_INVALID, "top_k = %d", cfg->top_k);
     const int32_t K = std::min(cfg->top_k, c.max_k);                      // memory_cuda.cu:1361
-    const int32_t n_live = __atomic_load_n(&g.n, __ATOMIC_ACQUIRE);       // nodes published so far
     const bool scoped = episode_scoped_active(g, *cfg);
     const int32_t hops = scoped ? 0 : std::max(0, cfg->bfs_max_hops);     // :1189
     const int32_t rcap = cfg->max_results_returned > 0 ? cfg->max_results_returned : K;
@@ -334,6 +311,8 @@ int query_impl(const mars_graph* gh, mars_ctx* ch, const float* h_q, const float
     return MARS_OK;
 }
 
+}  // namespace
+
 // Row ranges x query blocks for the batched scan: one 512-thread workgroup per CU
 // (256 CUs), all query blocks of a row range on one XCD.
 void batch_grid(int64_t n, int32_t q, int32_t* n_rranges, int32_t* n_qblocks, int64_t* rows_per_range) {
@@ -346,6 +325,8 @@ void batch_grid(int64_t n, int32_t q, int32_t* n_rranges, int32_t* n_qblocks, in
     *rows_per_range = ((n + rr - 1) / rr + 15) / 16 * 16;
     *n_rranges = int32_t((n + *rows_per_range - 1) / *rows_per_range);
 }
+
+namespace {
 
 int ensure_batch_scratch(Ctx& c, int32_t q, int64_t part_keys) {
     if (q > c.bcap_q) {
@@ -417,7 +398,11 @@ int mars_graph_create(const mars_graph_desc* d, mars_graph** out) {
     g.device = devid;
     g.n = d->num_nodes; g.e = d->num_edges; g.d = d->embedding_dim;
     g.cap_n = std::max(d->capacity_nodes, d->num_nodes);
-    g.cap_e = std::max<int64_t>(d->capacity_edges, d->num_edges);
+    // default edge room for streaming inserts: 256 col slots per node of spare capacity
+    // (a new row, and the old rows it links to when they move to the tail)
+    const int64_t grow = int64_t(g.cap_n - g.n) * 256 + (g.cap_n > g.n ? 4096 : 0);
+    g.cap_e = d->capacity_edges > 0 ? std::max<int64_t>(d->capacity_edges, d->num_edges)
+                                    : int64_t(d->num_edges) + grow;
     const size_t N = size_t(g.n), D = size_t(g.d), CN = size_t(g.cap_n);
     int rc = MARS_OK;
     auto fail = [&](int r) { graph_free(g); delete gh; return r; };
@@ -466,10 +451,13 @@ int mars_graph_set_episode_ids(mars_graph* gh, const int32_t* ids, int32_t n) {
     Graph& g = gh->g;
     MARS_TRY(use_device(g.device));
     dfree(g.ep_ids);                                      // memory_cuda.cu:814-826
+    g.ep_next = g.num_eps;
     if (!ids || n <= 0) return MARS_OK;                   // cleared
     MARS_CHECK(n == g.n, MARS_ERR_INVALID, "episode ids: %d entries for %d nodes", n, g.n);
     MARS_TRY(dmalloc(&g.ep_ids, size_t(g.cap_n)));
     MARS_HIP(hipMemcpy(g.ep_ids, ids, size_t(n) * sizeof(int32_t), hipMemcpyHostToDevice));
+    for (int32_t i = 0; i < n; ++i)
+        if (ids[i] >= g.ep_next) g.ep_next = ids[i] == INT32_MAX ? INT32_MAX : ids[i] + 1;
     return MARS_OK;
 }
 
@@ -482,6 +470,7 @@ int mars_graph_set_episode_csr(mars_graph* gh, int32_t num_eps, const int32_t* o
     dfree(g.ep_off); dfree(g.ep_mem);                     // memory_cuda.cu:828-855
     g.num_eps = 0;
     g.member_total = 0;
+    g.ep_off_cap = g.ep_mem_cap = 0;
     if (num_eps <= 0) return MARS_OK;
     MARS_CHECK(off && (member_total == 0 || mem), MARS_ERR_INVALID, "episode CSR arrays missing");
     MARS_CHECK(off[num_eps] == member_total && member_total >= 0, MARS_ERR_INVALID,
@@ -493,18 +482,22 @@ int mars_graph_set_episode_csr(mars_graph* gh, int32_t num_eps, const int32_t* o
         MARS_CHECK(mem[j] >= 0 && mem[j] < g.n, MARS_ERR_INVALID, "episode member %d = %d out of range", j,
                    mem[j]);
     // capacity for episodes appended by streaming inserts (at most one per node)
-    MARS_TRY(dmalloc(&g.ep_off, size_t(std::max(num_eps, g.cap_n)) + 1));
-    MARS_TRY(dmalloc(&g.ep_mem, size_t(std::max(member_total, g.cap_n))));
+    g.ep_off_cap = int64_t(std::max(num_eps, g.cap_n)) + 1;
+    g.ep_mem_cap = int64_t(std::max(member_total, g.cap_n));
+    MARS_TRY(dmalloc(&g.ep_off, size_t(g.ep_off_cap)));
+    MARS_TRY(dmalloc(&g.ep_mem, size_t(g.ep_mem_cap)));
     MARS_HIP(hipMemcpy(g.ep_off, off, (size_t(num_eps) + 1) * sizeof(int32_t), hipMemcpyHostToDevice));
     if (member_total > 0)
         MARS_HIP(hipMemcpy(g.ep_mem, mem, size_t(member_total) * sizeof(int32_t), hipMemcpyHostToDevice));
     g.num_eps = num_eps;
     g.member_total = member_total;
+    g.ep_next = std::max(g.ep_next, num_eps);
     return MARS_OK;
 }
 
 int mars_graph_enable_fp16(mars_graph* gh) {
     MARS_CHECK(gh, MARS_ERR_INVALID, "null graph");
+    std::lock_guard<std::mutex> lock(gh->mu);
     Graph& g = gh->g;
     MARS_TRY(use_device(g.device));
     if (!g.emb16) MARS_TRY(dmalloc(&g.emb16, size_t(g.cap_n) * size_t(g.d)));
@@ -515,6 +508,7 @@ int mars_graph_enable_fp16(mars_graph* gh) {
 
 int mars_graph_disable_fp16(mars_graph* gh) {
     MARS_CHECK(gh, MARS_ERR_INVALID, "null graph");
+    std::lock_guard<std::mutex> lock(gh->mu);
     MARS_TRY(use_device(gh->g.device));
     dfree(gh->g.emb16);
     return MARS_OK;
@@ -522,6 +516,7 @@ int mars_graph_disable_fp16(mars_graph* gh) {
 
 int mars_graph_get_view(const mars_graph* gh, mars_graph_view* v) {
     MARS_CHECK(gh && v, MARS_ERR_INVALID, "null argument");
+    std::lock_guard<std::mutex> lock(gh->mu);
     const Graph& g = gh->g;
     v->num_nodes = g.n; v->num_edges = g.e; v->embedding_dim = g.d;
     v->episode_num_episodes = g.num_eps; v->episode_csr_member_total = g.member_total;
@@ -534,6 +529,7 @@ int mars_graph_get_view(const mars_graph* gh, mars_graph_view* v) {
 
 int mars_graph_download(const mars_graph* gh, int32_t* row, int32_t* col, int32_t* ep_off, int32_t* ep_mem) {
     MARS_CHECK(gh, MARS_ERR_INVALID, "null graph");
+    std::lock_guard<std::mutex> lock(gh->mu);
     const Graph& g = gh->g;
     MARS_TRY(use_device(g.device));
     if (row || col) {
@@ -709,9 +705,10 @@ int mars_query_batch(const mars_graph* gh, mars_ctx* ch, const float* dq, int32_
                cfg->top_k);
     MARS_TRY(use_device(c.device));
     const int32_t K = cfg->top_k;
+    const int32_t n_live = __atomic_load_n(&g.n, __ATOMIC_ACQUIRE);
     int32_t nrr = 0, nqb = 0;
     int64_t rpr = 0;
-    batch_grid(g.n, Q, &nrr, &nqb, &rpr);
+    batch_grid(n_live, Q, &nrr, &nqb, &rpr);
     const int32_t kp = batch_kpart(K);
     MARS_TRY(ensure_batch_scratch(c, Q, int64_t(nqb) * nrr * 64 * kp));
     hipStream_t s = c.stream;
@@ -720,7 +717,7 @@ int mars_query_batch(const mars_graph* gh, mars_ctx* ch, const float* dq, int32_
     const bool timing = (c.flags & MARS_CTX_TIMING) != 0;
     if (timing) MARS_HIP(hipEventRecord(c.ev[0], s));
     BatchArgs a{};
-    a.emb16 = g.emb16; a.n = g.n; a.d = g.d; a.qh = c.bq; a.q = Q; a.tq = c.btq; a.ts = g.ts; a.mods = g.mods;
+    a.emb16 = g.emb16; a.n = n_live; a.d = g.d; a.qh = c.bq; a.q = Q; a.tq = c.btq; a.ts = g.ts; a.mods = g.mods;
     a.lambda = cfg->time_decay_lambda; a.mod_filter = cfg->modality_filter; a.k = K; a.self_base = -1;
     a.part = c.bpart; a.rows_per_range = rpr; a.n_rranges = nrr; a.n_qblocks = nqb;
     MARS_TRY(launch_batch_scan(a, s));
@@ -745,7 +742,7 @@ int mars_query_batch(const mars_graph* gh, mars_ctx* ch, const float* dq, int32_
             MARS_HIP(hipEventElapsedTime(&ms, c.ev[0], c.ev[2]));
             st.gpu_ms_total = ms;
         }
-        st.nodes_scanned = g.n;
+        st.nodes_scanned = n_live;
         st.used_fp16 = 1;
         st.wall_us = std::chrono::duration<double, std::micro>(std::chrono::steady_clock::now() - t0).count();
         *stats = st;
@@ -755,6 +752,7 @@ int mars_query_batch(const mars_graph* gh, mars_ctx* ch, const float* dq, int32_
 
 int mars_graph_knn(mars_graph* gh, int32_t k, int32_t* nbrs) {
     MARS_CHECK(gh && nbrs && k >= 1 && k <= 16, MARS_ERR_INVALID, "k-NN: bad arguments (k=%d)", k);
+    std::lock_guard<std::mutex> lock(gh->mu);
     Graph& g = gh->g;
     MARS_CHECK(g.emb16 != nullptr, MARS_ERR_UNSUPPORTED, "k-NN reads the fp16 corpus: enable it first");
     MARS_CHECK(batch_dim_supported(g.d), MARS_ERR_UNSUPPORTED, "k-NN: embedding_dim %d unsupported", g.d);

@@ -39,6 +39,38 @@ int set_error(int code, const char* fmt, ...);
         if (!(cond)) return ::mars::set_error((code), __VA_ARGS__);                  \
     } while (0)
 
+#define MARS_TRY(expr)                    \
+    do {                                  \
+        int rc__ = (expr);                \
+        if (rc__ != MARS_OK) return rc__; \
+    } while (0)
+
+inline int use_device(int dev) {
+    int cur = -1;
+    MARS_HIP(hipGetDevice(&cur));
+    if (cur != dev) MARS_HIP(hipSetDevice(dev));
+    return MARS_OK;
+}
+
+template <typename T>
+int dmalloc(T** p, size_t count) {
+    *p = nullptr;
+    if (count == 0) count = 1;
+    hipError_t e = hipMalloc(reinterpret_cast<void**>(p), count * sizeof(T));
+    if (e != hipSuccess)
+        return set_error(MARS_ERR_NOMEM, "hipMalloc(%zu bytes): %s", count * sizeof(T), hipGetErrorString(e));
+    return MARS_OK;
+}
+
+template <typename T>
+void dfree(T*& p) {
+    if (p) (void)hipFree(p);
+    p = nullptr;
+}
+
+// Row ranges x query blocks of the batched scan (defined in api.hip).
+void batch_grid(int64_t n, int32_t q, int32_t* n_rranges, int32_t* n_qblocks, int64_t* rows_per_range);
+
 constexpr int kMaxK = 64;              // seeds per query (wave-held list), as MAX_TOP_K
 constexpr int kSortCap = 8192;         // results sorted in LDS by the finalize kernel
 constexpr int kFrontierChunk = 4096;   // frontier nodes per BFS chunk (LDS)
@@ -89,19 +121,23 @@ struct Graph {
     std::vector<int64_t> ro_h;
     std::vector<int32_t> rcap_h;
     int64_t e_used = 0;
-    hipStream_t ins_stream = nullptr;    // side stream of streaming inserts
-    // insert scratch (grown on demand)
-    void* ins_pinned = nullptr;          // pinned staging of rows / patches
-    size_t ins_pinned_bytes = 0;
-    void* ins_dev = nullptr;             // device copy of patches
+    int32_t max_deg = 0;                 // longest row
+    // streaming inserts (under the graph mutex)
+    hipStream_t ins_stream = nullptr;    // side stream
+    int32_t ep_next = 0;                 // smallest episode id an insert may open
+    int64_t ep_off_cap = 0;              // entries allocated in ep_off / ep_mem
+    int64_t ep_mem_cap = 0;
+    void* ins_pin = nullptr;             // pinned staging of rows and row patches
+    size_t ins_pin_bytes = 0;
+    void* ins_dev = nullptr;             // device copy of the row patches
     size_t ins_dev_bytes = 0;
-    uint64_t* ins_part = nullptr;        // batched-scan keys
-    uint64_t* ins_cand = nullptr;        // merged candidates
+    uint64_t* ins_part = nullptr;        // batched-scan keys of the neighbour search
+    int64_t ins_part_cap = 0;
+    uint64_t* ins_cand = nullptr;        // merged candidates (1024 x 16)
     int32_t* ins_nbrs = nullptr;         // rescored neighbours
     float* ins_tq = nullptr;             // zero query times (no decay)
-    __half* ins_qh = nullptr;            // unused slot kept for symmetry with the context
     int32_t ins_cap_q = 0;
-    hipEvent_t ins_ev[4] = {nullptr, nullptr, nullptr, nullptr};
+    hipEvent_t ins_ev[2] = {nullptr, nullptr};
 };
 
 // Result staging written by the finalize / episode kernels straight into
@@ -175,15 +211,15 @@ struct PatchArgs {
     int32_t* rcap;
     const int64_t* reloc;      // n_reloc x {src_start, len, dst_start}
     int32_t n_reloc;
-    const int32_t* tail;       // values for col[tail_base ..); -1 marks a relocated slot
+    const int32_t* tail;       // values for col[tail_base ..); INT32_MIN: filled by a relocation
     int64_t tail_base;
-    int32_t n_tail;
+    int64_t n_tail;
     const int64_t* app;        // n_app x {offset, value}: appends inside existing row slack
     int32_t n_app;
     const int64_t* rows;       // n_rows x {node, row word, capacity}
     int32_t n_rows;
 };
-int launch_patch(const PatchArgs& a, hipStream_t s);
+int graph_insert_free(Graph& g);     // insert scratch of a graph
 
 // ---- launch helpers (defined in kernels.hip) --------------------------------------
 struct ScanArgs {
@@ -307,6 +343,6 @@ int launch_f32_to_f16_rows(const float* in, __half* out, int64_t count, hipStrea
 
 struct mars_graph {
     mars::Graph g;
-    std::mutex mu;      // serialises inserts / CSR and episode replacement
+    mutable std::mutex mu;   // serialises inserts, CSR / episode / fp16 replacement and downloads
 };
 struct mars_ctx { mars::Ctx c; };

@@ -532,7 +532,7 @@ __device__ int bfs_lds(FinShared& sh, const FinalizeArgs& a, int ns, int* levels
                 }
 #pragma unroll
                 for (int r = 0; r < R; ++r) {
-                    if (s0 + r * kFinThreads + tid < T && nb[r] < a.n_live) {
+                    if (s0 + r * kFinThreads + tid < T && uint32_t(nb[r]) < uint32_t(a.n_live)) {
                         fv[r] = a.fin[nb[r]];
                         rw[r] = a.ro[nb[r]];
                         ps[r] = ld_coherent(a.vscore + pp[r]);
@@ -592,7 +592,7 @@ __device__ int bfs_global(FinShared& sh, const FinalizeArgs& a, int ns, int* lev
             for (int t = tid; t < T; t += kFinThreads) {
                 const int p = owner_of(sh.u.bfs.eoff, cn, t);
                 const int32_t nb = a.col[sh.u.bfs.rstart[p] + (t - sh.u.bfs.eoff[p])];
-                if (nb < a.n_live && ld_coherent(a.vis + nb) != a.epoch)
+                if (uint32_t(nb) < uint32_t(a.n_live) && ld_coherent(a.vis + nb) != a.epoch)
                     atomicMin(reinterpret_cast<unsigned long long*>(a.claim + nb),
                               (unsigned long long)(hi | uint32_t(c0 + p)));
             }
@@ -606,7 +606,7 @@ __device__ int bfs_global(FinShared& sh, const FinalizeArgs& a, int ns, int* lev
                 if (t < T) {
                     p = owner_of(sh.u.bfs.eoff, cn, t);
                     nb = a.col[sh.u.bfs.rstart[p] + (t - sh.u.bfs.eoff[p])];
-                    won = nb < a.n_live && ld_coherent(a.claim + nb) == (hi | uint32_t(c0 + p));
+                    won = uint32_t(nb) < uint32_t(a.n_live) && ld_coherent(a.claim + nb) == (hi | uint32_t(c0 + p));
                 }
                 int rank = 0;
                 const int wtot = round_rank(sh, won, &rank);

@@ -63,6 +63,8 @@ def _load():
         "oracle_query": (I32, [C.POINTER(OracleGraph), VP, C.c_float, C.POINTER(OracleConfig), I32, VP, I32,
                                VP, VP, VP, VP, I32, VP]),
         "oracle_tiled_query": (I32, [C.POINTER(OracleGraph), VP, C.c_float, C.c_float, I32, I32, I32, VP, VP]),
+        "oracle_knn": (None, [VP, I64, I32, VP, I32, I32, VP, VP]),
+        "oracle_insert_edges": (I64, [I32, VP, VP, I32, VP, VP, I32, VP, VP]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -226,3 +228,29 @@ def tiled_query(g: Graph, q, t_q: float, lam: float, k: int, tile: int, mod_filt
     gc = g.c()
     m = lib.oracle_tiled_query(C.byref(gc), _p(q), t_q, lam, mod_filter, k, tile, _p(ids), _p(sc))
     return ids[:m], sc[:m]
+
+
+def knn(emb, qids, k: int, n: Optional[int] = None):
+    """k nearest neighbours (fp64 cosine, ties: lower id) of nodes qids among rows [0, n)."""
+    emb = np.ascontiguousarray(emb, np.float32)
+    n = emb.shape[0] if n is None else int(n)
+    qids = np.ascontiguousarray(qids, np.int32)
+    ids = np.empty((len(qids), k), np.int32)
+    sims = np.empty((len(qids), k), np.float64)
+    lib.oracle_knn(_p(emb), n, emb.shape[1], _p(qids), len(qids), k, _p(ids), _p(sims))
+    return ids, sims
+
+
+def insert_edges(row, col, n_old: int, n_new: int, ep_new, knn_ids):
+    """CSR after a streaming insert of n_new nodes (episode pairs + given k-NN, both directions)."""
+    row = None if row is None else np.ascontiguousarray(row, np.int32)
+    col = None if col is None else np.ascontiguousarray(col, np.int32)
+    ep = None if ep_new is None else np.ascontiguousarray(ep_new, np.int32)
+    kn = np.ascontiguousarray(knn_ids, np.int32)
+    k = kn.size // n_new if n_new else 0
+    kn = kn.reshape(n_new, k) if k else np.full((1, 1), -1, np.int32)
+    out_row = np.empty(n_old + n_new + 1, np.int32)
+    e = lib.oracle_insert_edges(n_old, _p(row), _p(col), n_new, _p(ep), _p(kn), k, _p(out_row), None)
+    out_col = np.empty(max(e, 1), np.int32)
+    lib.oracle_insert_edges(n_old, _p(row), _p(col), n_new, _p(ep), _p(kn), k, _p(out_row), _p(out_col))
+    return out_row, out_col[:e]

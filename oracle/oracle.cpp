@@ -35,6 +35,7 @@
 #include <cstdint>
 #include <cstring>
 #include <numeric>
+#include <set>
 #include <vector>
 
 #ifdef _OPENMP
@@ -440,4 +441,81 @@ int32_t oracle_tiled_query(const oracle_graph* g, const float* q, float t_q, flo
     return n;
 }
 
+// ---------------------------------------------------------------------------
+// k nearest neighbours by cosine: fp64 dot of the fp32 rows (unit rows, so the
+// dot is the cosine) of each node in qids against rows [0, n), the node itself
+// excluded, order (similarity desc, id asc). The k-NN half of the benchmark's
+// NSN rule ("intra-episode pairs + 8 nearest neighbours"); the reference's own
+// neighbour search is the tiled brute force of cmng_build.cu:135-245.
+// Fewer than k candidates: the rest of the row is -1 / -inf.
+// ---------------------------------------------------------------------------
+void oracle_knn(const float* emb, int64_t n, int32_t d, const int32_t* qids, int32_t nq, int32_t k,
+                int32_t* out, double* sims) {
+#pragma omp parallel for schedule(dynamic, 4)
+    for (int32_t i = 0; i < nq; ++i) {
+        const int64_t u = qids[i];
+        const float* x = emb + u * d;
+        std::vector<std::pair<double, int64_t>> best;      // (-sim, id), kept sorted, <= k
+        best.reserve(size_t(k) + 1);
+        for (int64_t v = 0; v < n; ++v) {
+            if (v == u) continue;
+            const float* y = emb + v * d;
+            double acc = 0.0;
+            for (int32_t j = 0; j < d; ++j) acc += double(x[j]) * double(y[j]);
+            const std::pair<double, int64_t> key(-acc, v);
+            if (int32_t(best.size()) == k && !(key < best.back())) continue;
+            best.insert(std::upper_bound(best.begin(), best.end(), key), key);
+            if (int32_t(best.size()) > k) best.pop_back();
+        }
+        for (int32_t j = 0; j < k; ++j) {
+            const bool ok = j < int32_t(best.size());
+            out[int64_t(i) * k + j] = ok ? int32_t(best[size_t(j)].second) : -1;
+            if (sims) sims[int64_t(i) * k + j] = ok ? -best[size_t(j)].first : -HUGE_VAL;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Streaming insert edge rule. The reference's flush keeps every old edge, adds
+// edges for the new nodes to both endpoints through a std::set adjacency and
+// re-packs the CSR with rows ascending (streaming.cpp:35-80, 97-104, 155-162);
+// which edges it adds (ring lattice by id + sampled cross-modal bridges,
+// :111-153) is replaced by the benchmark's NSN rule: for each new node u
+// (ids n_old .. n_old + n_new - 1) every other new node with the same episode
+// id (ep_new may be NULL: no episode edges) and its k neighbours knn[u] (ids
+// < 0 skipped). out_row: n_old + n_new + 1 entries. Returns the edge count;
+// call with out_col == NULL to size it.
+// ---------------------------------------------------------------------------
+int64_t oracle_insert_edges(int32_t n_old, const int32_t* row, const int32_t* col, int32_t n_new,
+                            const int32_t* ep_new, const int32_t* knn, int32_t k, int32_t* out_row,
+                            int32_t* out_col) {
+    const int32_t n = n_old + n_new;
+    std::vector<std::set<int32_t>> adj(static_cast<size_t>(n));
+    for (int32_t i = 0; i < n_old; ++i)
+        if (row)
+            for (int32_t j = row[i]; j < row[i + 1]; ++j) adj[size_t(i)].insert(col[j]);
+    auto link = [&](int32_t a, int32_t b) {
+        if (a == b || b < 0 || b >= n) return;
+        adj[size_t(a)].insert(b);
+        adj[size_t(b)].insert(a);
+    };
+    for (int32_t i = 0; i < n_new; ++i) {
+        if (ep_new)
+            for (int32_t j = 0; j < n_new; ++j)
+                if (j != i && ep_new[j] == ep_new[i]) link(n_old + i, n_old + j);
+        for (int32_t j = 0; j < k; ++j) link(n_old + i, knn[int64_t(i) * k + j]);
+    }
+    int64_t e = 0;
+    if (out_row) out_row[0] = 0;
+    for (int32_t i = 0; i < n; ++i) {
+        for (int32_t v : adj[size_t(i)]) {
+            if (out_col) out_col[e] = v;
+            ++e;
+        }
+        if (out_row) out_row[i + 1] = int32_t(e);
+    }
+    return e;
+}
+
 }  // extern "C"
+

@@ -297,3 +297,122 @@ def test_reference_kids_corpus_episode_hit(golden):
         r = oracle.query(g, z["emb"][node], float(z["ts"][node]), cfg)
         mods = {x[2] for x in r["results"] if z["ep"][x[0]] == ep}
         assert {0, 1} <= mods
+
+
+# ---------------------------------------------------------------- k-NN
+def test_knn_matches_numpy_lexsort(rng):
+    n, d, k = 300, 32, 8
+    emb = rng.standard_normal((n, d)).astype(np.float32)
+    emb /= np.linalg.norm(emb, axis=1, keepdims=True)
+    emb[50] = emb[10]                     # exact ties: equal similarity, lower id first
+    emb[51] = emb[10]
+    qids = np.array([0, 10, 50, 51, 299, 7], np.int32)
+    ids, sims = oracle.knn(emb, qids, k)
+    e64 = emb.astype(np.float64)
+    for row, u in enumerate(qids):
+        s = e64 @ e64[u]
+        s[u] = -np.inf
+        order = np.lexsort((np.arange(n), -s))[:k]
+        np.testing.assert_array_equal(ids[row], order, err_msg=f"node {u}")
+        np.testing.assert_allclose(sims[row], s[order], rtol=0, atol=1e-12)
+    # node 50's two nearest are its exact copies 10 and 51 (sim 1), lower id first
+    assert list(ids[2][:2]) == [10, 51]
+
+
+def test_knn_restricted_prefix_and_short_rows(rng):
+    emb = rng.standard_normal((40, 16)).astype(np.float32)
+    ids, sims = oracle.knn(emb, np.array([3, 4], np.int32), 8, n=5)   # only rows 0..4 exist
+    assert set(ids[0][:4]) == {0, 1, 2, 4} and list(ids[0][4:]) == [-1] * 4
+    assert np.all(np.isneginf(sims[0][4:]))
+    assert 4 not in ids[1] and ids[1][4] == -1
+
+
+# ---------------------------------------------------------------- streaming insert edges
+def _sets_insert(row, col, n_old, n_new, ep, knn):
+    adj = [set(col[row[i]:row[i + 1]]) if row is not None else set() for i in range(n_old)]
+    adj += [set() for _ in range(n_new)]
+    for i in range(n_new):
+        u = n_old + i
+        peers = [n_old + j for j in range(n_new) if ep is not None and j != i and ep[j] == ep[i]]
+        for v in peers + [int(x) for x in knn[i] if x >= 0]:
+            if v != u:
+                adj[u].add(v)
+                adj[v].add(u)
+    r = np.zeros(n_old + n_new + 1, np.int32)
+    c = []
+    for i, a in enumerate(adj):
+        c += sorted(a)
+        r[i + 1] = len(c)
+    return r, np.array(c, np.int32)
+
+
+def _random_csr(rng, n, deg):
+    adj = [set() for _ in range(n)]
+    for u in range(n):
+        for v in rng.choice(n, size=deg, replace=False):
+            if v != u:
+                adj[u].add(int(v))
+                adj[int(v)].add(u)
+    row = np.zeros(n + 1, np.int32)
+    col = []
+    for i, a in enumerate(adj):
+        col += sorted(a)
+        row[i + 1] = len(col)
+    return row, np.array(col, np.int32)
+
+
+def test_insert_edges_match_set_brute_force(rng):
+    for n_old, n_new, k in [(0, 12, 3), (30, 10, 4), (60, 1, 8), (25, 17, 2)]:
+        row, col = _random_csr(rng, n_old, 3) if n_old else (None, None)
+        ep = rng.integers(100, 104, size=n_new).astype(np.int32)
+        knn = rng.integers(-1, n_old + n_new, size=(n_new, k)).astype(np.int32)
+        got_r, got_c = oracle.insert_edges(row, col, n_old, n_new, ep, knn)
+        want_r, want_c = _sets_insert(row, col, n_old, n_new, ep, knn)
+        np.testing.assert_array_equal(got_r, want_r)
+        np.testing.assert_array_equal(got_c, want_c)
+
+
+def test_insert_edges_two_batches_equal_one(rng):
+    """Edge union is associative: inserting A then B (same neighbour lists, B's
+    episodes new) equals inserting A+B at once."""
+    n_old = 40
+    row, col = _random_csr(rng, n_old, 4)
+    ep = np.array([7] * 5 + [8] * 6 + [9] * 4, np.int32)
+    knn = rng.integers(0, n_old + 15, size=(15, 5)).astype(np.int32)
+    knn[:11] = np.minimum(knn[:11], n_old + 10)      # batch A only sees nodes up to its own
+    r1, c1 = oracle.insert_edges(row, col, n_old, 11, ep[:11], knn[:11])
+    r2, c2 = oracle.insert_edges(r1, c1, n_old + 11, 4, ep[11:], knn[11:])
+    ra, ca = oracle.insert_edges(row, col, n_old, 15, ep, knn)
+    np.testing.assert_array_equal(r2, ra)
+    np.testing.assert_array_equal(c2, ca)
+
+
+def _check_flush_invariants(row0, col0, row1, col1, n_old, n_new):
+    assert len(row1) == n_old + n_new + 1
+    for i in range(n_old):                    # every old edge kept
+        assert set(col0[row0[i]:row0[i + 1]]) <= set(col1[row1[i]:row1[i + 1]]), i
+    edges = set()
+    for i in range(n_old + n_new):
+        r = col1[row1[i]:row1[i + 1]]
+        assert np.all(np.diff(r) > 0), f"row {i} not strictly ascending"
+        assert i not in set(r.tolist())
+        edges |= {(i, int(v)) for v in r}
+    assert all((v, u) in edges for (u, v) in edges), "not symmetric"
+    assert len(col1) > len(col0)              # T15: edges were added
+    for i in range(n_old, n_old + n_new):     # every new node linked
+        assert row1[i + 1] > row1[i], i
+
+
+def test_insert_edges_keep_reference_flush_invariants(golden):
+    """The reference's own flush (fixture made by StreamingBuffer, streaming.cpp:35-163)
+    and the oracle's rule share its contract: old edges kept, symmetric, rows
+    ascending, every new node linked."""
+    z = np.load(golden / "stream_flush.npz")
+    n_old = len(z["before_mods"])
+    n_new = len(z["new_mods"])
+    _check_flush_invariants(z["before_row"], z["before_col"], z["after_row"], z["after_col"], n_old, n_new)
+    emb = np.concatenate([z["before_emb"].reshape(n_old, -1), z["new_emb"]]).astype(np.float32)
+    knn, _ = oracle.knn(emb, np.arange(n_old, n_old + n_new, dtype=np.int32), 8)
+    ep = np.array([0] * 4 + [1] * 3 + [2] * 3, np.int32)
+    r, c = oracle.insert_edges(z["before_row"], z["before_col"], n_old, n_new, ep, knn)
+    _check_flush_invariants(z["before_row"], z["before_col"], r, c, n_old, n_new)
