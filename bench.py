@@ -33,6 +33,22 @@ def log(*a):
     print("[bench]", *a, file=sys.stderr, flush=True)
 
 
+def scan_traffic(n: int, d: int):
+    """HBM bytes per k_scan launch measured with rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE,
+    scaled by a plain-copy calibration) for this workload, from the committed profile."""
+    p = ROOT / "profiles" / "k_scan_fp32_1M.md"
+    if not p.exists():
+        return None
+    kv = {}
+    for line in p.read_text().splitlines():
+        if ":" in line and not line.startswith(("#", " ", "|")):
+            k, v = line.split(":", 1)
+            kv[k.strip()] = v.split("(")[0].strip()
+    if kv.get("workload") != f"N={n} D={d}":
+        return None
+    return int(kv["traffic_bytes_per_launch"])
+
+
 def pctl(v, p):
     v = np.sort(np.asarray(v, np.float64))
     return float(v[int(p * (len(v) - 1))]) if len(v) else 0.0
@@ -231,7 +247,7 @@ def main() -> int:
                                                     select=float(ph[:, 2].mean()))),
         **out,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": scan_traffic(N, D),
                      "kernel": "k_scan<float,QF32<12>>", "bytes_per_launch": bytes_f32},
     }
 
