@@ -199,6 +199,53 @@ int mars_graph_insert(mars_graph* g, int32_t n_new, const float* embeddings, con
                       const float* timestamps, const int32_t* episode_ids, int32_t knn_k,
                       int32_t* out_knn, mars_insert_stats* stats);
 
+/* ---- tiled out-of-core comparator (include/tiled_query.h:33-102) ------------- */
+/* TiledQueryConfig (tiled_query.h:33-39), same defaults (mars_tiled_config_default).
+ * use_fp16 is accepted and ignored, as in the reference (its tiles are always fp32). */
+typedef struct mars_tiled_config {
+    int32_t tile_size;             /* rows per tile, default 5,000,000            */
+    int32_t top_k;                 /* default 10                                   */
+    float   time_decay_lambda;     /* default 1e-8                                 */
+    int32_t modality_filter;       /* default -1                                   */
+    int32_t use_fp16;              /* default 1, no effect                         */
+} mars_tiled_config;
+/* TiledQueryResult (tiled_query.h:41-45), 12 bytes. */
+typedef struct mars_tiled_result {
+    int32_t node_id;
+    float   score;
+    int32_t modality;
+} mars_tiled_result;
+/* TiledQueryStats (tiled_query.h:47-54) plus the achieved host-to-device rate.
+ * Copies of tile i+1 overlap the scan of tile i, so transfer_ms + compute_ms can
+ * exceed total_ms. */
+typedef struct mars_tiled_stats {
+    int32_t total_nodes;
+    int32_t num_tiles;
+    float   total_ms;
+    float   transfer_ms;           /* sum of tile copy times (events on the copy stream) */
+    float   compute_ms;            /* sum of tile scan + merge times                      */
+    float   merge_ms;              /* host decode of the K keys                           */
+    double  h2d_gbs;               /* bytes copied / transfer_ms                          */
+} mars_tiled_stats;
+typedef struct mars_tiled_ctx mars_tiled_ctx;
+void mars_tiled_config_default(mars_tiled_config* cfg);
+/* create_tiled_context / destroy_tiled_context (tiled_query.h:79-83): two device tile
+ * buffers of max_tile_size rows (copy of tile i+1 overlaps the scan of tile i). */
+int mars_tiled_ctx_create(int32_t max_tile_size, int32_t embedding_dim, int32_t max_k, mars_tiled_ctx** out);
+int mars_tiled_ctx_destroy(mars_tiled_ctx* ctx);
+/* tiled_query (tiled_query.h:85-102, tiled_query.cu:174-314): host-resident corpus
+ * (embeddings n * d fp32, modalities, timestamps); per tile the exact decayed top-K,
+ * filtered rows (score -FLT_MAX) dropped, the K best of all tiles by (score desc, id
+ * asc) in out[0 .. *n_out). Host arrays from mars_host_alloc are copied at PCIe rate;
+ * pageable arrays are staged by the runtime. */
+int mars_tiled_query(mars_tiled_ctx* ctx, const float* embeddings, const int32_t* modalities,
+                     const float* timestamps, int32_t n, int32_t d, const float* query, float query_timestamp,
+                     const mars_tiled_config* cfg, mars_tiled_result* out, int32_t cap, int32_t* n_out,
+                     mars_tiled_stats* stats);
+/* Pinned host memory (hipHostMalloc) for corpora streamed by mars_tiled_query. */
+int mars_host_alloc(size_t bytes, void** ptr);
+int mars_host_free(void* ptr);
+
 /* ---- query context (memory_cuda.cuh:141-231) --------------------------------- */
 #define MARS_CTX_USE_FP16    0x1u   /* scan the fp16 copy when present (ctx.use_fp16)      */
 #define MARS_CTX_USE_GRAPH   0x2u   /* replay the query pipeline as a hipGraph             */

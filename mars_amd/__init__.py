@@ -399,6 +399,95 @@ def insert_nodes(dg: DeviceMemoryGraph, embeddings, modalities, timestamps, epis
     return (out, knn[:, :knn_k]) if return_knn else out
 
 
+@dataclass
+class TiledQueryConfig:                             # tiled_query.h:33-39 (same defaults)
+    tile_size: int = 5_000_000
+    top_k: int = 10
+    time_decay_lambda: float = 1e-8
+    modality_filter: int = -1
+    use_fp16: bool = True                           # accepted, no effect (as the reference)
+
+    def to_c(self) -> _lib.TiledConfigC:
+        return _lib.TiledConfigC(int(self.tile_size), int(self.top_k), float(self.time_decay_lambda),
+                                 int(self.modality_filter), int(bool(self.use_fp16)))
+
+
+@dataclass
+class TiledQueryResult:                             # tiled_query.h:41-45
+    node_id: int
+    score: float
+    modality: int
+
+
+@dataclass
+class TiledQueryStats:                              # tiled_query.h:47-54 (+ h2d_gbs)
+    total_nodes: int = 0
+    num_tiles: int = 0
+    total_ms: float = 0.0
+    transfer_ms: float = 0.0
+    compute_ms: float = 0.0
+    merge_ms: float = 0.0
+    h2d_gbs: float = 0.0
+
+
+class TiledQueryContext:
+    """create_tiled_context (tiled_query.h:56-83): two device tile buffers."""
+
+    def __init__(self, handle: C.c_void_p, max_tile_size: int, dim: int, max_k: int):
+        self.handle, self.max_tile_size, self.embedding_dim, self.max_k = handle, max_tile_size, dim, max_k
+
+
+def create_tiled_context(max_tile_size: int, embedding_dim: int, max_k: int = 64) -> TiledQueryContext:
+    h = C.c_void_p()
+    check(lib.mars_tiled_ctx_create(int(max_tile_size), int(embedding_dim), int(max_k), C.byref(h)),
+          "create_tiled_context")
+    return TiledQueryContext(h, int(max_tile_size), int(embedding_dim), int(max_k))
+
+
+def destroy_tiled_context(ctx: TiledQueryContext) -> None:
+    if ctx.handle:
+        check(lib.mars_tiled_ctx_destroy(ctx.handle), "destroy_tiled_context")
+        ctx.handle = C.c_void_p()
+
+
+def tiled_query(ctx: TiledQueryContext, embeddings, modalities, timestamps, query, query_timestamp: float,
+                cfg: TiledQueryConfig, stats: Optional[TiledQueryStats] = None) -> List[TiledQueryResult]:
+    """tiled_query (tiled_query.cu:174-314) over host arrays (numpy, or HostBuffer views)."""
+    emb = _f32(embeddings).reshape(-1)
+    mods, ts, q = _i32(modalities), _f32(timestamps), _f32(query)
+    n = len(mods)
+    out = (_lib.TiledResultC * max(cfg.top_k, 1))()
+    nout = C.c_int32()
+    st = _lib.TiledStatsC()
+    c = cfg.to_c()
+    check(lib.mars_tiled_query(ctx.handle, _ptr(emb), _ptr(mods), _ptr(ts), n, len(q), _ptr(q),
+                               C.c_float(query_timestamp), C.byref(c), out, cfg.top_k, C.byref(nout), C.byref(st)),
+          "tiled_query")
+    if stats is not None:
+        for f in ("total_nodes", "num_tiles", "total_ms", "transfer_ms", "compute_ms", "merge_ms", "h2d_gbs"):
+            setattr(stats, f, getattr(st, f))
+    return [TiledQueryResult(out[i].node_id, out[i].score, out[i].modality) for i in range(min(nout.value, cfg.top_k))]
+
+
+class HostBuffer:
+    """Pinned host memory (hipHostMalloc) viewed as a numpy array; freed with free()."""
+
+    def __init__(self, shape, dtype):
+        self.array = None
+        nbytes = int(np.prod(shape)) * np.dtype(dtype).itemsize
+        p = C.c_void_p()
+        check(lib.mars_host_alloc(nbytes, C.byref(p)), "mars_host_alloc")
+        self.ptr = p.value
+        buf = (C.c_char * max(nbytes, 1)).from_address(self.ptr)
+        self.array = np.frombuffer(buf, dtype=dtype, count=int(np.prod(shape))).reshape(shape)
+
+    def free(self) -> None:
+        if self.ptr:
+            self.array = None
+            check(lib.mars_host_free(C.c_void_p(self.ptr)), "mars_host_free")
+            self.ptr = None
+
+
 class DeviceBuffer:
     """Device memory owned by libmars_amd's HIP runtime (holds e.g. query vectors)."""
 

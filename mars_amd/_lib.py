@@ -116,6 +116,21 @@ class InsertStatsC(C.Structure):
     ]
 
 
+class TiledConfigC(C.Structure):
+    _fields_ = [("tile_size", C.c_int32), ("top_k", C.c_int32), ("time_decay_lambda", C.c_float),
+                ("modality_filter", C.c_int32), ("use_fp16", C.c_int32)]
+
+
+class TiledResultC(C.Structure):
+    _fields_ = [("node_id", C.c_int32), ("score", C.c_float), ("modality", C.c_int32)]
+
+
+class TiledStatsC(C.Structure):
+    _fields_ = [("total_nodes", C.c_int32), ("num_tiles", C.c_int32), ("total_ms", C.c_float),
+                ("transfer_ms", C.c_float), ("compute_ms", C.c_float), ("merge_ms", C.c_float),
+                ("h2d_gbs", C.c_double)]
+
+
 class CorpusParamsC(C.Structure):
     _fields_ = [
         ("num_nodes", C.c_int64),
@@ -171,6 +186,13 @@ SIGNATURES = {
     "mars_copy_device": (C.c_int, [VP, VP, C.c_size_t]),
     "mars_bench_queries": (C.c_int, [VP, VP, VP, I64, I32, C.c_float, C.POINTER(RetrievalConfigC), I32, VP, VP,
                                      VP, VP]),
+    "mars_tiled_config_default": (None, [C.POINTER(TiledConfigC)]),
+    "mars_tiled_ctx_create": (C.c_int, [I32, I32, I32, C.POINTER(VP)]),
+    "mars_tiled_ctx_destroy": (C.c_int, [VP]),
+    "mars_tiled_query": (C.c_int, [VP, VP, VP, VP, I32, I32, VP, C.c_float, C.POINTER(TiledConfigC), VP, I32, PI32,
+                                   C.POINTER(TiledStatsC)]),
+    "mars_host_alloc": (C.c_int, [C.c_size_t, C.POINTER(VP)]),
+    "mars_host_free": (C.c_int, [VP]),
     # mars_corpus.h
     "mars_corpus_default": (None, [C.POINTER(CorpusParamsC), I64, I32, C.c_uint64]),
     "mars_corpus_generate": (C.c_int, [C.POINTER(CorpusParamsC), VP, VP, VP, VP, I32]),

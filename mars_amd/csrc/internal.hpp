@@ -243,6 +243,7 @@ struct ScanArgs {
     uint32_t* gcnt;          // number of candidate keys appended (atomicAdd)
     int32_t rows_per_wg;     // unused (grid-stride scan)
     int32_t num_wg;
+    int64_t id_base;         // node id of row 0 (tiles of a host-resident corpus)
 };
 // Kernel entry point + launch shape of one launch (for graph kernel nodes).
 struct KernelLaunch {
@@ -286,6 +287,9 @@ struct FinalizeArgs {
     uint64_t* stamps;        // 4 realtime stamps (start, seeds, BFS done, end) or null
 };
 int launch_finalize(const FinalizeArgs& a, hipStream_t s);
+// Tiled query: fold the candidate keys the scan of one tile appended (part[0..*gcnt))
+// into the running K best (carry, ascending) and clear *gcnt; the scan's bound stays.
+int launch_tile_merge(uint64_t* part, uint32_t* gcnt, uint64_t* carry, int32_t k, hipStream_t s);
 
 struct EpisodeArgs {
     const float* emb;

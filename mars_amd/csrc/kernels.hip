@@ -293,7 +293,7 @@ __global__ __launch_bounds__(256) void k_scan(ScanArgs a) {
             const bool valid = r < a.n;
             const float s = fuse_score(row16_sum(dot[u]), ts[u], mod[u], ep[u], a);
             if (valid && sub == 0) a.fin[r] = s;
-            const uint64_t key = valid ? make_key(s, uint32_t(r)) : kEmptyKey;
+            const uint64_t key = valid ? make_key(s, uint32_t(a.id_base + r)) : kEmptyKey;
             list_offer(list, thr, key, sub == 0, lane, k);
         }
     }
@@ -936,6 +936,29 @@ __global__ void k_convert_f16(const float* __restrict__ in, __half* __restrict__
         out[i] = __float2half_rn(in[i]);
 }
 
+// Tiled query (host-resident corpus, tiled_query.cu:174-314): after the scan of one
+// tile, fold its candidate keys into the running K best and clear the count. Four
+// waves sort-merge strided chunks of 64 keys, then wave 0 merges the four lists.
+__global__ __launch_bounds__(256) void k_tile_merge(uint64_t* __restrict__ part, uint32_t* gcnt,
+                                                    uint64_t* __restrict__ carry, int32_t k) {
+    __shared__ uint64_t s_l[4][64];
+    const int lane = lane_id(), wave = int(threadIdx.x >> 6);
+    const uint32_t n = *gcnt;
+    uint64_t list = (wave == 0 && lane < k) ? carry[lane] : kEmptyKey;
+    for (uint32_t c0 = uint32_t(wave) * 64u; c0 < n; c0 += 256u) {
+        const uint32_t i = c0 + uint32_t(lane);
+        list = wave_merge64(list, wave_sort64(i < n ? part[i] : kEmptyKey, lane), lane, k);
+    }
+    s_l[wave][lane] = list;
+    __syncthreads();
+    if (wave == 0) {
+        list = wave_merge64(list, s_l[1][lane], lane, k);
+        list = wave_merge64(list, wave_merge64(s_l[2][lane], s_l[3][lane], lane, k), lane, k);
+        if (lane < k) carry[lane] = list;
+        if (lane == 0) *gcnt = 0u;
+    }
+}
+
 template <typename T, typename QF>
 KernelLaunch scan_launch_t(const ScanArgs& a) {
     KernelLaunch l;
@@ -1003,6 +1026,12 @@ int launch_scan(const ScanArgs& a, hipStream_t s) {
     const KernelLaunch l = scan_launch(a);
     void* args[] = {const_cast<ScanArgs*>(&a)};
     MARS_HIP(hipLaunchKernel(l.fn, l.grid, l.block, args, 0, s));
+    return MARS_OK;
+}
+
+int launch_tile_merge(uint64_t* part, uint32_t* gcnt, uint64_t* carry, int32_t k, hipStream_t s) {
+    hipLaunchKernelGGL(k_tile_merge, dim3(1), dim3(256), 0, s, part, gcnt, carry, k);
+    MARS_HIP(hipGetLastError());
     return MARS_OK;
 }
 

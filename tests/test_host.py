@@ -50,6 +50,20 @@ def test_config_defaults_match_reference():
 def test_struct_layouts():
     assert C.sizeof(_lib.QueryResultC) == 16
     assert C.sizeof(_lib.RetrievalConfigC) == 48
+    assert C.sizeof(_lib.TiledResultC) == 12                      # TiledQueryResult
+    assert C.sizeof(_lib.TiledConfigC) == 20
+    assert C.sizeof(_lib.InsertStatsC) == 48
+    assert _lib.InsertStatsC.queryable_us.offset == 24
+
+
+def test_tiled_config_defaults_match_reference():
+    """TiledQueryConfig defaults (include/tiled_query.h:33-39)."""
+    c = _lib.TiledConfigC()
+    _lib.lib.mars_tiled_config_default(C.byref(c))
+    assert (c.tile_size, c.top_k, c.modality_filter, c.use_fp16) == (5_000_000, 10, -1, 1)
+    assert c.time_decay_lambda == pytest.approx(1e-8)
+    py = mars_amd.TiledQueryConfig()
+    assert (py.tile_size, py.top_k, py.modality_filter) == (c.tile_size, c.top_k, c.modality_filter)
 
 
 # ------------------------------------------------------------------ corpus
