@@ -49,6 +49,91 @@ def scan_traffic(n: int, d: int):
     return int(kv["traffic_bytes_per_launch"])
 
 
+def tiled_pass(args, mars_amd, corpus, c, qnodes, N, D, K, pctl, lat_resident):
+    """tiled_query contract over a host-RAM (pinned) copy of the corpus: tiles of 250K rows
+    (copy of tile i+1 overlapping the scan of tile i), and one whole-corpus tile."""
+    from mars_amd import TiledQueryConfig
+    bufs = [mars_amd.HostBuffer((N, D), np.float32), mars_amd.HostBuffer((N,), np.int32),
+            mars_amd.HostBuffer((N,), np.float32)]
+    tctx = mars_amd.create_tiled_context(min(N, 250_000), D, 64)
+    res = {}
+    try:
+        bufs[0].array[:] = c.embeddings
+        bufs[1].array[:] = c.modalities
+        bufs[2].array[:] = c.timestamps
+        for tile in (min(N, 250_000),):
+            cfg = TiledQueryConfig(tile_size=tile, top_k=K, time_decay_lambda=corpus.DECAY_LAMBDA)
+            tot, x, comp, gbs = [], [], [], []
+            for i, node in enumerate(qnodes[:args.tiled_queries + 1]):
+                st = mars_amd.TiledQueryStats()
+                mars_amd.tiled_query(tctx, bufs[0].array, bufs[1].array, bufs[2].array, c.embeddings[node],
+                                     corpus.QUERY_TIME, cfg, st)
+                if i:                                   # first call warms the copy path
+                    tot.append(st.total_ms); x.append(st.transfer_ms); comp.append(st.compute_ms)
+                    gbs.append(st.h2d_gbs)
+            res = dict(tile_rows=tile, tiles=(N + tile - 1) // tile, queries=len(tot), host_memory="pinned",
+                       total_ms_p50=pctl(tot, .5), total_ms_p99=pctl(tot, .99), transfer_ms_mean=float(np.mean(x)),
+                       compute_ms_mean=float(np.mean(comp)), h2d_gbs_mean=float(np.mean(gbs)),
+                       resident_global_p50_ms=pctl(lat_resident, .5) / 1e3,
+                       speedup_resident_vs_tiled=pctl(tot, .5) / (pctl(lat_resident, .5) / 1e3))
+            log(f"tiled comparator ({res['tiles']} tiles of {tile} rows, pinned host RAM): total p50 "
+                f"{res['total_ms_p50']:.1f} ms (H2D {res['transfer_ms_mean']:.1f} ms at {res['h2d_gbs_mean']:.1f} "
+                f"GB/s, scan {res['compute_ms_mean']:.2f} ms) vs HBM-resident global p50 "
+                f"{pctl(lat_resident, .5) / 1e3:.3f} ms ({res['speedup_resident_vs_tiled']:.0f}x)")
+    finally:
+        mars_amd.destroy_tiled_context(tctx)
+        for b in bufs:
+            b.free()
+    return res
+
+
+def stream_pass(args, mars_amd, corpus, lib, check, RetrievalConfigC, full, dg, ctx, dq, qnodes, ep_cfgs, gcfg,
+                N, D, M, pctl):
+    """Streaming: 10-node episodes inserted at 2,000 nodes/s on the graph's side stream
+    while Q=1 queries arrive at 1,000/s, alternating global and episode-scoped."""
+    from mars_amd import _lib
+    nq = min(args.stream_queries, len(qnodes))
+    cfgs = (RetrievalConfigC * nq)()
+    epc = ep_cfgs(qnodes[:nq])
+    g1 = gcfg.to_c()
+    for i in range(nq):
+        cfgs[i] = g1 if i % 2 == 0 else epc[i]
+    nb = (M + 9) // 10
+    ins = (_lib.InsertStatsC * nb)()
+    lat = np.zeros(nq, np.float64)
+    qstart = np.zeros(nq, np.float64)
+    istart = np.zeros(nb, np.float64)
+    emb = np.ascontiguousarray(full.embeddings[N:N + M])
+    mods, ts = np.ascontiguousarray(full.modalities[N:N + M]), np.ascontiguousarray(full.timestamps[N:N + M])
+    ep = np.ascontiguousarray(full.episode_ids[N:N + M])
+    pv = lambda a: C.c_void_p(a.ctypes.data)
+    b = _lib.StreamBenchC(dq.ptr, D, nq, corpus.QUERY_TIME, C.cast(cfgs, C.c_void_p).value, 1000.0, pv(emb).value,
+                          pv(mods).value, pv(ts).value, pv(ep).value, M, 10, 2000.0, corpus.KNN_K, pv(lat).value,
+                          pv(qstart).value, C.cast(ins, C.c_void_p).value, pv(istart).value)
+    t0 = time.time()
+    check(lib.mars_bench_stream(dg.handle, ctx.handle, C.byref(b)), "mars_bench_stream")
+    wall = time.time() - t0
+    dg.refresh()
+    assert dg.num_nodes == N + M
+    lg, le = lat[0::2], lat[1::2]
+    qa = np.array([s.queryable_us for s in ins])
+    li = np.array([s.linked_us for s in ins])
+    kn = np.array([s.knn_us for s in ins])
+    span = istart[-1] - istart[0] + li[-1]
+    res = dict(base_nodes=N, inserted_nodes=M, insert_batch=10, insert_rate_target=2000.0,
+               insert_rate_achieved=M / (span / 1e6), query_rate_target=1000.0, queries=nq,
+               global_p50_us=pctl(lg, .5), global_p99_us=pctl(lg, .99), episode_p50_us=pctl(le, .5),
+               episode_p99_us=pctl(le, .99), queryable_p50_us=pctl(qa, .5), queryable_p99_us=pctl(qa, .99),
+               linked_p50_us=pctl(li, .5), linked_p99_us=pctl(li, .99), knn_mean_us=float(kn.mean()),
+               rows_relocated=int(sum(s.rows_relocated for s in ins)),
+               rows_appended=int(sum(s.rows_appended for s in ins)), wall_s=wall)
+    log(f"streaming ({M} nodes at 2000/s onto {N}, 1000 q/s 50/50): global p99 {res['global_p99_us']:.0f} us, "
+        f"episode p99 {res['episode_p99_us']:.0f} us; time-to-queryable p50 {res['queryable_p50_us']:.0f} us "
+        f"p99 {res['queryable_p99_us']:.0f} us; linked p50 {res['linked_p50_us']:.0f} us p99 "
+        f"{res['linked_p99_us']:.0f} us (k-NN {res['knn_mean_us']:.0f} us)")
+    return res
+
+
 def pctl(v, p):
     v = np.sort(np.asarray(v, np.float64))
     return float(v[int(p * (len(v) - 1))]) if len(v) else 0.0
@@ -66,6 +151,10 @@ def main() -> int:
     ap.add_argument("--cpu-queries", type=int, default=40)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--profile-only", action="store_true", help="only the global fp32 pass (for rocprofv3)")
+    ap.add_argument("--stream-nodes", type=int, default=8000,
+                    help="nodes inserted during the streaming pass (10-node episodes at 2,000 nodes/s)")
+    ap.add_argument("--stream-queries", type=int, default=4000, help="queries of the streaming pass (1,000/s)")
+    ap.add_argument("--tiled-queries", type=int, default=8, help="queries of the tiled out-of-core comparator")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU; --gpus above 1 is not supported here "
@@ -78,12 +167,14 @@ def main() -> int:
 
     mars_amd.init(0)
     N, D, K = args.n, args.dim, 10
+    M = 0 if args.profile_only else max(0, args.stream_nodes) // 10 * 10     # whole 10-node episodes
     t = time.time()
-    c = corpus.make_corpus(N, D, seed=args.seed)
-    log(f"corpus N={N} D={D} seed={args.seed}: {time.time() - t:.1f}s")
+    full = corpus.make_corpus(N + M, D, seed=args.seed)      # the generator is prefix-stable: rows >= N arrive later
+    c = corpus.Corpus(full.embeddings[:N], full.modalities[:N], full.timestamps[:N], full.episode_ids[:N], args.seed)
+    log(f"corpus N={N} D={D} seed={args.seed} (+{M} streamed): {time.time() - t:.1f}s")
     t = time.time()
     g = mars_amd.MemoryGraph(N, D, None, None, c.embeddings, c.modalities, c.timestamps)
-    dg = mars_amd.upload_to_device(g)
+    dg = mars_amd.upload_to_device(g, capacity_nodes=N + M)
     mars_amd.upload_fp16_embeddings(dg)
     log(f"upload + fp16 copy: {time.time() - t:.1f}s")
     t = time.time()
@@ -97,7 +188,7 @@ def main() -> int:
     mars_amd.upload_episode_ids(dg, c.episode_ids)
     csr = mars_amd.build_episode_csr(c.episode_ids, N)
     mars_amd.upload_episode_csr(dg, csr)
-    ctx = mars_amd.create_query_context(N, D, 64, flags=0)
+    ctx = mars_amd.create_query_context(N + M, D, 64, flags=0)
 
     nq = args.steps + args.warmup
     qnodes = corpus.pick_queries(c.modalities, nq, seed=args.query_seed)
@@ -220,6 +311,12 @@ def main() -> int:
                                   scan_kernel_mean_us=float(kern_h.mean()),
                                   scan_gbs=bytes_f16 / float(kern_h.mean()) / 1e3,
                                   scan_frac=bytes_f16 / float(kern_h.mean()) / 1e3 / HBM_PEAK_GBS)
+
+    if not args.profile_only and args.tiled_queries > 0:
+        out["tiled_comparator"] = tiled_pass(args, mars_amd, corpus, c, qnodes[W:], N, D, K, pctl, lat_g)
+    if M > 0 and args.stream_queries > 0:
+        out["streaming"] = stream_pass(args, mars_amd, corpus, lib, check, RetrievalConfigC, full, dg, ctx, dq,
+                                       qnodes, ep_cfgs, gcfg, N, D, M, pctl)
 
     achieved = bytes_f32 / float(kern_g.mean()) / 1e3       # GB/s
     res = {

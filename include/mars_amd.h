@@ -313,6 +313,36 @@ int mars_bench_queries(const mars_graph* g, mars_ctx* ctx, const float* d_querie
                        int32_t n, float t_q, const mars_retrieval_config* cfgs, int32_t n_cfg,
                        double* lat_us, float* kern_us, float* bfs_us, int32_t* n_res);
 
+/* Streaming workload driver (no reference counterpart; the BASELINE streaming
+ * configuration): on one thread, n_queries single queries paced at query_rate per
+ * second (query i starts at i / query_rate s, or when the previous one returns);
+ * on a second thread, n_insert host rows inserted with mars_graph_insert in
+ * batches of insert_batch nodes paced at insert_rate nodes per second. Both start
+ * together. query_lat_us[i] = wall latency of query i (inside the library);
+ * query_start_us[i] = its start since the run began; ins_stats[j] / ins_start_us[j]
+ * for insert batch j (ceil(n_insert / insert_batch) batches). */
+typedef struct mars_stream_bench {
+    const float*                 d_queries;      /* device, n_queries * stride floats   */
+    int64_t                      stride;
+    int32_t                      n_queries;
+    float                        t_q;
+    const mars_retrieval_config* cfgs;           /* n_queries configurations            */
+    double                       query_rate;     /* queries per second                  */
+    const float*                 ins_emb;        /* host, n_insert * embedding_dim      */
+    const int32_t*               ins_mods;
+    const float*                 ins_ts;
+    const int32_t*               ins_ep;         /* NULL if the graph has no episode ids */
+    int32_t                      n_insert;
+    int32_t                      insert_batch;
+    double                       insert_rate;    /* nodes per second                    */
+    int32_t                      knn_k;
+    double*                      query_lat_us;
+    double*                      query_start_us;
+    mars_insert_stats*           ins_stats;
+    double*                      ins_start_us;
+} mars_stream_bench;
+int mars_bench_stream(mars_graph* g, mars_ctx* ctx, mars_stream_bench* bench);
+
 #ifdef __cplusplus
 }
 #endif

@@ -131,6 +131,14 @@ class TiledStatsC(C.Structure):
                 ("h2d_gbs", C.c_double)]
 
 
+class StreamBenchC(C.Structure):
+    _fields_ = [("d_queries", C.c_void_p), ("stride", C.c_int64), ("n_queries", C.c_int32), ("t_q", C.c_float),
+                ("cfgs", C.c_void_p), ("query_rate", C.c_double), ("ins_emb", C.c_void_p), ("ins_mods", C.c_void_p),
+                ("ins_ts", C.c_void_p), ("ins_ep", C.c_void_p), ("n_insert", C.c_int32), ("insert_batch", C.c_int32),
+                ("insert_rate", C.c_double), ("knn_k", C.c_int32), ("query_lat_us", C.c_void_p),
+                ("query_start_us", C.c_void_p), ("ins_stats", C.c_void_p), ("ins_start_us", C.c_void_p)]
+
+
 class CorpusParamsC(C.Structure):
     _fields_ = [
         ("num_nodes", C.c_int64),
@@ -186,6 +194,7 @@ SIGNATURES = {
     "mars_copy_device": (C.c_int, [VP, VP, C.c_size_t]),
     "mars_bench_queries": (C.c_int, [VP, VP, VP, I64, I32, C.c_float, C.POINTER(RetrievalConfigC), I32, VP, VP,
                                      VP, VP]),
+    "mars_bench_stream": (C.c_int, [VP, VP, C.POINTER(StreamBenchC)]),
     "mars_tiled_config_default": (None, [C.POINTER(TiledConfigC)]),
     "mars_tiled_ctx_create": (C.c_int, [I32, I32, I32, C.POINTER(VP)]),
     "mars_tiled_ctx_destroy": (C.c_int, [VP]),

@@ -15,6 +15,8 @@
 #include <chrono>
 #include <cstdarg>
 #include <cstring>
+#include <string>
+#include <thread>
 #include <vector>
 
 
@@ -125,6 +127,12 @@ int load_csr(Graph& g, int32_t n, int32_t e, const int32_t* row, const int32_t* 
 }
 
 void graph_slot_free(Ctx::GraphSlot& g);
+
+// Default col room for streaming inserts: 256 slots per node of spare capacity (a new
+// row, and the old rows it links to when they move to the tail).
+int64_t edge_room(const Graph& g) {
+    return int64_t(g.cap_n - g.n) * 256 + (g.cap_n > g.n ? 4096 : 0);
+}
 
 int ctx_free(Ctx& c) {
     (void)use_device(c.device);
@@ -398,11 +406,8 @@ int mars_graph_create(const mars_graph_desc* d, mars_graph** out) {
     g.device = devid;
     g.n = d->num_nodes; g.e = d->num_edges; g.d = d->embedding_dim;
     g.cap_n = std::max(d->capacity_nodes, d->num_nodes);
-    // default edge room for streaming inserts: 256 col slots per node of spare capacity
-    // (a new row, and the old rows it links to when they move to the tail)
-    const int64_t grow = int64_t(g.cap_n - g.n) * 256 + (g.cap_n > g.n ? 4096 : 0);
     g.cap_e = d->capacity_edges > 0 ? std::max<int64_t>(d->capacity_edges, d->num_edges)
-                                    : int64_t(d->num_edges) + grow;
+                                    : int64_t(d->num_edges) + edge_room(g);
     const size_t N = size_t(g.n), D = size_t(g.d), CN = size_t(g.cap_n);
     int rc = MARS_OK;
     auto fail = [&](int r) { graph_free(g); delete gh; return r; };
@@ -435,12 +440,12 @@ int mars_graph_set_csr(mars_graph* gh, int32_t ne, const int32_t* row, const int
     MARS_TRY(validate_csr(g.n, ne, row, col));
     MARS_TRY(use_device(g.device));
     MARS_HIP(hipStreamSynchronize(g.ins_stream));
-    if (int64_t(ne) > g.cap_e) {
+    if (int64_t(ne) + edge_room(g) > g.cap_e) {
         int32_t* ncol = nullptr;
-        MARS_TRY(dmalloc(&ncol, size_t(ne)));
+        MARS_TRY(dmalloc(&ncol, size_t(ne + edge_room(g))));
         dfree(g.col);
         g.col = ncol;
-        g.cap_e = ne;
+        g.cap_e = int64_t(ne) + edge_room(g);
     }
     return load_csr(g, g.n, ne, row, col, hipMemcpyHostToDevice);
 }
@@ -689,6 +694,49 @@ int mars_bench_queries(const mars_graph* g, mars_ctx* c, const float* dq, int64_
         if (bfs_us) bfs_us[i] = st.gpu_ms_bfs * 1000.0f;
         if (n_res) n_res[i] = nr;
     }
+    return MARS_OK;
+}
+
+int mars_bench_stream(mars_graph* g, mars_ctx* c, mars_stream_bench* b) {
+    MARS_CHECK(g && c && b && b->d_queries && b->cfgs && b->query_lat_us && b->n_queries >= 0 && b->query_rate > 0.0 &&
+                   b->stride >= g->g.d && b->n_insert >= 0 && (b->n_insert == 0 || (b->ins_emb && b->ins_mods &&
+                   b->ins_ts && b->ins_stats && b->insert_batch > 0 && b->insert_rate > 0.0)),
+               MARS_ERR_INVALID, "bad streaming benchmark arguments");
+    using clk = std::chrono::steady_clock;
+    const auto start = clk::now();
+    auto since = [&](clk::time_point t) { return std::chrono::duration<double, std::micro>(t - start).count(); };
+    int ins_rc = MARS_OK;
+    std::string ins_err;
+    std::thread writer([&]() {
+        const int32_t nb = (b->n_insert + b->insert_batch - 1) / b->insert_batch;
+        const int64_t d = g->g.d;
+        for (int32_t j = 0; j < nb && ins_rc == MARS_OK; ++j) {
+            const int64_t first = int64_t(j) * b->insert_batch;
+            const int32_t m = int32_t(std::min<int64_t>(b->insert_batch, b->n_insert - first));
+            std::this_thread::sleep_until(start + std::chrono::duration_cast<clk::duration>(
+                                                      std::chrono::duration<double>(double(first) / b->insert_rate)));
+            if (b->ins_start_us) b->ins_start_us[j] = since(clk::now());
+            ins_rc = mars_graph_insert(g, m, b->ins_emb + first * d, b->ins_mods + first, b->ins_ts + first,
+                                       b->ins_ep ? b->ins_ep + first : nullptr, b->knn_k, nullptr, &b->ins_stats[j]);
+            if (ins_rc != MARS_OK) ins_err = mars_last_error();
+        }
+    });
+    int rc = MARS_OK;
+    mars_query_result out[64];
+    for (int32_t i = 0; i < b->n_queries && rc == MARS_OK; ++i) {
+        std::this_thread::sleep_until(start + std::chrono::duration_cast<clk::duration>(
+                                                  std::chrono::duration<double>(double(i) / b->query_rate)));
+        mars_stats st{};
+        int32_t nr = 0;
+        const auto t0 = clk::now();
+        rc = query_impl(g, c, nullptr, b->d_queries + int64_t(i) * b->stride, b->t_q, &b->cfgs[i], out, 64, &nr, &st);
+        const auto t1 = clk::now();
+        b->query_lat_us[i] = std::chrono::duration<double, std::micro>(t1 - t0).count();
+        if (b->query_start_us) b->query_start_us[i] = since(t0);
+    }
+    writer.join();
+    if (rc != MARS_OK) return rc;
+    if (ins_rc != MARS_OK) return set_error(ins_rc, "%s", ins_err.c_str());
     return MARS_OK;
 }
 

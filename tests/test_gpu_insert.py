@@ -299,3 +299,54 @@ def test_queries_while_inserting(full):
     finally:
         done.wait()
         live.close()
+
+
+def test_stream_driver_paced_inserts_and_queries(full):
+    """mars_bench_stream: paced inserts on one thread, paced mixed queries on the
+    caller's; the grown graph keeps every old edge and is symmetric."""
+    import ctypes as C
+    from mars_amd import _lib
+    live = Live(full, BASE, BASE + EXTRA)
+    try:
+        row0, col0 = live.row, live.col
+        nq = 60
+        qs = corpus.pick_queries(full.modalities[:BASE], nq, seed=23)
+        dq = mars_amd.DeviceBuffer.from_array(full.embeddings[qs])
+        off = mars_amd.build_episode_csr(full.episode_ids[:BASE], BASE).ep_csr_offsets
+        cfgs = (_lib.RetrievalConfigC * nq)()
+        for i, node in enumerate(qs):
+            ep = int(full.episode_ids[node])
+            cfg = RetrievalConfig(top_k=10, bfs_max_hops=2, time_decay_lambda=corpus.DECAY_LAMBDA)
+            if i % 2:
+                cfg = RetrievalConfig(top_k=10, time_decay_lambda=corpus.DECAY_LAMBDA,
+                                      retrieval_scope=RetrievalScope.EpisodeScoped, query_episode_id=ep,
+                                      query_episode_member_begin=int(off[ep]),
+                                      query_episode_member_count=int(off[ep + 1] - off[ep]))
+            cfgs[i] = cfg.to_c()
+        M = EXTRA
+        emb = np.ascontiguousarray(full.embeddings[BASE:])
+        mods, ts = np.ascontiguousarray(full.modalities[BASE:]), np.ascontiguousarray(full.timestamps[BASE:])
+        ep = np.ascontiguousarray(full.episode_ids[BASE:])
+        ins = (_lib.InsertStatsC * (M // 10))()
+        lat, qst, ist = np.zeros(nq), np.zeros(nq), np.zeros(M // 10)
+        v = lambda a: a.ctypes.data
+        b = _lib.StreamBenchC(dq.ptr, 768, nq, T_Q, C.cast(cfgs, C.c_void_p).value, 2000.0, v(emb), v(mods), v(ts),
+                              v(ep), M, 10, 4000.0, K_NN, v(lat), v(qst), C.cast(ins, C.c_void_p).value, v(ist))
+        _lib.check(_lib.lib.mars_bench_stream(live.dg.handle, live.ctx.handle, C.byref(b)), "mars_bench_stream")
+        dq.free()
+        assert np.all(lat > 0) and np.all(np.diff(qst) > 0)
+        assert [s.nodes_added for s in ins] == [10] * (M // 10)
+        assert [s.first_node for s in ins] == list(range(BASE, BASE + M, 10))
+        assert all(0 < s.queryable_us <= s.linked_us for s in ins)
+        row, col = live.dg.download_csr()
+        assert len(row) == BASE + M + 1
+        edges = set()
+        for u in range(BASE + M):
+            r = col[row[u]:row[u + 1]]
+            assert np.all(np.diff(r) > 0)
+            if u < BASE:
+                np.testing.assert_array_equal(r[:row0[u + 1] - row0[u]], col0[row0[u]:row0[u + 1]])
+            edges |= {(u, int(x)) for x in r}
+        assert all((y, x) in edges for (x, y) in edges)
+    finally:
+        live.close()

@@ -54,6 +54,7 @@ def test_struct_layouts():
     assert C.sizeof(_lib.TiledConfigC) == 20
     assert C.sizeof(_lib.InsertStatsC) == 48
     assert _lib.InsertStatsC.queryable_us.offset == 24
+    assert C.sizeof(_lib.StreamBenchC) == 128 and _lib.StreamBenchC.knn_k.offset == 88
 
 
 def test_tiled_config_defaults_match_reference():
