@@ -768,6 +768,7 @@ int mars_query_batch(const mars_graph* gh, mars_ctx* ch, const float* dq, int32_
     a.emb16 = g.emb16; a.n = n_live; a.d = g.d; a.qh = c.bq; a.q = Q; a.tq = c.btq; a.ts = g.ts; a.mods = g.mods;
     a.lambda = cfg->time_decay_lambda; a.mod_filter = cfg->modality_filter; a.k = K; a.self_base = -1;
     a.part = c.bpart; a.rows_per_range = rpr; a.n_rranges = nrr; a.n_qblocks = nqb;
+    a.uniform_tq = std::all_of(h_tq, h_tq + Q, [&](float x) { return x == h_tq[0]; }) ? 1 : 0;
     MARS_TRY(launch_batch_scan(a, s));
     if (timing) MARS_HIP(hipEventRecord(c.ev[1], s));
     MARS_TRY(launch_batch_merge(c.bpart, nrr, kp, Q, K, c.bout, s));
@@ -827,6 +828,7 @@ int mars_graph_knn(mars_graph* gh, int32_t k, int32_t* nbrs) {
         BatchArgs a{};
         a.emb16 = g.emb16; a.n = g.n; a.d = g.d; a.qh = g.emb16 + q0 * g.d; a.q = q; a.tq = tq; a.ts = g.ts;
         a.mods = g.mods; a.lambda = 0.0f; a.mod_filter = -1; a.k = kCand; a.self_base = q0; a.part = part;
+        a.uniform_tq = 1;
         a.rows_per_range = rpr; a.n_rranges = nrr; a.n_qblocks = (q + 63) / 64;
         rc = launch_batch_scan(a, s);
         if (rc == MARS_OK) rc = launch_batch_merge(part, nrr, kCand, q, kCand, cand, s);

@@ -55,6 +55,13 @@ __device__ inline void reg_insert(uint64_t (&list)[K], uint64_t x) {
     }
 }
 
+// Ascending order-preserving code of a score (-0.0 folded onto +0.0): a < b as floats
+// iff ord32(a) < ord32(b) as unsigned; 0 is below every score (no bound yet).
+__device__ inline uint32_t ord32(float s) {
+    const uint32_t u = __float_as_uint(s + 0.0f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
 template <int KCH, int K>
 struct BatchLds {
     static constexpr size_t kQBytes = size_t(4) * KCH * 64 * 16;
@@ -68,13 +75,18 @@ __global__ __launch_bounds__(kBWaves * 64) void k_batch_scan(BatchArgs a) {
     __shared__ __attribute__((aligned(16))) unsigned char s_raw[BatchLds<KCH, K>::kBytes];
     u32x4 (*s_q)[KCH][64] = reinterpret_cast<u32x4 (*)[KCH][64]>(s_raw);
     __shared__ float s_stage[kBWaves][kTile][kBQ + 1];  // per-wave score tile (+1: bank spread)
-    __shared__ float s_ts[kBWaves][kTile];
-    __shared__ int32_t s_mod[kBWaves][kTile];
+    __shared__ float s_w[kBWaves][kTile];      // row decay weight (one query time) or row timestamp
+    __shared__ int32_t s_keep[kBWaves][kTile]; // row passes the modality filter
+    // Best known K-th score per query in this workgroup: a wave whose own list is full
+    // publishes its K-th score here; a row scoring strictly below it cannot enter the
+    // workgroup's top-K (K better rows are already held), so no wave keeps it.
+    __shared__ uint32_t s_thr[kBQ];
     const int lane = int(threadIdx.x & 63u), wave = int(threadIdx.x >> 6);
     const int m = lane & 15, kg = lane >> 4;
     const int r_id = int(blockIdx.x) % a.n_rranges;
     const int qb = int(blockIdx.x) / a.n_rranges;
     const int d = KCH * 32;
+    constexpr int H = KCH / 2;                 // k steps per half tile
 
     // stage this block's 64 queries (zero rows past the batch)
     for (int idx = int(threadIdx.x); idx < 4 * KCH * 64; idx += kBWaves * 64) {
@@ -85,40 +97,63 @@ __global__ __launch_bounds__(kBWaves * 64) void k_batch_scan(BatchArgs a) {
             v = *reinterpret_cast<const u32x4*>(a.qh + int64_t(qrow) * d + ks * 32 + (l >> 4) * 8);
         s_q[qt][ks][l] = v;
     }
+    if (threadIdx.x < kBQ) s_thr[threadIdx.x] = 0u;
     __syncthreads();
 
     // lane j owns query (qb*64 + j)
     const int myq = qb * kBQ + lane;
     const bool qvalid = myq < a.q;
     const float tq = qvalid ? a.tq[myq] : 0.0f;
+    const bool uni = a.uniform_tq != 0;
+    const float tq0 = a.tq[0];
     const int64_t self_id = (a.self_base >= 0 && qvalid) ? a.self_base + myq : -1;
     uint64_t list[K];
 #pragma unroll
     for (int j = 0; j < K; ++j) list[j] = kEmptyKey;
+    uint32_t own = 0u;                         // ord32 of list[K-1]'s score once the list is full
 
     const int64_t r0 = int64_t(r_id) * a.rows_per_range;
     const int64_t r1 = (a.n < r0 + a.rows_per_range) ? a.n : r0 + a.rows_per_range;
-    for (int64_t t0 = r0 + int64_t(wave) * kTile; t0 < r1; t0 += int64_t(kBWaves) * kTile) {
-        const int64_t row = t0 + m;
+    const int64_t step = int64_t(kBWaves) * kTile;
+    // row fragments of a half tile (k steps half*H .. half*H + H - 1); the next half's
+    // loads are issued before the current half's MFMAs
+    auto load_half = [&](u32x4 (&b)[H], int64_t t, int half) {
+        const int64_t row = t + m;
         const int64_t rr = row < r1 ? row : r1 - 1;
-        const u32x4* bp = reinterpret_cast<const u32x4*>(a.emb16 + rr * d + kg * 8);
-        u32x4 b[KCH];
+        const u32x4* bp = reinterpret_cast<const u32x4*>(a.emb16 + rr * d + kg * 8) + half * H * 4;
 #pragma unroll
-        for (int ks = 0; ks < KCH; ++ks) b[ks] = __builtin_nontemporal_load(bp + ks * 4);
+        for (int ks = 0; ks < H; ++ks) b[ks] = bp[ks * 4];
+    };
+    u32x4 b0[H], b1[H];
+    int64_t t0 = r0 + int64_t(wave) * kTile;
+    if (t0 < r1) load_half(b0, t0, 0);
+    for (; t0 < r1; t0 += step) {
+        load_half(b1, t0, 1);
         if (lane < kTile) {
             const int64_t rl = (t0 + lane < r1) ? t0 + lane : r1 - 1;
-            s_ts[wave][lane] = a.ts[rl];
-            s_mod[wave][lane] = (a.mod_filter >= 0) ? a.mods[rl] : 0;
+            s_keep[wave][lane] = (a.mod_filter < 0 || a.mods[rl] == a.mod_filter) ? 1 : 0;
+            const float ts = a.ts[rl];
+            s_w[wave][lane] = !uni ? ts : (a.lambda != 0.0f ? expf(-a.lambda * fmaxf(0.0f, tq0 - ts)) : 1.0f);
         }
         f32x4 acc[4];
 #pragma unroll
         for (int qt = 0; qt < 4; ++qt) acc[qt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int ks = 0; ks < KCH; ++ks) {
-            const f16x8 bf = __builtin_bit_cast(f16x8, b[ks]);
+        for (int ks = 0; ks < H; ++ks) {
+            const f16x8 bf = __builtin_bit_cast(f16x8, b0[ks]);
 #pragma unroll
             for (int qt = 0; qt < 4; ++qt) {
                 const f16x8 af = __builtin_bit_cast(f16x8, s_q[qt][ks][lane]);
+                acc[qt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf, acc[qt], 0, 0, 0);
+            }
+        }
+        if (t0 + step < r1) load_half(b0, t0 + step, 0);
+#pragma unroll
+        for (int ks = 0; ks < H; ++ks) {
+            const f16x8 bf = __builtin_bit_cast(f16x8, b1[ks]);
+#pragma unroll
+            for (int qt = 0; qt < 4; ++qt) {
+                const f16x8 af = __builtin_bit_cast(f16x8, s_q[qt][H + ks][lane]);
                 acc[qt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf, acc[qt], 0, 0, 0);
             }
         }
@@ -129,22 +164,28 @@ __global__ __launch_bounds__(kBWaves * 64) void k_batch_scan(BatchArgs a) {
             for (int i = 0; i < 4; ++i) s_stage[wave][m][qt * 16 + 4 * kg + i] = acc[qt][i];
         wave_lds_sync();
         if (qvalid) {
+            uint32_t bound = own > s_thr[lane] ? own : s_thr[lane];
+            const uint32_t own0 = own;
             const int nr = int((r1 - t0) < kTile ? (r1 - t0) : kTile);
-            for (int rr2 = 0; rr2 < nr; ++rr2) {
-                const int64_t id = t0 + rr2;
-                if (id == self_id) continue;
+            for (int j = 0; j < nr; ++j) {
+                // fused score: dot * w (the reference's order), filtered rows -FLT_MAX
                 float s;
-                if (a.mod_filter >= 0 && s_mod[wave][rr2] != a.mod_filter) {
-                    s = -FLT_MAX;
-                } else if (a.lambda != 0.0f) {
-                    const float age = fmaxf(0.0f, tq - s_ts[wave][rr2]);
-                    s = s_stage[wave][rr2][lane] * expf(-a.lambda * age);
-                } else {
-                    s = s_stage[wave][rr2][lane];
+                if (!s_keep[wave][j]) s = -FLT_MAX;
+                else if (uni) s = s_stage[wave][j][lane] * s_w[wave][j];
+                else if (a.lambda != 0.0f) s = s_stage[wave][j][lane] * expf(-a.lambda * fmaxf(0.0f, tq - s_w[wave][j]));
+                else s = s_stage[wave][j][lane];
+                if (ord32(s) >= bound && t0 + j != self_id) {
+                    const uint64_t key = make_key(s, uint32_t(t0 + j));
+                    if (key < list[K - 1]) {
+                        reg_insert<K>(list, key);
+                        if (list[K - 1] != kEmptyKey) {
+                            own = ord32(key_score(list[K - 1]));
+                            bound = bound > own ? bound : own;
+                        }
+                    }
                 }
-                const uint64_t key = make_key(s, uint32_t(id));
-                if (key < list[K - 1]) reg_insert<K>(list, key);
             }
+            if (own > own0) atomicMax(&s_thr[lane], own);
         }
         wave_lds_sync();
     }

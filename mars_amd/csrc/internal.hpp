@@ -333,6 +333,7 @@ struct BatchArgs {
     int64_t rows_per_range;
     int32_t n_rranges;
     int32_t n_qblocks;
+    int32_t uniform_tq;      // all query times equal: one decay weight per row
 };
 bool batch_dim_supported(int32_t d);
 int batch_kpart(int32_t k);  // keys per (query, row range) the scan writes
