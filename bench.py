@@ -49,37 +49,34 @@ def scan_traffic(n: int, d: int):
     return int(kv["traffic_bytes_per_launch"])
 
 
-def tiled_pass(args, mars_amd, corpus, c, qnodes, N, D, K, pctl, lat_resident):
-    """tiled_query contract over a host-RAM (pinned) copy of the corpus: tiles of 250K rows
-    (copy of tile i+1 overlapping the scan of tile i), and one whole-corpus tile."""
+def tiled_pass(args, mars_amd, corpus, c, qnodes, N, D, K, pctl, lat_resident, host_memory):
+    """tiled_query contract over the corpus held in host RAM (pinned when the host grants it):
+    tiles of --tiled-tile rows (the copy of tile i+1 overlaps the scan of tile i)."""
     from mars_amd import TiledQueryConfig
-    bufs = [mars_amd.HostBuffer((N, D), np.float32), mars_amd.HostBuffer((N,), np.int32),
-            mars_amd.HostBuffer((N,), np.float32)]
-    tctx = mars_amd.create_tiled_context(min(N, 250_000), D, 64)
-    res = {}
+    bufs = [mars_amd.HostBuffer((N,), np.int32), mars_amd.HostBuffer((N,), np.float32)]
+    tile = min(N, args.tiled_tile)
+    tctx = mars_amd.create_tiled_context(tile, D, 64)
     try:
-        bufs[0].array[:] = c.embeddings
-        bufs[1].array[:] = c.modalities
-        bufs[2].array[:] = c.timestamps
-        for tile in (min(N, 250_000),):
-            cfg = TiledQueryConfig(tile_size=tile, top_k=K, time_decay_lambda=corpus.DECAY_LAMBDA)
-            tot, x, comp, gbs = [], [], [], []
-            for i, node in enumerate(qnodes[:args.tiled_queries + 1]):
-                st = mars_amd.TiledQueryStats()
-                mars_amd.tiled_query(tctx, bufs[0].array, bufs[1].array, bufs[2].array, c.embeddings[node],
-                                     corpus.QUERY_TIME, cfg, st)
-                if i:                                   # first call warms the copy path
-                    tot.append(st.total_ms); x.append(st.transfer_ms); comp.append(st.compute_ms)
-                    gbs.append(st.h2d_gbs)
-            res = dict(tile_rows=tile, tiles=(N + tile - 1) // tile, queries=len(tot), host_memory="pinned",
-                       total_ms_p50=pctl(tot, .5), total_ms_p99=pctl(tot, .99), transfer_ms_mean=float(np.mean(x)),
-                       compute_ms_mean=float(np.mean(comp)), h2d_gbs_mean=float(np.mean(gbs)),
-                       resident_global_p50_ms=pctl(lat_resident, .5) / 1e3,
-                       speedup_resident_vs_tiled=pctl(tot, .5) / (pctl(lat_resident, .5) / 1e3))
-            log(f"tiled comparator ({res['tiles']} tiles of {tile} rows, pinned host RAM): total p50 "
-                f"{res['total_ms_p50']:.1f} ms (H2D {res['transfer_ms_mean']:.1f} ms at {res['h2d_gbs_mean']:.1f} "
-                f"GB/s, scan {res['compute_ms_mean']:.2f} ms) vs HBM-resident global p50 "
-                f"{pctl(lat_resident, .5) / 1e3:.3f} ms ({res['speedup_resident_vs_tiled']:.0f}x)")
+        bufs[0].array[:] = c.modalities
+        bufs[1].array[:] = c.timestamps
+        cfg = TiledQueryConfig(tile_size=tile, top_k=K, time_decay_lambda=corpus.DECAY_LAMBDA)
+        tot, x, comp, gbs = [], [], [], []
+        for i, node in enumerate(qnodes[:args.tiled_queries + 1]):
+            st = mars_amd.TiledQueryStats()
+            mars_amd.tiled_query(tctx, c.embeddings, bufs[0].array, bufs[1].array, c.embeddings[node],
+                                 corpus.QUERY_TIME, cfg, st)
+            if i:                                       # the first call warms the copy path
+                tot.append(st.total_ms); x.append(st.transfer_ms); comp.append(st.compute_ms)
+                gbs.append(st.h2d_gbs)
+        res = dict(tile_rows=tile, tiles=(N + tile - 1) // tile, queries=len(tot), host_memory=host_memory,
+                   total_ms_p50=pctl(tot, .5), total_ms_p99=pctl(tot, .99), transfer_ms_mean=float(np.mean(x)),
+                   compute_ms_mean=float(np.mean(comp)), h2d_gbs_mean=float(np.mean(gbs)),
+                   resident_global_p50_ms=pctl(lat_resident, .5) / 1e3,
+                   speedup_resident_vs_tiled=pctl(tot, .5) / (pctl(lat_resident, .5) / 1e3))
+        log(f"tiled comparator ({res['tiles']} tiles of {tile} rows, {host_memory} host RAM): total p50 "
+            f"{res['total_ms_p50']:.1f} ms (H2D {res['transfer_ms_mean']:.1f} ms at {res['h2d_gbs_mean']:.1f} "
+            f"GB/s, scan {res['compute_ms_mean']:.2f} ms) vs HBM-resident global p50 "
+            f"{pctl(lat_resident, .5) / 1e3:.3f} ms ({res['speedup_resident_vs_tiled']:.0f}x)")
     finally:
         mars_amd.destroy_tiled_context(tctx)
         for b in bufs:
@@ -155,6 +152,10 @@ def main() -> int:
                     help="nodes inserted during the streaming pass (10-node episodes at 2,000 nodes/s)")
     ap.add_argument("--stream-queries", type=int, default=4000, help="queries of the streaming pass (1,000/s)")
     ap.add_argument("--tiled-queries", type=int, default=8, help="queries of the tiled out-of-core comparator")
+    ap.add_argument("--tiled-tile", type=int, default=250_000, help="rows per tile of the tiled comparator")
+    ap.add_argument("--knn-k", type=int, default=8,
+                    help="nearest neighbours per node in the NSN graph (0: intra-episode pairs only)")
+    ap.add_argument("--batch-q", type=int, default=64, help="queries per batched MFMA scoring call")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU; --gpus above 1 is not supported here "
@@ -169,7 +170,15 @@ def main() -> int:
     N, D, K = args.n, args.dim, 10
     M = 0 if args.profile_only else max(0, args.stream_nodes) // 10 * 10     # whole 10-node episodes
     t = time.time()
-    full = corpus.make_corpus(N + M, D, seed=args.seed)      # the generator is prefix-stable: rows >= N arrive later
+    # rows in pinned host memory when the host grants it (uploaded once, streamed again by the
+    # tiled comparator), otherwise pageable
+    try:
+        host_rows = mars_amd.HostBuffer((N + M, D), np.float32)
+    except mars_amd.MarsError as e:
+        log(f"pinned host rows unavailable ({e}); using pageable memory")
+        host_rows = None
+    full = corpus.make_corpus(N + M, D, seed=args.seed,               # prefix-stable: rows >= N arrive later
+                              out_emb=host_rows.array if host_rows else None)
     c = corpus.Corpus(full.embeddings[:N], full.modalities[:N], full.timestamps[:N], full.episode_ids[:N], args.seed)
     log(f"corpus N={N} D={D} seed={args.seed} (+{M} streamed): {time.time() - t:.1f}s")
     t = time.time()
@@ -178,8 +187,12 @@ def main() -> int:
     mars_amd.upload_fp16_embeddings(dg)
     log(f"upload + fp16 copy: {time.time() - t:.1f}s")
     t = time.time()
-    knn = mars_amd.graph_knn(dg, corpus.KNN_K)          # fp16 MFMA candidates + exact fp32 rescoring
-    log(f"8-NN on the GPU: {time.time() - t:.1f}s")
+    if args.knn_k > 0:
+        knn = mars_amd.graph_knn(dg, args.knn_k)       # fp16 MFMA candidates + exact fp32 rescoring
+        log(f"{args.knn_k}-NN on the GPU: {time.time() - t:.1f}s")
+    else:
+        knn = np.empty((N, 0), np.int32)
+        log("NSN graph without k-NN edges (intra-episode pairs only)")
     t = time.time()
     corpus.nsn_graph(c, knn)
     mars_amd.set_csr(dg, c.row_offsets, c.col_indices)
@@ -286,7 +299,7 @@ def main() -> int:
             f"{kern_h.mean():.1f} us ({bytes_f16 / kern_h.mean() / 1e3:.0f} GB/s)")
         # ---- batched Q=64 global scoring on MFMA fp16 tiles
         ctx.timing = True
-        B, reps = 64, 30
+        B, reps = args.batch_q, 30
         bl, bk = [], []
         for r in range(reps + 3):
             st = mars_amd.RetrievalStats()
@@ -298,11 +311,11 @@ def main() -> int:
         ctx.timing = False
         bkm = float(np.mean(bk))
         flops = 2.0 * B * N * D
-        out["batch_q64_fp16"] = dict(p50_us=pctl(bl, .5), p99_us=pctl(bl, .99), queries_per_s=B / (pctl(bl, .5) / 1e6),
+        out[f"batch_q{B}_fp16"] = dict(p50_us=pctl(bl, .5), p99_us=pctl(bl, .99), queries_per_s=B / (pctl(bl, .5) / 1e6),
                                      scan_kernel_mean_us=bkm, tflops=flops / bkm / 1e6,
                                      mfma_util=flops / bkm / 1e6 / 2500.0,
                                      hbm_gbs=bytes_f16 / bkm / 1e3, hbm_frac=bytes_f16 / bkm / 1e3 / HBM_PEAK_GBS)
-        log(f"batch Q=64: p50 {pctl(bl, .5):.0f} us; scan {bkm:.0f} us = {flops / bkm / 1e6:.0f} TFLOP/s "
+        log(f"batch Q={B}: p50 {pctl(bl, .5):.0f} us; scan {bkm:.0f} us = {flops / bkm / 1e6:.0f} TFLOP/s "
             f"({flops / bkm / 1e6 / 25:.1f}% of 2.5 PF), {bytes_f16 / bkm / 1e3:.0f} GB/s")
         out["episode"] = dict(p50_us=pctl(lat_e, .5), p99_us=pctl(lat_e, .99), qps=S / wall_e,
                               kernel_mean_us=float(kern_e.mean()),
@@ -313,7 +326,8 @@ def main() -> int:
                                   scan_frac=bytes_f16 / float(kern_h.mean()) / 1e3 / HBM_PEAK_GBS)
 
     if not args.profile_only and args.tiled_queries > 0:
-        out["tiled_comparator"] = tiled_pass(args, mars_amd, corpus, c, qnodes[W:], N, D, K, pctl, lat_g)
+        out["tiled_comparator"] = tiled_pass(args, mars_amd, corpus, c, qnodes[W:], N, D, K, pctl, lat_g,
+                                             "pinned" if host_rows else "pageable")
     if M > 0 and args.stream_queries > 0:
         out["streaming"] = stream_pass(args, mars_amd, corpus, lib, check, RetrievalConfigC, full, dg, ctx, dq,
                                        qnodes, ep_cfgs, gcfg, N, D, M, pctl)
@@ -332,10 +346,12 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic",
-        "config": {"workload": "global Q=1 decay+top-K+depth-2 BFS over N=1M D=768 fp32, K=10 (episode-scoped and "
-                               "fp16 global reported alongside)",
+        "config": {"workload": f"global Q=1 decay+top-K+depth-2 BFS over N={N:,} D={D} fp32, K={K} (episode-scoped "
+                               f"and fp16 global reported alongside)",
                    "num_nodes": N, "dim": D, "top_k": K, "bfs_hops": 2, "decay_lambda": corpus.DECAY_LAMBDA,
-                   "corpus_seed": args.seed, "query_seed": args.query_seed, "num_edges": int(len(c.col_indices))},
+                   "corpus_seed": args.seed, "query_seed": args.query_seed, "num_edges": int(len(c.col_indices)),
+                   "nsn_graph": (f"intra-episode pairs + {args.knn_k}-NN" if args.knn_k > 0 else
+                                 "intra-episode pairs only (k-NN edges omitted)")},
         "global_fp32": dict(p50_us=pctl(lat_g, .5), p99_us=pctl(lat_g, .99), qps=S / wall_g,
                             p99_us_with_events=pctl(lat_gk, .99),
                             graph_replay=dict(p50_us=pctl(lat_gg, .5), p99_us=pctl(lat_gg, .99)),
@@ -367,6 +383,9 @@ def main() -> int:
     dq.free()
     mars_amd.destroy_query_context(ctx)
     mars_amd.free_device(dg)
+    del c, full
+    if host_rows:
+        host_rows.free()
     print(json.dumps(res), flush=True)
     return 0
 

@@ -42,10 +42,18 @@ def _p(a: np.ndarray):
     return C.c_void_p(a.ctypes.data)
 
 
-def make_corpus(n: int, dim: int = 768, seed: int = 2026, threads: int = 0, embeddings: bool = True) -> Corpus:
+def make_corpus(n: int, dim: int = 768, seed: int = 2026, threads: int = 0, embeddings: bool = True,
+                out_emb: Optional[np.ndarray] = None) -> Corpus:
+    """Seeded corpus of the benchmark generator; out_emb (an (n, dim) float32 C-contiguous
+    array, e.g. a pinned HostBuffer view) receives the rows instead of a new array."""
     p = CorpusParamsC()
     lib.mars_corpus_default(C.byref(p), int(n), int(dim), int(seed))
-    emb = np.empty((n, dim) if embeddings else (0, dim), np.float32)
+    if out_emb is not None:
+        if out_emb.shape != (n, dim) or out_emb.dtype != np.float32 or not out_emb.flags.c_contiguous:
+            raise ValueError("out_emb must be a C-contiguous float32 array of shape (n, dim)")
+        emb = out_emb
+    else:
+        emb = np.empty((n, dim) if embeddings else (0, dim), np.float32)
     mods = np.empty(n, np.int32)
     ts = np.empty(n, np.float32)
     ep = np.empty(n, np.int32)

@@ -289,8 +289,7 @@ __global__ void k_f32_to_f16_rows(const float* __restrict__ in, __half* __restri
 template <int KCH, int K>
 int launch_batch_t(const BatchArgs& a, hipStream_t s) {
     const unsigned grid = unsigned(a.n_rranges * a.n_qblocks);
-    hipLaunchKernelGGL((k_batch_scan<KCH, K>), dim3(grid), dim3(kBWaves * 64), 0, s, a);
-    MARS_HIP(hipGetLastError());
+    MARS_LAUNCH((k_batch_scan<KCH, K>), dim3(grid), dim3(kBWaves * 64), 0, s, a);
     return MARS_OK;
 }
 
@@ -318,25 +317,22 @@ int launch_batch_scan(const BatchArgs& a, hipStream_t s) {
 
 int launch_batch_merge(const uint64_t* part, int32_t n_rranges, int32_t kpart, int32_t q, int32_t k_out,
                        uint64_t* out, hipStream_t s) {
-    hipLaunchKernelGGL(k_batch_merge, dim3(unsigned(q)), dim3(64), 0, s, part, n_rranges, kpart, q, k_out, out);
-    MARS_HIP(hipGetLastError());
+    MARS_LAUNCH(k_batch_merge, dim3(unsigned(q)), dim3(64), 0, s, part, n_rranges, kpart, q, k_out, out);
     return MARS_OK;
 }
 
 int launch_knn_rerank(const float* emb, int64_t q0, int64_t nq, int32_t d, const uint64_t* cand, int32_t kc,
                       int32_t k_out, int32_t* nbrs, hipStream_t s) {
     const int64_t threads = nq * 16;
-    hipLaunchKernelGGL(k_knn_rerank, dim3(unsigned((threads + 255) / 256)), dim3(256), 0, s, emb, q0, nq, d, cand, kc,
+    MARS_LAUNCH(k_knn_rerank, dim3(unsigned((threads + 255) / 256)), dim3(256), 0, s, emb, q0, nq, d, cand, kc,
                        k_out, nbrs);
-    MARS_HIP(hipGetLastError());
     return MARS_OK;
 }
 
 int launch_f32_to_f16_rows(const float* in, __half* out, int64_t count, hipStream_t s) {
     int64_t blocks = (count + 255) / 256;
     if (blocks > 4096) blocks = 4096;
-    hipLaunchKernelGGL(k_f32_to_f16_rows, dim3(unsigned(blocks)), dim3(256), 0, s, in, out, count);
-    MARS_HIP(hipGetLastError());
+    MARS_LAUNCH(k_f32_to_f16_rows, dim3(unsigned(blocks)), dim3(256), 0, s, in, out, count);
     return MARS_OK;
 }
 

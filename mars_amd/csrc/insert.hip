@@ -422,10 +422,8 @@ extern "C" int mars_graph_insert(mars_graph* gh, int32_t n_new, const float* emb
     pa.app = reinterpret_cast<const int64_t*>(dev + o_app); pa.n_app = int32_t(app.size() / 2);
     pa.rows = reinterpret_cast<const int64_t*>(dev + o_rows); pa.n_rows = int32_t(rows.size() / 3);
     const int64_t data_work = std::max<int64_t>({int64_t(pa.n_reloc) * 64, pa.n_tail, int64_t(pa.n_app)});
-    hipLaunchKernelGGL(k_patch_data, dim3(patch_grid(data_work)), dim3(256), 0, s, pa);
-    MARS_HIP(hipGetLastError());
-    hipLaunchKernelGGL(k_patch_rows, dim3(patch_grid(pa.n_rows)), dim3(256), 0, s, pa);
-    MARS_HIP(hipGetLastError());
+    MARS_LAUNCH(k_patch_data, dim3(patch_grid(data_work)), dim3(256), 0, s, pa);
+    MARS_LAUNCH(k_patch_rows, dim3(patch_grid(pa.n_rows)), dim3(256), 0, s, pa);
     MARS_HIP(hipStreamSynchronize(s));
     for (size_t i = 0; i < rows.size(); i += 3) {
         g.ro_h[size_t(rows[i])] = rows[i + 1];

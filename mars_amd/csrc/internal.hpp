@@ -39,6 +39,17 @@ int set_error(int code, const char* fmt, ...);
         if (!(cond)) return ::mars::set_error((code), __VA_ARGS__);                  \
     } while (0)
 
+// Launch a kernel and report this launch's own error only. The thread's last-error
+// state can still hold an error that an earlier HIP call recovered from by itself (a
+// large pageable copy whose source the runtime failed to pin, then staged), which a
+// bare hipGetLastError after the launch would report as the launch's.
+#define MARS_LAUNCH(...)                  \
+    do {                                  \
+        (void)hipGetLastError();          \
+        hipLaunchKernelGGL(__VA_ARGS__);  \
+        MARS_HIP(hipGetLastError());      \
+    } while (0)
+
 #define MARS_TRY(expr)                    \
     do {                                  \
         int rc__ = (expr);                \

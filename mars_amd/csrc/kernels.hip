@@ -1030,20 +1030,17 @@ int launch_scan(const ScanArgs& a, hipStream_t s) {
 }
 
 int launch_tile_merge(uint64_t* part, uint32_t* gcnt, uint64_t* carry, int32_t k, hipStream_t s) {
-    hipLaunchKernelGGL(k_tile_merge, dim3(1), dim3(256), 0, s, part, gcnt, carry, k);
-    MARS_HIP(hipGetLastError());
+    MARS_LAUNCH(k_tile_merge, dim3(1), dim3(256), 0, s, part, gcnt, carry, k);
     return MARS_OK;
 }
 
 int launch_finalize(const FinalizeArgs& a, hipStream_t s) {
-    hipLaunchKernelGGL(k_finalize, dim3(1), dim3(kFinThreads), 0, s, a);
-    MARS_HIP(hipGetLastError());
+    MARS_LAUNCH(k_finalize, dim3(1), dim3(kFinThreads), 0, s, a);
     return MARS_OK;
 }
 
 int launch_episode(const EpisodeArgs& a, hipStream_t s) {
-    hipLaunchKernelGGL(k_episode, dim3(1), dim3(256), 0, s, a);
-    MARS_HIP(hipGetLastError());
+    MARS_LAUNCH(k_episode, dim3(1), dim3(256), 0, s, a);
     return MARS_OK;
 }
 
@@ -1051,8 +1048,7 @@ int launch_convert_f16(const float* in, __half* out, int64_t count, hipStream_t 
     int64_t blocks = (count / 8 + 255) / 256;
     if (blocks < 1) blocks = 1;
     if (blocks > 65536) blocks = 65536;
-    hipLaunchKernelGGL(k_convert_f16, dim3(unsigned(blocks)), dim3(256), 0, s, in, out, count);
-    MARS_HIP(hipGetLastError());
+    MARS_LAUNCH(k_convert_f16, dim3(unsigned(blocks)), dim3(256), 0, s, in, out, count);
     return MARS_OK;
 }
 
