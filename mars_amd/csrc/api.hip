@@ -324,13 +324,16 @@ int query_impl(const mars_graph* gh, mars_ctx* ch, const float* h_q, const float
 // Row ranges x query blocks for the batched scan: one 512-thread workgroup per CU
 // (256 CUs), all query blocks of a row range on one XCD.
 void batch_grid(int64_t n, int32_t q, int32_t* n_rranges, int32_t* n_qblocks, int64_t* rows_per_range) {
+    // n_qblocks counts 64-query blocks (the layout of the partial keys) for both kernels
     const int32_t qblocks = (q + 63) / 64;
-    int32_t rr = std::max(8, (256 / std::max(qblocks, 1)) / 8 * 8);
-    const int64_t max_rr = std::max<int64_t>(1, (n + 15) / 16);      // at least one tile per range
+    const bool gemm = batch_uses_gemm(q);
+    const int32_t tiles = gemm ? (q + 255) / 256 : qblocks;       // workgroups per row range
+    const int64_t align = gemm ? 64 : 16;                          // rows per tile
+    int32_t rr = std::max(8, (256 / std::max(tiles, 1)) / 8 * 8);
+    const int64_t max_rr = std::max<int64_t>(1, (n + align - 1) / align);   // at least one tile per range
     if (rr > max_rr) rr = int32_t(max_rr);
-    *n_rranges = rr;
     *n_qblocks = qblocks;
-    *rows_per_range = ((n + rr - 1) / rr + 15) / 16 * 16;
+    *rows_per_range = ((n + rr - 1) / rr + align - 1) / align * align;
     *n_rranges = int32_t((n + *rows_per_range - 1) / *rows_per_range);
 }
 

@@ -362,7 +362,8 @@ def test_batch_parity_q64(dev10k, corpus_10k):
     _batch_check(dev10k, qn, RetrievalConfig(top_k=10, time_decay_lambda=LAM), T_Q, corpus_10k.embeddings)
 
 
-@pytest.mark.parametrize("q,k,filt", [(1, 10, -1), (200, 16, -1), (130, 5, 1), (64, 16, 2)])
+@pytest.mark.parametrize("q,k,filt", [(1, 10, -1), (200, 16, -1), (130, 5, 1), (64, 16, 2), (520, 16, -1),
+                                       (600, 10, 2)])
 def test_batch_parity_shapes(dev10k, corpus_10k, q, k, filt, rng):
     qn = corpus.pick_queries(corpus_10k.modalities, q, seed=q)
     tq = rng.uniform(400, 600, size=q).astype(np.float32)             # per-query times
