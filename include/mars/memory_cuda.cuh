@@ -51,6 +51,8 @@ struct DeviceMemoryGraph {
 };
 
 DeviceMemoryGraph upload_to_device(const MemoryGraph& h);
+// Extension: reserve room for capacity_nodes nodes (streaming inserts, mars/streaming.h).
+DeviceMemoryGraph upload_to_device(const MemoryGraph& h, int32_t capacity_nodes);
 void free_device(DeviceMemoryGraph& d);
 void upload_episode_ids(DeviceMemoryGraph& dg, const int32_t* host_episode_ids, int32_t num_ids);
 void upload_episode_csr(DeviceMemoryGraph& dg, const HostEpisodeCSR& csr);

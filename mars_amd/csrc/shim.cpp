@@ -8,10 +8,13 @@
 // ============================================================================
 #include "mars/memory_cuda.cuh"
 #include "mars/memory_graph.h"
+#include "mars/streaming.h"
+#include "mars/tiled_query.h"
 #include "mars_amd.h"
 #include "mars_corpus.h"
 
 #include <algorithm>
+#include <chrono>
 #include <cstdio>
 #include <cstdlib>
 
@@ -74,8 +77,11 @@ HostEpisodeCSR build_episode_csr(const std::vector<int32_t>& episode_ids, int32_
     return out;
 }
 
-DeviceMemoryGraph upload_to_device(const MemoryGraph& h) {
+DeviceMemoryGraph upload_to_device(const MemoryGraph& h) { return upload_to_device(h, 0); }
+
+DeviceMemoryGraph upload_to_device(const MemoryGraph& h, int32_t capacity_nodes) {
     mars_graph_desc desc{};
+    desc.capacity_nodes = capacity_nodes;
     desc.num_nodes = h.num_nodes;
     desc.num_edges = int32_t(h.col_indices.size());
     desc.embedding_dim = h.embedding_dim;
@@ -176,4 +182,129 @@ std::vector<QueryResult> query_memory(const DeviceMemoryGraph& dg, const float* 
     std::vector<QueryResult> r = query_memory_fast(dg, ctx, h_query, query_timestamp, cfg, stats);
     destroy_query_context(ctx);
     return r;
+}
+
+// ---- tiled out-of-core query (include/tiled_query.h:79-102) --------------------------
+
+TiledQueryContext create_tiled_context(int32_t max_tile_size, int32_t embedding_dim, int32_t max_k) {
+    TiledQueryContext ctx;
+    die_on(mars_tiled_ctx_create(max_tile_size, embedding_dim, max_k, &ctx.handle), "create_tiled_context");
+    ctx.max_tile_size = max_tile_size;
+    ctx.embedding_dim = embedding_dim;
+    ctx.max_k = std::min(max_k, 64);
+    ctx.valid = true;
+    return ctx;
+}
+
+void destroy_tiled_context(TiledQueryContext& ctx) {
+    if (!ctx.valid) return;
+    mars_tiled_ctx_destroy(ctx.handle);
+    ctx = TiledQueryContext{};
+}
+
+std::vector<TiledQueryResult> tiled_query(TiledQueryContext& ctx, const float* h_embeddings,
+                                          const int32_t* h_modalities, const float* h_timestamps, int32_t N,
+                                          int32_t D, const float* h_query, float query_timestamp,
+                                          const TiledQueryConfig& cfg, TiledQueryStats& stats) {
+    mars_tiled_config c;
+    c.tile_size = cfg.tile_size;
+    c.top_k = cfg.top_k;
+    c.time_decay_lambda = cfg.time_decay_lambda;
+    c.modality_filter = cfg.modality_filter;
+    c.use_fp16 = cfg.use_fp16 ? 1 : 0;
+    std::vector<mars_tiled_result> buf(static_cast<size_t>(std::max(1, cfg.top_k)));
+    int32_t n = 0;
+    mars_tiled_stats st{};
+    die_on(mars_tiled_query(ctx.handle, h_embeddings, h_modalities, h_timestamps, N, D, h_query, query_timestamp, &c,
+                            buf.data(), int32_t(buf.size()), &n, &st),
+           "tiled_query");
+    std::vector<TiledQueryResult> out;
+    for (int32_t i = 0; i < std::min<int32_t>(n, int32_t(buf.size())); ++i)
+        out.push_back({buf[size_t(i)].node_id, buf[size_t(i)].score, buf[size_t(i)].modality});
+    stats.total_nodes = st.total_nodes;
+    stats.num_tiles = st.num_tiles;
+    stats.total_ms = st.total_ms;
+    stats.transfer_ms = st.transfer_ms;
+    stats.compute_ms = st.compute_ms;
+    stats.merge_ms = st.merge_ms;
+    return out;
+}
+
+// ---- streaming insert buffer (include/streaming.h:42-81) ------------------------------
+
+StreamingBuffer::StreamingBuffer(const StreamingConfig& cfg) : cfg_(cfg) {
+    buffer_.reserve(size_t(std::max(cfg.capacity, 0)));
+}
+
+bool StreamingBuffer::insert(int32_t id, int32_t modality, float timestamp, const float* embedding,
+                             int32_t episode_id) {
+    std::lock_guard<std::mutex> lock(mu_);
+    if (int32_t(buffer_.size()) >= cfg_.capacity) return false;      // streaming.cpp:15-21
+    StagedNode n;
+    n.id = id;
+    n.modality = modality;
+    n.timestamp = timestamp;
+    n.embedding.assign(embedding, embedding + cfg_.embedding_dim);
+    n.episode_id = episode_id;
+    buffer_.push_back(std::move(n));
+    return true;
+}
+
+bool StreamingBuffer::insert(const StagedNode& node) {
+    return insert(node.id, node.modality, node.timestamp, node.embedding.data(), node.episode_id);
+}
+
+FlushStats StreamingBuffer::flush(DeviceMemoryGraph& target) {
+    std::lock_guard<std::mutex> lock(mu_);
+    FlushStats stats;
+    if (buffer_.empty() || !target.handle) return stats;
+    const int32_t n = int32_t(buffer_.size());
+    const int32_t d = cfg_.embedding_dim;
+    if (d != target.embedding_dim) {
+        std::fprintf(stderr, "StreamingBuffer::flush: embedding_dim %d, graph has %d\n", d, target.embedding_dim);
+        std::exit(EXIT_FAILURE);
+    }
+    std::vector<float> rows(size_t(n) * size_t(d));
+    std::vector<int32_t> mods(static_cast<size_t>(n)), eps(static_cast<size_t>(n));
+    std::vector<float> ts(static_cast<size_t>(n));
+    bool with_eps = target.d_episode_ids != nullptr;
+    for (int32_t i = 0; i < n; ++i) {
+        const StagedNode& s = buffer_[size_t(i)];
+        if (s.id != target.num_nodes + i) {
+            std::fprintf(stderr, "StreamingBuffer::flush: staged id %d, the graph's next id is %d\n", s.id,
+                         target.num_nodes + i);
+            std::exit(EXIT_FAILURE);
+        }
+        std::copy(s.embedding.begin(), s.embedding.end(), rows.begin() + int64_t(i) * d);
+        mods[size_t(i)] = s.modality;
+        ts[size_t(i)] = s.timestamp;
+        eps[size_t(i)] = s.episode_id;
+    }
+    mars_insert_stats st{};
+    die_on(mars_graph_insert(target.handle, n, rows.data(), mods.data(), ts.data(), with_eps ? eps.data() : nullptr,
+                             cfg_.nsn_k, nullptr, &st),
+           "StreamingBuffer::flush");
+    refresh_view(target);
+    stats.nodes_committed = st.nodes_added;
+    stats.edges_added = int32_t(std::min<int64_t>(st.edges_added, INT32_MAX));
+    stats.flush_ms = float(st.linked_us / 1000.0);
+    stats.queryable_ms = float(st.queryable_us / 1000.0);
+    total_flushed_ += n;
+    buffer_.clear();
+    return stats;
+}
+
+int32_t StreamingBuffer::staged_count() const {
+    std::lock_guard<std::mutex> lock(mu_);
+    return int32_t(buffer_.size());
+}
+
+int64_t StreamingBuffer::total_flushed() const {
+    std::lock_guard<std::mutex> lock(mu_);
+    return total_flushed_;
+}
+
+void StreamingBuffer::reset() {
+    std::lock_guard<std::mutex> lock(mu_);
+    buffer_.clear();
 }

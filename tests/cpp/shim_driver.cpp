@@ -3,12 +3,21 @@
 //  API (the calls of demos/embodied_scene/bench_kids_sweep.cu:589-680), built
 //  against include/mars/ and linked with libmars_amd.so.
 //
-//  usage: shim_driver host            host-only checks (no GPU): T19 episode CSR
+//  usage: shim_driver host            host-only checks (no GPU): T19 episode CSR,
+//                                     T16 streaming capacity
 //         shim_driver query N SEED Q  N-node benchmark corpus; prints one line per
 //                                     query: "<scope> <node> id:score:mod:hops ..."
+//         shim_driver stream N SEED   StreamingBuffer flush of the next 10-node episode
+//                                     onto N nodes (T15), then one global query from an
+//                                     inserted node at its own timestamp: "flush ..."
+//                                     and "global ..." lines
+//         shim_driver tiled N SEED Q  tiled_query over the host corpus (tiles of N/7):
+//                                     "tiled <node> id:score:mod ..."
 // ============================================================================
 #include "mars/memory_cuda.cuh"
 #include "mars/memory_graph.h"
+#include "mars/streaming.h"
+#include "mars/tiled_query.h"
 #include "mars_corpus.h"
 
 #include <cstdio>
@@ -33,12 +42,130 @@ static int host_checks() {
         if (seen[i] != 1) { std::printf("FAIL member %d\n", i); return 1; }
     HostEpisodeCSR bad = build_episode_csr(ids, 31);
     if (bad.num_episodes != 0) { std::printf("FAIL size mismatch\n"); return 1; }
+    // T16 (tests/test_memory_graph.cpp:364-377): the sixth insert into a 5-node buffer fails
+    StreamingConfig sc;
+    sc.capacity = 5;
+    sc.embedding_dim = 32;
+    sc.auto_flush = false;
+    StreamingBuffer buf(sc);
+    std::vector<float> emb(32, 0.5f);
+    for (int i = 0; i < 5; ++i)
+        if (!buf.insert(i, MOD_AUDIO, 1.0f, emb.data())) { std::printf("FAIL insert %d\n", i); return 1; }
+    if (buf.insert(5, MOD_AUDIO, 1.0f, emb.data()) || buf.staged_count() != 5) {
+        std::printf("FAIL capacity\n");
+        return 1;
+    }
+    buf.reset();
+    if (buf.staged_count() != 0) { std::printf("FAIL reset\n"); return 1; }
     std::printf("host ok\n");
+    return 0;
+}
+
+static void make_corpus(int32_t N, int32_t D, uint64_t seed, MemoryGraph& g, std::vector<int32_t>& ep) {
+    g.num_nodes = N;
+    g.embedding_dim = D;
+    g.embeddings.resize(size_t(N) * D);
+    g.modalities.resize(size_t(N));
+    g.timestamps.resize(size_t(N));
+    ep.resize(size_t(N));
+    mars_corpus_params p;
+    mars_corpus_default(&p, N, D, seed);
+    mars_corpus_generate(&p, g.embeddings.data(), g.modalities.data(), g.timestamps.data(), ep.data(), 0);
+}
+
+static void print_results(const char* tag, int32_t node, const std::vector<QueryResult>& res, const char* tail) {
+    std::printf("%s %d", tag, node);
+    for (const QueryResult& r : res) std::printf(" %d:%.9g:%d:%d", r.node_id, r.score, r.modality, r.hops_from_seed);
+    std::printf(" | %s\n", tail);
+}
+
+// T15 (tests/test_memory_graph.cpp:339-362) against the device graph: N nodes of the
+// benchmark corpus (episode pairs only), then the next episode streamed in.
+static int stream_check(int32_t N, uint64_t seed) {
+    const int32_t D = 768;
+    MemoryGraph full;
+    std::vector<int32_t> ep;
+    make_corpus(N + 10, D, seed, full, ep);
+    MemoryGraph g;
+    g.num_nodes = N;
+    g.embedding_dim = D;
+    g.embeddings.assign(full.embeddings.begin(), full.embeddings.begin() + int64_t(N) * D);
+    g.modalities.assign(full.modalities.begin(), full.modalities.begin() + N);
+    g.timestamps.assign(full.timestamps.begin(), full.timestamps.begin() + N);
+    std::vector<int32_t> ep0(ep.begin(), ep.begin() + N);
+    HostEpisodeCSR csr = build_episode_csr(ep0, N);
+    // NSN CSR: intra-episode pairs
+    g.row_offsets.assign(size_t(N) + 1, 0);
+    for (int32_t i = 0; i < N; ++i) {
+        const int32_t e = ep0[size_t(i)];
+        for (int32_t m = csr.ep_csr_offsets[size_t(e)]; m < csr.ep_csr_offsets[size_t(e) + 1]; ++m)
+            if (csr.ep_csr_members[size_t(m)] != i) g.col_indices.push_back(csr.ep_csr_members[size_t(m)]);
+        g.row_offsets[size_t(i) + 1] = int32_t(g.col_indices.size());
+    }
+    g.num_edges = int32_t(g.col_indices.size());
+    DeviceMemoryGraph dg = upload_to_device(g, N + 10);
+    upload_episode_ids(dg, ep0.data(), N);
+    upload_episode_csr(dg, csr);
+    upload_fp16_embeddings(dg);
+    StreamingConfig sc;
+    sc.capacity = 64;
+    sc.embedding_dim = D;
+    StreamingBuffer buf(sc);
+    for (int32_t i = 0; i < 10; ++i)
+        if (!buf.insert(N + i, full.modalities[size_t(N + i)], full.timestamps[size_t(N + i)],
+                        &full.embeddings[size_t(N + i) * D], ep[size_t(N + i)])) {
+            std::printf("FAIL insert\n");
+            return 1;
+        }
+    const int32_t edges0 = dg.num_edges;
+    FlushStats fs = buf.flush(dg);
+    std::printf("flush committed=%d edges_added=%d nodes=%d edges=%d staged=%d total=%lld\n", fs.nodes_committed,
+                fs.edges_added, dg.num_nodes, dg.num_edges - edges0, buf.staged_count(),
+                (long long)buf.total_flushed());
+    QueryContext ctx = create_query_context(N + 10, D, 64);
+    RetrievalConfig cfg;
+    cfg.top_k = 10;
+    cfg.time_decay_lambda = 0.1f;
+    RetrievalStats st;
+    const int32_t node = N + 2;
+    // query time = the node's own timestamp: it, and every newer node, is undecayed
+    auto res = query_memory_fast(dg, ctx, &full.embeddings[size_t(node) * D], full.timestamps[size_t(node)], cfg, st);
+    print_results("global", node, res, "");
+    destroy_query_context(ctx);
+    free_device(dg);
+    return 0;
+}
+
+static int tiled_check(int32_t N, uint64_t seed, int32_t Q) {
+    const int32_t D = 768;
+    MemoryGraph g;
+    std::vector<int32_t> ep;
+    make_corpus(N, D, seed, g, ep);
+    const int32_t tile = (N + 6) / 7;
+    TiledQueryContext ctx = create_tiled_context(tile, D, 64);
+    TiledQueryConfig cfg;
+    cfg.tile_size = tile;
+    cfg.top_k = 10;
+    cfg.time_decay_lambda = 0.1f;
+    for (int32_t qi = 0; qi < Q; ++qi) {
+        const int32_t node = (qi * 7919) % N;
+        TiledQueryStats st;
+        auto res = tiled_query(ctx, g.embeddings.data(), g.modalities.data(), g.timestamps.data(), N, D,
+                               &g.embeddings[size_t(node) * D], 600.0f, cfg, st);
+        std::printf("tiled %d", node);
+        for (const TiledQueryResult& r : res) std::printf(" %d:%.9g:%d", r.node_id, r.score, r.modality);
+        std::printf(" | tiles=%d\n", st.num_tiles);
+    }
+    destroy_tiled_context(ctx);
     return 0;
 }
 
 int main(int argc, char** argv) {
     if (argc >= 2 && std::strcmp(argv[1], "host") == 0) return host_checks();
+    if (argc >= 4 && std::strcmp(argv[1], "stream") == 0)
+        return stream_check(std::atoi(argv[2]), std::strtoull(argv[3], nullptr, 10));
+    if (argc >= 5 && std::strcmp(argv[1], "tiled") == 0)
+        return tiled_check(std::atoi(argv[2]), std::strtoull(argv[3], nullptr, 10), std::atoi(argv[4]));
     if (argc < 5 || std::strcmp(argv[1], "query") != 0) {
         std::fprintf(stderr, "usage: shim_driver host | query N SEED Q\n");
         return 2;

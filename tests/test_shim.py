@@ -48,3 +48,54 @@ def test_shim_driver_matches_oracle():
             assert abs(got[1] - w[1]) <= 1e-5 * max(1.0, abs(w[1]))
         assert ("scanned=10 " in tail) == (scope == "episode")
         assert ("waves=0" in tail) == (scope == "episode")
+
+
+@pytest.mark.gpu
+def test_shim_streaming_buffer_flush():
+    """StreamingBuffer (mars/streaming.h) committing one 10-node episode into the device
+    graph (T15: nodes committed, edges added, buffer empty); queried at its own
+    timestamp, the inserted node is then its own best match and finds its episode's
+    other IMAGE nodes."""
+    from mars_amd import corpus
+    n, seed = 3000, 5
+    r = subprocess.run([str(DRIVER), "stream", str(n), str(seed)], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr
+    flush = next(ln for ln in r.stdout.splitlines() if ln.startswith("flush"))
+    kv = dict(p.split("=") for p in flush.split()[1:])
+    assert int(kv["committed"]) == 10 and int(kv["nodes"]) == n + 10
+    assert int(kv["edges_added"]) == int(kv["edges"]) > 10 * 9
+    assert int(kv["staged"]) == 0 and int(kv["total"]) == 10
+    line = next(ln for ln in r.stdout.splitlines() if ln.startswith("global"))
+    head = line.split(" | ")[0].split()
+    node = int(head[1])
+    res = [tuple(p.split(":")) for p in head[2:]]
+    assert int(res[0][0]) == node and int(res[0][3]) == 0
+    ep = corpus.make_corpus(n + 10, 768, seed=seed).episode_ids
+    peers = {int(x[0]) for x in res if ep[int(x[0])] == ep[node]}
+    assert len(peers) >= 4
+
+
+@pytest.mark.gpu
+def test_shim_tiled_query_matches_oracle():
+    import oracle
+    from mars_amd import corpus
+    n, seed, q = 20000, 3, 4
+    r = subprocess.run([str(DRIVER), "tiled", str(n), str(seed), str(q)], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr
+    c = corpus.make_corpus(n, 768, seed=seed)
+    og = oracle.make_graph(c.embeddings, c.modalities, c.timestamps)
+    tile = (n + 6) // 7
+    lines = [ln for ln in r.stdout.splitlines() if ln.startswith("tiled")]
+    assert len(lines) == q
+    for ln in lines:
+        head, tail = ln.split(" | ")
+        assert tail.strip() == "tiles=7"
+        parts = head.split()
+        node = int(parts[1])
+        got = [(int(a), float(b), int(m)) for a, b, m in (p.split(":") for p in parts[2:])]
+        ids, sc = oracle.tiled_query(og, c.embeddings[node], 600.0, 0.1, 10, tile)
+        fin, scale = oracle.scores(og, c.embeddings[node], 600.0, 0.1)
+        assert [g[0] for g in got] == ids.tolist() or all(
+            abs(fin[a] - fin[b]) <= 2e-5 * max(scale[a], 1e-30) for a, b in zip([g[0] for g in got], ids))
+        for (i, s, m), w in zip(got, sc):
+            assert abs(s - fin[i]) <= 1e-5 * max(abs(fin[i]), scale[i]) and m == int(c.modalities[i])
