@@ -20,6 +20,8 @@
  *   include/memory_cuda.cuh:141-231  query_memory, QueryContext, create_query_context,
  *                                    destroy_query_context, query_memory_fast
  *   include/memory_graph.h:70-81     HostEpisodeCSR, build_episode_csr, RetrievalScope
+ *   include/streaming.h:42-81        StreamingBuffer::insert / flush (device-side append)
+ *   include/tiled_query.h:33-102     TiledQueryConfig/Result/Stats, tiled_query
  */
 #ifndef MARS_AMD_H
 #define MARS_AMD_H
