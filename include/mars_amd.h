@@ -282,6 +282,40 @@ int mars_query_batch(const mars_graph* g, mars_ctx* ctx, const float* d_queries,
                      const float* t_q, const mars_retrieval_config* cfg, int32_t* out_ids,
                      float* out_scores, mars_stats* stats);
 
+/* Batched global queries: Q global queries (the same cfg, query i at time t_q[i], a host
+ * array; query vectors in device memory, row-major Q x embedding_dim fp32). Query i gets
+ * exactly the results mars_query_device gives it with this context (same ids, scores,
+ * hops and order; cap and n_out[i] as there), written to out + i * cap.
+ * One fp16 MFMA scan of the corpus (mars_graph_enable_fp16) serves the whole batch: it
+ * keeps 16 candidates per query, which are rescored in the Q=1 path's arithmetic and
+ * certified against the fp16 error bound; certified queries then run their BFS together
+ * (one workgroup each). A query whose seeds miss the certificate, or whose visit set
+ * outgrows the batched BFS table (7168 nodes), is answered by the Q=1 path, as is the
+ * whole batch when cfg is episode-scoped (and active), K > 16, time_decay_lambda < 0,
+ * a same-episode boost applies, or the fp16 copy is absent. The node count is read once
+ * per call. stats may be NULL. Reference analogue: none (query_memory_fast,
+ * memory_cuda.cu:1351-1464, answers one query per call). */
+typedef struct mars_batch_stats {
+    int32_t queries;            /* Q                                                      */
+    int32_t batched;            /* answered by the shared scan and the batched BFS        */
+    int32_t uncertified;        /* seeds not certified: answered by the Q=1 path          */
+    int32_t overflow;           /* visit set beyond the batched table: Q=1 path           */
+    int32_t whole_batch_q1;     /* 1 if the configuration sent every query to the Q=1 path */
+    int32_t n_live;             /* nodes the batch was answered over                       */
+    float   gpu_ms_scan;        /* MARS_CTX_TIMING: shared fp16 scan + candidate merge     */
+    float   gpu_ms_seeds;       /* exact rescoring of the candidates + certificate        */
+    float   gpu_ms_bfs;         /* BFS, visit scores and results                          */
+    float   gpu_ms_total;
+    float   min_margin;         /* smallest certificate margin of a certified query        */
+    float   reserved;
+    double  wall_us;            /* host wall time of the call (Q=1 answers included)      */
+    double  q1_us;              /* of which Q=1 answers                                   */
+} mars_batch_stats;
+int mars_query_global_batch(const mars_graph* g, mars_ctx* ctx, const float* d_queries, int32_t Q,
+                            const float* t_q, const mars_retrieval_config* cfg,
+                            mars_query_result* out, int32_t cap, int32_t* n_out,
+                            mars_batch_stats* stats);
+
 /* Debug / parity hooks: copy the last query's per-node fp32 scores (N floats) and
  * its seed list (top-K ids and scores, K entries) to host memory. */
 int mars_ctx_last_scores(mars_ctx* ctx, float* h_scores, int64_t n);

@@ -31,7 +31,8 @@ __all__ = [
     "HostEpisodeCSR", "DeviceMemoryGraph", "QueryContext", "build_episode_csr", "upload_to_device",
     "upload_episode_ids", "upload_episode_csr", "upload_fp16_embeddings", "free_fp16_embeddings",
     "free_device", "create_query_context", "destroy_query_context", "query_memory_fast",
-    "query_memory_fast_device", "init", "MarsError", "corpus", "DeviceBuffer", "query_batch", "graph_knn", "set_csr",
+    "query_memory_fast_device", "init", "MarsError", "corpus", "DeviceBuffer", "query_batch", "query_global_batch",
+    "BatchStats", "graph_knn", "set_csr",
 ]
 
 MOD_TEXT, MOD_AUDIO, MOD_IMAGE = 0, 1, 2
@@ -354,6 +355,50 @@ def query_batch(dg: DeviceMemoryGraph, ctx: QueryContext, d_queries_ptr: int, n_
     if stats is not None:
         stats._fill(st)
     return ids, sc
+
+
+@dataclass
+class BatchStats:
+    queries: int = 0
+    batched: int = 0
+    uncertified: int = 0
+    overflow: int = 0
+    whole_batch_q1: int = 0
+    n_live: int = 0
+    gpu_ms_scan: float = 0.0
+    gpu_ms_seeds: float = 0.0
+    gpu_ms_bfs: float = 0.0
+    gpu_ms_total: float = 0.0
+    min_margin: float = 0.0
+    wall_us: float = 0.0
+    q1_us: float = 0.0
+
+    def _fill(self, c) -> None:
+        for f in ("queries", "batched", "uncertified", "overflow", "whole_batch_q1", "n_live", "gpu_ms_scan",
+                  "gpu_ms_seeds", "gpu_ms_bfs", "gpu_ms_total", "min_margin", "wall_us", "q1_us"):
+            setattr(self, f, getattr(c, f))
+
+
+def query_global_batch(dg: DeviceMemoryGraph, ctx: QueryContext, d_queries_ptr: int, n_queries: int, t_q,
+                       cfg: RetrievalConfig, cap: int = 64,
+                       stats: Optional[BatchStats] = None) -> List[List[QueryResult]]:
+    """Q global queries in one call (shared fp16 MFMA scan, certified exact seeds, batched
+    BFS): query i's results are exactly query_memory_fast's for it (capped at cap)."""
+    tq = np.ascontiguousarray(np.broadcast_to(np.asarray(t_q, np.float32), (n_queries,)))
+    out = (_lib.QueryResultC * (max(1, n_queries * cap)))()
+    n_out = np.zeros(n_queries, np.int32)
+    st = _lib.BatchStatsC()
+    c = cfg.to_c()
+    check(lib.mars_query_global_batch(dg.handle, ctx.handle, C.c_void_p(d_queries_ptr), int(n_queries), _ptr(tq),
+                                      C.byref(c), out, int(cap), _ptr(n_out), C.byref(st)), "mars_query_global_batch")
+    if stats is not None:
+        stats._fill(st)
+    res = []
+    for i in range(n_queries):
+        b = i * cap
+        res.append([QueryResult(out[b + j].node_id, out[b + j].score, out[b + j].modality, out[b + j].hops_from_seed)
+                    for j in range(min(int(n_out[i]), cap))])
+    return res
 
 
 def graph_knn(dg: DeviceMemoryGraph, k: int = 8) -> np.ndarray:

@@ -116,6 +116,25 @@ class InsertStatsC(C.Structure):
     ]
 
 
+class BatchStatsC(C.Structure):
+    _fields_ = [
+        ("queries", C.c_int32),
+        ("batched", C.c_int32),
+        ("uncertified", C.c_int32),
+        ("overflow", C.c_int32),
+        ("whole_batch_q1", C.c_int32),
+        ("n_live", C.c_int32),
+        ("gpu_ms_scan", C.c_float),
+        ("gpu_ms_seeds", C.c_float),
+        ("gpu_ms_bfs", C.c_float),
+        ("gpu_ms_total", C.c_float),
+        ("min_margin", C.c_float),
+        ("reserved", C.c_float),
+        ("wall_us", C.c_double),
+        ("q1_us", C.c_double),
+    ]
+
+
 class TiledConfigC(C.Structure):
     _fields_ = [("tile_size", C.c_int32), ("top_k", C.c_int32), ("time_decay_lambda", C.c_float),
                 ("modality_filter", C.c_int32), ("use_fp16", C.c_int32)]
@@ -181,6 +200,8 @@ SIGNATURES = {
                                     C.POINTER(StatsC)]),
     "mars_ctx_last_scores": (C.c_int, [VP, VP, I64]),
     "mars_query_batch": (C.c_int, [VP, VP, VP, I32, VP, C.POINTER(RetrievalConfigC), VP, VP, C.POINTER(StatsC)]),
+    "mars_query_global_batch": (C.c_int, [VP, VP, VP, I32, VP, C.POINTER(RetrievalConfigC), VP, I32, VP,
+                                          C.POINTER(BatchStatsC)]),
     "mars_graph_knn": (C.c_int, [VP, I32, VP]),
     "mars_graph_set_csr": (C.c_int, [VP, I32, VP, VP]),
     "mars_graph_insert": (C.c_int, [VP, I32, VP, VP, VP, VP, I32, VP, C.POINTER(InsertStatsC)]),

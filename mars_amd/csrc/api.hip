@@ -92,7 +92,7 @@ namespace {
 int graph_free(Graph& g) {
     (void)use_device(g.device);
     if (g.ins_stream) (void)hipStreamSynchronize(g.ins_stream);
-    dfree(g.emb); dfree(g.emb16); dfree(g.mods); dfree(g.ts); dfree(g.ro); dfree(g.rcap); dfree(g.col);
+    dfree(g.emb); dfree(g.emb16); dfree(g.nrm); dfree(g.mods); dfree(g.ts); dfree(g.ro); dfree(g.rcap); dfree(g.col);
     dfree(g.ep_ids); dfree(g.ep_off); dfree(g.ep_mem);
     graph_insert_free(g);
     if (g.ins_stream) (void)hipStreamDestroy(g.ins_stream);
@@ -134,6 +134,16 @@ int64_t edge_room(const Graph& g) {
     return int64_t(g.cap_n - g.n) * 256 + (g.cap_n > g.n ? 4096 : 0);
 }
 
+void multi_free(Ctx& c) {
+    dfree(c.mqn); dfree(c.mseed); dfree(c.mstat); dfree(c.minfo); dfree(c.mmargin);
+    dfree(c.mvlist); dfree(c.mvhop); dfree(c.mvpar); dfree(c.mvro); dfree(c.mvfin); dfree(c.mvscore);
+    c.mcap_q = 0;
+    if (c.h_mres) (void)hipHostFree(c.h_mres);
+    c.h_mres = nullptr;
+    c.d_mres = nullptr;
+    c.mres_bytes = 0;
+}
+
 int ctx_free(Ctx& c) {
     (void)use_device(c.device);
     if (c.stream) (void)hipStreamSynchronize(c.stream);
@@ -141,6 +151,7 @@ int ctx_free(Ctx& c) {
     dfree(c.vhop); dfree(c.vscore); dfree(c.vro); dfree(c.sortbuf); dfree(c.seed_idx); dfree(c.seed_val); dfree(c.stamps);
     dfree(c.gthr); dfree(c.gcnt);
     dfree(c.bq); dfree(c.btq); dfree(c.bpart); dfree(c.bout);
+    multi_free(c);
     if (c.h_query) (void)hipHostFree(c.h_query);
     if (c.h_res) (void)hipHostFree(c.h_res);
     for (auto& e : c.ev) if (e) (void)hipEventDestroy(e);
@@ -187,9 +198,11 @@ int graph_launch(Ctx::GraphSlot& g, int n, const KernelLaunch* l, void* const* a
     return MARS_OK;
 }
 
+// n_pin >= 0: answer over the first n_pin nodes (a batch that already read the node
+// count), else over the nodes published when the query starts.
 int query_impl(const mars_graph* gh, mars_ctx* ch, const float* h_q, const float* d_q, float t_q,
                const mars_retrieval_config* cfg, mars_query_result* out, int32_t cap, int32_t* n_out,
-               mars_stats* stats) {
+               mars_stats* stats, int32_t n_pin = -1) {
     const auto t0 = std::chrono::steady_clock::now();
     MARS_CHECK(gh && ch && cfg && n_out && (h_q || d_q), MARS_ERR_INVALID, "null argument");
     MARS_CHECK(cap >= 0 && (cap == 0 || out), MARS_ERR_INVALID, "bad output buffer");
@@ -197,7 +210,7 @@ int query_impl(const mars_graph* gh, mars_ctx* ch, const float* h_q, const float
     Ctx& c = ch->c;
     MARS_CHECK(g.d == c.d, MARS_ERR_INVALID, "graph dim %d != context dim %d", g.d, c.d);
     // nodes published so far: loaded once, every kernel of this query is bounded by it
-    const int32_t n_live = __atomic_load_n(&g.n, __ATOMIC_ACQUIRE);
+    const int32_t n_live = n_pin >= 0 ? n_pin : __atomic_load_n(&g.n, __ATOMIC_ACQUIRE);
     MARS_CHECK(n_live <= c.max_nodes, MARS_ERR_CAPACITY, "graph has %d nodes, context sized for %d", n_live,
                c.max_nodes);
     MARS_CHECK(n_live > 0, MARS_ERR_INVALID, "empty graph");
@@ -338,6 +351,40 @@ void batch_grid(int64_t n, int32_t q, int32_t* n_rranges, int32_t* n_qblocks, in
 }
 
 namespace {
+
+// Scratch of the batched global path: q queries' visit slots, and host-mapped room for
+// q result headers + q x rcap results.
+int ensure_multi_scratch(Ctx& c, int32_t q, int32_t rcap) {
+    if (q > c.mcap_q) {
+        dfree(c.mqn); dfree(c.mseed); dfree(c.mstat); dfree(c.minfo); dfree(c.mmargin);
+        dfree(c.mvlist); dfree(c.mvhop); dfree(c.mvpar); dfree(c.mvro); dfree(c.mvfin); dfree(c.mvscore);
+        c.mcap_q = 0;
+        const size_t nv = size_t(q) * kMultiVisit;
+        MARS_TRY(dmalloc(&c.mqn, size_t(q) * 4));
+        MARS_TRY(dmalloc(&c.mseed, size_t(q) * kMultiCand));
+        MARS_TRY(dmalloc(&c.mstat, size_t(q)));
+        MARS_TRY(dmalloc(&c.minfo, size_t(q) * 4));
+        MARS_TRY(dmalloc(&c.mmargin, size_t(q)));
+        MARS_TRY(dmalloc(&c.mvlist, nv));
+        MARS_TRY(dmalloc(&c.mvhop, nv));
+        MARS_TRY(dmalloc(&c.mvpar, nv));
+        MARS_TRY(dmalloc(&c.mvro, nv));
+        MARS_TRY(dmalloc(&c.mvfin, nv));
+        MARS_TRY(dmalloc(&c.mvscore, nv));
+        c.mcap_q = q;
+    }
+    const size_t need = size_t(q) * sizeof(ResultHeader) + size_t(q) * size_t(rcap) * sizeof(mars_query_result);
+    if (need > c.mres_bytes) {
+        if (c.h_mres) (void)hipHostFree(c.h_mres);
+        c.h_mres = nullptr;
+        c.d_mres = nullptr;
+        c.mres_bytes = 0;
+        MARS_HIP(hipHostMalloc(&c.h_mres, need, hipHostMallocMapped));
+        MARS_HIP(hipHostGetDevicePointer(&c.d_mres, c.h_mres, 0));
+        c.mres_bytes = need;
+    }
+    return MARS_OK;
+}
 
 int ensure_batch_scratch(Ctx& c, int32_t q, int64_t part_keys) {
     if (q > c.bcap_q) {
@@ -509,7 +556,10 @@ int mars_graph_enable_fp16(mars_graph* gh) {
     Graph& g = gh->g;
     MARS_TRY(use_device(g.device));
     if (!g.emb16) MARS_TRY(dmalloc(&g.emb16, size_t(g.cap_n) * size_t(g.d)));
+    if (!g.nrm) MARS_TRY(dmalloc(&g.nrm, 4));
+    MARS_HIP(hipMemset(g.nrm, 0, 4 * sizeof(uint32_t)));
     MARS_TRY(launch_convert_f16(g.emb, g.emb16, int64_t(g.n) * g.d, nullptr));
+    MARS_TRY(launch_row_norms(g.emb, g.emb16, 0, g.n, g.d, g.nrm, nullptr));
     MARS_HIP(hipStreamSynchronize(nullptr));
     return MARS_OK;
 }
@@ -519,6 +569,7 @@ int mars_graph_disable_fp16(mars_graph* gh) {
     std::lock_guard<std::mutex> lock(gh->mu);
     MARS_TRY(use_device(gh->g.device));
     dfree(gh->g.emb16);
+    dfree(gh->g.nrm);
     return MARS_OK;
 }
 
@@ -799,6 +850,126 @@ int mars_query_batch(const mars_graph* gh, mars_ctx* ch, const float* dq, int32_
         st.wall_us = std::chrono::duration<double, std::micro>(std::chrono::steady_clock::now() - t0).count();
         *stats = st;
     }
+    return MARS_OK;
+}
+
+int mars_query_global_batch(const mars_graph* gh, mars_ctx* ch, const float* dq, int32_t Q, const float* h_tq,
+                            const mars_retrieval_config* cfg, mars_query_result* out, int32_t cap,
+                            int32_t* n_out, mars_batch_stats* stats) {
+    using clk = std::chrono::steady_clock;
+    const auto t0 = clk::now();
+    MARS_CHECK(gh && ch && dq && h_tq && cfg && n_out && Q > 0, MARS_ERR_INVALID, "bad arguments");
+    MARS_CHECK(cap >= 0 && (cap == 0 || out), MARS_ERR_INVALID, "bad output buffer");
+    const Graph& g = gh->g;
+    Ctx& c = ch->c;
+    MARS_CHECK(g.d == c.d, MARS_ERR_INVALID, "graph dim %d != context dim %d", g.d, c.d);
+    const int32_t n_live = __atomic_load_n(&g.n, __ATOMIC_ACQUIRE);
+    MARS_CHECK(n_live <= c.max_nodes, MARS_ERR_CAPACITY, "graph has %d nodes, context sized for %d", n_live,
+               c.max_nodes);
+    MARS_CHECK(n_live > 0, MARS_ERR_INVALID, "empty graph");
+    MARS_CHECK(cfg->top_k > 0, MARS_ERR_INVALID, "top_k = %d", cfg->top_k);
+    const int32_t K = std::min(cfg->top_k, c.max_k);
+    const bool scoped = episode_scoped_active(g, *cfg);
+    const int32_t hops = scoped ? 0 : std::max(0, cfg->bfs_max_hops);
+    const int32_t rcap = cfg->max_results_returned > 0 ? cfg->max_results_returned : K;
+    MARS_CHECK(rcap <= c.res_cap, MARS_ERR_UNSUPPORTED, "max_results_returned %d exceeds %d", rcap, c.res_cap);
+    MARS_TRY(use_device(c.device));
+    const bool fp16 = (c.flags & MARS_CTX_USE_FP16) && g.emb16 != nullptr;
+    const bool boost = g.ep_ids && cfg->query_episode_id >= 0 && cfg->episode_same_boost > 0.0f;
+    const float lambda = cfg->time_decay_lambda;
+    const bool batched = !scoped && g.emb16 && g.nrm && batch_dim_supported(g.d) && K <= kMultiCand && !boost &&
+                         lambda >= 0.0f && lambda <= FLT_MAX && hops < 255;
+    mars_batch_stats st{};
+    st.queries = Q;
+    st.n_live = n_live;
+    st.min_margin = FLT_MAX;
+    std::vector<int32_t> q1;                    // queries the Q=1 path answers
+    if (batched) {
+        int32_t nrr = 0, nqb = 0;
+        int64_t rpr = 0;
+        batch_grid(n_live, Q, &nrr, &nqb, &rpr);
+        const int32_t kp = batch_kpart(kMultiCand);
+        MARS_TRY(ensure_batch_scratch(c, Q, int64_t(nqb) * nrr * 64 * kp));
+        MARS_TRY(ensure_multi_scratch(c, Q, rcap));
+        hipStream_t s = c.stream;
+        const bool timing = (c.flags & MARS_CTX_TIMING) != 0;
+        MARS_HIP(hipMemcpyAsync(c.btq, h_tq, size_t(Q) * sizeof(float), hipMemcpyHostToDevice, s));
+        MARS_TRY(launch_f32_to_f16_rows(dq, c.bq, int64_t(Q) * g.d, s));
+        MARS_TRY(launch_query_norms(dq, c.bq, Q, g.d, c.mqn, s));
+        if (timing) MARS_HIP(hipEventRecord(c.ev[0], s));
+        BatchArgs b{};
+        b.emb16 = g.emb16; b.n = n_live; b.d = g.d; b.qh = c.bq; b.q = Q; b.tq = c.btq; b.ts = g.ts;
+        b.mods = g.mods; b.lambda = lambda; b.mod_filter = cfg->modality_filter; b.k = kMultiCand;
+        b.self_base = -1; b.part = c.bpart; b.rows_per_range = rpr; b.n_rranges = nrr; b.n_qblocks = nqb;
+        b.uniform_tq = std::all_of(h_tq, h_tq + Q, [&](float x) { return x == h_tq[0]; }) ? 1 : 0;
+        MARS_TRY(launch_batch_scan(b, s));
+        MARS_TRY(launch_batch_merge(c.bpart, nrr, kp, Q, kMultiCand, c.bout, s));
+        if (timing) MARS_HIP(hipEventRecord(c.ev[1], s));
+        SeedArgs sa{};
+        sa.emb = fp16 ? static_cast<const void*>(g.emb16) : static_cast<const void*>(g.emb);
+        sa.fp16 = fp16 ? 1 : 0; sa.d = g.d; sa.ts = g.ts; sa.mods = g.mods; sa.queries = dq; sa.tq = c.btq;
+        sa.lambda = lambda; sa.mod_filter = cfg->modality_filter; sa.q = Q; sa.k = K; sa.cand = c.bout;
+        sa.qn = c.mqn; sa.nrm = g.nrm; sa.seeds = c.mseed; sa.status = c.mstat; sa.margin = c.mmargin;
+        MARS_TRY(launch_multi_seed(sa, s));
+        if (timing) MARS_HIP(hipEventRecord(c.ev[2], s));
+        auto* hdr = static_cast<ResultHeader*>(c.h_mres);
+        auto* rec = reinterpret_cast<mars_query_result*>(hdr + Q);
+        MultiArgs m{};
+        m.ro = g.ro; m.col = g.col; m.mods = g.mods; m.n_live = n_live; m.hops = hops;
+        m.hop_decay = cfg->bfs_score_decay; m.k = K; m.rcap = rcap; m.q = Q; m.seeds = c.mseed;
+        m.status = c.mstat; m.info = c.minfo; m.vlist = c.mvlist; m.vhop = c.mvhop; m.vpar = c.mvpar;
+        m.vro = c.mvro; m.vfin = c.mvfin; m.vscore = c.mvscore;
+        m.res = static_cast<ResultHeader*>(c.d_mres);
+        m.rec = reinterpret_cast<mars_query_result*>(m.res + Q);
+        MARS_TRY(launch_multi_bfs(m, s));
+        VisitScoreArgs va{};
+        va.emb = sa.emb; va.fp16 = sa.fp16; va.d = g.d; va.ts = g.ts; va.mods = g.mods; va.queries = dq;
+        va.tq = c.btq; va.lambda = lambda; va.mod_filter = cfg->modality_filter; va.q = Q; va.status = c.mstat;
+        va.info = c.minfo; va.vlist = c.mvlist; va.vfin = c.mvfin;
+        MARS_TRY(launch_visit_scores(va, s));
+        MARS_TRY(launch_multi_select(m, s));
+        if (timing) MARS_HIP(hipEventRecord(c.ev[3], s));
+        std::vector<float> margin(static_cast<size_t>(Q));
+        MARS_HIP(hipMemcpyAsync(margin.data(), c.mmargin, size_t(Q) * sizeof(float), hipMemcpyDeviceToHost, s));
+        MARS_HIP(hipStreamSynchronize(s));
+        for (int32_t j = 0; j < Q; ++j) {
+            const ResultHeader h = hdr[j];
+            if (h.count < 0) {
+                if (h.visited == kMultiOverflow) ++st.overflow;
+                else ++st.uncertified;
+                q1.push_back(j);
+                continue;
+            }
+            const int32_t nw = std::min(h.count, cap);
+            if (nw > 0)
+                std::memcpy(out + int64_t(j) * cap, rec + int64_t(j) * rcap, size_t(nw) * sizeof(mars_query_result));
+            n_out[j] = h.count;
+            ++st.batched;
+            st.min_margin = std::min(st.min_margin, margin[size_t(j)]);
+        }
+        if (timing) {
+            float ms = 0.0f;
+            MARS_HIP(hipEventElapsedTime(&ms, c.ev[0], c.ev[1]));
+            st.gpu_ms_scan = ms;
+            MARS_HIP(hipEventElapsedTime(&ms, c.ev[1], c.ev[2]));
+            st.gpu_ms_seeds = ms;
+            MARS_HIP(hipEventElapsedTime(&ms, c.ev[2], c.ev[3]));
+            st.gpu_ms_bfs = ms;
+            MARS_HIP(hipEventElapsedTime(&ms, c.ev[0], c.ev[3]));
+            st.gpu_ms_total = ms;
+        }
+    } else {
+        st.whole_batch_q1 = 1;
+        for (int32_t j = 0; j < Q; ++j) q1.push_back(j);
+    }
+    const auto t1 = clk::now();
+    for (const int32_t j : q1)
+        MARS_TRY(query_impl(gh, ch, nullptr, dq + int64_t(j) * g.d, h_tq[j], cfg, cap ? out + int64_t(j) * cap : nullptr,
+                            cap, &n_out[j], nullptr, n_live));
+    const auto t2 = clk::now();
+    st.q1_us = std::chrono::duration<double, std::micro>(t2 - t1).count();
+    st.wall_us = std::chrono::duration<double, std::micro>(t2 - t0).count();
+    if (stats) *stats = st;
     return MARS_OK;
 }
 

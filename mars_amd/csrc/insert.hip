@@ -280,8 +280,11 @@ extern "C" int mars_graph_insert(mars_graph* gh, int32_t n_new, const float* emb
                                 hipMemcpyHostToDevice, s));
         MARS_HIP(hipMemcpyAsync(g.ep_mem + g.member_total, p_mem, att_bytes, hipMemcpyHostToDevice, s));
     }
-    if (g.emb16)
+    if (g.emb16) {
         MARS_TRY(launch_convert_f16(g.emb + int64_t(n_old) * D, g.emb16 + int64_t(n_old) * D, int64_t(n_new) * D, s));
+        // the batched global path's bound covers every published row
+        if (g.nrm) MARS_TRY(launch_row_norms(g.emb, g.emb16, n_old, n_after, D, g.nrm, s));
+    }
     MARS_HIP(hipStreamSynchronize(s));
     // publish: scans, episode scope and the boost see the new nodes from here on
     double t_queryable = 0.0;

@@ -86,6 +86,13 @@ constexpr int kMaxK = 64;              // seeds per query (wave-held list), as M
 constexpr int kSortCap = 8192;         // results sorted in LDS by the finalize kernel
 constexpr int kFrontierChunk = 4096;   // frontier nodes per BFS chunk (LDS)
 constexpr uint64_t kEmptyKey = ~0ull;
+// batched global queries: fp16 candidates per query (the batched scan's list), and
+// visit slots per query (the LDS-hash BFS never visits more than 6144 + 1024 nodes)
+constexpr int kMultiCand = 16;
+constexpr int kMultiVisit = 8192;
+constexpr int32_t kMultiUncertified = 0;   // seeds not certified: answered by the Q=1 path
+constexpr int32_t kMultiOk = 1;
+constexpr int32_t kMultiOverflow = 2;      // visit set outgrew the LDS hash: Q=1 path
 
 // ---- score keys ----------------------------------------------------------------
 __host__ __device__ inline uint32_t desc32(float s) {
@@ -118,6 +125,10 @@ struct Graph {
     int64_t cap_e = 0;
     float* emb = nullptr;
     __half* emb16 = nullptr;
+    // with the fp16 copy: upper bounds over the rows of max |e|, |e16| and |e16 - e|
+    // (Euclidean norms; e16 with subnormals flushed in the difference), fp32 bit
+    // patterns rounded up, raised by atomicMax as rows are converted
+    uint32_t* nrm = nullptr;
     int32_t* mods = nullptr;
     float* ts = nullptr;
     int64_t* ro = nullptr;    // cap_n: (row length << 32) | row start in col
@@ -204,6 +215,22 @@ struct Ctx {
     uint64_t* bout = nullptr;      // merged keys per query
     int32_t bcap_q = 0;
     int64_t bcap_part = 0;
+    // batched global queries (grown on demand; kMultiVisit visit slots per query)
+    double* mqn = nullptr;         // [q][4] |q|, |q16|, |q16 - q|
+    uint64_t* mseed = nullptr;     // [q][kMultiCand] certified exact seed keys
+    int32_t* mstat = nullptr;      // [q] kMultiOk / kMultiUncertified / kMultiOverflow
+    int32_t* minfo = nullptr;      // [q][4] visited, levels, seeds
+    float* mmargin = nullptr;      // [q] certificate margin
+    int32_t* mvlist = nullptr;
+    int32_t* mvhop = nullptr;
+    int32_t* mvpar = nullptr;
+    int64_t* mvro = nullptr;
+    float* mvfin = nullptr;        // exact fused score of each visited node
+    float* mvscore = nullptr;
+    int32_t mcap_q = 0;
+    void* h_mres = nullptr;        // pinned, mapped: [q] ResultHeader then [q][rcap] results
+    void* d_mres = nullptr;
+    size_t mres_bytes = 0;
     // replayed query graphs (kernel nodes updated per query)
     struct GraphSlot {
         hipGraph_t graph = nullptr;
@@ -288,6 +315,7 @@ struct FinalizeArgs {
     int32_t* vhop;
     float* vscore;
     int64_t* vro;            // per visit position: the node's (len << 32) | start
+    int32_t* vpar;           // per visit position: the parent's position (unscored BFS only)
     uint64_t* sortbuf;
     int32_t cap_visit;
     int32_t rcap;            // results requested (max_results or K)
@@ -360,6 +388,80 @@ int launch_batch_merge(const uint64_t* part, int32_t n_rranges, int32_t kpart, i
 int launch_knn_rerank(const float* emb, int64_t q0, int64_t nq, int32_t d, const uint64_t* cand, int32_t kc,
                       int32_t k_out, int32_t* nbrs, hipStream_t s);
 int launch_f32_to_f16_rows(const float* in, __half* out, int64_t count, hipStream_t s);
+
+// ---- batched global queries (multi.hip; BFS / select kernels in kernels.hip) -----------
+// Query terms of the fused score, as ScanArgs carries them for one query.
+struct QueryTerms {
+    float t_q;
+    float lambda;
+    int32_t mod_filter;
+    int32_t query_ep;
+    float boost;
+};
+struct SeedArgs {
+    const void* emb;         // rows the Q=1 path scores: fp32, or fp16 when fp16 != 0
+    int32_t fp16;
+    int32_t d;
+    const float* ts;
+    const int32_t* mods;
+    const float* queries;    // q x d fp32
+    const float* tq;         // q query times
+    float lambda;
+    int32_t mod_filter;
+    int32_t q;
+    int32_t k;               // seeds per query (<= kMultiCand)
+    const uint64_t* cand;    // [q][kMultiCand] fp16 candidate keys, ascending
+    const double* qn;        // [q][4] query norms
+    const uint32_t* nrm;     // graph row-norm bounds (Graph::nrm)
+    uint64_t* seeds;         // [q][kMultiCand] out: exact keys, ascending
+    int32_t* status;         // [q] out
+    float* margin;           // [q] out: K-th exact score - (C-th fp16 score + bound)
+};
+struct MultiArgs {
+    const int64_t* ro;
+    const int32_t* col;
+    const int32_t* mods;
+    int32_t n_live;
+    int32_t hops;
+    float hop_decay;
+    int32_t k;
+    int32_t rcap;
+    int32_t q;
+    const uint64_t* seeds;   // [q][kMultiCand]
+    int32_t* status;         // [q]
+    int32_t* info;           // [q][4] visited, levels, seeds
+    int32_t* vlist;          // [q][kMultiVisit] each
+    int32_t* vhop;
+    int32_t* vpar;
+    int64_t* vro;
+    float* vfin;
+    float* vscore;
+    ResultHeader* res;       // [q] (host-mapped)
+    mars_query_result* rec;  // [q][rcap] (host-mapped)
+};
+struct VisitScoreArgs {
+    const void* emb;
+    int32_t fp16;
+    int32_t d;
+    const float* ts;
+    const int32_t* mods;
+    const float* queries;
+    const float* tq;
+    float lambda;
+    int32_t mod_filter;
+    int32_t q;
+    const int32_t* status;
+    const int32_t* info;
+    const int32_t* vlist;
+    float* vfin;
+};
+int launch_row_norms(const float* emb, const __half* emb16, int64_t r0, int64_t r1, int32_t d, uint32_t* nrm,
+                     hipStream_t s);
+int launch_query_norms(const float* q32, const __half* q16, int32_t q, int32_t d, double* out, hipStream_t s);
+int launch_multi_seed(const SeedArgs& a, hipStream_t s);
+int launch_multi_bfs(const MultiArgs& a, hipStream_t s);
+int launch_visit_scores(const VisitScoreArgs& a, hipStream_t s);
+int launch_multi_select(const MultiArgs& a, hipStream_t s);
 
 }  // namespace mars
 

@@ -27,233 +27,10 @@
 //  k_convert_f16  RNE fp32 -> fp16 copy with 64-bit indexing (convert_f32_to_f16,
 //               src/memory_cuda.cu:207-211 and :858-868, which overflows int32).
 // ============================================================================
-#include "internal.hpp"
-
-#include <cfloat>
-#include <type_traits>
+#include "device.hpp"
 
 namespace mars {
 namespace {
-
-__device__ inline int lane_id() { return int(threadIdx.x & 63u); }
-
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-
-// Loads of data written earlier in the same kernel by other threads: served by
-// L2 (agent-coherent), never by a stale L1 line.
-template <typename T>
-__device__ inline T ld_coherent(const T* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// ---- lane exchanges: value of lane (lane ^ J) -----------------------------------
-// J = 1, 2: DPP quad_perm; J = 4: DPP row_shl/row_shr; J = 8: DPP row_ror:8 (within a
-// 16-lane row i^8 == i+-8); J = 16: ds_swizzle (xor within 32 lanes); J = 32: bpermute.
-template <int J>
-__device__ inline uint32_t xor_lane(uint32_t v) {
-    if constexpr (J == 1) return uint32_t(__builtin_amdgcn_mov_dpp(int(v), 0xB1, 0xF, 0xF, false));
-    else if constexpr (J == 2) return uint32_t(__builtin_amdgcn_mov_dpp(int(v), 0x4E, 0xF, 0xF, false));
-    else if constexpr (J == 4) {
-        const uint32_t up = uint32_t(__builtin_amdgcn_mov_dpp(int(v), 0x104, 0xF, 0xF, false));   // lane + 4
-        const uint32_t dn = uint32_t(__builtin_amdgcn_mov_dpp(int(v), 0x114, 0xF, 0xF, false));   // lane - 4
-        return (threadIdx.x & 4u) ? dn : up;
-    } else if constexpr (J == 8) return uint32_t(__builtin_amdgcn_mov_dpp(int(v), 0x128, 0xF, 0xF, false));
-    else if constexpr (J == 16) return uint32_t(__builtin_amdgcn_ds_swizzle(int(v), 0x401F));
-    else return uint32_t(__shfl_xor(int(v), J));
-}
-template <int J>
-__device__ inline uint64_t xor_lane64(uint64_t v) {
-    return (uint64_t(xor_lane<J>(uint32_t(v >> 32))) << 32) | xor_lane<J>(uint32_t(v));
-}
-template <int J>
-__device__ inline float xor_lanef(float v) {
-    return __uint_as_float(xor_lane<J>(__float_as_uint(v)));
-}
-
-// Insert key x into the wave-held ascending list (lane i = i-th smallest; lanes
-// >= k hold kEmptyKey). Caller guarantees x < list[k-1].
-__device__ inline void list_insert(uint64_t& list, uint64_t x, int lane, int k) {
-    const uint64_t below = __ballot(list < x);
-    const int pos = __popcll(below);
-    const uint64_t up = __shfl_up(list, 1u);
-    uint64_t v = (lane < pos) ? list : ((lane == pos) ? x : up);
-    list = (lane < k) ? v : kEmptyKey;
-}
-
-// Offer one candidate key per lane where `offer` holds; keeps thr = list[k-1].
-__device__ inline void list_offer(uint64_t& list, uint64_t& thr, uint64_t key, bool offer,
-                                  int lane, int k) {
-    uint64_t m = __ballot(offer && key < thr);
-    while (m) {
-        const int src = __ffsll((unsigned long long)m) - 1;
-        m &= m - 1;
-        const uint64_t x = __shfl(key, src);
-        if (x < thr) {
-            list_insert(list, x, lane, k);
-            thr = __shfl(list, k - 1);
-        }
-    }
-}
-
-template <int J>
-__device__ inline uint64_t cmpx(uint64_t x, int lane, bool ascending_block) {
-    const uint64_t y = xor_lane64<J>(x);
-    const bool lower = (lane & J) == 0;
-    const uint64_t lo = x < y ? x : y, hi = x < y ? y : x;
-    return (lower == ascending_block) ? lo : hi;
-}
-
-// Ascending bitonic sort of one key per lane across the wave.
-__device__ inline uint64_t wave_sort64(uint64_t x, int lane) {
-    x = cmpx<1>(x, lane, (lane & 2) == 0);
-    x = cmpx<2>(x, lane, (lane & 4) == 0);
-    x = cmpx<1>(x, lane, (lane & 4) == 0);
-    x = cmpx<4>(x, lane, (lane & 8) == 0);
-    x = cmpx<2>(x, lane, (lane & 8) == 0);
-    x = cmpx<1>(x, lane, (lane & 8) == 0);
-    x = cmpx<8>(x, lane, (lane & 16) == 0);
-    x = cmpx<4>(x, lane, (lane & 16) == 0);
-    x = cmpx<2>(x, lane, (lane & 16) == 0);
-    x = cmpx<1>(x, lane, (lane & 16) == 0);
-    x = cmpx<16>(x, lane, (lane & 32) == 0);
-    x = cmpx<8>(x, lane, (lane & 32) == 0);
-    x = cmpx<4>(x, lane, (lane & 32) == 0);
-    x = cmpx<2>(x, lane, (lane & 32) == 0);
-    x = cmpx<1>(x, lane, (lane & 32) == 0);
-    x = cmpx<32>(x, lane, true);
-    x = cmpx<16>(x, lane, true);
-    x = cmpx<8>(x, lane, true);
-    x = cmpx<4>(x, lane, true);
-    x = cmpx<2>(x, lane, true);
-    x = cmpx<1>(x, lane, true);
-    return x;
-}
-
-// Smallest k of two ascending wave lists (lanes >= k of the result hold kEmptyKey):
-// min(a[i], b[63-i]) is bitonic and holds the 64 smallest; six half-cleaners sort it.
-__device__ inline uint64_t wave_merge64(uint64_t a, uint64_t b, int lane, int k) {
-    const uint64_t r = __shfl(b, 63 - lane);
-    uint64_t c = a < r ? a : r;
-    c = cmpx<32>(c, lane, true);
-    c = cmpx<16>(c, lane, true);
-    c = cmpx<8>(c, lane, true);
-    c = cmpx<4>(c, lane, true);
-    c = cmpx<2>(c, lane, true);
-    c = cmpx<1>(c, lane, true);
-    return lane < k ? c : kEmptyKey;
-}
-
-// Offer one key per lane: few winners are inserted one by one, many are sorted
-// and merged in registers.
-__device__ inline void wave_offer(uint64_t& list, uint64_t& thr, uint64_t key, int lane, int k) {
-    const uint64_t m = __ballot(key < thr);
-    if (m == 0) return;
-    if (__popcll(m) <= 2) {
-        list_offer(list, thr, key, true, lane, k);
-        return;
-    }
-    const uint64_t xs = wave_sort64(key < thr ? key : kEmptyKey, lane);
-    list = wave_merge64(list, xs, lane, k);
-    thr = __shfl(list, k - 1);
-}
-
-// Sum over the 16 lanes of a DPP row; every lane of the row gets the total.
-__device__ inline float row16_sum(float v) {
-    v += xor_lanef<8>(v);
-    v += xor_lanef<4>(v);
-    v += xor_lanef<2>(v);
-    v += xor_lanef<1>(v);
-    return v;
-}
-
-// ---- per-row dot products -------------------------------------------------------
-// fp32 rows: chunk c covers floats [64c, 64c+64); lane s holds 4 of them.
-template <int NCH>
-struct QF32 {
-    float v[NCH][4];
-    __device__ void load(const float* q, int sub) {
-#pragma unroll
-        for (int c = 0; c < NCH; ++c) {
-            const float4 x = reinterpret_cast<const float4*>(q + c * 64)[sub];
-            v[c][0] = x.x; v[c][1] = x.y; v[c][2] = x.z; v[c][3] = x.w;
-        }
-    }
-    __device__ float dot(const float* row, int sub) const {
-        const f32x4* r = reinterpret_cast<const f32x4*>(row) + sub;
-        f32x4 x[NCH];
-#pragma unroll
-        for (int c = 0; c < NCH; ++c) x[c] = __builtin_nontemporal_load(r + c * 16);
-        float acc = 0.0f;
-#pragma unroll
-        for (int c = 0; c < NCH; ++c) {
-            acc = fmaf(x[c].x, v[c][0], acc);
-            acc = fmaf(x[c].y, v[c][1], acc);
-            acc = fmaf(x[c].z, v[c][2], acc);
-            acc = fmaf(x[c].w, v[c][3], acc);
-        }
-        return acc;
-    }
-};
-
-// fp16 rows: chunk c covers halves [128c, 128c+128); lane s holds 8 of them.
-template <int NCH>
-struct QF16 {
-    float v[NCH][8];
-    __device__ void load(const float* q, int sub) {
-#pragma unroll
-        for (int c = 0; c < NCH; ++c)
-#pragma unroll
-            for (int j = 0; j < 8; ++j) v[c][j] = q[c * 128 + sub * 8 + j];
-    }
-    __device__ float dot(const __half* row, int sub) const {
-        const u32x4* r = reinterpret_cast<const u32x4*>(row) + sub;
-        u32x4 x[NCH];
-#pragma unroll
-        for (int c = 0; c < NCH; ++c) x[c] = __builtin_nontemporal_load(r + c * 16);
-        float acc = 0.0f;
-#pragma unroll
-        for (int c = 0; c < NCH; ++c) {
-            const uint32_t w[4] = {x[c].x, x[c].y, x[c].z, x[c].w};
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const __half2 h2 = *reinterpret_cast<const __half2*>(&w[j]);
-                const float2 f = __half22float2(h2);
-                acc = fmaf(f.x, v[c][2 * j], acc);
-                acc = fmaf(f.y, v[c][2 * j + 1], acc);
-            }
-        }
-        return acc;
-    }
-};
-
-// Any D: lane s of the group takes elements s, s+16, ... (q read through cache).
-struct QGeneric {
-    const float* q;
-    int d;
-    __device__ void load(const float* q_, int) { q = q_; }
-    __device__ float dot(const float* row, int sub) const {
-        float acc = 0.0f;
-        for (int i = sub; i < d; i += 16) acc = fmaf(row[i], q[i], acc);
-        return acc;
-    }
-    __device__ float dot(const __half* row, int sub) const {
-        float acc = 0.0f;
-        for (int i = sub; i < d; i += 16) acc = fmaf(__half2float(row[i]), q[i], acc);
-        return acc;
-    }
-};
-
-// fused stage-1/2 epilogue (reference order of fp32 operations: dot * w, then
-// * (1 + boost); filtered rows are -FLT_MAX and not decayed).
-__device__ inline float fuse_score(float dot, float ts, int32_t mod, int32_t ep,
-                                   const ScanArgs& a) {
-    if (a.mod_filter >= 0 && mod != a.mod_filter) return -FLT_MAX;
-    const float age = fmaxf(0.0f, a.t_q - ts);
-    float s = dot * expf(-a.lambda * age);
-    if (a.boost > 0.0f && ep == a.query_ep && s > -FLT_MAX * 0.5f) s = s * (1.0f + a.boost);
-    return s;
-}
 
 // Row groups of 4 rows (one per 16-lane group) are dealt out grid-stride: wave w of
 // workgroup b takes groups (it * gridDim.x * 4 + b * 4 + w) * kUnroll + u, so at any
@@ -495,6 +272,10 @@ __device__ inline int round_rank(FinShared& sh, bool won, int* rank) {
 // was touched, so the caller can run the global-array BFS instead).
 // With rk > 0 every wave also keeps the rk best (score, id) keys it emits in
 // `best` (wave 0 starts from the seeds), so the results need only a tree merge.
+// SCORED == false: the visit set, hops and parents only (a.vpar gets each node's
+// parent position, no score is read or written; rk must be 0). The visit order
+// and the parents do not depend on scores, so scores can be propagated later.
+template <bool SCORED>
 __device__ int bfs_lds(FinShared& sh, const FinalizeArgs& a, int ns, int* levels_out, uint64_t& best,
                        uint64_t& bthr, int rk) {
     constexpr int R = 4;                       // 1024-edge rounds cached in registers
@@ -533,9 +314,11 @@ __device__ int bfs_lds(FinShared& sh, const FinalizeArgs& a, int ns, int* levels
 #pragma unroll
                 for (int r = 0; r < R; ++r) {
                     if (s0 + r * kFinThreads + tid < T && uint32_t(nb[r]) < uint32_t(a.n_live)) {
-                        fv[r] = a.fin[nb[r]];
+                        if constexpr (SCORED) {
+                            fv[r] = a.fin[nb[r]];
+                            ps[r] = ld_coherent(a.vscore + pp[r]);
+                        }
                         rw[r] = a.ro[nb[r]];
-                        ps[r] = ld_coherent(a.vscore + pp[r]);
                         slot[r] = hash_find_or_insert(sh, nb[r]);
                         if (slot[r] >= 0) atomicMin(&sh.u.bfs.hval[slot[r]], (kClaimHop << 16) | uint32_t(pp[r]));
                     }
@@ -555,11 +338,13 @@ __device__ int bfs_lds(FinShared& sh, const FinalizeArgs& a, int ns, int* levels
                         const int pos = out + rank;
                         a.vlist[pos] = nb[r];
                         a.vhop[pos] = h + 1;
-                        a.vscore[pos] = sc;
+                        if constexpr (SCORED) a.vscore[pos] = sc;
+                        else a.vpar[pos] = pp[r];
                         a.vro[pos] = rw[r];
                         sh.u.bfs.hval[slot[r]] = (uint32_t(h + 1) << 16) | uint32_t(pos);
                     }
-                    if (rk > 0) wave_offer(best, bthr, won ? make_key(sc, uint32_t(nb[r])) : kEmptyKey, lane_id(), rk);
+                    if (SCORED && rk > 0)
+                        wave_offer(best, bthr, won ? make_key(sc, uint32_t(nb[r])) : kEmptyKey, lane_id(), rk);
                     out += wtot;
                     __syncthreads();
                 }
@@ -792,7 +577,7 @@ __global__ __launch_bounds__(kFinThreads) void k_finalize(FinalizeArgs a) {
     uint64_t best = (wave == 0 && lane < rk) ? list : kEmptyKey;
     uint64_t bthr = rk > 0 ? __shfl(best, rk - 1) : kEmptyKey;
     int levels = 0;
-    int V = (a.hops < int(kClaimHop)) ? bfs_lds(sh, a, ns, &levels, best, bthr, rk) : -1;   // hop below the claim mark
+    int V = (a.hops < int(kClaimHop)) ? bfs_lds<true>(sh, a, ns, &levels, best, bthr, rk) : -1;   // hop below the claim mark
     const bool in_lds = V >= 0;
     if (!in_lds) {
         __syncthreads();
@@ -829,6 +614,94 @@ __global__ __launch_bounds__(kFinThreads) void k_finalize(FinalizeArgs a) {
 }
 
 // ---- episode-scoped query ------------------------------------------------------------
+// ---- batched global queries: one workgroup per query ------------------------------
+// The view of query j's visit slots as the finalize helpers take them.
+__device__ inline FinalizeArgs multi_view(const MultiArgs& m, int j) {
+    FinalizeArgs a{};
+    const int64_t base = int64_t(j) * kMultiVisit;
+    a.k = m.k; a.ro = m.ro; a.col = m.col; a.n_live = m.n_live; a.mods = m.mods; a.hops = m.hops;
+    a.hop_decay = m.hop_decay; a.rcap = m.rcap; a.cap_visit = kMultiVisit;
+    a.vlist = m.vlist + base; a.vhop = m.vhop + base; a.vpar = m.vpar + base; a.vro = m.vro + base;
+    a.vscore = m.vscore + base; a.rec = m.rec + int64_t(j) * m.rcap;
+    return a;
+}
+
+// Visit set, hops and parents of query j from its certified seeds: the unscored LDS
+// BFS of k_finalize (same claims, same order). A visit set that outgrows the LDS hash
+// marks the query kMultiOverflow (the Q=1 path answers it).
+__global__ __launch_bounds__(kFinThreads) void k_multi_bfs(MultiArgs m) {
+    __shared__ FinShared sh;
+    const int j = int(blockIdx.x);
+    if (m.status[j] != kMultiOk) return;                  // block-uniform
+    const FinalizeArgs a = multi_view(m, j);
+    const int tid = int(threadIdx.x), lane = lane_id(), wave = tid >> 6;
+    if (wave == 0) {
+        const uint64_t key = lane < m.k ? m.seeds[int64_t(j) * kMultiCand + lane] : kEmptyKey;
+        const int ns = __popcll(__ballot(key != kEmptyKey));
+        if (key != kEmptyKey) {
+            const int32_t id = key_id(key);
+            a.vlist[lane] = id;
+            a.vhop[lane] = 0;
+            a.vpar[lane] = -1;
+            a.vscore[lane] = key_score(key);
+            a.vro[lane] = a.ro[id];
+        }
+        if (lane == 0) sh.s_misc[0] = ns;
+    }
+    __threadfence_block();
+    __syncthreads();
+    const int ns = sh.s_misc[0];
+    int levels = 0;
+    uint64_t best = kEmptyKey, bthr = kEmptyKey;
+    const int V = (a.hops < int(kClaimHop)) ? bfs_lds<false>(sh, a, ns, &levels, best, bthr, 0) : -1;
+    if (tid == 0) {
+        if (V < 0) {
+            m.status[j] = kMultiOverflow;
+        } else {
+            m.info[4 * j] = V;
+            m.info[4 * j + 1] = levels;
+            m.info[4 * j + 2] = ns;
+        }
+    }
+}
+
+// Scores of query j's visit set, level by level in the finalize kernel's arithmetic
+// (score = max(parent score * hop_decay, fin * 0.8), seeds keep their exact score),
+// then the first rcap by (score desc, id asc) into the host-mapped results. Every
+// query writes its header; count -1 marks one the Q=1 path must answer.
+__global__ __launch_bounds__(kFinThreads) void k_multi_select(MultiArgs m) {
+    __shared__ FinShared sh;
+    const int j = int(blockIdx.x);
+    const int st = m.status[j];
+    if (st != kMultiOk) {
+        if (threadIdx.x == 0) {
+            ResultHeader h;
+            h.count = -1; h.visited = st; h.levels = 0; h.n_seeds = 0;
+            m.res[j] = h;
+        }
+        return;
+    }
+    const FinalizeArgs a = multi_view(m, j);
+    const int tid = int(threadIdx.x);
+    const int V = m.info[4 * j], levels = m.info[4 * j + 1], ns = m.info[4 * j + 2];
+    const float* vfin = m.vfin + int64_t(j) * kMultiVisit;
+    for (int h = 1; h <= levels; ++h) {
+        for (int p = ns + tid; p < V; p += kFinThreads) {
+            if (a.vhop[p] == h)
+                a.vscore[p] = fmaxf(ld_coherent(a.vscore + a.vpar[p]) * a.hop_decay, vfin[p] * 0.8f);
+        }
+        __threadfence_block();
+        __syncthreads();
+    }
+    const int rc = min(a.rcap, V);
+    select_sorted(sh, a, V, rc);
+    if (tid == 0) {
+        ResultHeader h;
+        h.count = rc; h.visited = V; h.levels = levels; h.n_seeds = ns;
+        m.res[j] = h;
+    }
+}
+
 __global__ __launch_bounds__(256) void k_episode(EpisodeArgs a) {
     __shared__ uint64_t s_lists[4][64];
     __shared__ int32_t s_ids[64];
@@ -1036,6 +909,16 @@ int launch_tile_merge(uint64_t* part, uint32_t* gcnt, uint64_t* carry, int32_t k
 
 int launch_finalize(const FinalizeArgs& a, hipStream_t s) {
     MARS_LAUNCH(k_finalize, dim3(1), dim3(kFinThreads), 0, s, a);
+    return MARS_OK;
+}
+
+int launch_multi_bfs(const MultiArgs& a, hipStream_t s) {
+    MARS_LAUNCH(k_multi_bfs, dim3(unsigned(a.q)), dim3(kFinThreads), 0, s, a);
+    return MARS_OK;
+}
+
+int launch_multi_select(const MultiArgs& a, hipStream_t s) {
+    MARS_LAUNCH(k_multi_select, dim3(unsigned(a.q)), dim3(kFinThreads), 0, s, a);
     return MARS_OK;
 }
 
