@@ -84,50 +84,86 @@ def tiled_pass(args, mars_amd, corpus, c, qnodes, N, D, K, pctl, lat_resident, h
     return res
 
 
-def stream_pass(args, mars_amd, corpus, lib, check, RetrievalConfigC, full, dg, ctx, dq, qnodes, ep_cfgs, gcfg,
-                N, D, M, pctl):
-    """Streaming: 10-node episodes inserted at 2,000 nodes/s on the graph's side stream
-    while Q=1 queries arrive at 1,000/s, alternating global and episode-scoped."""
+SERVE_MODES = {
+    "q1": "one global query per call; each insert finds its own k-NN",
+    "batch": "batched global calls; each insert finds its own k-NN",
+    "link": "batched global calls that also find the k-NN of the nodes inserted since the last call "
+            "(one corpus pass for both); inserts publish rows and episode edges only",
+}
+
+
+def serve_pass(args, mars_amd, corpus, lib, check, full, dg, ctx, qnodes, nq, ep_cfgs, gcfg, ctx_nodes, D, first_ins,
+               M, mode, pctl):
+    """Streaming: 10-node episodes inserted at 2,000 nodes/s on the graph's side stream while
+    Q=1 queries arrive at 1,000/s, alternating global and episode-scoped. Episode queries
+    are answered on their own thread and context as they arrive; global queries by a
+    server thread (SERVE_MODES). Latency = completion - arrival (queueing included)."""
+    max_batch = 1 if mode == "q1" else args.batch_max
     from mars_amd import _lib
-    nq = min(args.stream_queries, len(qnodes))
-    cfgs = (RetrievalConfigC * nq)()
-    epc = ep_cfgs(qnodes[:nq])
+    nq = min(nq, len(qnodes))
+    ng, ne = (nq + 1) // 2, nq // 2
+    rate = 1000.0
+    g_arr = np.arange(ng, dtype=np.float64) * 2e6 / rate
+    e_arr = g_arr[:ne] + 1e6 / rate
+    gq = mars_amd.DeviceBuffer.from_array(np.ascontiguousarray(full.embeddings[qnodes[0:2 * ng:2]]))
+    eq = mars_amd.DeviceBuffer.from_array(np.ascontiguousarray(full.embeddings[qnodes[1:2 * ne:2]]))
+    ecf = ep_cfgs(qnodes[1:2 * ne:2])
     g1 = gcfg.to_c()
-    for i in range(nq):
-        cfgs[i] = g1 if i % 2 == 0 else epc[i]
-    nb = (M + 9) // 10
-    ins = (_lib.InsertStatsC * nb)()
-    lat = np.zeros(nq, np.float64)
-    qstart = np.zeros(nq, np.float64)
-    istart = np.zeros(nb, np.float64)
-    emb = np.ascontiguousarray(full.embeddings[N:N + M])
-    mods, ts = np.ascontiguousarray(full.modalities[N:N + M]), np.ascontiguousarray(full.timestamps[N:N + M])
-    ep = np.ascontiguousarray(full.episode_ids[N:N + M])
-    pv = lambda a: C.c_void_p(a.ctypes.data)
-    b = _lib.StreamBenchC(dq.ptr, D, nq, corpus.QUERY_TIME, C.cast(cfgs, C.c_void_p).value, 1000.0, pv(emb).value,
-                          pv(mods).value, pv(ts).value, pv(ep).value, M, 10, 2000.0, corpus.KNN_K, pv(lat).value,
-                          pv(qstart).value, C.cast(ins, C.c_void_p).value, pv(istart).value)
+    ectx = mars_amd.create_query_context(ctx_nodes, D, 64, flags=0)
+    ib = args.stream_insert_batch
+    nb = (M + ib - 1) // ib
+    ins = (_lib.InsertStatsC * max(1, nb))()
+    istart = np.zeros(max(1, nb), np.float64)
+    ilinked = np.zeros(max(1, nb), np.float64)
+    g_done = np.zeros(ng, np.float64)
+    g_batch = np.zeros(ng, np.int32)
+    e_done = np.zeros(ne, np.float64)
+    sl = slice(first_ins, first_ins + M)
+    emb = np.ascontiguousarray(full.embeddings[sl])
+    mods, ts = np.ascontiguousarray(full.modalities[sl]), np.ascontiguousarray(full.timestamps[sl])
+    ep = np.ascontiguousarray(full.episode_ids[sl])
+    pv = lambda a: a.ctypes.data
+    b = _lib.ServeBenchC()
+    b.t_q, b.max_batch = corpus.QUERY_TIME, max_batch
+    b.g_queries, b.n_global, b.g_arrival_us, b.gcfg = gq.ptr, ng, pv(g_arr), C.cast(C.pointer(g1), C.c_void_p).value
+    b.e_queries, b.n_episode, b.e_arrival_us, b.ecfgs = eq.ptr, ne, pv(e_arr), C.cast(ecf, C.c_void_p).value
+    b.ins_emb, b.ins_mods, b.ins_ts, b.ins_ep = pv(emb), pv(mods), pv(ts), pv(ep)
+    b.n_insert, b.insert_batch, b.insert_rate, b.knn_k = M, ib, 2000.0, args.knn_k
+    b.g_done_us, b.g_batch, b.e_done_us = pv(g_done), pv(g_batch), pv(e_done)
+    b.ins_stats, b.ins_start_us = C.cast(ins, C.c_void_p).value, pv(istart)
+    b.link_deferred, b.max_link, b.ins_linked_us, b.link_wait_us = int(mode == "link"), 1024, pv(ilinked), 5000.0
     t0 = time.time()
-    check(lib.mars_bench_stream(dg.handle, ctx.handle, C.byref(b)), "mars_bench_stream")
-    wall = time.time() - t0
+    try:
+        check(lib.mars_bench_serve(dg.handle, ctx.handle, ectx.handle, C.byref(b)), "mars_bench_serve")
+    finally:
+        wall = time.time() - t0
+        mars_amd.destroy_query_context(ectx)
+        gq.free()
+        eq.free()
     dg.refresh()
-    assert dg.num_nodes == N + M
-    lg, le = lat[0::2], lat[1::2]
-    qa = np.array([s.queryable_us for s in ins])
-    li = np.array([s.linked_us for s in ins])
-    kn = np.array([s.knn_us for s in ins])
-    span = istart[-1] - istart[0] + li[-1]
-    res = dict(base_nodes=N, inserted_nodes=M, insert_batch=10, insert_rate_target=2000.0,
-               insert_rate_achieved=M / (span / 1e6), query_rate_target=1000.0, queries=nq,
-               global_p50_us=pctl(lg, .5), global_p99_us=pctl(lg, .99), episode_p50_us=pctl(le, .5),
-               episode_p99_us=pctl(le, .99), queryable_p50_us=pctl(qa, .5), queryable_p99_us=pctl(qa, .99),
-               linked_p50_us=pctl(li, .5), linked_p99_us=pctl(li, .99), knn_mean_us=float(kn.mean()),
-               rows_relocated=int(sum(s.rows_relocated for s in ins)),
-               rows_appended=int(sum(s.rows_appended for s in ins)), wall_s=wall)
-    log(f"streaming ({M} nodes at 2000/s onto {N}, 1000 q/s 50/50): global p99 {res['global_p99_us']:.0f} us, "
-        f"episode p99 {res['episode_p99_us']:.0f} us; time-to-queryable p50 {res['queryable_p50_us']:.0f} us "
-        f"p99 {res['queryable_p99_us']:.0f} us; linked p50 {res['linked_p50_us']:.0f} us p99 "
-        f"{res['linked_p99_us']:.0f} us (k-NN {res['knn_mean_us']:.0f} us)")
+    lg, le = g_done - g_arr, e_done - e_arr
+    res = dict(mode=mode, global_server=SERVE_MODES[mode], max_batch=max_batch, queries=nq, global_p50_us=pctl(lg, .5), global_p99_us=pctl(lg, .99),
+               episode_p50_us=pctl(le, .5), episode_p99_us=pctl(le, .99),
+               global_mean_batch=float(g_batch.mean()), global_q1_answers=int(b.g_uncertified),
+               inserted_nodes=M, wall_s=wall)
+    if M > 0:
+        qa = np.array([s.queryable_us for s in ins[:nb]])
+        li = ilinked[:nb] - istart[:nb]                    # insert call -> k-NN edges visible
+        span = istart[nb - 1] + np.array([s.linked_us for s in ins[:nb]])[-1] - istart[0]
+        res.update(insert_rate_achieved=M / (span / 1e6), queryable_p50_us=pctl(qa, .5),
+                   queryable_p99_us=pctl(qa, .99), linked_p50_us=pctl(li, .5), linked_p99_us=pctl(li, .99),
+                   rows_relocated=int(sum(s.rows_relocated for s in ins[:nb])),
+                   rows_appended=int(sum(s.rows_appended for s in ins[:nb])))
+        if mode == "link":
+            res.update(link_calls=int(b.link_calls))
+        else:
+            res.update(knn_mean_us=float(np.mean([s.knn_us for s in ins[:nb]])))
+    log(f"streaming [{mode}] ({M} nodes at 2000/s onto {first_ins}, {nq} queries at 1000/s 50/50): "
+        f"global p50 {res['global_p50_us']:.0f} p99 {res['global_p99_us']:.0f} us (mean batch "
+        f"{res['global_mean_batch']:.1f}), episode p50 {res['episode_p50_us']:.0f} p99 {res['episode_p99_us']:.0f} us"
+        + (f"; time-to-queryable p50 {res['queryable_p50_us']:.0f} p99 {res['queryable_p99_us']:.0f} us; linked p50 "
+           f"{res['linked_p50_us']:.0f} p99 {res['linked_p99_us']:.0f} us; {res['insert_rate_achieved']:.0f} nodes/s"
+           if M > 0 else ""))
     return res
 
 
@@ -156,6 +192,12 @@ def main() -> int:
     ap.add_argument("--knn-k", type=int, default=8,
                     help="nearest neighbours per node in the NSN graph (0: intra-episode pairs only)")
     ap.add_argument("--batch-q", type=int, default=64, help="queries per batched MFMA scoring call")
+    ap.add_argument("--batch-max", type=int, default=64, help="most global queries per batched call when serving")
+    ap.add_argument("--serve-modes", default="q1,link",
+                    help="servers of the streaming pass, one run each: q1, batch, link (see SERVE_MODES)")
+    ap.add_argument("--stream-insert-batch", type=int, default=10, help="nodes per insert call when streaming")
+    ap.add_argument("--knn-block", type=int, default=0,
+                    help="k-NN of the NSN graph within blocks of this many consecutive ids (0: exact, all pairs)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU; --gpus above 1 is not supported here "
@@ -188,8 +230,9 @@ def main() -> int:
     log(f"upload + fp16 copy: {time.time() - t:.1f}s")
     t = time.time()
     if args.knn_k > 0:
-        knn = mars_amd.graph_knn(dg, args.knn_k)       # fp16 MFMA candidates + exact fp32 rescoring
-        log(f"{args.knn_k}-NN on the GPU: {time.time() - t:.1f}s")
+        knn = mars_amd.graph_knn(dg, args.knn_k, args.knn_block)   # fp16 MFMA candidates + exact fp32 rescoring
+        log(f"{args.knn_k}-NN on the GPU" + (f" (blocks of {args.knn_block} ids)" if args.knn_block else "") +
+            f": {time.time() - t:.1f}s")
     else:
         knn = np.empty((N, 0), np.int32)
         log("NSN graph without k-NN edges (intra-episode pairs only)")
@@ -203,7 +246,7 @@ def main() -> int:
     mars_amd.upload_episode_csr(dg, csr)
     ctx = mars_amd.create_query_context(N + M, D, 64, flags=0)
 
-    nq = args.steps + args.warmup
+    nq = max(args.steps, args.stream_queries) + args.warmup
     qnodes = corpus.pick_queries(c.modalities, nq, seed=args.query_seed)
     dq = mars_amd.DeviceBuffer.from_array(c.embeddings[qnodes])
 
@@ -328,9 +371,18 @@ def main() -> int:
     if not args.profile_only and args.tiled_queries > 0:
         out["tiled_comparator"] = tiled_pass(args, mars_amd, corpus, c, qnodes[W:], N, D, K, pctl, lat_g,
                                              "pinned" if host_rows else "pageable")
-    if M > 0 and args.stream_queries > 0:
-        out["streaming"] = stream_pass(args, mars_amd, corpus, lib, check, RetrievalConfigC, full, dg, ctx, dq,
-                                       qnodes, ep_cfgs, gcfg, N, D, M, pctl)
+    if args.stream_queries > 0 and args.serve_modes:
+        modes = [m for m in args.serve_modes.split(",") if m]
+        runs, first = [], N
+        per = M // len(modes) // 10 * 10                  # whole 10-node episodes per run
+        per_q = args.stream_queries // len(modes)
+        for i, m in enumerate(modes):
+            runs.append(serve_pass(args, mars_amd, corpus, lib, check, full, dg, ctx, qnodes[W + i * per_q:], per_q,
+                                   ep_cfgs, gcfg, N + M, D, first, per, m, pctl))
+            first += per
+        out["streaming"] = dict(base_nodes=N, insert_batch=args.stream_insert_batch, insert_rate_target=2000.0,
+                                query_rate_target=1000.0, knn_k=args.knn_k,
+                                latency="completion - arrival (queueing included)", runs=runs)
 
     achieved = bytes_f32 / float(kern_g.mean()) / 1e3       # GB/s
     res = {
@@ -350,8 +402,9 @@ def main() -> int:
                                f"and fp16 global reported alongside)",
                    "num_nodes": N, "dim": D, "top_k": K, "bfs_hops": 2, "decay_lambda": corpus.DECAY_LAMBDA,
                    "corpus_seed": args.seed, "query_seed": args.query_seed, "num_edges": int(len(c.col_indices)),
-                   "nsn_graph": (f"intra-episode pairs + {args.knn_k}-NN" if args.knn_k > 0 else
-                                 "intra-episode pairs only (k-NN edges omitted)")},
+                   "nsn_graph": (f"intra-episode pairs + {args.knn_k}-NN" +
+                                 (f" within blocks of {args.knn_block} ids" if args.knn_block else "")
+                                 if args.knn_k > 0 else "intra-episode pairs only (k-NN edges omitted)")},
         "global_fp32": dict(p50_us=pctl(lat_g, .5), p99_us=pctl(lat_g, .99), qps=S / wall_g,
                             p99_us_with_events=pctl(lat_gk, .99),
                             graph_replay=dict(p50_us=pctl(lat_gg, .5), p99_us=pctl(lat_gg, .99)),

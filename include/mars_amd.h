@@ -166,6 +166,10 @@ int mars_graph_set_csr(mars_graph* g, int32_t num_edges, const int32_t* row_offs
  * of the NSN graph at corpus sizes a CPU cannot (analogue of the tiled kNN build of
  * src/cmng_build.cu:135-245). */
 int mars_graph_knn(mars_graph* g, int32_t k, int32_t* nbrs);
+/* The same within blocks: each node's k nearest among the nodes of its block of
+ * block_rows consecutive ids (block_rows >= num_nodes: mars_graph_knn). For corpora
+ * where the exact all-pairs search is too long to build (13M rows: ~2.6e17 FLOP). */
+int mars_graph_knn_blocked(mars_graph* g, int32_t k, int32_t block_rows, int32_t* nbrs);
 /* Copy device arrays back to host (any pointer may be NULL to skip): the NSN graph as
  * a packed CSR (row_offsets: num_nodes + 1, col_indices: num_edges) and the episode CSR. */
 int mars_graph_download(const mars_graph* g, int32_t* row_offsets, int32_t* col_indices,
@@ -200,6 +204,24 @@ typedef struct mars_insert_stats {
 int mars_graph_insert(mars_graph* g, int32_t n_new, const float* embeddings, const int32_t* modalities,
                       const float* timestamps, const int32_t* episode_ids, int32_t knn_k,
                       int32_t* out_knn, mars_insert_stats* stats);
+
+/* Deferred k-NN edges (the second half of add_incremental_edges_, streaming.cpp:97-163,
+ * taken out of the insert so that many inserts share one corpus pass): nodes inserted
+ * with knn_k = 0 are queryable at once; later their neighbour edges are added here.
+ * mars_graph_link adds the edges between node first + i and each id nbrs[i * k + j]
+ * (-1 skipped, self skipped), in both directions; the edge set becomes the union (no
+ * duplicate entries), rows stay ascending. mars_graph_link_knn first finds each node's
+ * knn_k nearest neighbours among all published nodes (as mars_graph_insert does, over
+ * the nodes published when it runs; out_knn nullable, count * knn_k ids). Inserting
+ * with knn_k = 0 and then linking with knn_k gives the graph a single insert with
+ * knn_k gives. Nodes first .. first + count - 1 must be published. Runs on the side
+ * stream under the graph mutex; queries keep running and see each row before or after.
+ * stats: first_node, nodes_added (= count), edges_added, rows_relocated (rewritten
+ * into the tail), rows_appended, linked_us, knn_us. */
+int mars_graph_link(mars_graph* g, int32_t first, int32_t count, int32_t k, const int32_t* nbrs,
+                    mars_insert_stats* stats);
+int mars_graph_link_knn(mars_graph* g, int32_t first, int32_t count, int32_t knn_k, int32_t* out_knn,
+                        mars_insert_stats* stats);
 
 /* ---- tiled out-of-core comparator (include/tiled_query.h:33-102) ------------- */
 /* TiledQueryConfig (tiled_query.h:33-39), same defaults (mars_tiled_config_default).
@@ -315,6 +337,17 @@ int mars_query_global_batch(const mars_graph* g, mars_ctx* ctx, const float* d_q
                             const float* t_q, const mars_retrieval_config* cfg,
                             mars_query_result* out, int32_t cap, int32_t* n_out,
                             mars_batch_stats* stats);
+/* The same, with the neighbour search of knn_count published nodes knn_first ..
+ * knn_first + knn_count - 1 done in the same corpus pass: out_knn (host, knn_count x
+ * knn_k, -1 padded) receives each node's knn_k nearest neighbours among the nodes
+ * published when the call starts, as mars_graph_link_knn finds them; pass them to
+ * mars_graph_link. Q may be 0 (neighbour search only). A streaming server links the
+ * nodes it inserted with knn_k = 0 this way, one corpus pass serving both. */
+int mars_query_global_batch_knn(const mars_graph* g, mars_ctx* ctx, const float* d_queries, int32_t Q,
+                                const float* t_q, const mars_retrieval_config* cfg,
+                                mars_query_result* out, int32_t cap, int32_t* n_out,
+                                mars_batch_stats* stats, int32_t knn_first, int32_t knn_count,
+                                int32_t knn_k, int32_t* out_knn);
 
 /* Debug / parity hooks: copy the last query's per-node fp32 scores (N floats) and
  * its seed list (top-K ids and scores, K entries) to host memory. */
@@ -349,7 +382,7 @@ int mars_bench_queries(const mars_graph* g, mars_ctx* ctx, const float* d_querie
                        int32_t n, float t_q, const mars_retrieval_config* cfgs, int32_t n_cfg,
                        double* lat_us, float* kern_us, float* bfs_us, int32_t* n_res);
 
-/* Streaming workload driver (no reference counterpart; the BASELINE streaming
+/* Streaming workload driver (no reference counterpart; the streaming benchmark
  * configuration): on one thread, n_queries single queries paced at query_rate per
  * second (query i starts at i / query_rate s, or when the previous one returns);
  * on a second thread, n_insert host rows inserted with mars_graph_insert in
@@ -378,6 +411,63 @@ typedef struct mars_stream_bench {
     double*                      ins_start_us;
 } mars_stream_bench;
 int mars_bench_stream(mars_graph* g, mars_ctx* ctx, mars_stream_bench* bench);
+
+/* Serving workload driver (no reference counterpart): three threads start together.
+ *  - episode-scoped queries: query i (device vector e_queries + i * embedding_dim,
+ *    configuration ecfgs[i]) arrives at e_arrival_us[i] after the start and is answered
+ *    on ctx_episode as soon as it has arrived and the one before it is done;
+ *  - global queries: query i (g_queries + i * embedding_dim, configuration gcfg) arrives
+ *    at g_arrival_us[i]; whenever global queries wait, all that have arrived (at most
+ *    max_batch) are answered by one mars_query_global_batch call on ctx_global
+ *    (max_batch = 1: one mars_query_device per query);
+ *  - inserts: n_insert host rows inserted with mars_graph_insert in batches of
+ *    insert_batch nodes paced at insert_rate nodes per second. With link_deferred = 0
+ *    each insert finds its nodes' knn_k neighbours itself; with link_deferred = 1 the
+ *    inserts pass knn_k = 0 (queryable at once) and the global server links every
+ *    published, unlinked node (at most max_link per call) in its next batched call
+ *    (mars_query_global_batch_knn + mars_graph_link: one corpus pass for both), or
+ *    in a call of its own once the oldest unlinked insert has waited link_wait_us.
+ * All queries use query time t_q. g_done_us[i] / e_done_us[i] = when query i's results
+ * were in host memory (since the start), so done - arrival is its latency including
+ * the wait; g_batch[i] = size of the call that answered global query i;
+ * ins_stats[j] / ins_start_us[j] as in mars_bench_stream; ins_linked_us[j] = when the
+ * k-NN edges of insert j were visible (since the start). */
+typedef struct mars_serve_bench {
+    float                        t_q;
+    int32_t                      max_batch;
+    const float*                 g_queries;      /* device, n_global * embedding_dim     */
+    int32_t                      n_global;
+    int32_t                      pad0;
+    const double*                g_arrival_us;
+    const mars_retrieval_config* gcfg;
+    const float*                 e_queries;      /* device, n_episode * embedding_dim    */
+    int32_t                      n_episode;
+    int32_t                      pad1;
+    const double*                e_arrival_us;
+    const mars_retrieval_config* ecfgs;          /* n_episode configurations             */
+    const float*                 ins_emb;        /* host, n_insert * embedding_dim       */
+    const int32_t*               ins_mods;
+    const float*                 ins_ts;
+    const int32_t*               ins_ep;         /* NULL if the graph has no episode ids  */
+    int32_t                      n_insert;
+    int32_t                      insert_batch;
+    double                       insert_rate;    /* nodes per second                     */
+    int32_t                      knn_k;
+    int32_t                      pad2;
+    double*                      g_done_us;
+    int32_t*                     g_batch;
+    double*                      e_done_us;
+    mars_insert_stats*           ins_stats;
+    double*                      ins_start_us;
+    int64_t                      g_uncertified;  /* out: global queries the batch sent to the Q=1 path */
+    int64_t                      g_overflow;     /* out: of which for a visit overflow   */
+    int32_t                      link_deferred;
+    int32_t                      max_link;
+    double*                      ins_linked_us;
+    double                       link_wait_us;
+    int64_t                      link_calls;     /* out: server calls that linked nodes  */
+} mars_serve_bench;
+int mars_bench_serve(mars_graph* g, mars_ctx* ctx_global, mars_ctx* ctx_episode, mars_serve_bench* bench);
 
 #ifdef __cplusplus
 }

@@ -32,7 +32,7 @@ __all__ = [
     "upload_episode_ids", "upload_episode_csr", "upload_fp16_embeddings", "free_fp16_embeddings",
     "free_device", "create_query_context", "destroy_query_context", "query_memory_fast",
     "query_memory_fast_device", "init", "MarsError", "corpus", "DeviceBuffer", "query_batch", "query_global_batch",
-    "BatchStats", "graph_knn", "set_csr",
+    "BatchStats", "query_global_batch_knn", "link", "link_knn", "graph_knn", "set_csr",
 ]
 
 MOD_TEXT, MOD_AUDIO, MOD_IMAGE = 0, 1, 2
@@ -401,10 +401,14 @@ def query_global_batch(dg: DeviceMemoryGraph, ctx: QueryContext, d_queries_ptr: 
     return res
 
 
-def graph_knn(dg: DeviceMemoryGraph, k: int = 8) -> np.ndarray:
-    """k nearest neighbours of every node (fp16 MFMA candidates + exact fp32 rescoring)."""
+def graph_knn(dg: DeviceMemoryGraph, k: int = 8, block_rows: int = 0) -> np.ndarray:
+    """k nearest neighbours of every node (fp16 MFMA candidates + exact fp32 rescoring);
+    block_rows > 0: among the nodes of each block of block_rows consecutive ids."""
     out = np.empty((dg.num_nodes, k), np.int32)
-    check(lib.mars_graph_knn(dg.handle, int(k), _ptr(out)), "mars_graph_knn")
+    if block_rows > 0:
+        check(lib.mars_graph_knn_blocked(dg.handle, int(k), int(block_rows), _ptr(out)), "mars_graph_knn_blocked")
+    else:
+        check(lib.mars_graph_knn(dg.handle, int(k), _ptr(out)), "mars_graph_knn")
     return out
 
 
@@ -442,6 +446,60 @@ def insert_nodes(dg: DeviceMemoryGraph, embeddings, modalities, timestamps, epis
     out = InsertStats(st.first_node, st.nodes_added, st.edges_added, st.rows_relocated, st.rows_appended,
                       st.queryable_us, st.linked_us, st.knn_us)
     return (out, knn[:, :knn_k]) if return_knn else out
+
+
+def _istats(st) -> InsertStats:
+    return InsertStats(st.first_node, st.nodes_added, st.edges_added, st.rows_relocated, st.rows_appended,
+                       st.queryable_us, st.linked_us, st.knn_us)
+
+
+def link_knn(dg: DeviceMemoryGraph, first: int, count: int, knn_k: int = 8, return_knn: bool = False):
+    """Deferred k-NN edges of nodes [first, first + count) inserted with knn_k = 0 (the edge half of
+    StreamingBuffer::add_incremental_edges_, src/streaming.cpp:97-163). Returns InsertStats
+    (and the (count, knn_k) neighbour ids when return_knn)."""
+    knn = np.full((max(count, 1), knn_k), -1, np.int32)
+    st = _lib.InsertStatsC()
+    check(lib.mars_graph_link_knn(dg.handle, int(first), int(count), int(knn_k), _ptr(knn), C.byref(st)),
+          "mars_graph_link_knn")
+    dg.refresh()
+    return (_istats(st), knn[:count]) if return_knn else _istats(st)
+
+
+def link(dg: DeviceMemoryGraph, first: int, nbrs) -> InsertStats:
+    """Edges between node first + i and each id of nbrs[i] (-1 skipped), both directions (set union)."""
+    nb = np.ascontiguousarray(nbrs, np.int32)
+    if nb.ndim != 2:
+        raise ValueError("link: nbrs must be (count, k)")
+    st = _lib.InsertStatsC()
+    check(lib.mars_graph_link(dg.handle, int(first), int(nb.shape[0]), int(nb.shape[1]), _ptr(nb), C.byref(st)),
+          "mars_graph_link")
+    dg.refresh()
+    return _istats(st)
+
+
+def query_global_batch_knn(dg: DeviceMemoryGraph, ctx: QueryContext, d_queries_ptr: int, n_queries: int, t_q,
+                           cfg: RetrievalConfig, knn_first: int, knn_count: int, knn_k: int = 8, cap: int = 64,
+                           stats: Optional[BatchStats] = None):
+    """query_global_batch plus the neighbour search of nodes [knn_first, knn_first + knn_count)
+    in the same corpus pass: returns (results, (knn_count, knn_k) neighbour ids)."""
+    tq = np.ascontiguousarray(np.broadcast_to(np.asarray(t_q, np.float32), (n_queries,)))
+    out = (_lib.QueryResultC * (max(1, n_queries * cap)))()
+    n_out = np.zeros(max(1, n_queries), np.int32)
+    knn = np.full((max(knn_count, 1), knn_k), -1, np.int32)
+    st = _lib.BatchStatsC()
+    c = cfg.to_c()
+    check(lib.mars_query_global_batch_knn(dg.handle, ctx.handle, C.c_void_p(d_queries_ptr or None), int(n_queries),
+                                          _ptr(tq), C.byref(c), out, int(cap), _ptr(n_out), C.byref(st),
+                                          int(knn_first), int(knn_count), int(knn_k), _ptr(knn)),
+          "mars_query_global_batch_knn")
+    if stats is not None:
+        stats._fill(st)
+    res = []
+    for i in range(n_queries):
+        b = i * cap
+        res.append([QueryResult(out[b + j].node_id, out[b + j].score, out[b + j].modality, out[b + j].hops_from_seed)
+                    for j in range(min(int(n_out[i]), cap))])
+    return res, knn[:knn_count]
 
 
 @dataclass

@@ -158,6 +158,24 @@ class StreamBenchC(C.Structure):
                 ("query_start_us", C.c_void_p), ("ins_stats", C.c_void_p), ("ins_start_us", C.c_void_p)]
 
 
+class ServeBenchC(C.Structure):
+    _fields_ = [
+        ("t_q", C.c_float), ("max_batch", C.c_int32),
+        ("g_queries", C.c_void_p), ("n_global", C.c_int32), ("pad0", C.c_int32),
+        ("g_arrival_us", C.c_void_p), ("gcfg", C.c_void_p),
+        ("e_queries", C.c_void_p), ("n_episode", C.c_int32), ("pad1", C.c_int32),
+        ("e_arrival_us", C.c_void_p), ("ecfgs", C.c_void_p),
+        ("ins_emb", C.c_void_p), ("ins_mods", C.c_void_p), ("ins_ts", C.c_void_p), ("ins_ep", C.c_void_p),
+        ("n_insert", C.c_int32), ("insert_batch", C.c_int32), ("insert_rate", C.c_double),
+        ("knn_k", C.c_int32), ("pad2", C.c_int32),
+        ("g_done_us", C.c_void_p), ("g_batch", C.c_void_p), ("e_done_us", C.c_void_p),
+        ("ins_stats", C.c_void_p), ("ins_start_us", C.c_void_p),
+        ("g_uncertified", C.c_int64), ("g_overflow", C.c_int64),
+        ("link_deferred", C.c_int32), ("max_link", C.c_int32), ("ins_linked_us", C.c_void_p),
+        ("link_wait_us", C.c_double), ("link_calls", C.c_int64),
+    ]
+
+
 class CorpusParamsC(C.Structure):
     _fields_ = [
         ("num_nodes", C.c_int64),
@@ -202,7 +220,13 @@ SIGNATURES = {
     "mars_query_batch": (C.c_int, [VP, VP, VP, I32, VP, C.POINTER(RetrievalConfigC), VP, VP, C.POINTER(StatsC)]),
     "mars_query_global_batch": (C.c_int, [VP, VP, VP, I32, VP, C.POINTER(RetrievalConfigC), VP, I32, VP,
                                           C.POINTER(BatchStatsC)]),
+    "mars_bench_serve": (C.c_int, [VP, VP, VP, C.POINTER(ServeBenchC)]),
+    "mars_query_global_batch_knn": (C.c_int, [VP, VP, VP, I32, VP, C.POINTER(RetrievalConfigC), VP, I32, VP,
+                                              C.POINTER(BatchStatsC), I32, I32, I32, VP]),
+    "mars_graph_link": (C.c_int, [VP, I32, I32, I32, VP, C.POINTER(InsertStatsC)]),
+    "mars_graph_link_knn": (C.c_int, [VP, I32, I32, I32, VP, C.POINTER(InsertStatsC)]),
     "mars_graph_knn": (C.c_int, [VP, I32, VP]),
+    "mars_graph_knn_blocked": (C.c_int, [VP, I32, I32, VP]),
     "mars_graph_set_csr": (C.c_int, [VP, I32, VP, VP]),
     "mars_graph_insert": (C.c_int, [VP, I32, VP, VP, VP, VP, I32, VP, C.POINTER(InsertStatsC)]),
     "mars_ctx_last_seeds": (C.c_int, [VP, VP, VP, I32, PI32]),

@@ -11,10 +11,14 @@
 #include "internal.hpp"
 
 #include <algorithm>
+#include <atomic>
 #include <cfloat>
 #include <chrono>
+#include <cstddef>
 #include <cstdarg>
 #include <cstring>
+#include <deque>
+#include <mutex>
 #include <string>
 #include <thread>
 #include <vector>
@@ -135,6 +139,8 @@ int64_t edge_room(const Graph& g) {
 }
 
 void multi_free(Ctx& c) {
+    dfree(c.mknn);
+    c.mknn_cap = 0;
     dfree(c.mqn); dfree(c.mseed); dfree(c.mstat); dfree(c.minfo); dfree(c.mmargin);
     dfree(c.mvlist); dfree(c.mvhop); dfree(c.mvpar); dfree(c.mvro); dfree(c.mvfin); dfree(c.mvscore);
     c.mcap_q = 0;
@@ -408,6 +414,18 @@ int ensure_batch_scratch(Ctx& c, int32_t q, int64_t part_keys) {
 }  // namespace mars
 
 using namespace mars;
+
+// The ctypes mirrors (mars_amd/_lib.py) depend on these layouts.
+static_assert(sizeof(mars_query_result) == 16, "mars_query_result layout");
+static_assert(sizeof(mars_insert_stats) == 48 && offsetof(mars_insert_stats, queryable_us) == 24,
+              "mars_insert_stats layout");
+static_assert(sizeof(mars_stream_bench) == 128 && offsetof(mars_stream_bench, knn_k) == 88,
+              "mars_stream_bench layout");
+static_assert(sizeof(mars_batch_stats) == 64 && offsetof(mars_batch_stats, wall_us) == 48,
+              "mars_batch_stats layout");
+static_assert(sizeof(mars_serve_bench) == 216 && offsetof(mars_serve_bench, g_done_us) == 128 &&
+                  offsetof(mars_serve_bench, ins_linked_us) == 192,
+              "mars_serve_bench layout");
 
 extern "C" {
 
@@ -751,6 +769,191 @@ int mars_bench_queries(const mars_graph* g, mars_ctx* c, const float* dq, int64_
     return MARS_OK;
 }
 
+int mars_bench_serve(mars_graph* g, mars_ctx* cg, mars_ctx* ce, mars_serve_bench* b) {
+    MARS_CHECK(g && cg && ce && b && cg != ce && b->n_global >= 0 && b->n_episode >= 0 && b->max_batch >= 1 &&
+                   (b->n_global == 0 || (b->g_queries && b->g_arrival_us && b->gcfg && b->g_done_us && b->g_batch)) &&
+                   (b->n_episode == 0 || (b->e_queries && b->e_arrival_us && b->ecfgs && b->e_done_us)) &&
+                   b->n_insert >= 0 && (b->n_insert == 0 || (b->ins_emb && b->ins_mods && b->ins_ts &&
+                   b->ins_stats && b->ins_start_us && b->insert_batch > 0 && b->insert_rate > 0.0)) &&
+                   (!b->link_deferred || (b->knn_k >= 1 && b->knn_k <= 16 && b->max_link >= 1)),
+               MARS_ERR_INVALID, "bad serving benchmark arguments");
+    using clk = std::chrono::steady_clock;
+    const auto start = clk::now();
+    auto since = [&]() { return std::chrono::duration<double, std::micro>(clk::now() - start).count(); };
+    auto wait_until = [&](double us) {
+        std::this_thread::sleep_until(start + std::chrono::duration_cast<clk::duration>(
+                                                  std::chrono::duration<double, std::micro>(us)));
+    };
+    const int64_t D = g->g.d;
+    const bool deferred = b->link_deferred != 0 && b->n_insert > 0;
+    const int32_t n_base = __atomic_load_n(&g->g.n, __ATOMIC_ACQUIRE);
+    const int32_t ib = b->n_insert > 0 ? b->insert_batch : 1;
+    const int32_t nb_ins = (b->n_insert + ib - 1) / ib;
+    std::atomic<int> ins_rc{MARS_OK};
+    std::atomic<bool> writer_done{false};
+    int ep_rc = MARS_OK;
+    std::string ins_err, ep_err;
+    // Deferred mode: the global server finds neighbour lists in its corpus passes and
+    // hands them over; the writer applies every graph change (inserts and links), so
+    // no thread waits on the graph mutex for another.
+    struct LinkJob {
+        int32_t first, count;
+        std::vector<int32_t> knn;
+    };
+    std::mutex jobs_mu;
+    std::deque<LinkJob> jobs;
+    std::atomic<bool> server_done{false};
+    int32_t linked_done = 0;                    // writer: nodes whose edges are linked
+    auto apply_links = [&](bool drain_all) {
+        for (;;) {
+            LinkJob job;
+            {
+                std::lock_guard<std::mutex> lk(jobs_mu);
+                if (jobs.empty()) return drain_all ? false : true;
+                job = std::move(jobs.front());
+                jobs.pop_front();
+            }
+            const int rc = mars_graph_link(g, job.first, job.count, b->knn_k, job.knn.data(), nullptr);
+            if (rc != MARS_OK) {
+                ins_err = mars_last_error();
+                ins_rc.store(rc);
+                return false;
+            }
+            const double t = since();
+            linked_done += job.count;
+            for (int32_t x = 0; x < nb_ins; ++x) {
+                const int64_t last = std::min<int64_t>(int64_t(x + 1) * ib, b->n_insert);
+                if (last <= linked_done && last > linked_done - job.count && b->ins_linked_us) b->ins_linked_us[x] = t;
+            }
+            if (!drain_all) return true;
+        }
+    };
+    std::thread writer([&]() {
+        for (int32_t j = 0; j < nb_ins && ins_rc.load() == MARS_OK; ++j) {
+            const int64_t first = int64_t(j) * ib;
+            const int32_t m = int32_t(std::min<int64_t>(ib, b->n_insert - first));
+            const double due = double(first) / b->insert_rate * 1e6;
+            if (deferred) {
+                // link what the server found while waiting for this insert's time
+                while (since() < due && ins_rc.load() == MARS_OK) {
+                    bool any;
+                    {
+                        std::lock_guard<std::mutex> lk(jobs_mu);
+                        any = !jobs.empty();
+                    }
+                    if (any) apply_links(false);
+                    else wait_until(std::min(due, since() + 100.0));
+                }
+            }
+            wait_until(due);
+            b->ins_start_us[j] = since();
+            const int rc = mars_graph_insert(g, m, b->ins_emb + first * D, b->ins_mods + first, b->ins_ts + first,
+                                             b->ins_ep ? b->ins_ep + first : nullptr, deferred ? 0 : b->knn_k,
+                                             nullptr, &b->ins_stats[j]);
+            if (rc != MARS_OK) {
+                ins_err = mars_last_error();
+                ins_rc.store(rc);
+            } else if (!deferred && b->ins_linked_us) {
+                b->ins_linked_us[j] = b->ins_start_us[j] + b->ins_stats[j].linked_us;
+            }
+        }
+        writer_done.store(true);
+        // the rest of the links, until the server has handed over its last list
+        while (deferred && ins_rc.load() == MARS_OK) {
+            const bool done = server_done.load();
+            bool any;
+            {
+                std::lock_guard<std::mutex> lk(jobs_mu);
+                any = !jobs.empty();
+            }
+            if (any) apply_links(true);
+            else if (done) break;
+            else wait_until(since() + 100.0);
+        }
+    });
+    std::thread episode([&]() {
+        mars_query_result out[64];
+        for (int32_t i = 0; i < b->n_episode && ep_rc == MARS_OK; ++i) {
+            wait_until(b->e_arrival_us[i]);
+            int32_t nr = 0;
+            ep_rc = query_impl(g, ce, nullptr, b->e_queries + int64_t(i) * D, b->t_q, &b->ecfgs[i], out, 64, &nr,
+                               nullptr);
+            b->e_done_us[i] = since();
+            if (ep_rc != MARS_OK) ep_err = mars_last_error();
+        }
+    });
+    int rc = MARS_OK;
+    const int32_t mb = b->max_batch;
+    std::vector<mars_query_result> out(size_t(mb) * 64);
+    std::vector<int32_t> nout(static_cast<size_t>(mb));
+    std::vector<float> tq(static_cast<size_t>(mb), b->t_q);
+    std::vector<int32_t> knn(size_t(std::max(b->max_link, 1)) * size_t(std::max(b->knn_k, 1)));
+    b->g_uncertified = 0;
+    b->g_overflow = 0;
+    b->link_calls = 0;
+    int32_t linked = n_base;                    // nodes below this id are linked
+    const int32_t n_end = n_base + b->n_insert;
+    int32_t i = 0;
+    while (rc == MARS_OK) {
+        const double now = since();
+        const bool g_wait = i < b->n_global && b->g_arrival_us[i] <= now;
+        int32_t n_pub = deferred ? __atomic_load_n(&g->g.n, __ATOMIC_ACQUIRE) : linked;
+        // the insert that published node `linked` started before its nodes were published
+        const bool l_wait = n_pub > linked &&
+                            (g_wait || now - b->ins_start_us[(linked - n_base) / ib] >= b->link_wait_us);
+        if (!g_wait && !l_wait) {
+            const bool links_left = deferred && linked < n_end && ins_rc.load() == MARS_OK;
+            if (i >= b->n_global && !links_left) break;
+            if (i >= b->n_global && writer_done.load() && n_pub == linked &&
+                __atomic_load_n(&g->g.n, __ATOMIC_ACQUIRE) == linked)
+                break;                           // the writer stopped early (its error is reported)
+            double next = now + 100.0;           // poll for published nodes
+            if (i < b->n_global) next = std::min(next, b->g_arrival_us[i]);
+            wait_until(next);
+            continue;
+        }
+        int32_t j = i;
+        if (g_wait) {
+            j = i + 1;
+            while (j < b->n_global && j - i < mb && b->g_arrival_us[j] <= now) ++j;
+        }
+        const int32_t cnt = l_wait ? std::min(n_pub - linked, b->max_link) : 0;
+        if (mb == 1 && !deferred) {
+            rc = query_impl(g, cg, nullptr, b->g_queries + int64_t(i) * D, b->t_q, b->gcfg, out.data(), 64,
+                            nout.data(), nullptr);
+        } else {
+            mars_batch_stats st{};
+            rc = mars_query_global_batch_knn(g, cg, b->g_queries + int64_t(i) * D, j - i, tq.data(), b->gcfg,
+                                             out.data(), 64, nout.data(), &st, linked, cnt, b->knn_k, knn.data());
+            b->g_uncertified += st.uncertified + st.overflow;
+            b->g_overflow += st.overflow;
+        }
+        const double done = since();
+        for (int32_t x = i; x < j; ++x) {
+            b->g_done_us[x] = done;
+            b->g_batch[x] = j - i;
+        }
+        i = j;
+        if (rc == MARS_OK && cnt > 0) {
+            LinkJob job{linked, cnt, std::vector<int32_t>(knn.begin(), knn.begin() + size_t(cnt) * b->knn_k)};
+            {
+                std::lock_guard<std::mutex> lk(jobs_mu);
+                jobs.push_back(std::move(job));
+            }
+            ++b->link_calls;
+            linked += cnt;
+        }
+    }
+    server_done.store(true);
+    std::string err = rc != MARS_OK ? std::string(mars_last_error()) : std::string();
+    episode.join();
+    writer.join();
+    if (rc != MARS_OK) return set_error(rc, "%s", err.c_str());
+    if (ep_rc != MARS_OK) return set_error(ep_rc, "%s", ep_err.c_str());
+    if (ins_rc.load() != MARS_OK) return set_error(ins_rc.load(), "%s", ins_err.c_str());
+    return MARS_OK;
+}
+
 int mars_bench_stream(mars_graph* g, mars_ctx* c, mars_stream_bench* b) {
     MARS_CHECK(g && c && b && b->d_queries && b->cfgs && b->query_lat_us && b->n_queries >= 0 && b->query_rate > 0.0 &&
                    b->stride >= g->g.d && b->n_insert >= 0 && (b->n_insert == 0 || (b->ins_emb && b->ins_mods &&
@@ -820,7 +1023,7 @@ int mars_query_batch(const mars_graph* gh, mars_ctx* ch, const float* dq, int32_
     if (timing) MARS_HIP(hipEventRecord(c.ev[0], s));
     BatchArgs a{};
     a.emb16 = g.emb16; a.n = n_live; a.d = g.d; a.qh = c.bq; a.q = Q; a.tq = c.btq; a.ts = g.ts; a.mods = g.mods;
-    a.lambda = cfg->time_decay_lambda; a.mod_filter = cfg->modality_filter; a.k = K; a.self_base = -1;
+    a.lambda = cfg->time_decay_lambda; a.mod_filter = cfg->modality_filter; a.k = K; a.q_plain = Q; a.self_base = -1;
     a.part = c.bpart; a.rows_per_range = rpr; a.n_rranges = nrr; a.n_qblocks = nqb;
     a.uniform_tq = std::all_of(h_tq, h_tq + Q, [&](float x) { return x == h_tq[0]; }) ? 1 : 0;
     MARS_TRY(launch_batch_scan(a, s));
@@ -856,10 +1059,19 @@ int mars_query_batch(const mars_graph* gh, mars_ctx* ch, const float* dq, int32_
 int mars_query_global_batch(const mars_graph* gh, mars_ctx* ch, const float* dq, int32_t Q, const float* h_tq,
                             const mars_retrieval_config* cfg, mars_query_result* out, int32_t cap,
                             int32_t* n_out, mars_batch_stats* stats) {
+    MARS_CHECK(Q > 0, MARS_ERR_INVALID, "bad arguments");
+    return mars_query_global_batch_knn(gh, ch, dq, Q, h_tq, cfg, out, cap, n_out, stats, 0, 0, 0, nullptr);
+}
+
+int mars_query_global_batch_knn(const mars_graph* gh, mars_ctx* ch, const float* dq, int32_t Q, const float* h_tq,
+                                const mars_retrieval_config* cfg, mars_query_result* out, int32_t cap,
+                                int32_t* n_out, mars_batch_stats* stats, int32_t knn_first, int32_t knn_count,
+                                int32_t knn_k, int32_t* out_knn) {
     using clk = std::chrono::steady_clock;
     const auto t0 = clk::now();
-    MARS_CHECK(gh && ch && dq && h_tq && cfg && n_out && Q > 0, MARS_ERR_INVALID, "bad arguments");
-    MARS_CHECK(cap >= 0 && (cap == 0 || out), MARS_ERR_INVALID, "bad output buffer");
+    MARS_CHECK(gh && ch && Q >= 0 && knn_count >= 0 && Q + knn_count > 0, MARS_ERR_INVALID, "bad arguments");
+    MARS_CHECK(Q == 0 || (dq && h_tq && cfg && n_out && cap >= 0 && (cap == 0 || out)), MARS_ERR_INVALID,
+               "bad query arguments");
     const Graph& g = gh->g;
     Ctx& c = ch->c;
     MARS_CHECK(g.d == c.d, MARS_ERR_INVALID, "graph dim %d != context dim %d", g.d, c.d);
@@ -867,100 +1079,139 @@ int mars_query_global_batch(const mars_graph* gh, mars_ctx* ch, const float* dq,
     MARS_CHECK(n_live <= c.max_nodes, MARS_ERR_CAPACITY, "graph has %d nodes, context sized for %d", n_live,
                c.max_nodes);
     MARS_CHECK(n_live > 0, MARS_ERR_INVALID, "empty graph");
-    MARS_CHECK(cfg->top_k > 0, MARS_ERR_INVALID, "top_k = %d", cfg->top_k);
-    const int32_t K = std::min(cfg->top_k, c.max_k);
-    const bool scoped = episode_scoped_active(g, *cfg);
-    const int32_t hops = scoped ? 0 : std::max(0, cfg->bfs_max_hops);
-    const int32_t rcap = cfg->max_results_returned > 0 ? cfg->max_results_returned : K;
-    MARS_CHECK(rcap <= c.res_cap, MARS_ERR_UNSUPPORTED, "max_results_returned %d exceeds %d", rcap, c.res_cap);
+    if (knn_count > 0) {
+        MARS_CHECK(knn_k >= 1 && knn_k <= 16 && out_knn, MARS_ERR_INVALID, "k-NN queries: knn_k %d, out_knn %p",
+                   knn_k, static_cast<void*>(out_knn));
+        MARS_CHECK(knn_first >= 0 && int64_t(knn_first) + knn_count <= n_live, MARS_ERR_INVALID,
+                   "k-NN queries: nodes [%d, %lld) are not all published (%d nodes)", knn_first,
+                   (long long)knn_first + knn_count, n_live);
+        MARS_CHECK(g.emb16 != nullptr && batch_dim_supported(g.d), MARS_ERR_UNSUPPORTED,
+                   "k-NN queries need the fp16 rows and embedding_dim in {256, 384, 512, 768}");
+    }
+    int32_t K = 0, hops = 0, rcap = 0;
+    bool fp16 = false, batched = false;
+    float lambda = 0.0f;
+    if (Q > 0) {
+        MARS_CHECK(cfg->top_k > 0, MARS_ERR_INVALID, "top_k = %d", cfg->top_k);
+        K = std::min(cfg->top_k, c.max_k);
+        const bool scoped = episode_scoped_active(g, *cfg);
+        hops = scoped ? 0 : std::max(0, cfg->bfs_max_hops);
+        rcap = cfg->max_results_returned > 0 ? cfg->max_results_returned : K;
+        MARS_CHECK(rcap <= c.res_cap, MARS_ERR_UNSUPPORTED, "max_results_returned %d exceeds %d", rcap, c.res_cap);
+        fp16 = (c.flags & MARS_CTX_USE_FP16) && g.emb16 != nullptr;
+        const bool boost = g.ep_ids && cfg->query_episode_id >= 0 && cfg->episode_same_boost > 0.0f;
+        lambda = cfg->time_decay_lambda;
+        batched = !scoped && g.emb16 && g.nrm && batch_dim_supported(g.d) && K <= kMultiCand && !boost &&
+                  lambda >= 0.0f && lambda <= FLT_MAX && hops < 255;
+    }
     MARS_TRY(use_device(c.device));
-    const bool fp16 = (c.flags & MARS_CTX_USE_FP16) && g.emb16 != nullptr;
-    const bool boost = g.ep_ids && cfg->query_episode_id >= 0 && cfg->episode_same_boost > 0.0f;
-    const float lambda = cfg->time_decay_lambda;
-    const bool batched = !scoped && g.emb16 && g.nrm && batch_dim_supported(g.d) && K <= kMultiCand && !boost &&
-                         lambda >= 0.0f && lambda <= FLT_MAX && hops < 255;
     mars_batch_stats st{};
     st.queries = Q;
     st.n_live = n_live;
     st.min_margin = FLT_MAX;
     std::vector<int32_t> q1;                    // queries the Q=1 path answers
-    if (batched) {
+    const int32_t Qg = batched ? Q : 0;         // global queries in the shared scan
+    const int32_t Qt = Qg + knn_count;          // + k-NN queries (plain dot products)
+    if (!batched) {
+        st.whole_batch_q1 = Q > 0 ? 1 : 0;
+        for (int32_t j = 0; j < Q; ++j) q1.push_back(j);
+    }
+    if (Qt > 0) {
         int32_t nrr = 0, nqb = 0;
         int64_t rpr = 0;
-        batch_grid(n_live, Q, &nrr, &nqb, &rpr);
+        batch_grid(n_live, Qt, &nrr, &nqb, &rpr);
         const int32_t kp = batch_kpart(kMultiCand);
-        MARS_TRY(ensure_batch_scratch(c, Q, int64_t(nqb) * nrr * 64 * kp));
-        MARS_TRY(ensure_multi_scratch(c, Q, rcap));
+        MARS_TRY(ensure_batch_scratch(c, Qt, int64_t(nqb) * nrr * 64 * kp));
+        if (Qg > 0) MARS_TRY(ensure_multi_scratch(c, Qg, rcap));
+        if (knn_count > c.mknn_cap) {
+            dfree(c.mknn);
+            c.mknn_cap = 0;
+            MARS_TRY(dmalloc(&c.mknn, size_t(knn_count) * 16));
+            c.mknn_cap = knn_count;
+        }
         hipStream_t s = c.stream;
         const bool timing = (c.flags & MARS_CTX_TIMING) != 0;
-        MARS_HIP(hipMemcpyAsync(c.btq, h_tq, size_t(Q) * sizeof(float), hipMemcpyHostToDevice, s));
-        MARS_TRY(launch_f32_to_f16_rows(dq, c.bq, int64_t(Q) * g.d, s));
-        MARS_TRY(launch_query_norms(dq, c.bq, Q, g.d, c.mqn, s));
+        if (Qg > 0) {
+            MARS_HIP(hipMemcpyAsync(c.btq, h_tq, size_t(Qg) * sizeof(float), hipMemcpyHostToDevice, s));
+            MARS_TRY(launch_f32_to_f16_rows(dq, c.bq, int64_t(Qg) * g.d, s));
+            MARS_TRY(launch_query_norms(dq, c.bq, Qg, g.d, c.mqn, s));
+        }
+        if (knn_count > 0)     // the k-NN queries are the nodes' own fp16 rows
+            MARS_HIP(hipMemcpyAsync(c.bq + int64_t(Qg) * g.d, g.emb16 + int64_t(knn_first) * g.d,
+                                    size_t(knn_count) * size_t(g.d) * sizeof(__half), hipMemcpyDeviceToDevice, s));
         if (timing) MARS_HIP(hipEventRecord(c.ev[0], s));
         BatchArgs b{};
-        b.emb16 = g.emb16; b.n = n_live; b.d = g.d; b.qh = c.bq; b.q = Q; b.tq = c.btq; b.ts = g.ts;
-        b.mods = g.mods; b.lambda = lambda; b.mod_filter = cfg->modality_filter; b.k = kMultiCand;
-        b.self_base = -1; b.part = c.bpart; b.rows_per_range = rpr; b.n_rranges = nrr; b.n_qblocks = nqb;
-        b.uniform_tq = std::all_of(h_tq, h_tq + Q, [&](float x) { return x == h_tq[0]; }) ? 1 : 0;
+        b.emb16 = g.emb16; b.n = n_live; b.d = g.d; b.qh = c.bq; b.q = Qt; b.tq = c.btq; b.ts = g.ts;
+        b.mods = g.mods; b.lambda = Qg > 0 ? lambda : 0.0f; b.mod_filter = Qg > 0 ? cfg->modality_filter : -1;
+        b.k = kMultiCand; b.q_plain = Qg; b.self_base = knn_count > 0 ? knn_first : -1; b.part = c.bpart;
+        b.rows_per_range = rpr; b.n_rranges = nrr; b.n_qblocks = nqb;
+        b.uniform_tq = (Qg == 0 || std::all_of(h_tq, h_tq + Qg, [&](float x) { return x == h_tq[0]; })) ? 1 : 0;
         MARS_TRY(launch_batch_scan(b, s));
-        MARS_TRY(launch_batch_merge(c.bpart, nrr, kp, Q, kMultiCand, c.bout, s));
+        MARS_TRY(launch_batch_merge(c.bpart, nrr, kp, Qt, kMultiCand, c.bout, s));
         if (timing) MARS_HIP(hipEventRecord(c.ev[1], s));
-        SeedArgs sa{};
-        sa.emb = fp16 ? static_cast<const void*>(g.emb16) : static_cast<const void*>(g.emb);
-        sa.fp16 = fp16 ? 1 : 0; sa.d = g.d; sa.ts = g.ts; sa.mods = g.mods; sa.queries = dq; sa.tq = c.btq;
-        sa.lambda = lambda; sa.mod_filter = cfg->modality_filter; sa.q = Q; sa.k = K; sa.cand = c.bout;
-        sa.qn = c.mqn; sa.nrm = g.nrm; sa.seeds = c.mseed; sa.status = c.mstat; sa.margin = c.mmargin;
-        MARS_TRY(launch_multi_seed(sa, s));
-        if (timing) MARS_HIP(hipEventRecord(c.ev[2], s));
-        auto* hdr = static_cast<ResultHeader*>(c.h_mres);
-        auto* rec = reinterpret_cast<mars_query_result*>(hdr + Q);
-        MultiArgs m{};
-        m.ro = g.ro; m.col = g.col; m.mods = g.mods; m.n_live = n_live; m.hops = hops;
-        m.hop_decay = cfg->bfs_score_decay; m.k = K; m.rcap = rcap; m.q = Q; m.seeds = c.mseed;
-        m.status = c.mstat; m.info = c.minfo; m.vlist = c.mvlist; m.vhop = c.mvhop; m.vpar = c.mvpar;
-        m.vro = c.mvro; m.vfin = c.mvfin; m.vscore = c.mvscore;
-        m.res = static_cast<ResultHeader*>(c.d_mres);
-        m.rec = reinterpret_cast<mars_query_result*>(m.res + Q);
-        MARS_TRY(launch_multi_bfs(m, s));
-        VisitScoreArgs va{};
-        va.emb = sa.emb; va.fp16 = sa.fp16; va.d = g.d; va.ts = g.ts; va.mods = g.mods; va.queries = dq;
-        va.tq = c.btq; va.lambda = lambda; va.mod_filter = cfg->modality_filter; va.q = Q; va.status = c.mstat;
-        va.info = c.minfo; va.vlist = c.mvlist; va.vfin = c.mvfin;
-        MARS_TRY(launch_visit_scores(va, s));
-        MARS_TRY(launch_multi_select(m, s));
-        if (timing) MARS_HIP(hipEventRecord(c.ev[3], s));
-        std::vector<float> margin(static_cast<size_t>(Q));
-        MARS_HIP(hipMemcpyAsync(margin.data(), c.mmargin, size_t(Q) * sizeof(float), hipMemcpyDeviceToHost, s));
+        if (knn_count > 0)
+            MARS_TRY(launch_knn_rerank(g.emb, knn_first, knn_count, g.d, c.bout + int64_t(Qg) * kMultiCand,
+                                       kMultiCand, knn_k, c.mknn, s));
+        std::vector<float> margin(static_cast<size_t>(Qg));
+        if (Qg > 0) {
+            SeedArgs sa{};
+            sa.emb = fp16 ? static_cast<const void*>(g.emb16) : static_cast<const void*>(g.emb);
+            sa.fp16 = fp16 ? 1 : 0; sa.d = g.d; sa.ts = g.ts; sa.mods = g.mods; sa.queries = dq; sa.tq = c.btq;
+            sa.lambda = lambda; sa.mod_filter = cfg->modality_filter; sa.q = Qg; sa.k = K; sa.cand = c.bout;
+            sa.qn = c.mqn; sa.nrm = g.nrm; sa.seeds = c.mseed; sa.status = c.mstat; sa.margin = c.mmargin;
+            MARS_TRY(launch_multi_seed(sa, s));
+            if (timing) MARS_HIP(hipEventRecord(c.ev[2], s));
+            MultiArgs m{};
+            m.ro = g.ro; m.col = g.col; m.mods = g.mods; m.n_live = n_live; m.hops = hops;
+            m.hop_decay = cfg->bfs_score_decay; m.k = K; m.rcap = rcap; m.q = Qg; m.seeds = c.mseed;
+            m.status = c.mstat; m.info = c.minfo; m.vlist = c.mvlist; m.vhop = c.mvhop; m.vpar = c.mvpar;
+            m.vro = c.mvro; m.vfin = c.mvfin; m.vscore = c.mvscore;
+            m.res = static_cast<ResultHeader*>(c.d_mres);
+            m.rec = reinterpret_cast<mars_query_result*>(m.res + Qg);
+            MARS_TRY(launch_multi_bfs(m, s));
+            VisitScoreArgs va{};
+            va.emb = sa.emb; va.fp16 = sa.fp16; va.d = g.d; va.ts = g.ts; va.mods = g.mods; va.queries = dq;
+            va.tq = c.btq; va.lambda = lambda; va.mod_filter = cfg->modality_filter; va.q = Qg;
+            va.status = c.mstat; va.info = c.minfo; va.vlist = c.mvlist; va.vfin = c.mvfin;
+            MARS_TRY(launch_visit_scores(va, s));
+            MARS_TRY(launch_multi_select(m, s));
+            if (timing) MARS_HIP(hipEventRecord(c.ev[3], s));
+            MARS_HIP(hipMemcpyAsync(margin.data(), c.mmargin, size_t(Qg) * sizeof(float), hipMemcpyDeviceToHost, s));
+        }
+        if (knn_count > 0)
+            MARS_HIP(hipMemcpyAsync(out_knn, c.mknn, size_t(knn_count) * size_t(knn_k) * sizeof(int32_t),
+                                    hipMemcpyDeviceToHost, s));
         MARS_HIP(hipStreamSynchronize(s));
-        for (int32_t j = 0; j < Q; ++j) {
-            const ResultHeader h = hdr[j];
-            if (h.count < 0) {
-                if (h.visited == kMultiOverflow) ++st.overflow;
-                else ++st.uncertified;
-                q1.push_back(j);
-                continue;
+        if (Qg > 0) {
+            const auto* hdr = static_cast<const ResultHeader*>(c.h_mres);
+            const auto* rec = reinterpret_cast<const mars_query_result*>(hdr + Qg);
+            for (int32_t j = 0; j < Qg; ++j) {
+                const ResultHeader h = hdr[j];
+                if (h.count < 0) {
+                    if (h.visited == kMultiOverflow) ++st.overflow;
+                    else ++st.uncertified;
+                    q1.push_back(j);
+                    continue;
+                }
+                const int32_t nw = std::min(h.count, cap);
+                if (nw > 0)
+                    std::memcpy(out + int64_t(j) * cap, rec + int64_t(j) * rcap, size_t(nw) * sizeof(mars_query_result));
+                n_out[j] = h.count;
+                ++st.batched;
+                st.min_margin = std::min(st.min_margin, margin[size_t(j)]);
             }
-            const int32_t nw = std::min(h.count, cap);
-            if (nw > 0)
-                std::memcpy(out + int64_t(j) * cap, rec + int64_t(j) * rcap, size_t(nw) * sizeof(mars_query_result));
-            n_out[j] = h.count;
-            ++st.batched;
-            st.min_margin = std::min(st.min_margin, margin[size_t(j)]);
+            if (timing) {
+                float ms = 0.0f;
+                MARS_HIP(hipEventElapsedTime(&ms, c.ev[0], c.ev[1]));
+                st.gpu_ms_scan = ms;
+                MARS_HIP(hipEventElapsedTime(&ms, c.ev[1], c.ev[2]));
+                st.gpu_ms_seeds = ms;
+                MARS_HIP(hipEventElapsedTime(&ms, c.ev[2], c.ev[3]));
+                st.gpu_ms_bfs = ms;
+                MARS_HIP(hipEventElapsedTime(&ms, c.ev[0], c.ev[3]));
+                st.gpu_ms_total = ms;
+            }
         }
-        if (timing) {
-            float ms = 0.0f;
-            MARS_HIP(hipEventElapsedTime(&ms, c.ev[0], c.ev[1]));
-            st.gpu_ms_scan = ms;
-            MARS_HIP(hipEventElapsedTime(&ms, c.ev[1], c.ev[2]));
-            st.gpu_ms_seeds = ms;
-            MARS_HIP(hipEventElapsedTime(&ms, c.ev[2], c.ev[3]));
-            st.gpu_ms_bfs = ms;
-            MARS_HIP(hipEventElapsedTime(&ms, c.ev[0], c.ev[3]));
-            st.gpu_ms_total = ms;
-        }
-    } else {
-        st.whole_batch_q1 = 1;
-        for (int32_t j = 0; j < Q; ++j) q1.push_back(j);
     }
     const auto t1 = clk::now();
     for (const int32_t j : q1)
@@ -973,8 +1224,9 @@ int mars_query_global_batch(const mars_graph* gh, mars_ctx* ch, const float* dq,
     return MARS_OK;
 }
 
-int mars_graph_knn(mars_graph* gh, int32_t k, int32_t* nbrs) {
-    MARS_CHECK(gh && nbrs && k >= 1 && k <= 16, MARS_ERR_INVALID, "k-NN: bad arguments (k=%d)", k);
+int mars_graph_knn_blocked(mars_graph* gh, int32_t k, int32_t block_rows, int32_t* nbrs) {
+    MARS_CHECK(gh && nbrs && k >= 1 && k <= 16 && block_rows > 0, MARS_ERR_INVALID,
+               "k-NN: bad arguments (k=%d, block_rows=%d)", k, block_rows);
     std::lock_guard<std::mutex> lock(gh->mu);
     Graph& g = gh->g;
     MARS_CHECK(g.emb16 != nullptr, MARS_ERR_UNSUPPORTED, "k-NN reads the fp16 corpus: enable it first");
@@ -982,9 +1234,10 @@ int mars_graph_knn(mars_graph* gh, int32_t k, int32_t* nbrs) {
     MARS_TRY(use_device(g.device));
     constexpr int32_t kChunk = 1024;                 // queries per launch (16 query blocks)
     constexpr int32_t kCand = 16;
+    const int64_t B = std::min<int64_t>(block_rows, g.n);
     int32_t nrr = 0, nqb = 0;
     int64_t rpr = 0;
-    batch_grid(g.n, kChunk, &nrr, &nqb, &rpr);
+    batch_grid(B, kChunk, &nrr, &nqb, &rpr);         // the largest block sizes the scratch
     float* tq = nullptr; uint64_t* part = nullptr; uint64_t* cand = nullptr; int32_t* dn = nullptr;
     hipStream_t s = nullptr;
     int rc = MARS_OK;
@@ -997,16 +1250,22 @@ int mars_graph_knn(mars_graph* gh, int32_t k, int32_t* nbrs) {
     hipError_t e = hipStreamCreateWithFlags(&s, hipStreamNonBlocking);
     if (e == hipSuccess) e = hipMemsetAsync(tq, 0, kChunk * sizeof(float), s);
     if (e != hipSuccess) { cleanup(); return set_error(MARS_ERR_HIP, "k-NN setup: %s", hipGetErrorString(e)); }
-    for (int64_t q0 = 0; q0 < g.n && rc == MARS_OK; q0 += kChunk) {
-        const int32_t q = int32_t(std::min<int64_t>(kChunk, g.n - q0));
-        BatchArgs a{};
-        a.emb16 = g.emb16; a.n = g.n; a.d = g.d; a.qh = g.emb16 + q0 * g.d; a.q = q; a.tq = tq; a.ts = g.ts;
-        a.mods = g.mods; a.lambda = 0.0f; a.mod_filter = -1; a.k = kCand; a.self_base = q0; a.part = part;
-        a.uniform_tq = 1;
-        a.rows_per_range = rpr; a.n_rranges = nrr; a.n_qblocks = (q + 63) / 64;
-        rc = launch_batch_scan(a, s);
-        if (rc == MARS_OK) rc = launch_batch_merge(part, nrr, kCand, q, kCand, cand, s);
-        if (rc == MARS_OK) rc = launch_knn_rerank(g.emb, q0, q, g.d, cand, kCand, k, dn + q0 * k, s);
+    // block [r0, r1): rows, queries and candidate ids relative to r0
+    for (int64_t r0 = 0; r0 < g.n && rc == MARS_OK; r0 += B) {
+        const int64_t nb = std::min<int64_t>(B, g.n - r0);
+        batch_grid(nb, kChunk, &nrr, &nqb, &rpr);
+        for (int64_t q0 = 0; q0 < nb && rc == MARS_OK; q0 += kChunk) {
+            const int32_t q = int32_t(std::min<int64_t>(kChunk, nb - q0));
+            BatchArgs a{};
+            a.emb16 = g.emb16 + r0 * g.d; a.n = nb; a.d = g.d; a.qh = g.emb16 + (r0 + q0) * g.d; a.q = q; a.tq = tq;
+            a.ts = g.ts + r0; a.mods = g.mods + r0; a.lambda = 0.0f; a.mod_filter = -1; a.k = kCand; a.q_plain = 0; a.self_base = q0;
+            a.part = part; a.uniform_tq = 1;
+            a.rows_per_range = rpr; a.n_rranges = nrr; a.n_qblocks = (q + 63) / 64;
+            rc = launch_batch_scan(a, s);
+            if (rc == MARS_OK) rc = launch_batch_merge(part, nrr, kCand, q, kCand, cand, s);
+            if (rc == MARS_OK)
+                rc = launch_knn_rerank(g.emb + r0 * g.d, q0, q, g.d, cand, kCand, k, dn + (r0 + q0) * k, s);
+        }
     }
     if (rc == MARS_OK) {
         e = hipStreamSynchronize(s);
@@ -1014,7 +1273,19 @@ int mars_graph_knn(mars_graph* gh, int32_t k, int32_t* nbrs) {
         if (e != hipSuccess) rc = set_error(MARS_ERR_HIP, "k-NN: %s", hipGetErrorString(e));
     }
     cleanup();
+    if (rc == MARS_OK && B < g.n) {
+        for (int64_t i = 0; i < int64_t(g.n); ++i) {
+            const int32_t off = int32_t(i / B * B);
+            for (int32_t j = 0; j < k; ++j)
+                if (nbrs[i * k + j] >= 0) nbrs[i * k + j] += off;
+        }
+    }
     return rc;
+}
+
+int mars_graph_knn(mars_graph* gh, int32_t k, int32_t* nbrs) {
+    MARS_CHECK(gh, MARS_ERR_INVALID, "null graph");
+    return mars_graph_knn_blocked(gh, k, std::max<int32_t>(1, gh->g.n), nbrs);
 }
 
 int mars_ctx_last_scores(mars_ctx* ch, float* h, int64_t n) {

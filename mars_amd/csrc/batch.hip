@@ -106,7 +106,8 @@ __global__ __launch_bounds__(kBWaves * 64) void k_batch_scan(BatchArgs a) {
     const float tq = qvalid ? a.tq[myq] : 0.0f;
     const bool uni = a.uniform_tq != 0;
     const float tq0 = a.tq[0];
-    const int64_t self_id = (a.self_base >= 0 && qvalid) ? a.self_base + myq : -1;
+    const bool plain = myq >= a.q_plain;       // neighbour search: dot product only
+    const int64_t self_id = (a.self_base >= 0 && qvalid && plain) ? a.self_base + (myq - a.q_plain) : -1;
     uint64_t list[K];
 #pragma unroll
     for (int j = 0; j < K; ++j) list[j] = kEmptyKey;
@@ -170,7 +171,8 @@ __global__ __launch_bounds__(kBWaves * 64) void k_batch_scan(BatchArgs a) {
             for (int j = 0; j < nr; ++j) {
                 // fused score: dot * w (the reference's order), filtered rows -FLT_MAX
                 float s;
-                if (!s_keep[wave][j]) s = -FLT_MAX;
+                if (plain) s = s_stage[wave][j][lane];
+                else if (!s_keep[wave][j]) s = -FLT_MAX;
                 else if (uni) s = s_stage[wave][j][lane] * s_w[wave][j];
                 else if (a.lambda != 0.0f) s = s_stage[wave][j][lane] * expf(-a.lambda * fmaxf(0.0f, tq - s_w[wave][j]));
                 else s = s_stage[wave][j][lane];
@@ -376,13 +378,15 @@ void k_batch_gemm(BatchArgs a) {
             for (int i = 0; i < 4; ++i) {
                 const int ql = wq * 64 + qi * 16 + 4 * kg + i;
                 const int q = q0 + ql;
-                const int64_t self = a.self_base >= 0 ? a.self_base + q : -1;
+                const bool plain = q >= a.q_plain;
+                const int64_t self = (a.self_base >= 0 && plain) ? a.self_base + (q - a.q_plain) : -1;
                 const float tqq = uni ? 0.0f : sh.tq[ql];
 #pragma unroll
                 for (int ri = 0; ri < 4; ++ri) {
                     const int64_t row = t0 + ri * 16 + m;
                     float sc;
-                    if (!kp[ri]) sc = -FLT_MAX;
+                    if (plain) sc = acc[qi][ri][i];
+                    else if (!kp[ri]) sc = -FLT_MAX;
                     else if (uni) sc = acc[qi][ri][i] * wv[ri];
                     else if (a.lambda != 0.0f) sc = acc[qi][ri][i] * expf(-a.lambda * fmaxf(0.0f, tqq - wv[ri]));
                     else sc = acc[qi][ri][i];

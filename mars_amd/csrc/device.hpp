@@ -238,5 +238,38 @@ __device__ inline float fuse_score(float dot, float ts, int32_t mod, int32_t ep,
 }
 
 
+// ---- row-norm bounds of the fp16 copy (batched global certificate) -------------------
+constexpr float kHalfMinNormal = 6.103515625e-05f;   // 2^-14
+
+// fp32 bit pattern of a value >= v (v >= 0); NaN stays NaN
+__device__ inline uint32_t up_bits(double v) {
+    if (!(v == v)) return 0x7fc00000u;
+    float f = float(v);
+    if (double(f) < v) f = nextafterf(f, __builtin_inff());
+    return __float_as_uint(f);
+}
+
+__device__ inline double wave_sum_f64(double v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+// max that lets a NaN through (the certificate must then fail)
+__device__ inline double max_nan(double m, double v) { return (v <= m) ? m : v; }
+
+// Raises nrm[0..2] to |e|, |e16| and |ftz(e16) - e| of one row whose per-lane sums of
+// squares (fp64) the calling wave holds; lane 0 issues the atomics.
+__device__ inline void raise_row_norms(double s32, double s16, double sd, uint32_t* nrm) {
+    s32 = wave_sum_f64(s32);
+    s16 = wave_sum_f64(s16);
+    sd = wave_sum_f64(sd);
+    if ((threadIdx.x & 63u) == 0) {
+        atomicMax(nrm + 0, up_bits(sqrt(s32)));
+        atomicMax(nrm + 1, up_bits(sqrt(s16)));
+        atomicMax(nrm + 2, up_bits(sqrt(sd)));
+    }
+}
+
 }  // namespace
 }  // namespace mars

@@ -32,7 +32,7 @@
 //           like a neighbour id at or above its node count.
 //       Old column data is never overwritten.
 // ============================================================================
-#include "internal.hpp"
+#include "device.hpp"
 
 #include <algorithm>
 #include <chrono>
@@ -46,6 +46,67 @@ constexpr int32_t kCopySlot = INT32_MIN;    // tail value: filled by a relocatio
 constexpr int64_t kRegionAlign = 64;        // 256 bytes of col
 constexpr int32_t kInsertChunk = 1024;      // k-NN queries per batched-scan launch
 constexpr int32_t kKnnCand = 16;            // fp16 candidates rescored per new node
+
+// Step 1 of an insert in one launch: the staged block (rows | modalities | times |
+// episode ids | episode members | episode offsets) is scattered into the graph; each
+// new row is also converted to fp16 (round to nearest even, as k_convert_f16) and its
+// norms raise the fp16 error bounds. One wave per row, the attributes grid-stride.
+struct StageArgs {
+    const uint32_t* rows;      // n_new x d fp32 bit patterns
+    const int32_t* mods;
+    const float* ts;
+    const int32_t* ep;         // null: no episode ids
+    const int32_t* mem;        // null: no episode CSR
+    const int32_t* off;
+    float* emb;
+    __half* emb16;             // null: no fp16 copy
+    uint32_t* nrm;
+    int32_t* g_mods;
+    float* g_ts;
+    int32_t* g_ep;
+    int32_t* g_mem;
+    int32_t* g_off;
+    int64_t n_old;
+    int32_t n_new;
+    int32_t d;
+    int32_t ne_new;
+    int32_t mem_at;            // member_total
+    int32_t off_at;            // num_eps + 1
+};
+
+__global__ __launch_bounds__(256) void k_stage_insert(StageArgs a) {
+    const int64_t tid = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int64_t stride = int64_t(gridDim.x) * blockDim.x;
+    const int lane = int(threadIdx.x & 63u);
+    for (int64_t r = tid >> 6; r < a.n_new; r += stride >> 6) {
+        const uint32_t* src = a.rows + r * a.d;
+        uint32_t* dst = reinterpret_cast<uint32_t*>(a.emb) + (a.n_old + r) * a.d;
+        double s32 = 0.0, s16 = 0.0, sd = 0.0;
+        for (int i = lane; i < a.d; i += 64) {
+            const uint32_t bits = src[i];
+            dst[i] = bits;
+            if (a.emb16) {
+                const float x = __uint_as_float(bits);
+                const __half h = __float2half_rn(x);
+                a.emb16[(a.n_old + r) * a.d + i] = h;
+                const float hv = __half2float(h);
+                const float hf = fabsf(hv) < kHalfMinNormal ? 0.0f : hv;
+                s32 += double(x) * double(x);
+                s16 += double(hv) * double(hv);
+                const double df = double(hf) - double(x);
+                sd += df * df;
+            }
+        }
+        if (a.emb16 && a.nrm) raise_row_norms(s32, s16, sd, a.nrm);
+    }
+    for (int64_t i = tid; i < a.n_new; i += stride) {
+        a.g_mods[a.n_old + i] = a.mods[i];
+        a.g_ts[a.n_old + i] = a.ts[i];
+        if (a.g_ep) a.g_ep[a.n_old + i] = a.ep[i];
+        if (a.g_mem) a.g_mem[a.mem_at + i] = a.mem[i];
+    }
+    for (int64_t e = tid; e < a.ne_new; e += stride) a.g_off[a.off_at + e] = a.off[e];
+}
 
 __global__ void k_patch_data(PatchArgs a) {
     const int64_t tid = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -144,7 +205,7 @@ int insert_knn(Graph& g, int64_t first, int32_t nq, int64_t n, int32_t k, hipStr
         BatchArgs a{};
         a.emb16 = g.emb16; a.n = n; a.d = g.d; a.qh = g.emb16 + (first + c0) * g.d; a.q = q; a.tq = g.ins_tq;
         a.ts = g.ts; a.mods = g.mods; a.lambda = 0.0f; a.mod_filter = -1; a.k = kKnnCand;
-        a.self_base = first + c0; a.part = g.ins_part; a.rows_per_range = rpr; a.n_rranges = nrr;
+        a.q_plain = 0; a.self_base = first + c0; a.part = g.ins_part; a.rows_per_range = rpr; a.n_rranges = nrr;
         a.n_qblocks = nqb; a.uniform_tq = 1;
         MARS_TRY(launch_batch_scan(a, s));
         MARS_TRY(launch_batch_merge(g.ins_part, nrr, kKnnCand, q, kKnnCand, g.ins_cand, s));
@@ -153,7 +214,191 @@ int insert_knn(Graph& g, int64_t first, int32_t nq, int64_t n, int32_t k, hipStr
     return MARS_OK;
 }
 
+// Copies rows out of col: spec holds n x {start, len, out offset}; one wave per row.
+__global__ void k_gather_rows(const int32_t* __restrict__ col, const int64_t* __restrict__ spec, int32_t n,
+                              int32_t* __restrict__ out) {
+    const int64_t wave = (int64_t(blockIdx.x) * blockDim.x + threadIdx.x) >> 6;
+    const int64_t nwaves = (int64_t(gridDim.x) * blockDim.x) >> 6;
+    const int lane = int(threadIdx.x & 63u);
+    for (int64_t r = wave; r < n; r += nwaves) {
+        const int64_t start = spec[3 * r], len = spec[3 * r + 1], off = spec[3 * r + 2];
+        for (int64_t i = lane; i < len; i += 64) out[off + i] = col[start + i];
+    }
+}
+
+// A planned edit of col: relocations (device copies of old rows into the tail), appends
+// into row slack, the tail region [base, cursor) and the new row words.
+struct Patch {
+    std::vector<int64_t> reloc, app, rows;
+    std::vector<int32_t> tail;
+    int64_t base = 0, cursor = 0, added = 0;
+    int32_t max_deg = 0, n_reloc = 0, n_inplace = 0;
+    int64_t place(int64_t cap) {
+        const int64_t at = cursor;
+        tail.resize(size_t(at + cap - base), -1);
+        cursor += cap;
+        return at;
+    }
+};
+
+// Writes the column data, then publishes the row words (a later kernel on the same
+// stream), and updates the host mirrors.
+int commit_patch(Graph& g, Patch& p, hipStream_t s) {
+    const size_t b_reloc = p.reloc.size() * sizeof(int64_t), b_app = p.app.size() * sizeof(int64_t);
+    const size_t b_rows = p.rows.size() * sizeof(int64_t), b_tail = p.tail.size() * sizeof(int32_t);
+    const size_t total = b_reloc + b_app + b_rows + b_tail + 64;
+    MARS_TRY(grow_pinned<char>(&g.ins_pin, &g.ins_pin_bytes, total));
+    MARS_TRY(grow_device(&g.ins_dev, &g.ins_dev_bytes, total));
+    char* pin = static_cast<char*>(g.ins_pin);
+    char* dev = static_cast<char*>(g.ins_dev);
+    size_t off = 0;
+    auto put = [&](const void* src, size_t bytes) {
+        const size_t at = off;
+        if (bytes) std::memcpy(pin + at, src, bytes);
+        off += (bytes + 15) / 16 * 16;
+        return at;
+    };
+    const size_t o_reloc = put(p.reloc.data(), b_reloc), o_app = put(p.app.data(), b_app);
+    const size_t o_rows = put(p.rows.data(), b_rows), o_tail = put(p.tail.data(), b_tail);
+    MARS_HIP(hipMemcpyAsync(dev, pin, off, hipMemcpyHostToDevice, s));
+    PatchArgs pa{};
+    pa.col = g.col; pa.ro = g.ro; pa.rcap = g.rcap;
+    pa.reloc = reinterpret_cast<const int64_t*>(dev + o_reloc); pa.n_reloc = int32_t(p.reloc.size() / 3);
+    pa.tail = reinterpret_cast<const int32_t*>(dev + o_tail); pa.tail_base = p.base;
+    pa.n_tail = int64_t(p.tail.size());
+    pa.app = reinterpret_cast<const int64_t*>(dev + o_app); pa.n_app = int32_t(p.app.size() / 2);
+    pa.rows = reinterpret_cast<const int64_t*>(dev + o_rows); pa.n_rows = int32_t(p.rows.size() / 3);
+    const int64_t data_work = std::max<int64_t>({int64_t(pa.n_reloc) * 64, pa.n_tail, int64_t(pa.n_app)});
+    MARS_LAUNCH(k_patch_data, dim3(patch_grid(data_work)), dim3(256), 0, s, pa);
+    MARS_LAUNCH(k_patch_rows, dim3(patch_grid(pa.n_rows)), dim3(256), 0, s, pa);
+    MARS_HIP(hipStreamSynchronize(s));
+    for (size_t i = 0; i < p.rows.size(); i += 3) {
+        g.ro_h[size_t(p.rows[i])] = p.rows[i + 1];
+        g.rcap_h[size_t(p.rows[i])] = int32_t(p.rows[i + 2]);
+    }
+    if (p.cursor > p.base) g.e_used = p.cursor;
+    g.max_deg = p.max_deg;
+    g.e = int32_t(std::min<int64_t>(int64_t(g.e) + p.added, INT32_MAX));
+    return MARS_OK;
+}
+
 }  // namespace
+
+// k-NN edges of nodes [first, first + count) (already published), knn: count x k ids
+// among [0, g.n): the edge set becomes E u {(u, v), (v, u)} for every listed neighbour
+// v != u; rows stay ascending and free of duplicates. Rows that only gain ids above
+// their last entry and have slack append in place; the others are rewritten whole
+// into a fresh tail region (the host gathers their current content first).
+// Caller holds the graph mutex.
+int link_knn_apply(Graph& g, int32_t first, int32_t count, int32_t k, const int32_t* knn, hipStream_t s,
+                   mars_insert_stats* st) {
+    const int32_t n = g.n;
+    // rows touched: the linked nodes and their neighbours
+    std::vector<int32_t> touched;
+    touched.reserve(size_t(count) * size_t(k + 1));
+    for (int32_t i = 0; i < count; ++i) {
+        touched.push_back(first + i);
+        for (int32_t j = 0; j < k; ++j) {
+            const int32_t v = knn[size_t(i) * k + j];
+            if (v >= 0 && v < n && v != first + i) touched.push_back(v);
+        }
+    }
+    std::sort(touched.begin(), touched.end());
+    touched.erase(std::unique(touched.begin(), touched.end()), touched.end());
+    // gather their current content
+    std::vector<int64_t> spec(touched.size() * 3);
+    int64_t total = 0;
+    for (size_t i = 0; i < touched.size(); ++i) {
+        const int64_t w = g.ro_h[size_t(touched[i])];
+        spec[3 * i] = int64_t(uint32_t(w));
+        spec[3 * i + 1] = w >> 32;
+        spec[3 * i + 2] = total;
+        total += w >> 32;
+    }
+    const size_t b_spec = spec.size() * sizeof(int64_t), b_out = size_t(total) * sizeof(int32_t);
+    MARS_TRY(grow_pinned<char>(&g.ins_pin, &g.ins_pin_bytes, b_spec + b_out + 64));
+    MARS_TRY(grow_device(&g.ins_dev, &g.ins_dev_bytes, b_spec + b_out + 64));
+    char* pin = static_cast<char*>(g.ins_pin);
+    char* dev = static_cast<char*>(g.ins_dev);
+    const size_t o_out = (b_spec + 15) / 16 * 16;
+    std::memcpy(pin, spec.data(), b_spec);
+    MARS_HIP(hipMemcpyAsync(dev, pin, b_spec, hipMemcpyHostToDevice, s));
+    if (!touched.empty())
+        MARS_LAUNCH(k_gather_rows, dim3(patch_grid(int64_t(touched.size()) * 64)), dim3(256), 0, s, g.col,
+                    reinterpret_cast<const int64_t*>(dev), int32_t(touched.size()),
+                    reinterpret_cast<int32_t*>(dev + o_out));
+    if (b_out) MARS_HIP(hipMemcpyAsync(pin + o_out, dev + o_out, b_out, hipMemcpyDeviceToHost, s));
+    MARS_HIP(hipStreamSynchronize(s));
+    const int32_t* content = reinterpret_cast<const int32_t*>(pin + o_out);
+    auto row_of = [&](int32_t v) {
+        const size_t i = size_t(std::lower_bound(touched.begin(), touched.end(), v) - touched.begin());
+        const int32_t* at = content + spec[3 * i + 2];            // offset in the gathered copy
+        return std::make_pair(at, at + spec[3 * i + 1]);
+    };
+    // directed additions not already present
+    std::vector<std::pair<int32_t, int32_t>> add;
+    for (int32_t i = 0; i < count; ++i) {
+        const int32_t u = first + i;
+        for (int32_t j = 0; j < k; ++j) {
+            const int32_t v = knn[size_t(i) * k + j];
+            if (v < 0 || v >= n || v == u) continue;
+            add.emplace_back(u, v);
+            add.emplace_back(v, u);
+        }
+    }
+    std::sort(add.begin(), add.end());
+    add.erase(std::unique(add.begin(), add.end()), add.end());
+    add.erase(std::remove_if(add.begin(), add.end(), [&](const std::pair<int32_t, int32_t>& e) {
+                  const auto r = row_of(e.first);
+                  return std::find(r.first, r.second, e.second) != r.second;   // rows may be unsorted
+              }), add.end());
+    Patch p;
+    p.base = align_up(g.e_used, kRegionAlign);
+    p.cursor = p.base;
+    p.max_deg = g.max_deg;
+    std::vector<int32_t> merged;
+    for (size_t i = 0, j = 0; i < add.size(); i = j) {
+        const int32_t r = add[i].first;
+        while (j < add.size() && add[j].first == r) ++j;
+        const auto row = row_of(r);
+        const int64_t len = row.second - row.first, a = int64_t(j - i);
+        const int64_t w = g.ro_h[size_t(r)];
+        const int64_t start = int64_t(uint32_t(w)), cap = g.rcap_h[size_t(r)];
+        const bool ascending = std::is_sorted(row.first, row.second);
+        const int64_t nlen = len + a;
+        int64_t nstart = start, ncap = cap;
+        if (ascending && (len == 0 || add[i].second > row.second[-1]) && nlen <= cap) {
+            for (size_t x = i; x < j; ++x) {
+                p.app.push_back(start + len + int64_t(x - i));
+                p.app.push_back(add[x].second);
+            }
+            ++p.n_inplace;
+        } else {
+            merged.assign(row.first, row.second);
+            for (size_t x = i; x < j; ++x) merged.push_back(add[x].second);
+            std::sort(merged.begin(), merged.end());
+            ncap = row_capacity(nlen);
+            nstart = p.place(ncap);
+            std::memcpy(p.tail.data() + (nstart - p.base), merged.data(), merged.size() * sizeof(int32_t));
+            ++p.n_reloc;
+        }
+        p.rows.push_back(r); p.rows.push_back((nlen << 32) | int64_t(uint32_t(nstart))); p.rows.push_back(ncap);
+        p.max_deg = std::max<int32_t>(p.max_deg, int32_t(nlen));
+        p.added += a;
+    }
+    MARS_CHECK(p.cursor <= g.cap_e && p.cursor <= int64_t(UINT32_MAX), MARS_ERR_CAPACITY,
+               "link: edge capacity %lld too small (used %lld, this link needs %lld)", (long long)g.cap_e,
+               (long long)g.e_used, (long long)(p.cursor - g.e_used));
+    if (!p.rows.empty()) MARS_TRY(commit_patch(g, p, s));
+    if (st) {
+        st->first_node = first;
+        st->nodes_added = count;
+        st->edges_added = p.added;
+        st->rows_relocated = p.n_reloc;
+        st->rows_appended = p.n_inplace;
+    }
+    return MARS_OK;
+}
 
 int graph_insert_free(Graph& g) {
     if (g.ins_pin) (void)hipHostFree(g.ins_pin);
@@ -257,13 +502,7 @@ extern "C" int mars_graph_insert(mars_graph* gh, int32_t n_new, const float* emb
     std::memcpy(pin, emb, row_bytes);
     std::memcpy(p_mods, mods, att_bytes);
     std::memcpy(p_ts, ts, att_bytes);
-    MARS_HIP(hipMemcpyAsync(g.emb + int64_t(n_old) * D, pin, row_bytes, hipMemcpyHostToDevice, s));
-    MARS_HIP(hipMemcpyAsync(g.mods + n_old, p_mods, att_bytes, hipMemcpyHostToDevice, s));
-    MARS_HIP(hipMemcpyAsync(g.ts + n_old, p_ts, att_bytes, hipMemcpyHostToDevice, s));
-    if (ep_ids) {
-        std::memcpy(p_ep, ep_ids, att_bytes);
-        MARS_HIP(hipMemcpyAsync(g.ep_ids + n_old, p_ep, att_bytes, hipMemcpyHostToDevice, s));
-    }
+    if (ep_ids) std::memcpy(p_ep, ep_ids, att_bytes);
     if (ep_csr) {
         // build_episode_csr over all ids (src/memory_graph.cpp:12-44) restricted to the
         // appended episodes: counting sort of the new ids, members ascending
@@ -276,15 +515,25 @@ extern "C" int mars_graph_insert(mars_graph* gh, int32_t n_new, const float* emb
             p_off[e] = run;                         // ep_off[num_eps + 1 + e]
         }
         for (int32_t i = 0; i < n_new; ++i) p_mem[cur[size_t(ep_ids[i] - g.num_eps)]++] = n_old + i;
-        MARS_HIP(hipMemcpyAsync(g.ep_off + g.num_eps + 1, p_off, size_t(ne_new) * sizeof(int32_t),
-                                hipMemcpyHostToDevice, s));
-        MARS_HIP(hipMemcpyAsync(g.ep_mem + g.member_total, p_mem, att_bytes, hipMemcpyHostToDevice, s));
     }
-    if (g.emb16) {
-        MARS_TRY(launch_convert_f16(g.emb + int64_t(n_old) * D, g.emb16 + int64_t(n_old) * D, int64_t(n_new) * D, s));
-        // the batched global path's bound covers every published row
-        if (g.nrm) MARS_TRY(launch_row_norms(g.emb, g.emb16, n_old, n_after, D, g.nrm, s));
-    }
+    // one copy of the staged block, one kernel to place it (each GPU operation waits for
+    // a dispatch slot when scans fill the GPU, so an insert issues as few as it can)
+    MARS_TRY(grow_device(&g.ins_dev, &g.ins_dev_bytes, stage1));
+    char* dev = static_cast<char*>(g.ins_dev);
+    MARS_HIP(hipMemcpyAsync(dev, pin, stage1, hipMemcpyHostToDevice, s));
+    StageArgs sa{};
+    sa.rows = reinterpret_cast<const uint32_t*>(dev);
+    sa.mods = reinterpret_cast<const int32_t*>(dev + (p_mods - pin));
+    sa.ts = reinterpret_cast<const float*>(dev + (p_ts - pin));
+    sa.ep = ep_ids ? reinterpret_cast<const int32_t*>(dev + (p_ep - pin)) : nullptr;
+    sa.mem = ep_csr ? reinterpret_cast<const int32_t*>(dev + (reinterpret_cast<char*>(p_mem) - pin)) : nullptr;
+    sa.off = ep_csr ? reinterpret_cast<const int32_t*>(dev + (reinterpret_cast<char*>(p_off) - pin)) : nullptr;
+    sa.emb = g.emb; sa.emb16 = g.emb16; sa.nrm = g.nrm;
+    sa.g_mods = g.mods; sa.g_ts = g.ts; sa.g_ep = ep_ids ? g.ep_ids : nullptr;
+    sa.g_mem = ep_csr ? g.ep_mem : nullptr; sa.g_off = ep_csr ? g.ep_off : nullptr;
+    sa.n_old = n_old; sa.n_new = n_new; sa.d = int32_t(D); sa.ne_new = ne_new;
+    sa.mem_at = g.member_total; sa.off_at = g.num_eps + 1;
+    MARS_LAUNCH(k_stage_insert, dim3(patch_grid(int64_t(n_new) * 64)), dim3(256), 0, s, sa);
     MARS_HIP(hipStreamSynchronize(s));
     // publish: scans, episode scope and the boost see the new nodes from here on
     double t_queryable = 0.0;
@@ -342,18 +591,10 @@ extern "C" int mars_graph_insert(mars_graph* gh, int32_t n_new, const float* emb
         std::sort(r.begin(), r.end());
         r.erase(std::unique(r.begin(), r.end()), r.end());
     }
-    std::vector<int64_t> reloc, app, rows;
-    std::vector<int32_t> tail;
-    const int64_t base = align_up(g.e_used, kRegionAlign);
-    int64_t cursor = base;
-    int64_t added = 0;
-    int32_t n_reloc = 0, n_inplace = 0, max_deg = g.max_deg;
-    auto place = [&](int64_t cap) {
-        const int64_t at = cursor;
-        tail.resize(size_t(at + cap - base), -1);
-        cursor += cap;
-        return at;
-    };
+    Patch p;
+    p.base = align_up(g.e_used, kRegionAlign);
+    p.cursor = p.base;
+    p.max_deg = g.max_deg;
     for (size_t i = 0, j = 0; i < old_add.size(); i = j) {
         const int32_t v = old_add[i].first;
         while (j < old_add.size() && old_add[j].first == v) ++j;
@@ -364,89 +605,112 @@ extern "C" int mars_graph_insert(mars_graph* gh, int32_t n_new, const float* emb
         int64_t nstart = start, ncap = cap;
         if (nlen <= cap) {
             for (int64_t x = 0; x < a; ++x) {
-                app.push_back(start + len + x);
-                app.push_back(old_add[i + size_t(x)].second);
+                p.app.push_back(start + len + x);
+                p.app.push_back(old_add[i + size_t(x)].second);
             }
-            ++n_inplace;
+            ++p.n_inplace;
         } else {
             ncap = row_capacity(nlen);
-            nstart = place(ncap);
-            reloc.push_back(start); reloc.push_back(len); reloc.push_back(nstart);
-            for (int64_t x = 0; x < len; ++x) tail[size_t(nstart - base + x)] = kCopySlot;
-            for (int64_t x = 0; x < a; ++x) tail[size_t(nstart - base + len + x)] = old_add[i + size_t(x)].second;
-            ++n_reloc;
+            nstart = p.place(ncap);
+            p.reloc.push_back(start); p.reloc.push_back(len); p.reloc.push_back(nstart);
+            for (int64_t x = 0; x < len; ++x) p.tail[size_t(nstart - p.base + x)] = kCopySlot;
+            for (int64_t x = 0; x < a; ++x) p.tail[size_t(nstart - p.base + len + x)] = old_add[i + size_t(x)].second;
+            ++p.n_reloc;
         }
         const int64_t nw = (nlen << 32) | int64_t(uint32_t(nstart));
-        rows.push_back(v); rows.push_back(nw); rows.push_back(ncap);
-        max_deg = std::max<int32_t>(max_deg, int32_t(nlen));
-        added += a;
+        p.rows.push_back(v); p.rows.push_back(nw); p.rows.push_back(ncap);
+        p.max_deg = std::max<int32_t>(p.max_deg, int32_t(nlen));
+        p.added += a;
     }
     for (int32_t i = 0; i < n_new; ++i) {
         const auto& r = nrow[size_t(i)];
         const int64_t len = int64_t(r.size()), cap = row_capacity(len);
-        const int64_t at = place(cap);
-        std::memcpy(tail.data() + (at - base), r.data(), r.size() * sizeof(int32_t));
+        const int64_t at = p.place(cap);
+        std::memcpy(p.tail.data() + (at - p.base), r.data(), r.size() * sizeof(int32_t));
         const int64_t nw = (len << 32) | int64_t(uint32_t(at));
-        rows.push_back(n_old + i); rows.push_back(nw); rows.push_back(cap);
-        max_deg = std::max<int32_t>(max_deg, int32_t(len));
-        added += len;
+        p.rows.push_back(n_old + i); p.rows.push_back(nw); p.rows.push_back(cap);
+        p.max_deg = std::max<int32_t>(p.max_deg, int32_t(len));
+        p.added += len;
     }
-    if (cursor > g.cap_e || cursor > int64_t(UINT32_MAX)) {
+    if (p.cursor > g.cap_e || p.cursor > int64_t(UINT32_MAX)) {
         if (early)      // cannot happen: the worst case fitted
             return set_error(MARS_ERR_CAPACITY, "insert: planned %lld col slots beyond the worst case "
-                             "(nodes published without edges)", (long long)cursor);
+                             "(nodes published without edges)", (long long)p.cursor);
         return set_error(MARS_ERR_CAPACITY, "insert: edge capacity %lld too small (used %lld, this insert "
-                         "needs %lld)", (long long)g.cap_e, (long long)g.e_used, (long long)(cursor - g.e_used));
+                         "needs %lld)", (long long)g.cap_e, (long long)g.e_used, (long long)(p.cursor - g.e_used));
     }
     if (!early) publish();
 
     // ---- step 4: write column data, then publish the row words ------------------------------
-    const size_t b_reloc = reloc.size() * sizeof(int64_t), b_app = app.size() * sizeof(int64_t);
-    const size_t b_rows = rows.size() * sizeof(int64_t), b_tail = tail.size() * sizeof(int32_t);
-    const size_t total = b_reloc + b_app + b_rows + b_tail + 64;
-    MARS_TRY(grow_pinned<char>(&g.ins_pin, &g.ins_pin_bytes, total));
-    MARS_TRY(grow_device(&g.ins_dev, &g.ins_dev_bytes, total));
-    pin = static_cast<char*>(g.ins_pin);          // the staging of step 1 is consumed (synchronised)
-    char* dev = static_cast<char*>(g.ins_dev);
-    size_t off = 0;
-    auto put = [&](const void* src, size_t bytes) {
-        const size_t at = off;
-        if (bytes) std::memcpy(pin + at, src, bytes);
-        off += (bytes + 15) / 16 * 16;
-        return at;
-    };
-    const size_t o_reloc = put(reloc.data(), b_reloc), o_app = put(app.data(), b_app);
-    const size_t o_rows = put(rows.data(), b_rows), o_tail = put(tail.data(), b_tail);
-    MARS_HIP(hipMemcpyAsync(dev, pin, off, hipMemcpyHostToDevice, s));
-    PatchArgs pa{};
-    pa.col = g.col; pa.ro = g.ro; pa.rcap = g.rcap;
-    pa.reloc = reinterpret_cast<const int64_t*>(dev + o_reloc); pa.n_reloc = int32_t(reloc.size() / 3);
-    pa.tail = reinterpret_cast<const int32_t*>(dev + o_tail); pa.tail_base = base; pa.n_tail = int64_t(tail.size());
-    pa.app = reinterpret_cast<const int64_t*>(dev + o_app); pa.n_app = int32_t(app.size() / 2);
-    pa.rows = reinterpret_cast<const int64_t*>(dev + o_rows); pa.n_rows = int32_t(rows.size() / 3);
-    const int64_t data_work = std::max<int64_t>({int64_t(pa.n_reloc) * 64, pa.n_tail, int64_t(pa.n_app)});
-    MARS_LAUNCH(k_patch_data, dim3(patch_grid(data_work)), dim3(256), 0, s, pa);
-    MARS_LAUNCH(k_patch_rows, dim3(patch_grid(pa.n_rows)), dim3(256), 0, s, pa);
-    MARS_HIP(hipStreamSynchronize(s));
-    for (size_t i = 0; i < rows.size(); i += 3) {
-        g.ro_h[size_t(rows[i])] = rows[i + 1];
-        g.rcap_h[size_t(rows[i])] = int32_t(rows[i + 2]);
-    }
-    g.e_used = cursor;
-    g.max_deg = max_deg;
-    g.e = int32_t(std::min<int64_t>(int64_t(g.e) + added, INT32_MAX));
+    MARS_TRY(commit_patch(g, p, s));
     if (out_knn && knn_k > 0) std::memcpy(out_knn, knn.data(), knn.size() * sizeof(int32_t));
     if (st) {
         mars_insert_stats r{};
         r.first_node = n_old;
         r.nodes_added = n_new;
-        r.edges_added = added;
-        r.rows_relocated = n_reloc;
-        r.rows_appended = n_inplace;
+        r.edges_added = p.added;
+        r.rows_relocated = p.n_reloc;
+        r.rows_appended = p.n_inplace;
         r.queryable_us = t_queryable;
         r.linked_us = us_since(t0);
         r.knn_us = double(knn_ms) * 1000.0;
         *st = r;
     }
+    return MARS_OK;
+}
+
+extern "C" int mars_graph_link(mars_graph* gh, int32_t first, int32_t count, int32_t k, const int32_t* nbrs,
+                               mars_insert_stats* st) {
+    const auto t0 = std::chrono::steady_clock::now();
+    MARS_CHECK(gh && count >= 0 && k >= 0 && (count == 0 || k == 0 || nbrs), MARS_ERR_INVALID,
+               "link: bad arguments");
+    std::lock_guard<std::mutex> lock(gh->mu);
+    Graph& g = gh->g;
+    MARS_CHECK(first >= 0 && int64_t(first) + count <= g.n, MARS_ERR_INVALID,
+               "link: nodes [%d, %lld) are not all published (%d nodes)", first, (long long)first + count, g.n);
+    MARS_TRY(use_device(g.device));
+    mars_insert_stats r{};
+    if (count > 0 && k > 0) MARS_TRY(link_knn_apply(g, first, count, k, nbrs, g.ins_stream, &r));
+    r.first_node = first;
+    r.nodes_added = count;
+    r.linked_us = us_since(t0);
+    if (st) *st = r;
+    return MARS_OK;
+}
+
+extern "C" int mars_graph_link_knn(mars_graph* gh, int32_t first, int32_t count, int32_t knn_k, int32_t* out_knn,
+                                   mars_insert_stats* st) {
+    const auto t0 = std::chrono::steady_clock::now();
+    MARS_CHECK(gh && count >= 0 && knn_k >= 1 && knn_k <= 16, MARS_ERR_INVALID,
+               "link: bad arguments (count %d, knn_k %d)", count, knn_k);
+    std::lock_guard<std::mutex> lock(gh->mu);
+    Graph& g = gh->g;
+    MARS_CHECK(first >= 0 && int64_t(first) + count <= g.n, MARS_ERR_INVALID,
+               "link: nodes [%d, %lld) are not all published (%d nodes)", first, (long long)first + count, g.n);
+    MARS_CHECK(g.emb16 != nullptr, MARS_ERR_UNSUPPORTED, "link: the neighbour search reads the fp16 rows; "
+               "enable them first");
+    MARS_CHECK(batch_dim_supported(g.d), MARS_ERR_UNSUPPORTED, "link: embedding_dim %d unsupported", g.d);
+    MARS_TRY(use_device(g.device));
+    hipStream_t s = g.ins_stream;
+    for (auto& e : g.ins_ev)
+        if (!e) MARS_HIP(hipEventCreate(&e));
+    mars_insert_stats r{};
+    std::vector<int32_t> knn(size_t(count) * size_t(knn_k), -1);
+    float knn_ms = 0.0f;
+    if (count > 0) {
+        MARS_HIP(hipEventRecord(g.ins_ev[0], s));
+        MARS_TRY(insert_knn(g, first, count, g.n, knn_k, s));
+        MARS_HIP(hipEventRecord(g.ins_ev[1], s));
+        MARS_HIP(hipMemcpyAsync(knn.data(), g.ins_nbrs, knn.size() * sizeof(int32_t), hipMemcpyDeviceToHost, s));
+        MARS_HIP(hipStreamSynchronize(s));
+        MARS_HIP(hipEventElapsedTime(&knn_ms, g.ins_ev[0], g.ins_ev[1]));
+        MARS_TRY(link_knn_apply(g, first, count, knn_k, knn.data(), s, &r));
+    }
+    r.first_node = first;
+    r.nodes_added = count;
+    r.linked_us = us_since(t0);
+    r.knn_us = double(knn_ms) * 1000.0;
+    if (out_knn && count > 0) std::memcpy(out_knn, knn.data(), knn.size() * sizeof(int32_t));
+    if (st) *st = r;
     return MARS_OK;
 }

@@ -228,6 +228,8 @@ struct Ctx {
     float* mvfin = nullptr;        // exact fused score of each visited node
     float* mvscore = nullptr;
     int32_t mcap_q = 0;
+    int32_t* mknn = nullptr;       // neighbour lists of a shared scan's k-NN queries
+    int32_t mknn_cap = 0;          // nodes
     void* h_mres = nullptr;        // pinned, mapped: [q] ResultHeader then [q][rcap] results
     void* d_mres = nullptr;
     size_t mres_bytes = 0;
@@ -258,6 +260,10 @@ struct PatchArgs {
     int32_t n_rows;
 };
 int graph_insert_free(Graph& g);     // insert scratch of a graph
+// Edges between node first + i and each listed neighbour knn[i * k + j] (-1 skipped),
+// both directions, merged into the rows (insert.hip). Caller holds the graph mutex.
+int link_knn_apply(Graph& g, int32_t first, int32_t count, int32_t k, const int32_t* knn, hipStream_t s,
+                   mars_insert_stats* st);
 
 // ---- launch helpers (defined in kernels.hip) --------------------------------------
 struct ScanArgs {
@@ -367,7 +373,10 @@ struct BatchArgs {
     float lambda;
     int32_t mod_filter;
     int32_t k;               // <= 16 kept per query
-    int64_t self_base;       // >= 0: query j is node self_base + j and never its own neighbour
+    int32_t q_plain;         // queries q_plain .. q-1 are neighbour searches: plain dot product,
+                             // no decay, no filter (the rest use lambda / mod_filter / tq)
+    int64_t self_base;       // >= 0: neighbour search j (query q_plain + j) is node self_base + j
+                             // and never its own neighbour
     uint64_t* part;          // [n_qblocks][n_rranges][64][K] keys
     int64_t rows_per_range;
     int32_t n_rranges;

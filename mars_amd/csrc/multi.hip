@@ -30,25 +30,6 @@
 namespace mars {
 namespace {
 
-constexpr float kHalfMinNormal = 6.103515625e-05f;   // 2^-14
-
-// fp32 bit pattern of a value >= v (v >= 0); NaN stays NaN
-__device__ inline uint32_t up_bits(double v) {
-    if (!(v == v)) return 0x7fc00000u;
-    float f = float(v);
-    if (double(f) < v) f = nextafterf(f, __builtin_inff());
-    return __float_as_uint(f);
-}
-
-__device__ inline double wave_sum_f64(double v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-    return v;
-}
-
-// max that lets a NaN through (the certificate must then fail)
-__device__ inline double max_nan(double m, double v) { return (v <= m) ? m : v; }
-
 // One wave per row: |e|^2, |e16|^2 and |ftz(e16) - e|^2 in fp64; the block's maxima
 // raise nrm[0..2] (fp32 bits of non-negative values order as unsigned integers).
 __global__ __launch_bounds__(256) void k_row_norms(const float* __restrict__ emb, const __half* __restrict__ emb16,

@@ -65,6 +65,7 @@ def _load():
         "oracle_tiled_query": (I32, [C.POINTER(OracleGraph), VP, C.c_float, C.c_float, I32, I32, I32, VP, VP]),
         "oracle_knn": (None, [VP, I64, I32, VP, I32, I32, VP, VP]),
         "oracle_insert_edges": (I64, [I32, VP, VP, I32, VP, VP, I32, VP, VP]),
+        "oracle_link_edges": (I64, [I32, VP, VP, I32, I32, VP, I32, VP, VP]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -239,6 +240,22 @@ def knn(emb, qids, k: int, n: Optional[int] = None):
     sims = np.empty((len(qids), k), np.float64)
     lib.oracle_knn(_p(emb), n, emb.shape[1], _p(qids), len(qids), k, _p(ids), _p(sims))
     return ids, sims
+
+
+def link_edges(row, col, n: int, first: int, knn_ids):
+    """CSR after linking nodes first .. first + len(knn_ids) - 1 to their listed neighbours
+    (both directions, union with the existing edges)."""
+    row = None if row is None else np.ascontiguousarray(row, np.int32)
+    col = None if col is None else np.ascontiguousarray(col, np.int32)
+    kn = np.ascontiguousarray(knn_ids, np.int32)
+    count, k = (kn.shape[0], kn.shape[1]) if kn.ndim == 2 else (0, 0)
+    if count == 0 or k == 0:
+        kn = np.full((1, 1), -1, np.int32)
+    out_row = np.empty(n + 1, np.int32)
+    e = lib.oracle_link_edges(n, _p(row), _p(col), first, count, _p(kn), k, _p(out_row), None)
+    out_col = np.empty(max(e, 1), np.int32)
+    lib.oracle_link_edges(n, _p(row), _p(col), first, count, _p(kn), k, _p(out_row), _p(out_col))
+    return out_row, out_col[:e]
 
 
 def insert_edges(row, col, n_old: int, n_new: int, ep_new, knn_ids):

@@ -517,5 +517,39 @@ int64_t oracle_insert_edges(int32_t n_old, const int32_t* row, const int32_t* co
     return e;
 }
 
+// ---------------------------------------------------------------------------
+// Deferred k-NN edges of nodes already in the graph (ids first .. first+count-1):
+// the same std::set adjacency union as the insert rule above, over an existing
+// CSR of n nodes: every old edge kept, (u, v) and (v, u) added for each listed
+// neighbour v of u (ids < 0 or >= n and v == u skipped), rows ascending.
+// out_row: n + 1 entries. Returns the edge count; out_col == NULL sizes it.
+// ---------------------------------------------------------------------------
+int64_t oracle_link_edges(int32_t n, const int32_t* row, const int32_t* col, int32_t first, int32_t count,
+                          const int32_t* knn, int32_t k, int32_t* out_row, int32_t* out_col) {
+    std::vector<std::set<int32_t>> adj(static_cast<size_t>(n));
+    for (int32_t i = 0; i < n; ++i)
+        if (row)
+            for (int32_t j = row[i]; j < row[i + 1]; ++j) adj[size_t(i)].insert(col[j]);
+    for (int32_t i = 0; i < count; ++i) {
+        const int32_t u = first + i;
+        for (int32_t j = 0; j < k; ++j) {
+            const int32_t v = knn[int64_t(i) * k + j];
+            if (v < 0 || v >= n || v == u) continue;
+            adj[size_t(u)].insert(v);
+            adj[size_t(v)].insert(u);
+        }
+    }
+    int64_t e = 0;
+    if (out_row) out_row[0] = 0;
+    for (int32_t i = 0; i < n; ++i) {
+        for (int32_t v : adj[size_t(i)]) {
+            if (out_col) out_col[e] = v;
+            ++e;
+        }
+        if (out_row) out_row[i + 1] = int32_t(e);
+    }
+    return e;
+}
+
 }  // extern "C"
 

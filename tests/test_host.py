@@ -56,6 +56,8 @@ def test_struct_layouts():
     assert _lib.InsertStatsC.queryable_us.offset == 24
     assert C.sizeof(_lib.StreamBenchC) == 128 and _lib.StreamBenchC.knn_k.offset == 88
     assert C.sizeof(_lib.BatchStatsC) == 64 and _lib.BatchStatsC.wall_us.offset == 48
+    assert C.sizeof(_lib.ServeBenchC) == 216 and _lib.ServeBenchC.g_done_us.offset == 128
+    assert _lib.ServeBenchC.ins_linked_us.offset == 192
 
 
 def test_tiled_config_defaults_match_reference():

@@ -387,6 +387,51 @@ def test_insert_edges_two_batches_equal_one(rng):
     np.testing.assert_array_equal(c2, ca)
 
 
+def _sets_link(row, col, n, first, knn):
+    adj = [set() if row is None else set(col[row[i]:row[i + 1]].tolist()) for i in range(n)]
+    for i, lst in enumerate(knn):
+        u = first + i
+        for v in lst.tolist():
+            if 0 <= v < n and v != u:
+                adj[u].add(v)
+                adj[v].add(u)
+    r = np.zeros(n + 1, np.int32)
+    r[1:] = np.cumsum([len(a) for a in adj])
+    c = np.array([v for a in adj for v in sorted(a)], np.int32)
+    return r, c
+
+
+def test_link_edges_match_set_brute_force(rng):
+    for n, first, count, k in [(20, 0, 20, 3), (50, 30, 20, 4), (40, 39, 1, 8), (64, 10, 0, 2)]:
+        row, col = _random_csr(rng, n, 3)
+        knn = rng.integers(-2, n + 2, size=(count, k)).astype(np.int32)
+        got_r, got_c = oracle.link_edges(row, col, n, first, knn)
+        want_r, want_c = _sets_link(row, col, n, first, knn)
+        np.testing.assert_array_equal(got_r, want_r)
+        np.testing.assert_array_equal(got_c, want_c)
+
+
+def test_insert_then_link_equals_insert_with_knn(rng):
+    """Deferred linking: insert with no k-NN, then link the same lists = one insert."""
+    n_old = 45
+    row, col = _random_csr(rng, n_old, 4)
+    ep = np.array([3] * 6 + [4] * 4 + [5] * 5, np.int32)
+    knn = rng.integers(-1, n_old + 15, size=(15, 6)).astype(np.int32)
+    r0, c0 = oracle.insert_edges(row, col, n_old, 15, ep, np.empty((15, 0), np.int32))
+    r1, c1 = oracle.link_edges(r0, c0, n_old + 15, n_old, knn)
+    ra, ca = oracle.insert_edges(row, col, n_old, 15, ep, knn)
+    np.testing.assert_array_equal(r1, ra)
+    np.testing.assert_array_equal(c1, ca)
+    # linking is idempotent, and linking in two parts equals one
+    r2, c2 = oracle.link_edges(r1, c1, n_old + 15, n_old, knn)
+    np.testing.assert_array_equal(r2, r1)
+    np.testing.assert_array_equal(c2, c1)
+    ra1, ca1 = oracle.link_edges(r0, c0, n_old + 15, n_old, knn[:7])
+    ra2, ca2 = oracle.link_edges(ra1, ca1, n_old + 15, n_old + 7, knn[7:])
+    np.testing.assert_array_equal(ra2, r1)
+    np.testing.assert_array_equal(ca2, c1)
+
+
 def _check_flush_invariants(row0, col0, row1, col1, n_old, n_new):
     assert len(row1) == n_old + n_new + 1
     for i in range(n_old):                    # every old edge kept
