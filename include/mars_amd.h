@@ -92,6 +92,8 @@ typedef struct mars_stats {
     int32_t visited;            /* number of nodes reached (seeds + BFS)                  */
     int32_t bfs_levels_run;     /* BFS levels actually expanded                           */
     int32_t used_fp16;          /* 1 if the fp16 corpus was scanned                       */
+    int32_t seeds_certified;    /* MARS_CTX_CERTIFIED: 1 if the fp16 scan's seeds were certified
+                                   (0: the fp32 scan answered the query)                     */
     double  wall_us;            /* host wall time of the call                             */
 } mars_stats;
 
@@ -274,6 +276,16 @@ int mars_host_free(void* ptr);
 #define MARS_CTX_USE_FP16    0x1u   /* scan the fp16 copy when present (ctx.use_fp16)      */
 #define MARS_CTX_USE_GRAPH   0x2u   /* replay the query pipeline as a hipGraph             */
 #define MARS_CTX_TIMING      0x4u   /* fill per-stage gpu_ms_* with hipEvents              */
+/* Global queries scan the fp16 copy (half the bytes) and return exactly the fp32 path's
+ * results: the scan keeps 32 candidates (64 for K > 16), which are rescored in the
+ * fp32 scan's own arithmetic; when the K-th exact score exceeds the last candidate's
+ * fp16 score by more than the fp16 error bound of any row (from the rows' rounding
+ * residual norms, kept with the fp16 copy), those are the fp32 scan's seeds, and the
+ * BFS then scores every visited node exactly. Otherwise the fp32 scan answers the
+ * query (stats.seeds_certified = 0). Needs the fp16 copy; ignored with MARS_CTX_USE_FP16
+ * (which returns fp16 scores), for episode scope, a same-episode boost, lambda < 0 and
+ * embedding_dim not a multiple of 128. MARS_CTX_USE_GRAPH does not apply to it. */
+#define MARS_CTX_CERTIFIED   0x8u
 /* create_query_context(max_nodes, embedding_dim, max_k): max_k clamps to 64. */
 int mars_ctx_create(int32_t max_nodes, int32_t embedding_dim, int32_t max_k,
                     uint32_t flags, mars_ctx** out);

@@ -23,7 +23,7 @@ from typing import List, Optional
 import numpy as np
 
 from . import _lib
-from ._lib import (MARS_CTX_TIMING, MARS_CTX_USE_FP16, MARS_CTX_USE_GRAPH, MARS_DESC_DEVICE_POINTERS,
+from ._lib import (MARS_CTX_CERTIFIED, MARS_CTX_TIMING, MARS_CTX_USE_FP16, MARS_CTX_USE_GRAPH, MARS_DESC_DEVICE_POINTERS,
                    MarsError, check, lib)
 
 __all__ = [
@@ -86,6 +86,7 @@ class RetrievalStats:                              # memory_cuda.cuh:129-137 (+ 
     visited: int = 0
     bfs_levels_run: int = 0
     used_fp16: int = 0
+    seeds_certified: int = 0
     wall_us: float = 0.0
 
     def _fill(self, s: _lib.StatsC) -> None:
@@ -267,6 +268,8 @@ class QueryContext:
     use_fp16 = property(lambda s: s._flag(MARS_CTX_USE_FP16), lambda s, v: s._set(MARS_CTX_USE_FP16, v))
     use_cuda_graph = property(lambda s: s._flag(MARS_CTX_USE_GRAPH), lambda s, v: s._set(MARS_CTX_USE_GRAPH, v))
     timing = property(lambda s: s._flag(MARS_CTX_TIMING), lambda s, v: s._set(MARS_CTX_TIMING, v))
+    # fp16 scan with certified exact seeds: the fp32 path's results at half the scan bytes
+    certified = property(lambda s: s._flag(MARS_CTX_CERTIFIED), lambda s, v: s._set(MARS_CTX_CERTIFIED, v))
 
     def last_scores(self, n: int) -> np.ndarray:
         out = np.zeros(n, np.float32)

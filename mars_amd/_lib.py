@@ -26,6 +26,7 @@ MARS_DESC_DEVICE_POINTERS = 0x1
 MARS_CTX_USE_FP16 = 0x1
 MARS_CTX_USE_GRAPH = 0x2
 MARS_CTX_TIMING = 0x4
+MARS_CTX_CERTIFIED = 0x8
 
 
 class QueryResultC(C.Structure):
@@ -63,6 +64,7 @@ class StatsC(C.Structure):
         ("visited", C.c_int32),
         ("bfs_levels_run", C.c_int32),
         ("used_fp16", C.c_int32),
+        ("seeds_certified", C.c_int32),
         ("wall_us", C.c_double),
     ]
 

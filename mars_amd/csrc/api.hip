@@ -30,6 +30,7 @@ namespace {
 thread_local char g_err[1024] = "";
 constexpr int32_t kMaxWg = 4096;     // upper bound of scan workgroups (partials buffer)
 constexpr int32_t kTargetWg = 2048;  // scan workgroups (grid-stride; 8 per CU on 256 CUs)
+constexpr int32_t kTargetWgF16 = 1024;   // fp16 rows: 241 us vs 249 us at 2048 (N=1M, D=768)
 
 int ensure_device(int* dev) {
     int d = 0;
@@ -204,6 +205,74 @@ int graph_launch(Ctx::GraphSlot& g, int n, const KernelLaunch* l, void* const* a
     return MARS_OK;
 }
 
+int ensure_multi_scratch(Ctx& c, int32_t q, int32_t rcap);
+
+// Certified global query (MARS_CTX_CERTIFIED): fp16 scan keeping c candidates, exact
+// rescoring + certificate, then the unscored BFS, exact visit scores and the results
+// (the batched path's kernels with q = 1). *answered = false when the certificate or
+// the BFS table did not hold: the caller runs the fp32 scan.
+int certified_query(const Graph& g, Ctx& c, const float* q, float t_q, const mars_retrieval_config* cfg, int32_t K,
+                    int32_t hops, int32_t rcap, int32_t n_live, mars_query_result* out, int32_t cap, int32_t* n_out,
+                    bool* answered, ResultHeader* hdr_out) {
+    *answered = false;
+    MARS_TRY(ensure_multi_scratch(c, 1, rcap));
+    hipStream_t s = c.stream;
+    const bool timing = (c.flags & MARS_CTX_TIMING) != 0;
+    const int32_t cands = K <= 10 ? 16 : (K <= 16 ? 32 : 64);   // fp16 candidates the certificate checks
+    int32_t rpw = 0, nwg = 0;
+    scan_grid(n_live, kTargetWgF16, &rpw, &nwg);
+    ScanArgs a{};
+    a.emb = g.emb16; a.fp16 = 1; a.n = n_live; a.d = g.d; a.q = q; a.ts = g.ts; a.mods = g.mods; a.ep_ids = g.ep_ids;
+    a.t_q = t_q; a.lambda = cfg->time_decay_lambda; a.mod_filter = cfg->modality_filter; a.query_ep = -1;
+    a.boost = 0.0f; a.k = cands; a.fin = c.fin; a.part = c.part; a.gthr = c.gthr; a.gcnt = c.gcnt;
+    a.rows_per_wg = rpw; a.num_wg = nwg;
+    if (timing) MARS_HIP(hipEventRecord(c.ev[0], s));
+    MARS_TRY(launch_scan(a, s));
+    if (timing) MARS_HIP(hipEventRecord(c.ev[1], s));
+    CertArgs ca{};
+    ca.part = c.part; ca.gcnt = c.gcnt; ca.gthr = c.gthr; ca.c = cands; ca.k = K; ca.q = q; ca.d = g.d;
+    ca.emb = g.emb; ca.ts = g.ts; ca.mods = g.mods; ca.t_q = t_q; ca.lambda = cfg->time_decay_lambda;
+    ca.mod_filter = cfg->modality_filter; ca.nrm = g.nrm; ca.seeds = c.mseed; ca.status = c.mstat;
+    ca.margin = c.mmargin; ca.fin16 = c.fin;
+    // one workgroup finishes the query when the interval argument applies
+    const float dlt = cfg->bfs_score_decay;
+    ca.finish = (rcap <= 64 && dlt >= 0.0f && dlt <= 1.0f) ? 1 : 0;
+    MultiArgs m{};
+    m.ro = g.ro; m.col = g.col; m.mods = g.mods; m.n_live = n_live; m.hops = hops;
+    m.hop_decay = cfg->bfs_score_decay; m.k = K; m.rcap = rcap; m.q = 1; m.seeds = c.mseed; m.seed_stride = 64;
+    m.status = c.mstat; m.info = c.minfo; m.vlist = c.mvlist; m.vhop = c.mvhop; m.vpar = c.mvpar;
+    m.vro = c.mvro; m.vfin = c.mvfin; m.vscore = c.mvscore;
+    m.res = static_cast<ResultHeader*>(c.d_mres);
+    m.rec = reinterpret_cast<mars_query_result*>(m.res + 1);
+    if (launch_cert_bfs(ca, m, s) != MARS_OK) {
+        // the scan appended candidates: clear them for the next query
+        (void)hipMemsetAsync(c.gcnt, 0, sizeof(uint32_t), s);
+        (void)hipMemsetAsync(c.gthr, 0xFF, sizeof(uint64_t), s);
+        (void)hipStreamSynchronize(s);
+        return set_error(MARS_ERR_HIP, "certificate launch failed");
+    }
+    if (!ca.finish) {
+        VisitScoreArgs va{};
+        va.emb = g.emb; va.fp16 = 0; va.d = g.d; va.ts = g.ts; va.mods = g.mods; va.queries = q;
+        va.tq = nullptr; va.lambda = cfg->time_decay_lambda; va.mod_filter = cfg->modality_filter; va.q = 1;
+        va.status = c.mstat; va.info = c.minfo; va.vlist = c.mvlist; va.vfin = c.mvfin;
+        va.t_q_value = t_q;
+        MARS_TRY(launch_visit_scores(va, s));
+        MARS_TRY(launch_multi_select(m, s));
+    }
+    if (timing) MARS_HIP(hipEventRecord(c.ev[2], s));
+    MARS_HIP(hipStreamSynchronize(s));
+    const auto* hdr = static_cast<const ResultHeader*>(c.h_mres);
+    const ResultHeader h = hdr[0];
+    if (h.count < 0) return MARS_OK;
+    const int32_t nw = std::min(h.count, cap);
+    if (nw > 0) std::memcpy(out, hdr + 1, size_t(nw) * sizeof(mars_query_result));
+    *n_out = h.count;
+    *hdr_out = h;
+    *answered = true;
+    return MARS_OK;
+}
+
 // n_pin >= 0: answer over the first n_pin nodes (a batch that already read the node
 // count), else over the nodes published when the query starts.
 int query_impl(const mars_graph* gh, mars_ctx* ch, const float* h_q, const float* d_q, float t_q,
@@ -239,6 +308,42 @@ int query_impl(const mars_graph* gh, mars_ctx* ch, const float* h_q, const float
         MARS_HIP(hipMemcpyAsync(c.query, c.h_query, size_t(g.d) * sizeof(float), hipMemcpyHostToDevice, s));
         q = c.query;
     }
+    const float lam = cfg->time_decay_lambda;
+    const bool boost_on = g.ep_ids && cfg->query_episode_id >= 0 && cfg->episode_same_boost > 0.0f;
+    const bool cert = !scoped && !fp16 && (c.flags & MARS_CTX_CERTIFIED) && g.emb16 && g.nrm && g.d % 128 == 0 &&
+                      g.d <= 1024 && !boost_on && lam >= 0.0f && lam <= FLT_MAX && hops < 255;
+    if (cert) {
+        bool answered = false;
+        ResultHeader h{};
+        MARS_TRY(certified_query(g, c, q, t_q, cfg, K, hops, rcap, n_live, out, cap, n_out, &answered, &h));
+        if (answered) {
+            c.last_k = h.n_seeds;
+            c.last_visited = 0;               // the debug hooks describe fp32 scans only
+            c.last_n = 0;
+            if (stats) {
+                mars_stats st{};
+                if (timing) {
+                    float ms = 0.0f;
+                    MARS_HIP(hipEventElapsedTime(&ms, c.ev[0], c.ev[1]));
+                    st.gpu_ms_similarity = ms;
+                    MARS_HIP(hipEventElapsedTime(&ms, c.ev[1], c.ev[2]));
+                    st.gpu_ms_bfs = ms;
+                    MARS_HIP(hipEventElapsedTime(&ms, c.ev[0], c.ev[2]));
+                    st.gpu_ms_total = ms;
+                }
+                st.nodes_scanned = n_live;
+                st.bfs_waves = cfg->bfs_max_hops;
+                st.scope_fallback = (cfg->retrieval_scope == MARS_SCOPE_EPISODE_SCOPED) ? 1 : 0;
+                st.visited = h.visited;
+                st.bfs_levels_run = h.levels;
+                st.used_fp16 = 1;
+                st.seeds_certified = 1;
+                st.wall_us = std::chrono::duration<double, std::micro>(std::chrono::steady_clock::now() - t0).count();
+                *stats = st;
+            }
+            return MARS_OK;
+        }
+    }
     if (timing) MARS_HIP(hipEventRecord(c.ev[0], s));
     if (scoped) {
         EpisodeArgs a{};
@@ -258,7 +363,7 @@ int query_impl(const mars_graph* gh, mars_ctx* ch, const float* h_q, const float
         if (timing) MARS_HIP(hipEventRecord(c.ev[1], s));
     } else {
         int32_t rpw = 0, nwg = 0;
-        scan_grid(n_live, kTargetWg, &rpw, &nwg);
+        scan_grid(n_live, fp16 ? kTargetWgF16 : kTargetWg, &rpw, &nwg);
         ScanArgs a{};
         a.emb = fp16 ? static_cast<const void*>(g.emb16) : static_cast<const void*>(g.emb);
         a.fp16 = fp16 ? 1 : 0; a.n = n_live; a.d = g.d; a.q = q; a.ts = g.ts; a.mods = g.mods;
@@ -367,7 +472,7 @@ int ensure_multi_scratch(Ctx& c, int32_t q, int32_t rcap) {
         c.mcap_q = 0;
         const size_t nv = size_t(q) * kMultiVisit;
         MARS_TRY(dmalloc(&c.mqn, size_t(q) * 4));
-        MARS_TRY(dmalloc(&c.mseed, size_t(q) * kMultiCand));
+        MARS_TRY(dmalloc(&c.mseed, std::max<size_t>(size_t(q) * kMultiCand, 64)));
         MARS_TRY(dmalloc(&c.mstat, size_t(q)));
         MARS_TRY(dmalloc(&c.minfo, size_t(q) * 4));
         MARS_TRY(dmalloc(&c.mmargin, size_t(q)));
@@ -417,6 +522,9 @@ using namespace mars;
 
 // The ctypes mirrors (mars_amd/_lib.py) depend on these layouts.
 static_assert(sizeof(mars_query_result) == 16, "mars_query_result layout");
+static_assert(sizeof(mars_stats) == 56 && offsetof(mars_stats, seeds_certified) == 44 &&
+                  offsetof(mars_stats, wall_us) == 48,
+              "mars_stats layout");
 static_assert(sizeof(mars_insert_stats) == 48 && offsetof(mars_insert_stats, queryable_us) == 24,
               "mars_insert_stats layout");
 static_assert(sizeof(mars_stream_bench) == 128 && offsetof(mars_stream_bench, knn_k) == 88,
@@ -1164,6 +1272,7 @@ int mars_query_global_batch_knn(const mars_graph* gh, mars_ctx* ch, const float*
             MultiArgs m{};
             m.ro = g.ro; m.col = g.col; m.mods = g.mods; m.n_live = n_live; m.hops = hops;
             m.hop_decay = cfg->bfs_score_decay; m.k = K; m.rcap = rcap; m.q = Qg; m.seeds = c.mseed;
+            m.seed_stride = kMultiCand;
             m.status = c.mstat; m.info = c.minfo; m.vlist = c.mvlist; m.vhop = c.mvhop; m.vpar = c.mvpar;
             m.vro = c.mvro; m.vfin = c.mvfin; m.vscore = c.mvscore;
             m.res = static_cast<ResultHeader*>(c.d_mres);

@@ -436,7 +436,8 @@ struct MultiArgs {
     int32_t k;
     int32_t rcap;
     int32_t q;
-    const uint64_t* seeds;   // [q][kMultiCand]
+    const uint64_t* seeds;   // [q][seed_stride]
+    int32_t seed_stride;     // kMultiCand (batched), 64 (certified Q=1)
     int32_t* status;         // [q]
     int32_t* info;           // [q][4] visited, levels, seeds
     int32_t* vlist;          // [q][kMultiVisit] each
@@ -455,7 +456,8 @@ struct VisitScoreArgs {
     const float* ts;
     const int32_t* mods;
     const float* queries;
-    const float* tq;
+    const float* tq;         // q query times (device), or null: every query at t_q_value
+    float t_q_value;
     float lambda;
     int32_t mod_filter;
     int32_t q;
@@ -468,6 +470,33 @@ int launch_row_norms(const float* emb, const __half* emb16, int64_t r0, int64_t 
                      hipStream_t s);
 int launch_query_norms(const float* q32, const __half* q16, int32_t q, int32_t d, double* out, hipStream_t s);
 int launch_multi_seed(const SeedArgs& a, hipStream_t s);
+// Certified Q=1 global query: the fp16 scan (ScanArgs with k = c) appended its
+// candidate keys to part; one workgroup merges the c best, rescores them with the
+// fp32 scan's arithmetic, certifies the k best (status kMultiOk), resets the scan's
+// count and bound, and runs the certified seeds' BFS (k_multi_bfs's work for query 0).
+// k_visit_scores / k_multi_select (q = 1) finish the query.
+struct CertArgs {
+    const uint64_t* part;
+    uint32_t* gcnt;
+    uint64_t* gthr;
+    int32_t c;               // candidates the scan kept (<= 64)
+    int32_t k;               // seeds
+    const float* q;          // d floats
+    int32_t d;
+    const float* emb;        // fp32 rows
+    const float* ts;
+    const int32_t* mods;
+    float t_q;
+    float lambda;
+    int32_t mod_filter;
+    const uint32_t* nrm;     // Graph::nrm
+    const float* fin16;      // the fp16 scan's fused score of every row
+    int32_t finish;          // 1: also compute the results (hop decay in [0, 1], rcap <= 64)
+    uint64_t* seeds;         // 64 entries: ascending exact keys, the first k are the seeds
+    int32_t* status;
+    float* margin;
+};
+int launch_cert_bfs(const CertArgs& a, const struct MultiArgs& m, hipStream_t s);   // + BFS of query 0 of m
 int launch_multi_bfs(const MultiArgs& a, hipStream_t s);
 int launch_visit_scores(const VisitScoreArgs& a, hipStream_t s);
 int launch_multi_select(const MultiArgs& a, hipStream_t s);

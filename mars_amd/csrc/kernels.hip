@@ -534,13 +534,17 @@ __global__ __launch_bounds__(kFinThreads) void k_finalize(FinalizeArgs a) {
     // (left from earlier queries) are masked afterwards
     uint64_t list = kEmptyKey, thr = kEmptyKey;
     const int n_part = int(*a.gcnt);
+    // Every key of the K best is <= the scan's final bound (the smallest workgroup K-th
+    // key), so keys above it are dropped as they load and never reach the lists.
+    const uint64_t gb = *a.gthr;
     {
         uint64_t x[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) x[j] = a.part[wave * 64 + j * kFinThreads + lane];
 #pragma unroll
         for (int j = 0; j < 8; ++j)
-            wave_offer(list, thr, (wave * 64 + j * kFinThreads + lane < n_part) ? x[j] : kEmptyKey, lane, k);
+            wave_offer(list, thr, (wave * 64 + j * kFinThreads + lane < n_part && x[j] <= gb) ? x[j] : kEmptyKey,
+                       lane, k);
     }
     for (int base = kFinThreads * 8 + wave * 64; base < n_part; base += kFinThreads * 8) {
         uint64_t x[8];
@@ -550,7 +554,7 @@ __global__ __launch_bounds__(kFinThreads) void k_finalize(FinalizeArgs a) {
             x[j] = (i < n_part) ? a.part[i] : kEmptyKey;
         }
 #pragma unroll
-        for (int j = 0; j < 8; ++j) wave_offer(list, thr, x[j], lane, k);
+        for (int j = 0; j < 8; ++j) wave_offer(list, thr, x[j] <= gb ? x[j] : kEmptyKey, lane, k);
     }
     list = tree_merge(sh, list, k, n_part <= kFinThreads ? (n_part + 63) / 64 : kFinWaves);
     if (wave == 0) {
@@ -629,14 +633,13 @@ __device__ inline FinalizeArgs multi_view(const MultiArgs& m, int j) {
 // Visit set, hops and parents of query j from its certified seeds: the unscored LDS
 // BFS of k_finalize (same claims, same order). A visit set that outgrows the LDS hash
 // marks the query kMultiOverflow (the Q=1 path answers it).
-__global__ __launch_bounds__(kFinThreads) void k_multi_bfs(MultiArgs m) {
-    __shared__ FinShared sh;
-    const int j = int(blockIdx.x);
-    if (m.status[j] != kMultiOk) return;                  // block-uniform
+// Returns the visit count (-1: the visit set outgrew the LDS hash), block-uniform.
+__device__ int multi_bfs_query(FinShared& sh, const MultiArgs& m, int j, int* levels_out = nullptr,
+                               int* ns_out = nullptr) {
     const FinalizeArgs a = multi_view(m, j);
     const int tid = int(threadIdx.x), lane = lane_id(), wave = tid >> 6;
     if (wave == 0) {
-        const uint64_t key = lane < m.k ? m.seeds[int64_t(j) * kMultiCand + lane] : kEmptyKey;
+        const uint64_t key = lane < m.k ? m.seeds[int64_t(j) * m.seed_stride + lane] : kEmptyKey;
         const int ns = __popcll(__ballot(key != kEmptyKey));
         if (key != kEmptyKey) {
             const int32_t id = key_id(key);
@@ -663,6 +666,16 @@ __global__ __launch_bounds__(kFinThreads) void k_multi_bfs(MultiArgs m) {
             m.info[4 * j + 2] = ns;
         }
     }
+    if (levels_out) *levels_out = levels;
+    if (ns_out) *ns_out = ns;
+    return V;
+}
+
+__global__ __launch_bounds__(kFinThreads) void k_multi_bfs(MultiArgs m) {
+    __shared__ FinShared sh;
+    const int j = int(blockIdx.x);
+    if (m.status[j] != kMultiOk) return;                  // block-uniform
+    multi_bfs_query(sh, m, j);
 }
 
 // Scores of query j's visit set, level by level in the finalize kernel's arithmetic
@@ -694,11 +707,284 @@ __global__ __launch_bounds__(kFinThreads) void k_multi_select(MultiArgs m) {
         __syncthreads();
     }
     const int rc = min(a.rcap, V);
-    select_sorted(sh, a, V, rc);
+    if (a.rcap <= 64) {
+        // the rc best (score, id) keys from per-wave lists, then each result's hop from
+        // the one visit position that holds its node
+        __shared__ uint64_t s_res[64];
+        __shared__ int32_t s_hop[64];
+        const int lane = lane_id(), wave = tid >> 6;
+        uint64_t best = kEmptyKey, bthr = kEmptyKey;
+        for (int p0 = wave * 64; p0 < V; p0 += kFinThreads) {
+            const int p = p0 + lane;
+            wave_offer(best, bthr, p < V ? make_key(ld_coherent(a.vscore + p), uint32_t(a.vlist[p])) : kEmptyKey,
+                       lane, rc);
+        }
+        best = tree_merge(sh, best, rc);
+        if (wave == 0) s_res[lane] = best;
+        __syncthreads();
+        for (int p = tid; p < V; p += kFinThreads) {
+            const int32_t id = a.vlist[p];
+            for (int r = 0; r < rc; ++r)
+                if (key_id(s_res[r]) == id) s_hop[r] = a.vhop[p];
+        }
+        __syncthreads();
+        if (tid < rc) write_result(a, tid, s_res[tid], s_hop[tid]);
+    } else {
+        select_sorted(sh, a, V, rc);
+    }
     if (tid == 0) {
         ResultHeader h;
         h.count = rc; h.visited = V; h.levels = levels; h.n_seeds = ns;
         m.res[j] = h;
+    }
+}
+
+// ---- certified Q=1 global query ---------------------------------------------------------
+// The fp16 scan (rows e16, query q in fp32) kept its c best keys per workgroup in part.
+// Here they are merged to the c best overall, rescored in the fp32 scan's arithmetic
+// (QF32 dot, 16-lane reduction, fuse_score), and the k best exact keys are certified:
+// a row outside the candidates has fp16 score <= the c-th candidate's, and
+//   |fp16 score - fp32 score| <= |e16 - e|max |q| + g (|e16|max + |e|max) |q| + rounding
+// (g = (d/16 + 4) u, both scans' per-lane chains and reductions; weights <= 1), so a
+// k-th exact score above (c-th fp16 score + that bound) makes the seeds the fp32 scan's.
+template <typename QF>
+__global__ __launch_bounds__(kFinThreads) void k_cert_bfs(CertArgs a, MultiArgs m) {
+    __shared__ FinShared sh;
+    __shared__ uint64_t s_cand[64];
+    __shared__ uint64_t s_exact[64];
+    __shared__ double s_qn;
+    __shared__ double s_eps;
+    const int tid = int(threadIdx.x), lane = lane_id(), wave = tid >> 6;
+    const int c = a.c;
+    // A. the c best candidate keys (the finalize kernel's merge, 8 loads in flight per lane)
+    uint64_t list = kEmptyKey, thr = kEmptyKey;
+    const int n_part = int(*a.gcnt);
+    const uint64_t gb = *a.gthr;                 // the scan's final bound: the c best are <= it
+    for (int base = wave * 64; base < n_part; base += kFinThreads * 8) {
+        uint64_t x[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int i = base + j * kFinThreads + lane;
+            x[j] = (i < n_part && a.part[i] <= gb) ? a.part[i] : kEmptyKey;
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) wave_offer(list, thr, x[j], lane, c);
+    }
+    list = tree_merge(sh, list, c, n_part <= kFinThreads ? (n_part + 63) / 64 : kFinWaves);
+    if (wave == 0) s_cand[lane] = list;
+    if (wave == 1) {
+        double sq = 0.0;
+        for (int i = lane; i < a.d; i += 64) sq += double(a.q[i]) * double(a.q[i]);
+        sq = wave_sum_f64(sq);
+        if (lane == 0) s_qn = sqrt(sq);
+    }
+    __syncthreads();
+    // B. exact rescoring: 16-lane group g takes candidate g
+    const int g = tid >> 4, sub = tid & 15;
+    const uint64_t ck = s_cand[g];
+    uint64_t key = kEmptyKey;
+    if (ck != kEmptyKey) {                       // uniform over the group
+        QF qf;
+        qf.load(a.q, sub);
+        const int32_t id = key_id(ck);
+        const float dot = qf.dot(a.emb + int64_t(id) * a.d, sub);
+        const QueryTerms t{a.t_q, a.lambda, a.mod_filter, -1, 0.0f};
+        const float sc = fuse_score(row16_sum(dot), a.ts[id], (a.mod_filter >= 0) ? a.mods[id] : 0, -1, t);
+        key = make_key(sc, uint32_t(id));
+    }
+    if (sub == 0) s_exact[g] = key;
+    __syncthreads();
+    if (wave == 0) {
+    // C. the k best exact keys and the certificate
+    const uint64_t x = wave_sort64(s_exact[lane], lane);
+    const uint64_t cl = s_cand[lane];
+    const int nc = __popcll(__ballot(cl != kEmptyKey));
+    const uint64_t c_last = __shfl(cl, c - 1);
+    const int kk = a.k < c ? a.k : c;
+    const uint64_t kth = __shfl(x, kk - 1);
+    bool ok = false;
+    float margin = __builtin_inff();
+    const double e32 = double(__uint_as_float(a.nrm[0]));
+    const double e16 = double(__uint_as_float(a.nrm[1]));
+    const double de = double(__uint_as_float(a.nrm[2]));
+    const double qn = s_qn, u = 0x1p-24, nq = double(a.d) / 16.0 + 4.0;
+    const double gs = nq * u / (1.0 - nq * u);
+    const double eps = (de * qn + gs * (e16 + e32) * qn + u * (e16 + e32) * qn * (1.0 + gs)) * 1.01 +
+                       1e-30 * double(a.d);
+    if (lane == 0) s_eps = eps;
+    if (a.k <= c) {
+        if (nc < c) {
+            ok = true;                           // every live row was a candidate
+        } else {
+            const float s16 = key_score(c_last), s32 = key_score(kth);
+            if (eps < 1e30) {
+                if (s16 == -FLT_MAX) {
+                    ok = e16 * qn * 2.0 < double(FLT_MAX);    // the c-th candidate is filtered
+                } else {
+                    const double mg = double(s32) - (double(s16) + eps);
+                    ok = mg > 0.0;
+                    margin = float(mg);
+                }
+            } else {
+                margin = -__builtin_inff();
+            }
+        }
+    }
+    a.seeds[lane] = (ok && lane < kk) ? x : kEmptyKey;
+    if (lane == 0) {
+        *a.status = ok ? kMultiOk : kMultiUncertified;
+        *a.margin = margin;
+        *a.gcnt = 0u;                            // the scan's count and bound, for the next query
+        *a.gthr = kEmptyKey;
+        sh.s_misc[6] = ok ? 1 : 0;
+    }
+    }
+    __threadfence_block();
+    __syncthreads();
+    // D. the certified seeds' BFS (visit set, hops, parents) in the same workgroup
+    if (!a.finish) {
+        if (sh.s_misc[6]) multi_bfs_query(sh, m, 0);
+        return;
+    }
+    auto fail = [&](int32_t code) {
+        if (tid == 0) {
+            ResultHeader h;
+            h.count = -1; h.visited = code; h.levels = 0; h.n_seeds = 0;
+            m.res[0] = h;
+        }
+    };
+    if (!sh.s_misc[6]) { fail(kMultiUncertified); return; }
+    int levels = 0, ns = 0;
+    const int V = multi_bfs_query(sh, m, 0, &levels, &ns);
+    if (V < 0) { fail(kMultiOverflow); return; }
+    __threadfence_block();
+    __syncthreads();
+    // E. the results from intervals: BFS scores computed from the fp16 scan's fused scores
+    // (each within eps of the exact one) lie within a propagated bound of the exact BFS
+    // scores; at least rc nodes have exact scores >= the rc-th largest lower end, so a
+    // node whose upper end is below it cannot be a result. The others (with their BFS
+    // ancestors) are rescored exactly and propagated in the finalize kernel's arithmetic.
+    const FinalizeArgs v = multi_view(m, 0);
+    const float dlt = m.hop_decay;               // in [0, 1] (checked by the caller)
+    const double eps = s_eps;
+    const double u = 0x1p-24;
+    // per position: approximate BFS score (vscore) and a bound on its distance to the
+    // exact one (dv): seeds are exact; a node's bound is the larger of its two terms'
+    //   parent term  |fl(x d) - fl(y d)| <= d |x - y| + u d (|x| + |y|)
+    //   own term     |0.8 f16 - 0.8 f32| + rounding, with |f16 - f32| <= eps (0 for a
+    //                filtered row: both scans give -FLT_MAX)
+    float* dv = reinterpret_cast<float*>(&sh.u.bfs.rstart[0]);      // later: exact scores
+    if (tid == 0) sh.s_misc[7] = 0;
+    for (int p = tid; p < ns; p += kFinThreads) dv[p] = 0.0f;
+    __syncthreads();
+    for (int h = 1; h <= levels; ++h) {
+        for (int p = ns + tid; p < V; p += kFinThreads) {
+            if (ld_coherent(v.vhop + p) != h) continue;
+            const int32_t id = ld_coherent(v.vlist + p);
+            const int par = ld_coherent(v.vpar + p);
+            const float f = a.fin16[id];
+            const float sp = ld_coherent(v.vscore + par);
+            const double dp = double(dv[par]);
+            const float sc = fmaxf(sp * dlt, f * 0.8f);
+            const double ea = dp > 0.0 ? double(dlt) * dp + 2.0 * u * double(dlt) * (fabs(double(sp)) + dp) : 0.0;
+            const bool filtered = a.mod_filter >= 0 && a.mods[id] != a.mod_filter;
+            const double eb = filtered ? 0.0 : 0.8 * eps + 0.8 * u * (2.0 * fabs(double(f)) + eps);
+            const double d = (ea > eb ? ea : eb) * (1.0 + 1e-6);
+            v.vscore[p] = sc;
+            dv[p] = float(d) < d ? nextafterf(float(d), __builtin_inff()) : float(d);
+            if (!(fabs(double(sc)) < 1e38) && !filtered) sh.s_misc[7] = 1;
+            if (!(d < 1e30)) sh.s_misc[7] = 1;
+        }
+        __threadfence_block();
+        __syncthreads();
+    }
+    if (sh.s_misc[7]) { fail(kMultiUncertified); return; }
+    const int rc = min(m.rcap, V);
+    // the rc-th largest lower end (approximate score - bound, rounded down)
+    uint64_t best = kEmptyKey, bthr = kEmptyKey;
+    for (int p0 = wave * 64; p0 < V; p0 += kFinThreads) {
+        const int p = p0 + lane;
+        uint64_t key = kEmptyKey;
+        if (p < V) {
+            const double lo = double(ld_coherent(v.vscore + p)) - double(dv[p]);
+            float lf = float(lo);
+            if (double(lf) > lo) lf = nextafterf(lf, -__builtin_inff());
+            key = make_key(lf, uint32_t(ld_coherent(v.vlist + p)));
+        }
+        wave_offer(best, bthr, key, lane, rc);
+    }
+    best = tree_merge(sh, best, rc);
+    if (wave == 0 && lane == rc - 1) sh.s_misc[5] = int(__float_as_uint(key_score(best)));
+    __syncthreads();
+    const double cut = double(__uint_as_float(uint32_t(sh.s_misc[5])));
+    // mark the candidates and their ancestors (flags in the freed hash keys)
+    uint32_t* flag = sh.u.bfs.hkey;
+    int32_t* rlist = reinterpret_cast<int32_t*>(sh.u.bfs.hval);
+    for (int p = tid; p < V; p += kFinThreads) flag[p] = 0u;
+    __syncthreads();
+    for (int p = tid; p < V; p += kFinThreads) {
+        if (double(ld_coherent(v.vscore + p)) + double(dv[p]) >= cut) {
+            for (int x = p; x >= 0; x = ld_coherent(v.vpar + x)) flag[x] = 1u;
+        }
+    }
+    __syncthreads();
+    // compact the marked positions (ascending)
+    int r = 0;
+    for (int p0 = 0; p0 < V; p0 += kFinThreads) {
+        const int p = p0 + tid;
+        const int on = (p < V && flag[p]) ? 1 : 0;
+        int tot = 0;
+        const int o = block_excl_scan(on, sh.s_wave, &tot);
+        if (on) rlist[r + o] = p;
+        r += tot;
+    }
+    __syncthreads();
+    // exact fused scores of the marked nodes past the seeds (one per 16-lane group)
+    {
+        QF qf;
+        qf.load(a.q, sub);
+        const QueryTerms t{a.t_q, a.lambda, a.mod_filter, -1, 0.0f};
+        for (int i = g; i < r; i += kFinThreads / 16) {
+            const int p = rlist[i];
+            if (p < ns) continue;                // uniform over the group
+            const int32_t id = ld_coherent(v.vlist + p);
+            const float dot = qf.dot(a.emb + int64_t(id) * a.d, sub);
+            const float sc = fuse_score(row16_sum(dot), a.ts[id], (a.mod_filter >= 0) ? a.mods[id] : 0, -1, t);
+            if (sub == 0) m.vfin[p] = sc;
+        }
+    }
+    __threadfence_block();
+    __syncthreads();
+    // exact BFS scores over the marked set, level by level (parents are marked too);
+    // they replace the bounds in dv, which the marking above was the last to read
+    for (int h = 0; h <= levels; ++h) {
+        for (int i = tid; i < r; i += kFinThreads) {
+            const int p = rlist[i];
+            if (ld_coherent(v.vhop + p) != h) continue;
+            dv[p] = (h == 0) ? ld_coherent(v.vscore + p)
+                             : fmaxf(dv[ld_coherent(v.vpar + p)] * dlt, ld_coherent(m.vfin + p) * 0.8f);
+        }
+        __syncthreads();
+    }
+    // the rc best exact keys among the marked nodes, and their hops
+    best = kEmptyKey;
+    bthr = kEmptyKey;
+    for (int i0 = wave * 64; i0 < r; i0 += kFinThreads) {
+        const int i = i0 + lane;
+        wave_offer(best, bthr, i < r ? make_key(dv[rlist[i]], uint32_t(ld_coherent(v.vlist + rlist[i]))) : kEmptyKey, lane, rc);
+    }
+    best = tree_merge(sh, best, rc);
+    if (wave == 0 && lane < rc) {
+        const int32_t id = key_id(best);
+        int32_t hop = 0;
+        for (int i = 0; i < r; ++i)
+            if (ld_coherent(v.vlist + rlist[i]) == id) hop = ld_coherent(v.vhop + rlist[i]);
+        write_result(v, lane, best, hop);
+    }
+    if (tid == 0) {
+        ResultHeader h;
+        h.count = rc; h.visited = V; h.levels = levels; h.n_seeds = ns;
+        m.res[0] = h;
     }
 }
 
@@ -910,6 +1196,20 @@ int launch_tile_merge(uint64_t* part, uint32_t* gcnt, uint64_t* carry, int32_t k
 int launch_finalize(const FinalizeArgs& a, hipStream_t s) {
     MARS_LAUNCH(k_finalize, dim3(1), dim3(kFinThreads), 0, s, a);
     return MARS_OK;
+}
+
+int launch_cert_bfs(const CertArgs& a, const MultiArgs& m, hipStream_t s) {
+    if (a.d % 64 == 0) {
+        switch (a.d / 64) {
+            case 4: MARS_LAUNCH(k_cert_bfs<QF32<4>>, dim3(1), dim3(kFinThreads), 0, s, a, m); return MARS_OK;
+            case 6: MARS_LAUNCH(k_cert_bfs<QF32<6>>, dim3(1), dim3(kFinThreads), 0, s, a, m); return MARS_OK;
+            case 8: MARS_LAUNCH(k_cert_bfs<QF32<8>>, dim3(1), dim3(kFinThreads), 0, s, a, m); return MARS_OK;
+            case 12: MARS_LAUNCH(k_cert_bfs<QF32<12>>, dim3(1), dim3(kFinThreads), 0, s, a, m); return MARS_OK;
+            case 16: MARS_LAUNCH(k_cert_bfs<QF32<16>>, dim3(1), dim3(kFinThreads), 0, s, a, m); return MARS_OK;
+            default: break;
+        }
+    }
+    return set_error(MARS_ERR_UNSUPPORTED, "certified query: embedding_dim %d unsupported", a.d);
 }
 
 int launch_multi_bfs(const MultiArgs& a, hipStream_t s) {

@@ -169,38 +169,25 @@ __global__ __launch_bounds__(256) void k_multi_seed(SeedArgs a) {
 }
 
 // Exact fused score of every visited node past the seeds: block (x, j) covers visit
-// positions 64x .. 64x+63 of query j, four per 16-lane group (loads of all four rows
-// in flight; positions outside [seeds, visited) read row 0 and are not stored).
+// positions 16x .. 16x+15 of query j, one per 16-lane group (blocks past the visit
+// count exit at once).
 template <typename T, typename QF>
 __global__ __launch_bounds__(256) void k_visit_scores(VisitScoreArgs a) {
     const int j = int(blockIdx.y);
     if (a.status[j] != kMultiOk) return;
     const int V = a.info[4 * j], ns = a.info[4 * j + 2];
-    const int p0 = int(blockIdx.x) * 64;
-    if (p0 >= V) return;
-    const int tid = int(threadIdx.x), sub = tid & 15, g = tid >> 4;
+    const int p = int(blockIdx.x) * 16 + int(threadIdx.x >> 4);
+    if (int(blockIdx.x) * 16 >= V) return;
+    if (p < ns || p >= V) return;                // whole 16-lane group
+    const int sub = int(threadIdx.x & 15u);
     QF qf;
     if constexpr (std::is_same_v<QF, QGeneric>) qf.d = a.d;
     qf.load(a.queries + int64_t(j) * a.d, sub);
-    const QueryTerms t{a.tq[j], a.lambda, a.mod_filter, -1, 0.0f};
-    const int32_t* vl = a.vlist + int64_t(j) * kMultiVisit;
-    const T* emb = static_cast<const T*>(a.emb);
-    int32_t id[4];
-    bool valid[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int p = p0 + g + 16 * i;
-        valid[i] = p >= ns && p < V;
-        id[i] = valid[i] ? vl[p] : 0;
-    }
-    float dot[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) dot[i] = qf.dot(emb + int64_t(id[i]) * a.d, sub);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const float s = fuse_score(row16_sum(dot[i]), a.ts[id[i]], (a.mod_filter >= 0) ? a.mods[id[i]] : 0, -1, t);
-        if (valid[i] && sub == 0) a.vfin[int64_t(j) * kMultiVisit + p0 + g + 16 * i] = s;
-    }
+    const QueryTerms t{a.tq ? a.tq[j] : a.t_q_value, a.lambda, a.mod_filter, -1, 0.0f};
+    const int32_t id = a.vlist[int64_t(j) * kMultiVisit + p];
+    const float dot = qf.dot(static_cast<const T*>(a.emb) + int64_t(id) * a.d, sub);
+    const float s = fuse_score(row16_sum(dot), a.ts[id], (a.mod_filter >= 0) ? a.mods[id] : 0, -1, t);
+    if (sub == 0) a.vfin[int64_t(j) * kMultiVisit + p] = s;
 }
 
 template <typename T, typename QF>
@@ -211,7 +198,7 @@ int launch_seed_t(const SeedArgs& a, hipStream_t s) {
 
 template <typename T, typename QF>
 int launch_visit_t(const VisitScoreArgs& a, hipStream_t s) {
-    MARS_LAUNCH((k_visit_scores<T, QF>), dim3(unsigned(kMultiVisit / 64), unsigned(a.q)), dim3(256), 0, s, a);
+    MARS_LAUNCH((k_visit_scores<T, QF>), dim3(unsigned(kMultiVisit / 16), unsigned(a.q)), dim3(256), 0, s, a);
     return MARS_OK;
 }
 
