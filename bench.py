@@ -85,7 +85,7 @@ def tiled_pass(args, mars_amd, corpus, c, qnodes, N, D, K, pctl, lat_resident, h
 
 
 SERVE_MODES = {
-    "q1": "one global query per call; each insert finds its own k-NN",
+    "q1": "one global query per call (certified fp16 scan); each insert finds its own k-NN",
     "batch": "batched global calls; each insert finds its own k-NN",
     "link": "batched global calls that also find the k-NN of the nodes inserted since the last call "
             "(one corpus pass for both); inserts publish rows and episode edges only",
@@ -133,9 +133,11 @@ def serve_pass(args, mars_amd, corpus, lib, check, full, dg, ctx, qnodes, nq, ep
     b.ins_stats, b.ins_start_us = C.cast(ins, C.c_void_p).value, pv(istart)
     b.link_deferred, b.max_link, b.ins_linked_us, b.link_wait_us = int(mode == "link"), 1024, pv(ilinked), 5000.0
     t0 = time.time()
+    ctx.certified = True          # a global query answered alone uses the certified fp16 scan
     try:
         check(lib.mars_bench_serve(dg.handle, ctx.handle, ectx.handle, C.byref(b)), "mars_bench_serve")
     finally:
+        ctx.certified = False
         wall = time.time() - t0
         mars_amd.destroy_query_context(ectx)
         gq.free()

@@ -1218,11 +1218,29 @@ int mars_query_global_batch_knn(const mars_graph* gh, mars_ctx* ch, const float*
     st.n_live = n_live;
     st.min_margin = FLT_MAX;
     std::vector<int32_t> q1;                    // queries the Q=1 path answers
-    const int32_t Qg = batched ? Q : 0;         // global queries in the shared scan
-    const int32_t Qt = Qg + knn_count;          // + k-NN queries (plain dot products)
+    // A lone global query (no neighbour search) is cheaper on the Q=1 certified path: its
+    // fp16 scan beats the MFMA kernel with one query lane of 64, and the results are the same.
+    const bool lone = batched && Q == 1 && knn_count == 0 && !fp16 && g.d % 128 == 0 && g.d <= 1024;
+    const int32_t Qg = (batched && !lone) ? Q : 0;   // global queries in the shared scan
+    const int32_t Qt = Qg + knn_count;               // + k-NN queries (plain dot products)
     if (!batched) {
         st.whole_batch_q1 = Q > 0 ? 1 : 0;
         for (int32_t j = 0; j < Q; ++j) q1.push_back(j);
+    }
+    if (lone) {
+        const auto tl = clk::now();
+        const uint32_t saved = c.flags;
+        c.flags |= MARS_CTX_CERTIFIED;
+        mars_stats s1{};
+        const int rc = query_impl(gh, ch, nullptr, dq, h_tq[0], cfg, out, cap, &n_out[0], &s1, n_live);
+        c.flags = saved;
+        MARS_TRY(rc);
+        if (s1.seeds_certified) ++st.batched; else ++st.uncertified;
+        st.q1_us = 0.0;
+        st.wall_us = std::chrono::duration<double, std::micro>(clk::now() - t0).count();
+        (void)tl;
+        if (stats) *stats = st;
+        return MARS_OK;
     }
     if (Qt > 0) {
         int32_t nrr = 0, nqb = 0;

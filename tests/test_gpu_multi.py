@@ -107,6 +107,15 @@ def test_batched_equals_q1(dev10k, corpus_10k, ci):
         assert st.min_margin > 0
 
 
+def test_single_query_batch(dev10k, corpus_10k):
+    """A batch of one global query takes the certified Q=1 path: same answers."""
+    for i, cfg in enumerate(CONFIGS[:4]):
+        qn = corpus.pick_queries(corpus_10k.modalities, 1, seed=840 + i)
+        got, want, st = run_both(dev10k, corpus_10k.embeddings[qn], T_Q, cfg)
+        assert_same(got, want)
+        assert st.batched == 1
+
+
 def test_batched_per_query_times(dev10k, corpus_10k, rng):
     qn = corpus.pick_queries(corpus_10k.modalities, 40, seed=801)
     tq = rng.uniform(300, 600, size=40).astype(np.float32)
