@@ -203,7 +203,7 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU; --gpus above 1 is not supported here "
-              "(the path would shard by node range, see DESIGN.md)", file=sys.stderr)
+              "(the path would shard by node-id range: each GPU scans its share, then one all-gather of K keys)", file=sys.stderr)
         return 2
 
     import mars_amd
