@@ -322,7 +322,14 @@ def main() -> int:
         st = mars_amd.RetrievalStats()
         mars_amd.query_memory_fast_device(dg, ctx, dq.ptr + (W + i) * D * 4, corpus.QUERY_TIME, gcfg, st)
         n_cert += st.seeds_certified
+    cph = []
+    for node in qnodes[W:W + 200]:
+        mars_amd.query_memory_fast(dg, ctx, c.embeddings[node], corpus.QUERY_TIME, gcfg)
+        cph.append(ctx.last_phases(6))
+    cph = np.array(cph).mean(0)
     ctx.certified = False
+    log("certified phases (us, mean): merge {:.1f}  rescore+certify {:.1f}  bfs {:.1f}  mark {:.1f}  "
+        "exact {:.1f}  results {:.1f}".format(*cph))
     log(f"global certified (fp16 scan, exact results): p50 {pctl(lat_c, .5):.1f} us p99 {pctl(lat_c, .99):.1f} us; "
         f"{S / wall_c:.0f} q/s; scan kernel mean {kern_c.mean():.1f} us ({bytes_f16 / kern_c.mean() / 1e3:.0f} GB/s); "
         f"seeds + BFS + results {rest_c.mean():.1f} us; certified {n_cert}/{n_samp}")
@@ -430,7 +437,9 @@ def main() -> int:
                                  p99_us_with_events=pctl(lat_ck, .99), scan_kernel_mean_us=float(kern_c.mean()),
                                  seeds_bfs_results_mean_us=float(rest_c.mean()),
                                  scan_gbs=achieved, scan_frac=achieved / HBM_PEAK_GBS,
-                                 certified=n_cert, certified_sample=n_samp),
+                                 certified=n_cert, certified_sample=n_samp,
+                                 phases_us=dict(zip(("merge", "rescore_certify", "bfs", "mark", "exact", "results"),
+                                                    [round(float(x), 2) for x in cph]))),
         "global_fp32": dict(p50_us=pctl(lat_g, .5), p99_us=pctl(lat_g, .99), qps=S / wall_g,
                             p99_us_with_events=pctl(lat_gk, .99),
                             graph_replay=dict(p50_us=pctl(lat_gg, .5), p99_us=pctl(lat_gg, .99)),

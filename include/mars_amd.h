@@ -365,8 +365,10 @@ int mars_query_global_batch_knn(const mars_graph* g, mars_ctx* ctx, const float*
  * its seed list (top-K ids and scores, K entries) to host memory. */
 int mars_ctx_last_scores(mars_ctx* ctx, float* h_scores, int64_t n);
 int mars_ctx_last_seeds(mars_ctx* ctx, int32_t* h_idx, float* h_val, int32_t k, int32_t* k_out);
-/* Durations (us) of the last global query's finalize phases: seed merge, BFS,
- * result selection (n <= 3), from the GPU's 100 MHz realtime counter. */
+/* Durations (us) of the last global query's phases after the scan, from the GPU's
+ * 100 MHz realtime counter. fp32 path (n <= 3): seed merge, BFS, result selection.
+ * Certified path (n <= 6): candidate merge, exact rescoring + certificate, interval
+ * BFS, candidate marking, exact rescoring of the marked nodes, results. */
 int mars_ctx_last_phases(mars_ctx* ctx, double* us, int32_t n);
 /* The last global query's visit list in discovery order (seeds first, then BFS
  * level by level): node ids, hop levels and BFS scores; *n_out = nodes visited. */

@@ -283,9 +283,11 @@ class QueryContext:
         check(lib.mars_ctx_last_seeds(self.handle, _ptr(idx), _ptr(val), 64, C.byref(k)), "mars_ctx_last_seeds")
         return idx[: k.value].copy(), val[: k.value].copy()
 
-    def last_phases(self):
-        us = np.zeros(3, np.float64)
-        check(lib.mars_ctx_last_phases(self.handle, _ptr(us), 3), "mars_ctx_last_phases")
+    def last_phases(self, n: int = 3):
+        """Phase durations (us) after the last global query's scan: 3 for the fp32 path,
+        6 for the certified path (see mars_ctx_last_phases)."""
+        us = np.zeros(n, np.float64)
+        check(lib.mars_ctx_last_phases(self.handle, _ptr(us), n), "mars_ctx_last_phases")
         return us
 
     def last_visited(self):

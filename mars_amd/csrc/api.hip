@@ -30,7 +30,7 @@ namespace {
 thread_local char g_err[1024] = "";
 constexpr int32_t kMaxWg = 4096;     // upper bound of scan workgroups (partials buffer)
 constexpr int32_t kTargetWg = 2048;  // scan workgroups (grid-stride; 8 per CU on 256 CUs)
-constexpr int32_t kTargetWgF16 = 1024;   // fp16 rows: 241 us vs 249 us at 2048 (N=1M, D=768)
+constexpr int32_t kTargetWgF16 = 768;    // fp16 rows: 236 us vs 241 us at 1024, 249 us at 2048 (N=1M, D=768)
 
 int ensure_device(int* dev) {
     int d = 0;
@@ -233,7 +233,7 @@ int certified_query(const Graph& g, Ctx& c, const float* q, float t_q, const mar
     ca.part = c.part; ca.gcnt = c.gcnt; ca.gthr = c.gthr; ca.c = cands; ca.k = K; ca.q = q; ca.d = g.d;
     ca.emb = g.emb; ca.ts = g.ts; ca.mods = g.mods; ca.t_q = t_q; ca.lambda = cfg->time_decay_lambda;
     ca.mod_filter = cfg->modality_filter; ca.nrm = g.nrm; ca.seeds = c.mseed; ca.status = c.mstat;
-    ca.margin = c.mmargin; ca.fin16 = c.fin;
+    ca.margin = c.mmargin; ca.fin16 = c.fin; ca.stamps = c.stamps + 4;
     // one workgroup finishes the query when the interval argument applies
     const float dlt = cfg->bfs_score_decay;
     ca.finish = (rcap <= 64 && dlt >= 0.0f && dlt <= 1.0f) ? 1 : 0;
@@ -316,6 +316,7 @@ int query_impl(const mars_graph* gh, mars_ctx* ch, const float* h_q, const float
         bool answered = false;
         ResultHeader h{};
         MARS_TRY(certified_query(g, c, q, t_q, cfg, K, hops, rcap, n_live, out, cap, n_out, &answered, &h));
+        c.last_certified = answered ? 1 : 0;
         if (answered) {
             c.last_k = h.n_seeds;
             c.last_visited = 0;               // the debug hooks describe fp32 scans only
@@ -410,6 +411,7 @@ int query_impl(const mars_graph* gh, mars_ctx* ch, const float* h_q, const float
             return set_error(MARS_ERR_HIP, "finalize launch failed");
         }
         c.last_n = n_live;
+        c.last_certified = 0;
     }
     if (timing) MARS_HIP(hipEventRecord(c.ev[2], s));
     MARS_HIP(hipStreamSynchronize(s));
@@ -765,7 +767,7 @@ int mars_ctx_create(int32_t max_nodes, int32_t dim, int32_t max_k, uint32_t flag
         (rc = dmalloc(&c.claim, N)) || (rc = dmalloc(&c.vlist, N)) || (rc = dmalloc(&c.vhop, N)) ||
         (rc = dmalloc(&c.vscore, N)) || (rc = dmalloc(&c.vro, 2 * N)) || (rc = dmalloc(&c.sortbuf, 2 * size_t(kSortCap))) ||
         (rc = dmalloc(&c.seed_idx, size_t(kMaxK))) || (rc = dmalloc(&c.seed_val, size_t(kMaxK))) ||
-        (rc = dmalloc(&c.stamps, 4)) || (rc = dmalloc(&c.gthr, 1)) || (rc = dmalloc(&c.gcnt, 1)))
+        (rc = dmalloc(&c.stamps, 12)) || (rc = dmalloc(&c.gthr, 1)) || (rc = dmalloc(&c.gcnt, 1)))
         return fail(rc);
     e = hipMemset(c.vis, 0, N * sizeof(uint32_t));
     if (e == hipSuccess) e = hipMemset(c.gthr, 0xFF, sizeof(uint64_t));
@@ -888,9 +890,14 @@ int mars_bench_serve(mars_graph* g, mars_ctx* cg, mars_ctx* ce, mars_serve_bench
     using clk = std::chrono::steady_clock;
     const auto start = clk::now();
     auto since = [&]() { return std::chrono::duration<double, std::micro>(clk::now() - start).count(); };
+    // Arrival times are honoured to about a microsecond: sleep until shortly before (a
+    // sleeping thread may wake tens of microseconds late), then spin. Latency is measured
+    // from the arrival time, so a late wake-up would count against the query.
     auto wait_until = [&](double us) {
-        std::this_thread::sleep_until(start + std::chrono::duration_cast<clk::duration>(
-                                                  std::chrono::duration<double, std::micro>(us)));
+        const auto due = start + std::chrono::duration_cast<clk::duration>(std::chrono::duration<double, std::micro>(us));
+        const auto early = due - std::chrono::microseconds(200);
+        if (clk::now() < early) std::this_thread::sleep_until(early);
+        while (clk::now() < due) std::this_thread::yield();
     };
     const int64_t D = g->g.d;
     const bool deferred = b->link_deferred != 0 && b->n_insert > 0;
@@ -1439,11 +1446,13 @@ int mars_ctx_last_seeds(mars_ctx* ch, int32_t* idx, float* val, int32_t k, int32
 }
 
 int mars_ctx_last_phases(mars_ctx* ch, double* us, int32_t n) {
-    MARS_CHECK(ch && us && n >= 0 && n <= 3, MARS_ERR_INVALID, "bad arguments");
+    MARS_CHECK(ch && us && n >= 0 && n <= 6, MARS_ERR_INVALID, "bad arguments");
     MARS_TRY(use_device(ch->c.device));
-    uint64_t t[4] = {0, 0, 0, 0};
+    uint64_t t[12] = {};
     MARS_HIP(hipMemcpy(t, ch->c.stamps, sizeof(t), hipMemcpyDeviceToHost));
-    for (int32_t i = 0; i < n; ++i) us[i] = double(t[i + 1] - t[i]) * 0.01;   // 100 MHz counter
+    const uint64_t* p = ch->c.last_certified ? t + 4 : t;     // certified: 7 stamps from t[4]
+    const int32_t np = ch->c.last_certified ? 6 : 3;
+    for (int32_t i = 0; i < n; ++i) us[i] = i < np ? double(p[i + 1] - p[i]) * 0.01 : 0.0;   // 100 MHz counter
     return MARS_OK;
 }
 

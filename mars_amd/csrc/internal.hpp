@@ -208,6 +208,7 @@ struct Ctx {
     int32_t last_n = 0;            // node count of the last global query
     int32_t last_k = 0;
     int32_t last_visited = 0;      // visit-list length of the last global query
+    int32_t last_certified = 0;    // the last global query took the certified path
     // batched scoring scratch (grown on demand)
     __half* bq = nullptr;          // queries in fp16
     float* btq = nullptr;          // query times
@@ -321,7 +322,10 @@ struct FinalizeArgs {
     int32_t* vhop;
     float* vscore;
     int64_t* vro;            // per visit position: the node's (len << 32) | start
-    int32_t* vpar;           // per visit position: the parent's position (unscored BFS only)
+    int32_t* vpar;           // per visit position: the parent's position (unscored / interval BFS)
+    float* vdv;              // interval BFS: per visit position, a bound on the score's error
+    double eps;              // interval BFS: bound on |a.fin - exact fused score| of any row
+    int32_t mod_filter;      // interval BFS: filtered rows' scores are exact
     uint64_t* sortbuf;
     int32_t cap_visit;
     int32_t rcap;            // results requested (max_results or K)
@@ -495,6 +499,7 @@ struct CertArgs {
     uint64_t* seeds;         // 64 entries: ascending exact keys, the first k are the seeds
     int32_t* status;
     float* margin;
+    uint64_t* stamps;        // 7 realtime stamps of the phases, or null
 };
 int launch_cert_bfs(const CertArgs& a, const struct MultiArgs& m, hipStream_t s);   // + BFS of query 0 of m
 int launch_multi_bfs(const MultiArgs& a, hipStream_t s);

@@ -272,10 +272,16 @@ __device__ inline int round_rank(FinShared& sh, bool won, int* rank) {
 // was touched, so the caller can run the global-array BFS instead).
 // With rk > 0 every wave also keeps the rk best (score, id) keys it emits in
 // `best` (wave 0 starts from the seeds), so the results need only a tree merge.
-// SCORED == false: the visit set, hops and parents only (a.vpar gets each node's
-// parent position, no score is read or written; rk must be 0). The visit order
-// and the parents do not depend on scores, so scores can be propagated later.
-template <bool SCORED>
+// Modes: kBfsScored scores every node from a.fin (the finalize kernel). kBfsUnscored
+// records the visit set, hops and parents only (a.vpar gets each node's parent
+// position, no score is read or written; rk must be 0): the visit order and the
+// parents do not depend on scores, so scores can be propagated later. kBfsInterval
+// also records parents, scores every node from a.fin as an approximation of a score
+// with error <= a.eps per fused score, and writes a bound on each node's error to
+// a.vdv; `best` then tracks lower ends (score - bound, rounded down). A non-finite
+// score or bound sets sh.s_misc[7].
+constexpr int kBfsUnscored = 0, kBfsScored = 1, kBfsInterval = 2;
+template <int MODE>
 __device__ int bfs_lds(FinShared& sh, const FinalizeArgs& a, int ns, int* levels_out, uint64_t& best,
                        uint64_t& bthr, int rk) {
     constexpr int R = 4;                       // 1024-edge rounds cached in registers
@@ -300,11 +306,13 @@ __device__ int bfs_lds(FinShared& sh, const FinalizeArgs& a, int ns, int* levels
                 // and the two scores the emit needs stay in registers.
                 int32_t nb[R], pp[R], slot[R];
                 int64_t rw[R];
-                float fv[R], ps[R];
+                float fv[R], ps[R], pd[R];
+                bool filt[R];
 #pragma unroll
                 for (int r = 0; r < R; ++r) {
                     const int t = s0 + r * kFinThreads + tid;
                     slot[r] = -1; nb[r] = -1; pp[r] = 0; fv[r] = 0.0f; ps[r] = 0.0f; rw[r] = 0;
+                    pd[r] = 0.0f; filt[r] = false;
                     if (t < T) {
                         const int p = owner_of(sh.u.bfs.eoff, cn, t);
                         pp[r] = c0 + p;
@@ -314,9 +322,13 @@ __device__ int bfs_lds(FinShared& sh, const FinalizeArgs& a, int ns, int* levels
 #pragma unroll
                 for (int r = 0; r < R; ++r) {
                     if (s0 + r * kFinThreads + tid < T && uint32_t(nb[r]) < uint32_t(a.n_live)) {
-                        if constexpr (SCORED) {
+                        if constexpr (MODE != kBfsUnscored) {
                             fv[r] = a.fin[nb[r]];
                             ps[r] = ld_coherent(a.vscore + pp[r]);
+                        }
+                        if constexpr (MODE == kBfsInterval) {
+                            pd[r] = ld_coherent(a.vdv + pp[r]);
+                            filt[r] = a.mod_filter >= 0 && a.mods[nb[r]] != a.mod_filter;
                         }
                         rw[r] = a.ro[nb[r]];
                         slot[r] = hash_find_or_insert(sh, nb[r]);
@@ -334,17 +346,33 @@ __device__ int bfs_lds(FinShared& sh, const FinalizeArgs& a, int ns, int* levels
                     int rank = 0;
                     const int wtot = round_rank(sh, won, &rank);
                     const float sc = fmaxf(ps[r] * a.hop_decay, fv[r] * 0.8f);
+                    uint64_t lkey = kEmptyKey;
                     if (won) {
                         const int pos = out + rank;
                         a.vlist[pos] = nb[r];
                         a.vhop[pos] = h + 1;
-                        if constexpr (SCORED) a.vscore[pos] = sc;
-                        else a.vpar[pos] = pp[r];
+                        if constexpr (MODE != kBfsUnscored) a.vscore[pos] = sc;
+                        if constexpr (MODE != kBfsScored) a.vpar[pos] = pp[r];
+                        if constexpr (MODE == kBfsInterval) {
+                            // parent term |fl(x d) - fl(y d)| <= d |x - y| + u d (|x| + |y|); own
+                            // term 0.8 eps + rounding (0 for a filtered row: both scans give -FLT_MAX)
+                            const double u = 0x1p-24, dl = double(a.hop_decay), dp = double(pd[r]);
+                            const double ea = dp > 0.0 ? dl * dp + 2.0 * u * dl * (fabs(double(ps[r])) + dp) : 0.0;
+                            const double eb = filt[r] ? 0.0 : 0.8 * a.eps + 0.8 * u * (2.0 * fabs(double(fv[r])) + a.eps);
+                            const double d = (ea > eb ? ea : eb) * (1.0 + 1e-6);
+                            a.vdv[pos] = float(d) < d ? nextafterf(float(d), __builtin_inff()) : float(d);
+                            if ((!(fabs(double(sc)) < 1e38) && !filt[r]) || !(d < 1e30)) sh.s_misc[7] = 1;
+                            const double lo = double(sc) - d;
+                            float lf = float(lo);
+                            if (double(lf) > lo) lf = nextafterf(lf, -__builtin_inff());
+                            lkey = make_key(lf, uint32_t(nb[r]));
+                        }
                         a.vro[pos] = rw[r];
                         sh.u.bfs.hval[slot[r]] = (uint32_t(h + 1) << 16) | uint32_t(pos);
                     }
-                    if (SCORED && rk > 0)
+                    if (MODE == kBfsScored && rk > 0)
                         wave_offer(best, bthr, won ? make_key(sc, uint32_t(nb[r])) : kEmptyKey, lane_id(), rk);
+                    if (MODE == kBfsInterval && rk > 0) wave_offer(best, bthr, lkey, lane_id(), rk);
                     out += wtot;
                     __syncthreads();
                 }
@@ -581,7 +609,7 @@ __global__ __launch_bounds__(kFinThreads) void k_finalize(FinalizeArgs a) {
     uint64_t best = (wave == 0 && lane < rk) ? list : kEmptyKey;
     uint64_t bthr = rk > 0 ? __shfl(best, rk - 1) : kEmptyKey;
     int levels = 0;
-    int V = (a.hops < int(kClaimHop)) ? bfs_lds<true>(sh, a, ns, &levels, best, bthr, rk) : -1;   // hop below the claim mark
+    int V = (a.hops < int(kClaimHop)) ? bfs_lds<kBfsScored>(sh, a, ns, &levels, best, bthr, rk) : -1;   // hop below the claim mark
     const bool in_lds = V >= 0;
     if (!in_lds) {
         __syncthreads();
@@ -656,7 +684,7 @@ __device__ int multi_bfs_query(FinShared& sh, const MultiArgs& m, int j, int* le
     const int ns = sh.s_misc[0];
     int levels = 0;
     uint64_t best = kEmptyKey, bthr = kEmptyKey;
-    const int V = (a.hops < int(kClaimHop)) ? bfs_lds<false>(sh, a, ns, &levels, best, bthr, 0) : -1;
+    const int V = (a.hops < int(kClaimHop)) ? bfs_lds<kBfsUnscored>(sh, a, ns, &levels, best, bthr, 0) : -1;
     if (tid == 0) {
         if (V < 0) {
             m.status[j] = kMultiOverflow;
@@ -756,6 +784,10 @@ __global__ __launch_bounds__(kFinThreads) void k_cert_bfs(CertArgs a, MultiArgs 
     __shared__ double s_eps;
     const int tid = int(threadIdx.x), lane = lane_id(), wave = tid >> 6;
     const int c = a.c;
+    auto stamp_at = [&](int i) {
+        if (tid == 0 && a.stamps) a.stamps[i] = __builtin_amdgcn_s_memrealtime();
+    };
+    stamp_at(0);
     // A. the c best candidate keys (the finalize kernel's merge, 8 loads in flight per lane)
     uint64_t list = kEmptyKey, thr = kEmptyKey;
     const int n_part = int(*a.gcnt);
@@ -771,6 +803,7 @@ __global__ __launch_bounds__(kFinThreads) void k_cert_bfs(CertArgs a, MultiArgs 
         for (int j = 0; j < 8; ++j) wave_offer(list, thr, x[j], lane, c);
     }
     list = tree_merge(sh, list, c, n_part <= kFinThreads ? (n_part + 63) / 64 : kFinWaves);
+    stamp_at(1);
     if (wave == 0) s_cand[lane] = list;
     if (wave == 1) {
         double sq = 0.0;
@@ -853,77 +886,59 @@ __global__ __launch_bounds__(kFinThreads) void k_cert_bfs(CertArgs a, MultiArgs 
             m.res[0] = h;
         }
     };
+    stamp_at(2);
     if (!sh.s_misc[6]) { fail(kMultiUncertified); return; }
-    int levels = 0, ns = 0;
-    const int V = multi_bfs_query(sh, m, 0, &levels, &ns);
-    if (V < 0) { fail(kMultiOverflow); return; }
+    // E. the certified seeds' BFS in interval mode: every node's BFS score from the fp16
+    // scan's fused scores (each within eps of the exact one) and a bound on its distance
+    // to the exact BFS score. At least rc nodes have exact scores >= the rc-th largest
+    // lower end, so a node whose upper end is below it cannot be a result; the others
+    // (with their BFS ancestors) are rescored exactly and propagated in the finalize
+    // kernel's arithmetic.
+    FinalizeArgs v = multi_view(m, 0);
+    v.fin = a.fin16;
+    v.vdv = m.vfin;                              // bounds; later the exact fused scores
+    v.eps = s_eps;
+    v.mod_filter = a.mod_filter;
+    const float dlt = m.hop_decay;               // in [0, 1] (checked by the caller)
+    const int rk = m.rcap;                       // <= 64 (checked by the caller)
+    uint64_t seedkey = kEmptyKey;
+    if (wave == 0) {
+        seedkey = lane < m.k ? a.seeds[lane] : kEmptyKey;
+        const int nsd = __popcll(__ballot(seedkey != kEmptyKey));
+        if (seedkey != kEmptyKey) {
+            const int32_t id = key_id(seedkey);
+            v.vlist[lane] = id;
+            v.vhop[lane] = 0;
+            v.vpar[lane] = -1;
+            v.vscore[lane] = key_score(seedkey);
+            v.vdv[lane] = 0.0f;
+            v.vro[lane] = v.ro[id];
+        }
+        if (lane == 0) { sh.s_misc[0] = nsd; sh.s_misc[7] = 0; }
+    }
     __threadfence_block();
     __syncthreads();
-    // E. the results from intervals: BFS scores computed from the fp16 scan's fused scores
-    // (each within eps of the exact one) lie within a propagated bound of the exact BFS
-    // scores; at least rc nodes have exact scores >= the rc-th largest lower end, so a
-    // node whose upper end is below it cannot be a result. The others (with their BFS
-    // ancestors) are rescored exactly and propagated in the finalize kernel's arithmetic.
-    const FinalizeArgs v = multi_view(m, 0);
-    const float dlt = m.hop_decay;               // in [0, 1] (checked by the caller)
-    const double eps = s_eps;
-    const double u = 0x1p-24;
-    // per position: approximate BFS score (vscore) and a bound on its distance to the
-    // exact one (dv): seeds are exact; a node's bound is the larger of its two terms'
-    //   parent term  |fl(x d) - fl(y d)| <= d |x - y| + u d (|x| + |y|)
-    //   own term     |0.8 f16 - 0.8 f32| + rounding, with |f16 - f32| <= eps (0 for a
-    //                filtered row: both scans give -FLT_MAX)
-    float* dv = reinterpret_cast<float*>(&sh.u.bfs.rstart[0]);      // later: exact scores
-    if (tid == 0) sh.s_misc[7] = 0;
-    for (int p = tid; p < ns; p += kFinThreads) dv[p] = 0.0f;
-    __syncthreads();
-    for (int h = 1; h <= levels; ++h) {
-        for (int p = ns + tid; p < V; p += kFinThreads) {
-            if (ld_coherent(v.vhop + p) != h) continue;
-            const int32_t id = ld_coherent(v.vlist + p);
-            const int par = ld_coherent(v.vpar + p);
-            const float f = a.fin16[id];
-            const float sp = ld_coherent(v.vscore + par);
-            const double dp = double(dv[par]);
-            const float sc = fmaxf(sp * dlt, f * 0.8f);
-            const double ea = dp > 0.0 ? double(dlt) * dp + 2.0 * u * double(dlt) * (fabs(double(sp)) + dp) : 0.0;
-            const bool filtered = a.mod_filter >= 0 && a.mods[id] != a.mod_filter;
-            const double eb = filtered ? 0.0 : 0.8 * eps + 0.8 * u * (2.0 * fabs(double(f)) + eps);
-            const double d = (ea > eb ? ea : eb) * (1.0 + 1e-6);
-            v.vscore[p] = sc;
-            dv[p] = float(d) < d ? nextafterf(float(d), __builtin_inff()) : float(d);
-            if (!(fabs(double(sc)) < 1e38) && !filtered) sh.s_misc[7] = 1;
-            if (!(d < 1e30)) sh.s_misc[7] = 1;
-        }
-        __threadfence_block();
-        __syncthreads();
-    }
+    const int ns = sh.s_misc[0];
+    int levels = 0;
+    uint64_t best = (wave == 0 && lane < rk) ? seedkey : kEmptyKey;   // seeds: exact lower ends
+    uint64_t bthr = __shfl(best, rk - 1);
+    const int V = (v.hops < int(kClaimHop)) ? bfs_lds<kBfsInterval>(sh, v, ns, &levels, best, bthr, rk) : -1;
+    if (V < 0) { fail(kMultiOverflow); return; }
     if (sh.s_misc[7]) { fail(kMultiUncertified); return; }
+    stamp_at(3);
     const int rc = min(m.rcap, V);
-    // the rc-th largest lower end (approximate score - bound, rounded down)
-    uint64_t best = kEmptyKey, bthr = kEmptyKey;
-    for (int p0 = wave * 64; p0 < V; p0 += kFinThreads) {
-        const int p = p0 + lane;
-        uint64_t key = kEmptyKey;
-        if (p < V) {
-            const double lo = double(ld_coherent(v.vscore + p)) - double(dv[p]);
-            float lf = float(lo);
-            if (double(lf) > lo) lf = nextafterf(lf, -__builtin_inff());
-            key = make_key(lf, uint32_t(ld_coherent(v.vlist + p)));
-        }
-        wave_offer(best, bthr, key, lane, rc);
-    }
-    best = tree_merge(sh, best, rc);
+    best = tree_merge(sh, best, rk);
     if (wave == 0 && lane == rc - 1) sh.s_misc[5] = int(__float_as_uint(key_score(best)));
     __syncthreads();
     const double cut = double(__uint_as_float(uint32_t(sh.s_misc[5])));
+    float* dv = reinterpret_cast<float*>(&sh.u.bfs.rstart[0]);      // exact BFS scores by position
     // mark the candidates and their ancestors (flags in the freed hash keys)
     uint32_t* flag = sh.u.bfs.hkey;
     int32_t* rlist = reinterpret_cast<int32_t*>(sh.u.bfs.hval);
     for (int p = tid; p < V; p += kFinThreads) flag[p] = 0u;
     __syncthreads();
     for (int p = tid; p < V; p += kFinThreads) {
-        if (double(ld_coherent(v.vscore + p)) + double(dv[p]) >= cut) {
+        if (double(ld_coherent(v.vscore + p)) + double(ld_coherent(v.vdv + p)) >= cut) {
             for (int x = p; x >= 0; x = ld_coherent(v.vpar + x)) flag[x] = 1u;
         }
     }
@@ -939,6 +954,7 @@ __global__ __launch_bounds__(kFinThreads) void k_cert_bfs(CertArgs a, MultiArgs 
         r += tot;
     }
     __syncthreads();
+    stamp_at(4);
     // exact fused scores of the marked nodes past the seeds (one per 16-lane group)
     {
         QF qf;
@@ -955,8 +971,8 @@ __global__ __launch_bounds__(kFinThreads) void k_cert_bfs(CertArgs a, MultiArgs 
     }
     __threadfence_block();
     __syncthreads();
-    // exact BFS scores over the marked set, level by level (parents are marked too);
-    // they replace the bounds in dv, which the marking above was the last to read
+    stamp_at(5);
+    // exact BFS scores over the marked set, level by level (parents are marked too)
     for (int h = 0; h <= levels; ++h) {
         for (int i = tid; i < r; i += kFinThreads) {
             const int p = rlist[i];
@@ -974,18 +990,24 @@ __global__ __launch_bounds__(kFinThreads) void k_cert_bfs(CertArgs a, MultiArgs 
         wave_offer(best, bthr, i < r ? make_key(dv[rlist[i]], uint32_t(ld_coherent(v.vlist + rlist[i]))) : kEmptyKey, lane, rc);
     }
     best = tree_merge(sh, best, rc);
-    if (wave == 0 && lane < rc) {
-        const int32_t id = key_id(best);
-        int32_t hop = 0;
-        for (int i = 0; i < r; ++i)
-            if (ld_coherent(v.vlist + rlist[i]) == id) hop = ld_coherent(v.vhop + rlist[i]);
-        write_result(v, lane, best, hop);
+    // each result's hop from the one marked position that holds its node
+    if (wave == 0) s_exact[lane] = best;
+    __syncthreads();
+    int32_t* s_hop = reinterpret_cast<int32_t*>(sh.lists[1]);        // free after the merge
+    for (int i = tid; i < r; i += kFinThreads) {
+        const int p = rlist[i];
+        const int32_t id = ld_coherent(v.vlist + p);
+        for (int j = 0; j < rc; ++j)
+            if (key_id(s_exact[j]) == id) s_hop[j] = ld_coherent(v.vhop + p);
     }
+    __syncthreads();
+    if (wave == 0 && lane < rc) write_result(v, lane, best, s_hop[lane]);
     if (tid == 0) {
         ResultHeader h;
         h.count = rc; h.visited = V; h.levels = levels; h.n_seeds = ns;
         m.res[0] = h;
     }
+    stamp_at(6);
 }
 
 __global__ __launch_bounds__(256) void k_episode(EpisodeArgs a) {
