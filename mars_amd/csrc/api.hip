@@ -29,8 +29,12 @@ namespace mars {
 namespace {
 thread_local char g_err[1024] = "";
 constexpr int32_t kMaxWg = 4096;     // upper bound of scan workgroups (partials buffer)
-constexpr int32_t kTargetWg = 2048;  // scan workgroups (grid-stride; 8 per CU on 256 CUs)
-constexpr int32_t kTargetWgF16 = 768;    // fp16 rows: 236 us vs 241 us at 1024, 249 us at 2048 (N=1M, D=768)
+// Scan workgroups (grid-stride), 2 per CU on 256 CUs. A count that is not a whole
+// multiple of the CU count loads the CUs unevenly (1M x 768 fp16 rows: 235 us at
+// 512, 246 us at 768, 270 us at 256, 255 us at 576; fp32 rows: 472 us at 512,
+// 510 us at 2048).
+constexpr int32_t kTargetWg = 512;
+constexpr int32_t kTargetWgF16 = 512;
 
 int ensure_device(int* dev) {
     int d = 0;

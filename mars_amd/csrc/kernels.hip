@@ -38,7 +38,12 @@ namespace {
 // step keep 2 x 4 rows of loads in flight per wave.
 constexpr int kScanUnroll = 2;
 
-template <typename T, typename QF>
+// SIDE = false: the query has no modality filter and no episode boost, so the
+// per-row modality and episode ids are not read (modality 0, episode -1 give
+// fuse_score's no-filter, no-boost result). The compiler also schedules that
+// variant better: 235 us against 245 us for the fp16 scan of 1M x 768 rows at 512
+// workgroups on MI355X.
+template <typename T, typename QF, bool SIDE>
 __global__ __launch_bounds__(256) void k_scan(ScanArgs a) {
     __shared__ uint64_t s_lists[4][64];
     const int lane = lane_id(), wave = int(threadIdx.x >> 6);
@@ -48,7 +53,7 @@ __global__ __launch_bounds__(256) void k_scan(ScanArgs a) {
     if constexpr (std::is_same_v<QF, QGeneric>) qf.d = a.d;
     qf.load(a.q, sub);
     const T* emb = static_cast<const T*>(a.emb);
-    const bool use_boost = a.boost > 0.0f && a.ep_ids != nullptr;
+    const bool use_boost = SIDE && a.boost > 0.0f && a.ep_ids != nullptr;
     uint64_t list = kEmptyKey, thr = kEmptyKey;
     const int64_t ngroups = (a.n + 3) / 4;
     const int64_t gstride = int64_t(gridDim.x) * 4 * kScanUnroll;
@@ -60,7 +65,7 @@ __global__ __launch_bounds__(256) void k_scan(ScanArgs a) {
             int64_t rr = (g0 + u) * 4 + grp;
             rr = rr < a.n ? rr : a.n - 1;
             ts[u] = a.ts[rr];
-            mod[u] = (a.mod_filter >= 0) ? a.mods[rr] : 0;
+            mod[u] = (SIDE && a.mod_filter >= 0) ? a.mods[rr] : 0;
             ep[u] = use_boost ? a.ep_ids[rr] : -1;
             dot[u] = qf.dot(emb + rr * a.d, sub);
         }
@@ -1143,7 +1148,9 @@ __global__ __launch_bounds__(256) void k_tile_merge(uint64_t* __restrict__ part,
 template <typename T, typename QF>
 KernelLaunch scan_launch_t(const ScanArgs& a) {
     KernelLaunch l;
-    l.fn = reinterpret_cast<const void*>(&k_scan<T, QF>);
+    const bool side = a.mod_filter >= 0 || (a.boost > 0.0f && a.ep_ids != nullptr);
+    l.fn = side ? reinterpret_cast<const void*>(&k_scan<T, QF, true>)
+                : reinterpret_cast<const void*>(&k_scan<T, QF, false>);
     l.grid = dim3(unsigned(a.num_wg));
     l.block = dim3(256);
     return l;

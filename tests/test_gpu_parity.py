@@ -412,7 +412,9 @@ def test_gpu_knn_matches_cpu_exact():
 # ---------------------------------------------------------------- replayed query graphs
 def test_graph_replay_matches_eager(dev10k, corpus_10k):
     """Replays of the query graph (arguments rewritten per query) interleaved with
-    eager queries: every replay returns exactly the eager result."""
+    eager queries: every replay returns exactly the eager result. A filtered,
+    boosted global query between plain ones switches the scan kernel variant, so the
+    graph is rebuilt rather than replayed with the wrong kernel."""
     qs = corpus.pick_queries(corpus_10k.modalities, 24, seed=606)
     off = dev10k.csr.ep_csr_offsets
     try:
@@ -421,6 +423,9 @@ def test_graph_replay_matches_eager(dev10k, corpus_10k):
             for i, node in enumerate(qs):
                 ep = int(corpus_10k.episode_ids[node])
                 cfgs = [RetrievalConfig(top_k=10, time_decay_lambda=LAM, max_results_returned=15),
+                        RetrievalConfig(top_k=10, time_decay_lambda=LAM, max_results_returned=15,
+                                        modality_filter=int(corpus_10k.modalities[node]), query_episode_id=ep,
+                                        episode_same_boost=0.5),
                         RetrievalConfig(top_k=10, time_decay_lambda=LAM, max_results_returned=15,
                                         retrieval_scope=RetrievalScope.EpisodeScoped, query_episode_id=ep,
                                         query_episode_member_begin=int(off[ep]),
