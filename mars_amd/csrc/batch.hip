@@ -75,8 +75,6 @@ __global__ __launch_bounds__(kBWaves * 64) void k_batch_scan(BatchArgs a) {
     __shared__ __attribute__((aligned(16))) unsigned char s_raw[BatchLds<KCH, K>::kBytes];
     u32x4 (*s_q)[KCH][64] = reinterpret_cast<u32x4 (*)[KCH][64]>(s_raw);
     __shared__ float s_stage[kBWaves][kTile][kBQ + 1];  // per-wave score tile (+1: bank spread)
-    __shared__ __attribute__((aligned(16))) float s_w[kBWaves][kTile];      // row decay weight (one query time) or row timestamp
-    __shared__ __attribute__((aligned(16))) int32_t s_keep[kBWaves][kTile]; // row passes the modality filter
     // Best known K-th score per query in this workgroup: a wave whose own list is full
     // publishes its K-th score here; a row scoring strictly below it cannot enter the
     // workgroup's top-K (K better rows are already held), so no wave keeps it.
@@ -125,27 +123,34 @@ __global__ __launch_bounds__(kBWaves * 64) void k_batch_scan(BatchArgs a) {
 #pragma unroll
         for (int ks = 0; ks < H; ++ks) b[ks] = bp[ks * 4];
     };
-    // A tile's side values (timestamp, modality) are loaded right before its rows, one
-    // tile ahead, so waiting for them never waits for younger row loads.
+    // Half 0 of a tile and its side values (timestamp, modality) load one half-tile
+    // ahead; the side values are loaded first, so waiting for them never waits for
+    // younger row loads. The kernel stays near 160 VGPRs, which leaves room on every
+    // CU for the small kernels of other streams (episode queries, inserts).
     u32x4 b0[H], b1[H];
     float side_ts = 0.0f;
     int32_t side_mod = 0;
-    auto load_tile = [&](int64_t t) {
+    auto load_head = [&](int64_t t) {
         if (lane < kTile) {
             const int64_t rl = (t + lane < r1) ? t + lane : r1 - 1;
             side_ts = a.ts[rl];
             side_mod = (a.mod_filter >= 0) ? a.mods[rl] : 0;
         }
         load_half(b0, t, 0);
-        load_half(b1, t, 1);
     };
     int64_t t0 = r0 + int64_t(wave) * kTile;
-    if (t0 < r1) load_tile(t0);
+    if (t0 < r1) load_head(t0);
     for (; t0 < r1; t0 += step) {
+        load_half(b1, t0, 1);
+        // lane j < 16: row j's weight (decay at the one query time, else its timestamp)
+        // and filter flag, taken before the next tile's loads reuse the side registers
+        float row_w = 0.0f;
+        bool row_keep = true;
         if (lane < kTile) {
-            s_keep[wave][lane] = (a.mod_filter < 0 || side_mod == a.mod_filter) ? 1 : 0;
-            s_w[wave][lane] = !uni ? side_ts : (a.lambda != 0.0f ? expf(-a.lambda * fmaxf(0.0f, tq0 - side_ts)) : 1.0f);
+            row_keep = a.mod_filter < 0 || side_mod == a.mod_filter;
+            row_w = !uni ? side_ts : (a.lambda != 0.0f ? expf(-a.lambda * fmaxf(0.0f, tq0 - side_ts)) : 1.0f);
         }
+        const uint64_t keepm = __ballot(row_keep);
         f32x4 acc[4];
 #pragma unroll
         for (int qt = 0; qt < 4; ++qt) acc[qt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -158,6 +163,7 @@ __global__ __launch_bounds__(kBWaves * 64) void k_batch_scan(BatchArgs a) {
                 acc[qt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf, acc[qt], 0, 0, 0);
             }
         }
+        if (t0 + step < r1) load_head(t0 + step);
 #pragma unroll
         for (int ks = 0; ks < H; ++ks) {
             const f16x8 bf = __builtin_bit_cast(f16x8, b1[ks]);
@@ -167,13 +173,15 @@ __global__ __launch_bounds__(kBWaves * 64) void k_batch_scan(BatchArgs a) {
                 acc[qt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf, acc[qt], 0, 0, 0);
             }
         }
-        // the next tile loads while this tile's scores are selected
-        if (t0 + step < r1) load_tile(t0 + step);
         // C[query = qt*16 + 4*kg + i][row = m]
 #pragma unroll
         for (int qt = 0; qt < 4; ++qt)
 #pragma unroll
             for (int i = 0; i < 4; ++i) s_stage[wave][m][qt * 16 + 4 * kg + i] = acc[qt][i];
+        // the row weights as wave-uniform values (read in uniform control flow)
+        float w[kTile];
+#pragma unroll
+        for (int j = 0; j < kTile; ++j) w[j] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(row_w), j));
         wave_lds_sync();
         if (qvalid) {
             uint32_t bound = own > s_thr[lane] ? own : s_thr[lane];
@@ -185,16 +193,12 @@ __global__ __launch_bounds__(kBWaves * 64) void k_batch_scan(BatchArgs a) {
 #pragma unroll
             for (int j = 0; j < kTile; ++j) sc[j] = s_stage[wave][j][lane];
             if (!plain) {
-                float w[kTile];
-                int32_t keep[kTile];
-#pragma unroll
-                for (int j = 0; j < kTile; ++j) { w[j] = s_w[wave][j]; keep[j] = s_keep[wave][j]; }
 #pragma unroll
                 for (int j = 0; j < kTile; ++j) {
-                    float s = sc[j];
-                    if (uni) s = s * w[j];
-                    else if (a.lambda != 0.0f) s = s * expf(-a.lambda * fmaxf(0.0f, tq - w[j]));
-                    sc[j] = keep[j] ? s : -FLT_MAX;
+                    float sv = sc[j];
+                    if (uni) sv = sv * w[j];
+                    else if (a.lambda != 0.0f) sv = sv * expf(-a.lambda * fmaxf(0.0f, tq - w[j]));
+                    sc[j] = ((keepm >> j) & 1u) ? sv : -FLT_MAX;
                 }
             }
             uint32_t top = 0u;
@@ -205,9 +209,9 @@ __global__ __launch_bounds__(kBWaves * 64) void k_batch_scan(BatchArgs a) {
             }
             if (top >= bound)
             for (int j = 0; j < nr; ++j) {
-                const float s = sc[j];
-                if (ord32(s) >= bound && t0 + j != self_id) {
-                    const uint64_t key = make_key(s, uint32_t(t0 + j));
+                const float sv = sc[j];
+                if (ord32(sv) >= bound && t0 + j != self_id) {
+                    const uint64_t key = make_key(sv, uint32_t(t0 + j));
                     if (key < list[K - 1]) {
                         reg_insert<K>(list, key);
                         if (list[K - 1] != kEmptyKey) {

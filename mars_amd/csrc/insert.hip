@@ -75,6 +75,7 @@ struct StageArgs {
 };
 
 __global__ __launch_bounds__(256) void k_stage_insert(StageArgs a) {
+    __builtin_amdgcn_s_setprio(3);     // publication is latency-bound: first issue on a shared CU
     const int64_t tid = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
     const int64_t stride = int64_t(gridDim.x) * blockDim.x;
     const int lane = int(threadIdx.x & 63u);
@@ -109,6 +110,7 @@ __global__ __launch_bounds__(256) void k_stage_insert(StageArgs a) {
 }
 
 __global__ void k_patch_data(PatchArgs a) {
+    __builtin_amdgcn_s_setprio(3);     // publication is latency-bound: first issue on a shared CU
     const int64_t tid = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
     const int64_t stride = int64_t(gridDim.x) * blockDim.x;
     // relocations: one 64-lane wave per row (rows are short)
@@ -126,6 +128,7 @@ __global__ void k_patch_data(PatchArgs a) {
 }
 
 __global__ void k_patch_rows(PatchArgs a) {
+    __builtin_amdgcn_s_setprio(3);     // publication is latency-bound: first issue on a shared CU
     const int64_t tid = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
     const int64_t stride = int64_t(gridDim.x) * blockDim.x;
     for (int64_t i = tid; i < a.n_rows; i += stride) {

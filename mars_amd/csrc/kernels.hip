@@ -1016,6 +1016,8 @@ __global__ __launch_bounds__(kFinThreads) void k_cert_bfs(CertArgs a, MultiArgs 
 }
 
 __global__ __launch_bounds__(256) void k_episode(EpisodeArgs a) {
+    // latency-bound and short: its waves go first when they share a CU with a scan
+    __builtin_amdgcn_s_setprio(3);
     __shared__ uint64_t s_lists[4][64];
     __shared__ int32_t s_ids[64];
     __shared__ uint64_t s_out[64];
