@@ -395,7 +395,9 @@ def main() -> int:
     if not args.profile_only and args.tiled_queries > 0:
         out["tiled_comparator"] = tiled_pass(args, mars_amd, corpus, c, qnodes[W:], N, D, K, pctl, lat_g,
                                              "pinned" if host_rows else "pageable")
-    if args.stream_queries > 0 and args.serve_modes and not args.profile_only:
+    # the streaming workload needs nodes to insert (--stream-nodes 0 measures the resident
+    # corpus only)
+    if args.stream_queries > 0 and args.serve_modes and not args.profile_only and M > 0:
         modes = [m for m in args.serve_modes.split(",") if m]
         runs, first = [], N
         per = M // len(modes) // 10 * 10                  # whole 10-node episodes per run

@@ -165,6 +165,7 @@ int ctx_free(Ctx& c) {
     multi_free(c);
     if (c.h_query) (void)hipHostFree(c.h_query);
     if (c.h_res) (void)hipHostFree(c.h_res);
+    if (c.h_done) (void)hipHostFree(c.h_done);
     for (auto& e : c.ev) if (e) (void)hipEventDestroy(e);
     graph_slot_free(c.g_global);
     graph_slot_free(c.g_episode);
@@ -211,6 +212,31 @@ int graph_launch(Ctx::GraphSlot& g, int n, const KernelLaunch* l, void* const* a
 
 int ensure_multi_scratch(Ctx& c, int32_t q, int32_t rcap);
 
+// Next sequence number of a Q=1 query (never 0, the word's initial value).
+uint32_t next_seq(Ctx& c) {
+    if (++c.seq == 0u) c.seq = 1u;
+    return c.seq;
+}
+
+// Waits for the Q=1 query whose last kernel stores seq into the completion word after
+// its results. The host spins on the word; every 50 us it also asks the stream, so a
+// failed launch or a fault is reported, and a stream that finished without storing the
+// word ends the wait as well (the results are then complete).
+int wait_done(const Ctx& c, uint32_t seq, hipStream_t s) {
+    using clk = std::chrono::steady_clock;
+    auto next = clk::now() + std::chrono::microseconds(50);
+    while (__atomic_load_n(c.h_done, __ATOMIC_ACQUIRE) != seq) {
+        __builtin_ia32_pause();
+        const auto now = clk::now();
+        if (now < next) continue;
+        const hipError_t e = hipStreamQuery(s);
+        if (e == hipSuccess) break;
+        if (e != hipErrorNotReady) return set_error(MARS_ERR_HIP, "query stream: %s", hipGetErrorString(e));
+        next = now + std::chrono::microseconds(50);
+    }
+    return MARS_OK;
+}
+
 // Certified global query (MARS_CTX_CERTIFIED): fp16 scan keeping c candidates, exact
 // rescoring + certificate, then the unscored BFS, exact visit scores and the results
 // (the batched path's kernels with q = 1). *answered = false when the certificate or
@@ -241,6 +267,11 @@ int certified_query(const Graph& g, Ctx& c, const float* q, float t_q, const mar
     // one workgroup finishes the query when the interval argument applies
     const float dlt = cfg->bfs_score_decay;
     ca.finish = (rcap <= 64 && dlt >= 0.0f && dlt <= 1.0f) ? 1 : 0;
+    // the last kernel (k_cert_bfs, else k_multi_select) stores the completion word
+    const uint32_t seq = next_seq(c);
+    uint32_t* const done = timing ? nullptr : c.d_done;
+    ca.done = ca.finish ? done : nullptr;
+    ca.seq = seq;
     MultiArgs m{};
     m.ro = g.ro; m.col = g.col; m.mods = g.mods; m.n_live = n_live; m.hops = hops;
     m.hop_decay = cfg->bfs_score_decay; m.k = K; m.rcap = rcap; m.q = 1; m.seeds = c.mseed; m.seed_stride = 64;
@@ -248,6 +279,8 @@ int certified_query(const Graph& g, Ctx& c, const float* q, float t_q, const mar
     m.vro = c.mvro; m.vfin = c.mvfin; m.vscore = c.mvscore;
     m.res = static_cast<ResultHeader*>(c.d_mres);
     m.rec = reinterpret_cast<mars_query_result*>(m.res + 1);
+    m.done = ca.finish ? nullptr : done;
+    m.seq = seq;
     if (launch_cert_bfs(ca, m, s) != MARS_OK) {
         // the scan appended candidates: clear them for the next query
         (void)hipMemsetAsync(c.gcnt, 0, sizeof(uint32_t), s);
@@ -264,8 +297,12 @@ int certified_query(const Graph& g, Ctx& c, const float* q, float t_q, const mar
         MARS_TRY(launch_visit_scores(va, s));
         MARS_TRY(launch_multi_select(m, s));
     }
-    if (timing) MARS_HIP(hipEventRecord(c.ev[2], s));
-    MARS_HIP(hipStreamSynchronize(s));
+    if (timing) {
+        MARS_HIP(hipEventRecord(c.ev[2], s));
+        MARS_HIP(hipStreamSynchronize(s));
+    } else {
+        MARS_TRY(wait_done(c, seq, s));
+    }
     const auto* hdr = static_cast<const ResultHeader*>(c.h_mres);
     const ResultHeader h = hdr[0];
     if (h.count < 0) return MARS_OK;
@@ -350,6 +387,10 @@ int query_impl(const mars_graph* gh, mars_ctx* ch, const float* h_q, const float
         }
     }
     if (timing) MARS_HIP(hipEventRecord(c.ev[0], s));
+    // the last kernel stores the completion word (timing keeps the stream sync: its
+    // events must have completed)
+    const uint32_t seq = next_seq(c);
+    uint32_t* const done = timing ? nullptr : c.d_done;
     if (scoped) {
         EpisodeArgs a{};
         a.emb = g.emb; a.d = g.d; a.n = n_live; a.q = q; a.ts = g.ts; a.mods = g.mods;
@@ -358,6 +399,7 @@ int query_impl(const mars_graph* gh, mars_ctx* ch, const float* h_q, const float
         a.t_q = t_q; a.lambda = cfg->time_decay_lambda; a.mod_filter = cfg->modality_filter;
         a.k = K; a.rcap = rcap; a.keybuf = c.sortbuf;
         a.seed_idx = c.seed_idx; a.seed_val = c.seed_val; a.res = c.d_res; a.rec = c.d_rec;
+        a.done = done; a.seq = seq;
         if (use_graph) {
             const KernelLaunch l = episode_launch();
             void* args[1] = {&a};
@@ -397,6 +439,7 @@ int query_impl(const mars_graph* gh, mars_ctx* ch, const float* h_q, const float
         f.vscore = c.vscore; f.vro = c.vro; f.sortbuf = c.sortbuf; f.cap_visit = c.max_nodes; f.rcap = rcap;
         f.seed_idx = c.seed_idx; f.seed_val = c.seed_val; f.res = c.d_res; f.rec = c.d_rec;
         f.stamps = c.stamps;
+        f.done = done; f.seq = seq;
         if (use_graph) {
             // one replayed graph for both kernels (the per-stage split is not timed)
             const KernelLaunch l[2] = {scan_launch(a), finalize_launch()};
@@ -417,8 +460,12 @@ int query_impl(const mars_graph* gh, mars_ctx* ch, const float* h_q, const float
         c.last_n = n_live;
         c.last_certified = 0;
     }
-    if (timing) MARS_HIP(hipEventRecord(c.ev[2], s));
-    MARS_HIP(hipStreamSynchronize(s));
+    if (timing) {
+        MARS_HIP(hipEventRecord(c.ev[2], s));
+        MARS_HIP(hipStreamSynchronize(s));
+    } else {
+        MARS_TRY(wait_done(c, seq, s));
+    }
     const ResultHeader h = *c.h_res;
     const int32_t nw = std::min(h.count, cap);
     if (nw > 0) std::memcpy(out, c.h_rec, size_t(nw) * sizeof(mars_query_result));
@@ -788,6 +835,12 @@ int mars_ctx_create(int32_t max_nodes, int32_t dim, int32_t max_k, uint32_t flag
     c.h_rec = reinterpret_cast<mars_query_result*>(c.h_res + 1);
     c.d_res = static_cast<ResultHeader*>(dres);
     c.d_rec = reinterpret_cast<mars_query_result*>(c.d_res + 1);
+    void* ddone = nullptr;
+    e = hipHostMalloc(reinterpret_cast<void**>(&c.h_done), 64, hipHostMallocMapped);
+    if (e == hipSuccess) e = hipHostGetDevicePointer(&ddone, c.h_done, 0);
+    if (e != hipSuccess) return fail(set_error(MARS_ERR_NOMEM, "context setup: %s", hipGetErrorString(e)));
+    *c.h_done = 0u;
+    c.d_done = static_cast<uint32_t*>(ddone);
     for (auto& ev : c.ev) {
         e = hipEventCreate(&ev);
         if (e != hipSuccess) return fail(set_error(MARS_ERR_HIP, "event: %s", hipGetErrorString(e)));
@@ -1432,6 +1485,7 @@ int mars_ctx_last_scores(mars_ctx* ch, float* h, int64_t n) {
     MARS_CHECK(n <= c.last_n && n >= 0, MARS_ERR_INVALID, "asked %lld scores, last global query had %d",
                (long long)n, c.last_n);
     MARS_TRY(use_device(c.device));
+    MARS_HIP(hipStreamSynchronize(c.stream));
     MARS_HIP(hipMemcpy(h, c.fin, size_t(n) * sizeof(float), hipMemcpyDeviceToHost));
     return MARS_OK;
 }
@@ -1440,6 +1494,7 @@ int mars_ctx_last_seeds(mars_ctx* ch, int32_t* idx, float* val, int32_t k, int32
     MARS_CHECK(ch && idx && val && k_out, MARS_ERR_INVALID, "null argument");
     Ctx& c = ch->c;
     MARS_TRY(use_device(c.device));
+    MARS_HIP(hipStreamSynchronize(c.stream));
     const int32_t n = std::min(k, c.last_k);
     if (n > 0) {
         MARS_HIP(hipMemcpy(idx, c.seed_idx, size_t(n) * sizeof(int32_t), hipMemcpyDeviceToHost));
@@ -1452,6 +1507,7 @@ int mars_ctx_last_seeds(mars_ctx* ch, int32_t* idx, float* val, int32_t k, int32
 int mars_ctx_last_phases(mars_ctx* ch, double* us, int32_t n) {
     MARS_CHECK(ch && us && n >= 0 && n <= 6, MARS_ERR_INVALID, "bad arguments");
     MARS_TRY(use_device(ch->c.device));
+    MARS_HIP(hipStreamSynchronize(ch->c.stream));
     uint64_t t[12] = {};
     MARS_HIP(hipMemcpy(t, ch->c.stamps, sizeof(t), hipMemcpyDeviceToHost));
     const uint64_t* p = ch->c.last_certified ? t + 4 : t;     // certified: 7 stamps from t[4]
@@ -1464,6 +1520,7 @@ int mars_ctx_last_visited(mars_ctx* ch, int32_t* ids, int32_t* hops, float* scor
     MARS_CHECK(ch && n_out && cap >= 0, MARS_ERR_INVALID, "null argument");
     Ctx& c = ch->c;
     MARS_TRY(use_device(c.device));
+    MARS_HIP(hipStreamSynchronize(c.stream));
     const int32_t n = std::min(cap, c.last_visited);
     if (n > 0) {
         if (ids) MARS_HIP(hipMemcpy(ids, c.vlist, size_t(n) * sizeof(int32_t), hipMemcpyDeviceToHost));

@@ -238,6 +238,16 @@ __device__ inline float fuse_score(float dot, float ts, int32_t mod, int32_t ep,
 }
 
 
+// Completion word of a Q=1 query (host-mapped): every thread's result writes are made
+// visible system-wide, then one thread stores seq. Called by all threads of the
+// workgroup that writes the query's last results, as its last action.
+__device__ inline void signal_done(uint32_t* done, uint32_t seq) {
+    if (done == nullptr) return;               // uniform
+    __threadfence_system();
+    __syncthreads();
+    if (threadIdx.x == 0) __hip_atomic_store(done, seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
 // ---- row-norm bounds of the fp16 copy (batched global certificate) -------------------
 constexpr float kHalfMinNormal = 6.103515625e-05f;   // 2^-14
 

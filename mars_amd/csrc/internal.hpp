@@ -201,6 +201,13 @@ struct Ctx {
     mars_query_result* h_rec = nullptr;
     ResultHeader* d_res = nullptr; // device alias of h_res
     mars_query_result* d_rec = nullptr;
+    // Completion word (pinned, mapped): the last kernel of a Q=1 query writes the
+    // query's sequence number into it after a system-scope fence on its result
+    // writes; the host spins on it instead of a stream synchronize (about 5 us less
+    // per query, and a tighter tail).
+    uint32_t* h_done = nullptr;
+    uint32_t* d_done = nullptr;
+    uint32_t seq = 0;
     int32_t res_cap = 0;
     uint32_t epoch = 0;            // last visit stamp used
     uint32_t gen = 0;              // next BFS claim generation
@@ -334,6 +341,8 @@ struct FinalizeArgs {
     ResultHeader* res;
     mars_query_result* rec;
     uint64_t* stamps;        // 4 realtime stamps (start, seeds, BFS done, end) or null
+    uint32_t* done;          // host-mapped completion word: seq after the results, or null
+    uint32_t seq;
 };
 int launch_finalize(const FinalizeArgs& a, hipStream_t s);
 // Tiled query: fold the candidate keys the scan of one tile appended (part[0..*gcnt))
@@ -359,6 +368,8 @@ struct EpisodeArgs {
     float* seed_val;
     ResultHeader* res;
     mars_query_result* rec;
+    uint32_t* done;          // host-mapped completion word: seq after the results, or null
+    uint32_t seq;
 };
 int launch_episode(const EpisodeArgs& a, hipStream_t s);
 
@@ -452,6 +463,8 @@ struct MultiArgs {
     float* vscore;
     ResultHeader* res;       // [q] (host-mapped)
     mars_query_result* rec;  // [q][rcap] (host-mapped)
+    uint32_t* done;          // q = 1: host-mapped completion word (k_multi_select), or null
+    uint32_t seq;
 };
 struct VisitScoreArgs {
     const void* emb;
@@ -500,6 +513,8 @@ struct CertArgs {
     int32_t* status;
     float* margin;
     uint64_t* stamps;        // 7 realtime stamps of the phases, or null
+    uint32_t* done;          // finish = 1: host-mapped completion word, or null
+    uint32_t seq;
 };
 int launch_cert_bfs(const CertArgs& a, const struct MultiArgs& m, hipStream_t s);   // + BFS of query 0 of m
 int launch_multi_bfs(const MultiArgs& a, hipStream_t s);

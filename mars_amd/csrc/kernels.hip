@@ -648,6 +648,7 @@ __global__ __launch_bounds__(kFinThreads) void k_finalize(FinalizeArgs a) {
         *a.gthr = kEmptyKey;
     }
     stamp(a, 3);
+    signal_done(a.done, a.seq);
 }
 
 // ---- episode-scoped query ------------------------------------------------------------
@@ -725,6 +726,7 @@ __global__ __launch_bounds__(kFinThreads) void k_multi_select(MultiArgs m) {
             h.count = -1; h.visited = st; h.levels = 0; h.n_seeds = 0;
             m.res[j] = h;
         }
+        signal_done(m.done, m.seq);
         return;
     }
     const FinalizeArgs a = multi_view(m, j);
@@ -770,6 +772,7 @@ __global__ __launch_bounds__(kFinThreads) void k_multi_select(MultiArgs m) {
         h.count = rc; h.visited = V; h.levels = levels; h.n_seeds = ns;
         m.res[j] = h;
     }
+    signal_done(m.done, m.seq);
 }
 
 // ---- certified Q=1 global query ---------------------------------------------------------
@@ -890,6 +893,7 @@ __global__ __launch_bounds__(kFinThreads) void k_cert_bfs(CertArgs a, MultiArgs 
             h.count = -1; h.visited = code; h.levels = 0; h.n_seeds = 0;
             m.res[0] = h;
         }
+        signal_done(a.done, a.seq);
     };
     stamp_at(2);
     if (!sh.s_misc[6]) { fail(kMultiUncertified); return; }
@@ -1013,6 +1017,7 @@ __global__ __launch_bounds__(kFinThreads) void k_cert_bfs(CertArgs a, MultiArgs 
         m.res[0] = h;
     }
     stamp_at(6);
+    signal_done(a.done, a.seq);
 }
 
 __global__ __launch_bounds__(256) void k_episode(EpisodeArgs a) {
@@ -1108,6 +1113,7 @@ __global__ __launch_bounds__(256) void k_episode(EpisodeArgs a) {
         h.n_seeds = kk;
         *a.res = h;
     }
+    signal_done(a.done, a.seq);
 }
 
 __global__ void k_convert_f16(const float* __restrict__ in, __half* __restrict__ out, int64_t count) {
