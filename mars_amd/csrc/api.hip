@@ -401,7 +401,7 @@ int query_impl(const mars_graph* gh, mars_ctx* ch, const float* h_q, const float
         a.seed_idx = c.seed_idx; a.seed_val = c.seed_val; a.res = c.d_res; a.rec = c.d_rec;
         a.done = done; a.seq = seq;
         if (use_graph) {
-            const KernelLaunch l = episode_launch();
+            const KernelLaunch l = episode_launch(g.d);
             void* args[1] = {&a};
             MARS_TRY(graph_launch(c.g_episode, 1, &l, args, s));
         } else {

@@ -160,11 +160,12 @@ struct QF32 {
             v[c][0] = x.x; v[c][1] = x.y; v[c][2] = x.z; v[c][3] = x.w;
         }
     }
-    __device__ float dot(const float* row, int sub) const {
+    __device__ void fetch(const float* row, int sub, f32x4 (&x)[NCH]) const {
         const f32x4* r = reinterpret_cast<const f32x4*>(row) + sub;
-        f32x4 x[NCH];
 #pragma unroll
         for (int c = 0; c < NCH; ++c) x[c] = __builtin_nontemporal_load(r + c * 16);
+    }
+    __device__ float dot_fetched(const f32x4 (&x)[NCH]) const {
         float acc = 0.0f;
 #pragma unroll
         for (int c = 0; c < NCH; ++c) {
@@ -174,6 +175,11 @@ struct QF32 {
             acc = fmaf(x[c].w, v[c][3], acc);
         }
         return acc;
+    }
+    __device__ float dot(const float* row, int sub) const {
+        f32x4 x[NCH];
+        fetch(row, sub, x);
+        return dot_fetched(x);
     }
 };
 

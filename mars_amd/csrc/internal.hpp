@@ -306,7 +306,7 @@ struct KernelLaunch {
 int launch_scan(const ScanArgs& a, hipStream_t s);
 KernelLaunch scan_launch(const ScanArgs& a);
 KernelLaunch finalize_launch();
-KernelLaunch episode_launch();
+KernelLaunch episode_launch(int32_t d);
 void scan_grid(int64_t n, int32_t max_wg, int32_t* rows_per_wg, int32_t* num_wg);
 
 struct FinalizeArgs {

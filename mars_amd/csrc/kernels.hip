@@ -1020,6 +1020,10 @@ __global__ __launch_bounds__(kFinThreads) void k_cert_bfs(CertArgs a, MultiArgs 
     signal_done(a.done, a.seq);
 }
 
+// NCH > 0 (d = 64 NCH): the query is held in registers in the Q=1 scan's fragment
+// layout and a member row's NCH 16-byte loads are all issued before its first FMA (the
+// same floats in the same fmaf order as the loop below, so the same scores).
+template <int NCH>
 __global__ __launch_bounds__(256) void k_episode(EpisodeArgs a) {
     // latency-bound and short: its waves go first when they share a CU with a scan
     __builtin_amdgcn_s_setprio(3);
@@ -1031,13 +1035,20 @@ __global__ __launch_bounds__(256) void k_episode(EpisodeArgs a) {
     const int sub = lane & 15, grp = lane >> 4;
     const int k = a.k;
     uint64_t list = kEmptyKey, thr = kEmptyKey;
+    QF32<(NCH > 0 ? NCH : 1)> qf;
+    if constexpr (NCH > 0) qf.load(a.q, sub);
     for (int base = 4 * wave; base < a.m; base += 16) {
         const int j = base + grp;
         const bool valid = j < a.m;
         const int32_t node = a.members[valid ? j : a.m - 1];
         float acc = 0.0f;
         const float* row = a.emb + int64_t(node) * a.d;
-        if ((a.d & 3) == 0) {
+        if constexpr (NCH > 0) {
+            f32x4 x[NCH];
+            qf.fetch(row, sub, x);
+            __builtin_amdgcn_sched_barrier(0);     // every load of the row before any FMA
+            acc = qf.dot_fetched(x);
+        } else if ((a.d & 3) == 0) {
             const float4* r4 = reinterpret_cast<const float4*>(row);
             const float4* q4 = reinterpret_cast<const float4*>(a.q);
             for (int i = sub; i < (a.d >> 2); i += 16) {
@@ -1210,9 +1221,19 @@ KernelLaunch finalize_launch() {
     return l;
 }
 
-KernelLaunch episode_launch() {
+KernelLaunch episode_launch(int32_t d) {
     KernelLaunch l;
-    l.fn = reinterpret_cast<const void*>(&k_episode);
+    l.fn = reinterpret_cast<const void*>(&k_episode<0>);
+    if (d % 64 == 0) {
+        switch (d / 64) {
+            case 4: l.fn = reinterpret_cast<const void*>(&k_episode<4>); break;
+            case 6: l.fn = reinterpret_cast<const void*>(&k_episode<6>); break;
+            case 8: l.fn = reinterpret_cast<const void*>(&k_episode<8>); break;
+            case 12: l.fn = reinterpret_cast<const void*>(&k_episode<12>); break;
+            case 16: l.fn = reinterpret_cast<const void*>(&k_episode<16>); break;
+            default: break;
+        }
+    }
     l.grid = dim3(1);
     l.block = dim3(256);
     return l;
@@ -1260,7 +1281,9 @@ int launch_multi_select(const MultiArgs& a, hipStream_t s) {
 }
 
 int launch_episode(const EpisodeArgs& a, hipStream_t s) {
-    MARS_LAUNCH(k_episode, dim3(1), dim3(256), 0, s, a);
+    const KernelLaunch l = episode_launch(a.d);
+    void* args[] = {const_cast<EpisodeArgs*>(&a)};
+    MARS_HIP(hipLaunchKernel(l.fn, l.grid, l.block, args, 0, s));
     return MARS_OK;
 }
 
