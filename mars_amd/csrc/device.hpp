@@ -181,6 +181,14 @@ struct QF32 {
         fetch(row, sub, x);
         return dot_fetched(x);
     }
+    // dot with every load of the row issued before the first FMA (latency-bound callers
+    // that score one row per group; the arithmetic is dot's)
+    __device__ float dot_all(const float* row, int sub) const {
+        f32x4 x[NCH];
+        fetch(row, sub, x);
+        __builtin_amdgcn_sched_barrier(0);
+        return dot_fetched(x);
+    }
 };
 
 // fp16 rows: chunk c covers halves [128c, 128c+128); lane s holds 8 of them.
@@ -198,6 +206,17 @@ struct QF16 {
         u32x4 x[NCH];
 #pragma unroll
         for (int c = 0; c < NCH; ++c) x[c] = __builtin_nontemporal_load(r + c * 16);
+        return dot_fetched(x);
+    }
+    __device__ float dot_all(const __half* row, int sub) const {
+        const u32x4* r = reinterpret_cast<const u32x4*>(row) + sub;
+        u32x4 x[NCH];
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) x[c] = __builtin_nontemporal_load(r + c * 16);
+        __builtin_amdgcn_sched_barrier(0);
+        return dot_fetched(x);
+    }
+    __device__ float dot_fetched(const u32x4 (&x)[NCH]) const {
         float acc = 0.0f;
 #pragma unroll
         for (int c = 0; c < NCH; ++c) {
@@ -229,6 +248,8 @@ struct QGeneric {
         for (int i = sub; i < d; i += 16) acc = fmaf(__half2float(row[i]), q[i], acc);
         return acc;
     }
+    template <typename T>
+    __device__ float dot_all(const T* row, int sub) const { return dot(row, sub); }
 };
 
 // fused stage-1/2 epilogue (reference order of fp32 operations: dot * w, then

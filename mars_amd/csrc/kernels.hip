@@ -1020,23 +1020,27 @@ __global__ __launch_bounds__(kFinThreads) void k_cert_bfs(CertArgs a, MultiArgs 
     signal_done(a.done, a.seq);
 }
 
-// NCH > 0 (d = 64 NCH): the query is held in registers in the Q=1 scan's fragment
-// layout and a member row's NCH 16-byte loads are all issued before its first FMA (the
-// same floats in the same fmaf order as the loop below, so the same scores).
+// NCH > 0 (d = 64 NCH, NCH <= 12): a member row's NCH 16-byte loads are all issued
+// before its first FMA, and the query is read from LDS chunk by chunk (the same floats
+// in the same fmaf order as the loop below, so the same scores). At most 64 VGPRs, so
+// the kernel still fits on a CU beside a batched scan's workgroup.
 template <int NCH>
-__global__ __launch_bounds__(256) void k_episode(EpisodeArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8))) void k_episode(EpisodeArgs a) {
     // latency-bound and short: its waves go first when they share a CU with a scan
     __builtin_amdgcn_s_setprio(3);
     __shared__ uint64_t s_lists[4][64];
     __shared__ int32_t s_ids[64];
     __shared__ uint64_t s_out[64];
     __shared__ int s_cnt[2];
+    __shared__ f32x4 s_q[NCH > 0 ? NCH * 16 : 1];     // float4 i = floats 4i .. 4i+3
     const int lane = lane_id(), wave = int(threadIdx.x >> 6);
     const int sub = lane & 15, grp = lane >> 4;
     const int k = a.k;
     uint64_t list = kEmptyKey, thr = kEmptyKey;
-    QF32<(NCH > 0 ? NCH : 1)> qf;
-    if constexpr (NCH > 0) qf.load(a.q, sub);
+    if constexpr (NCH > 0) {
+        for (int i = int(threadIdx.x); i < NCH * 16; i += 256) s_q[i] = reinterpret_cast<const f32x4*>(a.q)[i];
+        __syncthreads();
+    }
     for (int base = 4 * wave; base < a.m; base += 16) {
         const int j = base + grp;
         const bool valid = j < a.m;
@@ -1044,10 +1048,18 @@ __global__ __launch_bounds__(256) void k_episode(EpisodeArgs a) {
         float acc = 0.0f;
         const float* row = a.emb + int64_t(node) * a.d;
         if constexpr (NCH > 0) {
+            const f32x4* r4 = reinterpret_cast<const f32x4*>(row) + sub;
             f32x4 x[NCH];
-            qf.fetch(row, sub, x);
+#pragma unroll
+            for (int c = 0; c < NCH; ++c) x[c] = __builtin_nontemporal_load(r4 + c * 16);
             __builtin_amdgcn_sched_barrier(0);     // every load of the row before any FMA
-            acc = qf.dot_fetched(x);
+#pragma unroll
+            for (int c = 0; c < NCH; ++c) {
+                const f32x4 y = s_q[c * 16 + sub];
+                acc = fmaf(x[c].x, y.x, acc); acc = fmaf(x[c].y, y.y, acc);
+                acc = fmaf(x[c].z, y.z, acc); acc = fmaf(x[c].w, y.w, acc);
+                if (c % 3 == 2) __builtin_amdgcn_sched_barrier(0);   // a few LDS reads in flight
+            }
         } else if ((a.d & 3) == 0) {
             const float4* r4 = reinterpret_cast<const float4*>(row);
             const float4* q4 = reinterpret_cast<const float4*>(a.q);
@@ -1230,7 +1242,6 @@ KernelLaunch episode_launch(int32_t d) {
             case 6: l.fn = reinterpret_cast<const void*>(&k_episode<6>); break;
             case 8: l.fn = reinterpret_cast<const void*>(&k_episode<8>); break;
             case 12: l.fn = reinterpret_cast<const void*>(&k_episode<12>); break;
-            case 16: l.fn = reinterpret_cast<const void*>(&k_episode<16>); break;
             default: break;
         }
     }

@@ -122,7 +122,7 @@ __global__ __launch_bounds__(256) void k_multi_seed(SeedArgs a) {
         qf.load(a.queries + int64_t(j) * a.d, sub);
         const int32_t id = key_id(ck);
         const T* row = static_cast<const T*>(a.emb) + int64_t(id) * a.d;
-        const float dot = qf.dot(row, sub);
+        const float dot = qf.dot_all(row, sub);
         const QueryTerms t{a.tq[j], a.lambda, a.mod_filter, -1, 0.0f};
         const float s = fuse_score(row16_sum(dot), a.ts[id], (a.mod_filter >= 0) ? a.mods[id] : 0, -1, t);
         key = make_key(s, uint32_t(id));
@@ -185,7 +185,7 @@ __global__ __launch_bounds__(256) void k_visit_scores(VisitScoreArgs a) {
     qf.load(a.queries + int64_t(j) * a.d, sub);
     const QueryTerms t{a.tq ? a.tq[j] : a.t_q_value, a.lambda, a.mod_filter, -1, 0.0f};
     const int32_t id = a.vlist[int64_t(j) * kMultiVisit + p];
-    const float dot = qf.dot(static_cast<const T*>(a.emb) + int64_t(id) * a.d, sub);
+    const float dot = qf.dot_all(static_cast<const T*>(a.emb) + int64_t(id) * a.d, sub);
     const float s = fuse_score(row16_sum(dot), a.ts[id], (a.mod_filter >= 0) ? a.mods[id] : 0, -1, t);
     if (sub == 0) a.vfin[int64_t(j) * kMultiVisit + p] = s;
 }
