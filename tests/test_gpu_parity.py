@@ -277,13 +277,34 @@ def _random_graph(rng, n, d, deg=6, n_ep=None):
     return emb, mods, ts, row, col, ep
 
 
+def check_episode(dev, q, ep, k):
+    """Episode-scoped query against the oracle (ids exact, scores to the fp32 bar)."""
+    off = dev.csr.ep_csr_offsets
+    cfg = RetrievalConfig(top_k=k, time_decay_lambda=LAM, max_results_returned=k,
+                          retrieval_scope=RetrievalScope.EpisodeScoped, query_episode_id=ep,
+                          query_episode_member_begin=int(off[ep]),
+                          query_episode_member_count=int(off[ep + 1] - off[ep]))
+    res, st = dev.query(q, cfg)
+    ref = oracle.query(dev.og, q, T_Q, ocfg(cfg))
+    assert ref["scoped"] and st.scope_fallback == 0
+    assert [r.node_id for r in res] == [w[0] for w in ref["results"]]
+    for r, w in zip(res, ref["results"]):
+        if w[1] == -FLT_MAX:
+            assert r.score == np.float32(-FLT_MAX)
+        else:
+            assert abs(r.score - w[1]) <= RTOL_F32 * max(abs(w[1]), 1.0)
+
+
 @pytest.mark.parametrize("n,d", [(5, 768), (300, 100), (3000, 384), (2000, 1024), (777, 256), (1500, 64)])
 def test_shapes(n, d, rng):
+    """Global queries at several dimensions, and episode-scoped ones through each episode
+    kernel variant (register-fragment rows for d = 256 / 384 / 768, the loop otherwise)."""
     emb, mods, ts, row, col, ep = _random_graph(rng, n, d)
     dev = Dev(emb, mods, ts, row, col, ep, fp16=True)
     try:
         for node in (0, n // 2, n - 1):
             check_global(dev, emb[node], RetrievalConfig(top_k=10, time_decay_lambda=LAM, max_results_returned=20))
+            check_episode(dev, emb[node], int(ep[node]), 10)
         dev.ctx.use_fp16 = True
         e16 = oracle.to_f16_bits(emb)
         check_global(dev, emb[1], RetrievalConfig(top_k=10, time_decay_lambda=LAM), emb16=e16)
@@ -441,3 +462,33 @@ def test_graph_replay_matches_eager(dev10k, corpus_10k):
     finally:
         dev10k.ctx.use_cuda_graph = False
         dev10k.ctx.use_fp16 = False
+
+
+def test_completion_word_matches_stream_sync(dev10k, corpus_10k):
+    """Queries that complete through the host-mapped completion word (the default) and
+    ones that synchronise the stream (MARS_CTX_TIMING) return the same results, and the
+    debug readers see the polled query's state."""
+    qs = corpus.pick_queries(corpus_10k.modalities, 12, seed=607)
+    off = dev10k.csr.ep_csr_offsets
+    try:
+        for certified in (False, True):
+            dev10k.ctx.certified = certified
+            for node in qs:
+                ep = int(corpus_10k.episode_ids[node])
+                for cfg in (RetrievalConfig(top_k=10, time_decay_lambda=LAM, max_results_returned=100),
+                            RetrievalConfig(top_k=10, time_decay_lambda=LAM,
+                                            retrieval_scope=RetrievalScope.EpisodeScoped, query_episode_id=ep,
+                                            query_episode_member_begin=int(off[ep]),
+                                            query_episode_member_count=int(off[ep + 1] - off[ep]))):
+                    dev10k.ctx.timing = True
+                    synced, _ = dev10k.query(corpus_10k.embeddings[node], cfg)
+                    dev10k.ctx.timing = False
+                    polled, _ = dev10k.query(corpus_10k.embeddings[node], cfg)
+                    assert polled == synced
+        dev10k.ctx.certified = False
+        res, _ = dev10k.query(corpus_10k.embeddings[qs[0]], RetrievalConfig(top_k=10, time_decay_lambda=LAM))
+        ids, hops, scores = dev10k.ctx.last_visited()
+        assert len(ids) >= len(res) and set(r.node_id for r in res) <= set(int(i) for i in ids)
+    finally:
+        dev10k.ctx.timing = False
+        dev10k.ctx.certified = False
