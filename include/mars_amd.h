@@ -172,6 +172,11 @@ int mars_graph_knn(mars_graph* g, int32_t k, int32_t* nbrs);
  * block_rows consecutive ids (block_rows >= num_nodes: mars_graph_knn). For corpora
  * where the exact all-pairs search is too long to build (13M rows: ~2.6e17 FLOP). */
 int mars_graph_knn_blocked(mars_graph* g, int32_t k, int32_t block_rows, int32_t* nbrs);
+/* Measurement aid, no counterpart in the reference: the bandwidth (GB/s, best of 256,
+ * 512 and 1024 workgroups, reps timed launches each) of a plain streaming read of the
+ * graph's fp32 (fp16 = 0) or fp16 rows with no arithmetic, the practical ceiling of the
+ * row scans on this device. MARS_ERR_UNSUPPORTED when those rows are absent. */
+int mars_graph_read_ceiling(const mars_graph* g, int32_t fp16, int32_t reps, double* gbps);
 /* Copy device arrays back to host (any pointer may be NULL to skip): the NSN graph as
  * a packed CSR (row_offsets: num_nodes + 1, col_indices: num_edges) and the episode CSR. */
 int mars_graph_download(const mars_graph* g, int32_t* row_offsets, int32_t* col_indices,

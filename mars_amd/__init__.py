@@ -417,6 +417,15 @@ def graph_knn(dg: DeviceMemoryGraph, k: int = 8, block_rows: int = 0) -> np.ndar
     return out
 
 
+def read_ceiling(dg: DeviceMemoryGraph, fp16: bool = True, reps: int = 20) -> float:
+    """GB/s of a plain streaming read of the graph's rows (no arithmetic): the practical
+    ceiling of the row scans on this device."""
+    out = C.c_double()
+    check(lib.mars_graph_read_ceiling(dg.handle, 1 if fp16 else 0, int(reps), C.byref(out)),
+          "mars_graph_read_ceiling")
+    return float(out.value)
+
+
 @dataclass
 class InsertStats:
     first_node: int

@@ -229,6 +229,7 @@ SIGNATURES = {
     "mars_graph_link_knn": (C.c_int, [VP, I32, I32, I32, VP, C.POINTER(InsertStatsC)]),
     "mars_graph_knn": (C.c_int, [VP, I32, VP]),
     "mars_graph_knn_blocked": (C.c_int, [VP, I32, I32, VP]),
+    "mars_graph_read_ceiling": (C.c_int, [VP, I32, I32, C.POINTER(C.c_double)]),
     "mars_graph_set_csr": (C.c_int, [VP, I32, VP, VP]),
     "mars_graph_insert": (C.c_int, [VP, I32, VP, VP, VP, VP, I32, VP, C.POINTER(InsertStatsC)]),
     "mars_ctx_last_seeds": (C.c_int, [VP, VP, VP, I32, PI32]),

@@ -1415,6 +1415,49 @@ int mars_query_global_batch_knn(const mars_graph* gh, mars_ctx* ch, const float*
     return MARS_OK;
 }
 
+int mars_graph_read_ceiling(const mars_graph* gh, int32_t fp16, int32_t reps, double* gbps) {
+    MARS_CHECK(gh && gbps && reps > 0, MARS_ERR_INVALID, "bad arguments");
+    const Graph& g = gh->g;
+    const void* rows = fp16 ? static_cast<const void*>(g.emb16) : static_cast<const void*>(g.emb);
+    MARS_CHECK(rows != nullptr, MARS_ERR_UNSUPPORTED, "no %s rows", fp16 ? "fp16" : "fp32");
+    const int32_t n = __atomic_load_n(&g.n, __ATOMIC_ACQUIRE);
+    const int64_t bytes = int64_t(n) * g.d * (fp16 ? 2 : 4) / 16 * 16;
+    MARS_CHECK(bytes > 0, MARS_ERR_INVALID, "empty graph");
+    MARS_TRY(use_device(g.device));
+    constexpr int32_t kGrids[3] = {256, 512, 1024};
+    hipStream_t s = nullptr;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    uint32_t* out = nullptr;
+    hipError_t e = hipStreamCreateWithFlags(&s, hipStreamNonBlocking);
+    if (e == hipSuccess) e = hipEventCreate(&e0);
+    if (e == hipSuccess) e = hipEventCreate(&e1);
+    if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&out), 1024 * sizeof(uint32_t));
+    double best = 0.0;
+    int rc = MARS_OK;
+    for (int gi = 0; gi < 3 && e == hipSuccess && rc == MARS_OK; ++gi) {
+        for (int w = 0; w < 2 && rc == MARS_OK; ++w) rc = launch_read_rows(rows, bytes, kGrids[gi], 0x9E3779B9u, out, s);
+        if (rc != MARS_OK) break;
+        e = hipEventRecord(e0, s);
+        for (int r = 0; r < reps && rc == MARS_OK && e == hipSuccess; ++r)
+            rc = launch_read_rows(rows, bytes, kGrids[gi], 0x9E3779B9u, out, s);
+        if (rc != MARS_OK || e != hipSuccess) break;
+        e = hipEventRecord(e1, s);
+        if (e == hipSuccess) e = hipEventSynchronize(e1);
+        float ms = 0.0f;
+        if (e == hipSuccess) e = hipEventElapsedTime(&ms, e0, e1);
+        if (e == hipSuccess && ms > 0.0f) best = std::max(best, double(bytes) * reps / (double(ms) * 1e-3) / 1e9);
+    }
+    if (s) (void)hipStreamSynchronize(s);
+    if (out) (void)hipFree(out);
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    if (s) (void)hipStreamDestroy(s);
+    if (rc != MARS_OK) return rc;
+    if (e != hipSuccess) return set_error(MARS_ERR_HIP, "read ceiling: %s", hipGetErrorString(e));
+    *gbps = best;
+    return MARS_OK;
+}
+
 int mars_graph_knn_blocked(mars_graph* gh, int32_t k, int32_t block_rows, int32_t* nbrs) {
     MARS_CHECK(gh && nbrs && k >= 1 && k <= 16 && block_rows > 0, MARS_ERR_INVALID,
                "k-NN: bad arguments (k=%d, block_rows=%d)", k, block_rows);

@@ -1176,6 +1176,27 @@ __global__ __launch_bounds__(256) void k_tile_merge(uint64_t* __restrict__ part,
     }
 }
 
+// Plain streaming read of a row array, no arithmetic: the practical ceiling of the row
+// scans. Each lane keeps 8 non-temporal 16-byte loads in flight (grid-stride); the words
+// are folded so the loads stay live, and a workgroup writes its fold only if it equals
+// the caller's sentinel.
+__global__ __launch_bounds__(256) void k_read_rows(const u32x4* __restrict__ p, int64_t n16, uint32_t sentinel,
+                                                   uint32_t* out) {
+    uint32_t acc = 0u;
+    const int64_t stride = int64_t(gridDim.x) * 256 * 8;
+    for (int64_t base = int64_t(blockIdx.x) * 256 * 8 + threadIdx.x; base < n16; base += stride) {
+        u32x4 v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int64_t i = base + int64_t(j) * 256;
+            v[j] = (i < n16) ? __builtin_nontemporal_load(p + i) : u32x4{0u, 0u, 0u, 0u};
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc ^= v[j].x ^ v[j].y ^ v[j].z ^ v[j].w;
+    }
+    if (acc == sentinel && threadIdx.x == 0) out[blockIdx.x] = acc;
+}
+
 template <typename T, typename QF>
 KernelLaunch scan_launch_t(const ScanArgs& a) {
     KernelLaunch l;
@@ -1295,6 +1316,12 @@ int launch_episode(const EpisodeArgs& a, hipStream_t s) {
     const KernelLaunch l = episode_launch(a.d);
     void* args[] = {const_cast<EpisodeArgs*>(&a)};
     MARS_HIP(hipLaunchKernel(l.fn, l.grid, l.block, args, 0, s));
+    return MARS_OK;
+}
+
+int launch_read_rows(const void* p, int64_t bytes, int32_t wg, uint32_t sentinel, uint32_t* out, hipStream_t s) {
+    MARS_LAUNCH(k_read_rows, dim3(unsigned(wg)), dim3(256), 0, s, static_cast<const u32x4*>(p), bytes / 16,
+                sentinel, out);
     return MARS_OK;
 }
 

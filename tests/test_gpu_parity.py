@@ -492,3 +492,21 @@ def test_completion_word_matches_stream_sync(dev10k, corpus_10k):
     finally:
         dev10k.ctx.timing = False
         dev10k.ctx.certified = False
+
+
+def test_read_ceiling(rng):
+    """The streaming-read ceiling of a graph's rows: positive and below the HBM peak for
+    fp32 and fp16 rows; MARS_ERR_UNSUPPORTED once the fp16 copy is gone."""
+    from mars_amd._lib import MarsError
+    emb, mods, ts, row, col, ep = _random_graph(rng, 40000, 768)
+    dev = Dev(emb, mods, ts, row, col, ep, fp16=True)
+    try:
+        for fp16 in (False, True):
+            gbs = mars_amd.read_ceiling(dev.dg, fp16=fp16, reps=3)
+            assert 0.0 < gbs < 8000.0 * 1.1, (fp16, gbs)
+        mars_amd.free_fp16_embeddings(dev.dg)
+        with pytest.raises(MarsError) as e:
+            mars_amd.read_ceiling(dev.dg, fp16=True)
+        assert e.value.code == -5
+    finally:
+        dev.close()
