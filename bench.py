@@ -49,6 +49,29 @@ def scan_traffic(n: int, d: int, profile: str = "k_scan_fp32_1M.md"):
     return int(kv["traffic_bytes_per_launch"])
 
 
+def checkpoint_pass(args, mars_amd, dg):
+    """MARS v1 checkpoint of the device graph (mars_graph_save) and its reload through the
+    file reader (FNV-1a checked); the file is removed afterwards."""
+    path = Path(args.checkpoint_dir) / "bench_checkpoint.mars"
+    t0 = time.perf_counter()
+    mars_amd.save_device_graph(dg, path)
+    t_save = time.perf_counter() - t0
+    size = path.stat().st_size
+    t0 = time.perf_counter()
+    g = mars_amd.load_graph(path)
+    t_load = time.perf_counter() - t0
+    blob = np.zeros(256 << 20, np.uint8)
+    t0 = time.perf_counter()
+    mars_amd.fnv1a64(blob.tobytes())
+    fnv = blob.size / (time.perf_counter() - t0) / 1e9
+    path.unlink()
+    res = dict(bytes=size, nodes=g.num_nodes, edges=g.num_edges, save_s=t_save, load_s=t_load,
+               save_gbs=size / t_save / 1e9, load_gbs=size / t_load / 1e9, fnv1a_gbs=fnv)
+    log(f"checkpoint: {size / 1e9:.2f} GB MARS v1, save {t_save:.2f} s ({res['save_gbs']:.2f} GB/s), "
+        f"load + checksum {t_load:.2f} s ({res['load_gbs']:.2f} GB/s); FNV-1a alone {fnv:.2f} GB/s")
+    return res
+
+
 def tiled_pass(args, mars_amd, corpus, c, qnodes, N, D, K, pctl, lat_resident, host_memory):
     """tiled_query contract over the corpus held in host RAM (pinned when the host grants it):
     tiles of --tiled-tile rows (the copy of tile i+1 overlaps the scan of tile i)."""
@@ -200,6 +223,8 @@ def main() -> int:
     ap.add_argument("--stream-insert-batch", type=int, default=10, help="nodes per insert call when streaming")
     ap.add_argument("--knn-block", type=int, default=0,
                     help="k-NN of the NSN graph within blocks of this many consecutive ids (0: exact, all pairs)")
+    ap.add_argument("--checkpoint-dir", default="",
+                    help="also time a MARS v1 checkpoint of the device graph to this directory and its reload")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU; --gpus above 1 is not supported here "
@@ -392,6 +417,8 @@ def main() -> int:
                                   scan_gbs=bytes_f16 / float(kern_h.mean()) / 1e3,
                                   scan_frac=bytes_f16 / float(kern_h.mean()) / 1e3 / HBM_PEAK_GBS)
 
+    if args.checkpoint_dir and not args.profile_only:
+        out["checkpoint"] = checkpoint_pass(args, mars_amd, dg)
     if not args.profile_only and args.tiled_queries > 0:
         out["tiled_comparator"] = tiled_pass(args, mars_amd, corpus, c, qnodes[W:], N, D, K, pctl, lat_g,
                                              "pinned" if host_rows else "pageable")

@@ -182,6 +182,42 @@ int mars_graph_read_ceiling(const mars_graph* g, int32_t fp16, int32_t reps, dou
 int mars_graph_download(const mars_graph* g, int32_t* row_offsets, int32_t* col_indices,
                         int32_t* ep_offsets, int32_t* ep_members);
 
+/* ---- files: MARS v1 graph checkpoints and the KIDS corpus -------------------
+ * MARS v1 (persistence.h:8-18): "MARS", uint32 version 1, int32 num_nodes,
+ * num_edges, embedding_dim, row_offsets[num_nodes + 1], col_indices[num_edges],
+ * embeddings[num_nodes * dim] (float), modalities[num_nodes], timestamps[num_nodes]
+ * (float), then the FNV-1a 64-bit hash of every preceding byte; native byte order.
+ * A file loads only if magic, version (MARS_ERR_UNSUPPORTED otherwise), exact size
+ * and hash all check (persistence.cpp load_graph returns false on each). */
+/* fnv1a_checksum (persistence.h:37): FNV-1a 64 of len bytes. */
+int mars_fnv1a64(const void* data, int64_t len, uint64_t* out);
+/* save_graph (persistence.h:29) from host arrays. */
+int mars_graph_file_save(const char* path, int32_t num_nodes, int32_t num_edges, int32_t dim,
+                         const int32_t* row_offsets, const int32_t* col_indices,
+                         const float* embeddings, const int32_t* modalities,
+                         const float* timestamps);
+/* load_graph (persistence.h:33) in two calls: the sizes (header and file size
+ * checked), then the arrays into caller buffers of those sizes (hash checked; on an
+ * error the buffers' contents are unspecified, as the reference's graph is). */
+int mars_graph_file_info(const char* path, int32_t* num_nodes, int32_t* num_edges, int32_t* dim);
+int mars_graph_file_load(const char* path, int32_t num_nodes, int32_t num_edges, int32_t dim,
+                         int32_t* row_offsets, int32_t* col_indices, float* embeddings,
+                         int32_t* modalities, float* timestamps);
+/* save_graph of the device-resident graph (streamed inserts included): a checkpoint
+ * with no host copy of the whole corpus (rows are streamed in 64 MB pieces). */
+int mars_graph_save(const mars_graph* g, const char* path);
+/* KIDS binary corpus (bench_kids_sweep.cu:29-37, write_corpus_bin :84-102; reader
+ * scripts/bench_kids_ball_cuvs_cagra.py:49-60): uint32 0x5344494b ("KIDS"), uint32
+ * version 1, int32 N, D, embeddings[N * D], timestamps[N], modalities[N],
+ * episode_ids[N]. Reading checks the magic and the exact size (the version is not
+ * read, as in the reference reader). */
+int mars_kids_file_write(const char* path, int32_t n, int32_t d, const float* embeddings,
+                         const float* timestamps, const int32_t* modalities,
+                         const int32_t* episode_ids);
+int mars_kids_file_info(const char* path, int32_t* n, int32_t* d);
+int mars_kids_file_read(const char* path, int32_t n, int32_t d, float* embeddings, float* timestamps,
+                        int32_t* modalities, int32_t* episode_ids);
+
 /* ---- streaming insert (streaming.cpp:35-163, engine_server.cu:154-213) ------- */
 typedef struct mars_insert_stats {
     int32_t first_node;       /* id of the first inserted node (ids are consecutive)   */

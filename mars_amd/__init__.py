@@ -417,6 +417,69 @@ def graph_knn(dg: DeviceMemoryGraph, k: int = 8, block_rows: int = 0) -> np.ndar
     return out
 
 
+# ---- files: MARS v1 graph checkpoints (persistence.h) and the KIDS corpus ----------------
+def fnv1a64(data) -> int:
+    """FNV-1a 64 of a bytes-like object (fnv1a_checksum, persistence.h:37)."""
+    buf = np.frombuffer(bytes(data), np.uint8)
+    out = C.c_uint64()
+    check(lib.mars_fnv1a64(_ptr(buf) if buf.size else None, int(buf.size), C.byref(out)), "mars_fnv1a64")
+    return int(out.value)
+
+
+def save_graph(g: MemoryGraph, path) -> None:
+    """save_graph (persistence.h:29): a MARS v1 file of a host graph."""
+    ro, col = _i32(g.row_offsets), _i32(g.col_indices)
+    emb = np.ascontiguousarray(g.embeddings, np.float32)
+    mods, ts = _i32(g.modalities), np.ascontiguousarray(g.timestamps, np.float32)
+    check(lib.mars_graph_file_save(str(path).encode(), int(g.num_nodes), int(len(col)), int(g.embedding_dim),
+                                   _ptr(ro), _ptr(col), _ptr(emb), _ptr(mods), _ptr(ts)), "mars_graph_file_save")
+
+
+def load_graph(path) -> MemoryGraph:
+    """load_graph (persistence.h:33): a host graph from a MARS v1 file (MarsError when
+    the magic, version, size or checksum does not check)."""
+    p = str(path).encode()
+    n, e, d = C.c_int32(), C.c_int32(), C.c_int32()
+    check(lib.mars_graph_file_info(p, C.byref(n), C.byref(e), C.byref(d)), "mars_graph_file_info")
+    n, e, d = n.value, e.value, d.value
+    ro = np.zeros(n + 1, np.int32)
+    col = np.zeros(max(e, 1), np.int32)
+    emb = np.zeros((n, d), np.float32)
+    mods = np.zeros(max(n, 1), np.int32)
+    ts = np.zeros(max(n, 1), np.float32)
+    check(lib.mars_graph_file_load(p, n, e, d, _ptr(ro), _ptr(col), _ptr(emb), _ptr(mods), _ptr(ts)),
+          "mars_graph_file_load")
+    return MemoryGraph(n, d, ro, col[:e], emb, mods[:n], ts[:n])
+
+
+def save_device_graph(dg: DeviceMemoryGraph, path) -> None:
+    """Checkpoint of the device-resident graph (inserts included) as a MARS v1 file."""
+    check(lib.mars_graph_save(dg.handle, str(path).encode()), "mars_graph_save")
+
+
+def write_kids_corpus(path, embeddings, timestamps, modalities, episode_ids) -> None:
+    """KIDS binary corpus (bench_kids_sweep.cu:29-37, write_corpus_bin :84-102)."""
+    emb = np.ascontiguousarray(embeddings, np.float32)
+    n, d = emb.shape
+    ts, mods, ep = np.ascontiguousarray(timestamps, np.float32), _i32(modalities), _i32(episode_ids)
+    check(lib.mars_kids_file_write(str(path).encode(), int(n), int(d), _ptr(emb), _ptr(ts), _ptr(mods), _ptr(ep)),
+          "mars_kids_file_write")
+
+
+def read_kids_corpus(path):
+    """(embeddings, timestamps, modalities, episode_ids) of a KIDS corpus file."""
+    p = str(path).encode()
+    n, d = C.c_int32(), C.c_int32()
+    check(lib.mars_kids_file_info(p, C.byref(n), C.byref(d)), "mars_kids_file_info")
+    n, d = n.value, d.value
+    emb = np.zeros((n, d), np.float32)
+    ts = np.zeros(max(n, 1), np.float32)
+    mods = np.zeros(max(n, 1), np.int32)
+    ep = np.zeros(max(n, 1), np.int32)
+    check(lib.mars_kids_file_read(p, n, d, _ptr(emb), _ptr(ts), _ptr(mods), _ptr(ep)), "mars_kids_file_read")
+    return emb, ts[:n], mods[:n], ep[:n]
+
+
 def read_ceiling(dg: DeviceMemoryGraph, fp16: bool = True, reps: int = 20) -> float:
     """GB/s of a plain streaming read of the graph's rows (no arithmetic): the practical
     ceiling of the row scans on this device."""

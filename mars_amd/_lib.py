@@ -230,6 +230,14 @@ SIGNATURES = {
     "mars_graph_knn": (C.c_int, [VP, I32, VP]),
     "mars_graph_knn_blocked": (C.c_int, [VP, I32, I32, VP]),
     "mars_graph_read_ceiling": (C.c_int, [VP, I32, I32, C.POINTER(C.c_double)]),
+    "mars_fnv1a64": (C.c_int, [VP, I64, C.POINTER(C.c_uint64)]),
+    "mars_graph_file_save": (C.c_int, [C.c_char_p, I32, I32, I32, VP, VP, VP, VP, VP]),
+    "mars_graph_file_info": (C.c_int, [C.c_char_p, C.POINTER(I32), C.POINTER(I32), C.POINTER(I32)]),
+    "mars_graph_file_load": (C.c_int, [C.c_char_p, I32, I32, I32, VP, VP, VP, VP, VP]),
+    "mars_graph_save": (C.c_int, [VP, C.c_char_p]),
+    "mars_kids_file_write": (C.c_int, [C.c_char_p, I32, I32, VP, VP, VP, VP]),
+    "mars_kids_file_info": (C.c_int, [C.c_char_p, C.POINTER(I32), C.POINTER(I32)]),
+    "mars_kids_file_read": (C.c_int, [C.c_char_p, I32, I32, VP, VP, VP, VP]),
     "mars_graph_set_csr": (C.c_int, [VP, I32, VP, VP]),
     "mars_graph_insert": (C.c_int, [VP, I32, VP, VP, VP, VP, I32, VP, C.POINTER(InsertStatsC)]),
     "mars_ctx_last_seeds": (C.c_int, [VP, VP, VP, I32, PI32]),

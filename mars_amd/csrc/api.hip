@@ -9,6 +9,7 @@
 //  kernel writes the result records into mapped pinned memory.
 // ============================================================================
 #include "internal.hpp"
+#include "formats.hpp"
 
 #include <algorithm>
 #include <atomic>
@@ -790,6 +791,50 @@ int mars_graph_download(const mars_graph* gh, int32_t* row, int32_t* col, int32_
     if (ep_mem && g.ep_mem && g.member_total > 0)
         MARS_HIP(hipMemcpy(ep_mem, g.ep_mem, size_t(g.member_total) * sizeof(int32_t), hipMemcpyDeviceToHost));
     return MARS_OK;
+}
+
+// MARS v1 checkpoint of the device graph: the published nodes (inserts included) as
+// the packed CSR, fp32 rows, modalities and timestamps, streamed to the file in 64 MB
+// pieces. Holds the graph's lock, so an insert lands wholly before or after it.
+int mars_graph_save(const mars_graph* gh, const char* path) {
+    MARS_CHECK(gh && path, MARS_ERR_INVALID, "null argument");
+    std::lock_guard<std::mutex> lock(gh->mu);
+    const Graph& g = gh->g;
+    MARS_TRY(use_device(g.device));
+    if (g.ins_stream) MARS_HIP(hipStreamSynchronize(g.ins_stream));
+    const int32_t n = g.n, d = g.d;
+    std::vector<int32_t> dcol(size_t(std::max<int64_t>(g.e_used, 1)));
+    if (g.e_used > 0)
+        MARS_HIP(hipMemcpy(dcol.data(), g.col, size_t(g.e_used) * sizeof(int32_t), hipMemcpyDeviceToHost));
+    std::vector<int32_t> row(size_t(n) + 1, 0), col;
+    col.reserve(size_t(g.e));
+    for (int32_t i = 0; i < n; ++i) {
+        const int64_t w = g.ro_h[size_t(i)];
+        const int32_t b = int32_t(uint32_t(w)), len = int32_t(w >> 32);
+        col.insert(col.end(), dcol.begin() + b, dcol.begin() + b + len);
+        row[size_t(i) + 1] = int32_t(col.size());
+    }
+    GraphFileWriter w;
+    MARS_TRY(w.open(path, n, int32_t(col.size()), d));
+    MARS_TRY(w.put(row.data(), row.size() * sizeof(int32_t)));
+    MARS_TRY(w.put(col.data(), col.size() * sizeof(int32_t)));
+    const int64_t rows_per = std::max<int64_t>(1, (int64_t(64) << 20) / (int64_t(std::max(d, 1)) * 4));
+    std::vector<float> buf(size_t(std::min<int64_t>(rows_per, std::max(n, 1))) * size_t(std::max(d, 1)));
+    for (int64_t r0 = 0; r0 < n && d > 0; r0 += rows_per) {
+        const int64_t nr = std::min<int64_t>(rows_per, n - r0);
+        const size_t bytes = size_t(nr) * size_t(d) * sizeof(float);
+        MARS_HIP(hipMemcpy(buf.data(), g.emb + r0 * d, bytes, hipMemcpyDeviceToHost));
+        MARS_TRY(w.put(buf.data(), bytes));
+    }
+    std::vector<int32_t> mods(size_t(std::max(n, 1)));
+    std::vector<float> ts(size_t(std::max(n, 1)));
+    if (n > 0) {
+        MARS_HIP(hipMemcpy(mods.data(), g.mods, size_t(n) * sizeof(int32_t), hipMemcpyDeviceToHost));
+        MARS_HIP(hipMemcpy(ts.data(), g.ts, size_t(n) * sizeof(float), hipMemcpyDeviceToHost));
+    }
+    MARS_TRY(w.put(mods.data(), size_t(n) * sizeof(int32_t)));
+    MARS_TRY(w.put(ts.data(), size_t(n) * sizeof(float)));
+    return w.finish();
 }
 
 int mars_ctx_create(int32_t max_nodes, int32_t dim, int32_t max_k, uint32_t flags, mars_ctx** out) {

@@ -88,6 +88,10 @@ def _load_ref():
         "ref_graph_copy": (None, [VP, VP, VP, VP, VP, VP, VP]),
         "ref_stream_flush": (I32, [VP, I32, I32, I32, VP, VP, VP]),
         "ref_graph_free": (None, [VP]),
+        "ref_fnv1a": (C.c_uint64, [VP, C.c_size_t]),
+        "ref_save_graph": (C.c_int, [C.c_char_p, I32, I32, I32, VP, VP, VP, VP, VP]),
+        "ref_load_graph": (C.c_int, [C.c_char_p, C.POINTER(I32), C.POINTER(I32), C.POINTER(I32), VP, VP, VP, VP,
+                                     VP]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(r, name)

@@ -1,13 +1,15 @@
 // ============================================================================
 //  oracle/ref_shim.cpp — extern "C" wrappers over the reference's own host
 //  code, compiled together with the reference sources (src/memory_graph.cpp,
-//  src/streaming.cpp) where they lie, into oracle/_ref/libref.so.
+//  src/streaming.cpp, src/persistence.cpp) where they lie, into
+//  oracle/_ref/libref.so.
 //
 //  TEST INFRASTRUCTURE: used to pin the oracle and the product's host code
 //  against the reference's behaviour (episode CSR, kids corpus, NSN builder,
 //  streaming flush). Never loaded by the product.
 // ============================================================================
 #include "memory_graph.h"
+#include "persistence.h"
 #include "streaming.h"
 
 #include <cstring>
@@ -93,5 +95,38 @@ int32_t ref_stream_flush(void* h, int32_t capacity, int32_t nsn_k, int32_t n_new
 }
 
 void ref_graph_free(void* h) { delete static_cast<RefGraph*>(h); }
+
+// fnv1a_checksum (persistence.cpp:23-31).
+uint64_t ref_fnv1a(const void* data, size_t len) { return fnv1a_checksum(data, len); }
+
+// save_graph (persistence.cpp:43-108) of a graph given as arrays; 1 on success.
+int ref_save_graph(const char* path, int32_t n, int32_t e, int32_t d, const int32_t* row_offsets,
+                   const int32_t* col, const float* emb, const int32_t* mods, const float* ts) {
+    MemoryGraph g;
+    g.num_nodes = n;
+    g.num_edges = e;
+    g.embedding_dim = d;
+    g.row_offsets.assign(row_offsets, row_offsets + n + 1);
+    g.col_indices.assign(col, col + e);
+    g.embeddings.assign(emb, emb + size_t(n) * size_t(d));
+    g.modalities.assign(mods, mods + n);
+    g.timestamps.assign(ts, ts + n);
+    return save_graph(g, path) ? 1 : 0;
+}
+
+// load_graph (persistence.cpp:110-215); 1 on success. Sizes are always returned;
+// arrays are copied where the pointer is not null.
+int ref_load_graph(const char* path, int32_t* n, int32_t* e, int32_t* d, int32_t* row_offsets, int32_t* col,
+                   float* emb, int32_t* mods, float* ts) {
+    MemoryGraph g;
+    if (!load_graph(g, path)) return 0;
+    *n = g.num_nodes; *e = g.num_edges; *d = g.embedding_dim;
+    if (row_offsets) std::memcpy(row_offsets, g.row_offsets.data(), g.row_offsets.size() * 4);
+    if (col && !g.col_indices.empty()) std::memcpy(col, g.col_indices.data(), g.col_indices.size() * 4);
+    if (emb && !g.embeddings.empty()) std::memcpy(emb, g.embeddings.data(), g.embeddings.size() * 4);
+    if (mods && !g.modalities.empty()) std::memcpy(mods, g.modalities.data(), g.modalities.size() * 4);
+    if (ts && !g.timestamps.empty()) std::memcpy(ts, g.timestamps.data(), g.timestamps.size() * 4);
+    return 1;
+}
 
 }  // extern "C"
