@@ -247,6 +247,13 @@ typedef struct mars_insert_stats {
 int mars_graph_insert(mars_graph* g, int32_t n_new, const float* embeddings, const int32_t* modalities,
                       const float* timestamps, const int32_t* episode_ids, int32_t knn_k,
                       int32_t* out_knn, mars_insert_stats* stats);
+/* Replace published rows [first, first + count) in place: fp32 rows, modalities and
+ * timestamps (the fp16 copy follows); edges are unchanged. No counterpart function in
+ * the reference: its engine server rewrites the host MemoryGraph for an ADD of an
+ * existing id or a DELETE tombstone (engine_server.cu:154-191). Rows being replaced
+ * must not be read by a concurrent query. */
+int mars_graph_set_rows(mars_graph* g, int32_t first, int32_t count, const float* embeddings,
+                        const int32_t* modalities, const float* timestamps);
 
 /* Deferred k-NN edges (the second half of add_incremental_edges_, streaming.cpp:97-163,
  * taken out of the insert so that many inserts share one corpus pass): nodes inserted
@@ -425,6 +432,7 @@ int mars_device_free(void* ptr);
 int mars_copy_to_device(void* dst, const void* src, size_t bytes);
 int mars_copy_to_host(void* dst, const void* src, size_t bytes);
 int mars_copy_device(void* dst, const void* src, size_t bytes);   /* device to device */
+int mars_device_memory(size_t* free_bytes, size_t* total_bytes);  /* hipMemGetInfo of the device */
 
 /* ---- benchmark loop (harness semantics of src/latency_bench.cu:355-393) ------------ */
 /* Runs n single queries back to back, query i reading the device vector

@@ -501,6 +501,16 @@ class InsertStats:
     knn_us: float
 
 
+def set_rows(dg: DeviceMemoryGraph, first: int, embeddings, modalities, timestamps) -> None:
+    """Replace published rows first.. in place (rows, modalities, timestamps; edges kept)."""
+    emb = _f32(embeddings).reshape(-1)
+    mods, ts = _i32(modalities), _f32(timestamps)
+    if len(ts) != len(mods) or emb.size != len(mods) * dg.embedding_dim:
+        raise ValueError("set_rows: rows / modalities / timestamps disagree in length")
+    check(lib.mars_graph_set_rows(dg.handle, int(first), len(mods), _ptr(emb), _ptr(mods), _ptr(ts)),
+          "mars_graph_set_rows")
+
+
 def insert_nodes(dg: DeviceMemoryGraph, embeddings, modalities, timestamps, episode_ids=None, knn_k: int = 8,
                  return_knn: bool = False):
     """Streaming insert (replaces StreamingBuffer::insert + flush, src/streaming.cpp:13-163):

@@ -231,6 +231,8 @@ SIGNATURES = {
     "mars_graph_knn_blocked": (C.c_int, [VP, I32, I32, VP]),
     "mars_graph_read_ceiling": (C.c_int, [VP, I32, I32, C.POINTER(C.c_double)]),
     "mars_fnv1a64": (C.c_int, [VP, I64, C.POINTER(C.c_uint64)]),
+    "mars_graph_set_rows": (C.c_int, [VP, I32, I32, VP, VP, VP]),
+    "mars_device_memory": (C.c_int, [C.POINTER(C.c_size_t), C.POINTER(C.c_size_t)]),
     "mars_graph_file_save": (C.c_int, [C.c_char_p, I32, I32, I32, VP, VP, VP, VP, VP]),
     "mars_graph_file_info": (C.c_int, [C.c_char_p, C.POINTER(I32), C.POINTER(I32), C.POINTER(I32)]),
     "mars_graph_file_load": (C.c_int, [C.c_char_p, I32, I32, I32, VP, VP, VP, VP, VP]),

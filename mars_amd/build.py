@@ -29,6 +29,7 @@ SOURCES = ["api.hip", "kernels.hip", "batch.hip", "multi.hip", "insert.hip", "ti
            "shim.cpp"]
 DRIVER_SRC = ROOT / "tests" / "cpp" / "shim_driver.cpp"
 DRIVER = ROOT / "tests" / "cpp" / "shim_driver"
+ENGINE = PKG / "mars_engine"
 
 
 def _compile(src: str) -> Path:
@@ -61,8 +62,14 @@ def build_library(verbose: bool = False) -> Path:
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"driver build failed: {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
+    # the JSON-line engine server over the C ABI
+    cmd = [CXX, "-std=c++17", "-O2", "-Wall", "-Wextra", f"-I{ROOT / 'include'}", str(CSRC / "engine.cpp"), "-o",
+           str(ENGINE), f"-L{PKG}", "-lmars_amd", "-Wl,-rpath,$ORIGIN"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"engine build failed: {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
     if verbose:
-        print(f"built {LIB} and {DRIVER}")
+        print(f"built {LIB}, {DRIVER} and {ENGINE}")
     return LIB
 
 

@@ -959,6 +959,14 @@ int mars_copy_device(void* dst, const void* src, size_t bytes) {
     return MARS_OK;
 }
 
+int mars_device_memory(size_t* free_bytes, size_t* total_bytes) {
+    MARS_CHECK(free_bytes && total_bytes, MARS_ERR_INVALID, "null argument");
+    int devid = 0;
+    MARS_TRY(ensure_device(&devid));
+    MARS_HIP(hipMemGetInfo(free_bytes, total_bytes));
+    return MARS_OK;
+}
+
 int mars_bench_queries(const mars_graph* g, mars_ctx* c, const float* dq, int64_t stride, int32_t n, float t_q,
                        const mars_retrieval_config* cfgs, int32_t n_cfg, double* lat_us, float* kern_us,
                        float* bfs_us, int32_t* n_res) {

@@ -717,3 +717,29 @@ extern "C" int mars_graph_link_knn(mars_graph* gh, int32_t first, int32_t count,
     if (st) *st = r;
     return MARS_OK;
 }
+
+// In-place update of published rows (the engine server's ADD of an existing id and its
+// DELETE tombstone): new fp32 rows, modalities and timestamps; the fp16 copy and its
+// norm bounds follow (the bounds only rise, so the certificate stays valid). Edges are
+// unchanged. Rows being replaced must not be read by a concurrent query.
+extern "C" int mars_graph_set_rows(mars_graph* gh, int32_t first, int32_t count, const float* emb,
+                                   const int32_t* mods, const float* ts) {
+    MARS_CHECK(gh && emb && mods && ts, MARS_ERR_INVALID, "null argument");
+    std::lock_guard<std::mutex> lock(gh->mu);
+    Graph& g = gh->g;
+    MARS_CHECK(first >= 0 && count > 0 && int64_t(first) + count <= g.n, MARS_ERR_INVALID,
+               "rows [%d, %lld) outside the %d published nodes", first, (long long)first + count, g.n);
+    MARS_TRY(use_device(g.device));
+    hipStream_t s = g.ins_stream;
+    const size_t D = size_t(g.d);
+    MARS_HIP(hipMemcpyAsync(g.emb + size_t(first) * D, emb, size_t(count) * D * sizeof(float),
+                            hipMemcpyHostToDevice, s));
+    MARS_HIP(hipMemcpyAsync(g.mods + first, mods, size_t(count) * sizeof(int32_t), hipMemcpyHostToDevice, s));
+    MARS_HIP(hipMemcpyAsync(g.ts + first, ts, size_t(count) * sizeof(float), hipMemcpyHostToDevice, s));
+    if (g.emb16) {
+        MARS_TRY(launch_convert_f16(g.emb + size_t(first) * D, g.emb16 + size_t(first) * D, int64_t(count) * g.d, s));
+        MARS_TRY(launch_row_norms(g.emb, g.emb16, first, int64_t(first) + count, g.d, g.nrm, s));
+    }
+    MARS_HIP(hipStreamSynchronize(s));
+    return MARS_OK;
+}
