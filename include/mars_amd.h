@@ -423,6 +423,40 @@ int mars_ctx_last_phases(mars_ctx* ctx, double* us, int32_t n);
 int mars_ctx_last_visited(mars_ctx* ctx, int32_t* h_ids, int32_t* h_hops, float* h_scores,
                           int32_t cap, int32_t* n_out);
 
+/* ---- importance, novelty gate, graph maintenance --------------------------------------
+ * The reference's adjacent features (memory_cuda.cuh:234-270, memory_cuda.cu:1466-1658),
+ * kept on the device graph. Each call is synchronous and serialised with inserts. */
+
+/* init_importance (memory_cuda.cuh:240): every node's importance becomes 1.0; nodes
+ * inserted later start at 1.0 too. Allocates capacity_nodes floats on first use. */
+int mars_importance_init(mars_graph* g);
+/* update_importance (memory_cuda.cuh:246-249): importance[i] *= 1 - decay_rate for every
+ * node, then importance[id] = min(importance[id] + boost, max_importance) for each
+ * listed id, in fp32 operation by operation as the reference. Ids < 0 or >= the node
+ * count are skipped; an id listed twice is boosted twice (the reference races there).
+ * ids: host memory, or device memory when ids_on_device != 0. */
+int mars_importance_update(mars_graph* g, const int32_t* ids, int32_t n_ids, int32_t ids_on_device,
+                           float boost, float decay_rate, float max_importance);
+int mars_importance_read(const mars_graph* g, float* h_out, int32_t first, int32_t count);
+/* compute_novelty (memory_cuda.cuh:256-257): max over the nodes of <E_i, q>, at least -1,
+ * and 0 for an empty graph. The query is h_q (host) or d_q (device). ctx may be NULL:
+ * the graph's own context (certified fp16 scan, created on first use) answers; with a
+ * ctx, this is that context's last query. */
+int mars_novelty(const mars_graph* g, mars_ctx* ctx, const float* h_q, const float* d_q, float* max_sim);
+/* init_edge_hits (memory_cuda.cuh:261): one zeroed counter per edge. Counters follow
+ * their edges through inserts; mars_graph_set_csr zeroes them. */
+int mars_edge_hits_init(mars_graph* g);
+/* count_edge_hits_kernel (memory_cuda.cu:1612-1632; the reference has no host call for
+ * it): for the BFS of ctx's last global single query, +1 on every edge (v, u) with
+ * hop(v) >= 1 and hop(u) = hop(v) - 1. No-op after an episode-scoped query or a batch. */
+int mars_edge_hits_count(mars_graph* g, mars_ctx* ctx);
+/* The counters in the order of the graph's CSR (mars_graph_download's col array).
+ * *n_out = edge count; nothing is copied when cap is smaller. */
+int mars_edge_hits_read(const mars_graph* g, int32_t* h_hits, int64_t cap, int64_t* n_out);
+/* maintain_graph (memory_cuda.cuh:268-270): *low_utility = edges with hits <= min_hits,
+ * then every counter is reset to 0. window_queries is unused, as in the reference. */
+int mars_graph_maintain(mars_graph* g, int32_t min_hits, int32_t window_queries, int32_t* low_utility);
+
 /* ---- device memory helpers ----------------------------------------------------------
  * Device buffers for callers that hold no HIP runtime of their own (e.g. the ctypes
  * benchmark; a second HIP runtime in the same process, such as the one bundled with

@@ -33,6 +33,8 @@ __all__ = [
     "free_device", "create_query_context", "destroy_query_context", "query_memory_fast",
     "query_memory_fast_device", "init", "MarsError", "corpus", "DeviceBuffer", "query_batch", "query_global_batch",
     "BatchStats", "query_global_batch_knn", "link", "link_knn", "graph_knn", "set_csr",
+    "init_importance", "update_importance", "read_importance", "compute_novelty", "init_edge_hits",
+    "count_edge_hits", "read_edge_hits", "maintain_graph", "set_rows",
 ]
 
 MOD_TEXT, MOD_AUDIO, MOD_IMAGE = 0, 1, 2
@@ -499,6 +501,66 @@ class InsertStats:
     queryable_us: float
     linked_us: float
     knn_us: float
+
+
+# ---- importance, novelty gate, graph maintenance (memory_cuda.cuh:234-270) ----------
+def init_importance(dg: DeviceMemoryGraph) -> None:
+    check(lib.mars_importance_init(dg.handle), "mars_importance_init")
+
+
+def update_importance(dg: DeviceMemoryGraph, result_ids, boost: float = 0.1, decay_rate: float = 0.001,
+                      max_importance: float = 5.0, device_ptr: Optional[int] = None) -> None:
+    """Decay every node, then boost result_ids (host ints), or n ids at device_ptr."""
+    if device_ptr is not None:
+        n = int(result_ids)
+        check(lib.mars_importance_update(dg.handle, C.c_void_p(device_ptr), n, 1, boost, decay_rate, max_importance),
+              "mars_importance_update")
+        return
+    ids = _i32(result_ids)
+    check(lib.mars_importance_update(dg.handle, _ptr(ids) if len(ids) else None, len(ids), 0, boost, decay_rate,
+                                     max_importance), "mars_importance_update")
+
+
+def read_importance(dg: DeviceMemoryGraph, first: int = 0, count: Optional[int] = None) -> np.ndarray:
+    dg.refresh()
+    count = dg.num_nodes - first if count is None else count
+    out = np.empty(max(count, 0), np.float32)
+    check(lib.mars_importance_read(dg.handle, _ptr(out), int(first), int(count)), "mars_importance_read")
+    return out
+
+
+def compute_novelty(dg: DeviceMemoryGraph, query=None, ctx: Optional["QueryContext"] = None,
+                    device_ptr: Optional[int] = None) -> float:
+    """max_i <E_i, q> (>= -1; 0 for an empty graph). query: host vector, or device_ptr."""
+    out = C.c_float()
+    h = None if query is None else _f32(query)
+    check(lib.mars_novelty(dg.handle, ctx.handle if ctx else None, _ptr(h) if h is not None else None,
+                           C.c_void_p(device_ptr) if device_ptr is not None else None, C.byref(out)),
+          "mars_novelty")
+    return float(out.value)
+
+
+def init_edge_hits(dg: DeviceMemoryGraph) -> None:
+    check(lib.mars_edge_hits_init(dg.handle), "mars_edge_hits_init")
+
+
+def count_edge_hits(dg: DeviceMemoryGraph, ctx: "QueryContext") -> None:
+    """+1 on each edge from a node at hop h >= 1 to a node at hop h - 1 of ctx's last query."""
+    check(lib.mars_edge_hits_count(dg.handle, ctx.handle), "mars_edge_hits_count")
+
+
+def read_edge_hits(dg: DeviceMemoryGraph) -> np.ndarray:
+    n = C.c_int64()
+    check(lib.mars_edge_hits_read(dg.handle, None, 0, C.byref(n)), "mars_edge_hits_read")
+    out = np.zeros(max(n.value, 1), np.int32)
+    check(lib.mars_edge_hits_read(dg.handle, _ptr(out), len(out), C.byref(n)), "mars_edge_hits_read")
+    return out[: n.value]
+
+
+def maintain_graph(dg: DeviceMemoryGraph, min_hits: int = 0, window_queries: int = 1000) -> int:
+    low = C.c_int32()
+    check(lib.mars_graph_maintain(dg.handle, int(min_hits), int(window_queries), C.byref(low)), "mars_graph_maintain")
+    return int(low.value)
 
 
 def set_rows(dg: DeviceMemoryGraph, first: int, embeddings, modalities, timestamps) -> None:

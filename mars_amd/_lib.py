@@ -232,6 +232,14 @@ SIGNATURES = {
     "mars_graph_read_ceiling": (C.c_int, [VP, I32, I32, C.POINTER(C.c_double)]),
     "mars_fnv1a64": (C.c_int, [VP, I64, C.POINTER(C.c_uint64)]),
     "mars_graph_set_rows": (C.c_int, [VP, I32, I32, VP, VP, VP]),
+    "mars_importance_init": (C.c_int, [VP]),
+    "mars_importance_update": (C.c_int, [VP, VP, I32, I32, C.c_float, C.c_float, C.c_float]),
+    "mars_importance_read": (C.c_int, [VP, VP, I32, I32]),
+    "mars_novelty": (C.c_int, [VP, VP, VP, VP, C.POINTER(C.c_float)]),
+    "mars_edge_hits_init": (C.c_int, [VP]),
+    "mars_edge_hits_count": (C.c_int, [VP, VP]),
+    "mars_edge_hits_read": (C.c_int, [VP, VP, I64, C.POINTER(C.c_int64)]),
+    "mars_graph_maintain": (C.c_int, [VP, I32, I32, C.POINTER(C.c_int32)]),
     "mars_device_memory": (C.c_int, [C.POINTER(C.c_size_t), C.POINTER(C.c_size_t)]),
     "mars_graph_file_save": (C.c_int, [C.c_char_p, I32, I32, I32, VP, VP, VP, VP, VP]),
     "mars_graph_file_info": (C.c_int, [C.c_char_p, C.POINTER(I32), C.POINTER(I32), C.POINTER(I32)]),

@@ -104,6 +104,7 @@ int graph_free(Graph& g) {
     if (g.ins_stream) (void)hipStreamSynchronize(g.ins_stream);
     dfree(g.emb); dfree(g.emb16); dfree(g.nrm); dfree(g.mods); dfree(g.ts); dfree(g.ro); dfree(g.rcap); dfree(g.col);
     dfree(g.ep_ids); dfree(g.ep_off); dfree(g.ep_mem);
+    dfree(g.imp); dfree(g.hits); dfree(g.imp_ids); dfree(g.sweep_cnt);
     graph_insert_free(g);
     if (g.ins_stream) (void)hipStreamDestroy(g.ins_stream);
     g = Graph{};
@@ -161,7 +162,7 @@ int ctx_free(Ctx& c) {
     if (c.stream) (void)hipStreamSynchronize(c.stream);
     dfree(c.query); dfree(c.fin); dfree(c.part); dfree(c.vis); dfree(c.claim); dfree(c.vlist);
     dfree(c.vhop); dfree(c.vscore); dfree(c.vro); dfree(c.sortbuf); dfree(c.seed_idx); dfree(c.seed_val); dfree(c.stamps);
-    dfree(c.gthr); dfree(c.gcnt);
+    dfree(c.gthr); dfree(c.gcnt); dfree(c.hopmap);
     dfree(c.bq); dfree(c.btq); dfree(c.bpart); dfree(c.bout);
     multi_free(c);
     if (c.h_query) (void)hipHostFree(c.h_query);
@@ -326,6 +327,7 @@ int query_impl(const mars_graph* gh, mars_ctx* ch, const float* h_q, const float
     const Graph& g = gh->g;
     Ctx& c = ch->c;
     MARS_CHECK(g.d == c.d, MARS_ERR_INVALID, "graph dim %d != context dim %d", g.d, c.d);
+    c.hit_n = 0;                           // set again once this query has BFS levels
     // nodes published so far: loaded once, every kernel of this query is bounded by it
     const int32_t n_live = n_pin >= 0 ? n_pin : __atomic_load_n(&g.n, __ATOMIC_ACQUIRE);
     MARS_CHECK(n_live <= c.max_nodes, MARS_ERR_CAPACITY, "graph has %d nodes, context sized for %d", n_live,
@@ -360,6 +362,9 @@ int query_impl(const mars_graph* gh, mars_ctx* ch, const float* h_q, const float
         MARS_TRY(certified_query(g, c, q, t_q, cfg, K, hops, rcap, n_live, out, cap, n_out, &answered, &h));
         c.last_certified = answered ? 1 : 0;
         if (answered) {
+            c.hit_vlist = c.mvlist;           // BFS levels for edge-hit counting
+            c.hit_vhop = c.mvhop;
+            c.hit_n = h.visited;
             c.last_k = h.n_seeds;
             c.last_visited = 0;               // the debug hooks describe fp32 scans only
             c.last_n = 0;
@@ -473,6 +478,11 @@ int query_impl(const mars_graph* gh, mars_ctx* ch, const float* h_q, const float
     *n_out = h.count;
     c.last_k = h.n_seeds;
     c.last_visited = scoped ? 0 : h.visited;
+    if (!scoped) {
+        c.hit_vlist = c.vlist;
+        c.hit_vhop = c.vhop;
+        c.hit_n = h.visited;
+    }
     if (stats) {
         mars_stats st{};
         if (timing) {
@@ -658,6 +668,7 @@ int mars_graph_create(const mars_graph_desc* d, mars_graph** out) {
 
 int mars_graph_destroy(mars_graph* gh) {
     if (!gh) return MARS_OK;
+    if (gh->own_ctx) (void)mars_ctx_destroy(gh->own_ctx);
     graph_free(gh->g);
     delete gh;
     return MARS_OK;
@@ -677,6 +688,7 @@ int mars_graph_set_csr(mars_graph* gh, int32_t ne, const int32_t* row, const int
         g.col = ncol;
         g.cap_e = int64_t(ne) + edge_room(g);
     }
+    MARS_TRY(reset_edge_hits(g));
     return load_csr(g, g.n, ne, row, col, hipMemcpyHostToDevice);
 }
 
@@ -1295,6 +1307,11 @@ int mars_query_global_batch_knn(const mars_graph* gh, mars_ctx* ch, const float*
     using clk = std::chrono::steady_clock;
     const auto t0 = clk::now();
     MARS_CHECK(gh && ch && Q >= 0 && knn_count >= 0 && Q + knn_count > 0, MARS_ERR_INVALID, "bad arguments");
+    // a batch leaves no single query's BFS levels for edge-hit counting
+    struct HitReset {
+        Ctx& c;
+        ~HitReset() { c.hit_n = 0; }
+    } hit_reset{ch->c};
     MARS_CHECK(Q == 0 || (dq && h_tq && cfg && n_out && cap >= 0 && (cap == 0 || out)), MARS_ERR_INVALID,
                "bad query arguments");
     const Graph& g = gh->g;

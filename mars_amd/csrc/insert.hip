@@ -116,15 +116,36 @@ __global__ void k_patch_data(PatchArgs a) {
     // relocations: one 64-lane wave per row (rows are short)
     const int64_t wave = tid >> 6, nwaves = stride >> 6;
     const int lane = int(threadIdx.x & 63u);
+    // Edge-hit counters move with their edges and leave zeros behind (every source slot
+    // is read by one thread only, and sources lie below the tail, destinations in it).
     for (int64_t r = wave; r < a.n_reloc; r += nwaves) {
         const int64_t src = a.reloc[3 * r], len = a.reloc[3 * r + 1], dst = a.reloc[3 * r + 2];
-        for (int64_t i = lane; i < len; i += 64) a.col[dst + i] = a.col[src + i];
+        for (int64_t i = lane; i < len; i += 64) {
+            a.col[dst + i] = a.col[src + i];
+            if (a.hits) {
+                a.hits[dst + i] = a.hits[src + i];
+                a.hits[src + i] = 0;
+            }
+        }
     }
     for (int64_t i = tid; i < a.n_tail; i += stride) {
         const int32_t v = a.tail[i];
-        if (v != kCopySlot) a.col[a.tail_base + i] = v;
+        if (v == kCopySlot) continue;
+        a.col[a.tail_base + i] = v;
+        if (a.hits) {
+            const int64_t src = a.tail_src ? a.tail_src[i] : -1;
+            int32_t h = 0;
+            if (src >= 0) {
+                h = a.hits[src];
+                a.hits[src] = 0;
+            }
+            a.hits[a.tail_base + i] = h;
+        }
     }
-    for (int64_t i = tid; i < a.n_app; i += stride) a.col[a.app[2 * i]] = int32_t(a.app[2 * i + 1]);
+    for (int64_t i = tid; i < a.n_app; i += stride) {
+        a.col[a.app[2 * i]] = int32_t(a.app[2 * i + 1]);
+        if (a.hits) a.hits[a.app[2 * i]] = 0;
+    }
 }
 
 __global__ void k_patch_rows(PatchArgs a) {
@@ -234,11 +255,14 @@ __global__ void k_gather_rows(const int32_t* __restrict__ col, const int64_t* __
 struct Patch {
     std::vector<int64_t> reloc, app, rows;
     std::vector<int32_t> tail;
+    std::vector<int64_t> tail_src;   // with edge-hit counters: source slot of each tail entry (-1 new)
     int64_t base = 0, cursor = 0, added = 0;
     int32_t max_deg = 0, n_reloc = 0, n_inplace = 0;
+    bool track_src = false;
     int64_t place(int64_t cap) {
         const int64_t at = cursor;
         tail.resize(size_t(at + cap - base), -1);
+        if (!tail_src.empty() || track_src) tail_src.resize(tail.size(), -1);
         cursor += cap;
         return at;
     }
@@ -249,7 +273,8 @@ struct Patch {
 int commit_patch(Graph& g, Patch& p, hipStream_t s) {
     const size_t b_reloc = p.reloc.size() * sizeof(int64_t), b_app = p.app.size() * sizeof(int64_t);
     const size_t b_rows = p.rows.size() * sizeof(int64_t), b_tail = p.tail.size() * sizeof(int32_t);
-    const size_t total = b_reloc + b_app + b_rows + b_tail + 64;
+    const size_t b_src = p.tail_src.size() * sizeof(int64_t);
+    const size_t total = b_reloc + b_app + b_rows + b_tail + b_src + 96;   // + 16-byte padding of 5 pieces
     MARS_TRY(grow_pinned<char>(&g.ins_pin, &g.ins_pin_bytes, total));
     MARS_TRY(grow_device(&g.ins_dev, &g.ins_dev_bytes, total));
     char* pin = static_cast<char*>(g.ins_pin);
@@ -263,6 +288,7 @@ int commit_patch(Graph& g, Patch& p, hipStream_t s) {
     };
     const size_t o_reloc = put(p.reloc.data(), b_reloc), o_app = put(p.app.data(), b_app);
     const size_t o_rows = put(p.rows.data(), b_rows), o_tail = put(p.tail.data(), b_tail);
+    const size_t o_src = p.tail_src.empty() ? 0 : put(p.tail_src.data(), b_src);
     MARS_HIP(hipMemcpyAsync(dev, pin, off, hipMemcpyHostToDevice, s));
     PatchArgs pa{};
     pa.col = g.col; pa.ro = g.ro; pa.rcap = g.rcap;
@@ -271,6 +297,8 @@ int commit_patch(Graph& g, Patch& p, hipStream_t s) {
     pa.n_tail = int64_t(p.tail.size());
     pa.app = reinterpret_cast<const int64_t*>(dev + o_app); pa.n_app = int32_t(p.app.size() / 2);
     pa.rows = reinterpret_cast<const int64_t*>(dev + o_rows); pa.n_rows = int32_t(p.rows.size() / 3);
+    pa.hits = g.hits;
+    pa.tail_src = p.tail_src.empty() ? nullptr : reinterpret_cast<const int64_t*>(dev + o_src);
     const int64_t data_work = std::max<int64_t>({int64_t(pa.n_reloc) * 64, pa.n_tail, int64_t(pa.n_app)});
     MARS_LAUNCH(k_patch_data, dim3(patch_grid(data_work)), dim3(256), 0, s, pa);
     MARS_LAUNCH(k_patch_rows, dim3(patch_grid(pa.n_rows)), dim3(256), 0, s, pa);
@@ -359,7 +387,8 @@ int link_knn_apply(Graph& g, int32_t first, int32_t count, int32_t k, const int3
     p.base = align_up(g.e_used, kRegionAlign);
     p.cursor = p.base;
     p.max_deg = g.max_deg;
-    std::vector<int32_t> merged;
+    p.track_src = g.hits != nullptr;
+    std::vector<std::pair<int32_t, int64_t>> merged;   // (neighbour, col slot it came from or -1)
     for (size_t i = 0, j = 0; i < add.size(); i = j) {
         const int32_t r = add[i].first;
         while (j < add.size() && add[j].first == r) ++j;
@@ -377,12 +406,16 @@ int link_knn_apply(Graph& g, int32_t first, int32_t count, int32_t k, const int3
             }
             ++p.n_inplace;
         } else {
-            merged.assign(row.first, row.second);
-            for (size_t x = i; x < j; ++x) merged.push_back(add[x].second);
+            merged.clear();
+            for (int64_t x = 0; x < len; ++x) merged.emplace_back(row.first[x], start + x);
+            for (size_t x = i; x < j; ++x) merged.emplace_back(add[x].second, -1);
             std::sort(merged.begin(), merged.end());
             ncap = row_capacity(nlen);
             nstart = p.place(ncap);
-            std::memcpy(p.tail.data() + (nstart - p.base), merged.data(), merged.size() * sizeof(int32_t));
+            for (size_t x = 0; x < merged.size(); ++x) {
+                p.tail[size_t(nstart - p.base) + x] = merged[x].first;
+                if (p.track_src) p.tail_src[size_t(nstart - p.base) + x] = merged[x].second;
+            }
             ++p.n_reloc;
         }
         p.rows.push_back(r); p.rows.push_back((nlen << 32) | int64_t(uint32_t(nstart))); p.rows.push_back(ncap);

@@ -160,6 +160,12 @@ struct Graph {
     float* ins_tq = nullptr;             // zero query times (no decay)
     int32_t ins_cap_q = 0;
     hipEvent_t ins_ev[2] = {nullptr, nullptr};
+    // importance and edge-hit counters (allocated on request, under the graph mutex)
+    float* imp = nullptr;                // cap_n: importance of each node
+    int32_t* hits = nullptr;             // cap_e: BFS hits per col slot; slots no row uses hold 0
+    int32_t* imp_ids = nullptr;          // device copy of host-supplied boost ids
+    int64_t imp_ids_cap = 0;
+    unsigned long long* sweep_cnt = nullptr;   // edges counted by the maintenance sweep
 };
 
 // Result staging written by the finalize / episode kernels straight into
@@ -216,6 +222,12 @@ struct Ctx {
     int32_t last_k = 0;
     int32_t last_visited = 0;      // visit-list length of the last global query
     int32_t last_certified = 0;    // the last global query took the certified path
+    // BFS levels of the last global query (edge-hit counting): its visit list
+    const int32_t* hit_vlist = nullptr;
+    const int32_t* hit_vhop = nullptr;
+    int32_t hit_n = 0;
+    uint64_t* hopmap = nullptr;    // max_nodes: (stamp << 32) | hop of each visited node
+    uint32_t hop_stamp = 0;
     // batched scoring scratch (grown on demand)
     __half* bq = nullptr;          // queries in fp16
     float* btq = nullptr;          // query times
@@ -266,8 +278,11 @@ struct PatchArgs {
     int32_t n_app;
     const int64_t* rows;       // n_rows x {node, row word, capacity}
     int32_t n_rows;
+    int32_t* hits;             // null: no edge-hit counters; else they follow the edges
+    const int64_t* tail_src;   // null, or per tail slot: the col slot its edge came from (-1: new)
 };
 int graph_insert_free(Graph& g);     // insert scratch of a graph
+int reset_edge_hits(Graph& g);       // zero counters sized to cap_e (maintain.hip), if enabled
 // Edges between node first + i and each listed neighbour knn[i * k + j] (-1 skipped),
 // both directions, merged into the rows (insert.hip). Caller holds the graph mutex.
 int link_knn_apply(Graph& g, int32_t first, int32_t count, int32_t k, const int32_t* knn, hipStream_t s,
@@ -528,5 +543,7 @@ int launch_multi_select(const MultiArgs& a, hipStream_t s);
 struct mars_graph {
     mars::Graph g;
     mutable std::mutex mu;   // serialises inserts, CSR / episode / fp16 replacement and downloads
+    mars_ctx* own_ctx = nullptr;   // the graph's own query context (novelty without a caller context)
+    std::mutex own_mu;
 };
 struct mars_ctx { mars::Ctx c; };

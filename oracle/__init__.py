@@ -66,6 +66,10 @@ def _load():
         "oracle_knn": (None, [VP, I64, I32, VP, I32, I32, VP, VP]),
         "oracle_insert_edges": (I64, [I32, VP, VP, I32, VP, VP, I32, VP, VP]),
         "oracle_link_edges": (I64, [I32, VP, VP, I32, I32, VP, I32, VP, VP]),
+        "oracle_importance_update": (None, [VP, I32, VP, I32, C.c_float, C.c_float, C.c_float]),
+        "oracle_novelty": (C.c_double, [C.POINTER(OracleGraph), VP, C.POINTER(C.c_double)]),
+        "oracle_edge_hits": (None, [VP, VP, I32, VP, VP]),
+        "oracle_maintain": (I32, [VP, I64, I32]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -275,3 +279,38 @@ def insert_edges(row, col, n_old: int, n_new: int, ep_new, knn_ids):
     out_col = np.empty(max(e, 1), np.int32)
     lib.oracle_insert_edges(n_old, _p(row), _p(col), n_new, _p(ep), _p(kn), k, _p(out_row), _p(out_col))
     return out_row, out_col[:e]
+
+
+def importance_update(imp, ids, boost: float = 0.1, decay_rate: float = 0.001, max_imp: float = 5.0, n=None):
+    """update_importance on a copy of imp (float32); nodes [0, n) decay (default all)."""
+    out = np.array(imp, np.float32, copy=True)
+    ids = np.ascontiguousarray(ids, np.int32)
+    lib.oracle_importance_update(_p(out), len(out) if n is None else int(n), _p(ids) if len(ids) else None,
+                                 len(ids), boost, decay_rate, max_imp)
+    return out
+
+
+def novelty(g: "Graph", q):
+    """(max_i <E_i, q> floored at -1 (0 if empty), max_i sum_d |E_id q_d|)."""
+    q = np.ascontiguousarray(q, np.float32)
+    sc = C.c_double()
+    gc = g.c()
+    v = lib.oracle_novelty(C.byref(gc), _p(q), C.byref(sc))
+    return v, sc.value
+
+
+def edge_hits(row, col, hop_by_node, hits=None):
+    """hits (+)= count_edge_hits over a CSR for the BFS levels hop_by_node (-1 unvisited)."""
+    row = np.ascontiguousarray(row, np.int32)
+    col = np.ascontiguousarray(col, np.int32)
+    hop = np.ascontiguousarray(hop_by_node, np.int32)
+    out = np.zeros(len(col), np.int32) if hits is None else np.array(hits, np.int32, copy=True)
+    lib.oracle_edge_hits(_p(row), _p(col) if len(col) else None, len(row) - 1, _p(hop), _p(out) if len(out) else None)
+    return out
+
+
+def maintain(hits, min_hits: int = 0):
+    """(edges with hits <= min_hits, the counters after the reset)."""
+    h = np.array(hits, np.int32, copy=True)
+    low = lib.oracle_maintain(_p(h) if len(h) else None, len(h), int(min_hits))
+    return int(low), h

@@ -551,5 +551,82 @@ int64_t oracle_link_edges(int32_t n, const int32_t* row, const int32_t* col, int
     return e;
 }
 
+// ---------------------------------------------------------------------------
+// Importance update: update_importance, memory_cuda.cu:1484-1527. fp32 as the
+// reference: retain = 1.0f - decay_rate; every node i < n: imp[i] = imp[i] * retain
+// (importance_decay_kernel :1486-1491); then each listed id, in list order:
+// imp[id] = fminf(imp[id] + boost, max_imp) (importance_boost_kernel :1494-1505).
+// Ids < 0 are skipped (:1502); ids >= n are skipped here (the reference writes out of
+// bounds). A repeated id is boosted once per occurrence, in order (the reference's
+// threads race on it).
+// ---------------------------------------------------------------------------
+void oracle_importance_update(float* imp, int32_t n, const int32_t* ids, int32_t n_ids, float boost,
+                              float decay_rate, float max_imp) {
+    const float retain = 1.0f - decay_rate;
+    for (int32_t i = 0; i < n; ++i) imp[i] = imp[i] * retain;
+    for (int32_t t = 0; t < n_ids; ++t) {
+        const int32_t id = ids[t];
+        if (id < 0 || id >= n) continue;
+        const float sum = imp[id] + boost;
+        imp[id] = std::fmin(sum, max_imp);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Novelty: compute_novelty, memory_cuda.cu:1547-1596: max over i < N of <E_i, q>
+// (fp64 here), starting from -1 (:1589), and 0 when N <= 0 (:1570). *scale gets
+// max_i sum_d |E_id q_d|, which bounds the fp32 rounding error of any one dot.
+// ---------------------------------------------------------------------------
+double oracle_novelty(const oracle_graph* g, const float* q, double* scale) {
+    const int64_t N = g->num_nodes, D = g->dim;
+    if (scale) *scale = 0.0;
+    if (N <= 0) return 0.0;
+    double best = -1.0, sc = 0.0;
+#pragma omp parallel for reduction(max : best, sc) schedule(static)
+    for (int64_t i = 0; i < N; ++i) {
+        const float* e = g->emb + i * D;
+        double s = 0.0, a = 0.0;
+        for (int64_t d = 0; d < D; ++d) {
+            const double p = double(e[d]) * double(q[d]);
+            s += p;
+            a += std::fabs(p);
+        }
+        best = std::max(best, s);
+        sc = std::max(sc, a);
+    }
+    if (scale) *scale = sc;
+    return best;
+}
+
+// ---------------------------------------------------------------------------
+// Edge hits: count_edge_hits_kernel, memory_cuda.cu:1612-1632. hop[v] is the BFS
+// level of node v (-1 = unvisited; hop_by_node of oracle_bfs). For every node v with
+// hop[v] > 0 (:1619) and every edge e of v (:1621-1630): hits[e] += 1 when
+// hop[col[e]] == hop[v] - 1.
+// ---------------------------------------------------------------------------
+void oracle_edge_hits(const int32_t* row, const int32_t* col, int32_t n, const int32_t* hop, int32_t* hits) {
+    for (int32_t v = 0; v < n; ++v) {
+        const int32_t h = hop[v];
+        if (h <= 0) continue;
+        for (int32_t e = row[v]; e < row[v + 1]; ++e) {
+            const int32_t u = col[e];
+            if (u >= 0 && u < n && hop[u] == h - 1) ++hits[e];
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Maintenance sweep: maintain_graph, memory_cuda.cu:1636-1658: the number of edges
+// with hits <= min_hits (:1647-1649), then every counter reset to 0 (:1652).
+// ---------------------------------------------------------------------------
+int32_t oracle_maintain(int32_t* hits, int64_t n_edges, int32_t min_hits) {
+    int32_t low = 0;
+    for (int64_t e = 0; e < n_edges; ++e) {
+        if (hits[e] <= min_hits) ++low;
+        hits[e] = 0;
+    }
+    return low;
+}
+
 }  // extern "C"
 
