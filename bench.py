@@ -72,6 +72,57 @@ def checkpoint_pass(args, mars_amd, dg):
     return res
 
 
+def maintenance_pass(mars_amd, dg, ctx, dq, first, count, D, gcfg, pctl, reps=200):
+    """Importance update (decay every node + 10 boosts), novelty (top-1 raw dot on the
+    graph's own certified context), edge-hit counting after a depth-2 global query, and
+    the maintenance sweep; host wall time of each synchronous call."""
+    from mars_amd import RetrievalStats
+    dg.refresh()
+    n = dg.num_nodes
+    mars_amd.init_importance(dg)
+    mars_amd.init_edge_hits(dg)
+    rng = np.random.default_rng(5)
+    t_imp, t_nov, t_hit, t_q = [], [], [], []
+    for r in range(reps + 10):
+        ids = rng.integers(0, n, 10).astype(np.int32)
+        t0 = time.perf_counter()
+        mars_amd.update_importance(dg, ids)
+        t1 = time.perf_counter()
+        qp = dq.ptr + (first + r % count) * D * 4
+        mars_amd.compute_novelty(dg, device_ptr=qp)
+        t2 = time.perf_counter()
+        mars_amd.query_memory_fast_device(dg, ctx, qp, 600.0, gcfg, RetrievalStats())
+        t3 = time.perf_counter()
+        mars_amd.count_edge_hits(dg, ctx)
+        t4 = time.perf_counter()
+        if r >= 10:
+            t_imp.append((t1 - t0) * 1e6)
+            t_nov.append((t2 - t1) * 1e6)
+            t_q.append((t3 - t2) * 1e6)
+            t_hit.append((t4 - t3) * 1e6)
+    hits = mars_amd.read_edge_hits(dg)
+    touched = int(np.count_nonzero(hits))
+    t0 = time.perf_counter()
+    low = mars_amd.maintain_graph(dg, 0)
+    t_sweep = (time.perf_counter() - t0) * 1e6
+    t_again = []
+    for _ in range(20):                      # the same pass over counters already zero
+        t0 = time.perf_counter()
+        mars_amd.maintain_graph(dg, 0)
+        t_again.append((time.perf_counter() - t0) * 1e6)
+    res = dict(nodes=n, edges=int(len(hits)),
+               importance_update=dict(p50_us=pctl(t_imp, .5), p99_us=pctl(t_imp, .99), bytes=8 * n),
+               novelty=dict(p50_us=pctl(t_nov, .5), p99_us=pctl(t_nov, .99), path="certified fp16 scan, top-1"),
+               edge_hit_count=dict(p50_us=pctl(t_hit, .5), p99_us=pctl(t_hit, .99),
+                                   after="depth-2 global query (fp32 path)"),
+               maintenance_sweep=dict(us=t_sweep, low_utility=low, edges_hit=touched,
+                                      repeat_p50_us=pctl(t_again, .5)))
+    log(f"maintenance at N={n:,}: importance update p50 {res['importance_update']['p50_us']:.1f} us, novelty p50 "
+        f"{res['novelty']['p50_us']:.1f} us, edge-hit count p50 {res['edge_hit_count']['p50_us']:.1f} us, sweep "
+        f"{t_sweep:.1f} us ({low:,} of {len(hits):,} edges never hit over {reps + 10} queries)")
+    return res
+
+
 def tiled_pass(args, mars_amd, corpus, c, qnodes, N, D, K, pctl, lat_resident, host_memory):
     """tiled_query contract over the corpus held in host RAM (pinned when the host grants it):
     tiles of --tiled-tile rows (the copy of tile i+1 overlaps the scan of tile i)."""
@@ -223,6 +274,10 @@ def main() -> int:
     ap.add_argument("--stream-insert-batch", type=int, default=10, help="nodes per insert call when streaming")
     ap.add_argument("--knn-block", type=int, default=0,
                     help="k-NN of the NSN graph within blocks of this many consecutive ids (0: exact, all pairs)")
+    ap.add_argument("--no-maintenance", action="store_true",
+                    help="skip the importance / novelty / edge-hit maintenance pass")
+    ap.add_argument("--maintenance-only", action="store_true",
+                    help="only the maintenance pass (for rocprofv3)")
     ap.add_argument("--checkpoint-dir", default="",
                     help="also time a MARS v1 checkpoint of the device graph to this directory and its reload")
     args = ap.parse_args()
@@ -278,6 +333,13 @@ def main() -> int:
     dq = mars_amd.DeviceBuffer.from_array(c.embeddings[qnodes])
 
     gcfg = RetrievalConfig(top_k=K, bfs_max_hops=2, time_decay_lambda=corpus.DECAY_LAMBDA, bfs_score_decay=0.5)
+    if args.maintenance_only:
+        m = maintenance_pass(mars_amd, dg, ctx, dq, 0, nq, D, gcfg, pctl)
+        dq.free()
+        mars_amd.destroy_query_context(ctx)
+        mars_amd.free_device(dg)
+        print(json.dumps({"maintenance": m}), flush=True)
+        return 0
     off = csr.ep_csr_offsets
 
     def ep_cfgs(nodes):
@@ -436,6 +498,8 @@ def main() -> int:
         out["streaming"] = dict(base_nodes=N, insert_batch=args.stream_insert_batch, insert_rate_target=2000.0,
                                 query_rate_target=1000.0, knn_k=args.knn_k,
                                 latency="completion - arrival (queueing included)", runs=runs)
+    if not args.profile_only and not args.no_maintenance:
+        out["maintenance"] = maintenance_pass(mars_amd, dg, ctx, dq, W, S - W, D, gcfg, pctl)
 
     achieved = bytes_f16 / float(kern_c.mean()) / 1e3       # GB/s of the certified path's fp16 scan
     achieved32 = bytes_f32 / float(kern_g.mean()) / 1e3

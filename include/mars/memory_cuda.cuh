@@ -16,7 +16,8 @@
 //      malformed episode inputs are silent no-ops and an inactive episode scope
 //      falls back to Global, as in the reference (memory_cuda.cu:814-855, 1163-1171).
 //  The importance / novelty / graph-maintenance entry points (lines 234-272) are
-//  not part of this API (no driver calls them).
+//  served too. They run synchronously; the stream argument is accepted and unused.
+//  d_importance / d_edge_hits stay null (the arrays live in the library's graph).
 // ============================================================================
 #ifndef MEMORY_CUDA_CUH
 #define MEMORY_CUDA_CUH
@@ -44,8 +45,8 @@ struct DeviceMemoryGraph {
     int32_t* d_ep_csr_members = nullptr;
     int32_t episode_num_episodes = 0;
     int32_t episode_csr_member_total = 0;
-    float* d_importance = nullptr;         // never allocated here
-    int32_t* d_edge_hits = nullptr;        // never allocated here
+    float* d_importance = nullptr;         // null: the library's graph holds the array
+    int32_t* d_edge_hits = nullptr;        // null: the library's graph holds the array
     int64_t* d_row_words = nullptr;        // per node: (row length << 32) | row start in col
     mars_graph* handle = nullptr;
 };
@@ -112,5 +113,19 @@ void destroy_query_context(QueryContext& ctx);
 
 std::vector<QueryResult> query_memory_fast(const DeviceMemoryGraph& dg, QueryContext& ctx, const float* h_query,
                                            float query_timestamp, const RetrievalConfig& cfg, RetrievalStats& stats);
+
+// ---- importance, novelty gate, adaptive graph maintenance (lines 234-270) ----------
+void init_importance(DeviceMemoryGraph& dg);
+// d_result_ids: device memory (mars_device_alloc), as the reference.
+void update_importance(DeviceMemoryGraph& dg, const int32_t* d_result_ids, int32_t n_results, float boost = 0.1f,
+                       float decay_rate = 0.001f, float max_importance = 5.0f, void* stream = nullptr);
+// d_query: device memory. Max over the nodes of <E_i, q>, at least -1.
+float compute_novelty(const DeviceMemoryGraph& dg, const float* d_query, void* stream = nullptr);
+void init_edge_hits(DeviceMemoryGraph& dg);
+int32_t maintain_graph(DeviceMemoryGraph& dg, int32_t min_hits = 0, int32_t window_queries = 1000,
+                       void* stream = nullptr);
+// Extension (the reference has count_edge_hits_kernel, memory_cuda.cu:1612-1632, and no
+// host call for it): count the edges the BFS of ctx's last global query walked.
+void count_edge_hits(DeviceMemoryGraph& dg, QueryContext& ctx);
 
 #endif  // MEMORY_CUDA_CUH

@@ -96,6 +96,34 @@ DeviceMemoryGraph upload_to_device(const MemoryGraph& h, int32_t capacity_nodes)
     return d;
 }
 
+void init_importance(DeviceMemoryGraph& dg) { die_on(mars_importance_init(dg.handle), "init_importance"); }
+
+void update_importance(DeviceMemoryGraph& dg, const int32_t* d_result_ids, int32_t n_results, float boost,
+                       float decay_rate, float max_importance, void* /*stream*/) {
+    const int rc = mars_importance_update(dg.handle, d_result_ids, n_results > 0 ? n_results : 0, 1, boost,
+                                          decay_rate, max_importance);
+    if (rc == MARS_ERR_UNSUPPORTED) return;          // memory_cuda.cu:1510: no importance array, no-op
+    die_on(rc, "update_importance");
+}
+
+float compute_novelty(const DeviceMemoryGraph& dg, const float* d_query, void* /*stream*/) {
+    float v = 0.0f;
+    die_on(mars_novelty(dg.handle, nullptr, nullptr, d_query, &v), "compute_novelty");
+    return v;
+}
+
+void init_edge_hits(DeviceMemoryGraph& dg) { die_on(mars_edge_hits_init(dg.handle), "init_edge_hits"); }
+
+int32_t maintain_graph(DeviceMemoryGraph& dg, int32_t min_hits, int32_t window_queries, void* /*stream*/) {
+    int32_t low = 0;
+    die_on(mars_graph_maintain(dg.handle, min_hits, window_queries, &low), "maintain_graph");
+    return low;
+}
+
+void count_edge_hits(DeviceMemoryGraph& dg, QueryContext& ctx) {
+    die_on(mars_edge_hits_count(dg.handle, ctx.handle), "count_edge_hits");
+}
+
 void free_device(DeviceMemoryGraph& d) {
     if (d.handle) mars_graph_destroy(d.handle);
     d = DeviceMemoryGraph{};

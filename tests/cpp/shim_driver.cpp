@@ -13,11 +13,16 @@
 //                                     and "global ..." lines
 //         shim_driver tiled N SEED Q  tiled_query over the host corpus (tiles of N/7):
 //                                     "tiled <node> id:score:mod ..."
+//         shim_driver maintain N SEED Q  the query corpus with importance and edge hits:
+//                                     per query "novelty <node> <max dot>" and "ids <node>
+//                                     <result ids>"; then "importance <fp32 bits in hex>"
+//                                     and "low_utility <maintain_graph(dg, 0)>"
 // ============================================================================
 #include "mars/memory_cuda.cuh"
 #include "mars/memory_graph.h"
 #include "mars/streaming.h"
 #include "mars/tiled_query.h"
+#include "mars_amd.h"
 #include "mars_corpus.h"
 
 #include <cstdio>
@@ -166,8 +171,9 @@ int main(int argc, char** argv) {
         return stream_check(std::atoi(argv[2]), std::strtoull(argv[3], nullptr, 10));
     if (argc >= 5 && std::strcmp(argv[1], "tiled") == 0)
         return tiled_check(std::atoi(argv[2]), std::strtoull(argv[3], nullptr, 10), std::atoi(argv[4]));
-    if (argc < 5 || std::strcmp(argv[1], "query") != 0) {
-        std::fprintf(stderr, "usage: shim_driver host | query N SEED Q\n");
+    const bool maintain = argc >= 5 && std::strcmp(argv[1], "maintain") == 0;
+    if (argc < 5 || (std::strcmp(argv[1], "query") != 0 && !maintain)) {
+        std::fprintf(stderr, "usage: shim_driver host | query N SEED Q | maintain N SEED Q\n");
         return 2;
     }
     const int32_t N = std::atoi(argv[2]);
@@ -203,6 +209,56 @@ int main(int argc, char** argv) {
 
     std::vector<int32_t> qn(static_cast<size_t>(Q));
     mars_corpus_pick_queries(g.modalities.data(), N, MOD_IMAGE, Q, seed + 1, qn.data());
+    if (maintain) {
+        // memory_cuda.cuh:234-270 in the order a serving loop would call them
+        init_importance(dg);
+        init_edge_hits(dg);
+        void* d_q = nullptr;
+        void* d_ids = nullptr;
+        if (mars_device_alloc(size_t(D) * sizeof(float), &d_q) != MARS_OK ||
+            mars_device_alloc(64 * sizeof(int32_t), &d_ids) != MARS_OK) {
+            std::printf("FAIL alloc\n");
+            return 1;
+        }
+        for (int32_t i = 0; i < Q; ++i) {
+            const int32_t node = qn[size_t(i)];
+            const float* q = &g.embeddings[size_t(node) * D];
+            mars_copy_to_device(d_q, q, size_t(D) * sizeof(float));
+            std::printf("novelty %d %.9g\n", node, double(compute_novelty(dg, static_cast<const float*>(d_q))));
+            RetrievalConfig cfg;
+            cfg.top_k = 10;
+            cfg.max_results_returned = 15;
+            cfg.time_decay_lambda = 0.1f;
+            RetrievalStats stats;
+            auto res = query_memory_fast(dg, ctx, q, 600.0f, cfg, stats);
+            count_edge_hits(dg, ctx);
+            std::vector<int32_t> ids;
+            for (const auto& r : res) ids.push_back(r.node_id);
+            std::printf("ids %d", node);
+            for (int32_t id : ids) std::printf(" %d", id);
+            std::printf("\n");
+            mars_copy_to_device(d_ids, ids.data(), ids.size() * sizeof(int32_t));
+            update_importance(dg, static_cast<const int32_t*>(d_ids), int32_t(ids.size()));
+        }
+        std::vector<float> imp(static_cast<size_t>(N));
+        if (mars_importance_read(dg.handle, imp.data(), 0, N) != MARS_OK) {
+            std::printf("FAIL importance read\n");
+            return 1;
+        }
+        std::printf("importance");
+        for (const float v : imp) {
+            uint32_t u;
+            std::memcpy(&u, &v, 4);
+            std::printf(" %08x", u);
+        }
+        std::printf("\n");
+        std::printf("low_utility %d\n", maintain_graph(dg, 0));
+        mars_device_free(d_q);
+        mars_device_free(d_ids);
+        destroy_query_context(ctx);
+        free_device(dg);
+        return 0;
+    }
     for (int32_t i = 0; i < Q; ++i) {
         const int32_t node = qn[size_t(i)];
         for (int scope = 0; scope < 2; ++scope) {

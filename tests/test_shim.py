@@ -99,3 +99,43 @@ def test_shim_tiled_query_matches_oracle():
             abs(fin[a] - fin[b]) <= 2e-5 * max(scale[a], 1e-30) for a, b in zip([g[0] for g in got], ids))
         for (i, s, m), w in zip(got, sc):
             assert abs(s - fin[i]) <= 1e-5 * max(abs(fin[i]), scale[i]) and m == int(c.modalities[i])
+
+
+@pytest.mark.gpu
+def test_shim_maintenance_matches_oracle():
+    """init_importance / update_importance / compute_novelty / init_edge_hits /
+    maintain_graph (mars/memory_cuda.cuh, the reference's lines 234-270) and the
+    count_edge_hits extension, driven from C++ as a serving loop would: novelty within the
+    fp32 dot bound, importance bit for bit, the low-utility count exact, against the
+    oracle replaying the same queries."""
+    import oracle
+    from conftest import RTOL_F32
+    from mars_amd import corpus
+    n, seed, q = 3000, 7, 8
+    r = subprocess.run([str(DRIVER), "maintain", str(n), str(seed), str(q)], capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == 0, r.stderr
+    c = corpus.nsn_graph(corpus.make_corpus(n, 768, seed=seed))
+    og = oracle.make_graph(c.embeddings, c.modalities, c.timestamps, c.row_offsets, c.col_indices, c.episode_ids)
+    lines = r.stdout.splitlines()
+    nov = [ln.split() for ln in lines if ln.startswith("novelty")]
+    ids = [ln.split() for ln in lines if ln.startswith("ids")]
+    assert len(nov) == len(ids) == q
+    imp = np.ones(n, np.float32)
+    hits = np.zeros(len(c.col_indices), np.int32)
+    cfg = oracle.config(10, 2, 0.1, 0.5, -1, 15)
+    for nv, il in zip(nov, ids):
+        node = int(nv[1])
+        want, scale = oracle.novelty(og, c.embeddings[node])
+        assert abs(float(nv[2]) - want) <= RTOL_F32 * max(scale, abs(want))
+        ref = oracle.query(og, c.embeddings[node], 600.0, cfg)
+        got = [int(x) for x in il[2:]]
+        assert got == [w[0] for w in ref["results"]]
+        b = oracle.bfs(c.row_offsets, c.col_indices, ref["final"], ref["seeds"], ref["seed_vals"], 2, 0.5)
+        hits = oracle.edge_hits(c.row_offsets, c.col_indices, b["hop_by_node"], hits)
+        imp = oracle.importance_update(imp, got)
+    line = next(ln for ln in lines if ln.startswith("importance"))
+    got_bits = np.array([int(x, 16) for x in line.split()[1:]], np.uint32)
+    np.testing.assert_array_equal(got_bits, imp.view(np.uint32))
+    low = int(next(ln for ln in lines if ln.startswith("low_utility")).split()[1])
+    assert low == oracle.maintain(hits, 0)[0]
