@@ -4,11 +4,12 @@
 //  (lines 17-93) so that code written against it compiles unchanged.
 //
 //  Provided by libmars_amd: build_episode_csr (counting sort, identical bytes to
-//  src/memory_graph.cpp:12-44). The corpus generators and the NSN builder
-//  (MemoryGraph::synthetic, build_nsn_edges*, EmbodiedKidsBallCorpus::make,
-//  print_summary, device_bytes) are declared for source compatibility only: they
-//  belong to the reference's host code (src/memory_graph.cpp), which compiles
-//  against this header unchanged.
+//  src/memory_graph.cpp:12-44) and the NSN builder build_nsn_edges /
+//  build_nsn_edges_configurable (the same graph as src/memory_graph.cpp:95-189, edge
+//  for edge). The corpus generators (MemoryGraph::synthetic,
+//  EmbodiedKidsBallCorpus::make), print_summary and device_bytes are declared for
+//  source compatibility only: they belong to the reference's host code
+//  (src/memory_graph.cpp), which compiles against this header unchanged.
 // ============================================================================
 #ifndef MEMORY_GRAPH_H
 #define MEMORY_GRAPH_H

@@ -423,6 +423,23 @@ int mars_ctx_last_phases(mars_ctx* ctx, double* us, int32_t n);
 int mars_ctx_last_visited(mars_ctx* ctx, int32_t* h_ids, int32_t* h_hops, float* h_scores,
                           int32_t cap, int32_t* n_out);
 
+/* ---- NSN edges (host) -------------------------------------------------------------------
+ * MemoryGraph::build_nsn_edges_configurable (memory_graph.cpp:102-189): the same graph,
+ * edge for edge, as the reference built with the same C++ standard library (one
+ * std::mt19937 seeded 7, the same draws in the same order). phases: the NSNConfig
+ * enables as bits (MARS_NSN_ALL = the defaults). modalities (0..2) are needed for the
+ * bridges. Call with col == NULL for an upper bound of the edge count in *num_edges;
+ * then with col_cap >= that bound: row_offsets (n + 1) and col (rows ascending) are
+ * written and *num_edges is the count. */
+#define MARS_NSN_RING     0x1u
+#define MARS_NSN_SKIPS    0x2u
+#define MARS_NSN_HUBS     0x4u
+#define MARS_NSN_REWIRE   0x8u
+#define MARS_NSN_BRIDGES  0x10u
+#define MARS_NSN_ALL      0x1Fu
+int mars_nsn_edges(int32_t n, const int32_t* modalities, int32_t k, double p, uint32_t phases,
+                   int32_t* row_offsets, int32_t* col, int64_t col_cap, int64_t* num_edges);
+
 /* ---- importance, novelty gate, graph maintenance --------------------------------------
  * The reference's adjacent features (memory_cuda.cuh:234-270, memory_cuda.cu:1466-1658),
  * kept on the device graph. Each call is synchronous and serialised with inserts. */

@@ -232,6 +232,7 @@ SIGNATURES = {
     "mars_graph_read_ceiling": (C.c_int, [VP, I32, I32, C.POINTER(C.c_double)]),
     "mars_fnv1a64": (C.c_int, [VP, I64, C.POINTER(C.c_uint64)]),
     "mars_graph_set_rows": (C.c_int, [VP, I32, I32, VP, VP, VP]),
+    "mars_nsn_edges": (C.c_int, [I32, VP, I32, C.c_double, C.c_uint32, VP, VP, I64, C.POINTER(C.c_int64)]),
     "mars_importance_init": (C.c_int, [VP]),
     "mars_importance_update": (C.c_int, [VP, VP, I32, I32, C.c_float, C.c_float, C.c_float]),
     "mars_importance_read": (C.c_int, [VP, VP, I32, I32]),

@@ -105,3 +105,23 @@ def pick_queries(modalities: np.ndarray, n_queries: int, seed: int, modality: in
     check(lib.mars_corpus_pick_queries(_p(mods), len(mods), modality, n_queries, int(seed), _p(out)),
           "mars_corpus_pick_queries")
     return out
+
+
+NSN_RING, NSN_SKIPS, NSN_HUBS, NSN_REWIRE, NSN_BRIDGES = 0x1, 0x2, 0x4, 0x8, 0x10
+NSN_ALL = 0x1F
+
+
+def nsn_edges(modalities: np.ndarray, k: int = 6, p: float = 0.15, phases: int = NSN_ALL):
+    """MemoryGraph::build_nsn_edges_configurable (src/memory_graph.cpp:102-189): the
+    reference's 5-phase NSN graph over len(modalities) nodes. Returns (row_offsets, col)."""
+    mods = np.ascontiguousarray(modalities, np.int32)
+    n = len(mods)
+    bound = C.c_int64()
+    check(lib.mars_nsn_edges(n, _p(mods) if n else None, int(k), float(p), int(phases), None, None, 0,
+                             C.byref(bound)), "mars_nsn_edges")
+    row = np.zeros(n + 1, np.int32)
+    col = np.empty(max(bound.value, 1), np.int32)
+    ne = C.c_int64()
+    check(lib.mars_nsn_edges(n, _p(mods) if n else None, int(k), float(p), int(phases), _p(row), _p(col),
+                             len(col), C.byref(ne)), "mars_nsn_edges")
+    return row, col[: ne.value].copy()

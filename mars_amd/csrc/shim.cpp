@@ -96,6 +96,28 @@ DeviceMemoryGraph upload_to_device(const MemoryGraph& h, int32_t capacity_nodes)
     return d;
 }
 
+void MemoryGraph::build_nsn_edges(int32_t k, double p) {
+    NSNConfig cfg;
+    cfg.k = k;
+    cfg.p = p;
+    build_nsn_edges_configurable(cfg);
+}
+
+void MemoryGraph::build_nsn_edges_configurable(const NSNConfig& cfg) {
+    const uint32_t phases = (cfg.enable_ring ? MARS_NSN_RING : 0u) | (cfg.enable_skips ? MARS_NSN_SKIPS : 0u) |
+                            (cfg.enable_hubs ? MARS_NSN_HUBS : 0u) | (cfg.enable_rewire ? MARS_NSN_REWIRE : 0u) |
+                            (cfg.enable_bridges ? MARS_NSN_BRIDGES : 0u);
+    int64_t bound = 0, ne = 0;
+    die_on(mars_nsn_edges(num_nodes, modalities.data(), cfg.k, cfg.p, phases, nullptr, nullptr, 0, &bound),
+           "build_nsn_edges");
+    row_offsets.assign(size_t(num_nodes) + 1, 0);
+    col_indices.resize(size_t(std::max<int64_t>(bound, 1)));
+    die_on(mars_nsn_edges(num_nodes, modalities.data(), cfg.k, cfg.p, phases, row_offsets.data(),
+                          col_indices.data(), int64_t(col_indices.size()), &ne), "build_nsn_edges");
+    col_indices.resize(size_t(ne));
+    num_edges = int32_t(ne);
+}
+
 void init_importance(DeviceMemoryGraph& dg) { die_on(mars_importance_init(dg.handle), "init_importance"); }
 
 void update_importance(DeviceMemoryGraph& dg, const int32_t* d_result_ids, int32_t n_results, float boost,

@@ -93,6 +93,7 @@ def _load_ref():
         "ref_stream_flush": (I32, [VP, I32, I32, I32, VP, VP, VP]),
         "ref_graph_free": (None, [VP]),
         "ref_fnv1a": (C.c_uint64, [VP, C.c_size_t]),
+        "ref_nsn_edges": (I64, [I32, VP, I32, C.c_double, C.c_uint32, VP, VP, I64]),
         "ref_save_graph": (C.c_int, [C.c_char_p, I32, I32, I32, VP, VP, VP, VP, VP]),
         "ref_load_graph": (C.c_int, [C.c_char_p, C.POINTER(I32), C.POINTER(I32), C.POINTER(I32), VP, VP, VP, VP,
                                      VP]),

@@ -56,6 +56,29 @@ void* ref_synthetic_make(int32_t n_text, int32_t n_audio, int32_t n_image, int32
     return r;
 }
 
+// MemoryGraph::build_nsn_edges_configurable (memory_graph.cpp:102-189) over n nodes of
+// the given modalities; phases: ring 1, skips 2, hubs 4, rewire 8, bridges 16.
+// Returns the edge count; row (n + 1) and col (when large enough) receive the CSR.
+int64_t ref_nsn_edges(int32_t n, const int32_t* mods, int32_t k, double p, uint32_t phases, int32_t* row,
+                      int32_t* col, int64_t col_cap) {
+    MemoryGraph g;
+    g.num_nodes = n;
+    g.modalities.assign(mods, mods + n);
+    MemoryGraph::NSNConfig cfg;
+    cfg.k = k;
+    cfg.p = p;
+    cfg.enable_ring = phases & 1u;
+    cfg.enable_skips = phases & 2u;
+    cfg.enable_hubs = phases & 4u;
+    cfg.enable_rewire = phases & 8u;
+    cfg.enable_bridges = phases & 16u;
+    g.build_nsn_edges_configurable(cfg);
+    const int64_t e = int64_t(g.col_indices.size());
+    if (row) std::memcpy(row, g.row_offsets.data(), g.row_offsets.size() * 4);
+    if (col && e <= col_cap && e > 0) std::memcpy(col, g.col_indices.data(), size_t(e) * 4);
+    return e;
+}
+
 void ref_graph_sizes(void* h, int32_t* n, int32_t* dim, int32_t* num_edges) {
     auto* r = static_cast<RefGraph*>(h);
     *n = r->g.num_nodes; *dim = r->g.embedding_dim; *num_edges = int32_t(r->g.col_indices.size());
