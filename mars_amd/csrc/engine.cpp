@@ -18,7 +18,7 @@
 //  edges among the nodes present, the k nearest by cosine), an ADD of an existing id
 //  rewrites its row in place, and an id past the end first appends zero rows for the
 //  gap, as the reference's host graph grows; embeddings are L2-normalised on arrival
-//  (norm + 1e-8, as the reference). DELETE leaves a tombstone (zero row, timestamp -1).
+//  (fp32 sum of squares in order, sqrt + 1e-8, as the reference). DELETE leaves a tombstone (zero row, timestamp -1).
 //  QUERY runs the certified path (fp16 scan, answers bit-identical to the fp32 path;
 //  a query it cannot certify is answered by the fp32 path) with the reference server's
 //  decay 1e-8 and hop decay 0.5. SAVE / LOAD write and read MARS v1 checkpoints (the reference's are
@@ -114,6 +114,15 @@ private:
         i_ += size_t(end - p);
         return true;
     }
+    // array elements: decimal -> float in one rounding, as the reference's strtof
+    bool number_f(float* v) {
+        const char* p = s_.c_str() + i_;
+        char* end = nullptr;
+        *v = std::strtof(p, &end);
+        if (end == p) return false;
+        i_ += size_t(end - p);
+        return true;
+    }
     bool word(const char* w) {
         const size_t n = std::strlen(w);
         if (s_.compare(i_, n, w) != 0) return false;
@@ -130,10 +139,10 @@ private:
             ws();
             if (eat(']')) return true;
             for (;;) {
-                double v;
+                float v;
                 ws();
-                if (!number(&v)) return false;
-                a.push_back(float(v));
+                if (!number_f(&v)) return false;
+                a.push_back(v);
                 ws();
                 if (eat(']')) return true;
                 if (!eat(',')) return false;
@@ -220,10 +229,11 @@ struct Engine {
 
     // ADD: rows id (normalised) after zero rows for any gap; an existing id is rewritten.
     int add(int32_t id, int32_t modality, const std::vector<float>& e, float t) {
+        // L2 normalisation in fp32, accumulated in order, as the reference server's add_node
         std::vector<float> row(e);
-        double sq = 0.0;
-        for (const float x : e) sq += double(x) * double(x);
-        const float norm = float(std::sqrt(sq)) + 1e-8f;
+        float sq = 0.0f;
+        for (const float x : e) sq += x * x;
+        const float norm = std::sqrt(sq) + 1e-8f;
         for (float& x : row) x /= norm;
         if (g && id < n) return mars_graph_set_rows(g, id, 1, row.data(), &modality, &t);
         const int32_t first = g ? n : 0;

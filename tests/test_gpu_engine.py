@@ -46,8 +46,12 @@ class Engine:
 
 
 def normalised(e):
-    norm = np.float32(np.sqrt(np.sum(e.astype(np.float64) ** 2))) + np.float32(1e-8)
-    return (e / norm).astype(np.float32)
+    """fp32 sum of squares in order, sqrt, + 1e-8 (engine_server.cu:164-170)."""
+    sq = np.float32(0.0)
+    for x in e.astype(np.float32):
+        sq = np.float32(sq + np.float32(x * x))
+    norm = np.float32(np.sqrt(sq)) + np.float32(1e-8)
+    return (e.astype(np.float32) / norm).astype(np.float32)
 
 
 def replica(c):
