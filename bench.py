@@ -123,6 +123,54 @@ def maintenance_pass(mars_amd, dg, ctx, dq, first, count, D, gcfg, pctl, reps=20
     return res
 
 
+def engine_pass(n_nodes, n_queries, D, pctl):
+    """The JSON-line engine server (mars_amd/mars_engine) over its stdin/stdout pipe: n_nodes
+    ADDs of the benchmark corpus (each a one-node streaming insert with 8-NN edges once 8
+    nodes exist), then n_queries QUERYs (top-10, depth-2 BFS, certified path) timed from
+    the write of the request to the parsed response; requests are encoded before timing."""
+    import subprocess
+    from mars_amd import corpus as corp
+    exe = ROOT / "mars_amd" / "mars_engine"
+    c = corp.make_corpus(n_nodes, D, seed=11)
+    p = subprocess.Popen([str(exe), "--dim", str(D), "--capacity", str(n_nodes)], stdin=subprocess.PIPE,
+                         stdout=subprocess.PIPE, text=True, bufsize=1)
+
+    def call(line):
+        p.stdin.write(line)
+        p.stdin.flush()
+        return json.loads(p.stdout.readline())
+
+    adds = [json.dumps({"cmd": "ADD", "id": i, "modality": int(c.modalities[i]), "embedding": c.embeddings[i].tolist(),
+                        "timestamp": float(c.timestamps[i])}) + "\n" for i in range(n_nodes)]
+    t0 = time.perf_counter()
+    for line in adds:
+        r = call(line)
+        if r != {"ok": True}:
+            raise RuntimeError(f"engine ADD failed: {r}")
+    t_add = time.perf_counter() - t0
+    qn = corp.pick_queries(c.modalities, n_queries, seed=12)
+    qs = [json.dumps({"cmd": "QUERY", "embedding": c.embeddings[int(i)].tolist(), "top_k": 10, "bfs_max_hops": 2,
+                      "timestamp": float(corp.QUERY_TIME)}) + "\n" for i in qn]
+    lat, gpu = [], []
+    for line in qs:
+        t0 = time.perf_counter()
+        r = call(line)
+        lat.append((time.perf_counter() - t0) * 1e6)
+        gpu.append(r["gpu_ms"] * 1e3)
+        if len(r["results"]) != 10:
+            raise RuntimeError(f"engine QUERY returned {len(r['results'])} results")
+    st = call(json.dumps({"cmd": "STATS"}) + "\n")
+    call(json.dumps({"cmd": "SHUTDOWN"}) + "\n")
+    p.wait(timeout=60)
+    res = dict(nodes=n_nodes, edges=st["edges"], add_per_s=n_nodes / t_add,
+               query_rtt_p50_us=pctl(lat, .5), query_rtt_p99_us=pctl(lat, .99), query_gpu_p50_us=pctl(gpu, .5),
+               request_bytes=len(qs[0]))
+    log(f"engine server: {n_nodes:,} ADDs at {res['add_per_s']:.0f}/s ({st['edges']:,} undirected edges); QUERY "
+        f"round trip p50 {res['query_rtt_p50_us']:.0f} us p99 {res['query_rtt_p99_us']:.0f} us (GPU p50 "
+        f"{res['query_gpu_p50_us']:.0f} us, {len(qs[0]):,}-byte requests)")
+    return res
+
+
 def tiled_pass(args, mars_amd, corpus, c, qnodes, N, D, K, pctl, lat_resident, host_memory):
     """tiled_query contract over the corpus held in host RAM (pinned when the host grants it):
     tiles of --tiled-tile rows (the copy of tile i+1 overlaps the scan of tile i)."""
@@ -278,6 +326,8 @@ def main() -> int:
                     help="skip the importance / novelty / edge-hit maintenance pass")
     ap.add_argument("--maintenance-only", action="store_true",
                     help="only the maintenance pass (for rocprofv3)")
+    ap.add_argument("--engine-nodes", type=int, default=0,
+                    help="also drive the JSON-line engine server with this many ADDs and 500 QUERYs")
     ap.add_argument("--checkpoint-dir", default="",
                     help="also time a MARS v1 checkpoint of the device graph to this directory and its reload")
     args = ap.parse_args()
@@ -333,6 +383,8 @@ def main() -> int:
     dq = mars_amd.DeviceBuffer.from_array(c.embeddings[qnodes])
 
     gcfg = RetrievalConfig(top_k=K, bfs_max_hops=2, time_decay_lambda=corpus.DECAY_LAMBDA, bfs_score_decay=0.5)
+    if args.engine_nodes > 0 and args.maintenance_only:
+        print(json.dumps({"engine": engine_pass(args.engine_nodes, 500, D, pctl)}), flush=True)
     if args.maintenance_only:
         m = maintenance_pass(mars_amd, dg, ctx, dq, 0, nq, D, gcfg, pctl)
         dq.free()
@@ -498,6 +550,8 @@ def main() -> int:
         out["streaming"] = dict(base_nodes=N, insert_batch=args.stream_insert_batch, insert_rate_target=2000.0,
                                 query_rate_target=1000.0, knn_k=args.knn_k,
                                 latency="completion - arrival (queueing included)", runs=runs)
+    if args.engine_nodes > 0 and not args.profile_only:
+        out["engine_server"] = engine_pass(args.engine_nodes, 500, D, pctl)
     if not args.profile_only and not args.no_maintenance:
         out["maintenance"] = maintenance_pass(mars_amd, dg, ctx, dq, W, S - W, D, gcfg, pctl)
 
