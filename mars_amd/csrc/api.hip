@@ -511,7 +511,8 @@ int query_impl(const mars_graph* gh, mars_ctx* ch, const float* h_q, const float
 
 // Row ranges x query blocks for the batched scan: one 512-thread workgroup per CU
 // (256 CUs), all query blocks of a row range on one XCD.
-void batch_grid(int64_t n, int32_t q, int32_t* n_rranges, int32_t* n_qblocks, int64_t* rows_per_range) {
+void batch_grid(int64_t n, int32_t q, int32_t* n_rranges, int32_t* n_qblocks, int64_t* rows_per_range,
+                int32_t max_ranges) {
     // n_qblocks counts 64-query blocks (the layout of the partial keys) for both kernels
     const int32_t qblocks = (q + 63) / 64;
     const bool gemm = batch_uses_gemm(q);
@@ -519,6 +520,7 @@ void batch_grid(int64_t n, int32_t q, int32_t* n_rranges, int32_t* n_qblocks, in
     const int64_t align = gemm ? 64 : 16;                          // rows per tile
     int32_t rr = std::max(8, (256 / std::max(tiles, 1)) / 8 * 8);
     const int64_t max_rr = std::max<int64_t>(1, (n + align - 1) / align);   // at least one tile per range
+    if (rr > max_ranges) rr = std::max(1, max_ranges);
     if (rr > max_rr) rr = int32_t(max_rr);
     *n_qblocks = qblocks;
     *rows_per_range = ((n + rr - 1) / rr + align - 1) / align * align;

@@ -80,7 +80,9 @@ void dfree(T*& p) {
 }
 
 // Row ranges x query blocks of the batched scan (defined in api.hip).
-void batch_grid(int64_t n, int32_t q, int32_t* n_rranges, int32_t* n_qblocks, int64_t* rows_per_range);
+// max_ranges caps the row ranges (workgroups per 64-query block).
+void batch_grid(int64_t n, int32_t q, int32_t* n_rranges, int32_t* n_qblocks, int64_t* rows_per_range,
+                int32_t max_ranges = 256);
 
 constexpr int kMaxK = 64;              // seeds per query (wave-held list), as MAX_TOP_K
 constexpr int kSortCap = 8192;         // results sorted in LDS by the finalize kernel
