@@ -545,7 +545,9 @@ int launch_multi_select(const MultiArgs& a, hipStream_t s);
 struct mars_graph {
     mars::Graph g;
     mutable std::mutex mu;   // serialises inserts, CSR / episode / fp16 replacement and downloads
-    mars_ctx* own_ctx = nullptr;   // the graph's own query context (novelty without a caller context)
-    std::mutex own_mu;
+    // the graph's own query context (novelty without a caller context): a cache created
+    // on first use, so calls on a const graph may create it
+    mutable mars_ctx* own_ctx = nullptr;
+    mutable std::mutex own_mu;
 };
 struct mars_ctx { mars::Ctx c; };

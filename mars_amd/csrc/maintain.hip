@@ -251,9 +251,8 @@ int mars_importance_read(const mars_graph* gh, float* h_out, int32_t first, int3
     return MARS_OK;
 }
 
-int mars_novelty(const mars_graph* gc, mars_ctx* ctx, const float* h_q, const float* d_q, float* max_sim) {
-    MARS_CHECK(gc && max_sim && (h_q || d_q), MARS_ERR_INVALID, "null argument");
-    auto* gh = const_cast<mars_graph*>(gc);
+int mars_novelty(const mars_graph* gh, mars_ctx* ctx, const float* h_q, const float* d_q, float* max_sim) {
+    MARS_CHECK(gh && max_sim && (h_q || d_q), MARS_ERR_INVALID, "null argument");
     *max_sim = 0.0f;
     std::unique_lock<std::mutex> own;
     if (!ctx) {
@@ -272,8 +271,8 @@ int mars_novelty(const mars_graph* gc, mars_ctx* ctx, const float* h_q, const fl
     cfg.time_decay_lambda = 0.0f;
     mars_query_result r{};
     int32_t count = 0;
-    const int rc = h_q ? mars_query(gc, ctx, h_q, 0.0f, &cfg, &r, 1, &count, nullptr)
-                       : mars_query_device(gc, ctx, d_q, 0.0f, &cfg, &r, 1, &count, nullptr);
+    const int rc = h_q ? mars_query(gh, ctx, h_q, 0.0f, &cfg, &r, 1, &count, nullptr)
+                       : mars_query_device(gh, ctx, d_q, 0.0f, &cfg, &r, 1, &count, nullptr);
     MARS_TRY(rc);
     *max_sim = count > 0 ? std::max(-1.0f, r.score) : 0.0f;     // memory_cuda.cu:1589-1591
     return MARS_OK;
