@@ -627,6 +627,20 @@ def main() -> int:
                                          f"vectors), fp64 C++ oracle with OpenMP over rows; p99 of {nc}",
                                "p50_us": round(pctl(cl, .5), 1)}
         log(f"cpu oracle ({res['cpu_baseline']['cores']} threads): p50 {pctl(cl, .5):.0f} us p99 {pctl(cl, .99):.0f} us")
+        # the same oracle on one thread (a few queries: about 0.4 s each at 1M)
+        threads = oracle.lib.oracle_num_threads()
+        oracle.lib.oracle_set_num_threads(1)
+        c1 = []
+        for node in qnodes[W:W + 5]:
+            t0 = time.perf_counter()
+            oracle.query(og, c.embeddings[node], corpus.QUERY_TIME, ocfg)
+            c1.append((time.perf_counter() - t0) * 1e6)
+        oracle.lib.oracle_set_num_threads(threads)
+        model = next((ln.split(":", 1)[1].strip() for ln in Path("/proc/cpuinfo").read_text().splitlines()
+                      if ln.startswith("model name")), "unknown")
+        res["cpu_baseline"]["single_thread"] = {"p50_us": round(pctl(c1, .5), 1), "queries": len(c1)}
+        res["cpu_baseline"]["host"] = {"cpu": model, "nproc": os.cpu_count()}
+        log(f"cpu oracle (1 thread, {len(c1)} queries): p50 {pctl(c1, .5):.0f} us; host {model}, nproc {os.cpu_count()}")
     dq.free()
     mars_amd.destroy_query_context(ctx)
     mars_amd.free_device(dg)
