@@ -70,6 +70,7 @@ def _load():
         "oracle_novelty": (C.c_double, [C.POINTER(OracleGraph), VP, C.POINTER(C.c_double)]),
         "oracle_edge_hits": (None, [VP, VP, I32, VP, VP]),
         "oracle_maintain": (I32, [VP, I64, I32]),
+        "oracle_kids_probes": (None, [I32, I64, I32, VP]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -315,3 +316,10 @@ def maintain(hits, min_hits: int = 0):
     h = np.array(hits, np.int32, copy=True)
     low = lib.oracle_maintain(_p(h) if len(h) else None, len(h), int(min_hits))
     return int(low), h
+
+
+def kids_probes(n: int, n_image: int, count: int = 256) -> np.ndarray:
+    """Indices into the IMAGE-node list of the kids sweep's probes (bench_kids_sweep.cu:624-632)."""
+    out = np.empty(count, np.int64)
+    lib.oracle_kids_probes(int(n), int(n_image), int(count), _p(out))
+    return out
