@@ -362,7 +362,11 @@ def main() -> int:
     log(f"upload + fp16 copy: {time.time() - t:.1f}s")
     t = time.time()
     if args.knn_k > 0:
-        knn = mars_amd.graph_knn(dg, args.knn_k, args.knn_block)   # fp16 MFMA candidates + exact fp32 rescoring
+        def knn_progress(done, total):
+            if done % 10 == 0 or done == total:
+                log(f"{args.knn_k}-NN block {done}/{total}: {time.time() - t:.1f}s")
+        # fp16 MFMA candidates + exact fp32 rescoring
+        knn = mars_amd.graph_knn(dg, args.knn_k, args.knn_block, knn_progress if args.knn_block else None)
         log(f"{args.knn_k}-NN on the GPU" + (f" (blocks of {args.knn_block} ids)" if args.knn_block else "") +
             f": {time.time() - t:.1f}s")
     else:

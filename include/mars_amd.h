@@ -172,6 +172,11 @@ int mars_graph_knn(mars_graph* g, int32_t k, int32_t* nbrs);
  * block_rows consecutive ids (block_rows >= num_nodes: mars_graph_knn). For corpora
  * where the exact all-pairs search is too long to build (13M rows: ~2.6e17 FLOP). */
 int mars_graph_knn_blocked(mars_graph* g, int32_t k, int32_t block_rows, int32_t* nbrs);
+/* The same for blocks [first_block, first_block + n_blocks) only: nbrs receives the rows
+ * of nodes first_block * block_rows .. (at most n_blocks * block_rows rows, clipped to
+ * the node count), so a caller can build a large graph block by block. */
+int mars_graph_knn_blocks(mars_graph* g, int32_t k, int32_t block_rows, int32_t first_block, int32_t n_blocks,
+                          int32_t* nbrs);
 /* Measurement aid, no counterpart in the reference: the bandwidth (GB/s, best of 256,
  * 512 and 1024 workgroups, reps timed launches each) of a plain streaming read of the
  * graph's fp32 (fp16 = 0) or fp16 rows with no arithmetic, the practical ceiling of the

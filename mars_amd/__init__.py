@@ -408,11 +408,19 @@ def query_global_batch(dg: DeviceMemoryGraph, ctx: QueryContext, d_queries_ptr: 
     return res
 
 
-def graph_knn(dg: DeviceMemoryGraph, k: int = 8, block_rows: int = 0) -> np.ndarray:
+def graph_knn(dg: DeviceMemoryGraph, k: int = 8, block_rows: int = 0, progress=None) -> np.ndarray:
     """k nearest neighbours of every node (fp16 MFMA candidates + exact fp32 rescoring);
-    block_rows > 0: among the nodes of each block of block_rows consecutive ids."""
+    block_rows > 0: among the nodes of each block of block_rows consecutive ids
+    (progress(done, total) is called after each block when given)."""
     out = np.empty((dg.num_nodes, k), np.int32)
-    if block_rows > 0:
+    if block_rows > 0 and progress is not None:
+        nb = (dg.num_nodes + block_rows - 1) // block_rows
+        for b in range(nb):                  # one block per call: the caller reports each
+            lo = b * block_rows
+            check(lib.mars_graph_knn_blocks(dg.handle, int(k), int(block_rows), b, 1, _ptr(out[lo:])),
+                  "mars_graph_knn_blocks")
+            progress(b + 1, nb)
+    elif block_rows > 0:
         check(lib.mars_graph_knn_blocked(dg.handle, int(k), int(block_rows), _ptr(out)), "mars_graph_knn_blocked")
     else:
         check(lib.mars_graph_knn(dg.handle, int(k), _ptr(out)), "mars_graph_knn")

@@ -1531,8 +1531,16 @@ int mars_graph_read_ceiling(const mars_graph* gh, int32_t fp16, int32_t reps, do
 }
 
 int mars_graph_knn_blocked(mars_graph* gh, int32_t k, int32_t block_rows, int32_t* nbrs) {
-    MARS_CHECK(gh && nbrs && k >= 1 && k <= 16 && block_rows > 0, MARS_ERR_INVALID,
-               "k-NN: bad arguments (k=%d, block_rows=%d)", k, block_rows);
+    MARS_CHECK(gh && block_rows > 0, MARS_ERR_INVALID, "k-NN: bad arguments (block_rows=%d)", block_rows);
+    const int64_t n = gh->g.n;
+    return mars_graph_knn_blocks(gh, k, block_rows, 0, int32_t((n + block_rows - 1) / block_rows), nbrs);
+}
+
+int mars_graph_knn_blocks(mars_graph* gh, int32_t k, int32_t block_rows, int32_t first_block, int32_t n_blocks,
+                          int32_t* nbrs) {
+    MARS_CHECK(gh && nbrs && k >= 1 && k <= 16 && block_rows > 0 && first_block >= 0 && n_blocks >= 0,
+               MARS_ERR_INVALID, "k-NN: bad arguments (k=%d, block_rows=%d, blocks %d + %d)", k, block_rows,
+               first_block, n_blocks);
     std::lock_guard<std::mutex> lock(gh->mu);
     Graph& g = gh->g;
     MARS_CHECK(g.emb16 != nullptr, MARS_ERR_UNSUPPORTED, "k-NN reads the fp16 corpus: enable it first");
@@ -1541,6 +1549,10 @@ int mars_graph_knn_blocked(mars_graph* gh, int32_t k, int32_t block_rows, int32_
     constexpr int32_t kChunk = 1024;                 // queries per launch (16 query blocks)
     constexpr int32_t kCand = 16;
     const int64_t B = std::min<int64_t>(block_rows, g.n);
+    // nodes [lo, hi): the requested blocks
+    const int64_t lo = std::min<int64_t>(int64_t(first_block) * block_rows, g.n);
+    const int64_t hi = std::min<int64_t>(lo + int64_t(n_blocks) * block_rows, g.n);
+    if (hi <= lo) return MARS_OK;
     int32_t nrr = 0, nqb = 0;
     int64_t rpr = 0;
     batch_grid(B, kChunk, &nrr, &nqb, &rpr);         // the largest block sizes the scratch
@@ -1549,7 +1561,7 @@ int mars_graph_knn_blocked(mars_graph* gh, int32_t k, int32_t block_rows, int32_
     int rc = MARS_OK;
     auto cleanup = [&]() { dfree(tq); dfree(part); dfree(cand); dfree(dn); if (s) (void)hipStreamDestroy(s); };
     if ((rc = dmalloc(&tq, kChunk)) || (rc = dmalloc(&part, size_t(nqb) * nrr * 64 * kCand)) ||
-        (rc = dmalloc(&cand, size_t(kChunk) * kCand)) || (rc = dmalloc(&dn, size_t(g.n) * k))) {
+        (rc = dmalloc(&cand, size_t(kChunk) * kCand)) || (rc = dmalloc(&dn, size_t(hi - lo) * k))) {
         cleanup();
         return rc;
     }
@@ -1557,7 +1569,7 @@ int mars_graph_knn_blocked(mars_graph* gh, int32_t k, int32_t block_rows, int32_
     if (e == hipSuccess) e = hipMemsetAsync(tq, 0, kChunk * sizeof(float), s);
     if (e != hipSuccess) { cleanup(); return set_error(MARS_ERR_HIP, "k-NN setup: %s", hipGetErrorString(e)); }
     // block [r0, r1): rows, queries and candidate ids relative to r0
-    for (int64_t r0 = 0; r0 < g.n && rc == MARS_OK; r0 += B) {
+    for (int64_t r0 = lo; r0 < hi && rc == MARS_OK; r0 += B) {
         const int64_t nb = std::min<int64_t>(B, g.n - r0);
         batch_grid(nb, kChunk, &nrr, &nqb, &rpr);
         for (int64_t q0 = 0; q0 < nb && rc == MARS_OK; q0 += kChunk) {
@@ -1570,20 +1582,20 @@ int mars_graph_knn_blocked(mars_graph* gh, int32_t k, int32_t block_rows, int32_
             rc = launch_batch_scan(a, s);
             if (rc == MARS_OK) rc = launch_batch_merge(part, nrr, kCand, q, kCand, cand, s);
             if (rc == MARS_OK)
-                rc = launch_knn_rerank(g.emb + r0 * g.d, q0, q, g.d, cand, kCand, k, dn + (r0 + q0) * k, s);
+                rc = launch_knn_rerank(g.emb + r0 * g.d, q0, q, g.d, cand, kCand, k, dn + (r0 - lo + q0) * k, s);
         }
     }
     if (rc == MARS_OK) {
         e = hipStreamSynchronize(s);
-        if (e == hipSuccess) e = hipMemcpy(nbrs, dn, size_t(g.n) * k * sizeof(int32_t), hipMemcpyDeviceToHost);
+        if (e == hipSuccess) e = hipMemcpy(nbrs, dn, size_t(hi - lo) * k * sizeof(int32_t), hipMemcpyDeviceToHost);
         if (e != hipSuccess) rc = set_error(MARS_ERR_HIP, "k-NN: %s", hipGetErrorString(e));
     }
     cleanup();
-    if (rc == MARS_OK && B < g.n) {
-        for (int64_t i = 0; i < int64_t(g.n); ++i) {
+    if (rc == MARS_OK && B < g.n) {                      // block-relative ids -> node ids
+        for (int64_t i = lo; i < hi; ++i) {
             const int32_t off = int32_t(i / B * B);
             for (int32_t j = 0; j < k; ++j)
-                if (nbrs[i * k + j] >= 0) nbrs[i * k + j] += off;
+                if (nbrs[(i - lo) * k + j] >= 0) nbrs[(i - lo) * k + j] += off;
         }
     }
     return rc;

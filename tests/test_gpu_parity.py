@@ -426,6 +426,14 @@ def test_gpu_knn_matches_cpu_exact():
                     assert abs(s[i, j] - sims[i, 7]) <= 1e-5, (i, j)
         assert mism <= 0.01 * c.num_nodes
         assert np.all(got != np.arange(c.num_nodes)[:, None])
+        # blocks of 1,700 ids (the last one ragged): one call, and block by block
+        whole = mars_amd.graph_knn(dev.dg, 8, 1700)
+        seen = []
+        parts = mars_amd.graph_knn(dev.dg, 8, 1700, progress=lambda d, t: seen.append((d, t)))
+        np.testing.assert_array_equal(parts, whole)
+        assert seen == [(1, 4), (2, 4), (3, 4), (4, 4)]
+        blk = np.arange(c.num_nodes) // 1700
+        assert np.all(blk[whole] == blk[:, None])          # neighbours within the node's block
     finally:
         dev.close()
 
