@@ -507,26 +507,27 @@ def main() -> int:
         ctx.use_fp16 = False
         log(f"global fp16: p50 {pctl(lat_h, .5):.1f} us p99 {pctl(lat_h, .99):.1f} us; scan kernel mean "
             f"{kern_h.mean():.1f} us ({bytes_f16 / kern_h.mean() / 1e3:.0f} GB/s)")
-        # ---- batched Q=64 global scoring on MFMA fp16 tiles
-        ctx.timing = True
-        B, reps = args.batch_q, 30
-        bl, bk = [], []
-        for r in range(reps + 3):
-            st = mars_amd.RetrievalStats()
-            mars_amd.query_batch(dg, ctx, dq.ptr + ((W + r * B) % max(1, S - B)) * D * 4, B, corpus.QUERY_TIME,
-                                 RetrievalConfig(top_k=K, time_decay_lambda=corpus.DECAY_LAMBDA), st)
-            if r >= 3:
-                bl.append(st.wall_us)
-                bk.append(st.gpu_ms_similarity * 1e3)
-        ctx.timing = False
-        bkm = float(np.mean(bk))
-        flops = 2.0 * B * N * D
-        out[f"batch_q{B}_fp16"] = dict(p50_us=pctl(bl, .5), p99_us=pctl(bl, .99), queries_per_s=B / (pctl(bl, .5) / 1e6),
-                                     scan_kernel_mean_us=bkm, tflops=flops / bkm / 1e6,
-                                     mfma_util=flops / bkm / 1e6 / 2500.0,
-                                     hbm_gbs=bytes_f16 / bkm / 1e3, hbm_frac=bytes_f16 / bkm / 1e3 / HBM_PEAK_GBS)
-        log(f"batch Q={B}: p50 {pctl(bl, .5):.0f} us; scan {bkm:.0f} us = {flops / bkm / 1e6:.0f} TFLOP/s "
-            f"({flops / bkm / 1e6 / 25:.1f}% of 2.5 PF), {bytes_f16 / bkm / 1e3:.0f} GB/s")
+        # ---- batched global scoring on MFMA fp16 tiles (--batch-q 0 skips it)
+        if args.batch_q > 0:
+            ctx.timing = True
+            B, reps = args.batch_q, 30
+            bl, bk = [], []
+            for r in range(reps + 3):
+                st = mars_amd.RetrievalStats()
+                mars_amd.query_batch(dg, ctx, dq.ptr + ((W + r * B) % max(1, S - B)) * D * 4, B, corpus.QUERY_TIME,
+                                     RetrievalConfig(top_k=K, time_decay_lambda=corpus.DECAY_LAMBDA), st)
+                if r >= 3:
+                    bl.append(st.wall_us)
+                    bk.append(st.gpu_ms_similarity * 1e3)
+            ctx.timing = False
+            bkm = float(np.mean(bk))
+            flops = 2.0 * B * N * D
+            out[f"batch_q{B}_fp16"] = dict(p50_us=pctl(bl, .5), p99_us=pctl(bl, .99), queries_per_s=B / (pctl(bl, .5) / 1e6),
+                                         scan_kernel_mean_us=bkm, tflops=flops / bkm / 1e6,
+                                         mfma_util=flops / bkm / 1e6 / 2500.0,
+                                         hbm_gbs=bytes_f16 / bkm / 1e3, hbm_frac=bytes_f16 / bkm / 1e3 / HBM_PEAK_GBS)
+            log(f"batch Q={B}: p50 {pctl(bl, .5):.0f} us; scan {bkm:.0f} us = {flops / bkm / 1e6:.0f} TFLOP/s "
+                f"({flops / bkm / 1e6 / 25:.1f}% of 2.5 PF), {bytes_f16 / bkm / 1e3:.0f} GB/s")
         out["episode"] = dict(p50_us=pctl(lat_e, .5), p99_us=pctl(lat_e, .99), qps=S / wall_e,
                               kernel_mean_us=float(kern_e.mean()),
                               graph_replay=dict(p50_us=pctl(lat_eg, .5), p99_us=pctl(lat_eg, .99)))
