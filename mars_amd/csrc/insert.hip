@@ -51,8 +51,12 @@ constexpr int32_t kKnnCand = 16;            // fp16 candidates rescored per new 
 // the CUs it leaves them most of the bandwidth. At 1M nodes, 2,000 inserts/s and 500
 // global queries/s: global p99 573 us with 256 ranges, 299 us with 64 (idle: 278),
 // 336 us with 32; new nodes linked after 1.09 ms instead of 0.67 ms. The neighbours do
-// not change: every range keeps its own 16 best candidates.
+// not change: every range keeps its own 16 best candidates. Narrowing doubles the
+// search's duration, so it applies up to kInsertKnnNarrowRows rows: beyond them one
+// search per insert call already fills a large share of the GPU (at 13M rows a
+// full-width search takes about 4 ms), and a longer one would only delay the writer.
 constexpr int32_t kInsertKnnRanges = 64;
+constexpr int64_t kInsertKnnNarrowRows = 2000000;
 
 // Step 1 of an insert in one launch: the staged block (rows | modalities | times |
 // episode ids | episode members | episode offsets) is scattered into the graph; each
@@ -208,9 +212,10 @@ double us_since(std::chrono::steady_clock::time_point t0) {
 int insert_knn(Graph& g, int64_t first, int32_t nq, int64_t n, int32_t k, hipStream_t s) {
     int32_t nrr = 0, nqb = 0;
     int64_t rpr = 0, part_keys = 0;
+    const int32_t ranges = n <= kInsertKnnNarrowRows ? kInsertKnnRanges : 256;
     for (int32_t q : {std::min(nq, kInsertChunk), nq % kInsertChunk}) {   // full and last chunk
         if (q == 0) continue;
-        batch_grid(n, q, &nrr, &nqb, &rpr, kInsertKnnRanges);
+        batch_grid(n, q, &nrr, &nqb, &rpr, ranges);
         part_keys = std::max<int64_t>(part_keys, int64_t(nrr) * nqb * 64 * kKnnCand);
     }
     if (part_keys > g.ins_part_cap) {
@@ -232,7 +237,7 @@ int insert_knn(Graph& g, int64_t first, int32_t nq, int64_t n, int32_t k, hipStr
     }
     for (int32_t c0 = 0; c0 < nq; c0 += kInsertChunk) {
         const int32_t q = std::min(kInsertChunk, nq - c0);
-        batch_grid(n, q, &nrr, &nqb, &rpr, kInsertKnnRanges);
+        batch_grid(n, q, &nrr, &nqb, &rpr, ranges);
         BatchArgs a{};
         a.emb16 = g.emb16; a.n = n; a.d = g.d; a.qh = g.emb16 + (first + c0) * g.d; a.q = q; a.tq = g.ins_tq;
         a.ts = g.ts; a.mods = g.mods; a.lambda = 0.0f; a.mod_filter = -1; a.k = kKnnCand;
