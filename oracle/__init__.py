@@ -1,8 +1,8 @@
 """CPU oracle of the retrieval hot path (ctypes over oracle/liboracle.so).
 
 TEST INFRASTRUCTURE: imported only by tests/, __graft_entry__.smoke() and the
-cpu_baseline leg of bench.py, as the checker / CPU baseline. The product
-(mars_amd) never imports it.
+cpu_baseline leg of bench.py, which compare GPU results against it or time it as the
+CPU baseline. The product (mars_amd) never imports it.
 
 ``ref`` (oracle/_ref/libref.so, built from the reference's own host sources
 when the reference tree is present) is None when that library is absent.

@@ -2,8 +2,9 @@
 //  oracle/oracle.cpp — CPU restatement of the MARS retrieval hot path.
 //
 //  TEST INFRASTRUCTURE. Only tests/, __graft_entry__.smoke() and the
-//  cpu_baseline leg of bench.py may load this library, and only as the
-//  checker / CPU baseline. The product (mars_amd) never calls it.
+//  cpu_baseline leg of bench.py may load this library: to compare GPU results
+//  against it, or to time it as the CPU baseline. The product (mars_amd) never
+//  calls it.
 //
 //  Every function cites the reference file:line it restates (paths relative
 //  to the MARS source tree). Arithmetic is fp64 throughout (inputs are the
