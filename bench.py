@@ -124,10 +124,12 @@ def maintenance_pass(mars_amd, dg, ctx, dq, first, count, D, gcfg, pctl, reps=20
 
 
 def engine_pass(n_nodes, n_queries, D, pctl):
-    """The JSON-line engine server (mars_amd/mars_engine) over its stdin/stdout pipe: n_nodes
-    ADDs of the benchmark corpus (each a one-node streaming insert with 8-NN edges once 8
-    nodes exist), then n_queries QUERYs (top-10, depth-2 BFS, certified path) timed from
-    the write of the request to the parsed response; requests are encoded before timing."""
+    """The JSON-line engine server (mars_amd/mars_engine) over its stdin/stdout pipe, with the
+    reference server's edge policy (NSN graph rebuilt before a query after the node count
+    doubled or grew by 1000): n_nodes ADDs of the benchmark corpus (each a one-node
+    streaming insert), then n_queries QUERYs (top-10, depth-2 BFS, certified path; the
+    first one builds the NSN graph) timed from the write of the request to the parsed
+    response; requests are encoded before timing."""
     import subprocess
     from mars_amd import corpus as corp
     exe = ROOT / "mars_amd" / "mars_engine"
@@ -291,6 +293,59 @@ def serve_pass(args, mars_amd, corpus, lib, check, full, dg, ctx, qnodes, nq, ep
     return res
 
 
+def compare_results(got, want, scl):
+    """GPU results against oracle results from the same seeds: equal count; at each rank the
+    same id with the same hops and a score within 1e-5 * max(|s|, its BFS-carried scale), or
+    two ids whose scores are a near-tie under that bound."""
+    if len(got) != len(want):
+        return False
+    for r, w in zip(got, want):
+        tw = 1e-5 * max(abs(w[1]), scl[w[0]])
+        if r.node_id == w[0]:
+            if r.hops_from_seed != w[3] or abs(r.score - w[1]) > tw:
+                return False
+        elif abs(r.score - w[1]) > 2 * (tw + 1e-5 * max(abs(r.score), scl.get(r.node_id, float("inf")))):
+            return False
+    return True
+
+
+def parity_check(mars_amd, oracle, dg, ctx, dq, first, D, og, c, qnodes, t_q, gcfg, ocfg, refs):
+    """The GPU's answers to the queries the CPU baseline answered, against those oracle
+    answers. Each query runs on the fp32-scan path (whose seeds the context keeps) and on
+    the certified path (the one `value` times); the two must be bit-identical. The seed set
+    must equal the oracle's up to near-ties at the K-th score (the oracle then runs again
+    from the GPU's seeds); results as compare_results."""
+    bad = []
+    for i, ref in enumerate(refs):
+        q = c.embeddings[qnodes[first + i]]
+        ptr = dq.ptr + (first + i) * D * 4
+        ctx.certified = False
+        got = mars_amd.query_memory_fast_device(dg, ctx, ptr, t_q, gcfg)
+        seeds, _ = ctx.last_seeds()
+        ctx.certified = True
+        got_c = mars_amd.query_memory_fast_device(dg, ctx, ptr, t_q, gcfg)
+        ctx.certified = False
+        if got_c != got:
+            bad.append(i)
+            continue
+        fin = ref["final"]
+        _, scale = oracle.scores(og, q, t_q, gcfg.time_decay_lambda, gcfg.modality_filter)
+        tol = 1e-5 * np.maximum(np.abs(fin), scale)
+        kth = ref["seeds"][-1]
+        diff = set(seeds.tolist()) ^ set(ref["seeds"].tolist())
+        if any(abs(fin[j] - fin[kth]) > 2 * (tol[j] + tol[kth]) for j in diff):
+            bad.append(i)
+            continue
+        if diff:                                   # near-tie seeds: the oracle from the GPU's seeds
+            ref = oracle.query(og, q, t_q, ocfg, seeds_in=seeds)
+        if not compare_results(got, ref["results"], oracle.result_scales(og, q, t_q, ocfg, ref)):
+            bad.append(i)
+    return {"queries": len(refs), "mismatched": len(bad), "mismatched_queries": bad[:10],
+            "paths": "fp32 scan and MARS_CTX_CERTIFIED (bit-identical to each other)",
+            "against": "the cpu_baseline oracle answers (fp64, same corpus, graph and query vectors)",
+            "bar": "ids and hops exact, scores within 1e-5 * max(|s|, BFS-carried w * sum|e q|), near-ties allowed"}
+
+
 def pctl(v, p):
     v = np.sort(np.asarray(v, np.float64))
     return float(v[int(p * (len(v) - 1))]) if len(v) else 0.0
@@ -421,6 +476,18 @@ def main() -> int:
         assert np.all(nres == K), "every query must return K results"
         return lat, kern, bfs
 
+    hq = np.ascontiguousarray(c.embeddings[qnodes])          # the same query vectors in host memory
+
+    def run_host(first, count, cfgs, n_cfg):
+        """query_memory_fast's contract: a host vector, copied to the device inside each call."""
+        lat = np.zeros(count, np.float64)
+        nres = np.zeros(count, np.int32)
+        check(lib.mars_bench_queries_host(dg.handle, ctx.handle, C.c_void_p(hq.ctypes.data + first * D * 4), D, count,
+                                          C.c_float(corpus.QUERY_TIME), cfgs, n_cfg, C.c_void_p(lat.ctypes.data),
+                                          C.c_void_p(nres.ctypes.data)), "mars_bench_queries_host")
+        assert np.all(nres == K), "every query must return K results"
+        return lat
+
     W, S = args.warmup, args.steps
     KT = min(S, 2000)          # queries of the kernel-timing passes (HIP events on the query stream)
     g1 = gcfg.to_c()
@@ -460,6 +527,10 @@ def main() -> int:
     (lat_c, _, _), wall_c = timed(W, S, C.pointer(g1), 1, False)
     (lat_ck, kern_c, rest_c), _ = timed(W, KT, C.pointer(g1), 1, True)
     ctx.timing = False
+    run_host(0, W, C.pointer(g1), 1)
+    lat_ch = run_host(W, S, C.pointer(g1), 1)
+    log(f"global certified, host query vectors (3 KB H2D inside each call): p50 {pctl(lat_ch, .5):.1f} us "
+        f"p99 {pctl(lat_ch, .99):.1f} us")
     n_cert, n_samp = 0, min(S, 500)
     for i in range(n_samp):
         st = mars_amd.RetrievalStats()
@@ -494,6 +565,9 @@ def main() -> int:
         (_, kern_e, _), _ = timed(W, KT, ec_t, KT, True)
         log(f"episode: p50 {pctl(lat_e, .5):.1f} us p99 {pctl(lat_e, .99):.1f} us; {S / wall_e:.0f} q/s; kernel mean "
             f"{kern_e.mean():.1f} us")
+        run_host(0, W, ec, W) if W else None
+        lat_eh = run_host(W, S, ec_t, S)
+        log(f"episode, host query vectors: p50 {pctl(lat_eh, .5):.1f} us p99 {pctl(lat_eh, .99):.1f} us")
         ctx.use_cuda_graph = True
         run(0, W, ec, W) if W else None
         (lat_eg, _, _), _ = timed(W, S, ec_t, S, False)
@@ -529,6 +603,7 @@ def main() -> int:
             log(f"batch Q={B}: p50 {pctl(bl, .5):.0f} us; scan {bkm:.0f} us = {flops / bkm / 1e6:.0f} TFLOP/s "
                 f"({flops / bkm / 1e6 / 25:.1f}% of 2.5 PF), {bytes_f16 / bkm / 1e3:.0f} GB/s")
         out["episode"] = dict(p50_us=pctl(lat_e, .5), p99_us=pctl(lat_e, .99), qps=S / wall_e,
+                              host_vector_p50_us=pctl(lat_eh, .5), host_vector_p99_us=pctl(lat_eh, .99),
                               kernel_mean_us=float(kern_e.mean()),
                               graph_replay=dict(p50_us=pctl(lat_eg, .5), p99_us=pctl(lat_eg, .99)))
         out["global_fp16"] = dict(p50_us=pctl(lat_h, .5), p99_us=pctl(lat_h, .99), qps=S / wall_h,
@@ -586,6 +661,7 @@ def main() -> int:
                                  (f" within blocks of {args.knn_block} ids" if args.knn_block else "")
                                  if args.knn_k > 0 else "intra-episode pairs only (k-NN edges omitted)")},
         "global_certified": dict(p50_us=pctl(lat_c, .5), p99_us=pctl(lat_c, .99), qps=S / wall_c,
+                                 host_vector_p50_us=pctl(lat_ch, .5), host_vector_p99_us=pctl(lat_ch, .99),
                                  p99_us_with_events=pctl(lat_ck, .99), scan_kernel_mean_us=float(kern_c.mean()),
                                  seeds_bfs_results_mean_us=float(rest_c.mean()),
                                  scan_gbs=achieved, scan_frac=achieved / HBM_PEAK_GBS,
@@ -620,12 +696,14 @@ def main() -> int:
         import oracle
         og = oracle.make_graph(c.embeddings, c.modalities, c.timestamps, c.row_offsets, c.col_indices)
         ocfg = oracle.config(K, 2, corpus.DECAY_LAMBDA, 0.5)
-        cl = []
+        cl, refs = [], []
         nc = min(args.cpu_queries, S)
         for node in qnodes[W:W + nc]:
             t0 = time.perf_counter()
-            oracle.query(og, c.embeddings[node], corpus.QUERY_TIME, ocfg)
+            refs.append(oracle.query(og, c.embeddings[node], corpus.QUERY_TIME, ocfg))
             cl.append((time.perf_counter() - t0) * 1e6)
+        res_parity = parity_check(mars_amd, oracle, dg, ctx, dq, W, D, og, c, qnodes, corpus.QUERY_TIME, gcfg, ocfg,
+                                  refs)
         res["cpu_baseline"] = {"value": round(pctl(cl, .99), 1), "unit": "us", "cores": oracle.lib.oracle_num_threads(),
                                "kind": "port",
                                "sample": f"first {nc} of the timed global queries (same corpus, graph and query "
@@ -643,6 +721,7 @@ def main() -> int:
         oracle.lib.oracle_set_num_threads(threads)
         model = next((ln.split(":", 1)[1].strip() for ln in Path("/proc/cpuinfo").read_text().splitlines()
                       if ln.startswith("model name")), "unknown")
+        res["parity_checked"] = res_parity
         res["cpu_baseline"]["single_thread"] = {"p50_us": round(pctl(c1, .5), 1), "queries": len(c1)}
         res["cpu_baseline"]["host"] = {"cpu": model, "nproc": os.cpu_count()}
         log(f"cpu oracle (1 thread, {len(c1)} queries): p50 {pctl(c1, .5):.0f} us; host {model}, nproc {os.cpu_count()}")
@@ -653,6 +732,10 @@ def main() -> int:
     if host_rows:
         host_rows.free()
     print(json.dumps(res), flush=True)
+    if res.get("parity_checked", {}).get("mismatched", 0):
+        log(f"PARITY FAILURE: {res['parity_checked']['mismatched']} of {res['parity_checked']['queries']} GPU answers "
+            f"differ from the oracle's")
+        return 3
     return 0
 
 

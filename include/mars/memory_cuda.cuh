@@ -11,7 +11,15 @@
 //    * QueryContext::use_cublas / use_cub_topk / use_wmma are accepted and have no
 //      effect (scoring and selection always run the fused HIP kernels);
 //    * results are sorted by (score desc, node_id asc) and the BFS is the
-//      deterministic first-discoverer BFS (no frontier cap, no compaction cap);
+//      deterministic first-discoverer BFS (no frontier cap); a query returns at most
+//      min(max_nodes, max_k * 500) results, the reference's compaction cap, keeping
+//      the best of them;
+//    * RetrievalStats: gpu_ms_similarity is the fused scan (dot, decay, per-wave
+//      top-K), gpu_ms_rerank is 0 (the decay is inside the scan), gpu_ms_topk the
+//      seed merge, gpu_ms_bfs the BFS and the sorted results;
+//    * DeviceMemoryGraph: d_row_offsets / d_col_indices are a packed copy of the
+//      edges, made again after they change; the queries read d_row_words and
+//      d_col_slots, where a row that grew by a streaming insert can sit apart;
 //    * library errors print a message and exit, as CUDA_CHECK does (lines 52-60);
 //      malformed episode inputs are silent no-ops and an inactive episode scope
 //      falls back to Global, as in the reference (memory_cuda.cu:814-855, 1163-1171).
@@ -34,8 +42,8 @@ struct DeviceMemoryGraph {
     int32_t num_nodes = 0;
     int32_t num_edges = 0;
     int32_t embedding_dim = 0;
-    int32_t* d_row_offsets = nullptr;      // not kept on the device (see d_row_words)
-    int32_t* d_col_indices = nullptr;
+    int32_t* d_row_offsets = nullptr;      // packed CSR [num_nodes + 1]: a copy (see d_row_words)
+    int32_t* d_col_indices = nullptr;      // packed CSR [num_edges]
     float* d_embeddings = nullptr;
     void* d_embeddings_fp16 = nullptr;     // binary16 rows
     int32_t* d_modalities = nullptr;
@@ -47,7 +55,8 @@ struct DeviceMemoryGraph {
     int32_t episode_csr_member_total = 0;
     float* d_importance = nullptr;         // null: the library's graph holds the array
     int32_t* d_edge_hits = nullptr;        // null: the library's graph holds the array
-    int64_t* d_row_words = nullptr;        // per node: (row length << 32) | row start in col
+    int64_t* d_row_words = nullptr;        // per node: (row length << 32) | row start in d_col_slots
+    int32_t* d_col_slots = nullptr;        // the column slots the queries read (rows may have slack)
     mars_graph* handle = nullptr;
 };
 
@@ -105,6 +114,7 @@ struct QueryContext {
     bool use_cublas = true;       // accepted, no effect
     bool use_cub_topk = true;     // accepted, no effect
     bool use_wmma = false;        // accepted, no effect
+    void* stream = nullptr;       // the context's hipStream_t (line 178): its queries run on it
     mars_ctx* handle = nullptr;
 };
 

@@ -186,6 +186,13 @@ int mars_graph_read_ceiling(const mars_graph* g, int32_t fp16, int32_t reps, dou
  * a packed CSR (row_offsets: num_nodes + 1, col_indices: num_edges) and the episode CSR. */
 int mars_graph_download(const mars_graph* g, int32_t* row_offsets, int32_t* col_indices,
                         int32_t* ep_offsets, int32_t* ep_members);
+/* DeviceMemoryGraph::d_row_offsets / d_col_indices (memory_cuda.cuh:63-85): the graph's
+ * edges as a packed CSR in device memory, int32 [num_nodes + 1] and [num_edges]. The
+ * queries read the graph's own row words, in which a row that grew by a streaming insert
+ * can sit apart from its neighbours; this is a copy made for callers that expect the
+ * reference's layout. Built on the first call and again after the edges changed; owned
+ * by the graph (valid until the next change of the edges or mars_graph_destroy). */
+int mars_graph_packed_csr(mars_graph* g, const int32_t** d_row_offsets, const int32_t** d_col_indices);
 
 /* ---- files: MARS v1 graph checkpoints and the KIDS corpus -------------------
  * MARS v1 (persistence.h:8-18): "MARS", uint32 version 1, int32 num_nodes,
@@ -339,17 +346,28 @@ int mars_host_free(void* ptr);
  * (which returns fp16 scores), for episode scope, a same-episode boost, lambda < 0 and
  * embedding_dim not a multiple of 128. MARS_CTX_USE_GRAPH does not apply to it. */
 #define MARS_CTX_CERTIFIED   0x8u
-/* create_query_context(max_nodes, embedding_dim, max_k): max_k clamps to 64. */
+/* create_query_context(max_nodes, embedding_dim, max_k): max_k clamps to 64. A query
+ * returns at most min(max_nodes, max_k * 500) results, the reference's compaction cap
+ * (max_compact, memory_cuda.cu:1059): 32,000 at the default max_k of 64. */
 int mars_ctx_create(int32_t max_nodes, int32_t embedding_dim, int32_t max_k,
                     uint32_t flags, mars_ctx** out);
 int mars_ctx_destroy(mars_ctx* ctx);
 int mars_ctx_set_flags(mars_ctx* ctx, uint32_t flags);
 int mars_ctx_get_flags(const mars_ctx* ctx, uint32_t* flags);
+/* QueryContext::stream (memory_cuda.cuh:178): the context's own stream, a hipStream_t
+ * passed as void*, on which every kernel of its queries runs. Work the caller enqueues
+ * there is ordered with those queries. */
+int mars_ctx_get_stream(const mars_ctx* ctx, void** stream);
 
 /* query_memory_fast: one query from a host vector (embedding_dim floats).
  * Writes min(cap, n) results sorted by (score desc, node_id asc) and sets
- * *n_out = n, the number of results the query produced (n <= cap is the
- * caller's check). stats may be NULL. */
+ * *n_out = n, the number of results the query produced: min(max_results_returned
+ * (K when <= 0), nodes visited, the context's result cap); n <= cap is the caller's
+ * check. stats may be NULL. With MARS_CTX_TIMING the stage timers follow the
+ * reference's split (memory_cuda.cu:1450-1454): gpu_ms_similarity = the scan (dot,
+ * decay and per-wave top-K are one kernel), gpu_ms_rerank = 0 (the decay is fused into
+ * the scan), gpu_ms_topk = the seed merge, gpu_ms_bfs = the BFS and the sorted results,
+ * gpu_ms_total = all of them. */
 int mars_query(const mars_graph* g, mars_ctx* ctx, const float* h_query, float t_q,
                const mars_retrieval_config* cfg, mars_query_result* out, int32_t cap,
                int32_t* n_out, mars_stats* stats);
@@ -496,10 +514,17 @@ int mars_device_memory(size_t* free_bytes, size_t* total_bytes);  /* hipMemGetIn
  * receives the host wall latency of the whole call (steady_clock, measured here,
  * not through any binding layer); with MARS_CTX_TIMING set, kern_us[i] (may be NULL)
  * receives the GPU time of the scan / episode kernel and bfs_us[i] (may be NULL)
- * that of the finalize kernel. n_res[i] (may be NULL) gets the result count. */
+ * the GPU time after it (seeds, BFS and results). n_res[i] (may be NULL) gets the
+ * result count. */
 int mars_bench_queries(const mars_graph* g, mars_ctx* ctx, const float* d_queries, int64_t stride,
                        int32_t n, float t_q, const mars_retrieval_config* cfgs, int32_t n_cfg,
                        double* lat_us, float* kern_us, float* bfs_us, int32_t* n_res);
+/* The same loop over host query vectors h_queries + i*stride: each call copies its
+ * vector to the device as query_memory_fast does (memory_cuda.cu:1365-1368), and
+ * lat_us[i] includes that copy. */
+int mars_bench_queries_host(const mars_graph* g, mars_ctx* ctx, const float* h_queries, int64_t stride,
+                            int32_t n, float t_q, const mars_retrieval_config* cfgs, int32_t n_cfg,
+                            double* lat_us, int32_t* n_res);
 
 /* Streaming workload driver (no reference counterpart; the streaming benchmark
  * configuration): on one thread, n_queries single queries paced at query_rate per

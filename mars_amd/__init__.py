@@ -38,6 +38,8 @@ __all__ = [
 ]
 
 MOD_TEXT, MOD_AUDIO, MOD_IMAGE = 0, 1, 2
+# most results one query returns: the reference's compaction cap at max_k = 64 (64 * 500)
+RESULT_CAP = 32000
 
 
 class Modality(enum.IntEnum):                      # memory_graph.h:17-22
@@ -254,7 +256,7 @@ class QueryContext:
         self.max_nodes = max_nodes
         self.embedding_dim = dim
         self.max_k = min(max_k, 64)
-        self._out = (_lib.QueryResultC * 8192)()
+        self._out = (_lib.QueryResultC * RESULT_CAP)()
 
     def _flag(self, bit: int) -> bool:
         f = C.c_uint32()
@@ -317,7 +319,7 @@ def destroy_query_context(ctx: QueryContext) -> None:
 
 def _results(ctx: QueryContext, n: int) -> List[QueryResult]:
     o = ctx._out
-    return [QueryResult(o[i].node_id, o[i].score, o[i].modality, o[i].hops_from_seed) for i in range(min(n, 8192))]
+    return [QueryResult(o[i].node_id, o[i].score, o[i].modality, o[i].hops_from_seed) for i in range(min(n, RESULT_CAP))]
 
 
 def query_memory_fast(dg: DeviceMemoryGraph, ctx: QueryContext, h_query, query_timestamp: float,
@@ -329,7 +331,7 @@ def query_memory_fast(dg: DeviceMemoryGraph, ctx: QueryContext, h_query, query_t
     n = C.c_int32()
     st = _lib.StatsC()
     c = cfg.to_c()
-    check(lib.mars_query(dg.handle, ctx.handle, _ptr(q), float(query_timestamp), C.byref(c), ctx._out, 8192,
+    check(lib.mars_query(dg.handle, ctx.handle, _ptr(q), float(query_timestamp), C.byref(c), ctx._out, RESULT_CAP,
                          C.byref(n), C.byref(st)), "query_memory_fast")
     if stats is not None:
         stats._fill(st)
@@ -343,7 +345,7 @@ def query_memory_fast_device(dg: DeviceMemoryGraph, ctx: QueryContext, d_query_p
     st = _lib.StatsC()
     c = cfg.to_c()
     check(lib.mars_query_device(dg.handle, ctx.handle, C.c_void_p(d_query_ptr), float(query_timestamp),
-                                C.byref(c), ctx._out, 8192, C.byref(n), C.byref(st)), "query_memory_fast_device")
+                                C.byref(c), ctx._out, RESULT_CAP, C.byref(n), C.byref(st)), "query_memory_fast_device")
     if stats is not None:
         stats._fill(st)
     return _results(ctx, n.value)

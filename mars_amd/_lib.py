@@ -210,6 +210,8 @@ SIGNATURES = {
     "mars_graph_disable_fp16": (C.c_int, [VP]),
     "mars_graph_get_view": (C.c_int, [VP, C.POINTER(GraphViewC)]),
     "mars_graph_download": (C.c_int, [VP, VP, VP, VP, VP]),
+    "mars_graph_packed_csr": (C.c_int, [VP, C.POINTER(VP), C.POINTER(VP)]),
+    "mars_ctx_get_stream": (C.c_int, [VP, C.POINTER(VP)]),
     "mars_ctx_create": (C.c_int, [I32, I32, I32, C.c_uint32, C.POINTER(VP)]),
     "mars_ctx_destroy": (C.c_int, [VP]),
     "mars_ctx_set_flags": (C.c_int, [VP, C.c_uint32]),
@@ -262,6 +264,8 @@ SIGNATURES = {
     "mars_copy_device": (C.c_int, [VP, VP, C.c_size_t]),
     "mars_bench_queries": (C.c_int, [VP, VP, VP, I64, I32, C.c_float, C.POINTER(RetrievalConfigC), I32, VP, VP,
                                      VP, VP]),
+    "mars_bench_queries_host": (C.c_int, [VP, VP, VP, I64, I32, C.c_float, C.POINTER(RetrievalConfigC), I32, VP,
+                                          VP]),
     "mars_bench_stream": (C.c_int, [VP, VP, C.POINTER(StreamBenchC)]),
     "mars_tiled_config_default": (None, [C.POINTER(TiledConfigC)]),
     "mars_tiled_ctx_create": (C.c_int, [I32, I32, I32, C.POINTER(VP)]),

@@ -104,7 +104,7 @@ int graph_free(Graph& g) {
     if (g.ins_stream) (void)hipStreamSynchronize(g.ins_stream);
     dfree(g.emb); dfree(g.emb16); dfree(g.nrm); dfree(g.mods); dfree(g.ts); dfree(g.ro); dfree(g.rcap); dfree(g.col);
     dfree(g.ep_ids); dfree(g.ep_off); dfree(g.ep_mem);
-    dfree(g.imp); dfree(g.hits); dfree(g.imp_ids); dfree(g.sweep_cnt);
+    dfree(g.imp); dfree(g.hits); dfree(g.imp_ids); dfree(g.sweep_cnt); dfree(g.pk_row); dfree(g.pk_col);
     graph_insert_free(g);
     if (g.ins_stream) (void)hipStreamDestroy(g.ins_stream);
     g = Graph{};
@@ -134,7 +134,23 @@ int load_csr(Graph& g, int32_t n, int32_t e, const int32_t* row, const int32_t* 
     if (e > 0) MARS_HIP(hipMemcpy(g.col, col, size_t(e) * sizeof(int32_t), kind));
     g.e = e;
     g.e_used = e;
+    ++g.csr_version;
     return MARS_OK;
+}
+
+// Packed CSR export: row i's live slots col[start, start + len) copied to
+// out[off[i], off[i + 1]), 16 lanes per row (one DPP row group), grid-stride.
+__global__ __launch_bounds__(256) void k_pack_csr(const int64_t* __restrict__ ro, const int32_t* __restrict__ col,
+                                                  const int32_t* __restrict__ off, int32_t* __restrict__ out,
+                                                  int32_t n) {
+    const int sub = int(threadIdx.x & 15u);
+    const int64_t groups = int64_t(gridDim.x) * (blockDim.x / 16);
+    for (int64_t i = (int64_t(blockIdx.x) * blockDim.x + threadIdx.x) / 16; i < n; i += groups) {
+        const int64_t w = ro[i];
+        const int32_t b = int32_t(uint32_t(w)), len = int32_t(w >> 32);
+        const int32_t o = off[i];
+        for (int32_t j = sub; j < len; j += 16) out[o + j] = col[b + j];
+    }
 }
 
 void graph_slot_free(Ctx::GraphSlot& g);
@@ -161,13 +177,14 @@ int ctx_free(Ctx& c) {
     (void)use_device(c.device);
     if (c.stream) (void)hipStreamSynchronize(c.stream);
     dfree(c.query); dfree(c.fin); dfree(c.part); dfree(c.vis); dfree(c.claim); dfree(c.vlist);
-    dfree(c.vhop); dfree(c.vscore); dfree(c.vro); dfree(c.sortbuf); dfree(c.seed_idx); dfree(c.seed_val); dfree(c.stamps);
+    dfree(c.vhop); dfree(c.vscore); dfree(c.vro); dfree(c.sortbuf); dfree(c.seed_idx); dfree(c.seed_val);
     dfree(c.gthr); dfree(c.gcnt); dfree(c.hopmap);
     dfree(c.bq); dfree(c.btq); dfree(c.bpart); dfree(c.bout);
     multi_free(c);
     if (c.h_query) (void)hipHostFree(c.h_query);
     if (c.h_res) (void)hipHostFree(c.h_res);
     if (c.h_done) (void)hipHostFree(c.h_done);
+    if (c.h_stamps) (void)hipHostFree(c.h_stamps);
     for (auto& e : c.ev) if (e) (void)hipEventDestroy(e);
     graph_slot_free(c.g_global);
     graph_slot_free(c.g_episode);
@@ -337,9 +354,9 @@ int query_impl(const mars_graph* gh, mars_ctx* ch, const float* h_q, const float
     const int32_t K = std::min(cfg->top_k, c.max_k);                      // memory_cuda.cu:1361
     const bool scoped = episode_scoped_active(g, *cfg);
     const int32_t hops = scoped ? 0 : std::max(0, cfg->bfs_max_hops);     // :1189
-    const int32_t rcap = cfg->max_results_returned > 0 ? cfg->max_results_returned : K;
-    MARS_CHECK(rcap <= c.res_cap, MARS_ERR_UNSUPPORTED, "max_results_returned %d exceeds %d", rcap,
-               c.res_cap);
+    // results: max_results_returned (else K), at most the context's compaction cap
+    // min(max_nodes, max_k * 500) (memory_cuda.cu:1059, 1421-1447)
+    const int32_t rcap = std::min(cfg->max_results_returned > 0 ? cfg->max_results_returned : K, c.res_cap);
     MARS_TRY(use_device(c.device));
     hipStream_t s = c.stream;
     const bool timing = (c.flags & MARS_CTX_TIMING) != 0;
@@ -374,10 +391,15 @@ int query_impl(const mars_graph* gh, mars_ctx* ch, const float* h_q, const float
                     float ms = 0.0f;
                     MARS_HIP(hipEventElapsedTime(&ms, c.ev[0], c.ev[1]));
                     st.gpu_ms_similarity = ms;
-                    MARS_HIP(hipEventElapsedTime(&ms, c.ev[1], c.ev[2]));
-                    st.gpu_ms_bfs = ms;
                     MARS_HIP(hipEventElapsedTime(&ms, c.ev[0], c.ev[2]));
                     st.gpu_ms_total = ms;
+                    MARS_HIP(hipEventElapsedTime(&ms, c.ev[1], c.ev[2]));
+                    // certificate stamps (from t[4]): candidate merge and exact rescoring +
+                    // certificate select the seeds; BFS, marking, exact scores and the results
+                    // follow (the single-kernel form; the two-kernel form stamps the first part)
+                    const uint64_t* t = c.h_stamps + 4;
+                    st.gpu_ms_topk = std::min(ms, float(double(t[2] - t[0]) * 1e-5));
+                    st.gpu_ms_bfs = std::max(0.0f, ms - st.gpu_ms_topk);
                 }
                 st.nodes_scanned = n_live;
                 st.bfs_waves = cfg->bfs_max_hops;
@@ -489,12 +511,19 @@ int query_impl(const mars_graph* gh, mars_ctx* ch, const float* h_q, const float
             float ms = 0.0f;
             MARS_HIP(hipEventElapsedTime(&ms, c.ev[0], c.ev[1]));
             st.gpu_ms_similarity = ms;
-            MARS_HIP(hipEventElapsedTime(&ms, c.ev[1], c.ev[2]));
-            st.gpu_ms_bfs = ms;
             MARS_HIP(hipEventElapsedTime(&ms, c.ev[0], c.ev[2]));
             st.gpu_ms_total = ms;
+            MARS_HIP(hipEventElapsedTime(&ms, c.ev[1], c.ev[2]));
+            if (scoped) {
+                st.gpu_ms_topk = ms;                       // the episode kernel selects as it scores
+            } else {
+                // finalize stamps: start, seeds merged, BFS done, results written
+                const uint64_t* t = c.h_stamps;
+                st.gpu_ms_topk = float(double(t[1] - t[0]) * 1e-5);   // 100 MHz counter
+                st.gpu_ms_bfs = std::max(0.0f, ms - st.gpu_ms_topk);
+            }
         }
-        // rerank / top-K are fused into the scan: their time is inside gpu_ms_similarity
+        // the decay (the reference's rerank stage) is fused into the scan: gpu_ms_rerank = 0
         st.nodes_scanned = scoped ? cfg->query_episode_member_count : n_live;
         st.bfs_waves = scoped ? 0 : cfg->bfs_max_hops;                     // :1680-1686 semantics
         st.scope_fallback = (cfg->retrieval_scope == MARS_SCOPE_EPISODE_SCOPED && !scoped) ? 1 : 0;
@@ -807,6 +836,46 @@ int mars_graph_download(const mars_graph* gh, int32_t* row, int32_t* col, int32_
     return MARS_OK;
 }
 
+int mars_graph_packed_csr(mars_graph* gh, const int32_t** d_row_offsets, const int32_t** d_col_indices) {
+    MARS_CHECK(gh && d_row_offsets && d_col_indices, MARS_ERR_INVALID, "null argument");
+    std::lock_guard<std::mutex> lock(gh->mu);
+    Graph& g = gh->g;
+    MARS_TRY(use_device(g.device));
+    if (g.pk_row && g.pk_version == g.csr_version && g.pk_cap_n >= int64_t(g.n) + 1) {
+        *d_row_offsets = g.pk_row;
+        *d_col_indices = g.pk_col;
+        return MARS_OK;
+    }
+    if (g.ins_stream) MARS_HIP(hipStreamSynchronize(g.ins_stream));
+    const int32_t n = g.n;
+    std::vector<int32_t> off(size_t(n) + 1, 0);
+    for (int32_t i = 0; i < n; ++i) off[size_t(i) + 1] = off[size_t(i)] + int32_t(g.ro_h[size_t(i)] >> 32);
+    const int64_t ne = off[size_t(n)];
+    if (g.pk_cap_n < int64_t(n) + 1) {
+        dfree(g.pk_row);
+        g.pk_cap_n = 0;
+        MARS_TRY(dmalloc(&g.pk_row, size_t(g.cap_n) + 1));
+        g.pk_cap_n = int64_t(g.cap_n) + 1;
+    }
+    if (g.pk_cap_e < std::max<int64_t>(ne, 1)) {
+        dfree(g.pk_col);
+        g.pk_cap_e = 0;
+        MARS_TRY(dmalloc(&g.pk_col, size_t(std::max<int64_t>(ne, 1))));
+        g.pk_cap_e = std::max<int64_t>(ne, 1);
+    }
+    MARS_HIP(hipMemcpy(g.pk_row, off.data(), off.size() * sizeof(int32_t), hipMemcpyHostToDevice));
+    if (ne > 0) {
+        const int64_t blocks = std::min<int64_t>((int64_t(n) * 16 + 255) / 256, 65536);
+        MARS_LAUNCH(k_pack_csr, dim3(unsigned(std::max<int64_t>(blocks, 1))), dim3(256), 0, g.ins_stream, g.ro,
+                    g.col, g.pk_row, g.pk_col, n);
+        MARS_HIP(hipStreamSynchronize(g.ins_stream));
+    }
+    g.pk_version = g.csr_version;
+    *d_row_offsets = g.pk_row;
+    *d_col_indices = g.pk_col;
+    return MARS_OK;
+}
+
 // MARS v1 checkpoint of the device graph: the published nodes (inserts included) as
 // the packed CSR, fp32 rows, modalities and timestamps, streamed to the file in 64 MB
 // pieces. Holds the graph's lock, so an insert lands wholly before or after it.
@@ -866,7 +935,7 @@ int mars_ctx_create(int32_t max_nodes, int32_t dim, int32_t max_k, uint32_t flag
     c.max_k = std::min(max_k, kMaxK);                       // memory_cuda.cu:1036
     c.flags = flags;
     c.max_wg = kMaxWg;
-    c.res_cap = kSortCap;
+    c.res_cap = std::max(1, std::min(max_nodes, c.max_k * kCompactPerK));   // memory_cuda.cu:1059
     const size_t N = size_t(max_nodes);
     int rc = MARS_OK;
     auto fail = [&](int r) { ctx_free(c); delete ch; return r; };
@@ -877,14 +946,14 @@ int mars_ctx_create(int32_t max_nodes, int32_t dim, int32_t max_k, uint32_t flag
         (rc = dmalloc(&c.claim, N)) || (rc = dmalloc(&c.vlist, N)) || (rc = dmalloc(&c.vhop, N)) ||
         (rc = dmalloc(&c.vscore, N)) || (rc = dmalloc(&c.vro, 2 * N)) || (rc = dmalloc(&c.sortbuf, 2 * size_t(kSortCap))) ||
         (rc = dmalloc(&c.seed_idx, size_t(kMaxK))) || (rc = dmalloc(&c.seed_val, size_t(kMaxK))) ||
-        (rc = dmalloc(&c.stamps, 12)) || (rc = dmalloc(&c.gthr, 1)) || (rc = dmalloc(&c.gcnt, 1)))
+        (rc = dmalloc(&c.gthr, 1)) || (rc = dmalloc(&c.gcnt, 1)))
         return fail(rc);
     e = hipMemset(c.vis, 0, N * sizeof(uint32_t));
     if (e == hipSuccess) e = hipMemset(c.gthr, 0xFF, sizeof(uint64_t));
     if (e == hipSuccess) e = hipMemset(c.gcnt, 0, sizeof(uint32_t));
     if (e == hipSuccess) e = hipMemset(c.claim, 0xFF, N * sizeof(uint64_t));
     if (e == hipSuccess) e = hipHostMalloc(reinterpret_cast<void**>(&c.h_query), size_t(dim) * sizeof(float));
-    const size_t res_bytes = sizeof(ResultHeader) + size_t(kSortCap) * sizeof(mars_query_result);
+    const size_t res_bytes = sizeof(ResultHeader) + size_t(c.res_cap) * sizeof(mars_query_result);
     if (e == hipSuccess)
         e = hipHostMalloc(reinterpret_cast<void**>(&c.h_res), res_bytes, hipHostMallocMapped);
     void* dres = nullptr;
@@ -900,6 +969,13 @@ int mars_ctx_create(int32_t max_nodes, int32_t dim, int32_t max_k, uint32_t flag
     if (e != hipSuccess) return fail(set_error(MARS_ERR_NOMEM, "context setup: %s", hipGetErrorString(e)));
     *c.h_done = 0u;
     c.d_done = static_cast<uint32_t*>(ddone);
+    // phase stamps: written by the last kernels of a query, read on the host after it
+    void* dst = nullptr;
+    e = hipHostMalloc(reinterpret_cast<void**>(&c.h_stamps), 12 * sizeof(uint64_t), hipHostMallocMapped);
+    if (e == hipSuccess) e = hipHostGetDevicePointer(&dst, c.h_stamps, 0);
+    if (e != hipSuccess) return fail(set_error(MARS_ERR_NOMEM, "context setup: %s", hipGetErrorString(e)));
+    std::memset(c.h_stamps, 0, 12 * sizeof(uint64_t));
+    c.stamps = static_cast<uint64_t*>(dst);
     for (auto& ev : c.ev) {
         e = hipEventCreate(&ev);
         if (e != hipSuccess) return fail(set_error(MARS_ERR_HIP, "event: %s", hipGetErrorString(e)));
@@ -918,6 +994,12 @@ int mars_ctx_destroy(mars_ctx* ch) {
 int mars_ctx_set_flags(mars_ctx* ch, uint32_t flags) {
     MARS_CHECK(ch, MARS_ERR_INVALID, "null context");
     ch->c.flags = flags;
+    return MARS_OK;
+}
+
+int mars_ctx_get_stream(const mars_ctx* ch, void** stream) {
+    MARS_CHECK(ch && stream, MARS_ERR_INVALID, "null argument");
+    *stream = static_cast<void*>(ch->c.stream);
     return MARS_OK;
 }
 
@@ -997,7 +1079,27 @@ int mars_bench_queries(const mars_graph* g, mars_ctx* c, const float* dq, int64_
         if (rc != MARS_OK) return rc;
         lat_us[i] = std::chrono::duration<double, std::micro>(t1 - t0).count();
         if (kern_us) kern_us[i] = st.gpu_ms_similarity * 1000.0f;
-        if (bfs_us) bfs_us[i] = st.gpu_ms_bfs * 1000.0f;
+        if (bfs_us) bfs_us[i] = (st.gpu_ms_total - st.gpu_ms_similarity) * 1000.0f;   // after the scan
+        if (n_res) n_res[i] = nr;
+    }
+    return MARS_OK;
+}
+
+int mars_bench_queries_host(const mars_graph* g, mars_ctx* c, const float* hq, int64_t stride, int32_t n,
+                            float t_q, const mars_retrieval_config* cfgs, int32_t n_cfg, double* lat_us,
+                            int32_t* n_res) {
+    MARS_CHECK(g && c && hq && cfgs && lat_us && n >= 0 && (n_cfg == 1 || n_cfg == n) && stride >= g->g.d,
+               MARS_ERR_INVALID, "bad benchmark arguments");
+    mars_query_result out[64];
+    for (int32_t i = 0; i < n; ++i) {
+        mars_stats st{};
+        int32_t nr = 0;
+        const auto t0 = std::chrono::steady_clock::now();
+        const int rc = query_impl(g, c, hq + int64_t(i) * stride, nullptr, t_q, &cfgs[n_cfg == 1 ? 0 : i], out, 64,
+                                  &nr, &st);
+        const auto t1 = std::chrono::steady_clock::now();
+        if (rc != MARS_OK) return rc;
+        lat_us[i] = std::chrono::duration<double, std::micro>(t1 - t0).count();
         if (n_res) n_res[i] = nr;
     }
     return MARS_OK;
@@ -1340,8 +1442,7 @@ int mars_query_global_batch_knn(const mars_graph* gh, mars_ctx* ch, const float*
         K = std::min(cfg->top_k, c.max_k);
         const bool scoped = episode_scoped_active(g, *cfg);
         hops = scoped ? 0 : std::max(0, cfg->bfs_max_hops);
-        rcap = cfg->max_results_returned > 0 ? cfg->max_results_returned : K;
-        MARS_CHECK(rcap <= c.res_cap, MARS_ERR_UNSUPPORTED, "max_results_returned %d exceeds %d", rcap, c.res_cap);
+        rcap = std::min(cfg->max_results_returned > 0 ? cfg->max_results_returned : K, c.res_cap);
         fp16 = (c.flags & MARS_CTX_USE_FP16) && g.emb16 != nullptr;
         const bool boost = g.ep_ids && cfg->query_episode_id >= 0 && cfg->episode_same_boost > 0.0f;
         lambda = cfg->time_decay_lambda;
@@ -1635,8 +1736,7 @@ int mars_ctx_last_phases(mars_ctx* ch, double* us, int32_t n) {
     MARS_CHECK(ch && us && n >= 0 && n <= 6, MARS_ERR_INVALID, "bad arguments");
     MARS_TRY(use_device(ch->c.device));
     MARS_HIP(hipStreamSynchronize(ch->c.stream));
-    uint64_t t[12] = {};
-    MARS_HIP(hipMemcpy(t, ch->c.stamps, sizeof(t), hipMemcpyDeviceToHost));
+    const uint64_t* t = ch->c.h_stamps;
     const uint64_t* p = ch->c.last_certified ? t + 4 : t;     // certified: 7 stamps from t[4]
     const int32_t np = ch->c.last_certified ? 6 : 3;
     for (int32_t i = 0; i < n; ++i) us[i] = i < np ? double(p[i + 1] - p[i]) * 0.01 : 0.0;   // 100 MHz counter

@@ -14,17 +14,25 @@
 //    SHUTDOWN {"cmd":"SHUTDOWN"}                             -> {"ok":true}, then exit
 //  Errors: {"ok":false,"error":"..."}.
 //
-//  The graph lives on the device: ADD appends through the streaming insert (k-NN
-//  edges among the nodes present, the k nearest by cosine), an ADD of an existing id
-//  rewrites its row in place, and an id past the end first appends zero rows for the
-//  gap, as the reference's host graph grows; embeddings are L2-normalised on arrival
-//  (fp32 sum of squares in order, sqrt + 1e-8, as the reference). DELETE leaves a tombstone (zero row, timestamp -1).
+//  The graph lives on the device: ADD appends through the streaming insert, an ADD
+//  of an existing id rewrites its row in place, and an id past the end first appends
+//  zero rows for the gap, as the reference's host graph grows; embeddings are
+//  L2-normalised on arrival (fp32 sum of squares in order, sqrt + 1e-8, as the
+//  reference). DELETE leaves a tombstone (zero row, timestamp -1).
+//  Edges (--edges):
+//    nsn  (default) the reference server's: before a QUERY, the NSN graph
+//         (build_nsn_edges(6, 0.15), memory_graph.cpp:102-189) is rebuilt over all
+//         nodes on the first query, once the node count has doubled, or once more
+//         than 1000 nodes arrived since the last build (engine_server.cu:187-200);
+//         only the CSR is replaced, the rows stay resident. Nodes added since the last
+//         build have no edges yet.
+//    knn  each ADD links the new node to its --knn nearest neighbours by cosine.
 //  QUERY runs the certified path (fp16 scan, answers bit-identical to the fp32 path;
 //  a query it cannot certify is answered by the fp32 path) with the reference server's
-//  decay 1e-8 and hop decay 0.5. SAVE / LOAD write and read MARS v1 checkpoints (the reference's are
-//  stubs). No GPU call is made before the first ADD or LOAD.
+//  decay 1e-8 and hop decay 0.5. SAVE / LOAD write and read MARS v1 checkpoints (the
+//  reference's are stubs). No GPU call is made before the first ADD or LOAD.
 //
-//  Usage: mars_engine [--dim 768] [--capacity 1000000] [--knn 8]
+//  Usage: mars_engine [--dim 768] [--capacity 1000000] [--edges nsn|knn] [--knn 8]
 // ============================================================================
 #include "mars_amd.h"
 
@@ -188,9 +196,12 @@ struct Engine {
     int32_t dim = 768;
     int32_t capacity = 1000000;
     int32_t knn = 8;
+    bool nsn = true;                 // --edges nsn: the reference server's rebuild policy
     mars_graph* g = nullptr;
     mars_ctx* ctx = nullptr;
     int32_t n = 0;
+    std::vector<int32_t> mods;       // host copy of every node's modality (the NSN bridges read it)
+    int32_t last_rebuild = 0;        // node count of the last NSN build (0: none yet)
 
     ~Engine() { drop(); }
 
@@ -224,7 +235,25 @@ struct Engine {
             return rc;
         }
         n = nodes;
+        this->mods.assign(mods, mods + nodes);
+        last_rebuild = edges > 0 ? nodes : 0;        // a loaded graph keeps its edges until the next rebuild
         return MARS_OK;
+    }
+
+    // ensure_device of the reference server (engine_server.cu:187-200): the NSN graph over
+    // all nodes on the first query, after the node count doubled, or after 1000 more.
+    int ensure_edges() {
+        if (!nsn || !g || n <= 0) return MARS_OK;
+        if (last_rebuild != 0 && n < 2 * last_rebuild && n - last_rebuild <= 1000) return MARS_OK;
+        int64_t bound = 0;
+        int rc = mars_nsn_edges(n, mods.data(), 6, 0.15, MARS_NSN_ALL, nullptr, nullptr, 0, &bound);
+        if (rc != MARS_OK) return rc;
+        std::vector<int32_t> ro(size_t(n) + 1), col(size_t(bound > 0 ? bound : 1));
+        int64_t ne = 0;
+        rc = mars_nsn_edges(n, mods.data(), 6, 0.15, MARS_NSN_ALL, ro.data(), col.data(), int64_t(col.size()), &ne);
+        if (rc == MARS_OK) rc = mars_graph_set_csr(g, int32_t(ne), ro.data(), ne > 0 ? col.data() : nullptr);
+        if (rc == MARS_OK) last_rebuild = n;
+        return rc;
     }
 
     // ADD: rows id (normalised) after zero rows for any gap; an existing id is rewritten.
@@ -235,7 +264,11 @@ struct Engine {
         for (const float x : e) sq += x * x;
         const float norm = std::sqrt(sq) + 1e-8f;
         for (float& x : row) x /= norm;
-        if (g && id < n) return mars_graph_set_rows(g, id, 1, row.data(), &modality, &t);
+        if (g && id < n) {
+            const int rc = mars_graph_set_rows(g, id, 1, row.data(), &modality, &t);
+            if (rc == MARS_OK) this->mods[size_t(id)] = modality;
+            return rc;
+        }
         const int32_t first = g ? n : 0;
         const int32_t count = id - first + 1;
         std::vector<float> rows(size_t(count) * size_t(dim), 0.0f);
@@ -249,8 +282,11 @@ struct Engine {
             return create(count, 0, ro.data(), nullptr, rows.data(), mods.data(), ts.data());
         }
         const int rc = mars_graph_insert(g, count, rows.data(), mods.data(), ts.data(), nullptr,
-                                         n >= knn ? knn : 0, nullptr, nullptr);
-        if (rc == MARS_OK) n += count;
+                                         (!nsn && n >= knn) ? knn : 0, nullptr, nullptr);
+        if (rc == MARS_OK) {
+            n += count;
+            this->mods.insert(this->mods.end(), mods.begin(), mods.end());
+        }
         return rc;
     }
 
@@ -270,6 +306,11 @@ int main(int argc, char** argv) {
         if (!std::strcmp(argv[i], "--dim")) eng.dim = std::atoi(argv[i + 1]);
         else if (!std::strcmp(argv[i], "--capacity")) eng.capacity = std::atoi(argv[i + 1]);
         else if (!std::strcmp(argv[i], "--knn")) eng.knn = std::atoi(argv[i + 1]);
+        else if (!std::strcmp(argv[i], "--edges")) {
+            if (!std::strcmp(argv[i + 1], "nsn")) eng.nsn = true;
+            else if (!std::strcmp(argv[i + 1], "knn")) eng.nsn = false;
+            else eng.knn = -1;                         // rejected below
+        }
     }
     if (eng.dim <= 0 || eng.capacity <= 0 || eng.knn < 0 || eng.knn > 16) {
         std::fprintf(stderr, "mars_engine: bad arguments\n");
@@ -312,6 +353,10 @@ int main(int argc, char** argv) {
             }
             if (!eng.g) {
                 respond("{\"results\":[]}");
+                continue;
+            }
+            if (eng.ensure_edges() != MARS_OK) {
+                respond_error(last_error());
                 continue;
             }
             mars_retrieval_config cfg;

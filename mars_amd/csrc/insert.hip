@@ -322,6 +322,7 @@ int commit_patch(Graph& g, Patch& p, hipStream_t s) {
     if (p.cursor > p.base) g.e_used = p.cursor;
     g.max_deg = p.max_deg;
     g.e = int32_t(std::min<int64_t>(int64_t(g.e) + p.added, INT32_MAX));
+    ++g.csr_version;
     return MARS_OK;
 }
 

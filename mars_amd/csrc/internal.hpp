@@ -85,7 +85,8 @@ void batch_grid(int64_t n, int32_t q, int32_t* n_rranges, int32_t* n_qblocks, in
                 int32_t max_ranges = 256);
 
 constexpr int kMaxK = 64;              // seeds per query (wave-held list), as MAX_TOP_K
-constexpr int kSortCap = 8192;         // results sorted in LDS by the finalize kernel
+constexpr int kSortCap = 8192;         // results sorted in LDS by the finalize kernel (one band)
+constexpr int kCompactPerK = 500;      // result cap per seed slot: the reference's max_compact = max_k * 500
 constexpr int kFrontierChunk = 4096;   // frontier nodes per BFS chunk (LDS)
 constexpr uint64_t kEmptyKey = ~0ull;
 // batched global queries: fp16 candidates per query (the batched scan's list), and
@@ -168,6 +169,13 @@ struct Graph {
     int32_t* imp_ids = nullptr;          // device copy of host-supplied boost ids
     int64_t imp_ids_cap = 0;
     unsigned long long* sweep_cnt = nullptr;   // edges counted by the maintenance sweep
+    // the packed CSR export (mars_graph_packed_csr), rebuilt when csr_version moved on
+    uint64_t csr_version = 0;            // bumped by every change of the edge set
+    uint64_t pk_version = ~0ull;
+    int32_t* pk_row = nullptr;           // [pk_cap_n + 1]
+    int32_t* pk_col = nullptr;           // [pk_cap_e]
+    int64_t pk_cap_n = 0;
+    int64_t pk_cap_e = 0;
 };
 
 // Result staging written by the finalize / episode kernels straight into
@@ -201,7 +209,8 @@ struct Ctx {
     int64_t* vro = nullptr;        // max_nodes: row (len << 32 | start) of each visited node
     uint64_t* sortbuf = nullptr;   // max_nodes keys (large-result fallback)
     int32_t* seed_idx = nullptr;   // kMaxK
-    uint64_t* stamps = nullptr;    // finalize phase stamps (100 MHz realtime counter)
+    uint64_t* stamps = nullptr;    // phase stamps (100 MHz realtime counter): device alias of h_stamps
+    uint64_t* h_stamps = nullptr;  // 12 stamps in pinned, mapped host memory
     float* seed_val = nullptr;     // kMaxK
     // pinned host staging
     float* h_query = nullptr;      // d

@@ -459,31 +459,11 @@ __device__ inline void write_result(const FinalizeArgs& a, int j, uint64_t key, 
     a.rec[j] = r;
 }
 
-// Results by full sort of the visit set (bitonic in LDS, radix select beyond).
-__device__ void select_sorted(FinShared& sh, const FinalizeArgs& a, int V, int rc) {
+// Key of rank `need` (1-based, ascending) among the V visit keys: eight 8-bit radix
+// passes over the visit list, counting in LDS.
+__device__ uint64_t radix_select_key(FinShared& sh, const FinalizeArgs& a, int V, int need) {
     const int tid = int(threadIdx.x);
-    if (V <= kSortCap) {
-        int n2 = 1;
-        while (n2 < V) n2 <<= 1;
-        for (int i = tid; i < n2; i += kFinThreads) {
-            if (i < V) {
-                sh.u.sort.key[i] = make_key(ld_coherent(a.vscore + i), uint32_t(ld_coherent(a.vlist + i)));
-                sh.u.sort.pay[i] = uint16_t(i);
-            } else {
-                sh.u.sort.key[i] = kEmptyKey;
-                sh.u.sort.pay[i] = 0;
-            }
-        }
-        __syncthreads();
-        block_bitonic(sh.u.sort.key, sh.u.sort.pay, n2);
-        for (int j = tid; j < rc; j += kFinThreads)
-            write_result(a, j, sh.u.sort.key[j], ld_coherent(a.vhop + sh.u.sort.pay[j]));
-        return;
-    }
-    // radix-select the key of rank rc (keys are unique), then sort the rc smallest
-    // (rc <= kSortCap is enforced by the host)
     uint64_t prefix = 0, mask = 0;
-    int need = rc;
     for (int shift = 56; shift >= 0; shift -= 8) {
         for (int i = tid; i < 256; i += kFinThreads) sh.u.hist[i] = 0;
         __syncthreads();
@@ -507,33 +487,69 @@ __device__ void select_sorted(FinShared& sh, const FinalizeArgs& a, int V, int r
         need = sh.s_misc[2];
         __syncthreads();
     }
-    int base = 0;
-    for (int r0 = 0; r0 < V; r0 += kFinThreads) {
-        const int i = r0 + tid;
-        uint64_t key = kEmptyKey;
-        bool take = false;
-        if (i < V) {
-            key = make_key(ld_coherent(a.vscore + i), uint32_t(ld_coherent(a.vlist + i)));
-            take = key <= prefix;
+    return prefix;
+}
+
+// Results by full sort of the visit set (bitonic in LDS, radix select beyond).
+__device__ void select_sorted(FinShared& sh, const FinalizeArgs& a, int V, int rc) {
+    const int tid = int(threadIdx.x);
+    if (V <= kSortCap) {
+        int n2 = 1;
+        while (n2 < V) n2 <<= 1;
+        for (int i = tid; i < n2; i += kFinThreads) {
+            if (i < V) {
+                sh.u.sort.key[i] = make_key(ld_coherent(a.vscore + i), uint32_t(ld_coherent(a.vlist + i)));
+                sh.u.sort.pay[i] = uint16_t(i);
+            } else {
+                sh.u.sort.key[i] = kEmptyKey;
+                sh.u.sort.pay[i] = 0;
+            }
         }
-        int tot = 0;
-        const int o = block_excl_scan(take ? 1 : 0, sh.s_wave, &tot);
-        if (take) { a.sortbuf[2 * (base + o)] = key; a.sortbuf[2 * (base + o) + 1] = uint64_t(i); }
-        base += tot;
+        __syncthreads();
+        block_bitonic(sh.u.sort.key, sh.u.sort.pay, n2);
+        for (int j = tid; j < rc; j += kFinThreads)
+            write_result(a, j, sh.u.sort.key[j], ld_coherent(a.vhop + sh.u.sort.pay[j]));
+        return;
     }
-    __threadfence();
-    __syncthreads();
-    int n2 = 1;
-    while (n2 < rc) n2 <<= 1;
-    for (int i = tid; i < n2; i += kFinThreads) {
-        sh.u.sort.key[i] = (i < rc) ? ld_coherent(a.sortbuf + 2 * i) : kEmptyKey;
-        sh.u.sort.pay[i] = uint16_t(i < rc ? i : 0);
-    }
-    __syncthreads();
-    block_bitonic(sh.u.sort.key, sh.u.sort.pay, n2);
-    for (int j = tid; j < rc; j += kFinThreads) {
-        const int pos = int(ld_coherent(a.sortbuf + 2 * sh.u.sort.pay[j] + 1));
-        write_result(a, j, sh.u.sort.key[j], ld_coherent(a.vhop + pos));
+    // Keys are unique. Results go out in bands of at most kSortCap ranks: radix-select
+    // the key of the band's last rank, gather the band's keys (above the previous
+    // band's last key, at most this one), sort them in LDS and write them. Up to
+    // kResultCap results take ceil(rc / kSortCap) bands.
+    uint64_t lo_key = 0;
+    for (int done = 0; done < rc;) {
+        const int band = min(kSortCap, rc - done);
+        const uint64_t hi_key = radix_select_key(sh, a, V, done + band);
+        int base = 0;
+        for (int r0 = 0; r0 < V; r0 += kFinThreads) {
+            const int i = r0 + tid;
+            uint64_t key = kEmptyKey;
+            bool take = false;
+            if (i < V) {
+                key = make_key(ld_coherent(a.vscore + i), uint32_t(ld_coherent(a.vlist + i)));
+                take = key <= hi_key && (done == 0 || key > lo_key);
+            }
+            int tot = 0;
+            const int o = block_excl_scan(take ? 1 : 0, sh.s_wave, &tot);
+            if (take) { a.sortbuf[2 * (base + o)] = key; a.sortbuf[2 * (base + o) + 1] = uint64_t(i); }
+            base += tot;
+        }
+        __threadfence();
+        __syncthreads();
+        int n2 = 1;
+        while (n2 < band) n2 <<= 1;
+        for (int i = tid; i < n2; i += kFinThreads) {
+            sh.u.sort.key[i] = (i < band) ? ld_coherent(a.sortbuf + 2 * i) : kEmptyKey;
+            sh.u.sort.pay[i] = uint16_t(i < band ? i : 0);
+        }
+        __syncthreads();
+        block_bitonic(sh.u.sort.key, sh.u.sort.pay, n2);
+        for (int j = tid; j < band; j += kFinThreads) {
+            const int pos = int(ld_coherent(a.sortbuf + 2 * sh.u.sort.pay[j] + 1));
+            write_result(a, done + j, sh.u.sort.key[j], ld_coherent(a.vhop + pos));
+        }
+        __syncthreads();                        // LDS and sortbuf are reused by the next band
+        done += band;
+        lo_key = hi_key;
     }
 }
 

@@ -32,9 +32,15 @@ void refresh_view(DeviceMemoryGraph& d) {
     d.num_nodes = v.num_nodes;
     d.num_edges = v.num_edges;
     d.embedding_dim = v.embedding_dim;
-    d.d_row_offsets = nullptr;                       // rows are (start, length) words: d_row_words
+    // the reference's packed CSR (a copy, rebuilt when the edges changed); the queries
+    // read the row words and their column slots
+    const int32_t* prow = nullptr;
+    const int32_t* pcol = nullptr;
+    die_on(mars_graph_packed_csr(d.handle, &prow, &pcol), "mars_graph_packed_csr");
+    d.d_row_offsets = const_cast<int32_t*>(prow);
+    d.d_col_indices = const_cast<int32_t*>(pcol);
     d.d_row_words = static_cast<int64_t*>(v.d_row_words);
-    d.d_col_indices = static_cast<int32_t*>(v.d_col_indices);
+    d.d_col_slots = static_cast<int32_t*>(v.d_col_indices);
     d.d_embeddings = static_cast<float*>(v.d_embeddings);
     d.d_embeddings_fp16 = v.d_embeddings_fp16;
     d.d_modalities = static_cast<int32_t*>(v.d_modalities);
@@ -187,6 +193,7 @@ QueryContext create_query_context(int32_t max_nodes, int32_t embedding_dim, int3
     ctx.max_nodes = max_nodes;
     ctx.embedding_dim = embedding_dim;
     ctx.max_k = std::min(max_k, 64);
+    die_on(mars_ctx_get_stream(ctx.handle, &ctx.stream), "create_query_context");
     ctx.valid = true;
     return ctx;
 }

@@ -202,6 +202,32 @@ def bfs(row, col, fin, seeds, seed_vals, hops: int, decay: float):
     return dict(ids=ids[:m], hops=hp[:m], scores=sc[:m], parent=par[:m], hop_by_node=hop_by, levels=lv.value)
 
 
+def bfs_scales(b, scale, decay):
+    """Error scale of each visited node's BFS score, in the visit order of bfs() output b:
+    a seed keeps scale[seed]; a node reached from the node at visit position p takes
+    max(|decay| * scale_p, 0.8 * scale[node]), the scales of the two terms its score is the
+    larger of (memory_cuda.cu:686-693). A score that is within rtol of each term's scale is
+    within rtol * this scale of the oracle's, because max() is 1-Lipschitz."""
+    ids, par = b["ids"], b["parent"]
+    out = np.empty(len(ids), np.float64)
+    for j in range(len(ids)):
+        p = int(par[j])
+        u = int(ids[j])
+        out[j] = scale[u] if p < 0 else max(abs(decay) * out[p], 0.8 * scale[u])
+    return out
+
+
+def result_scales(g: "Graph", q, t_q: float, cfg: "OracleConfig", ref: dict) -> dict:
+    """node id -> error scale of its result score for query() output ref (the BFS from
+    ref's seeds; the per-row scale w * sum_d |e_d q_d| from scores(), times (1 + boost))."""
+    _, scale = scores(g, q, t_q, cfg.time_decay_lambda, cfg.modality_filter)
+    if cfg.episode_same_boost > 0:
+        scale = scale * (1.0 + cfg.episode_same_boost)
+    hops = 0 if ref["scoped"] else max(0, cfg.bfs_max_hops)
+    b = bfs(g.row_offsets, g.col_indices, ref["final"], ref["seeds"], ref["seed_vals"], hops, cfg.bfs_score_decay)
+    return dict(zip(b["ids"].tolist(), bfs_scales(b, scale, cfg.bfs_score_decay).tolist()))
+
+
 def config(top_k=10, bfs_max_hops=2, time_decay_lambda=1e-8, bfs_score_decay=0.5, modality_filter=-1,
            max_results_returned=-1, retrieval_scope=0, query_episode_id=-1, query_episode_member_begin=0,
            query_episode_member_count=0, episode_same_boost=0.0) -> OracleConfig:

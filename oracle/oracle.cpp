@@ -557,9 +557,10 @@ int64_t oracle_link_edges(int32_t n, const int32_t* row, const int32_t* col, int
 // Probe sample of the kids sweep: demos/embodied_scene/bench_kids_sweep.cu:624-632.
 // std::mt19937 seeded uint32(N) ^ 0xA5A5A5A5 and uniform_int_distribution<size_t>
 // over [0, n_image - 1] (the same engine and distribution of this C++ library);
-// out[p] = the index into the IMAGE-node list of probe p. Parity unpinned: nothing
-// here checks the sample against the reference's (its sweep is CUDA code); the sample
-// only chooses which nodes an outcome check queries.
+// out[p] = the index into the IMAGE-node list of probe p. Pinned by tests/test_oracle.py
+// against numpy's MT19937 (the standard's seeding; the standard's 10000th-output known
+// answer) and Lemire's nearly-divisionless method restated there, the algorithm libstdc++
+// uses for a 32-bit engine. The sweep itself is CUDA code and cannot run here.
 // ---------------------------------------------------------------------------
 void oracle_kids_probes(int32_t N, int64_t n_image, int32_t count, int64_t* out) {
     std::mt19937 rng(uint32_t(N) ^ 0xA5A5A5A5u);

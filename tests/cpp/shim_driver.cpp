@@ -13,6 +13,12 @@
 //                                     and "global ..." lines
 //         shim_driver tiled N SEED Q  tiled_query over the host corpus (tiles of N/7):
 //                                     "tiled <node> id:score:mod ..."
+//         shim_driver many N SEED HOPS R  N-node corpus with the reference's NSN graph
+//                                     (build_nsn_edges(6, 0.15)): checks the packed CSR
+//                                     (d_row_offsets / d_col_indices) against the host
+//                                     graph ("packed_csr ok"), then one global query from
+//                                     node 0 with HOPS hops and max_results_returned = R:
+//                                     "stats ..." and "global 0 id:score:mod:hops ..."
 //         shim_driver maintain N SEED Q  the query corpus with importance and edge hits:
 //                                     per query "novelty <node> <max dot>" and "ids <node>
 //                                     <result ids>"; then "importance <fp32 bits in hex>"
@@ -165,10 +171,50 @@ static int tiled_check(int32_t N, uint64_t seed, int32_t Q) {
     return 0;
 }
 
+// Many results (memory_cuda.cu:1059, 1421-1447) and the device-side members of the
+// reference structs (DeviceMemoryGraph::d_row_offsets / d_col_indices, QueryContext::stream,
+// RetrievalStats).
+static int many_check(int32_t N, uint64_t seed, int32_t hops, int32_t max_results) {
+    const int32_t D = 768;
+    MemoryGraph g;
+    std::vector<int32_t> ep;
+    make_corpus(N, D, seed, g, ep);
+    g.build_nsn_edges(6, 0.15);
+    DeviceMemoryGraph dg = upload_to_device(g);
+    std::vector<int32_t> row(size_t(N) + 1), col(size_t(g.num_edges));
+    if (!dg.d_row_offsets || !dg.d_col_indices ||
+        mars_copy_to_host(row.data(), dg.d_row_offsets, row.size() * sizeof(int32_t)) != MARS_OK ||
+        mars_copy_to_host(col.data(), dg.d_col_indices, col.size() * sizeof(int32_t)) != MARS_OK ||
+        row != g.row_offsets || col != g.col_indices) {
+        std::printf("FAIL packed csr\n");
+        return 1;
+    }
+    std::printf("packed_csr ok %d %d\n", N, g.num_edges);
+    QueryContext ctx = create_query_context(N, D, 64);
+    if (!ctx.stream) { std::printf("FAIL stream\n"); return 1; }
+    RetrievalConfig cfg;
+    cfg.top_k = 10;
+    cfg.bfs_max_hops = hops;
+    cfg.time_decay_lambda = 0.1f;
+    cfg.max_results_returned = max_results;
+    RetrievalStats st;
+    auto res = query_memory_fast(dg, ctx, &g.embeddings[0], 600.0f, cfg, st);
+    std::printf("stats similarity=%.6f rerank=%.6f topk=%.6f bfs=%.6f total=%.6f scanned=%d waves=%d\n",
+                st.gpu_ms_similarity, st.gpu_ms_rerank, st.gpu_ms_topk, st.gpu_ms_bfs, st.gpu_ms_total,
+                st.nodes_scanned, st.bfs_waves);
+    print_results("global", 0, res, "");
+    destroy_query_context(ctx);
+    free_device(dg);
+    return 0;
+}
+
 int main(int argc, char** argv) {
     if (argc >= 2 && std::strcmp(argv[1], "host") == 0) return host_checks();
     if (argc >= 4 && std::strcmp(argv[1], "stream") == 0)
         return stream_check(std::atoi(argv[2]), std::strtoull(argv[3], nullptr, 10));
+    if (argc >= 6 && std::strcmp(argv[1], "many") == 0)
+        return many_check(std::atoi(argv[2]), std::strtoull(argv[3], nullptr, 10), std::atoi(argv[4]),
+                          std::atoi(argv[5]));
     if (argc >= 5 && std::strcmp(argv[1], "tiled") == 0)
         return tiled_check(std::atoi(argv[2]), std::strtoull(argv[3], nullptr, 10), std::atoi(argv[4]));
     const bool maintain = argc >= 5 && std::strcmp(argv[1], "maintain") == 0;

@@ -1,13 +1,16 @@
 """The JSON-line engine server (mars_amd/mars_engine) on the GPU.
 
-Bar: the engine adds no semantics of its own over the C ABI. The engine answers on the
-certified path; a replica queried on the fp32 path and built with the same library calls
-the engine makes (first ADD creates the graph, each later ADD is a
-one-node insert with k-NN edges once 8 nodes exist, embeddings normalised as the
-engine does, DELETE as an in-place tombstone) answers every QUERY with the same ids,
-modalities and hops, and scores equal to the engine's 6-decimal output; SAVE writes
-the file the replica's checkpoint writes, byte for byte, and a second engine LOADs it
-and answers the same.
+Default edges (--edges nsn, the reference server's policy, engine_server.cu:187-200): the
+engine's QUERY answers against the CPU oracle on the engine's own graph (read back from its
+SAVE file), whose edges are the reference's NSN builder's at the reference's rebuild points.
+
+--edges knn: the engine adds no semantics of its own over the C ABI. The engine answers on
+the certified path; a replica queried on the fp32 path and built with the same library calls
+the engine makes (first ADD creates the graph, each later ADD is a one-node insert with
+k-NN edges once 8 nodes exist, embeddings normalised as the engine does, DELETE as an
+in-place tombstone) answers every QUERY with the same ids, modalities and hops, and scores
+equal to the engine's 6-decimal output; SAVE writes the file the replica's checkpoint
+writes, byte for byte, and a second engine LOADs it and answers the same.
 """
 from __future__ import annotations
 
@@ -28,9 +31,9 @@ N, D, CAP = 300, 768, 1000
 
 
 class Engine:
-    def __init__(self):
-        self.p = subprocess.Popen([str(ENGINE), "--dim", str(D), "--capacity", str(CAP)], stdin=subprocess.PIPE,
-                                  stdout=subprocess.PIPE, text=True, bufsize=1)
+    def __init__(self, *args):
+        self.p = subprocess.Popen([str(ENGINE), "--dim", str(D), "--capacity", str(CAP), *args],
+                                  stdin=subprocess.PIPE, stdout=subprocess.PIPE, text=True, bufsize=1)
 
     def __call__(self, **req):
         self.p.stdin.write(json.dumps(req) + "\n")
@@ -80,7 +83,7 @@ def same_answer(eng, dg, ctx, q, t, top_k=10, hops=2, filt=-1):
 
 def test_engine_matches_library(tmp_path):
     c = corpus.make_corpus(N, D, seed=91)
-    eng = Engine()
+    eng = Engine("--edges", "knn")
     dg = replica(c)
     ctx = mars_amd.create_query_context(CAP, D, 64)
     eng2 = None
@@ -113,7 +116,7 @@ def test_engine_matches_library(tmp_path):
         assert eng(cmd="SAVE", path=str(tmp_path / "eng.mars")) == {"ok": True}
         mars_amd.save_device_graph(dg, tmp_path / "rep.mars")
         assert (tmp_path / "eng.mars").read_bytes() == (tmp_path / "rep.mars").read_bytes()
-        eng2 = Engine()
+        eng2 = Engine("--edges", "knn")
         assert eng2(cmd="LOAD", path=str(tmp_path / "eng.mars")) == {"ok": True, "n": N}
         for node in qs:
             q = c.embeddings[node].tolist()
@@ -132,3 +135,68 @@ def test_engine_matches_library(tmp_path):
             eng2.close()
         mars_amd.destroy_query_context(ctx)
         mars_amd.free_device(dg)
+
+
+def check_against_oracle(got, g, q, t, top_k, hops, filt):
+    """Engine QUERY results against oracle.query on the engine's graph g (a MemoryGraph read
+    from its SAVE file): the reference server's lambda 1e-8 and hop decay 0.5, K = top_k.
+    Ids, modalities and hops exact up to near-ties; scores within the fp32 bar plus the
+    6-decimal rounding of the response."""
+    import oracle
+    og = oracle.make_graph(g.embeddings, g.modalities, g.timestamps, g.row_offsets, g.col_indices)
+    cfg = oracle.config(top_k, hops, 1e-8, 0.5, filt)
+    ref = oracle.query(og, q, t, cfg)
+    scl = oracle.result_scales(og, q, t, cfg, ref)
+    want = ref["results"]
+    assert len(got) == len(want)
+    for r, w in zip(got, want):
+        tol = 1e-5 * max(abs(w[1]), scl[w[0]]) + 5e-7
+        if r["id"] == w[0]:
+            assert abs(r["score"] - w[1]) <= tol and (r["modality"], r["hops"]) == (w[2], w[3]), (r, w)
+        else:
+            assert abs(r["score"] - w[1]) <= 2 * tol, (r, w)
+
+
+def test_engine_nsn_edges_against_oracle(tmp_path):
+    """ADDs in two waves around the reference's rebuild points: the first QUERY builds the
+    NSN graph over 1,300 nodes; 600 more nodes (under 1000 new, not doubled) get no edges
+    and leave the graph as it was; 800 more (1,400 since the build) trigger a rebuild over
+    all 2,700. After each wave the engine's SAVE file holds exactly the reference builder's
+    CSR over the nodes built (corpus.nsn_edges, edge-identical to the reference's own), and
+    QUERY answers match the oracle on that graph."""
+    from mars_amd import load_graph
+    c = corpus.make_corpus(2700, D, seed=92)
+    eng = Engine("--capacity", "4000")
+    try:
+        def add(lo, hi):
+            for i in range(lo, hi):
+                assert eng(cmd="ADD", id=i, modality=int(c.modalities[i]), embedding=c.embeddings[i].tolist(),
+                           timestamp=float(c.timestamps[i])) == {"ok": True}
+
+        def check(n_nodes, n_built, seed):
+            path = tmp_path / f"e{n_nodes}.mars"
+            assert eng(cmd="SAVE", path=str(path)) == {"ok": True}
+            g = load_graph(path)
+            assert g.num_nodes == n_nodes
+            row, col = corpus.nsn_edges(c.modalities[:n_built], 6, 0.15)
+            want_row = np.concatenate([row, np.full(n_nodes - n_built, row[-1], np.int32)])
+            np.testing.assert_array_equal(g.row_offsets, want_row)
+            np.testing.assert_array_equal(g.col_indices, col)
+            for j, node in enumerate(corpus.pick_queries(c.modalities[:n_nodes], 6, seed=seed)):
+                q = c.embeddings[node]
+                top_k, hops, filt = 5 + 3 * j, j % 3, (-1 if j % 2 else int(c.modalities[node]))
+                got = eng(cmd="QUERY", embedding=q.tolist(), top_k=top_k, bfs_max_hops=hops, modality_filter=filt,
+                          timestamp=corpus.QUERY_TIME)["results"]
+                check_against_oracle(got, g, q, corpus.QUERY_TIME, top_k, hops, filt)
+
+        add(0, 1300)
+        eng(cmd="QUERY", embedding=c.embeddings[0].tolist(), top_k=10, timestamp=corpus.QUERY_TIME)
+        check(1300, 1300, 1)
+        add(1300, 1900)
+        check(1900, 1300, 2)
+        add(1900, 2700)
+        eng(cmd="QUERY", embedding=c.embeddings[0].tolist(), top_k=10, timestamp=corpus.QUERY_TIME)
+        check(2700, 2700, 3)
+        assert eng(cmd="STATS")["edges"] == len(corpus.nsn_edges(c.modalities, 6, 0.15)[1]) // 2
+    finally:
+        eng.close()

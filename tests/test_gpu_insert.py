@@ -25,7 +25,7 @@ import oracle
 from mars_amd import RetrievalConfig, RetrievalScope, corpus
 from mars_amd._lib import MarsError
 
-from test_gpu_parity import T_Q, check_global, ocfg
+from parity import T_Q, check_global, ocfg
 
 pytestmark = pytest.mark.gpu
 K_NN = corpus.KNN_K

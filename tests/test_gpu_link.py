@@ -204,7 +204,7 @@ def test_queries_while_linking(full):
         for j, got in enumerate(lists):
             live.row, live.col = oracle.link_edges(live.row, live.col, live.n, BASE + 20 * j, got)
         check_device_csr(live)
-        from test_gpu_parity import check_global
+        from parity import check_global
         for node in qn[:4]:
             check_global(live, full.embeddings[node], cfg)
     finally:

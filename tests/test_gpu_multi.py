@@ -20,30 +20,21 @@ import numpy as np
 import pytest
 
 import mars_amd
-import oracle
 from mars_amd import BatchStats, RetrievalConfig, RetrievalScope, corpus
 
-from conftest import RTOL_F32
+import parity
+from parity import check_global, check_results_exact
 
 pytestmark = pytest.mark.gpu
 T_Q = corpus.QUERY_TIME
 LAM = corpus.DECAY_LAMBDA
 
 
-class Dev:
-    def __init__(self, emb, mods, ts, row, col, ep=None, cap_nodes=0, max_k=64):
-        self.n, self.d = emb.shape
-        g = mars_amd.MemoryGraph(self.n, self.d, row, col, emb, mods, ts)
-        self.dg = mars_amd.upload_to_device(g, capacity_nodes=cap_nodes) if cap_nodes else mars_amd.upload_to_device(g)
-        if ep is not None:
-            mars_amd.upload_episode_ids(self.dg, ep)
-            mars_amd.upload_episode_csr(self.dg, mars_amd.build_episode_csr(ep, self.n))
-        mars_amd.upload_fp16_embeddings(self.dg)
-        self.ctx = mars_amd.create_query_context(max(self.n, cap_nodes), self.d, max_k)
+class Dev(parity.Dev):
+    """parity.Dev with the fp16 copy every batched call reads."""
 
-    def close(self):
-        mars_amd.destroy_query_context(self.ctx)
-        mars_amd.free_device(self.dg)
+    def __init__(self, emb, mods, ts, row, col, ep=None, cap_nodes=0, max_k=64):
+        super().__init__(emb, mods, ts, row, col, ep, max_k=max_k, fp16=True, capacity_nodes=cap_nodes)
 
 
 def run_both(dev: Dev, qs: np.ndarray, t_q, cfg: RetrievalConfig, cap: int = 256):
@@ -148,31 +139,18 @@ def test_batched_results_against_oracle(dev10k, corpus_10k):
     """Batched answers against the fp64 oracle run from the same seeds (the seed set
     itself is held to the oracle's top-K up to near-ties)."""
     c = corpus_10k
-    og = oracle.make_graph(c.embeddings, c.modalities, c.timestamps, c.row_offsets, c.col_indices, c.episode_ids)
     cfg = RetrievalConfig(top_k=10, time_decay_lambda=LAM, max_results_returned=15)
-    ocfg = oracle.config(10, 2, LAM, 0.5, -1, 15)
     qn = corpus.pick_queries(c.modalities, 4, seed=804)
     got, want, st = run_both(dev10k, c.embeddings[qn], T_Q, cfg)
     assert_same(got, want)
     assert st.batched == 4
     for i, node in enumerate(qn):
         q = c.embeddings[node]
-        mars_amd.query_memory_fast(dev10k.dg, dev10k.ctx, q, T_Q, cfg)
-        seeds, _ = dev10k.ctx.last_seeds()
-        fin, scale = oracle.scores(og, q, T_Q, LAM, -1)
-        tol = RTOL_F32 * np.maximum(np.abs(fin), scale)
-        ref = oracle.query(og, q, T_Q, ocfg)
-        kth = fin[ref["seeds"][-1]]
-        diff = set(seeds.tolist()) ^ set(ref["seeds"].tolist())
-        assert all(abs(fin[j] - kth) <= 2 * tol[j] + 2 * tol[ref["seeds"][-1]] for j in diff), diff
-        want_r = oracle.query(og, q, T_Q, ocfg, seeds_in=seeds)["results"]
-        assert len(got[i]) == len(want_r)
-        for r, w in zip(got[i], want_r):
-            if r.node_id != w[0]:
-                assert abs(r.score - w[1]) <= 2 * RTOL_F32 * max(abs(w[1]), 1.0), (r, w)
-            else:
-                assert r.hops_from_seed == w[3]
-            assert abs(r.score - w[1]) <= 2 * RTOL_F32 * max(abs(w[1]), 1.0)
+        st1 = mars_amd.RetrievalStats()
+        res = mars_amd.query_memory_fast(dev10k.dg, dev10k.ctx, q, T_Q, cfg, st1)
+        check_results_exact(got[i], res)
+        # the Q=1 answer (equal to the batch's) against the oracle: scores, seeds, BFS, results
+        check_global(dev10k, q, cfg, res=res, st=st1)
 
 
 def test_uncertified_queries_fall_back(corpus_10k):

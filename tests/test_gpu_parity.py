@@ -1,15 +1,10 @@
 """GPU parity: the HIP path (through the C ABI) against the CPU oracle on the
 same seeded inputs.
 
-Bars (written here as the tests apply them):
-  * fused scores:  |gpu - oracle| <= 1e-5 * max(|oracle|, w * sum|e q|)  (fp32; fp16 rows
-                   against the oracle on the same RNE-rounded rows), and <= 2e-3 of the
-                   same scale for the fp16 path against the fp32 oracle;
-  * seeds / results: identical id sets except ids whose oracle score lies within
-                   that tolerance of the cut;
-  * BFS given the GPU's seeds: visit order (ids), hop levels and visited count
-                   bit-exact; BFS scores within the score tolerance;
-  * episode CSR / episode-scoped results: ids and hops exact.
+The bars are those of tests/parity.py: fused scores within 1e-5 * max(|oracle|, w * sum|e q|)
+(fp32) or 2e-3 of that scale (fp16 path against the fp32 oracle), BFS scores with the scale
+carried along the BFS, seeds and results equal up to near-ties, BFS visit order and hops
+bit-exact, episode-scoped ids exact.
 """
 from __future__ import annotations
 
@@ -21,104 +16,10 @@ import oracle
 from mars_amd import RetrievalConfig, RetrievalScope, corpus
 
 from conftest import RTOL_F16_VS_F32, RTOL_F32
+from parity import (FLT_MAX, LAM, T_Q, Dev, batch_check, check_episode, check_episode_results, check_global,
+                    check_results_exact, check_scores, episode_cfg, ocfg, random_graph)
 
 pytestmark = pytest.mark.gpu
-FLT_MAX = float(np.finfo(np.float32).max)
-T_Q = corpus.QUERY_TIME
-LAM = corpus.DECAY_LAMBDA
-
-
-class Dev:
-    def __init__(self, emb, mods, ts, row, col, ep=None, max_k=64, fp16=False):
-        self.n, self.d = emb.shape
-        g = mars_amd.MemoryGraph(self.n, self.d, row, col, emb, mods, ts)
-        self.dg = mars_amd.upload_to_device(g)
-        self.csr = None
-        if ep is not None:
-            mars_amd.upload_episode_ids(self.dg, ep)
-            self.csr = mars_amd.build_episode_csr(ep, self.n)
-            mars_amd.upload_episode_csr(self.dg, self.csr)
-        if fp16:
-            mars_amd.upload_fp16_embeddings(self.dg)
-        self.ctx = mars_amd.create_query_context(self.n, self.d, max_k)
-        self.og = oracle.make_graph(emb, mods, ts, row, col, ep)
-
-    def close(self):
-        mars_amd.destroy_query_context(self.ctx)
-        mars_amd.free_device(self.dg)
-
-    def query(self, q, cfg, t_q=T_Q):
-        st = mars_amd.RetrievalStats()
-        res = mars_amd.query_memory_fast(self.dg, self.ctx, q, t_q, cfg, st)
-        return res, st
-
-
-def ocfg(cfg: RetrievalConfig):
-    return oracle.config(cfg.top_k, cfg.bfs_max_hops, cfg.time_decay_lambda, cfg.bfs_score_decay,
-                         cfg.modality_filter, cfg.max_results_returned, int(cfg.retrieval_scope),
-                         cfg.query_episode_id, cfg.query_episode_member_begin, cfg.query_episode_member_count,
-                         cfg.episode_same_boost)
-
-
-def check_scores(gpu, ref, scale, rtol):
-    bound = rtol * np.maximum(np.abs(ref), scale) + 1e-30
-    filt = ref == -FLT_MAX
-    assert np.all(gpu[filt] == np.float32(-FLT_MAX))
-    err = np.abs(gpu[~filt].astype(np.float64) - ref[~filt])
-    worst = np.max(err / bound[~filt]) if err.size else 0.0
-    assert worst <= 1.0, f"score error {worst:.3f}x the bound"
-
-
-def check_global(dev: Dev, q, cfg: RetrievalConfig, emb16=None, rtol=RTOL_F32):
-    """Full global-query parity for one query; returns the GPU results."""
-    res, st = dev.query(q, cfg)
-    assert st.scope_fallback == 0 or cfg.retrieval_scope == RetrievalScope.EpisodeScoped
-    og = dev.og
-    if emb16 is not None:
-        og = oracle.Graph(og.embeddings, og.modalities, og.timestamps, og.row_offsets, og.col_indices,
-                          og.episode_ids, og.ep_offsets, og.ep_members, emb16)
-    ref = oracle.query(og, q, T_Q, ocfg(cfg))
-    fin_ref = ref["final"]
-    _, scale = oracle.scores(og, q, T_Q, cfg.time_decay_lambda, cfg.modality_filter)
-    tol = rtol * np.maximum(np.abs(fin_ref), scale)
-    # 1) fused scores over all N
-    fin_gpu = dev.ctx.last_scores(dev.n)
-    if cfg.episode_same_boost > 0:
-        scale = scale * (1.0 + cfg.episode_same_boost)
-    check_scores(fin_gpu, fin_ref, scale, rtol)
-    # 2) seeds: same set up to near-ties at the K-th score
-    seeds, seed_vals = dev.ctx.last_seeds()
-    k = ref["k"]
-    assert len(seeds) == min(k, dev.n)
-    kth = fin_ref[ref["seeds"][-1]]
-    diff = set(seeds.tolist()) ^ set(ref["seeds"].tolist())
-    assert all(abs(fin_ref[i] - kth) <= 2 * tol[i] + 2 * tol[ref["seeds"][-1]] for i in diff), diff
-    np.testing.assert_array_equal(seed_vals, fin_gpu[seeds])
-    # seeds come out in (score desc, id asc) order of the GPU's own scores
-    order = np.lexsort((seeds, -seed_vals.astype(np.float64)))
-    np.testing.assert_array_equal(order, np.arange(len(seeds)))
-    # 3) BFS from the GPU's seeds: visit order / hops exact, scores in tolerance
-    ids, hops, vsc = dev.ctx.last_visited()
-    b = oracle.bfs(og.row_offsets, og.col_indices, fin_ref, seeds, fin_ref[seeds],
-                   max(0, cfg.bfs_max_hops), cfg.bfs_score_decay)
-    np.testing.assert_array_equal(ids, b["ids"])
-    np.testing.assert_array_equal(hops, b["hops"])
-    vtol = rtol * np.maximum(np.abs(b["scores"]), np.max(scale)) + 1e-30
-    assert np.all(np.abs(vsc - b["scores"]) <= vtol)
-    assert st.visited == len(ids)
-    # 4) final results: oracle given the same seeds
-    r2 = oracle.query(og, q, T_Q, ocfg(cfg), seeds_in=seeds)
-    want = r2["results"]
-    assert len(res) == len(want) == r2["n_results"]
-    vis_score = dict(zip(b["ids"].tolist(), b["scores"].tolist()))
-    vis_hop = dict(zip(b["ids"].tolist(), b["hops"].tolist()))
-    for j, (r, w) in enumerate(zip(res, want)):
-        if r.node_id != w[0]:
-            assert abs(vis_score[r.node_id] - w[1]) <= 2 * RTOL_F32 * max(abs(w[1]), 1.0), (j, r, w)
-        assert r.hops_from_seed == vis_hop[r.node_id]
-        assert r.modality == int(dev.og.modalities[r.node_id])
-        assert abs(r.score - vis_score[r.node_id]) <= rtol * max(abs(vis_score[r.node_id]), 1.0)
-    return res
 
 
 # ---------------------------------------------------------------- corpus N=10K (CPU plumbing size)
@@ -173,15 +74,7 @@ def test_episode_parity_10k(dev10k, corpus_10k):
                               query_episode_member_count=int(off[ep + 1] - off[ep]))
         res, st = dev10k.query(corpus_10k.embeddings[node], cfg)
         assert st.scope_fallback == 0 and st.nodes_scanned == 10 and st.bfs_waves == 0
-        ref = oracle.query(dev10k.og, corpus_10k.embeddings[node], T_Q, ocfg(cfg))
-        assert ref["scoped"]
-        assert [r.node_id for r in res] == [w[0] for w in ref["results"]]
-        assert all(r.hops_from_seed == 0 for r in res)
-        for r, w in zip(res, ref["results"]):
-            if w[1] == -FLT_MAX:
-                assert r.score == np.float32(-FLT_MAX)
-            else:
-                assert abs(r.score - w[1]) <= RTOL_F32 * max(abs(w[1]), 1.0)
+        check_episode_results(dev10k, corpus_10k.embeddings[node], cfg, res)
         # published outcome: episode-scoped retrieval returns the episode's TEXT and AUDIO
         mods = {r.modality for r in res if corpus_10k.episode_ids[r.node_id] == ep}
         assert {0, 1} <= mods
@@ -230,10 +123,29 @@ def test_device_query_pointer(dev10k, corpus_10k):
     assert host == dev_res
 
 
-def test_unsupported_result_count(dev10k, corpus_10k):
-    cfg = RetrievalConfig(top_k=10, max_results_returned=9000)
-    with pytest.raises(mars_amd.MarsError, match="MARS_ERR_UNSUPPORTED"):
-        dev10k.query(corpus_10k.embeddings[0], cfg)
+def test_result_counts_up_to_the_compaction_cap(rng):
+    """max_results_returned above one LDS sort (8,192): results go out in sorted bands, up to
+    the reference's compaction cap min(max_nodes, max_k * 500) (memory_cuda.cu:1059); a
+    larger request returns that many, as the reference's compaction truncates there."""
+    emb, mods, ts, row, col, ep = random_graph(rng, 40000, 128, deg=5)
+    dev = Dev(emb, mods, ts, row, col, ep)
+    try:
+        cfg = RetrievalConfig(top_k=10, bfs_max_hops=4, time_decay_lambda=LAM, max_results_returned=20000)
+        res = check_global(dev, emb[7], cfg)
+        assert len(res) == 20000
+        _, st = dev.query(emb[7], cfg)
+        assert st.visited > 32000
+        big = RetrievalConfig(top_k=8, bfs_max_hops=4, time_decay_lambda=LAM, max_results_returned=39000)
+        res, st = dev.query(emb[7], big)
+        assert len(res) == 32000                               # 64 * 500
+        small_ctx = mars_amd.create_query_context(dev.n, dev.d, 8)   # cap 8 * 500; K = 8 on both
+        try:
+            res8 = mars_amd.query_memory_fast(dev.dg, small_ctx, emb[7], T_Q, big)
+            assert len(res8) == 4000 and res8 == res[:4000]
+        finally:
+            mars_amd.destroy_query_context(small_ctx)
+    finally:
+        dev.close()
 
 
 # ---------------------------------------------------------------- the reference's own corpus
@@ -266,40 +178,11 @@ def test_reference_kids_corpus(golden):
 
 
 # ---------------------------------------------------------------- shapes and edge cases
-def _random_graph(rng, n, d, deg=6, n_ep=None):
-    emb = rng.standard_normal((n, d)).astype(np.float32)
-    emb /= np.linalg.norm(emb, axis=1, keepdims=True)
-    mods = rng.integers(0, 3, size=n).astype(np.int32)
-    ts = rng.uniform(0, 600, size=n).astype(np.float32)
-    ep = (np.arange(n) // 10).astype(np.int32) if n_ep is None else np.sort(rng.integers(0, n_ep, n)).astype(np.int32)
-    knn = rng.integers(0, n, size=(n, deg)).astype(np.int32)
-    row, col = corpus.build_nsn_csr(ep, knn)
-    return emb, mods, ts, row, col, ep
-
-
-def check_episode(dev, q, ep, k):
-    """Episode-scoped query against the oracle (ids exact, scores to the fp32 bar)."""
-    off = dev.csr.ep_csr_offsets
-    cfg = RetrievalConfig(top_k=k, time_decay_lambda=LAM, max_results_returned=k,
-                          retrieval_scope=RetrievalScope.EpisodeScoped, query_episode_id=ep,
-                          query_episode_member_begin=int(off[ep]),
-                          query_episode_member_count=int(off[ep + 1] - off[ep]))
-    res, st = dev.query(q, cfg)
-    ref = oracle.query(dev.og, q, T_Q, ocfg(cfg))
-    assert ref["scoped"] and st.scope_fallback == 0
-    assert [r.node_id for r in res] == [w[0] for w in ref["results"]]
-    for r, w in zip(res, ref["results"]):
-        if w[1] == -FLT_MAX:
-            assert r.score == np.float32(-FLT_MAX)
-        else:
-            assert abs(r.score - w[1]) <= RTOL_F32 * max(abs(w[1]), 1.0)
-
-
 @pytest.mark.parametrize("n,d", [(5, 768), (300, 100), (3000, 384), (2000, 1024), (777, 256), (1500, 64)])
 def test_shapes(n, d, rng):
     """Global queries at several dimensions, and episode-scoped ones through each episode
     kernel variant (register-fragment rows for d = 256 / 384 / 768, the loop otherwise)."""
-    emb, mods, ts, row, col, ep = _random_graph(rng, n, d)
+    emb, mods, ts, row, col, ep = random_graph(rng, n, d)
     dev = Dev(emb, mods, ts, row, col, ep, fp16=True)
     try:
         for node in (0, n // 2, n - 1):
@@ -354,33 +237,9 @@ def test_large_frontier_and_visited(rng):
 
 
 # ---------------------------------------------------------------- batched MFMA scoring
-def _batch_check(dev: Dev, qnodes, cfg, t_q, emb):
-    qs = emb[qnodes]
-    buf = mars_amd.DeviceBuffer.from_array(qs)
-    try:
-        ids, sc = mars_amd.query_batch(dev.dg, dev.ctx, buf.ptr, len(qnodes), t_q, cfg)
-    finally:
-        buf.free()
-    tq = np.broadcast_to(np.asarray(t_q, np.float32), (len(qnodes),))
-    k = cfg.top_k
-    for i in range(len(qnodes)):
-        fin, scale = oracle.scores(dev.og, qs[i], float(tq[i]), cfg.time_decay_lambda, cfg.modality_filter)
-        want, _ = oracle.topk(fin, k)
-        tol = RTOL_F16_VS_F32 * np.maximum(np.abs(fin), scale)
-        got = ids[i][ids[i] >= 0]
-        assert len(got) == min(k, dev.n)
-        ok = fin[got] != -FLT_MAX
-        assert np.all(np.abs(sc[i][: len(got)][ok] - fin[got][ok]) <= tol[got][ok])
-        kth = fin[want[-1]]
-        for j in set(got.tolist()) ^ set(want.tolist()):
-            assert abs(fin[j] - kth) <= 2 * (tol[j] + tol[want[-1]]), (i, j)
-        assert np.all(np.diff(sc[i][: len(got)].astype(np.float64)) <= 0)      # sorted desc
-    return ids, sc
-
-
 def test_batch_parity_q64(dev10k, corpus_10k):
     qn = corpus.pick_queries(corpus_10k.modalities, 64, seed=404)
-    _batch_check(dev10k, qn, RetrievalConfig(top_k=10, time_decay_lambda=LAM), T_Q, corpus_10k.embeddings)
+    batch_check(dev10k, qn, RetrievalConfig(top_k=10, time_decay_lambda=LAM), T_Q, corpus_10k.embeddings)
 
 
 @pytest.mark.parametrize("q,k,filt", [(1, 10, -1), (200, 16, -1), (130, 5, 1), (64, 16, 2), (520, 16, -1),
@@ -388,7 +247,7 @@ def test_batch_parity_q64(dev10k, corpus_10k):
 def test_batch_parity_shapes(dev10k, corpus_10k, q, k, filt, rng):
     qn = corpus.pick_queries(corpus_10k.modalities, q, seed=q)
     tq = rng.uniform(400, 600, size=q).astype(np.float32)             # per-query times
-    _batch_check(dev10k, qn, RetrievalConfig(top_k=k, time_decay_lambda=LAM, modality_filter=filt), tq,
+    batch_check(dev10k, qn, RetrievalConfig(top_k=k, time_decay_lambda=LAM, modality_filter=filt), tq,
                  corpus_10k.embeddings)
 
 
@@ -396,7 +255,7 @@ def test_batch_matches_single_query_seeds(dev10k, corpus_10k):
     """The batched seeds agree with the Q=1 fp16 path's seeds up to fp16 near-ties."""
     qn = corpus.pick_queries(corpus_10k.modalities, 32, seed=505)
     cfg = RetrievalConfig(top_k=10, time_decay_lambda=LAM)
-    ids, _ = _batch_check(dev10k, qn, cfg, T_Q, corpus_10k.embeddings)
+    ids, _ = batch_check(dev10k, qn, cfg, T_Q, corpus_10k.embeddings)
     dev10k.ctx.use_fp16 = True
     try:
         agree = 0
@@ -441,32 +300,39 @@ def test_gpu_knn_matches_cpu_exact():
 # ---------------------------------------------------------------- replayed query graphs
 def test_graph_replay_matches_eager(dev10k, corpus_10k):
     """Replays of the query graph (arguments rewritten per query) interleaved with
-    eager queries: every replay returns exactly the eager result. A filtered,
-    boosted global query between plain ones switches the scan kernel variant, so the
-    graph is rebuilt rather than replayed with the wrong kernel."""
+    eager queries: every replay returns exactly the eager result, and each replay is
+    checked against the oracle (scores, seeds, BFS and results for global queries; ids
+    and scores for episode-scoped ones). A filtered, boosted global query between plain
+    ones switches the scan kernel variant, so the graph is rebuilt rather than replayed
+    with the wrong kernel. The query time changes between replays, which the reference's
+    recapture key misses (memory_cuda.cu:1375-1385)."""
     qs = corpus.pick_queries(corpus_10k.modalities, 24, seed=606)
-    off = dev10k.csr.ep_csr_offsets
+    emb16 = oracle.to_f16_bits(corpus_10k.embeddings)
     try:
         for fp16 in (False, True):
             dev10k.ctx.use_fp16 = fp16
             for i, node in enumerate(qs):
                 ep = int(corpus_10k.episode_ids[node])
+                q = corpus_10k.embeddings[node]
                 cfgs = [RetrievalConfig(top_k=10, time_decay_lambda=LAM, max_results_returned=15),
                         RetrievalConfig(top_k=10, time_decay_lambda=LAM, max_results_returned=15,
                                         modality_filter=int(corpus_10k.modalities[node]), query_episode_id=ep,
                                         episode_same_boost=0.5),
-                        RetrievalConfig(top_k=10, time_decay_lambda=LAM, max_results_returned=15,
-                                        retrieval_scope=RetrievalScope.EpisodeScoped, query_episode_id=ep,
-                                        query_episode_member_begin=int(off[ep]),
-                                        query_episode_member_count=int(off[ep + 1] - off[ep]))]
+                        episode_cfg(dev10k.csr, ep, 10, 15)]
                 for cfg in cfgs:
                     t = T_Q - 5.0 * (i % 3)                   # the query time changes between replays
                     dev10k.ctx.use_cuda_graph = False
-                    eager, _ = dev10k.query(corpus_10k.embeddings[node], cfg, t_q=t)
+                    eager, _ = dev10k.query(q, cfg, t_q=t)
                     dev10k.ctx.use_cuda_graph = True
-                    replay, _ = dev10k.query(corpus_10k.embeddings[node], cfg, t_q=t)
-                    replay2, _ = dev10k.query(corpus_10k.embeddings[node], cfg, t_q=t)
+                    replay, _ = dev10k.query(q, cfg, t_q=t)
+                    replay2, st2 = dev10k.query(q, cfg, t_q=t)
                     assert replay == eager and replay2 == eager, (fp16, i, cfg.retrieval_scope)
+                    if i % 4:                                 # the oracle on every fourth query
+                        continue
+                    if cfg.retrieval_scope == RetrievalScope.EpisodeScoped:   # fp32 rows on both paths
+                        check_episode_results(dev10k, q, cfg, replay2, t_q=t)
+                    else:
+                        check_global(dev10k, q, cfg, emb16=emb16 if fp16 else None, t_q=t, res=replay2, st=st2)
     finally:
         dev10k.ctx.use_cuda_graph = False
         dev10k.ctx.use_fp16 = False
@@ -506,7 +372,7 @@ def test_read_ceiling(rng):
     """The streaming-read ceiling of a graph's rows: positive and below the HBM peak for
     fp32 and fp16 rows; MARS_ERR_UNSUPPORTED once the fp16 copy is gone."""
     from mars_amd._lib import MarsError
-    emb, mods, ts, row, col, ep = _random_graph(rng, 40000, 768)
+    emb, mods, ts, row, col, ep = random_graph(rng, 40000, 768)
     dev = Dev(emb, mods, ts, row, col, ep, fp16=True)
     try:
         for fp16 in (False, True):

@@ -461,3 +461,48 @@ def test_insert_edges_keep_reference_flush_invariants(golden):
     ep = np.array([0] * 4 + [1] * 3 + [2] * 3, np.int32)
     r, c = oracle.insert_edges(z["before_row"], z["before_col"], n_old, n_new, ep, knn)
     _check_flush_invariants(z["before_row"], z["before_col"], r, c, n_old, n_new)
+
+
+# ---------------------------------------------------------------- the kids sweep's probe sample
+def _mt19937_raw(seed: int, count: int) -> np.ndarray:
+    """Raw 32-bit outputs of std::mt19937(seed), from numpy's own MT19937 with the
+    standard's init_genrand seeding: an implementation independent of the C++ library."""
+    bg = np.random.MT19937()
+    bg._legacy_seeding(seed)
+    return bg.random_raw(count)
+
+
+def _uniform_index(raw, hi: int, count: int):
+    """uniform_int_distribution<size_t>(0, hi) over a 32-bit engine: Lemire's
+    nearly-divisionless method (ACM TOMACS 29(1), 2019; arXiv 1805.10941), which libstdc++
+    uses when the engine's range is exactly 32 bits: product = draw * (hi + 1); a low half
+    below (2^32 - (hi + 1)) mod (hi + 1) rejects the draw; the result is the high half."""
+    rng_range = hi + 1
+    thr = ((1 << 32) - rng_range) % rng_range
+    out, i = [], 0
+    while len(out) < count:
+        prod = int(raw[i]) * rng_range
+        i += 1
+        if (prod & 0xFFFFFFFF) < thr:
+            continue
+        out.append(prod >> 32)
+    return np.array(out, np.int64)
+
+
+def test_mt19937_known_answer():
+    """The C++ standard's known answer for mt19937 ([rand.predef]: the 10000th output of a
+    default-constructed engine, seed 5489, is 4123659995) holds for the stream the sampler
+    pin below reads."""
+    assert int(_mt19937_raw(5489, 10000)[-1]) == 4123659995
+
+
+@pytest.mark.parametrize("n,n_image", [(1000, 300), (5000, 1500), (10000, 3000), (50000, 15000), (7, 1), (12345, 4097)])
+def test_kids_probes_match_independent_sampler(n, n_image):
+    """oracle_kids_probes (bench_kids_sweep.cu:624-632: std::mt19937(N ^ 0xA5A5A5A5) and
+    uniform_int_distribution<size_t>(0, n_image - 1), 256 draws) against numpy's MT19937
+    and Lemire's method restated above. A wrong seed, range bound or distribution fails."""
+    got = oracle.kids_probes(n, n_image, 256)
+    seed = (n ^ 0xA5A5A5A5) & 0xFFFFFFFF
+    want = _uniform_index(_mt19937_raw(seed, 4096), n_image - 1, 256)
+    np.testing.assert_array_equal(got, want)
+    assert got.min() >= 0 and got.max() < n_image
