@@ -386,6 +386,20 @@ int mars_query_device(const mars_graph* g, mars_ctx* ctx, const float* d_query, 
 int mars_query_batch(const mars_graph* g, mars_ctx* ctx, const float* d_queries, int32_t Q,
                      const float* t_q, const mars_retrieval_config* cfg, int32_t* out_ids,
                      float* out_scores, mars_stats* stats);
+/* mars_query_batch without allocation. No counterpart in the reference: for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving loops). The
+ * same kernels and results as mars_query_batch, with their scratch in a static device
+ * array of the library (about 8.4 MiB, held per GPU until the process ends): Q <= 256
+ * queries (MARS_ERR_CAPACITY beyond), top_k <= 16, embedding_dim 256 / 384 / 512 / 768.
+ * Inputs and outputs are device memory: d_queries Q x embedding_dim fp32, d_tq Q query
+ * times (uniform_tq != 0 promises they are all equal: one decay weight per row), d_ids /
+ * d_scores Q x top_k, each row sorted (score desc, id asc), -1 / -FLT_MAX past the rows
+ * that exist. Runs on `stream` (a hipStream_t; NULL = the null stream) and returns
+ * without waiting; the results are there once the stream reaches that point. Calls that
+ * overlap on one GPU share the array and race: order them on one stream. */
+int mars_query_batch_static(const mars_graph* g, const float* d_queries, int32_t Q, const float* d_tq,
+                            int32_t uniform_tq, const mars_retrieval_config* cfg, int32_t* d_ids,
+                            float* d_scores, void* stream);
 
 /* Batched global queries: Q global queries (the same cfg, query i at time t_q[i], a host
  * array; query vectors in device memory, row-major Q x embedding_dim fp32). Query i gets
@@ -507,6 +521,7 @@ int mars_copy_to_device(void* dst, const void* src, size_t bytes);
 int mars_copy_to_host(void* dst, const void* src, size_t bytes);
 int mars_copy_device(void* dst, const void* src, size_t bytes);   /* device to device */
 int mars_device_memory(size_t* free_bytes, size_t* total_bytes);  /* hipMemGetInfo of the device */
+int mars_device_synchronize(void);   /* hipDeviceSynchronize: all streams of the device drained */
 
 /* ---- benchmark loop (harness semantics of src/latency_bench.cu:355-393) ------------ */
 /* Runs n single queries back to back, query i reading the device vector

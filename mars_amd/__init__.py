@@ -366,6 +366,24 @@ def query_batch(dg: DeviceMemoryGraph, ctx: QueryContext, d_queries_ptr: int, n_
     return ids, sc
 
 
+def query_batch_static(dg: DeviceMemoryGraph, d_queries_ptr: int, n_queries: int, d_tq_ptr: int,
+                       cfg: RetrievalConfig, d_ids_ptr: int, d_scores_ptr: int, uniform_tq: bool = False,
+                       stream: Optional[int] = None) -> None:
+    """query_batch with every buffer in device memory and no allocation (the library's static
+    scratch): queries, times, ids (int32) and scores (fp32) are device pointers. Asynchronous
+    on `stream` (None = the null stream)."""
+    c = cfg.to_c()
+    check(lib.mars_query_batch_static(dg.handle, C.c_void_p(d_queries_ptr), int(n_queries), C.c_void_p(d_tq_ptr),
+                                      1 if uniform_tq else 0, C.byref(c), C.c_void_p(d_ids_ptr),
+                                      C.c_void_p(d_scores_ptr), C.c_void_p(stream) if stream else None),
+          "mars_query_batch_static")
+
+
+def synchronize() -> None:
+    """Wait for all work on the current device (its null stream included)."""
+    check(lib.mars_device_synchronize(), "mars_device_synchronize")
+
+
 @dataclass
 class BatchStats:
     queries: int = 0

@@ -222,6 +222,7 @@ SIGNATURES = {
                                     C.POINTER(StatsC)]),
     "mars_ctx_last_scores": (C.c_int, [VP, VP, I64]),
     "mars_query_batch": (C.c_int, [VP, VP, VP, I32, VP, C.POINTER(RetrievalConfigC), VP, VP, C.POINTER(StatsC)]),
+    "mars_query_batch_static": (C.c_int, [VP, VP, I32, VP, I32, C.POINTER(RetrievalConfigC), VP, VP, VP]),
     "mars_query_global_batch": (C.c_int, [VP, VP, VP, I32, VP, C.POINTER(RetrievalConfigC), VP, I32, VP,
                                           C.POINTER(BatchStatsC)]),
     "mars_bench_serve": (C.c_int, [VP, VP, VP, C.POINTER(ServeBenchC)]),
@@ -262,6 +263,7 @@ SIGNATURES = {
     "mars_copy_to_device": (C.c_int, [VP, VP, C.c_size_t]),
     "mars_copy_to_host": (C.c_int, [VP, VP, C.c_size_t]),
     "mars_copy_device": (C.c_int, [VP, VP, C.c_size_t]),
+    "mars_device_synchronize": (C.c_int, []),
     "mars_bench_queries": (C.c_int, [VP, VP, VP, I64, I32, C.c_float, C.POINTER(RetrievalConfigC), I32, VP, VP,
                                      VP, VP]),
     "mars_bench_queries_host": (C.c_int, [VP, VP, VP, I64, I32, C.c_float, C.POINTER(RetrievalConfigC), I32, VP,

@@ -1063,6 +1063,12 @@ int mars_device_memory(size_t* free_bytes, size_t* total_bytes) {
     return MARS_OK;
 }
 
+int mars_device_synchronize(void) {
+    MARS_TRY(ensure_device(nullptr));
+    MARS_HIP(hipDeviceSynchronize());
+    return MARS_OK;
+}
+
 int mars_bench_queries(const mars_graph* g, mars_ctx* c, const float* dq, int64_t stride, int32_t n, float t_q,
                        const mars_retrieval_config* cfgs, int32_t n_cfg, double* lat_us, float* kern_us,
                        float* bfs_us, int32_t* n_res) {

@@ -1,0 +1,63 @@
+"""mars_query_batch_static, the entry point that allocates nothing (its scratch is a static
+device array of the library), against mars_query_batch, the entry point whose kernels it
+shares: ids and scores identical on two calls in a row, the second with fewer queries
+(the array keeps the first call's contents), per-query and uniform query times; sizes
+beyond the static array rejected with MARS_ERR_CAPACITY before any launch."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import mars_amd
+from mars_amd import RetrievalConfig, corpus
+from mars_amd._lib import MarsError
+
+pytestmark = pytest.mark.gpu
+N, D = 20000, 768
+
+
+def static_call(dg, qs, tq, cfg, uniform):
+    q = len(qs)
+    bq = mars_amd.DeviceBuffer.from_array(np.ascontiguousarray(qs, np.float32))
+    bt = mars_amd.DeviceBuffer.from_array(np.ascontiguousarray(tq, np.float32))
+    bi = mars_amd.DeviceBuffer(q * cfg.top_k * 4)
+    bs = mars_amd.DeviceBuffer(q * cfg.top_k * 4)
+    try:
+        mars_amd.query_batch_static(dg, bq.ptr, q, bt.ptr, cfg, bi.ptr, bs.ptr, uniform_tq=uniform)
+        mars_amd.synchronize()
+        return (bi.to_array(np.int32, q * cfg.top_k).reshape(q, cfg.top_k),
+                bs.to_array(np.float32, q * cfg.top_k).reshape(q, cfg.top_k))
+    finally:
+        for b in (bq, bt, bi, bs):
+            b.free()
+
+
+def test_static_batch_matches_query_batch():
+    mars_amd.init(0)
+    c = corpus.make_corpus(N, D, seed=47)
+    g = mars_amd.MemoryGraph(N, D, None, None, c.embeddings, c.modalities, c.timestamps)
+    dg = mars_amd.upload_to_device(g)
+    mars_amd.upload_fp16_embeddings(dg)
+    ctx = mars_amd.create_query_context(N, D, 64)
+    rng = np.random.default_rng(8)
+    try:
+        for q, k, uniform, filt in ((200, 10, True, -1), (37, 16, False, 1), (256, 5, False, -1)):
+            nodes = corpus.pick_queries(c.modalities, q, seed=q)
+            qs = c.embeddings[nodes]
+            tq = np.full(q, corpus.QUERY_TIME, np.float32) if uniform else \
+                rng.uniform(300, 600, size=q).astype(np.float32)
+            cfg = RetrievalConfig(top_k=k, time_decay_lambda=corpus.DECAY_LAMBDA, modality_filter=filt)
+            buf = mars_amd.DeviceBuffer.from_array(np.ascontiguousarray(qs))
+            try:
+                want_ids, want_sc = mars_amd.query_batch(dg, ctx, buf.ptr, q, tq, cfg)
+            finally:
+                buf.free()
+            got_ids, got_sc = static_call(dg, qs, tq, cfg, uniform)
+            np.testing.assert_array_equal(got_ids, want_ids)
+            np.testing.assert_array_equal(got_sc.view(np.uint32), want_sc.view(np.uint32))
+        with pytest.raises(MarsError) as e:
+            static_call(dg, c.embeddings[:257], np.zeros(257, np.float32), RetrievalConfig(top_k=10), True)
+        assert e.value.code == -4                      # MARS_ERR_CAPACITY
+    finally:
+        mars_amd.destroy_query_context(ctx)
+        mars_amd.free_device(dg)
