@@ -546,7 +546,7 @@ void batch_grid(int64_t n, int32_t q, int32_t* n_rranges, int32_t* n_qblocks, in
     const int32_t qblocks = (q + 63) / 64;
     const bool gemm = batch_uses_gemm(q);
     const int32_t tiles = gemm ? (q + 255) / 256 : qblocks;       // workgroups per row range
-    const int64_t align = gemm ? 64 : 16;                          // rows per tile
+    const int64_t align = gemm ? 256 : 16;                         // rows per tile
     int32_t rr = std::max(8, (256 / std::max(tiles, 1)) / 8 * 8);
     const int64_t max_rr = std::max<int64_t>(1, (n + align - 1) / align);   // at least one tile per range
     if (rr > max_ranges) rr = std::max(1, max_ranges);

@@ -19,16 +19,12 @@
 //  Reference analogue: wmma_mma_similarity_kernel / wmma_similarity_kernel
 //  (src/wmma_similarity.cu:55-138), which score one query and are never called.
 // ============================================================================
-#include "internal.hpp"
+#include "device.hpp"
 
 #include <cfloat>
 
 namespace mars {
 namespace {
-
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kBQ = 64;        // queries per workgroup (4 MFMA row tiles of 16)
 constexpr int kBWaves = 8;     // waves per workgroup
@@ -40,26 +36,6 @@ __device__ inline void wave_lds_sync() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
-template <int K>
-__device__ inline void reg_insert(uint64_t (&list)[K], uint64_t x) {
-    // list ascending; x < list[K-1] is checked by the caller
-    uint64_t v = x;
-#pragma unroll
-    for (int j = 0; j < K; ++j) {
-        const uint64_t lo = list[j] < v ? list[j] : v;
-        const uint64_t hi = list[j] < v ? v : list[j];
-        list[j] = lo;
-        v = hi;
-    }
-}
-
-// Ascending order-preserving code of a score (-0.0 folded onto +0.0): a < b as floats
-// iff ord32(a) < ord32(b) as unsigned; 0 is below every score (no bound yet).
-__device__ inline uint32_t ord32(float s) {
-    const uint32_t u = __float_as_uint(s + 0.0f);
-    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
 template <int KCH, int K>
@@ -245,243 +221,6 @@ __global__ __launch_bounds__(kBWaves * 64) void k_batch_scan(BatchArgs a) {
     }
 }
 
-// ---------------------------------------------------------------------------------
-// k_batch_gemm — batched scoring for larger Q: a query tile of 256 against row tiles
-// of 64, C = Q_tile x E_tile^T on MFMA 16x16x32 f16 with both operands staged in LDS
-// in k-stages of 64 (staged rows padded to 72 halfs, so the 16-byte fragment reads of
-// each 8 lanes fall in distinct banks). Four waves, one per SIMD with the whole
-// register file: wave w owns queries 64w .. 64w+63 against all 64 rows (4 x 4 MFMA
-// tiles), and thread t owns the top-K list of query t. Row data is read from HBM
-// once per query tile and runs PB stages ahead in registers.
-// Selection: a score at or above its query's bound (the score of the query's K-th
-// key, once K are held) is appended to that query's candidate slots in LDS; the
-// owner thread folds the slots into its list and raises the bound. A query whose
-// slots overflow makes the workgroup repeat the round for the scores not yet taken,
-// against the raised bound, so no candidate is lost.
-// ---------------------------------------------------------------------------------
-constexpr int kGQ = 256;        // queries per workgroup
-constexpr int kGR = 64;         // rows per row tile
-constexpr int kGK = 64;         // k per LDS stage
-constexpr int kGPad = 72;       // halfs per staged row (64 + 8)
-constexpr int kGCand = 16;      // candidate slots per query and round
-constexpr int kGThreads = 256;
-
-struct GemmLds {
-    __half a[2][kGQ * kGPad];
-    __half b[2][kGR * kGPad];
-    uint64_t cand[kGQ][kGCand];
-    uint32_t cnt[kGQ];
-    uint32_t thr[kGQ];
-    float tq[kGQ];
-    float w[kGR];                 // row decay weight (one query time) or row timestamp
-    int32_t keep[kGR];            // row passes the modality filter
-    int32_t flag;                 // a query's slots overflowed this round
-};
-
-template <int NS, int K>
-__global__ __launch_bounds__(kGThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
-void k_batch_gemm(BatchArgs a) {
-    constexpr int PB = (NS % 4 == 0) ? 4 : 3;     // row stages in flight
-    constexpr int PA = 2;                          // query stages in flight
-    static_assert(NS % PB == 0 && NS % PA == 0 && NS % 2 == 0, "stage ring must divide the stage count");
-    __shared__ __attribute__((aligned(16))) GemmLds sh;
-    const int tid = int(threadIdx.x), lane = tid & 63, wq = tid >> 6;
-    const int m = lane & 15, kg = lane >> 4;
-    constexpr int d = NS * kGK;
-    const int r_id = int(blockIdx.x) % a.n_rranges;
-    const int q0 = (int(blockIdx.x) / a.n_rranges) * kGQ;
-    const int64_t r0 = int64_t(r_id) * a.rows_per_range;
-    const int64_t r1 = (a.n < r0 + a.rows_per_range) ? a.n : r0 + a.rows_per_range;
-    const int64_t ntiles = r1 > r0 ? (r1 - r0 + kGR - 1) / kGR : 0;
-    const bool uni = a.uniform_tq != 0;
-    sh.cnt[tid] = 0u;
-    sh.thr[tid] = 0u;
-    sh.tq[tid] = (q0 + tid < a.q) ? a.tq[q0 + tid] : 0.0f;
-    if (tid == 0) sh.flag = 0;
-
-    // staging of one k-stage: thread t moves 16-byte piece (t & 7) of query rows
-    // (t >> 3) + 32 j (j < 8) and of corpus rows (t >> 3) + 32 j (j < 2)
-    const int piece = tid & 7, srow = tid >> 3;
-    // Loads are unconditional (indices clamped into range; what a clamped load brings is
-    // never used): with no branch around them the compiler keeps exact wait counts, so
-    // the stages in flight stay in flight.
-    auto load_a = [&](u32x4 (&ra)[8], int st) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            int q = q0 + srow + 32 * j;
-            q = q < a.q ? q : a.q - 1;
-            ra[j] = *reinterpret_cast<const u32x4*>(a.qh + int64_t(q) * d + st * kGK + piece * 8);
-        }
-    };
-    auto load_b = [&](u32x4 (&rb)[2], int64_t tile, int st) {
-        tile = tile < ntiles ? tile : ntiles - 1;
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            int64_t row = r0 + tile * kGR + srow + 32 * j;
-            row = row < r1 ? row : r1 - 1;
-            rb[j] = *reinterpret_cast<const u32x4*>(a.emb16 + row * d + st * kGK + piece * 8);
-        }
-    };
-    auto store = [&](int buf, const u32x4 (&ra)[8], const u32x4 (&rb)[2]) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-            *reinterpret_cast<u32x4*>(&sh.a[buf][(srow + 32 * j) * kGPad + piece * 8]) = ra[j];
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-            *reinterpret_cast<u32x4*>(&sh.b[buf][(srow + 32 * j) * kGPad + piece * 8]) = rb[j];
-    };
-
-    uint64_t list[K];                              // query q0 + tid
-#pragma unroll
-    for (int j = 0; j < K; ++j) list[j] = kEmptyKey;
-
-    // stage g = tile * NS + st lives in ring slot st % PB (rows) / st % PA (queries)
-    u32x4 RA[PA][8], RB[PB][2];
-    if (ntiles > 0) {
-#pragma unroll
-        for (int g = 0; g < PB; ++g) load_b(RB[g], 0, g);
-#pragma unroll
-        for (int g = 0; g < PA; ++g) load_a(RA[g], g);
-        store(0, RA[0], RB[0]);
-        load_b(RB[0], PB / NS, PB % NS);
-        load_a(RA[0], PA % NS);
-    }
-    // row attributes (timestamp, modality) of the next tile, prefetched one tile ahead
-    const float tq0 = a.tq[0];
-    float p_ts = 0.0f;
-    int32_t p_mod = 0;
-    // (all threads load and write; the four copies of a row's entry are identical)
-    auto load_attr = [&](int64_t tile) {
-        tile = tile < ntiles ? tile : ntiles - 1;
-        int64_t row = r0 + tile * kGR + (tid & (kGR - 1));
-        row = row < r1 ? row : r1 - 1;
-        p_ts = a.ts[row];
-        p_mod = a.mods[row];
-    };
-    if (ntiles > 0) load_attr(0);
-    __syncthreads();
-
-    for (int64_t t = 0; t < ntiles; ++t) {
-        const int64_t t0 = r0 + t * kGR;
-        sh.keep[tid & (kGR - 1)] = (a.mod_filter < 0 || p_mod == a.mod_filter) ? 1 : 0;
-        sh.w[tid & (kGR - 1)] = !uni ? p_ts : (a.lambda != 0.0f ? expf(-a.lambda * fmaxf(0.0f, tq0 - p_ts)) : 1.0f);
-        load_attr(t + 1);
-        f32x4 acc[4][4];
-#pragma unroll
-        for (int qi = 0; qi < 4; ++qi)
-#pragma unroll
-            for (int ri = 0; ri < 4; ++ri) acc[qi][ri] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int st = 0; st < NS; ++st) {
-            const int buf = st & 1;                    // NS even: parity of the global stage
-            // stage g + 1 into the other buffer, then refill its ring slots
-            const int st1 = (st + 1) % NS;
-            store(buf ^ 1, RA[st1 % PA], RB[st1 % PB]);
-            load_b(RB[st1 % PB], t + (st + 1 + PB) / NS, (st + 1 + PB) % NS);
-            load_a(RA[st1 % PA], (st + 1 + PA) % NS);
-            // stage g from this buffer: two k-steps of 32
-#pragma unroll
-            for (int ks = 0; ks < 2; ++ks) {
-                f16x8 af[4], bf[4];
-#pragma unroll
-                for (int x = 0; x < 4; ++x) {
-                    af[x] = *reinterpret_cast<const f16x8*>(&sh.a[buf][(wq * 64 + x * 16 + m) * kGPad + ks * 32 + kg * 8]);
-                    bf[x] = *reinterpret_cast<const f16x8*>(&sh.b[buf][(x * 16 + m) * kGPad + ks * 32 + kg * 8]);
-                }
-#pragma unroll
-                for (int qi = 0; qi < 4; ++qi)
-#pragma unroll
-                    for (int ri = 0; ri < 4; ++ri)
-                        acc[qi][ri] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[qi], bf[ri], acc[qi][ri], 0, 0, 0);
-            }
-            __syncthreads();
-        }
-        // selection over this tile; acc[qi][ri][i] = C[query 4*kg + i of subtile qi][row m of subtile ri].
-        // Scores are fused in place once; bit e of `pend` marks a score still to offer.
-        float wv[4];
-        bool kp[4];
-#pragma unroll
-        for (int ri = 0; ri < 4; ++ri) {
-            wv[ri] = sh.w[ri * 16 + m];
-            kp[ri] = sh.keep[ri * 16 + m] != 0;
-        }
-        uint64_t pend = 0ull;
-#pragma unroll
-        for (int qi = 0; qi < 4; ++qi)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int ql = wq * 64 + qi * 16 + 4 * kg + i;
-                const int q = q0 + ql;
-                const bool plain = q >= a.q_plain;
-                const int64_t self = (a.self_base >= 0 && plain) ? a.self_base + (q - a.q_plain) : -1;
-                const float tqq = uni ? 0.0f : sh.tq[ql];
-#pragma unroll
-                for (int ri = 0; ri < 4; ++ri) {
-                    const int64_t row = t0 + ri * 16 + m;
-                    float sc;
-                    if (plain) sc = acc[qi][ri][i];
-                    else if (!kp[ri]) sc = -FLT_MAX;
-                    else if (uni) sc = acc[qi][ri][i] * wv[ri];
-                    else if (a.lambda != 0.0f) sc = acc[qi][ri][i] * expf(-a.lambda * fmaxf(0.0f, tqq - wv[ri]));
-                    else sc = acc[qi][ri][i];
-                    acc[qi][ri][i] = sc;
-                    const bool ok = q < a.q && row < r1 && row != self;
-                    pend |= uint64_t(ok) << ((qi * 4 + i) * 4 + ri);
-                }
-            }
-        while (true) {
-            uint32_t th[16];
-#pragma unroll
-            for (int qi = 0; qi < 4; ++qi)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) th[qi * 4 + i] = sh.thr[wq * 64 + qi * 16 + 4 * kg + i];
-#pragma unroll
-            for (int qi = 0; qi < 4; ++qi)
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-#pragma unroll
-                    for (int ri = 0; ri < 4; ++ri) {
-                        const int e = (qi * 4 + i) * 4 + ri;
-                        const float sc = acc[qi][ri][i];
-                        const bool live = (pend >> e) & 1ull;
-                        if (live && ord32(sc) >= th[qi * 4 + i]) {
-                            const int ql = wq * 64 + qi * 16 + 4 * kg + i;
-                            const uint32_t slot = atomicAdd(&sh.cnt[ql], 1u);
-                            if (slot < uint32_t(kGCand)) {
-                                sh.cand[ql][slot] = make_key(sc, uint32_t(t0 + ri * 16 + m));
-                                pend &= ~(1ull << e);
-                            } else {
-                                sh.flag = 1;                 // offered again next round
-                            }
-                        } else {
-                            pend &= ~(1ull << e);            // below the bound: never needed
-                        }
-                    }
-            __syncthreads();
-            const int again = sh.flag;
-            {
-                const uint32_t c = sh.cnt[tid] < uint32_t(kGCand) ? sh.cnt[tid] : uint32_t(kGCand);
-                for (uint32_t j = 0; j < c; ++j) {
-                    const uint64_t key = sh.cand[tid][j];
-                    if (key < list[K - 1]) reg_insert<K>(list, key);
-                }
-                if (list[K - 1] != kEmptyKey) sh.thr[tid] = ord32(key_score(list[K - 1]));
-                sh.cnt[tid] = 0u;
-            }
-            __syncthreads();
-            if (!again) break;
-            if (tid == 0) sh.flag = 0;
-            __syncthreads();
-        }
-    }
-    if (q0 + tid < a.q) {
-        const int q = q0 + tid;
-        uint64_t* out = a.part + ((int64_t(q >> 6) * a.n_rranges + r_id) * kBQ + (q & 63)) * K;
-#pragma unroll
-        for (int j = 0; j < K; ++j) out[j] = list[j];
-    }
-}
-
 // One wave per query: merge n_rranges lists of K keys into the best k_out.
 __global__ __launch_bounds__(64) void k_batch_merge(const uint64_t* __restrict__ part, int32_t n_rranges,
                                                     int32_t kpart, int32_t q, int32_t k_out,
@@ -566,27 +305,9 @@ int launch_batch_t(const BatchArgs& a, hipStream_t s) {
     return MARS_OK;
 }
 
-template <int NS, int K>
-int launch_gemm_t(const BatchArgs& a, hipStream_t s) {
-    const unsigned grid = unsigned(a.n_rranges * ((a.q + kGQ - 1) / kGQ));
-    MARS_LAUNCH((k_batch_gemm<NS, K>), dim3(grid), dim3(kGThreads), 0, s, a);
-    return MARS_OK;
-}
-
-template <int K>
-int launch_gemm_k(const BatchArgs& a, hipStream_t s) {
-    switch (a.d / kGK) {
-        case 4: return launch_gemm_t<4, K>(a, s);
-        case 6: return launch_gemm_t<6, K>(a, s);
-        case 8: return launch_gemm_t<8, K>(a, s);
-        case 12: return launch_gemm_t<12, K>(a, s);
-        default: return set_error(MARS_ERR_UNSUPPORTED, "batched scoring: embedding_dim %d not in {256,384,512,768}", a.d);
-    }
-}
-
 template <int K>
 int launch_batch_k(const BatchArgs& a, hipStream_t s) {
-    if (batch_uses_gemm(a.q)) return launch_gemm_k<K>(a, s);
+    if (batch_uses_gemm(a.q)) return launch_batch_mm(a, s);
     switch (a.d / 32) {
         case 8: return launch_batch_t<8, K>(a, s);
         case 12: return launch_batch_t<12, K>(a, s);

@@ -1,0 +1,345 @@
+// ============================================================================
+//  batch_mm.hip — k_batch_mm: batched scoring for Q >= kGemmMinQ queries, the
+//  shared corpus pass of large query batches and of the k-NN graph builder.
+//
+//  C = E_tile x Q_tile^T for 256 corpus rows x 256 queries per tile on
+//  v_mfma_f32_32x32x16_f16 (fp16 operands, fp32 accumulation). Four waves, one per
+//  SIMD with the whole register file: wave w holds rows 128 (w & 1) .. +127 against
+//  queries 128 (w >> 1) .. +127, 4 x 4 tiles of 32 x 32 (256 accumulators per lane).
+//  Each corpus row is read from HBM once per 256 queries, and the 384 KiB query tile
+//  is read from L2 once per 256 rows.
+//
+//  Operands reach LDS in k-stages of 32 straight from global memory
+//  (global_load_lds_dwordx4, no staging registers), four stage buffers deep: while
+//  stage g computes, stages g + 1 .. g + 3 are in flight. The stage pipeline waits for
+//  its own loads by count (s_waitcnt vmcnt) and meets at plain s_barriers: the
+//  __syncthreads fence would wait for every load in flight, the prefetches included.
+//  Buffer b holds a stage's corpus pieces in the first 64 KiB of LDS and its query
+//  pieces in the next, so every fragment read is one base register plus an immediate.
+//
+//  Selection: after a tile, the raw accumulators go through the free stage buffer 32
+//  rows at a time ([query][row], 16-byte writes and reads), and thread t, the owner of
+//  query q0 + t, fuses its scores (decay, filter) and keeps its best K keys in
+//  registers. Output: K keys per (query, row range) in the layout k_batch_merge reads.
+// ============================================================================
+#include "device.hpp"
+
+#include <cfloat>
+
+namespace mars {
+namespace {
+
+constexpr int kMQ = 256;        // queries per workgroup
+constexpr int kMR = 256;        // rows per tile
+constexpr int kMK = 32;         // k per LDS stage
+constexpr int kMB = 4;          // LDS stage buffers: stages g + 1 .. g + 3 load while g computes
+constexpr int kMThreads = 256;
+constexpr int kMChunk = 32;     // rows per staged chunk of the first tile
+constexpr int kPartQ = 64;      // queries per block of the partial-key layout
+constexpr int kMDma = 4;        // load instructions per wave and operand per stage
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+// All corpus stages in the first 64 KiB and all query stages in the next, so every
+// fragment read is one base register plus an immediate offset.
+struct MmLds {
+    u32x4 e[kMB][kMR * 4];      // 4 x 16 KiB: 256 rows x 4 pieces per stage
+    u32x4 q[kMB][kMQ * 4];      // 4 x 16 KiB: 256 queries x 4 pieces per stage
+    float w[kMR];               // row decay weight (one query time) or row timestamp
+    uint32_t keepm[kMR / kMChunk];   // bit j of word c: row 32 c + j passes the modality filter
+};
+static_assert(sizeof(u32x4) * kMR * 4 == size_t(kMQ / 2) * kMChunk * sizeof(float), "half the queries per operand");
+static_assert(kMThreads / 64 * kMDma * 64 == kMR * 4, "the waves' loads cover a stage");
+
+// s_waitcnt immediates (gfx9 encoding: vmcnt[3:0] and [15:14], expcnt[6:4], lgkmcnt[11:8])
+constexpr int wait_vm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+constexpr int kWaitLgkm0 = 15 | (3 << 14) | (7 << 4);
+
+// Workgroup barrier without the memory fence of __syncthreads (which waits for every
+// load in flight, the stage prefetches included): callers wait for what they need first.
+__device__ inline void lds_barrier() {
+    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+    __builtin_amdgcn_s_barrier();
+}
+
+template <int NS, int K>
+__global__ __launch_bounds__(kMThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void k_batch_mm(BatchArgs a) {
+    static_assert(NS % kMB == 0, "stages are taken kMB at a time");
+    __shared__ __attribute__((aligned(16))) MmLds sh;
+    const int tid = int(threadIdx.x), lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wr = wave & 1, wq = wave >> 1;       // row half, query half
+    const int lm = lane & 31, lh = lane >> 5;
+    constexpr int d = NS * kMK;
+    const int r_id = int(blockIdx.x) % a.n_rranges;
+    const int q0 = (int(blockIdx.x) / a.n_rranges) * kMQ;
+    const int64_t r0 = int64_t(r_id) * a.rows_per_range;
+    const int64_t r1 = (a.n < r0 + a.rows_per_range) ? a.n : r0 + a.rows_per_range;
+    const int64_t ntiles = r1 > r0 ? (r1 - r0 + kMR - 1) / kMR : 0;
+    const bool uni = a.uniform_tq != 0;
+
+    // Stage loads go straight from global memory to LDS (global_load_lds_dwordx4): load
+    // j of a wave fills 64 consecutive 16-byte slots, s = (wave * kMDma + j) * 64 + lane,
+    // i.e. slot s & 3 of row s >> 2, which holds piece (s & 3) ^ ((row >> 1) & 3) of the
+    // row's 32 k. The fragment reads of 8 consecutive rows then hit 8 distinct 16-byte
+    // bank groups. Every stage issues the same loads (rows clamped into range; stages past
+    // the last tile load a clamped tile nobody reads), so the wait counts stay exact.
+    const int srow = (wave * kMDma) * 16 + (lane >> 2);            // + 16 j
+    const int spiece = (lane & 3) ^ ((srow >> 1) & 3);             // the same for every j
+    int qrow[kMDma];
+#pragma unroll
+    for (int j = 0; j < kMDma; ++j) {
+        const int q = q0 + srow + 16 * j;
+        qrow[j] = q < a.q ? q : a.q - 1;
+    }
+    // stage st of tile `tile` (clamped: stages past the last tile load the last one again)
+    auto issue_stage = [&](int tile, int st) {
+        const int b = st & (kMB - 1);              // NS % kMB == 0: a stage's buffer is st % kMB
+        tile = tile < int(ntiles) ? tile : int(ntiles) - 1;
+        const int koff = st * kMK + spiece * 8;
+        const int64_t tbase = r0 + int64_t(tile) * kMR + srow;
+#pragma unroll
+        for (int j = 0; j < kMDma; ++j) {
+            int64_t row = tbase + 16 * j;
+            row = row < r1 ? row : r1 - 1;
+            __builtin_amdgcn_global_load_lds(a.emb16 + row * d + koff, &sh.e[b][(wave * kMDma + j) * 64], 16, 0, 0);
+        }
+#pragma unroll
+        for (int j = 0; j < kMDma; ++j)
+            __builtin_amdgcn_global_load_lds(a.qh + int64_t(qrow[j]) * d + koff, &sh.q[b][(wave * kMDma + j) * 64],
+                                             16, 0, 0);
+    };
+
+    uint64_t list[K];                              // query q0 + tid
+#pragma unroll
+    for (int j = 0; j < K; ++j) list[j] = kEmptyKey;
+    const int my_q = q0 + tid;
+    const bool my_plain = my_q >= a.q_plain;
+    const int64_t my_self = (a.self_base >= 0 && my_plain) ? a.self_base + (my_q - a.q_plain) : -1;
+    const float my_tq = my_q < a.q ? a.tq[my_q] : 0.0f;
+
+    // row attributes (timestamp, modality) of the next tile, one tile ahead
+    const float tq0 = a.tq[0];
+    float p_ts = 0.0f;
+    int32_t p_mod = 0;
+    auto load_attr = [&](int64_t tile) {
+        tile = tile < ntiles ? tile : ntiles - 1;
+        int64_t row = r0 + tile * kMR + tid;
+        row = row < r1 ? row : r1 - 1;
+        p_ts = a.ts[row];
+        p_mod = a.mods[row];
+    };
+    if (ntiles > 0) {
+        load_attr(0);
+        issue_stage(0, 0);
+        issue_stage(0, 1);
+        issue_stage(0, 2);
+        issue_stage(0, 3);
+    }
+
+    f32x16 acc[4][4];
+    f16x8 fa0[4], fb0[4], fa1[4], fb1[4];          // fragments of k-step 0 / 1 of a stage
+    auto read_frags = [&](int b, int kk, f16x8 (&af)[4], f16x8 (&bf)[4]) {
+        const int pc = (2 * kk + lh) ^ ((lm >> 1) & 3);        // swizzled slot of this lane's piece
+#pragma unroll
+        for (int x = 0; x < 4; ++x) {
+            af[x] = __builtin_bit_cast(f16x8, sh.e[b][(wr * 128 + x * 32 + lm) * 4 + pc]);
+            bf[x] = __builtin_bit_cast(f16x8, sh.q[b][(wq * 128 + x * 32 + lm) * 4 + pc]);
+        }
+    };
+    auto mma = [&](const f16x8 (&af)[4], const f16x8 (&bf)[4]) {
+#pragma unroll
+        for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+            for (int qt = 0; qt < 4; ++qt)
+                acc[rt][qt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[rt], bf[qt], acc[rt][qt], 0, 0, 0);
+    };
+    // Stage st of tile t (buffer st % kMB), with its k-step-0 fragments already read:
+    //   read k-step 1; MFMAs of k-step 0 (the reads land meanwhile);
+    //   wait for the loads of stage st + 1 (stages st + 2, st + 3 may stay in flight) and
+    //   meet: every wave's loads of st + 1 landed, every wave is done reading stage st;
+    //   refill this buffer with stage st + 4 (the tile's last stage leaves that to after
+    //   the selection, which needs the buffer); read k-step 0 of stage st + 1;
+    //   MFMAs of k-step 1 (the reads land meanwhile).
+    // Every stage issues one stage of loads, so the wait counts stay exact.
+    // (sched_barrier keeps each block of reads ahead of the MFMAs it overlaps: the
+    // scheduler would otherwise sink the reads next to their uses)
+    auto run_stage = [&](int t, int st, int b) {
+        read_frags(b, 1, fa1, fb1);
+        __builtin_amdgcn_sched_barrier(0);
+        mma(fa0, fb0);
+        if (st + 1 < NS) {
+            __builtin_amdgcn_s_waitcnt(wait_vm(2 * 2 * kMDma));
+            lds_barrier();
+            if (st + 4 < NS) issue_stage(t, st + 4);
+            else issue_stage(t + 1, st + 4 - NS);
+            read_frags((b + 1) & (kMB - 1), 0, fa0, fb0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        mma(fa1, fb1);
+    };
+
+    // Selection staging: a chunk's raw scores as [query][row] fp32, queries 0 .. 127 in the
+    // corpus half of the free stage buffer and 128 .. 255 in its query half. Query q's 32
+    // rows are eight 16-byte slots; rows 4 s .. 4 s + 3 sit in slot s ^ ((q >> 1) & 7), so
+    // the 16-byte writes and reads of 16 consecutive queries hit 16 distinct bank groups.
+    float* const stg_lo = reinterpret_cast<float*>(&sh.e[kMB - 1][0]);
+    float* const stg_hi = reinterpret_cast<float*>(&sh.q[kMB - 1][0]);
+    float* const wbase = wq ? stg_hi : stg_lo;                      // this wave's 128 queries
+    const float* const obase = (tid < 128 ? stg_lo : stg_hi) + (tid & 127) * kMChunk;
+    const int oswz = (tid >> 1) & 7;
+    // acc[rt][qt][v] = C[row wr*128 + rt*32 + 8*(v/4) + 4*lh + v%4][query wq*128 + qt*32 + lm]:
+    // v = 4 g .. 4 g + 3 are rows 4 (2 g + lh) .. + 3 of the chunk, one 16-byte slot
+    auto stage_rows = [&](const f32x16 (&ac)[4]) {
+#pragma unroll
+        for (int qt = 0; qt < 4; ++qt) {
+            const int ql = qt * 32 + lm;
+            const int sw = (ql >> 1) & 7;
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+                *reinterpret_cast<float4*>(wbase + ql * kMChunk + ((2 * g + lh) ^ sw) * 4) =
+                    float4{ac[qt][4 * g], ac[qt][4 * g + 1], ac[qt][4 * g + 2], ac[qt][4 * g + 3]};
+        }
+    };
+    // The fused score: dot * w in the reference's order, filtered rows -FLT_MAX, neighbour
+    // searches (plain queries) the plain dot product. fuse_row is the single-row form of
+    // the chunk loop in select_chunk: the same operations, so the same bits.
+    auto fuse_row = [&](float x, float wv, uint32_t keep) {
+        float f;
+        if (uni) f = x * wv;
+        else if (a.lambda != 0.0f) f = x * expf(-a.lambda * fmaxf(0.0f, my_tq - wv));
+        else f = x;
+        f = keep ? f : -FLT_MAX;
+        return my_plain ? x : f;
+    };
+    // The owner's pass over chunk c of the tile at row t0: its 32 raw scores, the rows'
+    // weights and filter bits, then the rows that can enter its list.
+    auto select_chunk = [&](int c, int64_t t0) {
+        float x[kMChunk], wv[kMChunk];
+        const float* const wc = sh.w + c * kMChunk;
+#pragma unroll
+        for (int s4 = 0; s4 < kMChunk / 4; ++s4) {
+            const float4 v4 = *reinterpret_cast<const float4*>(obase + (s4 ^ oswz) * 4);
+            const float4 w4 = *reinterpret_cast<const float4*>(wc + 4 * s4);
+            x[4 * s4] = v4.x; x[4 * s4 + 1] = v4.y; x[4 * s4 + 2] = v4.z; x[4 * s4 + 3] = v4.w;
+            wv[4 * s4] = w4.x; wv[4 * s4 + 1] = w4.y; wv[4 * s4 + 2] = w4.z; wv[4 * s4 + 3] = w4.w;
+        }
+        const uint32_t km = sh.keepm[c];
+        float sc[kMChunk];
+        if (uni) {
+#pragma unroll
+            for (int j = 0; j < kMChunk; ++j) sc[j] = x[j] * wv[j];
+        } else if (a.lambda != 0.0f) {
+#pragma unroll
+            for (int j = 0; j < kMChunk; ++j) sc[j] = x[j] * expf(-a.lambda * fmaxf(0.0f, my_tq - wv[j]));
+        } else {
+#pragma unroll
+            for (int j = 0; j < kMChunk; ++j) sc[j] = x[j];
+        }
+        // rows at or above the K-th score held (NaN passes to the key test)
+        const float bound = list[K - 1] != kEmptyKey ? key_score(list[K - 1]) : -INFINITY;
+        uint32_t pass = 0u;
+#pragma unroll
+        for (int j = 0; j < kMChunk; ++j) {
+            float f = ((km >> j) & 1u) ? sc[j] : -FLT_MAX;
+            f = my_plain ? x[j] : f;
+            pass |= uint32_t(!(f < bound)) << j;
+        }
+        const int64_t rbase = t0 + c * kMChunk;
+        if (rbase + kMChunk > r1) pass &= (r1 > rbase) ? (0xFFFFFFFFu >> (kMChunk - int(r1 - rbase))) : 0u;
+        if (my_self >= rbase && my_self < rbase + kMChunk) pass &= ~(1u << int(my_self - rbase));
+        while (pass) {
+            const int j = __builtin_ctz(pass);
+            pass &= pass - 1u;
+            // row j's score again, from its raw score in the staging
+            const float v = fuse_row(obase[((j >> 2) ^ oswz) * 4 + (j & 3)], wc[j], (km >> j) & 1u);
+            const uint64_t key = make_key(v, uint32_t(rbase + j));
+            if (key < list[K - 1]) reg_insert<K>(list, key);
+        }
+    };
+
+    for (int64_t t = 0; t < ntiles; ++t) {
+        const int64_t t0 = r0 + t * kMR;
+        {
+            const uint64_t km = __ballot((a.mod_filter < 0 || p_mod == a.mod_filter) ? 1 : 0);
+            if (lane == 0) {
+                sh.keepm[2 * wave] = uint32_t(km);
+                sh.keepm[2 * wave + 1] = uint32_t(km >> 32);
+            }
+        }
+        sh.w[tid] = !uni ? p_ts : (a.lambda != 0.0f ? expf(-a.lambda * fmaxf(0.0f, tq0 - p_ts)) : 1.0f);
+        load_attr(t + 1);
+#pragma unroll
+        for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+            for (int qt = 0; qt < 4; ++qt)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) acc[rt][qt][v] = 0.0f;
+        // stage 0's loads (stages 1 .. 3 may stay in flight), then its k-step-0 fragments
+        __builtin_amdgcn_s_waitcnt(wait_vm(3 * 2 * kMDma));
+        lds_barrier();
+        read_frags(0, 0, fa0, fb0);
+#pragma unroll 1
+        for (int st = 0; st < NS; st += kMB) {
+            run_stage(int(t), st, 0);
+            run_stage(int(t), st + 1, 1);
+            run_stage(int(t), st + 2, 2);
+            run_stage(int(t), st + 3, 3);
+        }
+        // every wave is done with buffer kMB - 1 (the tile's last stage): the selection's
+        // LDS until the deferred load of the next tile's stage kMB - 1 refills it
+        lds_barrier();
+        // 32 rows at a time: the two waves holding them stage their raw scores, then the
+        // owner of each query fuses its 32 scores and keeps its best K. Row half h is a loop,
+        // not unrolled (the code then stays in the instruction cache); the four 32-row tiles
+        // of a half are unrolled, so each stages a fixed accumulator. (The order of the rows
+        // does not change the result: the list keeps the K least keys of a total order.)
+#pragma unroll 1
+        for (int h = 0; h < 2; ++h) {
+#pragma unroll
+            for (int rt = 0; rt < 4; ++rt) {
+                if (wr == h) stage_rows(acc[rt]);
+                lds_barrier();
+                if (my_q < a.q) select_chunk(4 * h + rt, t0);
+                lds_barrier();
+            }
+        }
+        issue_stage(int(t) + 1, kMB - 1);      // into the buffer the selection used
+    }
+    // the last stages' loads (past the last tile) must land before the workgroup ends
+    __builtin_amdgcn_s_waitcnt(wait_vm(0));
+    if (my_q < a.q) {
+        uint64_t* out = a.part + ((int64_t(my_q / kPartQ) * a.n_rranges + r_id) * kPartQ + (my_q % kPartQ)) * K;
+#pragma unroll
+        for (int j = 0; j < K; ++j) out[j] = list[j];
+    }
+}
+
+template <int NS, int K>
+int launch_mm_t(const BatchArgs& a, hipStream_t s) {
+    const unsigned grid = unsigned(a.n_rranges * ((a.q + kMQ - 1) / kMQ));
+    MARS_LAUNCH((k_batch_mm<NS, K>), dim3(grid), dim3(kMThreads), 0, s, a);
+    return MARS_OK;
+}
+
+template <int K>
+int launch_mm_k(const BatchArgs& a, hipStream_t s) {
+    switch (a.d / kMK) {
+        case 8: return launch_mm_t<8, K>(a, s);
+        case 12: return launch_mm_t<12, K>(a, s);
+        case 16: return launch_mm_t<16, K>(a, s);
+        case 24: return launch_mm_t<24, K>(a, s);
+        default: return set_error(MARS_ERR_UNSUPPORTED, "batched scoring: embedding_dim %d not in {256,384,512,768}", a.d);
+    }
+}
+
+}  // namespace
+
+int launch_batch_mm(const BatchArgs& a, hipStream_t s) {
+    MARS_CHECK(a.k >= 1 && a.k <= 16, MARS_ERR_UNSUPPORTED, "batched scoring keeps at most 16 per query (asked %d)",
+               a.k);
+    return a.k <= 8 ? launch_mm_k<8>(a, s) : launch_mm_k<16>(a, s);
+}
+
+}  // namespace mars

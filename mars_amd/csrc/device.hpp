@@ -20,6 +20,28 @@ __device__ inline int lane_id() { return int(threadIdx.x & 63u); }
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+// Insert key x into a register list of K keys kept ascending; x < list[K-1] is
+// checked by the caller.
+template <int K>
+__device__ inline void reg_insert(uint64_t (&list)[K], uint64_t x) {
+    uint64_t v = x;
+#pragma unroll
+    for (int j = 0; j < K; ++j) {
+        const uint64_t lo = list[j] < v ? list[j] : v;
+        const uint64_t hi = list[j] < v ? v : list[j];
+        list[j] = lo;
+        v = hi;
+    }
+}
+
+// Ascending order-preserving code of a score (-0.0 folded onto +0.0): a < b as floats
+// iff ord32(a) < ord32(b) as unsigned; 0 is below every score (no bound yet).
+__device__ inline uint32_t ord32(float s) {
+    const uint32_t u = __float_as_uint(s + 0.0f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
 
 // Loads of data written earlier in the same kernel by other threads: served by
 // L2 (agent-coherent), never by a stale L1 line.

@@ -427,14 +427,17 @@ struct BatchArgs {
     int32_t uniform_tq;      // all query times equal: one decay weight per row
 };
 bool batch_dim_supported(int32_t d);
-// Batches of at least kGemmMinQ queries run the LDS-tiled MFMA kernel (256-query tiles,
-// rows_per_range a multiple of 64); smaller ones the register-streaming scan, which
-// measures faster up to a few hundred queries (1M rows: Q=256 0.8 ms vs 1.36 ms; the
-// tiled kernel wins from ~1K queries: 4.5 ms vs 5.5 ms at Q=1024).
+// Batches of at least kGemmMinQ queries run the LDS-tiled MFMA kernel k_batch_mm
+// (256-query x 256-row tiles, rows_per_range a multiple of 256); smaller ones the
+// register-streaming scan, which measures faster up to a few hundred queries (1M rows:
+// Q=256 0.77 ms vs 0.85 ms; k_batch_mm wins from Q=512: 1.39 ms vs ~1.5 ms, and 2.35 ms
+// at Q=1024).
 constexpr int32_t kGemmMinQ = 512;
 bool batch_uses_gemm(int32_t q);
 int batch_kpart(int32_t k);  // keys per (query, row range) the scan writes
 int launch_batch_scan(const BatchArgs& a, hipStream_t s);
+// Batches of at least kGemmMinQ queries: k_batch_mm (batch_mm.hip).
+int launch_batch_mm(const BatchArgs& a, hipStream_t s);
 int launch_batch_merge(const uint64_t* part, int32_t n_rranges, int32_t kpart, int32_t q, int32_t k_out,
                        uint64_t* out, hipStream_t s);
 int launch_knn_rerank(const float* emb, int64_t q0, int64_t nq, int32_t d, const uint64_t* cand, int32_t kc,

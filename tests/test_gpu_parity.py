@@ -251,6 +251,46 @@ def test_batch_parity_shapes(dev10k, corpus_10k, q, k, filt, rng):
                  corpus_10k.embeddings)
 
 
+@pytest.mark.parametrize("d,k,filt,uniform", [(256, 5, -1, False), (384, 16, 1, True), (512, 8, 2, False),
+                                               (768, 3, -1, True)])
+def test_batch_tiled_widths(d, k, filt, uniform, rng):
+    """520 queries run the 256-query x 256-row tiled kernel: every supported width, both
+    list sizes (K <= 8 and K <= 16), ragged row tiles (2,600 rows), filters and per-query
+    times, against the oracle's top-K."""
+    n = 2600
+    emb, mods, ts, row, col, _ = random_graph(rng, n, d)
+    dev = Dev(emb, mods, ts, row, col, fp16=True)
+    try:
+        qn = rng.choice(n, 520, replace=False)
+        tq = np.float32(T_Q) if uniform else rng.uniform(300, 600, 520).astype(np.float32)
+        batch_check(dev, qn, RetrievalConfig(top_k=k, time_decay_lambda=LAM, modality_filter=filt), tq, emb)
+    finally:
+        dev.close()
+
+
+def test_knn_tiled_width_384(rng):
+    """The k-NN builder (plain dot products, the node itself excluded) at width 384
+    against the exact CPU k-NN; differing neighbours must be near-ties with the 8th."""
+    n, d = 1500, 384
+    emb, mods, ts, _, _, _ = random_graph(rng, n, d)
+    dev = Dev(emb, mods, ts, None, None, fp16=True)
+    try:
+        got = mars_amd.graph_knn(dev.dg, 8)
+        want, sims = corpus.knn_cpu(emb, 8)
+        s = emb @ emb.T
+        np.fill_diagonal(s, -np.inf)
+        mism = 0
+        for i in range(n):
+            if not np.array_equal(got[i], want[i]):
+                mism += 1
+                for j in set(got[i].tolist()) ^ set(want[i].tolist()):
+                    assert abs(s[i, j] - sims[i, 7]) <= 1e-3, (i, j)
+        assert mism <= 0.02 * n
+        assert np.all(got != np.arange(n)[:, None])
+    finally:
+        dev.close()
+
+
 def test_batch_matches_single_query_seeds(dev10k, corpus_10k):
     """The batched seeds agree with the Q=1 fp16 path's seeds up to fp16 near-ties."""
     qn = corpus.pick_queries(corpus_10k.modalities, 32, seed=505)
