@@ -691,6 +691,13 @@ def main() -> int:
                                "scan_frac_of_ceiling": round(achieved / ceiling, 4)}
         log(f"streaming-read ceiling (fp16 rows, no arithmetic): {ceiling:.0f} GB/s = "
             f"{ceiling / HBM_PEAK_GBS:.1%} of peak; the certified scan runs at {achieved / ceiling:.1%} of it")
+        # the batched scan's fragment pattern (16 rows x 64 B per load), ordinary and non-temporal
+        frag = mars_amd.read_pattern(dg, mars_amd.READ_FRAGMENTS, reps=20)
+        frag_nt = mars_amd.read_pattern(dg, mars_amd.READ_FRAGMENTS_NT, reps=20)
+        res["read_ceiling"]["fragments_16x64B"] = round(frag, 1)
+        res["read_ceiling"]["fragments_16x64B_nontemporal"] = round(frag_nt, 1)
+        log(f"fragment-pattern read (16 rows x 64 B per load, no arithmetic): {frag:.0f} GB/s, "
+            f"non-temporal {frag_nt:.0f} GB/s")
 
     if not args.no_cpu and not args.profile_only:
         import oracle

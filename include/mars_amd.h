@@ -182,6 +182,13 @@ int mars_graph_knn_blocks(mars_graph* g, int32_t k, int32_t block_rows, int32_t 
  * graph's fp32 (fp16 = 0) or fp16 rows with no arithmetic, the practical ceiling of the
  * row scans on this device. MARS_ERR_UNSUPPORTED when those rows are absent. */
 int mars_graph_read_ceiling(const mars_graph* g, int32_t fp16, int32_t reps, double* gbps);
+/* Measurement aid, no counterpart in the reference: the same measurement for an access
+ * pattern over the fp16 rows. pattern 0: the plain stream of mars_graph_read_ceiling;
+ * 1: the batched scan's fragment loads, 16 rows x 64 bytes per load instruction (a row's
+ * 64-byte k-chunks back to back, 16-row tiles grid-strided); 2: pattern 1 with
+ * non-temporal loads. Counts whole 16-row tiles. MARS_ERR_INVALID for another pattern,
+ * MARS_ERR_UNSUPPORTED without fp16 rows or when embedding_dim is not a multiple of 32. */
+int mars_graph_read_pattern(const mars_graph* g, int32_t pattern, int32_t reps, double* gbps);
 /* Copy device arrays back to host (any pointer may be NULL to skip): the NSN graph as
  * a packed CSR (row_offsets: num_nodes + 1, col_indices: num_edges) and the episode CSR. */
 int mars_graph_download(const mars_graph* g, int32_t* row_offsets, int32_t* col_indices,

@@ -234,6 +234,7 @@ SIGNATURES = {
     "mars_graph_knn_blocked": (C.c_int, [VP, I32, I32, VP]),
     "mars_graph_knn_blocks": (C.c_int, [VP, I32, I32, I32, I32, VP]),
     "mars_graph_read_ceiling": (C.c_int, [VP, I32, I32, C.POINTER(C.c_double)]),
+    "mars_graph_read_pattern": (C.c_int, [VP, I32, I32, C.POINTER(C.c_double)]),
     "mars_fnv1a64": (C.c_int, [VP, I64, C.POINTER(C.c_uint64)]),
     "mars_graph_set_rows": (C.c_int, [VP, I32, I32, VP, VP, VP]),
     "mars_nsn_edges": (C.c_int, [I32, VP, I32, C.c_double, C.c_uint32, VP, VP, I64, C.POINTER(C.c_int64)]),

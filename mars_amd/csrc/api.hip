@@ -630,6 +630,47 @@ static_assert(sizeof(mars_serve_bench) == 216 && offsetof(mars_serve_bench, g_do
                   offsetof(mars_serve_bench, ins_linked_us) == 192,
               "mars_serve_bench layout");
 
+namespace {
+
+// Best bandwidth (GB/s) of `launch(grid, out, stream)` over 256, 512 and 1024 workgroups:
+// two untimed launches, then reps timed ones, on a stream of its own.
+template <typename Launch>
+int time_read(int64_t bytes, int32_t reps, const char* what, Launch&& launch, double* gbps) {
+    constexpr int32_t kGrids[3] = {256, 512, 1024};
+    hipStream_t s = nullptr;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    uint32_t* out = nullptr;
+    hipError_t e = hipStreamCreateWithFlags(&s, hipStreamNonBlocking);
+    if (e == hipSuccess) e = hipEventCreate(&e0);
+    if (e == hipSuccess) e = hipEventCreate(&e1);
+    if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&out), 1024 * sizeof(uint32_t));
+    double best = 0.0;
+    int rc = MARS_OK;
+    for (int gi = 0; gi < 3 && e == hipSuccess && rc == MARS_OK; ++gi) {
+        for (int w = 0; w < 2 && rc == MARS_OK; ++w) rc = launch(kGrids[gi], out, s);
+        if (rc != MARS_OK) break;
+        e = hipEventRecord(e0, s);
+        for (int r = 0; r < reps && rc == MARS_OK && e == hipSuccess; ++r) rc = launch(kGrids[gi], out, s);
+        if (rc != MARS_OK || e != hipSuccess) break;
+        e = hipEventRecord(e1, s);
+        if (e == hipSuccess) e = hipEventSynchronize(e1);
+        float ms = 0.0f;
+        if (e == hipSuccess) e = hipEventElapsedTime(&ms, e0, e1);
+        if (e == hipSuccess && ms > 0.0f) best = std::max(best, double(bytes) * reps / (double(ms) * 1e-3) / 1e9);
+    }
+    if (s) (void)hipStreamSynchronize(s);
+    if (out) (void)hipFree(out);
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    if (s) (void)hipStreamDestroy(s);
+    if (rc != MARS_OK) return rc;
+    if (e != hipSuccess) return set_error(MARS_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+    *gbps = best;
+    return MARS_OK;
+}
+
+}  // namespace
+
 extern "C" {
 
 const char* mars_last_error(void) { return g_err; }
@@ -1594,6 +1635,7 @@ int mars_query_global_batch_knn(const mars_graph* gh, mars_ctx* ch, const float*
     return MARS_OK;
 }
 
+
 int mars_graph_read_ceiling(const mars_graph* gh, int32_t fp16, int32_t reps, double* gbps) {
     MARS_CHECK(gh && gbps && reps > 0, MARS_ERR_INVALID, "bad arguments");
     const Graph& g = gh->g;
@@ -1603,38 +1645,26 @@ int mars_graph_read_ceiling(const mars_graph* gh, int32_t fp16, int32_t reps, do
     const int64_t bytes = int64_t(n) * g.d * (fp16 ? 2 : 4) / 16 * 16;
     MARS_CHECK(bytes > 0, MARS_ERR_INVALID, "empty graph");
     MARS_TRY(use_device(g.device));
-    constexpr int32_t kGrids[3] = {256, 512, 1024};
-    hipStream_t s = nullptr;
-    hipEvent_t e0 = nullptr, e1 = nullptr;
-    uint32_t* out = nullptr;
-    hipError_t e = hipStreamCreateWithFlags(&s, hipStreamNonBlocking);
-    if (e == hipSuccess) e = hipEventCreate(&e0);
-    if (e == hipSuccess) e = hipEventCreate(&e1);
-    if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&out), 1024 * sizeof(uint32_t));
-    double best = 0.0;
-    int rc = MARS_OK;
-    for (int gi = 0; gi < 3 && e == hipSuccess && rc == MARS_OK; ++gi) {
-        for (int w = 0; w < 2 && rc == MARS_OK; ++w) rc = launch_read_rows(rows, bytes, kGrids[gi], 0x9E3779B9u, out, s);
-        if (rc != MARS_OK) break;
-        e = hipEventRecord(e0, s);
-        for (int r = 0; r < reps && rc == MARS_OK && e == hipSuccess; ++r)
-            rc = launch_read_rows(rows, bytes, kGrids[gi], 0x9E3779B9u, out, s);
-        if (rc != MARS_OK || e != hipSuccess) break;
-        e = hipEventRecord(e1, s);
-        if (e == hipSuccess) e = hipEventSynchronize(e1);
-        float ms = 0.0f;
-        if (e == hipSuccess) e = hipEventElapsedTime(&ms, e0, e1);
-        if (e == hipSuccess && ms > 0.0f) best = std::max(best, double(bytes) * reps / (double(ms) * 1e-3) / 1e9);
-    }
-    if (s) (void)hipStreamSynchronize(s);
-    if (out) (void)hipFree(out);
-    if (e0) (void)hipEventDestroy(e0);
-    if (e1) (void)hipEventDestroy(e1);
-    if (s) (void)hipStreamDestroy(s);
-    if (rc != MARS_OK) return rc;
-    if (e != hipSuccess) return set_error(MARS_ERR_HIP, "read ceiling: %s", hipGetErrorString(e));
-    *gbps = best;
-    return MARS_OK;
+    return time_read(bytes, reps, "read ceiling", [&](int32_t wg, uint32_t* out, hipStream_t s) {
+        return launch_read_rows(rows, bytes, wg, 0x9E3779B9u, out, s);
+    }, gbps);
+}
+
+int mars_graph_read_pattern(const mars_graph* gh, int32_t pattern, int32_t reps, double* gbps) {
+    MARS_CHECK(gh && gbps && reps > 0, MARS_ERR_INVALID, "bad arguments");
+    MARS_CHECK(pattern >= 0 && pattern <= 2, MARS_ERR_INVALID, "read pattern %d not in [0, 2]", pattern);
+    if (pattern == 0) return mars_graph_read_ceiling(gh, 1, reps, gbps);
+    const Graph& g = gh->g;
+    MARS_CHECK(g.emb16 != nullptr, MARS_ERR_UNSUPPORTED, "no fp16 rows");
+    MARS_CHECK(g.d % 32 == 0, MARS_ERR_UNSUPPORTED, "fragment pattern: embedding_dim %d not a multiple of 32", g.d);
+    const int32_t n = __atomic_load_n(&g.n, __ATOMIC_ACQUIRE);
+    const int64_t rows16 = int64_t(n) / 16 * 16;
+    MARS_CHECK(rows16 > 0, MARS_ERR_INVALID, "fewer than 16 rows");
+    MARS_TRY(use_device(g.device));
+    const int64_t bytes = rows16 * g.d * 2;
+    return time_read(bytes, reps, "read pattern", [&](int32_t wg, uint32_t* out, hipStream_t s) {
+        return launch_read_frags(g.emb16, rows16, g.d * 2, wg, pattern == 2, 0x9E3779B9u, out, s);
+    }, gbps);
 }
 
 int mars_graph_knn_blocked(mars_graph* gh, int32_t k, int32_t block_rows, int32_t* nbrs) {

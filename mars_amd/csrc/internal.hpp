@@ -402,6 +402,9 @@ int launch_episode(const EpisodeArgs& a, hipStream_t s);
 int launch_convert_f16(const float* in, __half* out, int64_t count, hipStream_t s);
 // Streaming read of bytes (a multiple of 16) with wg workgroups; out holds wg words.
 int launch_read_rows(const void* p, int64_t bytes, int32_t wg, uint32_t sentinel, uint32_t* out, hipStream_t s);
+// 16 rows x 64 B per load instruction over the first n_rows / 16 * 16 rows (nt: non-temporal)
+int launch_read_frags(const void* rows, int64_t n_rows, int32_t row_bytes, int32_t wg, bool nt, uint32_t sentinel,
+                      uint32_t* out, hipStream_t s);
 
 // ---- batched MFMA scoring (defined in batch.hip) ---------------------------------------
 struct BatchArgs {

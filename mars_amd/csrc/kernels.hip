@@ -1213,6 +1213,35 @@ __global__ __launch_bounds__(256) void k_read_rows(const u32x4* __restrict__ p, 
     if (acc == sentinel && threadIdx.x == 0) out[blockIdx.x] = acc;
 }
 
+// The batched scan's fragment pattern, no arithmetic: each load instruction reads 16 rows
+// x 64 bytes (lane l: row l % 16 of the tile, 16-byte piece l / 16 of the 64-byte k-chunk,
+// the v_mfma_f32_16x16x32_f16 B operand), a tile's k-chunks back to back, tiles of 16 rows
+// grid-strided over the waves. NT: non-temporal loads.
+template <bool NT>
+__global__ __launch_bounds__(256) void k_read_frags(const unsigned char* __restrict__ rows, int64_t n_tiles,
+                                                    int32_t row_bytes, uint32_t sentinel, uint32_t* out) {
+    const int lane = int(threadIdx.x) & 63;
+    const int64_t nwaves = int64_t(gridDim.x) * 4;
+    const int nchunks = row_bytes / 64;
+    uint32_t acc = 0u;
+    for (int64_t t = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6); t < n_tiles; t += nwaves) {
+        const u32x4* p = reinterpret_cast<const u32x4*>(rows + (t * 16 + (lane & 15)) * row_bytes + (lane >> 4) * 16);
+        int c = 0;
+        for (; c + 4 <= nchunks; c += 4) {
+            u32x4 v[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) v[j] = NT ? __builtin_nontemporal_load(p + (c + j) * 4) : p[(c + j) * 4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc ^= v[j].x ^ v[j].y ^ v[j].z ^ v[j].w;
+        }
+        for (; c < nchunks; ++c) {
+            const u32x4 v = NT ? __builtin_nontemporal_load(p + c * 4) : p[c * 4];
+            acc ^= v.x ^ v.y ^ v.z ^ v.w;
+        }
+    }
+    if (acc == sentinel && threadIdx.x == 0) out[blockIdx.x] = acc;
+}
+
 template <typename T, typename QF>
 KernelLaunch scan_launch_t(const ScanArgs& a) {
     KernelLaunch l;
@@ -1338,6 +1367,15 @@ int launch_episode(const EpisodeArgs& a, hipStream_t s) {
 int launch_read_rows(const void* p, int64_t bytes, int32_t wg, uint32_t sentinel, uint32_t* out, hipStream_t s) {
     MARS_LAUNCH(k_read_rows, dim3(unsigned(wg)), dim3(256), 0, s, static_cast<const u32x4*>(p), bytes / 16,
                 sentinel, out);
+    return MARS_OK;
+}
+
+int launch_read_frags(const void* rows, int64_t n_rows, int32_t row_bytes, int32_t wg, bool nt, uint32_t sentinel,
+                      uint32_t* out, hipStream_t s) {
+    const int64_t tiles = n_rows / 16;
+    const auto* r = static_cast<const unsigned char*>(rows);
+    if (nt) MARS_LAUNCH(k_read_frags<true>, dim3(unsigned(wg)), dim3(256), 0, s, r, tiles, row_bytes, sentinel, out);
+    else MARS_LAUNCH(k_read_frags<false>, dim3(unsigned(wg)), dim3(256), 0, s, r, tiles, row_bytes, sentinel, out);
     return MARS_OK;
 }
 
