@@ -209,6 +209,8 @@ def tiled_pass(args, mars_amd, corpus, c, qnodes, N, D, K, pctl, lat_resident, h
 
 
 SERVE_MODES = {
+    "auto": "q1 while one certified Q=1 query per arrival keeps the global server under half busy "
+            "(measured Q=1 latency x global arrival rate < 0.5), link beyond",
     "q1": "one global query per call (certified fp16 scan); each insert finds its own k-NN",
     "batch": "batched global calls; each insert finds its own k-NN",
     "link": "batched global calls that also find the k-NN of the nodes inserted since the last call "
@@ -372,8 +374,8 @@ def main() -> int:
                     help="nearest neighbours per node in the NSN graph (0: intra-episode pairs only)")
     ap.add_argument("--batch-q", type=int, default=64, help="queries per batched MFMA scoring call")
     ap.add_argument("--batch-max", type=int, default=64, help="most global queries per batched call when serving")
-    ap.add_argument("--serve-modes", default="q1,link",
-                    help="servers of the streaming pass, one run each: q1, batch, link (see SERVE_MODES)")
+    ap.add_argument("--serve-modes", default="auto,q1,link",
+                    help="servers of the streaming pass, one run each: auto, q1, batch, link (see SERVE_MODES)")
     ap.add_argument("--stream-insert-batch", type=int, default=10, help="nodes per insert call when streaming")
     ap.add_argument("--knn-block", type=int, default=0,
                     help="k-NN of the NSN graph within blocks of this many consecutive ids (0: exact, all pairs)")
@@ -624,8 +626,18 @@ def main() -> int:
         per = M // len(modes) // 10 * 10                  # whole 10-node episodes per run
         per_q = args.stream_queries // len(modes)
         for i, m in enumerate(modes):
-            runs.append(serve_pass(args, mars_amd, corpus, lib, check, full, dg, ctx, qnodes[W + i * per_q:], per_q,
-                                   ep_cfgs, gcfg, N + M, D, first, per, m, pctl))
+            chosen = m
+            if m == "auto":
+                # global queries arrive at half the query rate (1,000/s alternating global and episode)
+                load = float(np.median(lat_c)) * 1e-6 * 500.0
+                chosen = "q1" if load < 0.5 else "link"
+                log(f"streaming [auto]: certified Q=1 p50 {np.median(lat_c):.0f} us x 500 global/s = "
+                    f"{load:.0%} busy -> {chosen}")
+            r = serve_pass(args, mars_amd, corpus, lib, check, full, dg, ctx, qnodes[W + i * per_q:], per_q,
+                           ep_cfgs, gcfg, N + M, D, first, per, chosen, pctl)
+            if m == "auto":
+                r = dict(r, mode="auto", chosen=chosen, q1_load=round(load, 4))
+            runs.append(r)
             first += per
         out["streaming"] = dict(base_nodes=N, insert_batch=args.stream_insert_batch, insert_rate_target=2000.0,
                                 query_rate_target=1000.0, knn_k=args.knn_k,

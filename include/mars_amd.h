@@ -149,6 +149,11 @@ void        mars_config_default(mars_retrieval_config* cfg);
 int mars_graph_create(const mars_graph_desc* desc, mars_graph** out);
 /* free_device */
 int mars_graph_destroy(mars_graph* g);
+/* The calls below that replace device arrays (mars_graph_set_episode_ids,
+ * mars_graph_set_episode_csr, mars_graph_disable_fp16, mars_graph_set_csr) free the
+ * arrays they replace: no query, on any context or thread, may run on the graph during
+ * them. (Inserts and links do not free what queries read: queries keep running during
+ * those.) */
 /* upload_episode_ids: n must equal num_nodes; NULL/n<=0 clears (reference: silent no-op). */
 int mars_graph_set_episode_ids(mars_graph* g, const int32_t* episode_ids, int32_t n);
 /* upload_episode_csr: offsets has num_episodes+1 entries, members has offsets[num_episodes]. */
@@ -262,7 +267,12 @@ typedef struct mars_insert_stats {
  * neighbour ids found (-1: none). Nodes become visible to scans first (queryable_us),
  * then their edges (linked_us); a query that runs meanwhile sees each row either as
  * before or as after the insert. MARS_ERR_CAPACITY when capacity_nodes /
- * capacity_edges (mars_graph_desc) cannot hold the insert: nothing is changed then. */
+ * capacity_edges (mars_graph_desc) cannot hold the insert: nothing is changed then.
+ * Any other error (MARS_ERR_NOMEM, MARS_ERR_HIP) may come after the nodes were
+ * published: they are then queryable without their edges (num_nodes of
+ * mars_graph_get_view has moved past them, and their episodes count as opened), and the
+ * same insert cannot be repeated. mars_graph_link_knn(g, first, n_new, knn_k, ...) with
+ * first = the num_nodes read before the call adds the edges the insert would have. */
 int mars_graph_insert(mars_graph* g, int32_t n_new, const float* embeddings, const int32_t* modalities,
                       const float* timestamps, const int32_t* episode_ids, int32_t knn_k,
                       int32_t* out_knn, mars_insert_stats* stats);

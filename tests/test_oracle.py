@@ -199,6 +199,48 @@ def test_bfs_own_score_wins_when_larger():
     assert sc[1] == pytest.approx(0.9 * 0.8) and sc[2] == pytest.approx(0.95 * 0.8)
 
 
+def test_bfs_scales_hand_chains():
+    """bfs_scales on hand graphs: a seed keeps its own scale; a child takes
+    max(|decay| * parent's, 0.8 * own). The chain 3 -> 1 -> 0 -> 2 is visited out of id
+    order, so a parent looked up by id instead of visit position fails; the branch
+    4 -> {5, 6} checks that siblings share one parent scale."""
+    row, col = _csr(7, [(3, 1), (1, 0), (0, 2), (4, 5), (4, 6)])
+    fin = np.array([0.1, 0.2, 0.05, 0.9, 0.6, 0.3, 0.01])
+    r = oracle.bfs(row, col, fin, np.array([3, 4], np.int32), np.array([0.9, 0.6]), 3, 0.5)
+    scale = np.array([2.0, 1.0, 0.5, 3.0, 0.25, 4.0, 0.1])
+    got = dict(zip(r["ids"].tolist(), oracle.bfs_scales(r, scale, 0.5).tolist()))
+    want = {3: 3.0, 4: 0.25}
+    want[1] = max(0.5 * want[3], 0.8 * 1.0)          # 1.5
+    want[5] = max(0.5 * want[4], 0.8 * 4.0)          # 3.2: own scale wins
+    want[6] = max(0.5 * want[4], 0.8 * 0.1)          # 0.125: the parent's wins
+    want[0] = max(0.5 * want[1], 0.8 * 2.0)          # 1.6
+    want[2] = max(0.5 * want[0], 0.8 * 0.5)          # 0.8
+    assert got == pytest.approx(want)
+    # a negative decay scales by its magnitude
+    neg = dict(zip(r["ids"].tolist(), oracle.bfs_scales(r, scale, -0.5).tolist()))
+    assert neg == pytest.approx(want)
+
+
+def test_result_scales_seeds_are_the_row_scale(rng):
+    """result_scales of a whole query: every result has a scale; a seed's is the row scale
+    w * sum_d |e_d q_d| (numpy, fp64), and no node's is below 0.8 times its own."""
+    g = _query_graph(rng)
+    q = g.embeddings[3]
+    cfg = oracle.config(8, 2, 1e-3, 0.5, -1, 200)
+    ref = oracle.query(g, q, 600.0, cfg)
+    scl = oracle.result_scales(g, q, 600.0, cfg, ref)
+    ids = [r[0] for r in ref["results"]]
+    assert set(ids) <= set(scl)
+    # w = exp(-lambda * age), the age taken in fp32 as the reference does
+    age = np.maximum(np.float32(0), np.float32(600.0) - g.timestamps.astype(np.float32)).astype(np.float64)
+    w = np.exp(-np.float64(np.float32(1e-3)) * age)
+    row_scale = w * np.abs(g.embeddings.astype(np.float64) * q.astype(np.float64)).sum(1)
+    for s in ref["seeds"]:
+        assert scl[int(s)] == pytest.approx(row_scale[int(s)], rel=1e-6)
+    for u, v in scl.items():
+        assert v >= 0.8 * row_scale[u] * (1 - 1e-9)
+
+
 def test_bfs_stops_on_empty_frontier():
     row, col = _csr(4, [(0, 1)])
     r = oracle.bfs(row, col, np.zeros(4), np.array([0], np.int32), np.array([1.0]), 5, 0.5)
