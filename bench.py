@@ -311,22 +311,32 @@ def compare_results(got, want, scl):
     return True
 
 
-def parity_check(mars_amd, oracle, dg, ctx, dq, first, D, og, c, qnodes, t_q, gcfg, ocfg, refs):
-    """The GPU's answers to the queries the CPU baseline answered, against those oracle
-    answers. Each query runs on the fp32-scan path (whose seeds the context keeps) and on
-    the certified path (the one `value` times); the two must be bit-identical. The seed set
+def capture_answers(mars_amd, dg, ctx, dq, first, D, count, t_q, gcfg):
+    """The GPU's answers to timed queries first .. first + count - 1, taken on the resident
+    corpus before the streaming passes grow it: each query on the fp32-scan path (whose
+    seeds the context keeps) and on the certified path (the one `value` times)."""
+    out = []
+    for i in range(count):
+        ptr = dq.ptr + (first + i) * D * 4
+        ctx.certified = False
+        got = mars_amd.query_memory_fast_device(dg, ctx, ptr, t_q, gcfg)
+        seeds = ctx.last_seeds()[0].copy()
+        ctx.certified = True
+        got_c = mars_amd.query_memory_fast_device(dg, ctx, ptr, t_q, gcfg)
+        ctx.certified = False
+        out.append((got, seeds, got_c))
+    return out
+
+
+def parity_check(oracle, first, og, c, qnodes, t_q, gcfg, ocfg, refs, answers):
+    """The GPU's answers (capture_answers) to the queries the CPU baseline answered, against
+    those oracle answers. The fp32 and certified answers must be bit-identical. The seed set
     must equal the oracle's up to near-ties at the K-th score (the oracle then runs again
     from the GPU's seeds); results as compare_results."""
     bad = []
     for i, ref in enumerate(refs):
         q = c.embeddings[qnodes[first + i]]
-        ptr = dq.ptr + (first + i) * D * 4
-        ctx.certified = False
-        got = mars_amd.query_memory_fast_device(dg, ctx, ptr, t_q, gcfg)
-        seeds, _ = ctx.last_seeds()
-        ctx.certified = True
-        got_c = mars_amd.query_memory_fast_device(dg, ctx, ptr, t_q, gcfg)
-        ctx.certified = False
+        got, seeds, got_c = answers[i]
         if got_c != got:
             bad.append(i)
             continue
@@ -613,6 +623,11 @@ def main() -> int:
                                   scan_gbs=bytes_f16 / float(kern_h.mean()) / 1e3,
                                   scan_frac=bytes_f16 / float(kern_h.mean()) / 1e3 / HBM_PEAK_GBS)
 
+    # the GPU's answers for the parity check against the CPU baseline, before any pass
+    # below inserts nodes (the oracle holds the resident corpus)
+    answers = None
+    if not args.no_cpu and not args.profile_only:
+        answers = capture_answers(mars_amd, dg, ctx, dq, W, D, min(args.cpu_queries, S), corpus.QUERY_TIME, gcfg)
     if args.checkpoint_dir and not args.profile_only:
         out["checkpoint"] = checkpoint_pass(args, mars_amd, dg)
     if not args.profile_only and args.tiled_queries > 0:
@@ -721,8 +736,7 @@ def main() -> int:
             t0 = time.perf_counter()
             refs.append(oracle.query(og, c.embeddings[node], corpus.QUERY_TIME, ocfg))
             cl.append((time.perf_counter() - t0) * 1e6)
-        res_parity = parity_check(mars_amd, oracle, dg, ctx, dq, W, D, og, c, qnodes, corpus.QUERY_TIME, gcfg, ocfg,
-                                  refs)
+        res_parity = parity_check(oracle, W, og, c, qnodes, corpus.QUERY_TIME, gcfg, ocfg, refs, answers)
         res["cpu_baseline"] = {"value": round(pctl(cl, .99), 1), "unit": "us", "cores": oracle.lib.oracle_num_threads(),
                                "kind": "port",
                                "sample": f"first {nc} of the timed global queries (same corpus, graph and query "
