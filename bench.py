@@ -430,10 +430,13 @@ def main() -> int:
     t = time.time()
     if args.knn_k > 0:
         def knn_progress(done, total):
-            if done % 10 == 0 or done == total:
+            if done % 10 == 0 or done == total or N > 2_000_000:
                 log(f"{args.knn_k}-NN block {done}/{total}: {time.time() - t:.1f}s")
-        # fp16 MFMA candidates + exact fp32 rescoring
-        knn = mars_amd.graph_knn(dg, args.knn_k, args.knn_block, knn_progress if args.knn_block else None)
+        # fp16 MFMA candidates + exact fp32 rescoring; above 2M rows the all-pairs build runs in
+        # pieces of 1M query nodes (a progress line each)
+        big = args.knn_block == 0 and N > 2_000_000
+        knn = mars_amd.graph_knn(dg, args.knn_k, args.knn_block,
+                                 knn_progress if (args.knn_block or big) else None)
         log(f"{args.knn_k}-NN on the GPU" + (f" (blocks of {args.knn_block} ids)" if args.knn_block else "") +
             f": {time.time() - t:.1f}s")
     else:

@@ -182,6 +182,11 @@ int mars_graph_knn_blocked(mars_graph* g, int32_t k, int32_t block_rows, int32_t
  * the node count), so a caller can build a large graph block by block. */
 int mars_graph_knn_blocks(mars_graph* g, int32_t k, int32_t block_rows, int32_t first_block, int32_t n_blocks,
                           int32_t* nbrs);
+/* The all-pairs k-NN of nodes first .. first + count - 1 (each node's k nearest among all
+ * nodes, itself excluded; the same answer as rows first .. of mars_graph_knn), so that an
+ * all-pairs build can run in pieces (nbrs: count * k). No reference counterpart: the
+ * reference builds its graph on the host (memory_graph.cpp:102-189). */
+int mars_graph_knn_range(mars_graph* g, int32_t k, int32_t first, int32_t count, int32_t* nbrs);
 /* Measurement aid, no counterpart in the reference: the bandwidth (GB/s, best of 256,
  * 512 and 1024 workgroups, reps timed launches each) of a plain streaming read of the
  * graph's fp32 (fp16 = 0) or fp16 rows with no arithmetic, the practical ceiling of the

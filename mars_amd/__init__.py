@@ -428,12 +428,28 @@ def query_global_batch(dg: DeviceMemoryGraph, ctx: QueryContext, d_queries_ptr: 
     return res
 
 
-def graph_knn(dg: DeviceMemoryGraph, k: int = 8, block_rows: int = 0, progress=None) -> np.ndarray:
+def graph_knn_range(dg: DeviceMemoryGraph, k: int, first: int, count: int) -> np.ndarray:
+    """All-pairs k nearest neighbours of nodes first .. first + count - 1 (rows of graph_knn)."""
+    out = np.empty((count, k), np.int32)
+    check(lib.mars_graph_knn_range(dg.handle, int(k), int(first), int(count), _ptr(out)), "mars_graph_knn_range")
+    return out
+
+
+def graph_knn(dg: DeviceMemoryGraph, k: int = 8, block_rows: int = 0, progress=None,
+              piece: int = 1 << 20) -> np.ndarray:
     """k nearest neighbours of every node (fp16 MFMA candidates + exact fp32 rescoring);
     block_rows > 0: among the nodes of each block of block_rows consecutive ids
-    (progress(done, total) is called after each block when given)."""
+    (progress(done, total) is called after each block when given); block_rows = 0 with a
+    progress callback: all pairs, in pieces of `piece` query nodes, progress after each."""
     out = np.empty((dg.num_nodes, k), np.int32)
-    if block_rows > 0 and progress is not None:
+    if block_rows <= 0 and progress is not None:
+        n = dg.num_nodes
+        total = (n + piece - 1) // piece
+        for b in range(total):
+            lo = b * piece
+            out[lo:lo + piece] = graph_knn_range(dg, k, lo, min(piece, n - lo))
+            progress(b + 1, total)
+    elif block_rows > 0 and progress is not None:
         nb = (dg.num_nodes + block_rows - 1) // block_rows
         for b in range(nb):                  # one block per call: the caller reports each
             lo = b * block_rows

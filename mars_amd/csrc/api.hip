@@ -1738,6 +1738,56 @@ int mars_graph_knn_blocks(mars_graph* gh, int32_t k, int32_t block_rows, int32_t
     return rc;
 }
 
+int mars_graph_knn_range(mars_graph* gh, int32_t k, int32_t first, int32_t count, int32_t* nbrs) {
+    MARS_CHECK(gh && nbrs && k >= 1 && k <= 16 && first >= 0 && count >= 0, MARS_ERR_INVALID,
+               "k-NN range: bad arguments (k=%d, first=%d, count=%d)", k, first, count);
+    std::lock_guard<std::mutex> lock(gh->mu);
+    Graph& g = gh->g;
+    MARS_CHECK(g.emb16 != nullptr, MARS_ERR_UNSUPPORTED, "k-NN reads the fp16 corpus: enable it first");
+    MARS_CHECK(batch_dim_supported(g.d), MARS_ERR_UNSUPPORTED, "k-NN: embedding_dim %d unsupported", g.d);
+    MARS_CHECK(int64_t(first) + count <= g.n, MARS_ERR_INVALID, "k-NN range: [%d, %lld) beyond the %d nodes", first,
+               (long long)first + count, g.n);
+    if (count == 0) return MARS_OK;
+    MARS_TRY(use_device(g.device));
+    constexpr int32_t kChunk = 1024;                 // queries per launch
+    constexpr int32_t kCand = 16;
+    const int64_t n = g.n;
+    int32_t nrr = 0, nqb = 0;
+    int64_t rpr = 0;
+    batch_grid(n, kChunk, &nrr, &nqb, &rpr);
+    float* tq = nullptr; uint64_t* part = nullptr; uint64_t* cand = nullptr; int32_t* dn = nullptr;
+    hipStream_t s = nullptr;
+    int rc = MARS_OK;
+    auto cleanup = [&]() { dfree(tq); dfree(part); dfree(cand); dfree(dn); if (s) (void)hipStreamDestroy(s); };
+    if ((rc = dmalloc(&tq, kChunk)) || (rc = dmalloc(&part, size_t(nqb) * nrr * 64 * kCand)) ||
+        (rc = dmalloc(&cand, size_t(kChunk) * kCand)) || (rc = dmalloc(&dn, size_t(count) * k))) {
+        cleanup();
+        return rc;
+    }
+    hipError_t e = hipStreamCreateWithFlags(&s, hipStreamNonBlocking);
+    if (e == hipSuccess) e = hipMemsetAsync(tq, 0, kChunk * sizeof(float), s);
+    if (e != hipSuccess) { cleanup(); return set_error(MARS_ERR_HIP, "k-NN range setup: %s", hipGetErrorString(e)); }
+    // queries [q0, q0 + q) against every node; the query's own id is excluded
+    for (int64_t q0 = first; q0 < int64_t(first) + count && rc == MARS_OK; q0 += kChunk) {
+        const int32_t q = int32_t(std::min<int64_t>(kChunk, int64_t(first) + count - q0));
+        BatchArgs a{};
+        a.emb16 = g.emb16; a.n = n; a.d = g.d; a.qh = g.emb16 + q0 * g.d; a.q = q; a.tq = tq;
+        a.ts = g.ts; a.mods = g.mods; a.lambda = 0.0f; a.mod_filter = -1; a.k = kCand; a.q_plain = 0; a.self_base = q0;
+        a.part = part; a.uniform_tq = 1;
+        a.rows_per_range = rpr; a.n_rranges = nrr; a.n_qblocks = (q + 63) / 64;
+        rc = launch_batch_scan(a, s);
+        if (rc == MARS_OK) rc = launch_batch_merge(part, nrr, kCand, q, kCand, cand, s);
+        if (rc == MARS_OK) rc = launch_knn_rerank(g.emb, q0, q, g.d, cand, kCand, k, dn + (q0 - first) * k, s);
+    }
+    if (rc == MARS_OK) {
+        e = hipStreamSynchronize(s);
+        if (e == hipSuccess) e = hipMemcpy(nbrs, dn, size_t(count) * k * sizeof(int32_t), hipMemcpyDeviceToHost);
+        if (e != hipSuccess) rc = set_error(MARS_ERR_HIP, "k-NN range: %s", hipGetErrorString(e));
+    }
+    cleanup();
+    return rc;
+}
+
 int mars_graph_knn(mars_graph* gh, int32_t k, int32_t* nbrs) {
     MARS_CHECK(gh, MARS_ERR_INVALID, "null graph");
     return mars_graph_knn_blocked(gh, k, std::max<int32_t>(1, gh->g.n), nbrs);

@@ -333,6 +333,19 @@ def test_gpu_knn_matches_cpu_exact():
         assert seen == [(1, 4), (2, 4), (3, 4), (4, 4)]
         blk = np.arange(c.num_nodes) // 1700
         assert np.all(blk[whole] == blk[:, None])          # neighbours within the node's block
+        # the all-pairs build in query ranges (ragged last range) and in pieces with progress
+        n = c.num_nodes
+        ranged = np.concatenate([mars_amd.graph_knn_range(dev.dg, 8, a, min(1000, n - a)) for a in range(0, n, 1000)])
+        np.testing.assert_array_equal(ranged, got)
+        seen = []
+        pieced = mars_amd.graph_knn(dev.dg, 8, 0, progress=lambda d, t: seen.append((d, t)), piece=2500)
+        np.testing.assert_array_equal(pieced, got)
+        assert seen == [(1, 3), (2, 3), (3, 3)]
+        assert mars_amd.graph_knn_range(dev.dg, 8, n, 0).shape == (0, 8)
+        from mars_amd._lib import MarsError
+        with pytest.raises(MarsError) as e:
+            mars_amd.graph_knn_range(dev.dg, 8, n - 10, 20)
+        assert e.value.code == -1
     finally:
         dev.close()
 
