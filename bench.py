@@ -112,7 +112,7 @@ def maintenance_pass(mars_amd, dg, ctx, dq, first, count, D, gcfg, pctl, reps=20
         t_again.append((time.perf_counter() - t0) * 1e6)
     res = dict(nodes=n, edges=int(len(hits)),
                importance_update=dict(p50_us=pctl(t_imp, .5), p99_us=pctl(t_imp, .99), bytes=8 * n),
-               novelty=dict(p50_us=pctl(t_nov, .5), p99_us=pctl(t_nov, .99), path="certified fp16 scan, top-1"),
+               novelty=dict(p50_us=pctl(t_nov, .5), p99_us=pctl(t_nov, .99), path="certified candidate scan, top-1"),
                edge_hit_count=dict(p50_us=pctl(t_hit, .5), p99_us=pctl(t_hit, .99),
                                    after="depth-2 global query (fp32 path)"),
                maintenance_sweep=dict(us=t_sweep, low_utility=low, edges_hit=touched,
@@ -211,7 +211,7 @@ def tiled_pass(args, mars_amd, corpus, c, qnodes, N, D, K, pctl, lat_resident, h
 SERVE_MODES = {
     "auto": "q1 while one certified Q=1 query per arrival keeps the global server under half busy "
             "(measured Q=1 latency x global arrival rate < 0.5), link beyond",
-    "q1": "one global query per call (certified fp16 scan); each insert finds its own k-NN",
+    "q1": "one global query per call (certified candidate scan); each insert finds its own k-NN",
     "batch": "batched global calls; each insert finds its own k-NN",
     "link": "batched global calls that also find the k-NN of the nodes inserted since the last call "
             "(one corpus pass for both); inserts publish rows and episode edges only",
@@ -259,7 +259,7 @@ def serve_pass(args, mars_amd, corpus, lib, check, full, dg, ctx, qnodes, nq, ep
     b.ins_stats, b.ins_start_us = C.cast(ins, C.c_void_p).value, pv(istart)
     b.link_deferred, b.max_link, b.ins_linked_us, b.link_wait_us = int(mode == "link"), 1024, pv(ilinked), 5000.0
     t0 = time.time()
-    ctx.certified = True          # a global query answered alone uses the certified fp16 scan
+    ctx.certified = True          # a global query answered alone uses the certified candidate scan
     try:
         check(lib.mars_bench_serve(dg.handle, ctx.handle, ectx.handle, C.byref(b)), "mars_bench_serve")
     finally:
@@ -389,6 +389,9 @@ def main() -> int:
     ap.add_argument("--stream-insert-batch", type=int, default=10, help="nodes per insert call when streaming")
     ap.add_argument("--knn-block", type=int, default=0,
                     help="k-NN of the NSN graph within blocks of this many consecutive ids (0: exact, all pairs)")
+    ap.add_argument("--candidates", choices=("int8", "fp16"), default="int8",
+                    help="row copy the certified global query scans for candidates (the fp16 one is "
+                         "also timed alongside)")
     ap.add_argument("--no-maintenance", action="store_true",
                     help="skip the importance / novelty / edge-hit maintenance pass")
     ap.add_argument("--maintenance-only", action="store_true",
@@ -426,7 +429,9 @@ def main() -> int:
     g = mars_amd.MemoryGraph(N, D, None, None, c.embeddings, c.modalities, c.timestamps)
     dg = mars_amd.upload_to_device(g, capacity_nodes=N + M)
     mars_amd.upload_fp16_embeddings(dg)
-    log(f"upload + fp16 copy: {time.time() - t:.1f}s")
+    if args.candidates == "int8":
+        mars_amd.upload_int8_embeddings(dg)
+    log(f"upload + fp16 copy" + (" + int8 copy" if args.candidates == "int8" else "") + f": {time.time() - t:.1f}s")
     t = time.time()
     if args.knn_k > 0:
         def knn_progress(done, total):
@@ -516,6 +521,10 @@ def main() -> int:
     out = {}
     bytes_f32 = N * D * 4 + 4 * N
     bytes_f16 = N * D * 2 + 4 * N
+    # the int8 candidate scan: bytes, per-row scale and bound, timestamps
+    bytes_i8 = N * D + 8 * N + 4 * N
+    cand = args.candidates
+    bytes_cert = bytes_i8 if cand == "int8" else bytes_f16
 
     def timed(first, count, cfgs, n_cfg, events):
         ctx.timing = events
@@ -536,7 +545,7 @@ def main() -> int:
     (lat_gg, _, _), wall_gg = timed(W, S, C.pointer(g1), 1, False)
     ctx.use_cuda_graph = False
     log(f"global fp32 (graph replay): p50 {pctl(lat_gg, .5):.1f} us p99 {pctl(lat_gg, .99):.1f} us")
-    # ---- global, certified fp16 scan (results identical to the fp32 scan's)
+    # ---- global, certified candidate scan (results identical to the fp32 scan's)
     ctx.certified = True
     run(0, W, C.pointer(g1), 1)
     (lat_c, _, _), wall_c = timed(W, S, C.pointer(g1), 1, False)
@@ -559,9 +568,25 @@ def main() -> int:
     ctx.certified = False
     log("certified phases (us, mean): merge {:.1f}  rescore+certify {:.1f}  bfs {:.1f}  mark {:.1f}  "
         "exact {:.1f}  results {:.1f}".format(*cph))
-    log(f"global certified (fp16 scan, exact results): p50 {pctl(lat_c, .5):.1f} us p99 {pctl(lat_c, .99):.1f} us; "
-        f"{S / wall_c:.0f} q/s; scan kernel mean {kern_c.mean():.1f} us ({bytes_f16 / kern_c.mean() / 1e3:.0f} GB/s); "
+    log(f"global certified ({cand} scan, exact results): p50 {pctl(lat_c, .5):.1f} us p99 {pctl(lat_c, .99):.1f} us; "
+        f"{S / wall_c:.0f} q/s; scan kernel mean {kern_c.mean():.1f} us ({bytes_cert / kern_c.mean() / 1e3:.0f} GB/s); "
         f"seeds + BFS + results {rest_c.mean():.1f} us; certified {n_cert}/{n_samp}")
+    cert16 = None
+    if cand == "int8" and not args.profile_only:
+        # the same queries certified over the fp16 copy (the int8 copy set aside, then rebuilt)
+        mars_amd.free_int8_embeddings(dg)
+        ctx.certified = True
+        run(0, W, C.pointer(g1), 1)
+        (lat_c16, _, _), _ = timed(W, min(S, 4000), C.pointer(g1), 1, False)
+        (_, kern_c16, rest_c16), _ = timed(W, KT, C.pointer(g1), 1, True)
+        ctx.timing = False
+        ctx.certified = False
+        mars_amd.upload_int8_embeddings(dg)
+        cert16 = dict(p50_us=pctl(lat_c16, .5), p99_us=pctl(lat_c16, .99), scan_kernel_mean_us=float(kern_c16.mean()),
+                      seeds_bfs_results_mean_us=float(rest_c16.mean()),
+                      scan_gbs=bytes_f16 / float(kern_c16.mean()) / 1e3, queries=min(S, 4000))
+        log(f"global certified over the fp16 copy: p50 {cert16['p50_us']:.1f} us p99 {cert16['p99_us']:.1f} us; "
+            f"scan kernel mean {kern_c16.mean():.1f} us; seeds + BFS + results {rest_c16.mean():.1f} us")
     # finalize phase breakdown (seed merge, BFS, selection) from the GPU realtime counter
     ctx.timing = False
     ph = []
@@ -665,7 +690,7 @@ def main() -> int:
     if not args.profile_only and not args.no_maintenance:
         out["maintenance"] = maintenance_pass(mars_amd, dg, ctx, dq, W, S - W, D, gcfg, pctl)
 
-    achieved = bytes_f16 / float(kern_c.mean()) / 1e3       # GB/s of the certified path's fp16 scan
+    achieved = bytes_cert / float(kern_c.mean()) / 1e3      # GB/s of the certified path's candidate scan
     achieved32 = bytes_f32 / float(kern_g.mean()) / 1e3
     res = {
         "metric": METRIC,
@@ -680,11 +705,12 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic",
-        "config": {"workload": f"global Q=1 decay+top-K+depth-2 BFS over N={N:,} D={D}, K={K}: fp16 scan with "
-                               f"certified exact seeds and exact BFS scores (results bit-identical to the fp32 scan "
-                               f"path, which answers any query the certificate does not cover); the fp32-scan path, "
-                               f"episode-scoped and fp16 global reported alongside",
-                   "global_path": "MARS_CTX_CERTIFIED",
+        "config": {"workload": f"global Q=1 decay+top-K+depth-2 BFS over N={N:,} D={D}, K={K}: {cand} candidate "
+                               f"scan with certified exact seeds and exact BFS scores (results bit-identical to the "
+                               f"fp32 scan path, which answers any query the certificate does not cover); the "
+                               f"fp32-scan path, the fp16-candidate certified path, episode-scoped and fp16 global "
+                               f"reported alongside",
+                   "global_path": "MARS_CTX_CERTIFIED", "candidate_rows": cand,
                    "num_nodes": N, "dim": D, "top_k": K, "bfs_hops": 2, "decay_lambda": corpus.DECAY_LAMBDA,
                    "corpus_seed": args.seed, "query_seed": args.query_seed, "num_edges": int(len(c.col_indices)),
                    "nsn_graph": (f"intra-episode pairs + {args.knn_k}-NN" +
@@ -696,8 +722,10 @@ def main() -> int:
                                  seeds_bfs_results_mean_us=float(rest_c.mean()),
                                  scan_gbs=achieved, scan_frac=achieved / HBM_PEAK_GBS,
                                  certified=n_cert, certified_sample=n_samp,
+                                 candidate_rows=cand, scan_bytes_per_launch=bytes_cert,
                                  phases_us=dict(zip(("merge", "rescore_certify", "bfs", "mark", "exact", "results"),
                                                     [round(float(x), 2) for x in cph]))),
+        **({"global_certified_fp16": cert16} if cert16 else {}),
         "global_fp32": dict(p50_us=pctl(lat_g, .5), p99_us=pctl(lat_g, .99), qps=S / wall_g,
                             p99_us_with_events=pctl(lat_gk, .99),
                             graph_replay=dict(p50_us=pctl(lat_gg, .5), p99_us=pctl(lat_gg, .99)),
@@ -708,9 +736,12 @@ def main() -> int:
                                                     select=float(ph[:, 2].mean()))),
         **out,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": scan_traffic(N, D, "k_scan_fp16_1M.md"),
-                     "kernel": f"k_scan<__half,QF16<{D // 128}>,false> (16 candidates per workgroup)",
-                     "bytes_per_launch": bytes_f16},
+                     "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": scan_traffic(N, D, "k_scan_int8_1M.md" if cand == "int8" else "k_scan_fp16_1M.md"),
+                     "kernel": (f"k_scan8<{D // 256},false> (64 candidates per workgroup, keys = per-row upper bounds)"
+                                if cand == "int8" else f"k_scan<__half,QF16<{D // 128}>,false> (16 candidates per "
+                                                       f"workgroup)"),
+                     "bytes_per_launch": bytes_cert},
     }
     if not args.profile_only:
         # a plain streaming read of the same fp16 rows, no arithmetic: the scan's practical ceiling

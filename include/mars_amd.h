@@ -150,7 +150,8 @@ int mars_graph_create(const mars_graph_desc* desc, mars_graph** out);
 /* free_device */
 int mars_graph_destroy(mars_graph* g);
 /* The calls below that replace device arrays (mars_graph_set_episode_ids,
- * mars_graph_set_episode_csr, mars_graph_disable_fp16, mars_graph_set_csr) free the
+ * mars_graph_set_episode_csr, mars_graph_disable_fp16, mars_graph_disable_int8,
+ * mars_graph_set_csr) free the
  * arrays they replace: no query, on any context or thread, may run on the graph during
  * them. (Inserts and links do not free what queries read: queries keep running during
  * those.) */
@@ -163,6 +164,17 @@ int mars_graph_set_episode_csr(mars_graph* g, int32_t num_episodes,
 /* upload_fp16_embeddings / free_fp16_embeddings (RNE fp32->fp16, 64-bit indexing). */
 int mars_graph_enable_fp16(mars_graph* g);
 int mars_graph_disable_fp16(mars_graph* g);
+/* No counterpart in the reference: an int8 copy of the rows for the certified global
+ * query (MARS_CTX_CERTIFIED). Row r is kept as bytes v in [-127, 127] with one scale
+ * s_r = max|e_r| / 127 and a bound c_r on |int8 dot - fp32 dot| / |q| (its quantisation
+ * residual norm plus both scans' rounding), maintained through inserts and
+ * mars_graph_set_rows: d + 8 bytes per row (cap_n rows). embedding_dim must be 256, 512,
+ * 768, 1024 or 1536 (the certified query uses it up to 1024). */
+int mars_graph_enable_int8(mars_graph* g);
+int mars_graph_disable_int8(mars_graph* g);
+/* Copies rows [first, first + count) of the int8 copy to host memory: count * d bytes
+ * and/or count (scale, bound) float pairs (either pointer may be NULL). */
+int mars_graph_read_int8(const mars_graph* g, int32_t first, int32_t count, int8_t* bytes, float* meta);
 int mars_graph_get_view(const mars_graph* g, mars_graph_view* out);
 /* Replace the NSN CSR of a graph (host arrays, validated like mars_graph_create). */
 int mars_graph_set_csr(mars_graph* g, int32_t num_edges, const int32_t* row_offsets,
@@ -358,15 +370,22 @@ int mars_host_free(void* ptr);
 #define MARS_CTX_USE_FP16    0x1u   /* scan the fp16 copy when present (ctx.use_fp16)      */
 #define MARS_CTX_USE_GRAPH   0x2u   /* replay the query pipeline as a hipGraph             */
 #define MARS_CTX_TIMING      0x4u   /* fill per-stage gpu_ms_* with hipEvents              */
-/* Global queries scan the fp16 copy (half the bytes) and return exactly the fp32 path's
- * results: the scan keeps 32 candidates (64 for K > 16), which are rescored in the
- * fp32 scan's own arithmetic; when the K-th exact score exceeds the last candidate's
- * fp16 score by more than the fp16 error bound of any row (from the rows' rounding
- * residual norms, kept with the fp16 copy), those are the fp32 scan's seeds, and the
- * BFS then scores every visited node exactly. Otherwise the fp32 scan answers the
- * query (stats.seeds_certified = 0). Needs the fp16 copy; ignored with MARS_CTX_USE_FP16
- * (which returns fp16 scores), for episode scope, a same-episode boost, lambda < 0 and
- * embedding_dim not a multiple of 128. MARS_CTX_USE_GRAPH does not apply to it. */
+/* Global queries scan a reduced-precision copy and return exactly the fp32 path's
+ * results. With the int8 copy (mars_graph_enable_int8; a quarter of the fp32 bytes) the
+ * scan ranks rows by an upper bound of their fp32 score (int8 score + |q| c_r) and keeps
+ * 64 candidates; when the K-th exact score of the candidates exceeds the 64th candidate's
+ * bound, no other row can enter the top K. Otherwise, with the fp16 copy (half the
+ * bytes), it keeps 32 candidates (64 for K > 16, 16 for K <= 10) and the certificate
+ * asks the K-th exact score to exceed the last candidate's fp16 score by the fp16 error
+ * bound of any row (from the rows' rounding residual norms, kept with the fp16 copy).
+ * Candidates are rescored in the fp32 scan's own arithmetic, and the BFS then scores
+ * every visited node exactly. A query the certificate does not cover is answered by
+ * the fp32 scan (stats.seeds_certified = 0). Needs the int8 or the fp16 copy; ignored
+ * with MARS_CTX_USE_FP16 (which returns fp16 scores), for episode scope, a same-episode
+ * boost, lambda < 0 and embedding_dim not a multiple of 128 (above 1024: int8 copy
+ * unused, fp16 copy required up to 1024). MARS_CTX_USE_GRAPH does not apply to it.
+ * After a certified query, mars_ctx_last_scores is not filled (the debug hooks describe
+ * fp32 scans). */
 #define MARS_CTX_CERTIFIED   0x8u
 /* create_query_context(max_nodes, embedding_dim, max_k): max_k clamps to 64. A query
  * returns at most min(max_nodes, max_k * 500) results, the reference's compaction cap

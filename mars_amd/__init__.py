@@ -30,6 +30,7 @@ __all__ = [
     "Modality", "RetrievalScope", "RetrievalConfig", "RetrievalStats", "QueryResult", "MemoryGraph",
     "HostEpisodeCSR", "DeviceMemoryGraph", "QueryContext", "build_episode_csr", "upload_to_device",
     "upload_episode_ids", "upload_episode_csr", "upload_fp16_embeddings", "free_fp16_embeddings",
+    "upload_int8_embeddings", "free_int8_embeddings", "read_int8",
     "free_device", "create_query_context", "destroy_query_context", "query_memory_fast",
     "query_memory_fast_device", "init", "MarsError", "corpus", "DeviceBuffer", "query_batch", "query_global_batch",
     "BatchStats", "query_global_batch_knn", "link", "link_knn", "graph_knn", "set_csr",
@@ -240,6 +241,28 @@ def upload_fp16_embeddings(dg: DeviceMemoryGraph) -> None:
 
 def free_fp16_embeddings(dg: DeviceMemoryGraph) -> None:
     check(lib.mars_graph_disable_fp16(dg.handle), "free_fp16_embeddings")
+
+
+def upload_int8_embeddings(dg: DeviceMemoryGraph) -> None:
+    """The int8 copy of the rows that the certified global query scans (no reference
+    counterpart; mars_graph_enable_int8)."""
+    check(lib.mars_graph_enable_int8(dg.handle), "upload_int8_embeddings")
+
+
+def free_int8_embeddings(dg: DeviceMemoryGraph) -> None:
+    check(lib.mars_graph_disable_int8(dg.handle), "free_int8_embeddings")
+
+
+def read_int8(dg: DeviceMemoryGraph, first: int = 0, count: int | None = None):
+    """Rows [first, first + count) of the int8 copy: (bytes (count, d) int8, meta (count, 2)
+    float32 = per-row scale and error bound)."""
+    if count is None:
+        dg.refresh()
+        count = dg.num_nodes - first
+    b = np.zeros((count, dg.embedding_dim), np.int8)
+    m = np.zeros((count, 2), np.float32)
+    check(lib.mars_graph_read_int8(dg.handle, first, count, _ptr(b), _ptr(m)), "read_int8")
+    return b, m
 
 
 def free_device(dg: DeviceMemoryGraph) -> None:

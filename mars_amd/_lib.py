@@ -207,6 +207,9 @@ SIGNATURES = {
     "mars_graph_set_episode_ids": (C.c_int, [VP, VP, I32]),
     "mars_graph_set_episode_csr": (C.c_int, [VP, I32, VP, VP, I32]),
     "mars_graph_enable_fp16": (C.c_int, [VP]),
+    "mars_graph_enable_int8": (C.c_int, [VP]),
+    "mars_graph_disable_int8": (C.c_int, [VP]),
+    "mars_graph_read_int8": (C.c_int, [VP, I32, I32, VP, VP]),
     "mars_graph_disable_fp16": (C.c_int, [VP]),
     "mars_graph_get_view": (C.c_int, [VP, C.POINTER(GraphViewC)]),
     "mars_graph_download": (C.c_int, [VP, VP, VP, VP, VP]),

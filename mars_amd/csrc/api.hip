@@ -36,6 +36,13 @@ constexpr int32_t kMaxWg = 4096;     // upper bound of scan workgroups (partials
 // 510 us at 2048).
 constexpr int32_t kTargetWg = 512;
 constexpr int32_t kTargetWgF16 = 512;
+constexpr int32_t kTargetWgI8 = kScan8MaxLists;
+
+// The certified query scans the int8 copy when there is one (d <= 1024: the exact
+// rescoring's QF32 layouts), else the fp16 copy.
+bool cert_uses_int8(const Graph& g) {
+    return g.emb8 && g.meta8 && g.nrm8 && scan8_dim_supported(g.d) && g.d <= 1024;
+}
 
 int ensure_device(int* dev) {
     int d = 0;
@@ -102,7 +109,7 @@ namespace {
 int graph_free(Graph& g) {
     (void)use_device(g.device);
     if (g.ins_stream) (void)hipStreamSynchronize(g.ins_stream);
-    dfree(g.emb); dfree(g.emb16); dfree(g.nrm); dfree(g.mods); dfree(g.ts); dfree(g.ro); dfree(g.rcap); dfree(g.col);
+    dfree(g.emb); dfree(g.emb16); dfree(g.nrm); dfree(g.emb8); dfree(g.meta8); dfree(g.nrm8); dfree(g.mods); dfree(g.ts); dfree(g.ro); dfree(g.rcap); dfree(g.col);
     dfree(g.ep_ids); dfree(g.ep_off); dfree(g.ep_mem);
     dfree(g.imp); dfree(g.hits); dfree(g.imp_ids); dfree(g.sweep_cnt); dfree(g.pk_row); dfree(g.pk_col);
     graph_insert_free(g);
@@ -256,10 +263,11 @@ int wait_done(const Ctx& c, uint32_t seq, hipStream_t s) {
     return MARS_OK;
 }
 
-// Certified global query (MARS_CTX_CERTIFIED): fp16 scan keeping c candidates, exact
-// rescoring + certificate, then the unscored BFS, exact visit scores and the results
-// (the batched path's kernels with q = 1). *answered = false when the certificate or
-// the BFS table did not hold: the caller runs the fp32 scan.
+// Certified global query (MARS_CTX_CERTIFIED): a candidate scan of the int8 copy (64
+// candidates ranked by per-row upper bounds) or of the fp16 copy (c candidates ranked by
+// fp16 scores), exact rescoring + certificate, then the unscored BFS, exact visit scores
+// and the results (the batched path's kernels with q = 1). *answered = false when the
+// certificate or the BFS table did not hold: the caller runs the fp32 scan.
 int certified_query(const Graph& g, Ctx& c, const float* q, float t_q, const mars_retrieval_config* cfg, int32_t K,
                     int32_t hops, int32_t rcap, int32_t n_live, mars_query_result* out, int32_t cap, int32_t* n_out,
                     bool* answered, ResultHeader* hdr_out) {
@@ -267,21 +275,26 @@ int certified_query(const Graph& g, Ctx& c, const float* q, float t_q, const mar
     MARS_TRY(ensure_multi_scratch(c, 1, rcap));
     hipStream_t s = c.stream;
     const bool timing = (c.flags & MARS_CTX_TIMING) != 0;
-    const int32_t cands = K <= 10 ? 16 : (K <= 16 ? 32 : 64);   // fp16 candidates the certificate checks
+    const bool i8 = cert_uses_int8(g);
+    // candidates the certificate checks
+    const int32_t cands = i8 ? 64 : (K <= 10 ? 16 : (K <= 16 ? 32 : 64));
     int32_t rpw = 0, nwg = 0;
-    scan_grid(n_live, kTargetWgF16, &rpw, &nwg);
+    scan_grid(n_live, i8 ? kTargetWgI8 : kTargetWgF16, &rpw, &nwg);
     ScanArgs a{};
-    a.emb = g.emb16; a.fp16 = 1; a.n = n_live; a.d = g.d; a.q = q; a.ts = g.ts; a.mods = g.mods; a.ep_ids = g.ep_ids;
+    a.emb = i8 ? static_cast<const void*>(g.emb8) : static_cast<const void*>(g.emb16); a.fp16 = i8 ? 0 : 1;
+    a.meta8 = g.meta8; a.n = n_live; a.d = g.d; a.q = q; a.ts = g.ts; a.mods = g.mods; a.ep_ids = g.ep_ids;
     a.t_q = t_q; a.lambda = cfg->time_decay_lambda; a.mod_filter = cfg->modality_filter; a.query_ep = -1;
-    a.boost = 0.0f; a.k = cands; a.fin = c.fin; a.part = c.part; a.gthr = c.gthr; a.gcnt = c.gcnt;
-    a.rows_per_wg = rpw; a.num_wg = nwg;
+    a.boost = 0.0f; a.k = i8 ? kScan8List : cands; a.fin = c.fin; a.part = c.part; a.gthr = c.gthr;
+    a.gcnt = c.gcnt; a.rows_per_wg = rpw; a.num_wg = nwg;
     if (timing) MARS_HIP(hipEventRecord(c.ev[0], s));
-    MARS_TRY(launch_scan(a, s));
+    MARS_TRY(i8 ? launch_scan8(a, s) : launch_scan(a, s));
     if (timing) MARS_HIP(hipEventRecord(c.ev[1], s));
     CertArgs ca{};
     ca.part = c.part; ca.gcnt = c.gcnt; ca.gthr = c.gthr; ca.c = cands; ca.k = K; ca.q = q; ca.d = g.d;
+    ca.n_lists = i8 ? nwg : 0;
     ca.emb = g.emb; ca.ts = g.ts; ca.mods = g.mods; ca.t_q = t_q; ca.lambda = cfg->time_decay_lambda;
-    ca.mod_filter = cfg->modality_filter; ca.nrm = g.nrm; ca.seeds = c.mseed; ca.status = c.mstat;
+    ca.mod_filter = cfg->modality_filter; ca.nrm = g.nrm; ca.upper = i8 ? 1 : 0; ca.nrm8 = g.nrm8;
+    ca.seeds = c.mseed; ca.status = c.mstat;
     ca.margin = c.mmargin; ca.fin16 = c.fin; ca.stamps = c.stamps + 4;
     // one workgroup finishes the query when the interval argument applies
     const float dlt = cfg->bfs_score_decay;
@@ -371,8 +384,9 @@ int query_impl(const mars_graph* gh, mars_ctx* ch, const float* h_q, const float
     }
     const float lam = cfg->time_decay_lambda;
     const bool boost_on = g.ep_ids && cfg->query_episode_id >= 0 && cfg->episode_same_boost > 0.0f;
-    const bool cert = !scoped && !fp16 && (c.flags & MARS_CTX_CERTIFIED) && g.emb16 && g.nrm && g.d % 128 == 0 &&
-                      g.d <= 1024 && !boost_on && lam >= 0.0f && lam <= FLT_MAX && hops < 255;
+    const bool cert = !scoped && !fp16 && (c.flags & MARS_CTX_CERTIFIED) &&
+                      (cert_uses_int8(g) || (g.emb16 && g.nrm && g.d % 128 == 0 && g.d <= 1024)) &&
+                      !boost_on && lam >= 0.0f && lam <= FLT_MAX && hops < 255;
     if (cert) {
         bool answered = false;
         ResultHeader h{};
@@ -834,6 +848,47 @@ int mars_graph_disable_fp16(mars_graph* gh) {
     MARS_TRY(use_device(gh->g.device));
     dfree(gh->g.emb16);
     dfree(gh->g.nrm);
+    return MARS_OK;
+}
+
+int mars_graph_enable_int8(mars_graph* gh) {
+    MARS_CHECK(gh, MARS_ERR_INVALID, "null graph");
+    std::lock_guard<std::mutex> lock(gh->mu);
+    Graph& g = gh->g;
+    MARS_CHECK(scan8_dim_supported(g.d), MARS_ERR_UNSUPPORTED,
+               "int8 copy: embedding_dim %d is not 256, 512, 768, 1024 or 1536", g.d);
+    MARS_TRY(use_device(g.device));
+    if (!g.emb8) MARS_TRY(dmalloc(&g.emb8, size_t(g.cap_n) * size_t(g.d)));
+    if (!g.meta8) MARS_TRY(dmalloc(&g.meta8, size_t(g.cap_n) * 2));
+    if (!g.nrm8) MARS_TRY(dmalloc(&g.nrm8, 2));
+    MARS_HIP(hipMemset(g.nrm8, 0, 2 * sizeof(uint32_t)));
+    MARS_TRY(launch_convert_i8(g.emb, 0, g.n, g.d, g.emb8, g.meta8, g.nrm8, nullptr));
+    MARS_HIP(hipStreamSynchronize(nullptr));
+    return MARS_OK;
+}
+
+int mars_graph_disable_int8(mars_graph* gh) {
+    MARS_CHECK(gh, MARS_ERR_INVALID, "null graph");
+    std::lock_guard<std::mutex> lock(gh->mu);
+    MARS_TRY(use_device(gh->g.device));
+    dfree(gh->g.emb8);
+    dfree(gh->g.meta8);
+    dfree(gh->g.nrm8);
+    return MARS_OK;
+}
+
+int mars_graph_read_int8(const mars_graph* gh, int32_t first, int32_t count, int8_t* bytes, float* meta) {
+    MARS_CHECK(gh && (bytes || meta), MARS_ERR_INVALID, "null argument");
+    std::lock_guard<std::mutex> lock(gh->mu);
+    const Graph& g = gh->g;
+    MARS_CHECK(g.emb8 != nullptr, MARS_ERR_UNSUPPORTED, "no int8 copy");
+    MARS_CHECK(first >= 0 && count >= 0 && int64_t(first) + count <= g.n, MARS_ERR_INVALID,
+               "rows [%d, %lld) outside the %d published nodes", first, (long long)first + count, g.n);
+    MARS_TRY(use_device(g.device));
+    if (count == 0) return MARS_OK;
+    if (bytes) MARS_HIP(hipMemcpy(bytes, g.emb8 + size_t(first) * g.d, size_t(count) * g.d, hipMemcpyDeviceToHost));
+    if (meta) MARS_HIP(hipMemcpy(meta, g.meta8 + size_t(first) * 2, size_t(count) * 2 * sizeof(float),
+                                 hipMemcpyDeviceToHost));
     return MARS_OK;
 }
 

@@ -19,8 +19,10 @@ namespace {
 __device__ inline int lane_id() { return int(threadIdx.x & 63u); }
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef uint64_t u64x2 __attribute__((ext_vector_type(2)));
 
 // Insert key x into a register list of K keys kept ascending; x < list[K-1] is
 // checked by the caller.
@@ -278,14 +280,44 @@ struct QGeneric {
 // * (1 + boost); filtered rows are -FLT_MAX and not decayed). A is any struct with
 // the query terms t_q, lambda, mod_filter, query_ep, boost (ScanArgs, QueryTerms).
 template <class A>
+__device__ inline float decay_weight(float ts, const A& a) {
+    const float age = fmaxf(0.0f, a.t_q - ts);
+    return expf(-a.lambda * age);
+}
+template <class A>
 __device__ inline float fuse_score(float dot, float ts, int32_t mod, int32_t ep, const A& a) {
     if (a.mod_filter >= 0 && mod != a.mod_filter) return -FLT_MAX;
-    const float age = fmaxf(0.0f, a.t_q - ts);
-    float s = dot * expf(-a.lambda * age);
+    float s = dot * decay_weight(ts, a);
     if (a.boost > 0.0f && ep == a.query_ep && s > -FLT_MAX * 0.5f) s = s * (1.0f + a.boost);
     return s;
 }
 
+
+// End of a grid-stride scan: wave 0 merges the workgroup's four wave lists (s_lists,
+// written by every wave and synchronised by the caller) and appends its keys that can
+// still be among the global K best. Every key of the global top-K is <= the global K-th
+// key <= any workgroup's K-th key, so keys above the running minimum of those are
+// dropped here without changing the result. The bound is read first; only a workgroup
+// that lowers it issues the atomicMin (about ln(#workgroups) of them), and only one with
+// keys under it appends. A is any struct with part, gthr and gcnt (ScanArgs).
+template <class A>
+__device__ inline void wg_publish(const uint64_t (&s_lists)[4][64], int lane, int k, const A& a) {
+    uint64_t list = s_lists[0][lane];
+    list = wave_merge64(list, s_lists[1][lane], lane, k);
+    list = wave_merge64(list, wave_merge64(s_lists[2][lane], s_lists[3][lane], lane, k), lane, k);
+    const uint64_t kth = __shfl(list, k - 1);
+    uint64_t cur = kEmptyKey;
+    if (lane == 0) cur = ld_coherent(a.gthr);
+    cur = __shfl(cur, 0);
+    if (kth < cur && lane == 0) atomicMin(reinterpret_cast<unsigned long long*>(a.gthr), (unsigned long long)kth);
+    const uint64_t bound = cur < kth ? cur : kth;
+    const bool pass = lane < k && list != kEmptyKey && list <= bound;
+    const uint64_t m = __ballot(pass);
+    uint32_t base = 0;
+    if (lane == 0 && m) base = atomicAdd(a.gcnt, uint32_t(__popcll(m)));
+    base = __shfl(base, 0);
+    if (pass) a.part[base + uint32_t(__popcll(m & ((1ull << lane) - 1ull)))] = list;
+}
 
 // Completion word of a Q=1 query (host-mapped): every thread's result writes are made
 // visible system-wide, then one thread stores seq. Called by all threads of the
@@ -327,6 +359,60 @@ __device__ inline void raise_row_norms(double s32, double s16, double sd, uint32
         atomicMax(nrm + 0, up_bits(sqrt(s32)));
         atomicMax(nrm + 1, up_bits(sqrt(s16)));
         atomicMax(nrm + 2, up_bits(sqrt(sd)));
+    }
+}
+
+// ---- the int8 copy (certified global query) -------------------------------------------
+// Row r is stored as bytes v_i in [-127, 127] with one scale s_r = fl(max_i |e_i| / 127),
+// standing for e^_i = s_r v_i. The int8 scan's dot of a row (a per-lane fmaf chain of
+// d/16 steps, the 16-lane reduction, then * s_r) and the fp32 scan's (d/16 steps, the
+// reduction) both lie within gamma_n |q| |x| of their exact values (x = e^, e), with
+// n = d/16 + 6 rounded operations per term at most, so
+//     |dot8 - dot32| <= |q| (|e^ - e| + gamma_n (|e^| + |e|)) = |q| c_r.
+__device__ inline double i8_gamma(int32_t d) {
+    const double nu = (double(d) / 16.0 + 6.0) * 0x1p-24;
+    return nu / (1.0 - nu);
+}
+
+__device__ inline float wave_max_f(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+
+// One wave quantizes one row (d floats at e): the bytes go to out, (s_r, c_r) to meta;
+// lane 0 raises nrm8[0] to c_r and nrm8[1] to |e|. Sums of squares in fp64, c_r rounded
+// up to fp32. A NaN or infinite element makes c_r NaN or infinite, and with it nrm8[0]:
+// the certificate then never holds.
+__device__ inline void quantize_row_i8(const float* e, int32_t d, int8_t* out, float* meta, uint32_t* nrm8) {
+    const int lane = lane_id();
+    float m = 0.0f;
+    for (int i = lane; i < d; i += 64) m = fmaxf(m, fabsf(e[i]));
+    m = wave_max_f(m);
+    const float s = m / 127.0f;
+    double s32 = 0.0, s8 = 0.0, sd = 0.0;
+    for (int i = lane; i < d; i += 64) {
+        const float x = e[i];
+        float t = s > 0.0f ? rintf(x / s) : 0.0f;
+        t = fminf(fmaxf(t, -127.0f), 127.0f);
+        const int v = int(t);
+        out[i] = int8_t(v);
+        const double eh = double(s) * double(v);
+        s32 += double(x) * double(x);
+        s8 += eh * eh;
+        const double df = eh - double(x);
+        sd += df * df;
+    }
+    s32 = wave_sum_f64(s32);
+    s8 = wave_sum_f64(s8);
+    sd = wave_sum_f64(sd);
+    if (lane == 0) {
+        const double c = (sqrt(sd) + i8_gamma(d) * (sqrt(s8) + sqrt(s32))) * (1.0 + 1e-9);
+        const uint32_t cb = up_bits(c);
+        meta[0] = s;
+        meta[1] = __uint_as_float(cb);
+        atomicMax(nrm8 + 0, cb);
+        atomicMax(nrm8 + 1, up_bits(sqrt(s32)));
     }
 }
 

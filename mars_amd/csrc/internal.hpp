@@ -132,6 +132,13 @@ struct Graph {
     // (Euclidean norms; e16 with subnormals flushed in the difference), fp32 bit
     // patterns rounded up, raised by atomicMax as rows are converted
     uint32_t* nrm = nullptr;
+    // the int8 copy (certified global queries): row r as bytes v in [-127, 127] with one
+    // scale, meta8[2r] = s_r (e^ = s_r v), meta8[2r+1] = c_r, the row's bound on
+    // |int8 scan dot - fp32 scan dot| / |q|; nrm8[0] = max c_r, nrm8[1] = max |e| (fp32
+    // bit patterns rounded up, raised by atomicMax as rows are quantized)
+    int8_t* emb8 = nullptr;
+    float* meta8 = nullptr;
+    uint32_t* nrm8 = nullptr;
     int32_t* mods = nullptr;
     float* ts = nullptr;
     int64_t* ro = nullptr;    // cap_n: (row length << 32) | row start in col
@@ -322,6 +329,9 @@ struct ScanArgs {
     int32_t rows_per_wg;     // unused (grid-stride scan)
     int32_t num_wg;
     int64_t id_base;         // node id of row 0 (tiles of a host-resident corpus)
+    const float* meta8;      // int8 rows (launch_scan8): per-row scale and error bound; workgroup b
+                             // writes its k (= kScan8List) best keys, ascending and
+                             // kEmptyKey-padded, to part[k b .. k b + k - 1] (gthr, gcnt untouched)
 };
 // Kernel entry point + launch shape of one launch (for graph kernel nodes).
 struct KernelLaunch {
@@ -334,6 +344,15 @@ KernelLaunch scan_launch(const ScanArgs& a);
 KernelLaunch finalize_launch();
 KernelLaunch episode_launch(int32_t d);
 void scan_grid(int64_t n, int32_t max_wg, int32_t* rows_per_wg, int32_t* num_wg);
+// int8 candidate scan of the certified global query (scan8.hip): keys rank rows by an
+// upper bound of their fp32 scan score, fin gets the int8 estimate of every row.
+constexpr int32_t kScan8MaxLists = 512;    // int8 scan workgroups = lists k_cert_bfs merges
+constexpr int32_t kScan8List = 16;         // keys per workgroup list
+bool scan8_dim_supported(int32_t d);
+int launch_scan8(const ScanArgs& a, hipStream_t s);
+// Quantizes rows [r0, r1) of emb into emb8 / meta8 and raises nrm8.
+int launch_convert_i8(const float* emb, int64_t r0, int64_t r1, int32_t d, int8_t* emb8, float* meta8,
+                      uint32_t* nrm8, hipStream_t s);
 
 struct FinalizeArgs {
     const uint64_t* part;    // candidate keys from the scan
@@ -531,6 +550,9 @@ struct CertArgs {
     uint32_t* gcnt;
     uint64_t* gthr;
     int32_t c;               // candidates the scan kept (<= 64)
+    int32_t n_lists;         // > 0 (<= kScan8MaxLists): part holds n_lists ascending lists of
+                             // kScan8List keys (launch_scan8), else the keys the workgroups
+                             // appended (gcnt of them)
     int32_t k;               // seeds
     const float* q;          // d floats
     int32_t d;
@@ -541,7 +563,9 @@ struct CertArgs {
     float lambda;
     int32_t mod_filter;
     const uint32_t* nrm;     // Graph::nrm
-    const float* fin16;      // the fp16 scan's fused score of every row
+    int32_t upper;           // 1: int8 scan, candidate keys are upper bounds (nrm8 holds the bounds)
+    const uint32_t* nrm8;    // Graph::nrm8
+    const float* fin16;      // the candidate scan's fused score of every row
     int32_t finish;          // 1: also compute the results (hop decay in [0, 1], rcap <= 64)
     uint64_t* seeds;         // 64 entries: ascending exact keys, the first k are the seeds
     int32_t* status;

@@ -81,28 +81,7 @@ __global__ __launch_bounds__(256) void k_scan(ScanArgs a) {
     }
     s_lists[wave][lane] = list;
     __syncthreads();
-    if (wave == 0) {
-        list = wave_merge64(list, s_lists[1][lane], lane, k);
-        list = wave_merge64(list, wave_merge64(s_lists[2][lane], s_lists[3][lane], lane, k), lane, k);
-        // Every key of the global top-K is <= the global K-th key <= any
-        // workgroup's K-th key, so keys above the running minimum of those are
-        // dropped here without changing the result.
-        // The bound is read first; only a workgroup that lowers it issues the
-        // atomicMin (about ln(#workgroups) of them), and only one with keys under
-        // it appends.
-        const uint64_t kth = __shfl(list, k - 1);
-        uint64_t cur = kEmptyKey;
-        if (lane == 0) cur = ld_coherent(a.gthr);
-        cur = __shfl(cur, 0);
-        if (kth < cur && lane == 0) atomicMin(reinterpret_cast<unsigned long long*>(a.gthr), (unsigned long long)kth);
-        const uint64_t bound = cur < kth ? cur : kth;
-        const bool pass = lane < k && list != kEmptyKey && list <= bound;
-        const uint64_t m = __ballot(pass);
-        uint32_t base = 0;
-        if (lane == 0 && m) base = atomicAdd(a.gcnt, uint32_t(__popcll(m)));
-        base = __shfl(base, 0);
-        if (pass) a.part[base + uint32_t(__popcll(m & ((1ull << lane) - 1ull)))] = list;
-    }
+    if (wave == 0) wg_publish(s_lists, lane, k, a);
 }
 
 // ---- block-wide helpers (1024 threads) --------------------------------------------
@@ -568,14 +547,22 @@ __device__ inline uint64_t tree_merge(FinShared& sh, uint64_t list, int k, int a
     return list;
 }
 
-__device__ inline void stamp(const FinalizeArgs& a, int i) {
-    if (threadIdx.x == 0 && a.stamps) a.stamps[i] = __builtin_amdgcn_s_memrealtime();
+// Phase stamps (GPU realtime counter) are kept in LDS by thread 0 and stored once, at the
+// end: a store to the host-mapped stamp words takes a PCIe round trip to complete, and every
+// later load of the storing wave waits for it (stores and loads share one counter here).
+__device__ inline void flush_stamps(const uint64_t* st, int n, uint64_t* out) {
+    if (threadIdx.x == 0 && out)
+        for (int i = 0; i < n; ++i) out[i] = st[i];
 }
 
 __global__ __launch_bounds__(kFinThreads) void k_finalize(FinalizeArgs a) {
     __shared__ FinShared sh;
+    __shared__ uint64_t s_st[4];
     const int tid = int(threadIdx.x), lane = lane_id(), wave = tid >> 6;
     const int k = a.k;
+    auto stamp = [&](const FinalizeArgs&, int i) {
+        if (tid == 0) s_st[i] = __builtin_amdgcn_s_memrealtime();
+    };
     stamp(a, 0);
 
     // ---- A. merge the scan's candidate keys into the K seeds (8 loads in flight per lane)
@@ -664,6 +651,7 @@ __global__ __launch_bounds__(kFinThreads) void k_finalize(FinalizeArgs a) {
         *a.gthr = kEmptyKey;
     }
     stamp(a, 3);
+    flush_stamps(s_st, 4, a.stamps);
     signal_done(a.done, a.seq);
 }
 
@@ -792,13 +780,16 @@ __global__ __launch_bounds__(kFinThreads) void k_multi_select(MultiArgs m) {
 }
 
 // ---- certified Q=1 global query ---------------------------------------------------------
-// The fp16 scan (rows e16, query q in fp32) kept its c best keys per workgroup in part.
-// Here they are merged to the c best overall, rescored in the fp32 scan's arithmetic
-// (QF32 dot, 16-lane reduction, fuse_score), and the k best exact keys are certified:
-// a row outside the candidates has fp16 score <= the c-th candidate's, and
-//   |fp16 score - fp32 score| <= |e16 - e|max |q| + g (|e16|max + |e|max) |q| + rounding
-// (g = (d/16 + 4) u, both scans' per-lane chains and reductions; weights <= 1), so a
-// k-th exact score above (c-th fp16 score + that bound) makes the seeds the fp32 scan's.
+// The candidate scan kept its c best keys per workgroup in part. Here they are merged to
+// the c best overall, rescored in the fp32 scan's arithmetic (QF32 dot, 16-lane
+// reduction, fuse_score), and the k best exact keys are certified.
+//  * fp16 scan (rows e16, query q in fp32): a row outside the candidates has fp16 score
+//    <= the c-th candidate's, and
+//      |fp16 score - fp32 score| <= |e16 - e|max |q| + g (|e16|max + |e|max) |q| + rounding
+//    (g = (d/16 + 4) u, both scans' per-lane chains and reductions; weights <= 1), so a
+//    k-th exact score above (c-th fp16 score + that bound) makes the seeds the fp32 scan's.
+//  * int8 scan (upper = 1): the keys are per-row upper bounds of the fp32 scan's score,
+//    so a k-th exact score above the c-th candidate's key score is the certificate.
 template <typename QF>
 __global__ __launch_bounds__(kFinThreads) void k_cert_bfs(CertArgs a, MultiArgs m) {
     __shared__ FinShared sh;
@@ -806,27 +797,91 @@ __global__ __launch_bounds__(kFinThreads) void k_cert_bfs(CertArgs a, MultiArgs 
     __shared__ uint64_t s_exact[64];
     __shared__ double s_qn;
     __shared__ double s_eps;
+    __shared__ uint64_t s_cut;
+    __shared__ uint64_t s_lmin;
+    __shared__ uint64_t s_st[7];
     const int tid = int(threadIdx.x), lane = lane_id(), wave = tid >> 6;
     const int c = a.c;
     auto stamp_at = [&](int i) {
-        if (tid == 0 && a.stamps) a.stamps[i] = __builtin_amdgcn_s_memrealtime();
+        if (tid == 0) s_st[i] = __builtin_amdgcn_s_memrealtime();
     };
     stamp_at(0);
-    // A. the c best candidate keys (the finalize kernel's merge, 8 loads in flight per lane)
     uint64_t list = kEmptyKey, thr = kEmptyKey;
-    const int n_part = int(*a.gcnt);
-    const uint64_t gb = *a.gthr;                 // the scan's final bound: the c best are <= it
-    for (int base = wave * 64; base < n_part; base += kFinThreads * 8) {
+    if (a.n_lists > 0) {
+        // A. the c (<= 64) best keys of n_lists (<= kScan8MaxLists) ascending lists of
+        // kScan8List (16) keys, one per scan workgroup. The lists are read as 1 KB blocks of 8,
+        // one block per wave load instruction (lane l: keys 2l, 2l + 1 of the block, i.e. keys
+        // 2 (l & 7), +1 of list 8b + l / 8), wave w taking blocks w, w + 16, ...
+        // cut = the 8th smallest of the lists' 8th keys: 8 lists hold 8 keys <= cut each, so
+        // the 64 best keys are <= cut. The keys <= cut are compacted into LDS: the 8 lists
+        // with 8th key <= cut give at most 16 each and every other list at most 7, so at most
+        // 8 * 16 + 7 * 512 < kSortCap (also with cut = kEmptyKey, which needs fewer than 8
+        // lists of 8 keys). lmin = the smallest 16th key: a row that a full list dropped has a
+        // key above it (the certificate's bound takes it into account).
+        static_assert(kScan8List == 16 && kScan8MaxLists <= 8 * 4 * kFinWaves, "block layout");
+        const int nl = a.n_lists;
         uint64_t x[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int i = base + j * kFinThreads + lane;
-            x[j] = (i < n_part && a.part[i] <= gb) ? a.part[i] : kEmptyKey;
+        for (int i = 0; i < 4; ++i) {
+            const int b = wave + i * kFinWaves;
+            const bool on = 8 * b + (lane >> 3) < nl;
+            const u64x2 v = on ? reinterpret_cast<const u64x2*>(a.part + int64_t(b) * 128)[lane]
+                               : u64x2{kEmptyKey, kEmptyKey};
+            x[2 * i] = v.x;
+            x[2 * i + 1] = v.y;
+        }
+        // the lists' 8th keys through LDS, then one offer per thread; the 16th keys' minimum
+        uint64_t* k8 = sh.u.sort.key;
+        uint64_t l16 = kEmptyKey;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int li = 8 * (wave + i * kFinWaves) + (lane >> 3);
+            if ((lane & 7) == 3) k8[li] = li < nl ? x[2 * i + 1] : kEmptyKey;
+            if ((lane & 7) == 7 && x[2 * i + 1] < l16) l16 = x[2 * i + 1];
         }
 #pragma unroll
-        for (int j = 0; j < 8; ++j) wave_offer(list, thr, x[j], lane, c);
+        for (int o = 32; o > 0; o >>= 1) {
+            const uint64_t y = __shfl_xor(l16, o);
+            l16 = y < l16 ? y : l16;
+        }
+        if (tid == 0) s_lmin = kEmptyKey;
+        __syncthreads();
+        if (lane == 0) atomicMin(reinterpret_cast<unsigned long long*>(&s_lmin), (unsigned long long)l16);
+        uint64_t l8 = kEmptyKey, t8 = kEmptyKey;
+        wave_offer(l8, t8, tid < 8 * 4 * kFinWaves ? k8[tid] : kEmptyKey, lane, 8);
+        l8 = tree_merge(sh, l8, 8);
+        if (wave == 0 && lane == 7) s_cut = l8;
+        if (tid == 0) sh.s_misc[4] = 0;
+        __syncthreads();
+        const uint64_t cut = s_cut;
+        uint64_t* buf = sh.u.sort.key;
+        int cnt = 0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) cnt += (x[j] <= cut && x[j] != kEmptyKey) ? 1 : 0;
+        int at = cnt ? atomicAdd(&sh.s_misc[4], cnt) : 0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            if (x[j] <= cut && x[j] != kEmptyKey) buf[at++] = x[j];
+        __syncthreads();
+        const int m = sh.s_misc[4];
+        for (int i = tid; i - lane < m; i += kFinThreads) wave_offer(list, thr, i < m ? buf[i] : kEmptyKey, lane, c);
+        list = tree_merge(sh, list, c, m < kFinThreads ? (m + 63) / 64 : kFinWaves);
+    } else {
+        // A. the c best candidate keys (the finalize kernel's merge, 8 loads in flight per lane)
+        const int n_part = int(*a.gcnt);
+        const uint64_t gb = *a.gthr;             // the scan's final bound: the c best are <= it
+        for (int base = wave * 64; base < n_part; base += kFinThreads * 8) {
+            uint64_t x[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int i = base + j * kFinThreads + lane;
+                x[j] = (i < n_part && a.part[i] <= gb) ? a.part[i] : kEmptyKey;
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) wave_offer(list, thr, x[j], lane, c);
+        }
+        list = tree_merge(sh, list, c, n_part <= kFinThreads ? (n_part + 63) / 64 : kFinWaves);
     }
-    list = tree_merge(sh, list, c, n_part <= kFinThreads ? (n_part + 63) / 64 : kFinWaves);
     stamp_at(1);
     if (wave == 0) s_cand[lane] = list;
     if (wave == 1) {
@@ -855,30 +910,46 @@ __global__ __launch_bounds__(kFinThreads) void k_cert_bfs(CertArgs a, MultiArgs 
     // C. the k best exact keys and the certificate
     const uint64_t x = wave_sort64(s_exact[lane], lane);
     const uint64_t cl = s_cand[lane];
-    const int nc = __popcll(__ballot(cl != kEmptyKey));
     const uint64_t c_last = __shfl(cl, c - 1);
     const int kk = a.k < c ? a.k : c;
     const uint64_t kth = __shfl(x, kk - 1);
     bool ok = false;
     float margin = __builtin_inff();
-    const double e32 = double(__uint_as_float(a.nrm[0]));
-    const double e16 = double(__uint_as_float(a.nrm[1]));
-    const double de = double(__uint_as_float(a.nrm[2]));
-    const double qn = s_qn, u = 0x1p-24, nq = double(a.d) / 16.0 + 4.0;
-    const double gs = nq * u / (1.0 - nq * u);
-    const double eps = (de * qn + gs * (e16 + e32) * qn + u * (e16 + e32) * qn * (1.0 + gs)) * 1.01 +
-                       1e-30 * double(a.d);
+    const double qn = s_qn, u = 0x1p-24;
+    // eps: bound on |scan score - exact score| of any row (the interval BFS's half-width);
+    // slack: what the certificate adds to the c-th candidate's key score; en: row norm bound
+    double eps, slack, en;
+    if (a.upper) {
+        // int8 scan: keys are per-row upper bounds of the exact score (no slack), the
+        // estimates in fin lie within |q| max c_r plus the two products' rounding
+        const double cm = double(__uint_as_float(a.nrm8[0]));
+        en = double(__uint_as_float(a.nrm8[1]));
+        eps = (cm * qn + 4.0 * u * (en + cm) * qn) * 1.01 + 1e-30 * double(a.d);
+        slack = 0.0;
+    } else {
+        const double e32 = double(__uint_as_float(a.nrm[0]));
+        const double e16 = double(__uint_as_float(a.nrm[1]));
+        const double de = double(__uint_as_float(a.nrm[2]));
+        const double nq = double(a.d) / 16.0 + 4.0;
+        const double gs = nq * u / (1.0 - nq * u);
+        eps = (de * qn + gs * (e16 + e32) * qn + u * (e16 + e32) * qn * (1.0 + gs)) * 1.01 + 1e-30 * double(a.d);
+        slack = eps;
+        en = e16;
+    }
     if (lane == 0) s_eps = eps;
+    // every row outside the candidates has a key above bnd: the c-th candidate's (none when
+    // fewer than c), and with per-workgroup lists the smallest last key of a full list
+    const uint64_t bnd = (a.n_lists > 0 && s_lmin < c_last) ? s_lmin : c_last;
     if (a.k <= c) {
-        if (nc < c) {
+        if (bnd == kEmptyKey) {
             ok = true;                           // every live row was a candidate
         } else {
-            const float s16 = key_score(c_last), s32 = key_score(kth);
-            if (eps < 1e30) {
+            const float s16 = key_score(bnd), s32 = key_score(kth);
+            if (eps < 1e30) {                    // also false for NaN bounds
                 if (s16 == -FLT_MAX) {
-                    ok = e16 * qn * 2.0 < double(FLT_MAX);    // the c-th candidate is filtered
+                    ok = en * qn * 2.0 < double(FLT_MAX);     // the c-th candidate is filtered
                 } else {
-                    const double mg = double(s32) - (double(s16) + eps);
+                    const double mg = double(s32) - (double(s16) + slack);
                     ok = mg > 0.0;
                     margin = float(mg);
                 }
@@ -900,18 +971,22 @@ __global__ __launch_bounds__(kFinThreads) void k_cert_bfs(CertArgs a, MultiArgs 
     __syncthreads();
     // D. the certified seeds' BFS (visit set, hops, parents) in the same workgroup
     if (!a.finish) {
+        flush_stamps(s_st, 2, a.stamps);
         if (sh.s_misc[6]) multi_bfs_query(sh, m, 0);
         return;
     }
+    int n_st = 2;                                // stamps taken so far
     auto fail = [&](int32_t code) {
         if (tid == 0) {
             ResultHeader h;
             h.count = -1; h.visited = code; h.levels = 0; h.n_seeds = 0;
             m.res[0] = h;
         }
+        flush_stamps(s_st, n_st, a.stamps);
         signal_done(a.done, a.seq);
     };
     stamp_at(2);
+    n_st = 3;
     if (!sh.s_misc[6]) { fail(kMultiUncertified); return; }
     // E. the certified seeds' BFS in interval mode: every node's BFS score from the fp16
     // scan's fused scores (each within eps of the exact one) and a bound on its distance
@@ -951,6 +1026,7 @@ __global__ __launch_bounds__(kFinThreads) void k_cert_bfs(CertArgs a, MultiArgs 
     if (V < 0) { fail(kMultiOverflow); return; }
     if (sh.s_misc[7]) { fail(kMultiUncertified); return; }
     stamp_at(3);
+    n_st = 4;
     const int rc = min(m.rcap, V);
     best = tree_merge(sh, best, rk);
     if (wave == 0 && lane == rc - 1) sh.s_misc[5] = int(__float_as_uint(key_score(best)));
@@ -1033,6 +1109,7 @@ __global__ __launch_bounds__(kFinThreads) void k_cert_bfs(CertArgs a, MultiArgs 
         m.res[0] = h;
     }
     stamp_at(6);
+    flush_stamps(s_st, 7, a.stamps);
     signal_done(a.done, a.seq);
 }
 
@@ -1334,6 +1411,7 @@ int launch_finalize(const FinalizeArgs& a, hipStream_t s) {
 }
 
 int launch_cert_bfs(const CertArgs& a, const MultiArgs& m, hipStream_t s) {
+    MARS_CHECK(a.n_lists <= kScan8MaxLists, MARS_ERR_INVALID, "certificate merge: %d lists", a.n_lists);
     if (a.d % 64 == 0) {
         switch (a.d / 64) {
             case 4: MARS_LAUNCH(k_cert_bfs<QF32<4>>, dim3(1), dim3(kFinThreads), 0, s, a, m); return MARS_OK;

@@ -1,4 +1,5 @@
-"""The fp16 certificate's error bound, checked numerically on the CPU.
+"""The certificates' error bounds (fp16 and int8 candidate scans), checked numerically
+on the CPU.
 
 The certified global path and the batched global path nominate candidates with fp16
 rows and certify them with a bound eps on |fp16-path score - fp32-path score|. This
@@ -183,3 +184,165 @@ def test_certificate_names_the_fp32_top_k():
         else:
             uncertified += 1
     assert certified >= 25 and uncertified >= 1, (certified, uncertified)
+
+
+# ---- the int8 candidate scan (k_scan8) ----------------------------------------------------
+# Row r is kept as bytes v in [-127, 127] and a scale s = fl(max|e| / 127); the scan's dot
+# is lane s chaining fmaf over bytes 256c + 16s + j (j = 0..15), the xor tree, then * s.
+# Its key is the upper bound U = fl(w * X), X = fmaf(|q|_up, c_r, dot8) raised by
+# max(|X| 2^-20, 1e-35); the interval BFS uses fin = fl(w * dot8) with half-width
+# eps8 = (|q| max c + 4u |q| (max|e| + max c)) * 1.01 + 1e-30 d.
+
+def up32(x):
+    """fp32 values >= x (float64 array)."""
+    f = np.asarray(x, np.float64).astype(F32)
+    return np.where(f.astype(np.float64) < x, np.nextafter(f, F32(np.inf)), f).astype(F32)
+
+
+def quantize_i8(e):
+    """The int8 copy of rows e: bytes, scales, per-row bounds c (quantize_row_i8)."""
+    d = e.shape[1]
+    s = (np.abs(e).max(1).astype(F32) / F32(127)).astype(F32)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        t = np.where(s[:, None] > 0, np.rint((e / s[:, None]).astype(F32)), F32(0))
+    v = np.clip(t, -127, 127).astype(np.int8)
+    e64, eh = e.astype(np.float64), s[:, None].astype(np.float64) * v.astype(np.float64)
+    nu = (d / 16 + 6) * U
+    g = nu / (1 - nu)
+    c = (np.sqrt(((eh - e64) ** 2).sum(1)) + g * (np.sqrt((eh ** 2).sum(1)) + np.sqrt((e64 ** 2).sum(1)))) * (1 + 1e-9)
+    return v, s, up32(c)
+
+
+def dot_qf8(v, s, q):
+    n, d = v.shape
+    x = v.astype(F32)
+    acc = np.zeros((n, 16), F32)
+    for c in range(d // 256):
+        for j in range(16):
+            idx = 256 * c + 16 * np.arange(16) + j
+            acc = fma32(x[:, idx], q[idx][None, :], acc)
+    return (tree16(acc) * s).astype(F32)
+
+
+def upper_i8(dot8, c, q, w):
+    qn_up = up32(np.sqrt((q.astype(np.float64) ** 2).sum()) * (1 + 1e-12))
+    x = fma32(np.full_like(dot8, qn_up), c, dot8)
+    x = (x + np.maximum(np.abs(x) * F32(2.0 ** -20), F32(1e-35))).astype(F32)
+    return fused(x, w)
+
+
+def eps_i8(c, e, q):
+    d = e.shape[1]
+    qn = float(np.sqrt((q.astype(np.float64) ** 2).sum()))
+    en = float(up32(np.sqrt((e.astype(np.float64) ** 2).sum(1)).max()))
+    cm = float(c.max())
+    return (cm * qn + 4 * U * (en + cm) * qn) * 1.01 + 1e-30 * d
+
+
+def make_cases_i8(rng, n=600, d=768):
+    e = rng.standard_normal((n, d)).astype(F32)
+    e /= np.linalg.norm(e, axis=1, keepdims=True)
+    cases = [("unit rows", e.copy())]
+    spike = e.copy()
+    spike[::2, 5] = F32(0.9)                                     # one large element: coarse scale
+    cases.append(("spiked rows", (spike / np.linalg.norm(spike, axis=1, keepdims=True)).astype(F32)))
+    mid = e.copy()
+    s = (np.abs(mid).max(1) / F32(127)).astype(F32)
+    k = np.rint(mid / s[:, None])
+    half = ((k[:, 1::2] + np.sign(k[:, 1::2]) * 0.5) * s[:, None]).astype(F32)     # int8 midpoints
+    mid[:, 1::2] = np.clip(half, -np.abs(mid).max(1, keepdims=True), np.abs(mid).max(1, keepdims=True))
+    cases.append(("rounding midpoints", mid))
+    cases.append(("large norms", (e * F32(900.0)).astype(F32)))
+    tiny = (e * F32(1e-30)).astype(F32)
+    cases.append(("tiny rows", tiny))
+    z = e.copy()
+    z[::7] = 0.0
+    cases.append(("zero rows", z))
+    return cases
+
+
+def test_int8_upper_bound_covers_every_row():
+    rng = np.random.default_rng(17)
+    for name, e in make_cases_i8(rng):
+        d = e.shape[1]
+        for qi, q in enumerate((e[3] + F32(0.01) * rng.standard_normal(d).astype(F32),
+                                rng.standard_normal(d).astype(F32) * np.where(np.arange(d) < d // 2, F32(1e-4), F32(1)))):
+            q = q.astype(F32)
+            v, s, c = quantize_i8(e)
+            w = np.exp(-0.1 * rng.uniform(0, 30, size=e.shape[0])).astype(F32)
+            s32 = fused(dot_qf32(e, q), w).astype(np.float64)
+            d8 = dot_qf8(v, s, q)
+            s8 = fused(d8, w).astype(np.float64)
+            up = upper_i8(d8, c, q, w).astype(np.float64)
+            assert (up >= s32).all(), (name, qi, float((s32 - up).max()))
+            eps = eps_i8(c, e, q)
+            assert np.abs(s8 - s32).max() <= eps, (name, qi, np.abs(s8 - s32).max(), eps)
+            # the bounds are not vacuous: within a small factor of the errors seen
+            gap = np.abs(s8 - s32).max()
+            if name != "tiny rows":                          # there the 1e-30 d floor dominates
+                assert eps <= 60 * gap, (name, qi, eps, gap)
+
+
+def test_int8_quantization_error_is_what_c_states():
+    """c_r is the row's residual norm plus rounding terms of relative size ~(d/16) u,
+    and the byte codes round to nearest (ties to even) within [-127, 127]."""
+    rng = np.random.default_rng(19)
+    e = rng.standard_normal((200, 512)).astype(F32)
+    v, s, c = quantize_i8(e)
+    resid = np.sqrt(((s[:, None].astype(np.float64) * v - e.astype(np.float64)) ** 2).sum(1))
+    assert (c >= resid).all() and (c <= resid * 1.01 + 1e-4).all()
+    assert np.abs(v).max() == 127 and (np.abs(v) == 127).sum(1).min() >= 1      # every row uses its range
+    assert (np.abs(e / s[:, None] - v) <= 0.5 + 1e-6).all()
+    assert np.array_equal(np.rint(np.array([0.5, 1.5, 2.5, -0.5], F32)), np.array([0, 2, 2, 0], F32))
+
+
+def workgroup_candidates(up, n_wg=8, block=64, kw=16, cands=64):
+    """k_scan8 + k_cert_bfs candidate selection: rows dealt to n_wg workgroups in blocks of
+    64 consecutive ids, each keeps its kw best keys; the cands best of their union, and the
+    bound key above which every other row lies (the cands-th candidate's, or the smallest
+    kw-th key of a full list)."""
+    order = keys(up)
+    wg = (np.arange(len(up)) // block) % n_wg
+    kept, last = [], []
+    for b in range(n_wg):
+        mine = order[wg[order] == b]
+        kept.extend(mine[:kw])
+        if len(mine) > kw:
+            last.append(mine[kw - 1])
+    kept = np.array(kept)
+    cand = kept[keys(up[kept])][:cands]
+    # key order: a smaller (score desc, id asc) rank is a smaller key
+    rank = np.empty(len(up), np.int64)
+    rank[order] = np.arange(len(up))
+    bound = [cand[-1]] if len(cand) == cands else []
+    bound += last
+    return cand, (min(bound, key=lambda r: rank[r]) if bound else None)
+
+
+def test_int8_certificate_names_the_fp32_top_k():
+    rng = np.random.default_rng(23)
+    n, d, k, cands = 3000, 512, 10, 64
+    certified = uncertified = 0
+    for trial in range(30):
+        e = rng.standard_normal((n, d)).astype(F32)
+        e /= np.linalg.norm(e, axis=1, keepdims=True)
+        if trial % 4 == 0:                                   # planted near-ties at the cut
+            e[100:180] = e[7] + F32(1e-5) * rng.standard_normal((80, d)).astype(F32)
+        if trial % 4 == 1:                                   # 40 near-copies in one workgroup
+            e[576:616] = e[7] + F32(0.05) * rng.standard_normal((40, d)).astype(F32)
+        q = (e[7] + F32(0.2) * rng.standard_normal(d).astype(F32)).astype(F32)
+        v, s, c = quantize_i8(e)
+        w = np.exp(-0.1 * rng.uniform(0, 20, size=n)).astype(F32)
+        if trial % 4 == 0:
+            w[100:180] = w[7] = F32(1.0)
+        s32 = fused(dot_qf32(e, q), w)
+        up = upper_i8(dot_qf8(v, s, q), c, q, w)
+        cand, bnd = workgroup_candidates(up)
+        exact = cand[keys(s32[cand])]
+        ok = bnd is None or float(s32[exact[k - 1]]) > float(up[bnd])
+        if ok:
+            certified += 1
+            np.testing.assert_array_equal(exact[:k], keys(s32)[:k])
+        else:
+            uncertified += 1
+    assert certified >= 20 and uncertified >= 1, (certified, uncertified)

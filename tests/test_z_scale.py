@@ -12,7 +12,8 @@ Graphs:
 
 Bars: those of tests/parity.py (fp32 scores within 1e-5 of max(|s|, w * sum|e q|), BFS
 scales carried along the BFS, seeds equal up to near-ties, BFS visit order and hops
-exact); the certified path (fp16 scan, exact fp32 results) bit-identical to the fp32 path;
+exact); the certified path (fp16 or int8 candidate scan, exact fp32 results)
+bit-identical to the fp32 path;
 batched fp16 MFMA scoring within 2e-3 of the fp32 oracle's scale. The reference's harness
 reports recall against a CPU top-K at scale (latency_bench.cu:399-409); these tests
 assert it.
@@ -33,6 +34,7 @@ import oracle
 from mars_amd import RetrievalConfig, corpus
 
 from parity import LAM, T_Q, check_batch_topk, check_episode, check_global, check_results_exact, episode_cfg
+from test_certificate import quantize_i8
 
 pytestmark = pytest.mark.gpu
 D = 768
@@ -45,7 +47,7 @@ class ScaleGraph:
     """A resident graph of the benchmark corpus (first n rows of an n + extra corpus), its
     episode CSR, an fp16 copy, one query context, and the oracle's view of the same arrays."""
 
-    def __init__(self, n, knn_k, extra=0, seed=2026):
+    def __init__(self, n, knn_k, extra=0, seed=2026, int8=False):
         self.full = corpus.make_corpus(n + extra, D, seed=seed, threads=THREADS)
         f = self.full
         self.n = n
@@ -54,6 +56,8 @@ class ScaleGraph:
         self.dg = mars_amd.upload_to_device(g, capacity_nodes=n + extra,
                                             capacity_edges=(int(n) * 10 + 1_000_000) if extra else 0)
         mars_amd.upload_fp16_embeddings(self.dg)
+        if int8:
+            mars_amd.upload_int8_embeddings(self.dg)
         nb = mars_amd.graph_knn(self.dg, knn_k) if knn_k else np.empty((n, 0), np.int32)
         corpus.nsn_graph(self.c, nb, threads=THREADS)
         mars_amd.set_csr(self.dg, self.c.row_offsets, self.c.col_indices)
@@ -161,18 +165,35 @@ class TestScale1M:
             buf.free()
         check_batch_topk(sg.og, qs, np.full(64, T_Q, np.float32), cfg, ids, sc, sg.n, check_rows=range(0, 64, 8))
 
+    def test_int8_certified_bit_identical_200(self, sg):
+        """The int8 candidate scan: its copy equals the numpy quantization (a sample of
+        rows), and 200 certified answers equal the fp32 path's."""
+        mars_amd.upload_int8_embeddings(sg.dg)
+        try:
+            for first in (0, 517_000, sg.n - 3000):
+                b, m = mars_amd.read_int8(sg.dg, first, 3000)
+                v, s, c = quantize_i8(sg.c.embeddings[first:first + 3000])
+                np.testing.assert_array_equal(b, v)
+                np.testing.assert_array_equal(m[:, 0], s)
+                np.testing.assert_array_equal(m[:, 1], c)
+            nodes = corpus.pick_queries(sg.c.modalities, 200, seed=2006)
+            assert certified_equals_fp32(sg, nodes) >= 195
+        finally:
+            mars_amd.free_int8_embeddings(sg.dg)
+
 
 # ------------------------------------------------------------------------------ N = 13M streaming
 @pytest.mark.timeout(900)
 class TestScale13MStreaming:
-    """N = 13,000,000 fp32 + fp16 rows; one 10-node episode inserted with 8-NN edges on the
-    graph's side stream while another context keeps querying."""
+    """N = 13,000,000 fp32 + fp16 + int8 rows; one 10-node episode inserted with 8-NN edges
+    on the graph's side stream while another context keeps querying (certified queries
+    scan the int8 copy, which the insert extends)."""
 
     N0, M = 13_000_000, 10
 
     @pytest.fixture(scope="class")
     def sg(self):
-        s = ScaleGraph(self.N0, knn_k=0, extra=self.M)
+        s = ScaleGraph(self.N0, knn_k=0, extra=self.M, int8=True)
         yield s
         s.close()
 
@@ -248,7 +269,12 @@ class TestScale13MStreaming:
         for node in (new_img, int(qn[0])):
             check_global(sg, f.embeddings[node], GCFG)
         check_episode(sg, f.embeddings[new_img], int(f.episode_ids[new_img]), 10)
-        # certified == fp32 on 20 queries of the grown graph, the new nodes among them
+        # the inserted rows' int8 copy, then certified == fp32 on 20 queries of the grown
+        # graph, the new nodes among them
+        b, mt = mars_amd.read_int8(sg.dg, n0, m)
+        v, sc, c = quantize_i8(f.embeddings[n0:n0 + m])
+        np.testing.assert_array_equal(b, v)
+        np.testing.assert_array_equal(mt, np.stack([sc, c], 1))
         nodes = np.concatenate([np.arange(n0, n0 + m), corpus.pick_queries(f.modalities, 10, seed=3002)])
         assert certified_equals_fp32(sg, nodes) >= 18
 
