@@ -205,11 +205,12 @@ int mars_graph_knn_range(mars_graph* g, int32_t k, int32_t first, int32_t count,
  * row scans on this device. MARS_ERR_UNSUPPORTED when those rows are absent. */
 int mars_graph_read_ceiling(const mars_graph* g, int32_t fp16, int32_t reps, double* gbps);
 /* Measurement aid, no counterpart in the reference: the same measurement for an access
- * pattern over the fp16 rows. pattern 0: the plain stream of mars_graph_read_ceiling;
- * 1: the batched scan's fragment loads, 16 rows x 64 bytes per load instruction (a row's
- * 64-byte k-chunks back to back, 16-row tiles grid-strided); 2: pattern 1 with
- * non-temporal loads. Counts whole 16-row tiles. MARS_ERR_INVALID for another pattern,
- * MARS_ERR_UNSUPPORTED without fp16 rows or when embedding_dim is not a multiple of 32. */
+ * pattern. pattern 0: the plain stream of mars_graph_read_ceiling over the fp16 rows;
+ * 1: the batched scan's fragment loads over the fp16 rows, 16 rows x 64 bytes per load
+ * instruction (a row's 64-byte k-chunks back to back, 16-row tiles grid-strided; whole
+ * 16-row tiles counted); 2: pattern 1 with non-temporal loads; 3: the plain stream over
+ * the int8 copy. MARS_ERR_INVALID for another pattern, MARS_ERR_UNSUPPORTED without the
+ * rows the pattern reads or (1, 2) when embedding_dim is not a multiple of 32. */
 int mars_graph_read_pattern(const mars_graph* g, int32_t pattern, int32_t reps, double* gbps);
 /* Copy device arrays back to host (any pointer may be NULL to skip): the NSN graph as
  * a packed CSR (row_offsets: num_nodes + 1, col_indices: num_edges) and the episode CSR. */

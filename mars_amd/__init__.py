@@ -558,13 +558,14 @@ def read_ceiling(dg: DeviceMemoryGraph, fp16: bool = True, reps: int = 20) -> fl
     return float(out.value)
 
 
-READ_STREAM, READ_FRAGMENTS, READ_FRAGMENTS_NT = 0, 1, 2
+READ_STREAM, READ_FRAGMENTS, READ_FRAGMENTS_NT, READ_STREAM_INT8 = 0, 1, 2, 3
 
 
 def read_pattern(dg: DeviceMemoryGraph, pattern: int = READ_FRAGMENTS, reps: int = 20) -> float:
-    """GB/s of a read of the fp16 rows in an access pattern, with no arithmetic:
-    READ_STREAM (the plain stream of read_ceiling), READ_FRAGMENTS (the batched scan's
-    16 rows x 64 B per load instruction) or READ_FRAGMENTS_NT (the same, non-temporal)."""
+    """GB/s of a read of the rows in an access pattern, with no arithmetic: READ_STREAM
+    (the plain stream of read_ceiling over the fp16 rows), READ_FRAGMENTS (the batched
+    scan's 16 rows x 64 B per load instruction), READ_FRAGMENTS_NT (the same,
+    non-temporal) or READ_STREAM_INT8 (the plain stream over the int8 copy)."""
     out = C.c_double()
     check(lib.mars_graph_read_pattern(dg.handle, int(pattern), int(reps), C.byref(out)), "mars_graph_read_pattern")
     return float(out.value)

@@ -1707,9 +1707,18 @@ int mars_graph_read_ceiling(const mars_graph* gh, int32_t fp16, int32_t reps, do
 
 int mars_graph_read_pattern(const mars_graph* gh, int32_t pattern, int32_t reps, double* gbps) {
     MARS_CHECK(gh && gbps && reps > 0, MARS_ERR_INVALID, "bad arguments");
-    MARS_CHECK(pattern >= 0 && pattern <= 2, MARS_ERR_INVALID, "read pattern %d not in [0, 2]", pattern);
+    MARS_CHECK(pattern >= 0 && pattern <= 3, MARS_ERR_INVALID, "read pattern %d not in [0, 3]", pattern);
     if (pattern == 0) return mars_graph_read_ceiling(gh, 1, reps, gbps);
     const Graph& g = gh->g;
+    if (pattern == 3) {
+        MARS_CHECK(g.emb8 != nullptr, MARS_ERR_UNSUPPORTED, "no int8 rows");
+        const int64_t bytes = int64_t(__atomic_load_n(&g.n, __ATOMIC_ACQUIRE)) * g.d / 16 * 16;
+        MARS_CHECK(bytes > 0, MARS_ERR_INVALID, "empty graph");
+        MARS_TRY(use_device(g.device));
+        return time_read(bytes, reps, "read pattern", [&](int32_t wg, uint32_t* out, hipStream_t s) {
+            return launch_read_rows(g.emb8, bytes, wg, 0x9E3779B9u, out, s);
+        }, gbps);
+    }
     MARS_CHECK(g.emb16 != nullptr, MARS_ERR_UNSUPPORTED, "no fp16 rows");
     MARS_CHECK(g.d % 32 == 0, MARS_ERR_UNSUPPORTED, "fragment pattern: embedding_dim %d not a multiple of 32", g.d);
     const int32_t n = __atomic_load_n(&g.n, __ATOMIC_ACQUIRE);

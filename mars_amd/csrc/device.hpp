@@ -163,6 +163,20 @@ __device__ inline void wave_offer(uint64_t& list, uint64_t& thr, uint64_t key, i
     thr = __shfl(list, k - 1);
 }
 
+// fp64 sum over the 16 lanes of a DPP row; every lane of the row gets the total.
+__device__ inline double row16_sum_f64(double v) {
+    auto x = [](double a, auto tag) {
+        constexpr int J = decltype(tag)::value;
+        const uint64_t b = uint64_t(__double_as_longlong(a));
+        return __longlong_as_double((long long)xor_lane64<J>(b));
+    };
+    v += x(v, std::integral_constant<int, 8>{});
+    v += x(v, std::integral_constant<int, 4>{});
+    v += x(v, std::integral_constant<int, 2>{});
+    v += x(v, std::integral_constant<int, 1>{});
+    return v;
+}
+
 // Sum over the 16 lanes of a DPP row; every lane of the row gets the total.
 __device__ inline float row16_sum(float v) {
     v += xor_lanef<8>(v);
@@ -212,6 +226,15 @@ struct QF32 {
         fetch(row, sub, x);
         __builtin_amdgcn_sched_barrier(0);
         return dot_fetched(x);
+    }
+    // |q|^2 over the lane's elements, fp64
+    __device__ double norm2() const {
+        double s = 0.0;
+#pragma unroll
+        for (int c = 0; c < NCH; ++c)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) s += double(v[c][j]) * double(v[c][j]);
+        return s;
     }
 };
 

@@ -812,13 +812,13 @@ __global__ __launch_bounds__(kFinThreads) void k_cert_bfs(CertArgs a, MultiArgs 
         // kScan8List (16) keys, one per scan workgroup. The lists are read as 1 KB blocks of 8,
         // one block per wave load instruction (lane l: keys 2l, 2l + 1 of the block, i.e. keys
         // 2 (l & 7), +1 of list 8b + l / 8), wave w taking blocks w, w + 16, ...
-        // cut = the 8th smallest of the lists' 8th keys: 8 lists hold 8 keys <= cut each, so
-        // the 64 best keys are <= cut. The keys <= cut are compacted into LDS: the 8 lists
-        // with 8th key <= cut give at most 16 each and every other list at most 7, so at most
-        // 8 * 16 + 7 * 512 < kSortCap (also with cut = kEmptyKey, which needs fewer than 8
-        // lists of 8 keys). lmin = the smallest 16th key: a row that a full list dropped has a
-        // key above it (the certificate's bound takes it into account).
+        // cut = the c-th smallest of the lists' first keys: c lists hold a key <= cut, so the c
+        // best keys are <= cut, and only those c lists hold keys <= cut: at most c * 16 keys
+        // (with cut = kEmptyKey, fewer than c lists hold any), compacted into LDS, one per
+        // thread for the final selection. lmin = the smallest 16th key: a row that a full list
+        // dropped has a key above it (the certificate's bound takes it into account).
         static_assert(kScan8List == 16 && kScan8MaxLists <= 8 * 4 * kFinWaves, "block layout");
+        static_assert(kScan8MaxLists + 64 * kScan8List <= kSortCap && 64 * kScan8List <= kFinThreads, "buffers");
         const int nl = a.n_lists;
         uint64_t x[8];
 #pragma unroll
@@ -830,13 +830,13 @@ __global__ __launch_bounds__(kFinThreads) void k_cert_bfs(CertArgs a, MultiArgs 
             x[2 * i] = v.x;
             x[2 * i + 1] = v.y;
         }
-        // the lists' 8th keys through LDS, then one offer per thread; the 16th keys' minimum
-        uint64_t* k8 = sh.u.sort.key;
+        uint64_t* k1 = sh.u.sort.key;                    // the lists' first keys
+        uint64_t* buf = sh.u.sort.key + kScan8MaxLists;  // the keys <= cut
         uint64_t l16 = kEmptyKey;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int li = 8 * (wave + i * kFinWaves) + (lane >> 3);
-            if ((lane & 7) == 3) k8[li] = li < nl ? x[2 * i + 1] : kEmptyKey;
+            if ((lane & 7) == 0) k1[li] = li < nl ? x[2 * i] : kEmptyKey;
             if ((lane & 7) == 7 && x[2 * i + 1] < l16) l16 = x[2 * i + 1];
         }
 #pragma unroll
@@ -844,17 +844,15 @@ __global__ __launch_bounds__(kFinThreads) void k_cert_bfs(CertArgs a, MultiArgs 
             const uint64_t y = __shfl_xor(l16, o);
             l16 = y < l16 ? y : l16;
         }
-        if (tid == 0) s_lmin = kEmptyKey;
+        if (tid == 0) { s_lmin = kEmptyKey; sh.s_misc[4] = 0; }
         __syncthreads();
         if (lane == 0) atomicMin(reinterpret_cast<unsigned long long*>(&s_lmin), (unsigned long long)l16);
-        uint64_t l8 = kEmptyKey, t8 = kEmptyKey;
-        wave_offer(l8, t8, tid < 8 * 4 * kFinWaves ? k8[tid] : kEmptyKey, lane, 8);
-        l8 = tree_merge(sh, l8, 8);
-        if (wave == 0 && lane == 7) s_cut = l8;
-        if (tid == 0) sh.s_misc[4] = 0;
+        uint64_t l1 = kEmptyKey, t1 = kEmptyKey;
+        wave_offer(l1, t1, tid < nl ? k1[tid] : kEmptyKey, lane, c);
+        l1 = tree_merge(sh, l1, c, (nl + 63) / 64);
+        if (wave == 0 && lane == c - 1) s_cut = l1;
         __syncthreads();
         const uint64_t cut = s_cut;
-        uint64_t* buf = sh.u.sort.key;
         int cnt = 0;
 #pragma unroll
         for (int j = 0; j < 8; ++j) cnt += (x[j] <= cut && x[j] != kEmptyKey) ? 1 : 0;
@@ -863,9 +861,9 @@ __global__ __launch_bounds__(kFinThreads) void k_cert_bfs(CertArgs a, MultiArgs 
         for (int j = 0; j < 8; ++j)
             if (x[j] <= cut && x[j] != kEmptyKey) buf[at++] = x[j];
         __syncthreads();
-        const int m = sh.s_misc[4];
-        for (int i = tid; i - lane < m; i += kFinThreads) wave_offer(list, thr, i < m ? buf[i] : kEmptyKey, lane, c);
-        list = tree_merge(sh, list, c, m < kFinThreads ? (m + 63) / 64 : kFinWaves);
+        const int m = sh.s_misc[4];                      // <= 64 * 16 = kFinThreads
+        wave_offer(list, thr, tid < m ? buf[tid] : kEmptyKey, lane, c);
+        list = tree_merge(sh, list, c, (m + 63) / 64);
     } else {
         // A. the c best candidate keys (the finalize kernel's merge, 8 loads in flight per lane)
         const int n_part = int(*a.gcnt);
@@ -883,21 +881,21 @@ __global__ __launch_bounds__(kFinThreads) void k_cert_bfs(CertArgs a, MultiArgs 
         list = tree_merge(sh, list, c, n_part <= kFinThreads ? (n_part + 63) / 64 : kFinWaves);
     }
     stamp_at(1);
+    // the query in the rescoring layout (every 16-lane group holds all of it); group 0 also
+    // takes |q| (fp64) from its registers
+    const int g = tid >> 4, sub = tid & 15;
+    QF qf;
+    qf.load(a.q, sub);
     if (wave == 0) s_cand[lane] = list;
-    if (wave == 1) {
-        double sq = 0.0;
-        for (int i = lane; i < a.d; i += 64) sq += double(a.q[i]) * double(a.q[i]);
-        sq = wave_sum_f64(sq);
-        if (lane == 0) s_qn = sqrt(sq);
+    if (g == 0) {
+        const double sq = row16_sum_f64(qf.norm2());
+        if (sub == 0) s_qn = sqrt(sq);
     }
     __syncthreads();
     // B. exact rescoring: 16-lane group g takes candidate g
-    const int g = tid >> 4, sub = tid & 15;
     const uint64_t ck = s_cand[g];
     uint64_t key = kEmptyKey;
     if (ck != kEmptyKey) {                       // uniform over the group
-        QF qf;
-        qf.load(a.q, sub);
         const int32_t id = key_id(ck);
         const float dot = qf.dot(a.emb + int64_t(id) * a.d, sub);
         const QueryTerms t{a.t_q, a.lambda, a.mod_filter, -1, 0.0f};

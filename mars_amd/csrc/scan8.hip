@@ -88,19 +88,6 @@ struct QF8 {
     }
 };
 
-__device__ inline double row16_sum_f64(double v) {
-    auto x = [](double a, auto tag) {
-        constexpr int J = decltype(tag)::value;
-        const uint64_t b = uint64_t(__double_as_longlong(a));
-        return __longlong_as_double((long long)xor_lane64<J>(b));
-    };
-    v += x(v, std::integral_constant<int, 8>{});
-    v += x(v, std::integral_constant<int, 4>{});
-    v += x(v, std::integral_constant<int, 2>{});
-    v += x(v, std::integral_constant<int, 1>{});
-    return v;
-}
-
 // FILTER: the query has a modality filter (mods are read). The certified query never
 // has a same-episode boost (ScanArgs boost = 0, query_ep = -1).
 template <int NCH, bool FILTER>

@@ -423,24 +423,28 @@ def test_completion_word_matches_stream_sync(dev10k, corpus_10k):
 
 def test_read_ceiling(rng):
     """The streaming-read ceiling of a graph's rows: positive and below the HBM peak for
-    fp32 and fp16 rows, and for the three fp16 access patterns; MARS_ERR_INVALID for an
-    unknown pattern; MARS_ERR_UNSUPPORTED once the fp16 copy is gone."""
+    fp32 and fp16 rows, and for the four access patterns; MARS_ERR_INVALID for an unknown
+    pattern; MARS_ERR_UNSUPPORTED once the fp16 and int8 copies are gone."""
     from mars_amd._lib import MarsError
     emb, mods, ts, row, col, ep = random_graph(rng, 40000, 768)
     dev = Dev(emb, mods, ts, row, col, ep, fp16=True)
+    mars_amd.upload_int8_embeddings(dev.dg)
     try:
         for fp16 in (False, True):
             gbs = mars_amd.read_ceiling(dev.dg, fp16=fp16, reps=3)
             assert 0.0 < gbs < 8000.0 * 1.1, (fp16, gbs)
-        for pattern in (mars_amd.READ_STREAM, mars_amd.READ_FRAGMENTS, mars_amd.READ_FRAGMENTS_NT):
+        for pattern in (mars_amd.READ_STREAM, mars_amd.READ_FRAGMENTS, mars_amd.READ_FRAGMENTS_NT,
+                        mars_amd.READ_STREAM_INT8):
             gbs = mars_amd.read_pattern(dev.dg, pattern, reps=3)
             assert 0.0 < gbs < 8000.0 * 1.1, (pattern, gbs)
         with pytest.raises(MarsError) as e:
-            mars_amd.read_pattern(dev.dg, 3)
+            mars_amd.read_pattern(dev.dg, 4)
         assert e.value.code == -1
         mars_amd.free_fp16_embeddings(dev.dg)
+        mars_amd.free_int8_embeddings(dev.dg)
         for call in (lambda: mars_amd.read_ceiling(dev.dg, fp16=True),
-                     lambda: mars_amd.read_pattern(dev.dg, mars_amd.READ_FRAGMENTS)):
+                     lambda: mars_amd.read_pattern(dev.dg, mars_amd.READ_FRAGMENTS),
+                     lambda: mars_amd.read_pattern(dev.dg, mars_amd.READ_STREAM_INT8)):
             with pytest.raises(MarsError) as e:
                 call()
             assert e.value.code == -5
