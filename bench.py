@@ -738,7 +738,8 @@ def main() -> int:
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": scan_traffic(N, D, "k_scan_int8_1M.md" if cand == "int8" else "k_scan_fp16_1M.md"),
-                     "kernel": (f"k_scan8<{D // 256},false> (64 candidates per workgroup, keys = per-row upper bounds)"
+                     "kernel": (f"k_scan8<{D // 256},false> (16 keys per workgroup, 64 candidates, keys = per-row "
+                                f"upper bounds)"
                                 if cand == "int8" else f"k_scan<__half,QF16<{D // 128}>,false> (16 candidates per "
                                                        f"workgroup)"),
                      "bytes_per_launch": bytes_cert},

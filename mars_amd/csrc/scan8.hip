@@ -17,7 +17,7 @@
 //  k_scan8     the scan: k_scan's 16-lane row layout (lane s of a group reads bytes
 //              16s .. 16s+15 of each 256-byte chunk of its row), signed bytes
 //              converted with one v_cvt_f32_i32 (SDWA byte select) each, fp32 fmaf
-//              chain, the 16-lane reduction, then the row scale. fin[r] gets the int8
+//              chain against the query in LDS, the 16-lane reduction, then the row scale. fin[r] gets the int8
 //              estimate fuse(dot8) (within |q| max c_r of the exact score, used by the
 //              interval BFS); the key is U_r. Each workgroup writes its 16 best keys to a
 //              slot of its own, part[16 b ..] (no running bound: the workgroups finish
@@ -37,69 +37,75 @@
 namespace mars {
 namespace {
 
-// 8 waves per workgroup and 2 row groups of 4 rows per wave and step: under 128 VGPRs at
-// d = 768, so 512 workgroups keep 4 waves on every SIMD (1M x 768 rows: 145 us with
-// 4 waves x 4 groups per workgroup, 2 waves per SIMD; 127-130 us at 3-4 waves per SIMD).
+// 8 waves per workgroup and 2 row groups of 4 rows per wave and step: 100 VGPRs at d = 768,
+// so 512 workgroups keep 4 waves on every SIMD and leave room for a wave of another kernel
+// (1M x 768 rows on MI355X: 133 us; 145 us with 4 waves x 4 groups per workgroup, 2 waves
+// per SIMD; 162 us with one group per wave; 127 us with the query in registers, which
+// fills the SIMDs: a streaming insert's publication then waits for the scan, 150 us at p99
+// instead of 65).
 constexpr int kScan8Waves = 8;
 constexpr int kScan8Unroll = 2;
 
-// int8 rows: chunk c covers bytes [256c, 256c + 256); lane s of a 16-lane group holds
-// query floats 256c + 16s .. 256c + 16s + 15, in the order the fmaf chain uses them.
+// int8 rows: chunk c covers bytes [256c, 256c + 256); lane s of a 16-lane group reads the
+// 16 bytes 256c + 16s .. + 15 of its row and multiplies them with the query floats of the
+// same index, which the workgroup keeps in LDS (s_q[64 c + 4 s + j] = floats 256c + 16s +
+// 4j .. + 3) and reads one chunk at a time: 16 query registers per lane instead of d / 16,
+// which keeps the scan under 96 VGPRs so that other kernels (inserts, episode queries)
+// still find room on a SIMD beside its 4 waves.
 template <int NCH>
-struct QF8 {
-    float v[NCH][16];
-    __device__ void load(const float* q, int sub) {
+__device__ inline void fetch8(const int8_t* row, int sub, u32x4 (&x)[NCH]) {
+    const u32x4* r = reinterpret_cast<const u32x4*>(row) + sub;
 #pragma unroll
-        for (int c = 0; c < NCH; ++c) {
-            const f32x4* p = reinterpret_cast<const f32x4*>(q + c * 256 + sub * 16);
+    for (int c = 0; c < NCH; ++c) x[c] = __builtin_nontemporal_load(r + c * 16);
+}
+
+// Per-lane partial dots of U rows (the fmaf chain over the lane's bytes in index order).
+template <int NCH, int U>
+__device__ inline void dot8(const f32x4* s_q, int sub, const u32x4 (&x)[U][NCH], float (&acc)[U]) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const f32x4 x = p[j];
-                v[c][4 * j] = x.x; v[c][4 * j + 1] = x.y; v[c][4 * j + 2] = x.z; v[c][4 * j + 3] = x.w;
-            }
-        }
-    }
-    __device__ void fetch(const int8_t* row, int sub, u32x4 (&x)[NCH]) const {
-        const u32x4* r = reinterpret_cast<const u32x4*>(row) + sub;
+    for (int u = 0; u < U; ++u) acc[u] = 0.0f;
 #pragma unroll
-        for (int c = 0; c < NCH; ++c) x[c] = __builtin_nontemporal_load(r + c * 16);
-    }
-    __device__ float dot_fetched(const u32x4 (&x)[NCH]) const {
-        float acc = 0.0f;
+    for (int c = 0; c < NCH; ++c) {
+        f32x4 qv[4];
 #pragma unroll
-        for (int c = 0; c < NCH; ++c) {
-            const uint32_t w[4] = {x[c].x, x[c].y, x[c].z, x[c].w};
+        for (int j = 0; j < 4; ++j) qv[j] = s_q[64 * c + 4 * sub + j];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const uint32_t w[4] = {x[u][c].x, x[u][c].y, x[u][c].z, x[u][c].w};
 #pragma unroll
             for (int j = 0; j < 4; ++j)
 #pragma unroll
                 for (int b = 0; b < 4; ++b)
-                    acc = fmaf(float(int8_t(w[j] >> (8 * b))), v[c][4 * j + b], acc);
+                    acc[u] = fmaf(float(int8_t(w[j] >> (8 * b))), qv[j][b], acc[u]);
         }
-        return acc;
     }
-    // |q|^2 over the lane's elements, fp64
-    __device__ double norm2() const {
-        double s = 0.0;
-#pragma unroll
-        for (int c = 0; c < NCH; ++c)
-#pragma unroll
-            for (int j = 0; j < 16; ++j) s += double(v[c][j]) * double(v[c][j]);
-        return s;
-    }
-};
+}
 
 // FILTER: the query has a modality filter (mods are read). The certified query never
 // has a same-episode boost (ScanArgs boost = 0, query_ep = -1).
 template <int NCH, bool FILTER>
 __global__ __launch_bounds__(kScan8Waves * 64) void k_scan8(ScanArgs a) {
     __shared__ uint64_t s_lists[kScan8Waves][64];
+    __shared__ f32x4 s_q[NCH * 64];
     const int lane = lane_id(), wave = int(threadIdx.x >> 6);
     const int sub = lane & 15, grp = lane >> 4;
     const int k = a.k;
-    QF8<NCH> qf;
-    qf.load(a.q, sub);
-    // |q| rounded up to fp32 (every 16-lane group holds the whole query)
-    const float qn = __uint_as_float(up_bits(sqrt(row16_sum_f64(qf.norm2())) * (1.0 + 1e-12)));
+    for (int i = int(threadIdx.x); i < NCH * 64; i += kScan8Waves * 64) {
+        // s_q[64 c + 4 s + j] = query floats 256c + 16s + 4j .. + 3: the same as float4 i
+        s_q[i] = reinterpret_cast<const f32x4*>(a.q)[i];
+    }
+    __syncthreads();
+    // |q| rounded up to fp32 (each 16-lane group sums the whole query)
+    double q2 = 0.0;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const f32x4 v = s_q[64 * c + 4 * sub + j];
+            q2 += double(v.x) * double(v.x) + double(v.y) * double(v.y) + double(v.z) * double(v.z) +
+                  double(v.w) * double(v.w);
+        }
+    const float qn = __uint_as_float(up_bits(sqrt(row16_sum_f64(q2)) * (1.0 + 1e-12)));
     const int8_t* emb = static_cast<const int8_t*>(a.emb);
     const f32x2* meta = reinterpret_cast<const f32x2*>(a.meta8);
     uint64_t list = kEmptyKey, thr = kEmptyKey;
@@ -117,13 +123,15 @@ __global__ __launch_bounds__(kScan8Waves * 64) void k_scan8(ScanArgs a) {
             ts[u] = a.ts[rr];
             mt[u] = meta[rr];
             mod[u] = FILTER ? a.mods[rr] : 0;
-            qf.fetch(emb + rr * a.d, sub, x[u]);
+            fetch8<NCH>(emb + rr * a.d, sub, x[u]);
         }
+        float acc[kScan8Unroll];
+        dot8<NCH, kScan8Unroll>(s_q, sub, x, acc);
 #pragma unroll
         for (int u = 0; u < kScan8Unroll; ++u) {
             const int64_t r = (g0 + u) * 4 + grp;
             const bool valid = r < a.n;
-            const float dot = row16_sum(qf.dot_fetched(x[u])) * mt[u].x;
+            const float dot = row16_sum(acc[u]) * mt[u].x;
             // dot + |q| c_r, then raised past the fmaf's rounding (and any underflow)
             float up = fmaf(qn, mt[u].y, dot);
             up = up + fmaxf(fabsf(up) * 0x1p-20f, 1e-35f);
