@@ -282,7 +282,7 @@ int certified_query(const Graph& g, Ctx& c, const float* q, float t_q, const mar
     scan_grid(n_live, i8 ? kTargetWgI8 : kTargetWgF16, &rpw, &nwg);
     ScanArgs a{};
     a.emb = i8 ? static_cast<const void*>(g.emb8) : static_cast<const void*>(g.emb16); a.fp16 = i8 ? 0 : 1;
-    a.meta8 = g.meta8; a.n = n_live; a.d = g.d; a.q = q; a.ts = g.ts; a.mods = g.mods; a.ep_ids = g.ep_ids;
+    a.meta8 = g.meta8; a.nrm8 = g.nrm8; a.n = n_live; a.d = g.d; a.q = q; a.ts = g.ts; a.mods = g.mods; a.ep_ids = g.ep_ids;
     a.t_q = t_q; a.lambda = cfg->time_decay_lambda; a.mod_filter = cfg->modality_filter; a.query_ep = -1;
     a.boost = 0.0f; a.k = i8 ? kScan8List : cands; a.fin = c.fin; a.part = c.part; a.gthr = c.gthr;
     a.gcnt = c.gcnt; a.rows_per_wg = rpw; a.num_wg = nwg;
@@ -858,7 +858,11 @@ int mars_graph_enable_int8(mars_graph* gh) {
     MARS_CHECK(scan8_dim_supported(g.d), MARS_ERR_UNSUPPORTED,
                "int8 copy: embedding_dim %d is not 256, 512, 768, 1024 or 1536", g.d);
     MARS_TRY(use_device(g.device));
-    if (!g.emb8) MARS_TRY(dmalloc(&g.emb8, size_t(g.cap_n) * size_t(g.d)));
+    const size_t bytes8 = size_t(i8_rows_alloc(g.cap_n)) * size_t(g.d);      // whole 16-row tiles
+    if (!g.emb8) {
+        MARS_TRY(dmalloc(&g.emb8, bytes8));
+        MARS_HIP(hipMemset(g.emb8, 0, bytes8));                             // rows past n score 0
+    }
     if (!g.meta8) MARS_TRY(dmalloc(&g.meta8, size_t(g.cap_n) * 2));
     if (!g.nrm8) MARS_TRY(dmalloc(&g.nrm8, 2));
     MARS_HIP(hipMemset(g.nrm8, 0, 2 * sizeof(uint32_t)));
@@ -886,7 +890,15 @@ int mars_graph_read_int8(const mars_graph* gh, int32_t first, int32_t count, int
                "rows [%d, %lld) outside the %d published nodes", first, (long long)first + count, g.n);
     MARS_TRY(use_device(g.device));
     if (count == 0) return MARS_OK;
-    if (bytes) MARS_HIP(hipMemcpy(bytes, g.emb8 + size_t(first) * g.d, size_t(count) * g.d, hipMemcpyDeviceToHost));
+    if (bytes) {
+        // the 16-row tiles that hold the rows, then back to row-major order
+        const int64_t t0 = first / 16, t1 = (int64_t(first) + count + 15) / 16;
+        std::vector<int8_t> tiles(size_t(t1 - t0) * 16 * size_t(g.d));
+        MARS_HIP(hipMemcpy(tiles.data(), g.emb8 + t0 * 16 * g.d, tiles.size(), hipMemcpyDeviceToHost));
+        for (int32_t r = 0; r < count; ++r)
+            for (int32_t k = 0; k < g.d; ++k)
+                bytes[size_t(r) * g.d + k] = tiles[size_t(i8_offset(int64_t(first) + r, k, g.d) - t0 * 16 * g.d)];
+    }
     if (meta) MARS_HIP(hipMemcpy(meta, g.meta8 + size_t(first) * 2, size_t(count) * 2 * sizeof(float),
                                  hipMemcpyDeviceToHost));
     return MARS_OK;

@@ -403,11 +403,12 @@ __device__ inline float wave_max_f(float v) {
     return v;
 }
 
-// One wave quantizes one row (d floats at e): the bytes go to out, (s_r, c_r) to meta;
-// lane 0 raises nrm8[0] to c_r and nrm8[1] to |e|. Sums of squares in fp64, c_r rounded
-// up to fp32. A NaN or infinite element makes c_r NaN or infinite, and with it nrm8[0]:
-// the certificate then never holds.
-__device__ inline void quantize_row_i8(const float* e, int32_t d, int8_t* out, float* meta, uint32_t* nrm8) {
+// One wave quantizes row `row` (d floats at e): the bytes go to the tiled copy emb8
+// (i8_offset), (s_r, c_r) to meta; lane 0 raises nrm8[0] to c_r and nrm8[1] to |e|. Sums of
+// squares in fp64, c_r rounded up to fp32. A NaN or infinite element makes c_r NaN or
+// infinite, and with it nrm8[0]: the certificate then never holds.
+__device__ inline void quantize_row_i8(const float* e, int32_t d, int8_t* emb8, int64_t row, float* meta,
+                                       uint32_t* nrm8) {
     const int lane = lane_id();
     float m = 0.0f;
     for (int i = lane; i < d; i += 64) m = fmaxf(m, fabsf(e[i]));
@@ -419,7 +420,7 @@ __device__ inline void quantize_row_i8(const float* e, int32_t d, int8_t* out, f
         float t = s > 0.0f ? rintf(x / s) : 0.0f;
         t = fminf(fmaxf(t, -127.0f), 127.0f);
         const int v = int(t);
-        out[i] = int8_t(v);
+        emb8[i8_offset(row, i, d)] = int8_t(v);
         const double eh = double(s) * double(v);
         s32 += double(x) * double(x);
         s8 += eh * eh;

@@ -115,8 +115,8 @@ __global__ __launch_bounds__(256) void k_stage_insert(StageArgs a) {
         }
         if (a.emb16 && a.nrm) raise_row_norms(s32, s16, sd, a.nrm);
         if (a.emb8)
-            quantize_row_i8(reinterpret_cast<const float*>(src), a.d, a.emb8 + (a.n_old + r) * a.d,
-                            a.meta8 + 2 * (a.n_old + r), a.nrm8);
+            quantize_row_i8(reinterpret_cast<const float*>(src), a.d, a.emb8, a.n_old + r, a.meta8 + 2 * (a.n_old + r),
+                            a.nrm8);
     }
     for (int64_t i = tid; i < a.n_new; i += stride) {
         a.g_mods[a.n_old + i] = a.mods[i];

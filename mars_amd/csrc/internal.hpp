@@ -331,7 +331,10 @@ struct ScanArgs {
     int64_t id_base;         // node id of row 0 (tiles of a host-resident corpus)
     const float* meta8;      // int8 rows (launch_scan8): per-row scale and error bound; workgroup b
                              // writes its k (= kScan8List) best keys, ascending and
-                             // kEmptyKey-padded, to part[k b .. k b + k - 1] (gthr, gcnt untouched)
+                             // kEmptyKey-padded, to part[k b .. k b + k - 1] (gthr, gcnt untouched),
+                             // and the query's rounding term tau to part[kScan8MaxLists *
+                             // kScan8List] (fp32 bits)
+    const uint32_t* nrm8;    // launch_scan8: Graph::nrm8
 };
 // Kernel entry point + launch shape of one launch (for graph kernel nodes).
 struct KernelLaunch {
@@ -346,6 +349,14 @@ KernelLaunch episode_launch(int32_t d);
 void scan_grid(int64_t n, int32_t max_wg, int32_t* rows_per_wg, int32_t* num_wg);
 // int8 candidate scan of the certified global query (scan8.hip): keys rank rows by an
 // upper bound of their fp32 scan score, fin gets the int8 estimate of every row.
+// The int8 copy is tiled for the MFMA scan: rows are grouped in tiles of 16, and each 64-byte
+// k-chunk i of a tile is a 1 KB block whose 16-byte piece 16 g + m holds bytes 64 i + 16 g ..
+// 64 i + 16 g + 15 of the tile's row m (the B operand of v_mfma_i32_16x16x64_i8, one load
+// instruction per block). d is a multiple of 64.
+__host__ __device__ inline int64_t i8_offset(int64_t row, int32_t k, int32_t d) {
+    return ((row >> 4) * (d >> 6) + (k >> 6)) * 1024 + ((((k & 63) >> 4) << 4) + (row & 15)) * 16 + (k & 15);
+}
+__host__ __device__ inline int64_t i8_rows_alloc(int64_t rows) { return (rows + 15) / 16 * 16; }
 constexpr int32_t kScan8MaxLists = 512;    // int8 scan workgroups = lists k_cert_bfs merges
 constexpr int32_t kScan8List = 16;         // keys per workgroup list
 bool scan8_dim_supported(int32_t d);

@@ -919,10 +919,12 @@ __global__ __launch_bounds__(kFinThreads) void k_cert_bfs(CertArgs a, MultiArgs 
     double eps, slack, en;
     if (a.upper) {
         // int8 scan: keys are per-row upper bounds of the exact score (no slack), the
-        // estimates in fin lie within |q| max c_r plus the two products' rounding
+        // estimates in fin lie within |q| max c_r + tau plus the two products' rounding
         const double cm = double(__uint_as_float(a.nrm8[0]));
         en = double(__uint_as_float(a.nrm8[1]));
-        eps = (cm * qn + 4.0 * u * (en + cm) * qn) * 1.01 + 1e-30 * double(a.d);
+        // plus the scan's per-query term (query split remainder and roundings)
+        const double tau = double(__uint_as_float(uint32_t(a.part[int64_t(kScan8MaxLists) * kScan8List])));
+        eps = (cm * qn + 4.0 * u * (en + cm) * qn) * 1.01 + tau + 1e-30 * double(a.d);
         slack = 0.0;
     } else {
         const double e32 = double(__uint_as_float(a.nrm[0]));

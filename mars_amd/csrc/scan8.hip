@@ -14,17 +14,21 @@
 //  per-row bound instead of one global bound is what makes 64 candidates enough: rows
 //  with large elements (coarse scales) are the only ones that pay for them.
 //
-//  k_scan8     the scan: k_scan's 16-lane row layout (lane s of a group reads bytes
-//              16s .. 16s+15 of each 256-byte chunk of its row), signed bytes
-//              converted with one v_cvt_f32_i32 (SDWA byte select) each, fp32 fmaf
-//              chain against the query in LDS, the 16-lane reduction, then the row scale. fin[r] gets the int8
-//              estimate fuse(dot8) (within |q| max c_r of the exact score, used by the
-//              interval BFS); the key is U_r. Each workgroup writes its 16 best keys to a
-//              slot of its own, part[16 b ..] (no running bound: the workgroups finish
-//              together, so one would filter little); k_cert_bfs merges them into the 64
-//              candidates and bounds the rows a list dropped by the smallest 16th key.
-//              (Rows are dealt to the workgroups in blocks of 64 consecutive ids; on the
-//              benchmark corpus, 16 per workgroup certify as often as 64 would.)
+//  k_scan8     the scan, on MFMA: the copy is tiled in blocks of 16 rows x 64 bytes
+//              (i8_offset), each block one 1 KB load instruction and the B operand of
+//              one v_mfma_i32_16x16x64_i8. The query is split into two int8 parts,
+//              q = s_hi q_hi + s_lo q_lo + r2 (|r2| ~ 1e-4 |q|), the A operand's first two
+//              rows, so the products are summed exactly in int32 and the row's dot is
+//              s_r (s_hi A_hi + s_lo A_lo) in three fp32 operations; r2 and those three
+//              roundings enter the bound as one per-query term tau. Lanes 0-15 of the
+//              wave then hold one row each: fin[r] gets the estimate fuse(dot8) (within
+//              |q| max c + tau of the exact score, used by the interval BFS); the key is
+//              U_r. Each workgroup writes its 16 best keys to a slot of its own,
+//              part[16 b ..] (no running bound: the workgroups finish together, so one
+//              would filter little); k_cert_bfs merges them into the 64 candidates and
+//              bounds the rows a list dropped by the smallest 16th key. (Rows are dealt
+//              to the workgroups in blocks of 128 consecutive ids; on the benchmark corpus,
+//              16 per workgroup certify as often as 64 would.)
 //  k_convert_i8  one wave per row: scale, bytes, c_r and the maxima (quantize_row_i8).
 //
 //  Reference analogue: none — the reference scores fp32 (cublasSgemv) or fp16 rows
@@ -37,113 +41,161 @@
 namespace mars {
 namespace {
 
-// 8 waves per workgroup and 2 row groups of 4 rows per wave and step: 100 VGPRs at d = 768,
-// so 512 workgroups keep 4 waves on every SIMD and leave room for a wave of another kernel
-// (1M x 768 rows on MI355X: 133 us; 145 us with 4 waves x 4 groups per workgroup, 2 waves
-// per SIMD; 162 us with one group per wave; 127 us with the query in registers, which
-// fills the SIMDs: a streaming insert's publication then waits for the scan, 150 us at p99
-// instead of 65).
-constexpr int kScan8Waves = 8;
-constexpr int kScan8Unroll = 2;
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 
-// int8 rows: chunk c covers bytes [256c, 256c + 256); lane s of a 16-lane group reads the
-// 16 bytes 256c + 16s .. + 15 of its row and multiplies them with the query floats of the
-// same index, which the workgroup keeps in LDS (s_q[64 c + 4 s + j] = floats 256c + 16s +
-// 4j .. + 3) and reads one chunk at a time: 16 query registers per lane instead of d / 16,
-// which keeps the scan under 96 VGPRs so that other kernels (inserts, episode queries)
-// still find room on a SIMD beside its 4 waves.
-template <int NCH>
-__device__ inline void fetch8(const int8_t* row, int sub, u32x4 (&x)[NCH]) {
-    const u32x4* r = reinterpret_cast<const u32x4*>(row) + sub;
-#pragma unroll
-    for (int c = 0; c < NCH; ++c) x[c] = __builtin_nontemporal_load(r + c * 16);
-}
+// 8 waves per workgroup, one tile of 16 rows per wave and step (d / 64 loads of 1 KB in
+// flight, the next tile's issued before the current tile's scores are fused): 512
+// workgroups keep 4 waves on every SIMD, with room beside them for a wave of another
+// kernel (inserts, episode queries).
+constexpr int kScan8Waves = 4;
+constexpr int kScan8Ring = 2;
+constexpr int kScan8Threads = kScan8Waves * 64;
 
-// Per-lane partial dots of U rows (the fmaf chain over the lane's bytes in index order).
-template <int NCH, int U>
-__device__ inline void dot8(const f32x4* s_q, int sub, const u32x4 (&x)[U][NCH], float (&acc)[U]) {
-#pragma unroll
-    for (int u = 0; u < U; ++u) acc[u] = 0.0f;
-#pragma unroll
-    for (int c = 0; c < NCH; ++c) {
-        f32x4 qv[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) qv[j] = s_q[64 * c + 4 * sub + j];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const uint32_t w[4] = {x[u][c].x, x[u][c].y, x[u][c].z, x[u][c].w};
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-#pragma unroll
-                for (int b = 0; b < 4; ++b)
-                    acc[u] = fmaf(float(int8_t(w[j] >> (8 * b))), qv[j][b], acc[u]);
-        }
-    }
-}
-
-// FILTER: the query has a modality filter (mods are read). The certified query never
-// has a same-episode boost (ScanArgs boost = 0, query_ep = -1).
-template <int NCH, bool FILTER>
-__global__ __launch_bounds__(kScan8Waves * 64) void k_scan8(ScanArgs a) {
-    __shared__ uint64_t s_lists[kScan8Waves][64];
-    __shared__ f32x4 s_q[NCH * 64];
-    const int lane = lane_id(), wave = int(threadIdx.x >> 6);
-    const int sub = lane & 15, grp = lane >> 4;
-    const int k = a.k;
-    for (int i = int(threadIdx.x); i < NCH * 64; i += kScan8Waves * 64) {
-        // s_q[64 c + 4 s + j] = query floats 256c + 16s + 4j .. + 3: the same as float4 i
-        s_q[i] = reinterpret_cast<const f32x4*>(a.q)[i];
-    }
+// Block reductions of the query split (every thread gets the result).
+__device__ inline float block_max8(float v, float* s_red) {
+    v = wave_max_f(v);
+    __syncthreads();                             // s_red free
+    if (lane_id() == 0) s_red[threadIdx.x >> 6] = v;
     __syncthreads();
-    // |q| rounded up to fp32 (each 16-lane group sums the whole query)
-    double q2 = 0.0;
+    float m = 0.0f;
 #pragma unroll
-    for (int c = 0; c < NCH; ++c)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const f32x4 v = s_q[64 * c + 4 * sub + j];
-            q2 += double(v.x) * double(v.x) + double(v.y) * double(v.y) + double(v.z) * double(v.z) +
-                  double(v.w) * double(v.w);
-        }
-    const float qn = __uint_as_float(up_bits(sqrt(row16_sum_f64(q2)) * (1.0 + 1e-12)));
-    const int8_t* emb = static_cast<const int8_t*>(a.emb);
+    for (int w = 0; w < kScan8Waves; ++w) m = fmaxf(m, s_red[w]);
+    return m;
+}
+
+// NK = d / 64 k-chunks. FILTER: the query has a modality filter (mods are read). The
+// certified query never has a same-episode boost (ScanArgs boost = 0, query_ep = -1).
+template <int NK, bool FILTER>
+__global__ __launch_bounds__(kScan8Threads) void k_scan8(ScanArgs a) {
+    __shared__ uint64_t s_lists[kScan8Waves][64];
+    __shared__ i32x4 s_qa[NK][64];               // A operand per k-chunk: rows 0 / 1 = q_hi / q_lo
+    __shared__ float s_red[kScan8Waves];
+    __shared__ double s_sum[kScan8Waves][4];
+    constexpr int D = NK * 64;
+    constexpr int kPer = (D + kScan8Threads - 1) / kScan8Threads;
+    const int tid = int(threadIdx.x), lane = lane_id(), wave = tid >> 6, m = lane & 15;
+    const int k = a.k;
+    const i32x4* blocks = static_cast<const i32x4*>(a.emb);        // 64 x 16 bytes per block
     const f32x2* meta = reinterpret_cast<const f32x2*>(a.meta8);
+    const int64_t ntiles = (a.n + 15) / 16;
+    const int64_t tstride = int64_t(gridDim.x) * kScan8Waves;
+    int64_t t = int64_t(blockIdx.x) * kScan8Waves + wave;
+    // kScan8Ring tiles in flight: a tile's row blocks and its rows' scale, bound, time and
+    // modality (lane m: row 16 t + m)
+    constexpr int R = NK <= 16 ? kScan8Ring : 1;  // d = 1536: one (the registers of two exceed a SIMD's share)
+    i32x4 b[R][NK];
+    f32x2 mt[R];
+    float tsv[R];
+    int32_t modv[R];
+    auto load_tile = [&](int sl, int64_t tt) {
+        int64_t rr = tt * 16 + m;
+        rr = rr < a.n ? rr : a.n - 1;
+        mt[sl] = meta[rr];
+        tsv[sl] = a.ts[rr];
+        modv[sl] = FILTER ? a.mods[rr] : 0;
+        const i32x4* p = blocks + tt * NK * 64 + lane;
+#pragma unroll
+        for (int i = 0; i < NK; ++i) b[sl][i] = __builtin_nontemporal_load(p + i * 64);
+    };
+#pragma unroll
+    for (int sl = 0; sl < R; ++sl)                // in flight while the query is split
+        if (t + sl * tstride < ntiles) load_tile(sl, t + sl * tstride);
+    // ---- q = s_hi q_hi + s_lo q_lo + r2, q_hi and q_lo in [-127, 127]
+    float qv[kPer];
+    float m1 = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+        const int e = tid + j * kScan8Threads;
+        qv[j] = e < D ? a.q[e] : 0.0f;
+        m1 = fmaxf(m1, fabsf(qv[j]));
+    }
+    const float s_hi = block_max8(m1, s_red) / 127.0f;
+    int32_t qh[kPer], ql[kPer];
+    float r1[kPer];
+    float m2 = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+        const float h = s_hi > 0.0f ? fminf(fmaxf(rintf(qv[j] / s_hi), -127.0f), 127.0f) : 0.0f;
+        qh[j] = int32_t(h);
+        r1[j] = fmaf(-s_hi, h, qv[j]);
+        m2 = fmaxf(m2, fabsf(r1[j]));
+    }
+    const float s_lo = block_max8(m2, s_red) / 127.0f;
+    double sr2 = 0.0, shi = 0.0, slo = 0.0, q2 = 0.0;
+    int8_t* qa = reinterpret_cast<int8_t*>(&s_qa[0][0]);
+    for (int i = tid; i < NK * 64 * 4; i += kScan8Threads) reinterpret_cast<int32_t*>(qa)[i] = 0;
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+        const int e = tid + j * kScan8Threads;
+        if (e < D) {
+            ql[j] = s_lo > 0.0f ? int32_t(fminf(fmaxf(rintf(r1[j] / s_lo), -127.0f), 127.0f)) : 0;
+            const double hq = double(s_hi) * double(qh[j]), lq = double(s_lo) * double(ql[j]);
+            const double r2 = double(qv[j]) - hq - lq;
+            sr2 += r2 * r2;
+            shi += hq * hq;
+            slo += lq * lq;
+            q2 += double(qv[j]) * double(qv[j]);
+            // chunk e / 64, lane 16 g + row (0: q_hi, 1: q_lo), byte e % 16
+            const int blk = (e >> 6) * 64 + (((e & 63) >> 4) << 4);
+            qa[size_t(blk) * 16 + (e & 15)] = int8_t(qh[j]);
+            qa[size_t(blk + 1) * 16 + (e & 15)] = int8_t(ql[j]);
+        }
+    }
+    sr2 = wave_sum_f64(sr2);
+    shi = wave_sum_f64(shi);
+    slo = wave_sum_f64(slo);
+    q2 = wave_sum_f64(q2);
+    if (lane == 0) { s_sum[wave][0] = sr2; s_sum[wave][1] = shi; s_sum[wave][2] = slo; s_sum[wave][3] = q2; }
+    __syncthreads();
+    sr2 = shi = slo = q2 = 0.0;
+#pragma unroll
+    for (int w = 0; w < kScan8Waves; ++w) {
+        sr2 += s_sum[w][0]; shi += s_sum[w][1]; slo += s_sum[w][2]; q2 += s_sum[w][3];
+    }
+    // |q| rounded up
+    const float qn = __uint_as_float(up_bits(sqrt(q2) * (1.0 + 1e-12)));
+    // tau: |e^_r| (|r2| + 3.1 u (|q_hi| + |q_lo|)) with |e^_r| <= max |e| + max c_r
+    const double en8 = double(__uint_as_float(a.nrm8[1])) + double(__uint_as_float(a.nrm8[0]));
+    const float tau = __uint_as_float(up_bits(en8 * (sqrt(sr2) + 3.1 * 0x1p-24 * (sqrt(shi) + sqrt(slo))) *
+                                              (1.0 + 1e-6) + 1e-30));
+    if (blockIdx.x == 0 && tid == 0) a.part[int64_t(kScan8MaxLists) * kScan8List] = uint64_t(__float_as_uint(tau));
     uint64_t list = kEmptyKey, thr = kEmptyKey;
-    const int64_t ngroups = (a.n + 3) / 4;
-    const int64_t gstride = int64_t(gridDim.x) * kScan8Waves * kScan8Unroll;
-    for (int64_t g0 = (int64_t(blockIdx.x) * kScan8Waves + wave) * kScan8Unroll; g0 < ngroups; g0 += gstride) {
-        u32x4 x[kScan8Unroll][NCH];
-        f32x2 mt[kScan8Unroll];
-        float ts[kScan8Unroll];
-        int32_t mod[kScan8Unroll];
+    for (int64_t t0 = t; t0 < ntiles; t0 += R * tstride)
 #pragma unroll
-        for (int u = 0; u < kScan8Unroll; ++u) {
-            int64_t rr = (g0 + u) * 4 + grp;
-            rr = rr < a.n ? rr : a.n - 1;
-            ts[u] = a.ts[rr];
-            mt[u] = meta[rr];
-            mod[u] = FILTER ? a.mods[rr] : 0;
-            fetch8<NCH>(emb + rr * a.d, sub, x[u]);
-        }
-        float acc[kScan8Unroll];
-        dot8<NCH, kScan8Unroll>(s_q, sub, x, acc);
+    for (int sl = 0; sl < R; ++sl) {
+        const int64_t t = t0 + sl * tstride;
+        if (t >= ntiles) break;                  // uniform over the wave
+        const f32x2 cmt = mt[sl];
+        const float cts = tsv[sl];
+        const int32_t cmod = modv[sl];
+        i32x4 acc = i32x4{0, 0, 0, 0};
+        // A fragments read from LDS four chunks ahead at most (16 VGPRs), not all at once
 #pragma unroll
-        for (int u = 0; u < kScan8Unroll; ++u) {
-            const int64_t r = (g0 + u) * 4 + grp;
-            const bool valid = r < a.n;
-            const float dot = row16_sum(acc[u]) * mt[u].x;
-            // dot + |q| c_r, then raised past the fmaf's rounding (and any underflow)
-            float up = fmaf(qn, mt[u].y, dot);
-            up = up + fmaxf(fabsf(up) * 0x1p-20f, 1e-35f);
-            // fuse_score's arithmetic with one exp: the filter, then dot * w
-            const bool out = FILTER && mod[u] != a.mod_filter;
-            const float w = decay_weight(ts[u], a);
-            const float s8 = out ? -FLT_MAX : dot * w;
-            const float su = out ? -FLT_MAX : up * w;
-            if (valid && sub == 0) a.fin[r] = s8;
-            const uint64_t key = valid ? make_key(su, uint32_t(a.id_base + r)) : kEmptyKey;
-            list_offer(list, thr, key, sub == 0, lane, k);
+        for (int i0 = 0; i0 < NK; i0 += 4) {
+#pragma unroll
+            for (int i = i0; i < i0 + 4 && i < NK; ++i)
+                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(s_qa[i][lane], b[sl][i], acc, 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
         }
+        // the slot's next tile (R strides on) reuses its registers once the MFMAs read them
+        if (t + R * tstride < ntiles) load_tile(sl, t + R * tstride);
+        __builtin_amdgcn_sched_barrier(0);
+        // lanes 0-15: C[0][m] = q_hi . row m, C[1][m] = q_lo . row m (exact int32 sums)
+        const int64_t r = t * 16 + m;
+        const bool valid = lane < 16 && r < a.n;
+        const float dot = fmaf(s_lo, float(acc[1]), s_hi * float(acc[0])) * cmt.x;
+        // dot + |q| c_r + tau, then raised past the roundings (and any underflow)
+        float up = fmaf(qn, cmt.y, dot) + tau;
+        up = up + fmaxf(fabsf(up) * 0x1p-20f, 1e-35f);
+        // fuse_score's arithmetic with one exp: the filter, then dot * w
+        const bool out = FILTER && cmod != a.mod_filter;
+        const float w = decay_weight(cts, a);
+        const float s8 = out ? -FLT_MAX : dot * w;
+        const float su = out ? -FLT_MAX : up * w;
+        if (valid) a.fin[r] = s8;
+        const uint64_t key = valid ? make_key(su, uint32_t(a.id_base + r)) : kEmptyKey;
+        list_offer(list, thr, key, valid, lane, k);
     }
     s_lists[wave][lane] = list;
     __syncthreads();
@@ -159,14 +211,14 @@ __global__ __launch_bounds__(256) void k_convert_i8(const float* __restrict__ em
                                                     uint32_t* __restrict__ nrm8) {
     const int wave = int(threadIdx.x >> 6);
     for (int64_t row = r0 + int64_t(blockIdx.x) * 4 + wave; row < r1; row += int64_t(gridDim.x) * 4)
-        quantize_row_i8(emb + row * d, d, emb8 + row * d, meta8 + 2 * row, nrm8);
+        quantize_row_i8(emb + row * d, d, emb8, row, meta8 + 2 * row, nrm8);
 }
 
-template <int NCH>
+template <int NK>
 int launch_scan8_t(const ScanArgs& a, hipStream_t s) {
-    const dim3 grid(unsigned(a.num_wg)), block(kScan8Waves * 64);
-    if (a.mod_filter >= 0) MARS_LAUNCH((k_scan8<NCH, true>), grid, block, 0, s, a);
-    else MARS_LAUNCH((k_scan8<NCH, false>), grid, block, 0, s, a);
+    const dim3 grid(unsigned(a.num_wg)), block(kScan8Threads);
+    if (a.mod_filter >= 0) MARS_LAUNCH((k_scan8<NK, true>), grid, block, 0, s, a);
+    else MARS_LAUNCH((k_scan8<NK, false>), grid, block, 0, s, a);
     return MARS_OK;
 }
 
@@ -183,12 +235,13 @@ int launch_scan8(const ScanArgs& a, hipStream_t s) {
                a.k);
     MARS_CHECK(a.boost == 0.0f && a.query_ep < 0, MARS_ERR_INVALID, "int8 scan: no same-episode boost");
     MARS_CHECK(a.num_wg >= 1 && a.num_wg <= kScan8MaxLists, MARS_ERR_INVALID, "int8 scan: %d workgroups", a.num_wg);
-    switch (scan8_dim_supported(a.d) ? a.d / 256 : 0) {
-        case 1: return launch_scan8_t<1>(a, s);
-        case 2: return launch_scan8_t<2>(a, s);
-        case 3: return launch_scan8_t<3>(a, s);
+    MARS_CHECK(a.nrm8 != nullptr, MARS_ERR_INVALID, "int8 scan: no row bounds");
+    switch (scan8_dim_supported(a.d) ? a.d / 64 : 0) {
         case 4: return launch_scan8_t<4>(a, s);
-        case 6: return launch_scan8_t<6>(a, s);
+        case 8: return launch_scan8_t<8>(a, s);
+        case 12: return launch_scan8_t<12>(a, s);
+        case 16: return launch_scan8_t<16>(a, s);
+        case 24: return launch_scan8_t<24>(a, s);
         default: break;
     }
     return set_error(MARS_ERR_UNSUPPORTED, "int8 scan: embedding_dim %d is not 256, 512, 768, 1024 or 1536", a.d);

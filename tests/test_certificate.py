@@ -187,11 +187,13 @@ def test_certificate_names_the_fp32_top_k():
 
 
 # ---- the int8 candidate scan (k_scan8) ----------------------------------------------------
-# Row r is kept as bytes v in [-127, 127] and a scale s = fl(max|e| / 127); the scan's dot
-# is lane s chaining fmaf over bytes 256c + 16s + j (j = 0..15), the xor tree, then * s.
-# Its key is the upper bound U = fl(w * X), X = fmaf(|q|_up, c_r, dot8) raised by
-# max(|X| 2^-20, 1e-35); the interval BFS uses fin = fl(w * dot8) with half-width
-# eps8 = (|q| max c + 4u |q| (max|e| + max c)) * 1.01 + 1e-30 d.
+# Row r is kept as bytes v in [-127, 127] and a scale s = fl(max|e| / 127). The query is split
+# into two int8 parts, q = s_hi q_hi + s_lo q_lo + r2, and the MFMA sums v . q_hi and v . q_lo
+# exactly in int32; the scan's dot is fmaf(s_lo, lo, s_hi * hi) * s. Its key is the upper bound
+# U = fl(w * X), X = fmaf(|q|_up, c_r, dot8) + tau raised by max(|X| 2^-20, 1e-35), with
+# tau = (max|e| + max c) (|r2| + 3.1 u (|s_hi q_hi| + |s_lo q_lo|)); the interval BFS uses
+# fin = fl(w * dot8) with half-width eps8 = (|q| max c + 4u |q| (max|e| + max c)) * 1.01 + tau
+# + 1e-30 d.
 
 def up32(x):
     """fp32 values >= x (float64 array)."""
@@ -213,30 +215,45 @@ def quantize_i8(e):
     return v, s, up32(c)
 
 
-def dot_qf8(v, s, q):
-    n, d = v.shape
-    x = v.astype(F32)
-    acc = np.zeros((n, 16), F32)
-    for c in range(d // 256):
-        for j in range(16):
-            idx = 256 * c + 16 * np.arange(16) + j
-            acc = fma32(x[:, idx], q[idx][None, :], acc)
-    return (tree16(acc) * s).astype(F32)
+def split_query(q):
+    """k_scan8's query split: (s_hi, s_lo, q_hi, q_lo, |r2|, |s_hi q_hi|, |s_lo q_lo|)."""
+    s_hi = F32(np.abs(q).max()) / F32(127)
+    qh = np.clip(np.rint((q / s_hi).astype(F32)), -127, 127) if s_hi > 0 else np.zeros_like(q)
+    r1 = fma32(np.full_like(q, -s_hi), qh.astype(F32), q)
+    s_lo = F32(np.abs(r1).max()) / F32(127)
+    ql = np.clip(np.rint((r1 / s_lo).astype(F32)), -127, 127) if s_lo > 0 else np.zeros_like(q)
+    hq, lq = np.float64(s_hi) * qh.astype(np.float64), np.float64(s_lo) * ql.astype(np.float64)
+    r2 = q.astype(np.float64) - hq - lq
+    return (s_hi, s_lo, qh.astype(np.int64), ql.astype(np.int64), float(np.sqrt((r2 ** 2).sum())),
+            float(np.sqrt((hq ** 2).sum())), float(np.sqrt((lq ** 2).sum())))
 
 
-def upper_i8(dot8, c, q, w):
+def dot_mfma8(v, s, q):
+    s_hi, s_lo, qh, ql = split_query(q)[:4]
+    hi = (v.astype(np.int64) @ qh).astype(F32)                # exact int32 sums, exact in fp32
+    lo = (v.astype(np.int64) @ ql).astype(F32)
+    return (fma32(np.full_like(lo, s_lo), lo, (s_hi * hi).astype(F32)) * s).astype(F32)
+
+
+def tau_i8(c, e, q):
+    _, _, _, _, r2, nh, nl = split_query(q)
+    en = float(up32(np.sqrt((e.astype(np.float64) ** 2).sum(1)).max())) + float(c.max())
+    return float(up32(en * (r2 + 3.1 * U * (nh + nl)) * (1 + 1e-6) + 1e-30))
+
+
+def upper_i8(dot8, c, q, w, tau):
     qn_up = up32(np.sqrt((q.astype(np.float64) ** 2).sum()) * (1 + 1e-12))
-    x = fma32(np.full_like(dot8, qn_up), c, dot8)
+    x = (fma32(np.full_like(dot8, qn_up), c, dot8) + F32(tau)).astype(F32)
     x = (x + np.maximum(np.abs(x) * F32(2.0 ** -20), F32(1e-35))).astype(F32)
     return fused(x, w)
 
 
-def eps_i8(c, e, q):
+def eps_i8(c, e, q, tau):
     d = e.shape[1]
     qn = float(np.sqrt((q.astype(np.float64) ** 2).sum()))
     en = float(up32(np.sqrt((e.astype(np.float64) ** 2).sum(1)).max()))
     cm = float(c.max())
-    return (cm * qn + 4 * U * (en + cm) * qn) * 1.01 + 1e-30 * d
+    return (cm * qn + 4 * U * (en + cm) * qn) * 1.01 + tau + 1e-30 * d
 
 
 def make_cases_i8(rng, n=600, d=768):
@@ -271,11 +288,12 @@ def test_int8_upper_bound_covers_every_row():
             v, s, c = quantize_i8(e)
             w = np.exp(-0.1 * rng.uniform(0, 30, size=e.shape[0])).astype(F32)
             s32 = fused(dot_qf32(e, q), w).astype(np.float64)
-            d8 = dot_qf8(v, s, q)
+            d8 = dot_mfma8(v, s, q)
+            tau = tau_i8(c, e, q)
             s8 = fused(d8, w).astype(np.float64)
-            up = upper_i8(d8, c, q, w).astype(np.float64)
+            up = upper_i8(d8, c, q, w, tau).astype(np.float64)
             assert (up >= s32).all(), (name, qi, float((s32 - up).max()))
-            eps = eps_i8(c, e, q)
+            eps = eps_i8(c, e, q, tau)
             assert np.abs(s8 - s32).max() <= eps, (name, qi, np.abs(s8 - s32).max(), eps)
             # the bounds are not vacuous: within a small factor of the errors seen
             gap = np.abs(s8 - s32).max()
@@ -336,7 +354,7 @@ def test_int8_certificate_names_the_fp32_top_k():
         if trial % 4 == 0:
             w[100:180] = w[7] = F32(1.0)
         s32 = fused(dot_qf32(e, q), w)
-        up = upper_i8(dot_qf8(v, s, q), c, q, w)
+        up = upper_i8(dot_mfma8(v, s, q), c, q, w, tau_i8(c, e, q))
         cand, bnd = workgroup_candidates(up)
         exact = cand[keys(s32[cand])]
         ok = bnd is None or float(s32[exact[k - 1]]) > float(up[bnd])
