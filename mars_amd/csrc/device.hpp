@@ -403,41 +403,76 @@ __device__ inline float wave_max_f(float v) {
     return v;
 }
 
-// One wave quantizes row `row` (d floats at e): the bytes go to the tiled copy emb8
-// (i8_offset), (s_r, c_r) to meta; lane 0 raises nrm8[0] to c_r and nrm8[1] to |e|. Sums of
-// squares in fp64, c_r rounded up to fp32. A NaN or infinite element makes c_r NaN or
-// infinite, and with it nrm8[0]: the certificate then never holds.
-__device__ inline void quantize_row_i8(const float* e, int32_t d, int8_t* emb8, int64_t row, float* meta,
-                                       uint32_t* nrm8) {
-    const int lane = lane_id();
-    float m = 0.0f;
-    for (int i = lane; i < d; i += 64) m = fmaxf(m, fabsf(e[i]));
-    m = wave_max_f(m);
-    const float s = m / 127.0f;
+// Quantizing one row (one wave): the scale from the row's max |e|, then per element its byte
+// (into the tiled copy) and fp64 sums of squares of e, e^ and e^ - e; lane 0 stores (s_r, c_r)
+// to meta and raises nrm8[0] to c_r and nrm8[1] to |e| (c_r rounded up to fp32). A NaN or
+// infinite element makes c_r NaN or infinite, and with it nrm8[0]: the certificate then
+// never holds.
+struct I8Row {
+    float s;                                  // the row's scale
+    int8_t* tile;                             // the row's byte 0 in its tile
     double s32 = 0.0, s8 = 0.0, sd = 0.0;
-    for (int i = lane; i < d; i += 64) {
-        const float x = e[i];
+    __device__ I8Row(float max_abs, int8_t* emb8, int64_t row, int32_t d)
+        : s(max_abs / 127.0f), tile(emb8 + i8_offset(row, 0, d)) {}
+    __device__ void put(int32_t i, float x) {
         float t = s > 0.0f ? rintf(x / s) : 0.0f;
         t = fminf(fmaxf(t, -127.0f), 127.0f);
         const int v = int(t);
-        emb8[i8_offset(row, i, d)] = int8_t(v);
+        tile[((i >> 6) << 10) + (((i & 63) >> 4) << 8) + (i & 15)] = int8_t(v);   // i8_offset(row, i) - i8_offset(row, 0)
         const double eh = double(s) * double(v);
         s32 += double(x) * double(x);
         s8 += eh * eh;
         const double df = eh - double(x);
         sd += df * df;
     }
-    s32 = wave_sum_f64(s32);
-    s8 = wave_sum_f64(s8);
-    sd = wave_sum_f64(sd);
-    if (lane == 0) {
-        const double c = (sqrt(sd) + i8_gamma(d) * (sqrt(s8) + sqrt(s32))) * (1.0 + 1e-9);
-        const uint32_t cb = up_bits(c);
-        meta[0] = s;
-        meta[1] = __uint_as_float(cb);
-        atomicMax(nrm8 + 0, cb);
-        atomicMax(nrm8 + 1, up_bits(sqrt(s32)));
+    __device__ void finish(int32_t d, float* meta, uint32_t* nrm8) {
+        s32 = wave_sum_f64(s32);
+        s8 = wave_sum_f64(s8);
+        sd = wave_sum_f64(sd);
+        if (lane_id() == 0) {
+            const double c = (sqrt(sd) + i8_gamma(d) * (sqrt(s8) + sqrt(s32))) * (1.0 + 1e-9);
+            const uint32_t cb = up_bits(c);
+            meta[0] = s;
+            meta[1] = __uint_as_float(cb);
+            atomicMax(nrm8 + 0, cb);
+            atomicMax(nrm8 + 1, up_bits(sqrt(s32)));
+        }
     }
+};
+
+// One wave quantizes row `row` (d floats at e) into the tiled copy emb8, meta and nrm8.
+// The row is read in chunks of 512 floats held in registers (every load of a chunk issued
+// at once), twice: one memory latency per chunk and pass.
+__device__ inline void quantize_row_i8(const float* e, int32_t d, int8_t* emb8, int64_t row, float* meta,
+                                       uint32_t* nrm8) {
+    constexpr int kPer = 8;
+    const int lane = lane_id();
+    float m = 0.0f;
+    for (int base = 0; base < d; base += 64 * kPer) {
+        float x[kPer];
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) {
+            const int i = base + lane + 64 * j;
+            x[j] = i < d ? e[i] : 0.0f;
+        }
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) m = fmaxf(m, fabsf(x[j]));
+    }
+    I8Row q(wave_max_f(m), emb8, row, d);
+    for (int base = 0; base < d; base += 64 * kPer) {
+        float x[kPer];
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) {
+            const int i = base + lane + 64 * j;
+            x[j] = i < d ? e[i] : 0.0f;
+        }
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) {
+            const int i = base + lane + 64 * j;
+            if (i < d) q.put(i, x[j]);
+        }
+    }
+    q.finish(d, meta, nrm8);
 }
 
 }  // namespace

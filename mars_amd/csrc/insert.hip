@@ -58,11 +58,11 @@ constexpr int32_t kKnnCand = 16;            // fp16 candidates rescored per new 
 constexpr int32_t kInsertKnnRanges = 64;
 constexpr int64_t kInsertKnnNarrowRows = 2000000;
 
-// Step 1 of an insert in one launch: the staged block (rows | modalities | times |
-// episode ids | episode members | episode offsets) is scattered into the graph; each
-// new row is also converted to fp16 (round to nearest even, as k_convert_f16) and its
-// norms raise the fp16 error bounds, and quantized into the int8 copy (as k_convert_i8).
-// One wave per row, the attributes grid-stride.
+// Step 1 of an insert: the staged block (rows | modalities | times | episode ids |
+// episode members | episode offsets) is scattered into the graph; each new row is also
+// converted to fp16 (round to nearest even, as k_convert_f16) and its norms raise the fp16
+// error bounds. One wave per row, the attributes grid-stride. k_convert_i8 then quantizes
+// the new rows into the int8 copy, before they are published.
 struct StageArgs {
     const uint32_t* rows;      // n_new x d fp32 bit patterns
     const int32_t* mods;
@@ -73,9 +73,6 @@ struct StageArgs {
     float* emb;
     __half* emb16;             // null: no fp16 copy
     uint32_t* nrm;
-    int8_t* emb8;              // null: no int8 copy
-    float* meta8;
-    uint32_t* nrm8;
     int32_t* g_mods;
     float* g_ts;
     int32_t* g_ep;
@@ -89,7 +86,7 @@ struct StageArgs {
     int32_t off_at;            // num_eps + 1
 };
 
-__global__ __launch_bounds__(256) void k_stage_insert(StageArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8))) void k_stage_insert(StageArgs a) {
     __builtin_amdgcn_s_setprio(3);     // publication is latency-bound: first issue on a shared CU
     const int64_t tid = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
     const int64_t stride = int64_t(gridDim.x) * blockDim.x;
@@ -98,8 +95,22 @@ __global__ __launch_bounds__(256) void k_stage_insert(StageArgs a) {
         const uint32_t* src = a.rows + r * a.d;
         uint32_t* dst = reinterpret_cast<uint32_t*>(a.emb) + (a.n_old + r) * a.d;
         double s32 = 0.0, s16 = 0.0, sd = 0.0;
-        for (int i = lane; i < a.d; i += 64) {
-            const uint32_t bits = src[i];
+        // the row's words in registers, every load of a 768-word chunk issued at once, then
+        // the copies: one memory latency per chunk, not one per 64 words (and few enough
+        // registers that the kernel still fits beside a batched scan's workgroup)
+        constexpr int kRowWords = 12;
+        uint32_t w[kRowWords];
+        for (int base = 0; base < a.d; base += 64 * kRowWords) {
+#pragma unroll
+        for (int j = 0; j < kRowWords; ++j) {
+            const int i = base + lane + 64 * j;
+            w[j] = i < a.d ? src[i] : 0u;
+        }
+#pragma unroll
+        for (int j = 0; j < kRowWords; ++j) {
+            const int i = base + lane + 64 * j;
+            if (i >= a.d) continue;
+            const uint32_t bits = w[j];
             dst[i] = bits;
             if (a.emb16) {
                 const float x = __uint_as_float(bits);
@@ -113,10 +124,8 @@ __global__ __launch_bounds__(256) void k_stage_insert(StageArgs a) {
                 sd += df * df;
             }
         }
+        }
         if (a.emb16 && a.nrm) raise_row_norms(s32, s16, sd, a.nrm);
-        if (a.emb8)
-            quantize_row_i8(reinterpret_cast<const float*>(src), a.d, a.emb8, a.n_old + r, a.meta8 + 2 * (a.n_old + r),
-                            a.nrm8);
     }
     for (int64_t i = tid; i < a.n_new; i += stride) {
         a.g_mods[a.n_old + i] = a.mods[i];
@@ -585,12 +594,12 @@ extern "C" int mars_graph_insert(mars_graph* gh, int32_t n_new, const float* emb
     sa.mem = ep_csr ? reinterpret_cast<const int32_t*>(dev + (reinterpret_cast<char*>(p_mem) - pin)) : nullptr;
     sa.off = ep_csr ? reinterpret_cast<const int32_t*>(dev + (reinterpret_cast<char*>(p_off) - pin)) : nullptr;
     sa.emb = g.emb; sa.emb16 = g.emb16; sa.nrm = g.nrm;
-    sa.emb8 = g.emb8; sa.meta8 = g.meta8; sa.nrm8 = g.nrm8;
     sa.g_mods = g.mods; sa.g_ts = g.ts; sa.g_ep = ep_ids ? g.ep_ids : nullptr;
     sa.g_mem = ep_csr ? g.ep_mem : nullptr; sa.g_off = ep_csr ? g.ep_off : nullptr;
     sa.n_old = n_old; sa.n_new = n_new; sa.d = int32_t(D); sa.ne_new = ne_new;
     sa.mem_at = g.member_total; sa.off_at = g.num_eps + 1;
     MARS_LAUNCH(k_stage_insert, dim3(patch_grid(int64_t(n_new) * 64)), dim3(256), 0, s, sa);
+    if (g.emb8) MARS_TRY(launch_convert_i8(g.emb, n_old, n_old + n_new, g.d, g.emb8, g.meta8, g.nrm8, s));
     MARS_HIP(hipStreamSynchronize(s));
     // publish: scans, episode scope and the boost see the new nodes from here on
     double t_queryable = 0.0;

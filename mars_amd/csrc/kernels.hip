@@ -141,6 +141,7 @@ __device__ inline void block_bitonic(uint64_t* key, uint16_t* pay, int n) {
 }
 
 constexpr int kHashCap = 8192;              // LDS hash slots (power of two)
+constexpr int kRoCache = 2048;              // visit positions whose row words stay in LDS
 constexpr int kHashLimit = 6144;            // more distinct nodes: use the global arrays instead
 constexpr uint32_t kClaimHop = 0xFFu;       // hop field of a claimed, not yet visited node
 
@@ -159,6 +160,7 @@ struct FinShared {
         uint32_t hist[256];
     } u;
     uint64_t lists[kFinWaves][64];
+    int64_t ro_cache[kRoCache];          // row words of visit positions < kRoCache (also in vro)
     int s_wave[kFinWaves];
     int s_misc[8];
 };
@@ -202,8 +204,9 @@ __device__ inline int hash_find(const FinShared& sh, int32_t v) {
 }
 
 // Degrees of frontier slots [c0, c0+cn) -> sh.u.bfs.eoff / rstart; returns the edge count.
-// CACHED: the row word of each visited node was stored in a.vro when it was
-// visited (one dependent HBM load less per level).
+// CACHED: the row word of each visited node was stored in a.vro when it was visited (one
+// dependent HBM load less per level), and for the first kRoCache positions in LDS too (no
+// global load at all).
 template <bool CACHED>
 __device__ inline int frontier_edges(FinShared& sh, const FinalizeArgs& a, int c0, int cn) {
     const int tid = int(threadIdx.x);
@@ -214,7 +217,7 @@ __device__ inline int frontier_edges(FinShared& sh, const FinalizeArgs& a, int c
         deg[j] = 0; rs[j] = 0;
         if (i < cn) {
             int64_t ro;
-            if constexpr (CACHED) ro = ld_coherent(a.vro + c0 + i);
+            if constexpr (CACHED) ro = (c0 + i < kRoCache) ? sh.ro_cache[c0 + i] : ld_coherent(a.vro + c0 + i);
             else ro = a.ro[ld_coherent(a.vlist + c0 + i)];
             rs[j] = int32_t(uint32_t(ro));
             deg[j] = int32_t(ro >> 32);
@@ -352,6 +355,7 @@ __device__ int bfs_lds(FinShared& sh, const FinalizeArgs& a, int ns, int* levels
                             lkey = make_key(lf, uint32_t(nb[r]));
                         }
                         a.vro[pos] = rw[r];
+                        if (pos < kRoCache) sh.ro_cache[pos] = rw[r];
                         sh.u.bfs.hval[slot[r]] = (uint32_t(h + 1) << 16) | uint32_t(pos);
                     }
                     if (MODE == kBfsScored && rk > 0)
@@ -603,7 +607,7 @@ __global__ __launch_bounds__(kFinThreads) void k_finalize(FinalizeArgs a) {
             a.vlist[lane] = id;
             a.vhop[lane] = 0;
             a.vscore[lane] = sc;
-            a.vro[lane] = a.ro[id];
+            a.vro[lane] = sh.ro_cache[lane] = a.ro[id];
         }
         if (lane == 0) sh.s_misc[0] = ns;
     }
@@ -685,7 +689,7 @@ __device__ int multi_bfs_query(FinShared& sh, const MultiArgs& m, int j, int* le
             a.vhop[lane] = 0;
             a.vpar[lane] = -1;
             a.vscore[lane] = key_score(key);
-            a.vro[lane] = a.ro[id];
+            a.vro[lane] = sh.ro_cache[lane] = a.ro[id];
         }
         if (lane == 0) sh.s_misc[0] = ns;
     }
@@ -1012,7 +1016,7 @@ __global__ __launch_bounds__(kFinThreads) void k_cert_bfs(CertArgs a, MultiArgs 
             v.vpar[lane] = -1;
             v.vscore[lane] = key_score(seedkey);
             v.vdv[lane] = 0.0f;
-            v.vro[lane] = v.ro[id];
+            v.vro[lane] = sh.ro_cache[lane] = v.ro[id];
         }
         if (lane == 0) { sh.s_misc[0] = nsd; sh.s_misc[7] = 0; }
     }
