@@ -558,9 +558,9 @@ void batch_grid(int64_t n, int32_t q, int32_t* n_rranges, int32_t* n_qblocks, in
                 int32_t max_ranges) {
     // n_qblocks counts 64-query blocks (the layout of the partial keys) for both kernels
     const int32_t qblocks = (q + 63) / 64;
-    const bool gemm = batch_uses_gemm(q);
-    const int32_t tiles = gemm ? (q + 255) / 256 : qblocks;       // workgroups per row range
-    const int64_t align = gemm ? 256 : 16;                         // rows per tile
+    const bool gemm = batch_uses_gemm(q), rq = batch_uses_rq(q);
+    const int32_t tiles = (gemm || rq) ? (q + 255) / 256 : qblocks;   // workgroups per row range
+    const int64_t align = gemm ? 256 : 16;                            // rows per tile
     int32_t rr = std::max(8, (256 / std::max(tiles, 1)) / 8 * 8);
     const int64_t max_rr = std::max<int64_t>(1, (n + align - 1) / align);   // at least one tile per range
     if (rr > max_ranges) rr = std::max(1, max_ranges);
@@ -1481,9 +1481,7 @@ int mars_query_batch(const mars_graph* gh, mars_ctx* ch, const float* dq, int32_
     a.lambda = cfg->time_decay_lambda; a.mod_filter = cfg->modality_filter; a.k = K; a.q_plain = Q; a.self_base = -1;
     a.part = c.bpart; a.rows_per_range = rpr; a.n_rranges = nrr; a.n_qblocks = nqb;
     a.uniform_tq = std::all_of(h_tq, h_tq + Q, [&](float x) { return x == h_tq[0]; }) ? 1 : 0;
-    MARS_TRY(launch_batch_scan(a, s));
-    if (timing) MARS_HIP(hipEventRecord(c.ev[1], s));
-    MARS_TRY(launch_batch_merge(c.bpart, nrr, kp, Q, K, c.bout, s));
+    MARS_TRY(launch_batch_topk(a, K, c.bout, s, timing ? c.ev[1] : nullptr));
     if (timing) MARS_HIP(hipEventRecord(c.ev[2], s));
     std::vector<uint64_t> keys(size_t(Q) * K);
     MARS_HIP(hipMemcpyAsync(keys.data(), c.bout, keys.size() * sizeof(uint64_t), hipMemcpyDeviceToHost, s));
@@ -1623,8 +1621,7 @@ int mars_query_global_batch_knn(const mars_graph* gh, mars_ctx* ch, const float*
         b.k = kMultiCand; b.q_plain = Qg; b.self_base = knn_count > 0 ? knn_first : -1; b.part = c.bpart;
         b.rows_per_range = rpr; b.n_rranges = nrr; b.n_qblocks = nqb;
         b.uniform_tq = (Qg == 0 || std::all_of(h_tq, h_tq + Qg, [&](float x) { return x == h_tq[0]; })) ? 1 : 0;
-        MARS_TRY(launch_batch_scan(b, s));
-        MARS_TRY(launch_batch_merge(c.bpart, nrr, kp, Qt, kMultiCand, c.bout, s));
+        MARS_TRY(launch_batch_topk(b, kMultiCand, c.bout, s));
         if (timing) MARS_HIP(hipEventRecord(c.ev[1], s));
         if (knn_count > 0)
             MARS_TRY(launch_knn_rerank(g.emb, knn_first, knn_count, g.d, c.bout + int64_t(Qg) * kMultiCand,
@@ -1792,8 +1789,7 @@ int mars_graph_knn_blocks(mars_graph* gh, int32_t k, int32_t block_rows, int32_t
             a.ts = g.ts + r0; a.mods = g.mods + r0; a.lambda = 0.0f; a.mod_filter = -1; a.k = kCand; a.q_plain = 0; a.self_base = q0;
             a.part = part; a.uniform_tq = 1;
             a.rows_per_range = rpr; a.n_rranges = nrr; a.n_qblocks = (q + 63) / 64;
-            rc = launch_batch_scan(a, s);
-            if (rc == MARS_OK) rc = launch_batch_merge(part, nrr, kCand, q, kCand, cand, s);
+            rc = launch_batch_topk(a, kCand, cand, s);
             if (rc == MARS_OK)
                 rc = launch_knn_rerank(g.emb + r0 * g.d, q0, q, g.d, cand, kCand, k, dn + (r0 - lo + q0) * k, s);
         }
@@ -1851,8 +1847,7 @@ int mars_graph_knn_range(mars_graph* gh, int32_t k, int32_t first, int32_t count
         a.ts = g.ts; a.mods = g.mods; a.lambda = 0.0f; a.mod_filter = -1; a.k = kCand; a.q_plain = 0; a.self_base = q0;
         a.part = part; a.uniform_tq = 1;
         a.rows_per_range = rpr; a.n_rranges = nrr; a.n_qblocks = (q + 63) / 64;
-        rc = launch_batch_scan(a, s);
-        if (rc == MARS_OK) rc = launch_batch_merge(part, nrr, kCand, q, kCand, cand, s);
+        rc = launch_batch_topk(a, kCand, cand, s);
         if (rc == MARS_OK) rc = launch_knn_rerank(g.emb, q0, q, g.d, cand, kCand, k, dn + (q0 - first) * k, s);
     }
     if (rc == MARS_OK) {

@@ -21,6 +21,7 @@
 // ============================================================================
 #include "device.hpp"
 
+#include <algorithm>
 #include <cfloat>
 
 namespace mars {
@@ -87,7 +88,7 @@ __global__ __launch_bounds__(kBWaves * 64) void k_batch_scan(BatchArgs a) {
     for (int j = 0; j < K; ++j) list[j] = kEmptyKey;
     uint32_t own = 0u;                         // ord32 of list[K-1]'s score once the list is full
 
-    const int64_t r0 = int64_t(r_id) * a.rows_per_range;
+    const int64_t r0 = int64_t(r_id) * (a.range_stride > 0 ? a.range_stride : a.rows_per_range);
     const int64_t r1 = (a.n < r0 + a.rows_per_range) ? a.n : r0 + a.rows_per_range;
     const int64_t step = int64_t(kBWaves) * kTile;
     // row fragments of a half tile (k steps half*H .. half*H + H - 1); the next half's
@@ -231,25 +232,35 @@ __global__ __launch_bounds__(64) void k_batch_merge(const uint64_t* __restrict__
     const int qb = qi / kBQ, j = qi % kBQ;
     uint64_t list = kEmptyKey, thr = kEmptyKey;
     const int total = n_rranges * kpart;
-    for (int base = 0; base < total; base += 64) {
-        const int t = base + lane;
-        uint64_t x = kEmptyKey;
-        if (t < total) {
-            const int r = t / kpart, s = t % kpart;
-            x = part[((int64_t(qb) * n_rranges + r) * kBQ + j) * kpart + s];
+    // eight 64-key chunks loaded at a time (their loads in flight together)
+    constexpr int kMergeLd = 8;
+    for (int base = 0; base < total; base += 64 * kMergeLd) {
+        uint64_t xs[kMergeLd];
+#pragma unroll
+        for (int c = 0; c < kMergeLd; ++c) {
+            const int t = base + c * 64 + lane;
+            xs[c] = kEmptyKey;
+            if (t < total) {
+                const int r = t / kpart, s = t % kpart;
+                xs[c] = part[((int64_t(qb) * n_rranges + r) * kBQ + j) * kpart + s];
+            }
         }
-        uint64_t msk = __ballot(x < thr);
-        while (msk) {
-            const int src = __ffsll((unsigned long long)msk) - 1;
-            msk &= msk - 1;
-            const uint64_t y = __shfl(x, src);
-            if (y < thr) {
-                const uint64_t below = __ballot(list < y);
-                const int pos = __popcll(below);
-                const uint64_t up = __shfl_up(list, 1u);
-                const uint64_t v = (lane < pos) ? list : ((lane == pos) ? y : up);
-                list = (lane < k_out) ? v : kEmptyKey;
-                thr = __shfl(list, k_out - 1);
+#pragma unroll
+        for (int c = 0; c < kMergeLd; ++c) {
+            const uint64_t x = xs[c];
+            uint64_t msk = __ballot(x < thr);
+            while (msk) {
+                const int src = __ffsll((unsigned long long)msk) - 1;
+                msk &= msk - 1;
+                const uint64_t y = __shfl(x, src);
+                if (y < thr) {
+                    const uint64_t below = __ballot(list < y);
+                    const int pos = __popcll(below);
+                    const uint64_t up = __shfl_up(list, 1u);
+                    const uint64_t v = (lane < pos) ? list : ((lane == pos) ? y : up);
+                    list = (lane < k_out) ? v : kEmptyKey;
+                    thr = __shfl(list, k_out - 1);
+                }
             }
         }
     }
@@ -307,7 +318,9 @@ int launch_batch_t(const BatchArgs& a, hipStream_t s) {
 
 template <int K>
 int launch_batch_k(const BatchArgs& a, hipStream_t s) {
+    if (batch_uses_rq(a.q)) return launch_batch_rq(a, s);
     if (batch_uses_gemm(a.q)) return launch_batch_mm(a, s);
+    MARS_CHECK(a.floor_keys == nullptr, MARS_ERR_INVALID, "k_batch_scan takes no score floor");
     switch (a.d / 32) {
         case 8: return launch_batch_t<8, K>(a, s);
         case 12: return launch_batch_t<12, K>(a, s);
@@ -321,6 +334,7 @@ int launch_batch_k(const BatchArgs& a, hipStream_t s) {
 
 bool batch_dim_supported(int32_t d) { return d == 256 || d == 384 || d == 512 || d == 768; }
 bool batch_uses_gemm(int32_t q) { return q >= kGemmMinQ; }
+bool batch_uses_rq(int32_t q) { return q > kRqMaxScanQ && q < kGemmMinQ; }
 int batch_kpart(int32_t k) { return k <= 8 ? 8 : 16; }
 
 int launch_batch_scan(const BatchArgs& a, hipStream_t s) {
@@ -333,6 +347,30 @@ int launch_batch_merge(const uint64_t* part, int32_t n_rranges, int32_t kpart, i
                        uint64_t* out, hipStream_t s) {
     MARS_LAUNCH(k_batch_merge, dim3(unsigned(q)), dim3(64), 0, s, part, n_rranges, kpart, q, k_out, out);
     return MARS_OK;
+}
+
+int launch_batch_topk(BatchArgs a, int32_t k_out, uint64_t* out, hipStream_t s, hipEvent_t scanned) {
+    MARS_CHECK(k_out >= 1 && k_out <= batch_kpart(a.k), MARS_ERR_INVALID, "batched top-K: %d of %d kept", k_out,
+               batch_kpart(a.k));
+    const int32_t kp = batch_kpart(a.k);
+    a.range_stride = 0;
+    a.floor_keys = nullptr;
+    a.floor_k = 0;
+    // The floor pays where a range is long: without it a query inserts about
+    // K (1 + ln(rows / K)) rows per range (every new best of the rows seen so far), with
+    // it about rows x K / sampled rows.
+    if (batch_uses_rq(a.q) && a.rows_per_range >= 16 * kSampleRowsMin) {
+        BatchArgs b = a;
+        b.rows_per_range = std::min<int64_t>(kSampleRowsMax, a.rows_per_range / 16 / 16 * 16);
+        b.range_stride = a.rows_per_range;
+        MARS_TRY(launch_batch_scan(b, s));
+        MARS_TRY(launch_batch_merge(a.part, a.n_rranges, kp, a.q, k_out, out, s));
+        a.floor_keys = out;
+        a.floor_k = k_out;
+    }
+    MARS_TRY(launch_batch_scan(a, s));
+    if (scanned != nullptr) MARS_HIP(hipEventRecord(scanned, s));
+    return launch_batch_merge(a.part, a.n_rranges, kp, a.q, k_out, out, s);
 }
 
 int launch_knn_rerank(const float* emb, int64_t q0, int64_t nq, int32_t d, const uint64_t* cand, int32_t kc,

@@ -74,7 +74,7 @@ void k_batch_mm(BatchArgs a) {
     constexpr int d = NS * kMK;
     const int r_id = int(blockIdx.x) % a.n_rranges;
     const int q0 = (int(blockIdx.x) / a.n_rranges) * kMQ;
-    const int64_t r0 = int64_t(r_id) * a.rows_per_range;
+    const int64_t r0 = int64_t(r_id) * (a.range_stride > 0 ? a.range_stride : a.rows_per_range);
     const int64_t r1 = (a.n < r0 + a.rows_per_range) ? a.n : r0 + a.rows_per_range;
     const int64_t ntiles = r1 > r0 ? (r1 - r0 + kMR - 1) / kMR : 0;
     const bool uni = a.uniform_tq != 0;
@@ -339,6 +339,7 @@ int launch_mm_k(const BatchArgs& a, hipStream_t s) {
 int launch_batch_mm(const BatchArgs& a, hipStream_t s) {
     MARS_CHECK(a.k >= 1 && a.k <= 16, MARS_ERR_UNSUPPORTED, "batched scoring keeps at most 16 per query (asked %d)",
                a.k);
+    MARS_CHECK(a.floor_keys == nullptr, MARS_ERR_INVALID, "k_batch_mm takes no score floor");
     return a.k <= 8 ? launch_mm_k<8>(a, s) : launch_mm_k<16>(a, s);
 }
 

@@ -45,6 +45,11 @@ __device__ inline uint32_t ord32(float s) {
     return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
+// The score whose ord32 is o (o != 0; -0.0 comes back as +0.0).
+__device__ inline float ord32_inv(uint32_t o) {
+    return __uint_as_float((o & 0x80000000u) ? (o & 0x7FFFFFFFu) : ~o);
+}
+
 // Loads of data written earlier in the same kernel by other threads: served by
 // L2 (agent-coherent), never by a stale L1 line.
 template <typename T>

@@ -259,8 +259,7 @@ int insert_knn(Graph& g, int64_t first, int32_t nq, int64_t n, int32_t k, hipStr
         a.ts = g.ts; a.mods = g.mods; a.lambda = 0.0f; a.mod_filter = -1; a.k = kKnnCand;
         a.q_plain = 0; a.self_base = first + c0; a.part = g.ins_part; a.rows_per_range = rpr; a.n_rranges = nrr;
         a.n_qblocks = nqb; a.uniform_tq = 1;
-        MARS_TRY(launch_batch_scan(a, s));
-        MARS_TRY(launch_batch_merge(g.ins_part, nrr, kKnnCand, q, kKnnCand, g.ins_cand, s));
+        MARS_TRY(launch_batch_topk(a, kKnnCand, g.ins_cand, s));
         MARS_TRY(launch_knn_rerank(g.emb, first + c0, q, g.d, g.ins_cand, kKnnCand, k, g.ins_nbrs + int64_t(c0) * k, s));
     }
     return MARS_OK;

@@ -455,24 +455,43 @@ struct BatchArgs {
                              // and never its own neighbour
     uint64_t* part;          // [n_qblocks][n_rranges][64][K] keys
     int64_t rows_per_range;
+    int64_t range_stride;    // row range r starts at row r * range_stride (0: rows_per_range)
+    const uint64_t* floor_keys;  // optional: query j keeps no row below the score of key
+    int32_t floor_k;             // floor_keys[j * floor_k + floor_k - 1] (a lower bound of its
+                                 // final floor_k-th best score; an empty key is no floor)
     int32_t n_rranges;
     int32_t n_qblocks;
     int32_t uniform_tq;      // all query times equal: one decay weight per row
 };
 bool batch_dim_supported(int32_t d);
-// Batches of at least kGemmMinQ queries run the LDS-tiled MFMA kernel k_batch_mm
-// (256-query x 256-row tiles, rows_per_range a multiple of 256); smaller ones the
-// register-streaming scan, which measures faster up to a few hundred queries (1M rows:
-// Q=256 0.77 ms vs 0.85 ms; k_batch_mm wins from Q=512: 1.39 ms vs ~1.5 ms, and 2.35 ms
-// at Q=1024).
-constexpr int32_t kGemmMinQ = 512;
+// Three kernels score a batch, by its size (1M rows, d = 768, one MI355X):
+//   Q <= kRqMaxScanQ              k_batch_scan: 64-query blocks, rows streamed into
+//                                 registers (Q = 64: 311 us; Q = 128: 472 us);
+//   kRqMaxScanQ < Q < kGemmMinQ   k_batch_rq (batch_rq.hip): 256 queries per workgroup
+//                                 held in registers, 16-row tiles streamed through LDS, a
+//                                 sampled score floor (Q = 256: 820 us, the scan 1.05 ms);
+//   Q >= kGemmMinQ                k_batch_mm: 256-query x 256-row LDS tiles (the k-NN
+//                                 builder's 1024-query chunks: 2.6 ms, as k_batch_rq).
+constexpr int32_t kGemmMinQ = 1024;
+constexpr int32_t kRqMaxScanQ = 128;
 bool batch_uses_gemm(int32_t q);
+bool batch_uses_rq(int32_t q);
+int launch_batch_rq(const BatchArgs& a, hipStream_t s);
 int batch_kpart(int32_t k);  // keys per (query, row range) the scan writes
 int launch_batch_scan(const BatchArgs& a, hipStream_t s);
 // Batches of at least kGemmMinQ queries: k_batch_mm (batch_mm.hip).
 int launch_batch_mm(const BatchArgs& a, hipStream_t s);
 int launch_batch_merge(const uint64_t* part, int32_t n_rranges, int32_t kpart, int32_t q, int32_t k_out,
                        uint64_t* out, hipStream_t s);
+// Scoring plus the merge: out[j * k_out ..] = query j's k_out best keys over all rows. On
+// large corpora (ranges of at least 16 kSampleRowsMin rows) a first pass over the first
+// sixteenth of every range (kSampleRowsMin .. kSampleRowsMax rows), merged into out, gives
+// each query a floor (its k_out-th best sampled score, a lower bound of the final one), so
+// the full pass keeps only rows at or above it.
+constexpr int64_t kSampleRowsMin = 64;
+constexpr int64_t kSampleRowsMax = 1024;
+// `scanned` (optional) is recorded after the full pass, before the final merge.
+int launch_batch_topk(BatchArgs a, int32_t k_out, uint64_t* out, hipStream_t s, hipEvent_t scanned = nullptr);
 int launch_knn_rerank(const float* emb, int64_t q0, int64_t nq, int32_t d, const uint64_t* cand, int32_t kc,
                       int32_t k_out, int32_t* nbrs, hipStream_t s);
 int launch_f32_to_f16_rows(const float* in, __half* out, int64_t count, hipStream_t s);

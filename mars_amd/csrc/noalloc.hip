@@ -104,8 +104,7 @@ extern "C" int mars_query_batch_static(const mars_graph* gh, const float* d_quer
     a.lambda = cfg->time_decay_lambda; a.mod_filter = cfg->modality_filter; a.k = K; a.q_plain = Q; a.self_base = -1;
     a.part = part; a.rows_per_range = rpr; a.n_rranges = nrr; a.n_qblocks = nqb;
     a.uniform_tq = uniform_tq ? 1 : 0;
-    MARS_TRY(launch_batch_scan(a, s));
-    MARS_TRY(launch_batch_merge(part, nrr, kp, Q, K, out, s));
+    MARS_TRY(launch_batch_topk(a, K, out, s));
     const int32_t n = Q * K;
     MARS_LAUNCH(k_keys_to_results, dim3(unsigned((n + 255) / 256)), dim3(256), 0, s, out, n, d_ids, d_scores);
     return MARS_OK;

@@ -1,0 +1,96 @@
+"""GPU parity of the batched scoring kernel for 129 .. 1023 queries (k_batch_rq: 256
+queries per workgroup in registers, 16-row tiles through LDS, a sampled score floor).
+
+- against the fp32 oracle's top-K (the bar of tests/parity.py: scores within 2e-3 of the
+  scale, id sets equal up to near-ties) at every supported width, both list sizes, with
+  and without a modality filter, one or per-query times, ragged row counts;
+- bit for bit against k_batch_scan (batches of at most 128 queries), which computes the
+  same MFMA products in the same order: the same queries scored as one batch of 256 and
+  as two batches of 128 give the same ids and scores;
+- with a corpus large enough that each row range is sampled for the score floor;
+- the neighbour-search form (plain dot products, the node itself excluded) against the
+  exact CPU k-NN.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import mars_amd
+from mars_amd import RetrievalConfig, corpus
+
+from parity import LAM, T_Q, Dev, batch_check, random_graph
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("d,q,k,filt,uniform", [(256, 129, 5, -1, True), (384, 200, 16, 1, False),
+                                                 (512, 256, 8, 2, True), (768, 300, 10, -1, False),
+                                                 (768, 520, 16, 0, True), (256, 1000, 3, -1, True)])
+def test_rq_against_oracle(d, q, k, filt, uniform, rng):
+    n = 3001                                   # ragged: not a multiple of the 16-row tile
+    emb, mods, ts, row, col, _ = random_graph(rng, n, d)
+    dev = Dev(emb, mods, ts, row, col, fp16=True)
+    try:
+        qn = rng.choice(n, q, replace=False)
+        tq = np.float32(T_Q) if uniform else rng.uniform(300, 600, q).astype(np.float32)
+        batch_check(dev, qn, RetrievalConfig(top_k=k, time_decay_lambda=LAM, modality_filter=filt), tq, emb)
+    finally:
+        dev.close()
+
+
+@pytest.mark.parametrize("k,filt,uniform", [(10, -1, True), (5, 1, False)])
+def test_rq_equals_scan_bit_for_bit(k, filt, uniform, rng):
+    n, d = 20000, 768
+    emb, mods, ts, row, col, _ = random_graph(rng, n, d)
+    dev = Dev(emb, mods, ts, row, col, fp16=True)
+    qs = np.ascontiguousarray(emb[rng.choice(n, 256, replace=False)])
+    tq = np.full(256, T_Q, np.float32) if uniform else rng.uniform(300, 600, 256).astype(np.float32)
+    cfg = RetrievalConfig(top_k=k, time_decay_lambda=LAM, modality_filter=filt)
+    buf = mars_amd.DeviceBuffer.from_array(qs)
+    try:
+        ids, sc = mars_amd.query_batch(dev.dg, dev.ctx, buf.ptr, 256, tq, cfg)                  # k_batch_rq
+        i0, s0 = mars_amd.query_batch(dev.dg, dev.ctx, buf.ptr, 128, tq[:128], cfg)            # k_batch_scan
+        i1, s1 = mars_amd.query_batch(dev.dg, dev.ctx, buf.ptr + 128 * d * 4, 128, tq[128:], cfg)
+    finally:
+        buf.free()
+        dev.close()
+    np.testing.assert_array_equal(ids, np.concatenate([i0, i1]))
+    np.testing.assert_array_equal(sc, np.concatenate([s0, s1]))
+
+
+def test_rq_sampled_floor(rng):
+    """120K rows, 600 queries (three 256-query groups over 80 row ranges of 1,504 rows):
+    each range's first sixteenth is scored first and sets the queries' floors."""
+    n, d = 120_000, 256
+    emb = rng.standard_normal((n, d)).astype(np.float32)
+    emb /= np.linalg.norm(emb, axis=1, keepdims=True)
+    mods = rng.integers(0, 3, size=n).astype(np.int32)
+    ts = rng.uniform(0, 600, size=n).astype(np.float32)
+    dev = Dev(emb, mods, ts, None, None, fp16=True)
+    try:
+        qn = rng.choice(n, 600, replace=False)
+        ids, _ = batch_check(dev, qn[:600], RetrievalConfig(top_k=10, time_decay_lambda=LAM), T_Q, emb)
+        assert np.all(ids[:, 0] >= 0)
+        batch_check(dev, qn[:300], RetrievalConfig(top_k=16, time_decay_lambda=LAM, modality_filter=1), T_Q, emb)
+    finally:
+        dev.close()
+
+
+def test_rq_neighbour_search(rng):
+    """graph_knn_range over 300 nodes runs one batch of 300 plain queries (self excluded)."""
+    n, d = 2500, 512
+    emb, mods, ts, _, _, _ = random_graph(rng, n, d)
+    dev = Dev(emb, mods, ts, None, None, fp16=True)
+    try:
+        got = mars_amd.graph_knn_range(dev.dg, 8, 100, 300)
+    finally:
+        dev.close()
+    want, sims = corpus.knn_cpu(emb, 8)
+    s = emb[100:400] @ emb.T
+    for i in range(300):
+        s[i, 100 + i] = -np.inf
+        if not np.array_equal(got[i], want[100 + i]):
+            for j in set(got[i].tolist()) ^ set(want[100 + i].tolist()):
+                assert abs(s[i, j] - sims[100 + i, 7]) <= 1e-3, (i, j)
+    assert np.all(got != np.arange(100, 400)[:, None])

@@ -254,15 +254,15 @@ def test_batch_parity_shapes(dev10k, corpus_10k, q, k, filt, rng):
 @pytest.mark.parametrize("d,k,filt,uniform", [(256, 5, -1, False), (384, 16, 1, True), (512, 8, 2, False),
                                                (768, 3, -1, True)])
 def test_batch_tiled_widths(d, k, filt, uniform, rng):
-    """520 queries run the 256-query x 256-row tiled kernel: every supported width, both
-    list sizes (K <= 8 and K <= 16), ragged row tiles (2,600 rows), filters and per-query
-    times, against the oracle's top-K."""
+    """1,030 queries run the 256-query x 256-row tiled kernel (k_batch_mm): every supported
+    width, both list sizes (K <= 8 and K <= 16), ragged row tiles (2,600 rows), filters and
+    per-query times, against the oracle's top-K."""
     n = 2600
     emb, mods, ts, row, col, _ = random_graph(rng, n, d)
     dev = Dev(emb, mods, ts, row, col, fp16=True)
     try:
-        qn = rng.choice(n, 520, replace=False)
-        tq = np.float32(T_Q) if uniform else rng.uniform(300, 600, 520).astype(np.float32)
+        qn = rng.choice(n, 1030, replace=False)
+        tq = np.float32(T_Q) if uniform else rng.uniform(300, 600, 1030).astype(np.float32)
         batch_check(dev, qn, RetrievalConfig(top_k=k, time_decay_lambda=LAM, modality_filter=filt), tq, emb)
     finally:
         dev.close()
