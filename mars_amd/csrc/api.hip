@@ -559,7 +559,8 @@ void batch_grid(int64_t n, int32_t q, int32_t* n_rranges, int32_t* n_qblocks, in
     // n_qblocks counts 64-query blocks (the layout of the partial keys) for both kernels
     const int32_t qblocks = (q + 63) / 64;
     const bool gemm = batch_uses_gemm(q), rq = batch_uses_rq(q);
-    const int32_t tiles = (gemm || rq) ? (q + 255) / 256 : qblocks;   // workgroups per row range
+    const int32_t wgq = gemm ? 256 : (rq ? 64 * batch_rq_tiles(q) : 64);   // queries per workgroup
+    const int32_t tiles = (q + wgq - 1) / wgq;                             // workgroups per row range
     const int64_t align = gemm ? 256 : 16;                            // rows per tile
     int32_t rr = std::max(8, (256 / std::max(tiles, 1)) / 8 * 8);
     const int64_t max_rr = std::max<int64_t>(1, (n + align - 1) / align);   // at least one tile per range

@@ -335,6 +335,7 @@ int launch_batch_k(const BatchArgs& a, hipStream_t s) {
 bool batch_dim_supported(int32_t d) { return d == 256 || d == 384 || d == 512 || d == 768; }
 bool batch_uses_gemm(int32_t q) { return q >= kGemmMinQ; }
 bool batch_uses_rq(int32_t q) { return q > kRqMaxScanQ && q < kGemmMinQ; }
+int batch_rq_tiles(int32_t q) { return q <= 128 ? 2 : 4; }
 int batch_kpart(int32_t k) { return k <= 8 ? 8 : 16; }
 
 int launch_batch_scan(const BatchArgs& a, hipStream_t s) {

@@ -1,17 +1,16 @@
 // ============================================================================
 //  batch_rq.hip — k_batch_rq: batched scoring with the queries held in registers,
-//  for batches of more than 128 queries (256 per workgroup, one corpus pass each).
+//  for batches of 65 .. 1023 queries (128 or 256 per workgroup, one corpus pass each).
 //
 //  A query tile of 256 fp16 queries x d does not fit in LDS (384 KiB at d = 768), but
 //  it fits in the register files of one CU: each of the four waves (one per SIMD, the
-//  whole 512-register file) holds 64 queries as MFMA A fragments for the whole kernel
-//  (NS x 4 fragments of 16 bytes per lane, 384 registers at d = 768). Only the corpus
-//  moves: 16-row tiles stream from HBM straight into LDS (global_load_lds_dwordx4, each
-//  wave loading a quarter of every tile, whole rows contiguous), five tile buffers deep,
-//  and all four waves read every tile's B fragments from LDS. Each corpus row is read
-//  from HBM once per 256 queries and the CU takes in nothing else, so the kernel runs at
-//  the corpus stream's rate while the MFMAs (16 x 16 x 32 f16, 96 per wave and tile at
-//  d = 768) keep pace with it.
+//  whole 512-register file) holds 16 QT queries as MFMA A fragments for the whole kernel
+//  (NS x QT fragments of 16 bytes per lane: 384 registers at d = 768 and QT = 4). Only
+//  the corpus moves: 16-row tiles stream from HBM straight into LDS
+//  (global_load_lds_dwordx4, each wave loading a quarter of every tile, whole rows
+//  contiguous), five tile buffers deep, and all four waves read every tile's B fragments
+//  from LDS. Each corpus row is read from HBM once per workgroup's 64 QT queries, and the
+//  CU takes in nothing else.
 //
 //  Tile layout in LDS: row r's 16-byte piece p sits in slot r * P + (p ^ (r & 15)),
 //  P = d / 8 pieces per row. A B-fragment read (lanes 16 g .. 16 g + 15: rows 0 .. 15,
@@ -19,10 +18,13 @@
 //
 //  Scores: the same MFMA, operands and k order as k_batch_scan (queries the A operand,
 //  rows the B operand, k-steps 0 .. NS - 1 accumulated in order from zero), so every raw
-//  score is bit-identical to that kernel's; the selection is its epilogue (a per-wave LDS
-//  transpose after which lane j owns query j, the decay, filter and per-query K-th-score
-//  bound, register lists). Output: K keys per (query, row range), the layout k_batch_merge
-//  reads.
+//  score is bit-identical to that kernel's, and so is every fused score. Selection: a tile
+//  first goes through a test in the MFMA layout (a lane holds one row's scores for 4 QT
+//  queries) against each query's floor (from the sampled pass of launch_batch_topk); only
+//  a tile with a score at or above its floor goes through k_batch_scan's epilogue (a
+//  per-wave LDS transpose after which lane j owns query j, the decay, filter and bound,
+//  register lists), inserting only the rows that reach the bound, one per lane and
+//  round. Output: K keys per (query, row range), the layout k_batch_merge reads.
 //
 //  Reference analogue: wmma_mma_similarity_kernel / wmma_similarity_kernel
 //  (src/wmma_similarity.cu:55-138), which score one query and are never called.
@@ -34,19 +36,18 @@
 namespace mars {
 namespace {
 
-constexpr int kRQ = 256;       // queries per workgroup (64 per wave)
-constexpr int kRWaves = 4;
+constexpr int kRWaves = 4;     // one per SIMD; each holds QT 16-query MFMA tiles
 constexpr int kRThreads = kRWaves * 64;
 constexpr int kRRows = 16;     // corpus rows per tile
 constexpr int kRBuf = 5;       // tile buffers: tiles i + 1 .. i + 4 load while tile i computes
 
-template <int NS>
+template <int NS, int QT>
 struct RqLds {
     u32x4 tile[kRBuf][kRRows * NS * 4];          // 16 rows x d / 8 pieces, swizzled
     uint32_t side[kRBuf][kRWaves][64];           // per wave: lanes 0-15 the rows' timestamps, 16-31 modalities
-    float stage[kRWaves][kRRows][65];            // per-wave score tile (+1: bank spread)
+    float stage[kRWaves][kRRows][16 * QT + 1];   // per-wave score tile (+1: bank spread)
     float wrow[kRWaves][kRRows];                 // per wave: the tile rows' weights (or timestamps)
-    float floorv[kRWaves][64];                   // per wave: its queries' floors (-inf: none)
+    float floorv[kRWaves][16 * QT];              // per wave: its queries' floors (-inf: none)
 };
 
 // s_waitcnt immediates (gfx9 encoding: vmcnt[3:0] and [15:14], expcnt[6:4], lgkmcnt[11:8])
@@ -70,10 +71,12 @@ __device__ __attribute__((always_inline)) inline void dma4(const void* g, uint32
     __builtin_amdgcn_global_load_lds(g, lds, 4, 0, 0);
 }
 
-template <int NS, int K>
+// QT: 16-query MFMA tiles per wave (2 or 4: 128 or 256 queries per workgroup).
+template <int NS, int K, int QT>
 __global__ __launch_bounds__(kRThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void k_batch_rq(BatchArgs a) {
-    __shared__ __attribute__((aligned(16))) RqLds<NS> sh;
+    __shared__ __attribute__((aligned(16))) RqLds<NS, QT> sh;
+    constexpr int WQ = 16 * QT;                  // queries per wave
     constexpr int P = NS * 4;                    // 16-byte pieces per row
     constexpr int kLd = NS / 4;                  // tile loads per wave (64 slots each)
     static_assert(NS % 4 == 0 && P % 16 == 0, "tile layout");
@@ -83,7 +86,7 @@ void k_batch_rq(BatchArgs a) {
     constexpr int d = NS * 32;
     const int r_id = int(blockIdx.x) % a.n_rranges;
     const int g = int(blockIdx.x) / a.n_rranges;                  // 256-query group
-    const int qb = g * (kRQ / 64) + wave;                         // this wave's 64-query block
+    const int wq0 = (g * kRWaves + wave) * WQ;                    // this wave's first query
     const int64_t r0 = int64_t(r_id) * (a.range_stride > 0 ? a.range_stride : a.rows_per_range);
     const int64_t r1 = (a.n < r0 + a.rows_per_range) ? a.n : r0 + a.rows_per_range;
     const int64_t ntiles = r1 > r0 ? (r1 - r0 + kRRows - 1) / kRRows : 0;
@@ -129,12 +132,12 @@ void k_batch_rq(BatchArgs a) {
         for (int b = 0; b < kRBuf - 1; ++b) issue_tile(b, b);
     }
 
-    // The wave's 64 queries as A fragments: af[qt][ks] = query qb*64 + qt*16 + m,
+    // The wave's WQ queries as A fragments: af[qt][ks] = query wq0 + qt*16 + m,
     // halves ks*32 + kg*8 .. +7 (zero past the batch).
-    f16x8 af[4][NS];
+    f16x8 af[QT][NS];
 #pragma unroll
-    for (int qt = 0; qt < 4; ++qt) {
-        const int qrow = qb * 64 + qt * 16 + m;
+    for (int qt = 0; qt < QT; ++qt) {
+        const int qrow = wq0 + qt * 16 + m;
         const bool ok = qrow < a.q;
         const u32x4* qp = reinterpret_cast<const u32x4*>(a.qh + int64_t(ok ? qrow : 0) * d + kg * 8);
 #pragma unroll
@@ -144,10 +147,10 @@ void k_batch_rq(BatchArgs a) {
         }
     }
 
-    // lane j owns query qb*64 + j
-    const int myq = qb * 64 + lane;
-    const bool qvalid = myq < a.q;
-    const bool wave_live = qb * 64 < a.q;        // uniform: the wave has queries to score
+    // lane j < WQ owns query wq0 + j
+    const int myq = wq0 + lane;
+    const bool qvalid = lane < WQ && myq < a.q;
+    const bool wave_live = wq0 < a.q;            // uniform: the wave has queries to score
     const float tq = qvalid ? a.tq[myq] : 0.0f;
     const bool uni = a.uniform_tq != 0;
     const float tq0 = a.tq[0];
@@ -161,7 +164,7 @@ void k_batch_rq(BatchArgs a) {
         const uint64_t fk = a.floor_keys[int64_t(myq) * a.floor_k + a.floor_k - 1];
         if (fk != kEmptyKey) own = ord32(key_score(fk));
     }
-    sh.floorv[wave][lane] = own != 0u ? ord32_inv(own) : -INFINITY;   // read after the loop's first barrier
+    if (lane < WQ) sh.floorv[wave][lane] = own != 0u ? ord32_inv(own) : -INFINITY;   // read after the loop's first barrier
     const bool prefilter = uni || a.lambda >= 0.0f;
 
     // B-fragment slots: k-step ks reads piece 4 ks + kg of row m, i.e. slot
@@ -182,9 +185,9 @@ void k_batch_rq(BatchArgs a) {
         const int64_t t0 = r0 + i * kRRows;
         if (wave_live) {
             const u32x4* tb = sh.tile[b];
-            f32x4 acc[4];
+            f32x4 acc[QT];
 #pragma unroll
-            for (int qt = 0; qt < 4; ++qt) acc[qt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            for (int qt = 0; qt < QT; ++qt) acc[qt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
             f16x8 bf[3];
             bf[0] = __builtin_bit_cast(f16x8, tb[boff[0]]);
             bf[1] = __builtin_bit_cast(f16x8, tb[boff[1]]);
@@ -193,7 +196,7 @@ void k_batch_rq(BatchArgs a) {
                 if (ks + 2 < NS)
                     bf[(ks + 2) % 3] = __builtin_bit_cast(f16x8, tb[boff[(ks + 2) & 3] + 16 * ((ks + 2) >> 2)]);
 #pragma unroll
-                for (int qt = 0; qt < 4; ++qt)
+                for (int qt = 0; qt < QT; ++qt)
                     acc[qt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[qt][ks], bf[ks % 3], acc[qt], 0, 0, 0);
                 __builtin_amdgcn_sched_barrier(0);
             }
@@ -212,14 +215,14 @@ void k_batch_rq(BatchArgs a) {
             if (prefilter) {
                 bool hit = false;
 #pragma unroll
-                for (int qt = 0; qt < 4; ++qt) {
+                for (int qt = 0; qt < QT; ++qt) {
                     const f32x4 fl = *reinterpret_cast<const f32x4*>(&sh.floorv[wave][qt * 16 + 4 * kg]);
 #pragma unroll
                     for (int v = 0; v < 4; ++v) {
                         const float x = acc[qt][v];
                         float sv = uni ? x * w_m : (x < 0.0f ? 0.0f : x);
                         sv = keep_m ? sv : -FLT_MAX;
-                        sv = (qb * 64 + qt * 16 + 4 * kg + v >= a.q_plain) ? x : sv;
+                        sv = (wq0 + qt * 16 + 4 * kg + v >= a.q_plain) ? x : sv;
                         hit = hit || !(sv < fl[v]);
                     }
                 }
@@ -230,7 +233,7 @@ void k_batch_rq(BatchArgs a) {
             const uint32_t keepm = uint32_t(__ballot(keep_m && lane < kRRows));
             // C[query = qt*16 + 4*kg + v][row = m]
 #pragma unroll
-            for (int qt = 0; qt < 4; ++qt)
+            for (int qt = 0; qt < QT; ++qt)
 #pragma unroll
                 for (int v = 0; v < 4; ++v) sh.stage[wave][m][qt * 16 + 4 * kg + v] = acc[qt][v];
             float w[kRRows];                     // wave-uniform (read in uniform control flow)
@@ -288,17 +291,23 @@ void k_batch_rq(BatchArgs a) {
     // workgroup ends and its LDS is handed to another
     __builtin_amdgcn_s_waitcnt(rq_wait_vm(0));
     if (qvalid) {
-        uint64_t* out = a.part + ((int64_t(qb) * a.n_rranges + r_id) * 64 + lane) * K;
+        uint64_t* out = a.part + ((int64_t(myq / 64) * a.n_rranges + r_id) * 64 + myq % 64) * K;
 #pragma unroll
         for (int j = 0; j < K; ++j) out[j] = list[j];
     }
 }
 
+template <int NS, int K, int QT>
+int launch_rq_q(const BatchArgs& a, hipStream_t s) {
+    constexpr int wgq = kRWaves * 16 * QT;       // queries per workgroup
+    const unsigned grid = unsigned(a.n_rranges * ((a.q + wgq - 1) / wgq));
+    MARS_LAUNCH((k_batch_rq<NS, K, QT>), dim3(grid), dim3(kRThreads), 0, s, a);
+    return MARS_OK;
+}
+
 template <int NS, int K>
 int launch_rq_t(const BatchArgs& a, hipStream_t s) {
-    const unsigned grid = unsigned(a.n_rranges * ((a.q + kRQ - 1) / kRQ));
-    MARS_LAUNCH((k_batch_rq<NS, K>), dim3(grid), dim3(kRThreads), 0, s, a);
-    return MARS_OK;
+    return batch_rq_tiles(a.q) == 2 ? launch_rq_q<NS, K, 2>(a, s) : launch_rq_q<NS, K, 4>(a, s);
 }
 
 template <int K>

@@ -466,16 +466,20 @@ struct BatchArgs {
 bool batch_dim_supported(int32_t d);
 // Three kernels score a batch, by its size (1M rows, d = 768, one MI355X):
 //   Q <= kRqMaxScanQ              k_batch_scan: 64-query blocks, rows streamed into
-//                                 registers (Q = 64: 311 us; Q = 128: 472 us);
-//   kRqMaxScanQ < Q < kGemmMinQ   k_batch_rq (batch_rq.hip): 256 queries per workgroup
-//                                 held in registers, 16-row tiles streamed through LDS, a
-//                                 sampled score floor (Q = 256: 820 us, the scan 1.05 ms);
+//                                 registers (Q = 64: 313 us);
+//   kRqMaxScanQ < Q < kGemmMinQ   k_batch_rq (batch_rq.hip): the queries held in registers
+//                                 (128 or 256 per workgroup, batch_rq_tiles x 16 per wave),
+//                                 16-row tiles streamed through LDS, a sampled score floor
+//                                 (Q = 256: 628 us, 774 us with the scan);
 //   Q >= kGemmMinQ                k_batch_mm: 256-query x 256-row LDS tiles (the k-NN
-//                                 builder's 1024-query chunks: 2.6 ms, as k_batch_rq).
+//                                 builder's 1024-query chunks).
+// (With 64 queries per workgroup k_batch_rq measured slower than the scan: 445 against
+// 408 us on a random 1M corpus.)
 constexpr int32_t kGemmMinQ = 1024;
-constexpr int32_t kRqMaxScanQ = 128;
+constexpr int32_t kRqMaxScanQ = 64;
 bool batch_uses_gemm(int32_t q);
 bool batch_uses_rq(int32_t q);
+int batch_rq_tiles(int32_t q);   // 16-query MFMA tiles per k_batch_rq wave: 2 or 4
 int launch_batch_rq(const BatchArgs& a, hipStream_t s);
 int batch_kpart(int32_t k);  // keys per (query, row range) the scan writes
 int launch_batch_scan(const BatchArgs& a, hipStream_t s);

@@ -1,12 +1,12 @@
-"""GPU parity of the batched scoring kernel for 129 .. 1023 queries (k_batch_rq: 256
+"""GPU parity of the batched scoring kernel for 65 .. 1023 queries (k_batch_rq: 128 or 256
 queries per workgroup in registers, 16-row tiles through LDS, a sampled score floor).
 
 - against the fp32 oracle's top-K (the bar of tests/parity.py: scores within 2e-3 of the
   scale, id sets equal up to near-ties) at every supported width, both list sizes, with
   and without a modality filter, one or per-query times, ragged row counts;
-- bit for bit against k_batch_scan (batches of at most 128 queries), which computes the
-  same MFMA products in the same order: the same queries scored as one batch of 256 and
-  as two batches of 128 give the same ids and scores;
+- bit for bit against k_batch_scan (batches of at most 64 queries), which computes the
+  same MFMA products in the same order: the same queries scored in one batch (256, 128 or
+  96 queries) and in batches of 32 give the same ids and scores;
 - with a corpus large enough that each row range is sampled for the score floor;
 - the neighbour-search form (plain dot products, the node itself excluded) against the
   exact CPU k-NN.
@@ -26,7 +26,9 @@ pytestmark = pytest.mark.gpu
 
 @pytest.mark.parametrize("d,q,k,filt,uniform", [(256, 129, 5, -1, True), (384, 200, 16, 1, False),
                                                  (512, 256, 8, 2, True), (768, 300, 10, -1, False),
-                                                 (768, 520, 16, 0, True), (256, 1000, 3, -1, True)])
+                                                 (768, 520, 16, 0, True), (256, 1000, 3, -1, True),
+                                                 (768, 65, 10, -1, True), (384, 96, 16, 2, False),
+                                                 (512, 100, 8, -1, False), (768, 128, 16, 1, True)])
 def test_rq_against_oracle(d, q, k, filt, uniform, rng):
     n = 3001                                   # ragged: not a multiple of the 16-row tile
     emb, mods, ts, row, col, _ = random_graph(rng, n, d)
@@ -39,24 +41,25 @@ def test_rq_against_oracle(d, q, k, filt, uniform, rng):
         dev.close()
 
 
-@pytest.mark.parametrize("k,filt,uniform", [(10, -1, True), (5, 1, False)])
-def test_rq_equals_scan_bit_for_bit(k, filt, uniform, rng):
+@pytest.mark.parametrize("q,k,filt,uniform", [(256, 10, -1, True), (256, 5, 1, False), (128, 16, 2, True),
+                                               (96, 10, -1, False)])
+def test_rq_equals_scan_bit_for_bit(q, k, filt, uniform, rng):
     n, d = 20000, 768
     emb, mods, ts, row, col, _ = random_graph(rng, n, d)
     dev = Dev(emb, mods, ts, row, col, fp16=True)
-    qs = np.ascontiguousarray(emb[rng.choice(n, 256, replace=False)])
-    tq = np.full(256, T_Q, np.float32) if uniform else rng.uniform(300, 600, 256).astype(np.float32)
+    qs = np.ascontiguousarray(emb[rng.choice(n, q, replace=False)])
+    tq = np.full(q, T_Q, np.float32) if uniform else rng.uniform(300, 600, q).astype(np.float32)
     cfg = RetrievalConfig(top_k=k, time_decay_lambda=LAM, modality_filter=filt)
     buf = mars_amd.DeviceBuffer.from_array(qs)
     try:
-        ids, sc = mars_amd.query_batch(dev.dg, dev.ctx, buf.ptr, 256, tq, cfg)                  # k_batch_rq
-        i0, s0 = mars_amd.query_batch(dev.dg, dev.ctx, buf.ptr, 128, tq[:128], cfg)            # k_batch_scan
-        i1, s1 = mars_amd.query_batch(dev.dg, dev.ctx, buf.ptr + 128 * d * 4, 128, tq[128:], cfg)
+        ids, sc = mars_amd.query_batch(dev.dg, dev.ctx, buf.ptr, q, tq, cfg)                  # k_batch_rq
+        parts = [mars_amd.query_batch(dev.dg, dev.ctx, buf.ptr + j * d * 4, 32, tq[j:j + 32], cfg)
+                 for j in range(0, q, 32)]                                                   # k_batch_scan
     finally:
         buf.free()
         dev.close()
-    np.testing.assert_array_equal(ids, np.concatenate([i0, i1]))
-    np.testing.assert_array_equal(sc, np.concatenate([s0, s1]))
+    np.testing.assert_array_equal(ids, np.concatenate([p[0] for p in parts]))
+    np.testing.assert_array_equal(sc, np.concatenate([p[1] for p in parts]))
 
 
 def test_rq_sampled_floor(rng):
