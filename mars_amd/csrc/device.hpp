@@ -446,11 +446,13 @@ struct I8Row {
 };
 
 // One wave quantizes row `row` (d floats at e) into the tiled copy emb8, meta and nrm8.
-// The row is read in chunks of 512 floats held in registers (every load of a chunk issued
+// The row is read in chunks of 64 kPer floats held in registers (every load of a chunk issued
 // at once), twice: one memory latency per chunk and pass.
+// (kPer: floats per lane and chunk; every kPer visits each lane's elements in the same
+// order, lane + 64 j, so it does not change the sums.)
+template <int kPer = 8>
 __device__ inline void quantize_row_i8(const float* e, int32_t d, int8_t* emb8, int64_t row, float* meta,
                                        uint32_t* nrm8) {
-    constexpr int kPer = 8;
     const int lane = lane_id();
     float m = 0.0f;
     for (int base = 0; base < d; base += 64 * kPer) {

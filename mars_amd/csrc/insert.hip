@@ -61,8 +61,8 @@ constexpr int64_t kInsertKnnNarrowRows = 2000000;
 // Step 1 of an insert: the staged block (rows | modalities | times | episode ids |
 // episode members | episode offsets) is scattered into the graph; each new row is also
 // converted to fp16 (round to nearest even, as k_convert_f16) and its norms raise the fp16
-// error bounds. One wave per row, the attributes grid-stride. k_convert_i8 then quantizes
-// the new rows into the int8 copy, before they are published.
+// error bounds, and, when the graph holds the int8 copy, quantized into it by the same wave
+// (quantize_row_i8, from the staged row). One wave per row, the attributes grid-stride.
 struct StageArgs {
     const uint32_t* rows;      // n_new x d fp32 bit patterns
     const int32_t* mods;
@@ -73,6 +73,9 @@ struct StageArgs {
     float* emb;
     __half* emb16;             // null: no fp16 copy
     uint32_t* nrm;
+    int8_t* emb8;              // null: no int8 copy
+    float* meta8;
+    uint32_t* nrm8;
     int32_t* g_mods;
     float* g_ts;
     int32_t* g_ep;
@@ -126,6 +129,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8))) void k
         }
         }
         if (a.emb16 && a.nrm) raise_row_norms(s32, s16, sd, a.nrm);
+        if (a.emb8) {
+            const int64_t row = a.n_old + r;
+            quantize_row_i8<4>(reinterpret_cast<const float*>(src), a.d, a.emb8, row, a.meta8 + 2 * row, a.nrm8);
+        }
     }
     for (int64_t i = tid; i < a.n_new; i += stride) {
         a.g_mods[a.n_old + i] = a.mods[i];
@@ -593,12 +600,12 @@ extern "C" int mars_graph_insert(mars_graph* gh, int32_t n_new, const float* emb
     sa.mem = ep_csr ? reinterpret_cast<const int32_t*>(dev + (reinterpret_cast<char*>(p_mem) - pin)) : nullptr;
     sa.off = ep_csr ? reinterpret_cast<const int32_t*>(dev + (reinterpret_cast<char*>(p_off) - pin)) : nullptr;
     sa.emb = g.emb; sa.emb16 = g.emb16; sa.nrm = g.nrm;
+    sa.emb8 = g.emb8; sa.meta8 = g.meta8; sa.nrm8 = g.nrm8;
     sa.g_mods = g.mods; sa.g_ts = g.ts; sa.g_ep = ep_ids ? g.ep_ids : nullptr;
     sa.g_mem = ep_csr ? g.ep_mem : nullptr; sa.g_off = ep_csr ? g.ep_off : nullptr;
     sa.n_old = n_old; sa.n_new = n_new; sa.d = int32_t(D); sa.ne_new = ne_new;
     sa.mem_at = g.member_total; sa.off_at = g.num_eps + 1;
     MARS_LAUNCH(k_stage_insert, dim3(patch_grid(int64_t(n_new) * 64)), dim3(256), 0, s, sa);
-    if (g.emb8) MARS_TRY(launch_convert_i8(g.emb, n_old, n_old + n_new, g.d, g.emb8, g.meta8, g.nrm8, s));
     MARS_HIP(hipStreamSynchronize(s));
     // publish: scans, episode scope and the boost see the new nodes from here on
     double t_queryable = 0.0;

@@ -80,6 +80,35 @@ def test_rq_sampled_floor(rng):
         dev.close()
 
 
+def test_rq_sampled_floor_sparse_filter_and_neighbours(rng):
+    """140K rows, 300 queries (two 256-query groups over 128 row ranges of 1,104 rows,
+    sampled): a modality filter that keeps 1 row in 2,000 (the sampled rows hold fewer than
+    K of them, so the floors are -FLT_MAX scores), and the neighbour-search form (plain dot
+    products, self excluded) over the same sampled ranges."""
+    n, d = 140_000, 256
+    emb = rng.standard_normal((n, d)).astype(np.float32)
+    emb /= np.linalg.norm(emb, axis=1, keepdims=True)
+    mods = (rng.random(n) < 0.0005).astype(np.int32)
+    ts = rng.uniform(0, 600, size=n).astype(np.float32)
+    dev = Dev(emb, mods, ts, None, None, fp16=True)
+    try:
+        qn = rng.choice(n, 300, replace=False)
+        batch_check(dev, qn, RetrievalConfig(top_k=10, time_decay_lambda=LAM, modality_filter=1), T_Q, emb)
+        got = mars_amd.graph_knn_range(dev.dg, 8, 5000, 300)
+    finally:
+        dev.close()
+    q = emb[5000:5300]
+    s = q @ emb.T
+    s[np.arange(300), 5000 + np.arange(300)] = -np.inf
+    want = np.argsort(-s, axis=1, kind="stable")[:, :8]
+    for i in range(300):
+        if not np.array_equal(np.sort(got[i]), np.sort(want[i])):
+            kth = s[i, want[i, 7]]
+            for j in set(got[i].tolist()) ^ set(want[i].tolist()):
+                assert abs(s[i, j] - kth) <= 1e-3, (i, j)
+    assert np.all(got != 5000 + np.arange(300)[:, None])
+
+
 def test_rq_neighbour_search(rng):
     """graph_knn_range over 300 nodes runs one batch of 300 plain queries (self excluded)."""
     n, d = 2500, 512
