@@ -85,7 +85,7 @@ void k_batch_rq(BatchArgs a) {
     const int m = lane & 15, kg = lane >> 4;
     constexpr int d = NS * 32;
     const int r_id = int(blockIdx.x) % a.n_rranges;
-    const int g = int(blockIdx.x) / a.n_rranges;                  // 256-query group
+    const int g = int(blockIdx.x) / a.n_rranges;                  // the workgroup's group of 64 QT queries
     const int wq0 = (g * kRWaves + wave) * WQ;                    // this wave's first query
     const int64_t r0 = int64_t(r_id) * (a.range_stride > 0 ? a.range_stride : a.rows_per_range);
     const int64_t r1 = (a.n < r0 + a.rows_per_range) ? a.n : r0 + a.rows_per_range;
@@ -229,60 +229,60 @@ void k_batch_rq(BatchArgs a) {
                 any = __ballot(hit && m < nr) != 0;
             }
             if (any) {
-            if (lane < kRRows) sh.wrow[wave][lane] = w_m;
-            const uint32_t keepm = uint32_t(__ballot(keep_m && lane < kRRows));
-            // C[query = qt*16 + 4*kg + v][row = m]
+                if (lane < kRRows) sh.wrow[wave][lane] = w_m;
+                const uint32_t keepm = uint32_t(__ballot(keep_m && lane < kRRows));
+                // C[query = qt*16 + 4*kg + v][row = m]
 #pragma unroll
-            for (int qt = 0; qt < QT; ++qt)
+                for (int qt = 0; qt < QT; ++qt)
 #pragma unroll
-                for (int v = 0; v < 4; ++v) sh.stage[wave][m][qt * 16 + 4 * kg + v] = acc[qt][v];
-            float w[kRRows];                     // wave-uniform (read in uniform control flow)
+                    for (int v = 0; v < 4; ++v) sh.stage[wave][m][qt * 16 + 4 * kg + v] = acc[qt][v];
+                float w[kRRows];                     // wave-uniform (read in uniform control flow)
 #pragma unroll
-            for (int j = 0; j < kRRows; ++j)
-                w[j] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w_m), j));
-            rq_wave_lds_sync();
-            // The fused score of row j for this lane's query: dot * w (k_batch_scan's
-            // arithmetic), filtered rows -FLT_MAX, neighbour searches the plain dot.
-            // (Branch-free per lane: the uni / lambda tests are wave-uniform.)
-            auto fuse = [&](float x, float wj, bool keep) {
-                float sv = x;
-                if (uni) sv = x * wj;
-                else if (a.lambda != 0.0f) sv = x * expf(-a.lambda * fmaxf(0.0f, tq - wj));
-                sv = keep ? sv : -FLT_MAX;
-                return plain ? x : sv;
-            };
-            if (qvalid) {
-                // The rows that may enter the list: not below its K-th score (a float test
-                // that never rejects a row the key test below accepts; NaN passes to it).
-                const float bound_f = own != 0u ? ord32_inv(own) : -INFINITY;
-                uint32_t pass = 0u;
+                for (int j = 0; j < kRRows; ++j)
+                    w[j] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w_m), j));
+                rq_wave_lds_sync();
+                // The fused score of row j for this lane's query: dot * w (k_batch_scan's
+                // arithmetic), filtered rows -FLT_MAX, neighbour searches the plain dot.
+                // (Branch-free per lane: the uni / lambda tests are wave-uniform.)
+                auto fuse = [&](float x, float wj, bool keep) {
+                    float sv = x;
+                    if (uni) sv = x * wj;
+                    else if (a.lambda != 0.0f) sv = x * expf(-a.lambda * fmaxf(0.0f, tq - wj));
+                    sv = keep ? sv : -FLT_MAX;
+                    return plain ? x : sv;
+                };
+                if (qvalid) {
+                    // The rows that may enter the list: not below its K-th score (a float test
+                    // that never rejects a row the key test below accepts; NaN passes to it).
+                    const float bound_f = own != 0u ? ord32_inv(own) : -INFINITY;
+                    uint32_t pass = 0u;
 #pragma unroll
-                for (int j = 0; j < kRRows; ++j) {
-                    const float sv = fuse(sh.stage[wave][j][lane], w[j], (keepm >> j) & 1u);
-                    pass |= uint32_t(!(sv < bound_f)) << j;
-                }
-                pass &= 0xFFFFu >> (kRRows - nr);
-                if (self_id >= t0 && self_id < t0 + kRRows) pass &= ~(1u << int(self_id - t0));
-                // one passing row per lane and round (a round costs what one insertion
-                // does; most tiles need one or none), its score again from the stage (the
-                // same operations, so the same bits)
-                while (pass) {
-                    const int j = __builtin_ctz(pass);
-                    pass &= pass - 1u;
-                    const float sv = fuse(sh.stage[wave][j][lane], sh.wrow[wave][j], (keepm >> j) & 1u);
-                    if (ord32(sv) >= own) {
-                        const uint64_t key = make_key(sv, uint32_t(t0 + j));
-                        if (key < list[K - 1]) {
-                            reg_insert<K>(list, key);
-                            if (list[K - 1] != kEmptyKey) {
-                                const uint32_t o = ord32(key_score(list[K - 1]));
-                                own = o > own ? o : own;
+                    for (int j = 0; j < kRRows; ++j) {
+                        const float sv = fuse(sh.stage[wave][j][lane], w[j], (keepm >> j) & 1u);
+                        pass |= uint32_t(!(sv < bound_f)) << j;
+                    }
+                    pass &= 0xFFFFu >> (kRRows - nr);
+                    if (self_id >= t0 && self_id < t0 + kRRows) pass &= ~(1u << int(self_id - t0));
+                    // one passing row per lane and round (a round costs what one insertion
+                    // does; most tiles need one or none), its score again from the stage (the
+                    // same operations, so the same bits)
+                    while (pass) {
+                        const int j = __builtin_ctz(pass);
+                        pass &= pass - 1u;
+                        const float sv = fuse(sh.stage[wave][j][lane], sh.wrow[wave][j], (keepm >> j) & 1u);
+                        if (ord32(sv) >= own) {
+                            const uint64_t key = make_key(sv, uint32_t(t0 + j));
+                            if (key < list[K - 1]) {
+                                reg_insert<K>(list, key);
+                                if (list[K - 1] != kEmptyKey) {
+                                    const uint32_t o = ord32(key_score(list[K - 1]));
+                                    own = o > own ? o : own;
+                                }
                             }
                         }
                     }
                 }
-            }
-            rq_wave_lds_sync();
+                rq_wave_lds_sync();
             }
         }
         b = b == kRBuf - 1 ? 0 : b + 1;
