@@ -463,7 +463,10 @@ def main() -> int:
     mars_amd.upload_episode_csr(dg, csr)
     ctx = mars_amd.create_query_context(N + M, D, 64, flags=0)
 
-    nq = max(args.steps, args.stream_queries) + args.warmup
+    batch_sizes = [int(x) for x in str(args.batch_q).split(",") if int(x) > 0]
+    # every batched pass reads B consecutive query vectors, so the set holds at least the
+    # largest batch
+    nq = max(args.steps, args.stream_queries, *batch_sizes, 0) + args.warmup
     qnodes = corpus.pick_queries(c.modalities, nq, seed=args.query_seed)
     dq = mars_amd.DeviceBuffer.from_array(c.embeddings[qnodes])
 
@@ -630,13 +633,14 @@ def main() -> int:
         # ---- batched global scoring on MFMA fp16 tiles (--batch-q 0 skips it). The scoring time
         # is the GPU time from the batch's first scoring launch to the end of its full corpus
         # pass (with more than 128 queries: the sampled floor pass and its merge included).
-        for B in [int(x) for x in str(args.batch_q).split(",") if int(x) > 0]:
+        for B in batch_sizes:
             ctx.timing = True
             reps = 30
             bl, bk = [], []
             for r in range(reps + 3):
                 st = mars_amd.RetrievalStats()
-                mars_amd.query_batch(dg, ctx, dq.ptr + ((W + r * B) % max(1, S - B)) * D * 4, B, corpus.QUERY_TIME,
+                assert B <= nq
+                mars_amd.query_batch(dg, ctx, dq.ptr + ((W + r * B) % (nq - B + 1)) * D * 4, B, corpus.QUERY_TIME,
                                      RetrievalConfig(top_k=K, time_decay_lambda=corpus.DECAY_LAMBDA), st)
                 if r >= 3:
                     bl.append(st.wall_us)

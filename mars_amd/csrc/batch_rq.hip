@@ -188,17 +188,45 @@ void k_batch_rq(BatchArgs a) {
             f32x4 acc[QT];
 #pragma unroll
             for (int qt = 0; qt < QT; ++qt) acc[qt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            auto bfrag = [&](int ks) { return __builtin_bit_cast(f16x8, tb[boff[ks & 3] + 16 * (ks >> 2)]); };
+            if constexpr (QT == 4) {
+            // B fragments two k-steps ahead in three registers (the 256-query form has no
+            // room for a fourth: at 512 VGPRs it ran at half speed)
             f16x8 bf[3];
-            bf[0] = __builtin_bit_cast(f16x8, tb[boff[0]]);
-            bf[1] = __builtin_bit_cast(f16x8, tb[boff[1]]);
+            bf[0] = bfrag(0);
+            bf[1] = bfrag(1);
 #pragma unroll
             for (int ks = 0; ks < NS; ++ks) {
-                if (ks + 2 < NS)
-                    bf[(ks + 2) % 3] = __builtin_bit_cast(f16x8, tb[boff[(ks + 2) & 3] + 16 * ((ks + 2) >> 2)]);
+                if (ks + 2 < NS) bf[(ks + 2) % 3] = bfrag(ks + 2);
 #pragma unroll
                 for (int qt = 0; qt < QT; ++qt)
                     acc[qt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[qt][ks], bf[ks % 3], acc[qt], 0, 0, 0);
                 __builtin_amdgcn_sched_barrier(0);
+            }
+            } else {
+            // B fragments in pairs of k-steps, two pairs of registers: pair p + 1 is read
+            // right after pair p's first MFMA, so each pair's reads have the 4 QT - 1 MFMAs
+            // of a pair to land (every wait for them also waits for everything issued before)
+            f16x8 bf[2][2];
+            bf[0][0] = bfrag(0);
+            bf[0][1] = bfrag(1);
+#pragma unroll
+            for (int p = 0; p < NS / 2; ++p) {
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+#pragma unroll
+                    for (int qt = 0; qt < QT; ++qt) {
+                        acc[qt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[qt][2 * p + j], bf[p & 1][j], acc[qt], 0, 0, 0);
+                        if (j == 0 && qt == 0 && p + 1 < NS / 2) {
+                            __builtin_amdgcn_sched_barrier(0);
+                            bf[(p + 1) & 1][0] = bfrag(2 * p + 2);
+                            bf[(p + 1) & 1][1] = bfrag(2 * p + 3);
+                            __builtin_amdgcn_sched_barrier(0);
+                        }
+                    }
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
             }
             // Row m of the score tile (this lane's row): its weight (decay at the one query
             // time, else its timestamp) and filter flag.
