@@ -488,11 +488,12 @@ int launch_batch_mm(const BatchArgs& a, hipStream_t s);
 int launch_batch_merge(const uint64_t* part, int32_t n_rranges, int32_t kpart, int32_t q, int32_t k_out,
                        uint64_t* out, hipStream_t s);
 // Scoring plus the merge: out[j * k_out ..] = query j's k_out best keys over all rows. On
-// large corpora (ranges of at least 16 kSampleRowsMin rows) a first pass over the first
-// sixteenth of every range (kSampleRowsMin .. kSampleRowsMax rows), merged into out, gives
+// large corpora (ranges of at least kSampleDiv kSampleRowsMin rows) a first pass over the
+// first 1 / kSampleDiv of every range (kSampleRowsMin .. kSampleRowsMax rows), merged into out, gives
 // each query a floor (its k_out-th best sampled score, a lower bound of the final one), so
 // the full pass keeps only rows at or above it.
-constexpr int64_t kSampleRowsMin = 64;
+constexpr int64_t kSampleDiv = 32;      // 1/16 of each range measured 5% slower at 1M rows
+constexpr int64_t kSampleRowsMin = 32;
 constexpr int64_t kSampleRowsMax = 1024;
 // `scanned` (optional) is recorded after the full pass, before the final merge.
 int launch_batch_topk(BatchArgs a, int32_t k_out, uint64_t* out, hipStream_t s, hipEvent_t scanned = nullptr);

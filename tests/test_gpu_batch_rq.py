@@ -64,7 +64,7 @@ def test_rq_equals_scan_bit_for_bit(q, k, filt, uniform, rng):
 
 def test_rq_sampled_floor(rng):
     """120K rows, 600 queries (three 256-query groups over 80 row ranges of 1,504 rows):
-    each range's first sixteenth is scored first and sets the queries' floors."""
+    each range's first thirty-second (32 rows) is scored first and sets the queries' floors."""
     n, d = 120_000, 256
     emb = rng.standard_normal((n, d)).astype(np.float32)
     emb /= np.linalg.norm(emb, axis=1, keepdims=True)
