@@ -358,6 +358,206 @@ def parity_check(oracle, first, og, c, qnodes, t_q, gcfg, ocfg, refs, answers):
             "bar": "ids and hops exact, scores within 1e-5 * max(|s|, BFS-carried w * sum|e q|), near-ties allowed"}
 
 
+def build_graph(mars_amd, corpus, n, D, seed, knn_k=8, threads=16):
+    """A resident graph of the benchmark generator: fp32 rows with fp16 and int8 copies, the
+    NSN graph (intra-episode pairs + knn_k-NN from the GPU builder), episode ids and CSR."""
+    c = corpus.make_corpus(n, D, seed=seed, threads=threads)
+    g = mars_amd.MemoryGraph(n, D, None, None, c.embeddings, c.modalities, c.timestamps)
+    dg = mars_amd.upload_to_device(g)
+    mars_amd.upload_fp16_embeddings(dg)
+    mars_amd.upload_int8_embeddings(dg)
+    knn = mars_amd.graph_knn(dg, knn_k) if knn_k > 0 else np.empty((n, 0), np.int32)
+    corpus.nsn_graph(c, knn, threads=threads)
+    mars_amd.set_csr(dg, c.row_offsets, c.col_indices)
+    mars_amd.upload_episode_ids(dg, c.episode_ids)
+    csr = mars_amd.build_episode_csr(c.episode_ids, n)
+    mars_amd.upload_episode_csr(dg, csr)
+    return c, dg, csr
+
+
+def episode_cfgs(RetrievalConfig, RetrievalScope, RetrievalConfigC, corpus, c, csr, nodes, K, max_results=-1):
+    """Episode-scoped configurations (one per query node) as a C array."""
+    off = csr.ep_csr_offsets
+    arr = (RetrievalConfigC * len(nodes))()
+    for i, node in enumerate(nodes):
+        ep = int(c.episode_ids[node])
+        arr[i] = RetrievalConfig(top_k=K, time_decay_lambda=corpus.DECAY_LAMBDA, max_results_returned=max_results,
+                                 retrieval_scope=RetrievalScope.EpisodeScoped, query_episode_id=ep,
+                                 query_episode_member_begin=int(off[ep]),
+                                 query_episode_member_count=int(off[ep + 1] - off[ep])).to_c()
+    return arr
+
+
+def bench_queries(lib, check, dg, ctx, dq_ptr, D, count, t_q, cfgs, n_cfg, K):
+    """mars_bench_queries: `count` Q=1 queries on consecutive device vectors; per query the
+    host wall latency (steady_clock inside the library) and, with the context's timing
+    flag, the scan and post-scan kernel times (HIP events on the query stream)."""
+    lat = np.zeros(count, np.float64)
+    kern = np.zeros(count, np.float32)
+    bfs = np.zeros(count, np.float32)
+    nres = np.zeros(count, np.int32)
+    check(lib.mars_bench_queries(dg.handle, ctx.handle, C.c_void_p(dq_ptr), D, count, C.c_float(t_q), cfgs, n_cfg,
+                                 C.c_void_p(lat.ctypes.data), C.c_void_p(kern.ctypes.data),
+                                 C.c_void_p(bfs.ctypes.data), C.c_void_p(nres.ctypes.data)), "mars_bench_queries")
+    assert np.all(nres == K), "every query must return K results"
+    return lat, kern, bfs
+
+
+def config_100k_pass(args, mars_amd, corpus, lib, check, evict, pctl):
+    """N=100,000 D=768: 10,000 Q=1 queries each global (certified and fp32 paths) and
+    episode-scoped; scan GB/s both as measured back to back (the rows stay in the 256 MB
+    Infinity Cache: cache-resident) and with a 1.5 GB read of another graph's rows between
+    queries (evicted: L2 and Infinity Cache refilled from HBM); the CPU oracle on the same
+    global queries."""
+    from mars_amd import RetrievalConfig, RetrievalScope
+    from mars_amd._lib import RetrievalConfigC
+    n, D, K, S, W = 100_000, args.dim, 10, args.queries_100k, 200
+    t = time.time()
+    c, dg, csr = build_graph(mars_amd, corpus, n, D, args.seed)
+    log(f"[100K] corpus + upload + 8-NN + NSN graph ({len(c.col_indices)} edges): {time.time() - t:.1f}s")
+    ctx = mars_amd.create_query_context(n, D, 64, flags=0)
+    qnodes = corpus.pick_queries(c.modalities, W + S, seed=args.query_seed)
+    dq = mars_amd.DeviceBuffer.from_array(np.ascontiguousarray(c.embeddings[qnodes]))
+    gcfg = RetrievalConfig(top_k=K, bfs_max_hops=2, time_decay_lambda=corpus.DECAY_LAMBDA, bfs_score_decay=0.5)
+    g1 = gcfg.to_c()
+    ec = episode_cfgs(RetrievalConfig, RetrievalScope, RetrievalConfigC, corpus, c, csr, qnodes, K)
+    ec_t = (RetrievalConfigC * S).from_buffer(ec, W * C.sizeof(RetrievalConfigC))
+    bytes_i8, bytes_f32 = n * D + 12 * n, n * D * 4 + 4 * n
+    out = {"num_nodes": n, "dim": D, "queries": S, "num_edges": int(len(c.col_indices)),
+           "nsn_graph": "intra-episode pairs + 8-NN"}
+    try:
+        def one(tag, cfgs, n_cfg, certified, nbytes):
+            ctx.certified = certified
+            ctx.timing = False
+            bench_queries(lib, check, dg, ctx, dq.ptr, D, W, corpus.QUERY_TIME, cfgs if n_cfg == 1 else ec,
+                          1 if n_cfg == 1 else W, K)
+            t0 = time.time()
+            lat, _, _ = bench_queries(lib, check, dg, ctx, dq.ptr + W * D * 4, D, S, corpus.QUERY_TIME, cfgs,
+                                      n_cfg, K)
+            wall = time.time() - t0
+            ctx.timing = True
+            _, kern, rest = bench_queries(lib, check, dg, ctx, dq.ptr + W * D * 4, D, min(S, 2000),
+                                          corpus.QUERY_TIME, cfgs, min(n_cfg, 2000), K)
+            r = dict(p50_us=pctl(lat, .5), p99_us=pctl(lat, .99), qps=S / wall, kernel_mean_us=float(kern.mean()),
+                     after_scan_mean_us=float(rest.mean()))
+            if nbytes:
+                r.update(scan_gbs_cache_resident=nbytes / float(kern.mean()) / 1e3)
+                # the same scan with the caches refilled from HBM: a 1.5 GB read before each query
+                ev = []
+                for i in range(200):
+                    evict()
+                    st = mars_amd.RetrievalStats()
+                    mars_amd.query_memory_fast_device(dg, ctx, dq.ptr + (W + i) * D * 4, corpus.QUERY_TIME, gcfg, st)
+                    ev.append(st.gpu_ms_similarity * 1e3)
+                r.update(scan_kernel_evicted_mean_us=float(np.mean(ev)),
+                         scan_gbs_evicted=nbytes / float(np.mean(ev)) / 1e3, scan_bytes_per_launch=nbytes)
+            ctx.timing = False
+            ctx.certified = False
+            log(f"[100K] {tag}: p50 {r['p50_us']:.1f} us p99 {r['p99_us']:.1f} us; kernel mean {r['kernel_mean_us']:.1f} us"
+                + (f" ({r['scan_gbs_cache_resident']:.0f} GB/s cache-resident, {r['scan_gbs_evicted']:.0f} GB/s "
+                   f"evicted)" if nbytes else ""))
+            return r
+
+        out["global_certified"] = one("global certified (int8 candidates)", C.pointer(g1), 1, True, bytes_i8)
+        out["global_fp32"] = one("global fp32", C.pointer(g1), 1, False, bytes_f32)
+        out["episode"] = one("episode-scoped", ec_t, S, False, 0)
+        out["cache_note"] = (f"cache-resident: queries back to back (int8 copy {bytes_i8 / 1e6:.0f} MB, fp32 rows "
+                             f"{bytes_f32 / 1e6:.0f} MB against the 256 MB Infinity Cache); evicted: a 1.5 GB kernel "
+                             f"read of another graph's rows before each timed query")
+        if not args.no_cpu:
+            import oracle
+            answers = capture_answers(mars_amd, dg, ctx, dq, W, D, min(50, S), corpus.QUERY_TIME, gcfg)
+            og = oracle.make_graph(c.embeddings, c.modalities, c.timestamps, c.row_offsets, c.col_indices)
+            ocfg = oracle.config(K, 2, corpus.DECAY_LAMBDA, 0.5)
+            nc = min(args.cpu_queries_100k, S)
+            cl, refs = [], []
+            for i, node in enumerate(qnodes[W:W + nc]):
+                t0 = time.perf_counter()
+                r = oracle.query(og, c.embeddings[node], corpus.QUERY_TIME, ocfg)
+                cl.append((time.perf_counter() - t0) * 1e6)
+                if i < len(answers):
+                    refs.append(r)
+            out["parity_checked"] = parity_check(oracle, W, og, c, qnodes, corpus.QUERY_TIME, gcfg, ocfg, refs,
+                                                 answers)
+            out["cpu_baseline"] = {"p50_us": pctl(cl, .5), "p99_us": pctl(cl, .99), "queries": nc,
+                                   "cores": oracle.lib.oracle_num_threads(), "kind": "port"}
+            log(f"[100K] cpu oracle ({out['cpu_baseline']['cores']} threads, {nc} queries): p50 {pctl(cl, .5):.0f} us "
+                f"p99 {pctl(cl, .99):.0f} us; parity {out['parity_checked']['queries'] - out['parity_checked']['mismatched']}"
+                f"/{out['parity_checked']['queries']}")
+    finally:
+        dq.free()
+        mars_amd.destroy_query_context(ctx)
+        mars_amd.free_device(dg)
+    return out
+
+
+def config_10k_recall_pass(args, mars_amd, corpus, pctl):
+    """N=10,000 D=768: TEXT+AUDIO recall in the top 15 over 1,000 IMAGE queries (K=10, 15
+    results; global depth-2 BFS and episode scope), from the GPU's answers and from the
+    oracle's on the same queries."""
+    from mars_amd import RetrievalConfig, RetrievalScope
+    n, D, K, Q = 10_000, args.dim, 10, 1000
+    c, dg, csr = build_graph(mars_amd, corpus, n, D, args.seed)
+    ctx = mars_amd.create_query_context(n, D, 64, flags=0)
+    nodes = corpus.pick_queries(c.modalities, Q, seed=args.seed)
+    dq = mars_amd.DeviceBuffer.from_array(np.ascontiguousarray(c.embeddings[nodes]))
+    off, mem = csr.ep_csr_offsets, csr.ep_csr_members
+    gcfg = RetrievalConfig(top_k=K, bfs_max_hops=2, time_decay_lambda=corpus.DECAY_LAMBDA, bfs_score_decay=0.5,
+                           max_results_returned=15)
+    out = {"num_nodes": n, "queries": Q, "metric": "hit@15: the query's episode has a TEXT and an AUDIO node among "
+           "the 15 results (bench_kids_sweep.cu:65-82); recall@15: fraction of the episode's 6 TEXT and AUDIO "
+           "members among them"}
+    per = {"global": [], "episode": []}
+    lat = {"global": [], "episode": []}
+    ctx.certified = True
+    try:
+        for i, node in enumerate(nodes):
+            ep = int(c.episode_ids[node])
+            members = mem[off[ep]:off[ep + 1]]
+            ecfg = RetrievalConfig(top_k=K, time_decay_lambda=corpus.DECAY_LAMBDA, max_results_returned=15,
+                                   retrieval_scope=RetrievalScope.EpisodeScoped, query_episode_id=ep,
+                                   query_episode_member_begin=int(off[ep]),
+                                   query_episode_member_count=int(off[ep + 1] - off[ep]))
+            for scope, cfg in (("global", gcfg), ("episode", ecfg)):
+                st = mars_amd.RetrievalStats()
+                res = mars_amd.query_memory_fast_device(dg, ctx, dq.ptr + i * D * 4, corpus.QUERY_TIME, cfg, st)
+                ids = [r.node_id for r in res]
+                per[scope].append((ids, ep, members))
+                lat[scope].append(st.wall_us)
+        for scope in per:
+            hit = [corpus.cross_modal_hit(ids, c.modalities, c.episode_ids, ep) for ids, ep, _ in per[scope]]
+            rec = [corpus.cross_modal_recall(ids, c.modalities, c.episode_ids, ep, m) for ids, ep, m in per[scope]]
+            out[scope] = {"hit_at_15": float(np.mean(hit)), "recall_at_15": float(np.mean(rec)),
+                          "p50_us": pctl(lat[scope], .5), "p99_us": pctl(lat[scope], .99)}
+        if not args.no_cpu:
+            import oracle
+            og = oracle.make_graph(c.embeddings, c.modalities, c.timestamps, c.row_offsets, c.col_indices,
+                                   c.episode_ids)
+            oh, orc, same = [], [], 0
+            for i, node in enumerate(nodes):
+                ids, ep, members = per["global"][i]
+                ref = oracle.query(og, c.embeddings[node], corpus.QUERY_TIME,
+                                   oracle.config(K, 2, corpus.DECAY_LAMBDA, 0.5, -1, 15))
+                want = [w[0] for w in ref["results"]]
+                same += set(want) == set(ids)
+                oh.append(corpus.cross_modal_hit(want, c.modalities, c.episode_ids, ep))
+                orc.append(corpus.cross_modal_recall(want, c.modalities, c.episode_ids, ep, members))
+            out["global"]["oracle_hit_at_15"] = float(np.mean(oh))
+            out["global"]["oracle_recall_at_15"] = float(np.mean(orc))
+            out["global"]["same_result_sets"] = same
+        log(f"[10K] {Q} IMAGE queries, top 15: global hit {out['global']['hit_at_15']:.4f} recall "
+            f"{out['global']['recall_at_15']:.4f}" +
+            (f" (oracle {out['global']['oracle_hit_at_15']:.4f} / {out['global']['oracle_recall_at_15']:.4f}, "
+             f"same result sets {out['global']['same_result_sets']}/{Q})" if not args.no_cpu else "") +
+            f"; episode scope hit {out['episode']['hit_at_15']:.4f} recall {out['episode']['recall_at_15']:.4f}")
+    finally:
+        ctx.certified = False
+        dq.free()
+        mars_amd.destroy_query_context(ctx)
+        mars_amd.free_device(dg)
+    return out
+
+
 def pctl(v, p):
     v = np.sort(np.asarray(v, np.float64))
     return float(v[int(p * (len(v) - 1))]) if len(v) else 0.0
@@ -401,6 +601,12 @@ def main() -> int:
                     help="also drive the JSON-line engine server with this many ADDs and 500 QUERYs")
     ap.add_argument("--checkpoint-dir", default="",
                     help="also time a MARS v1 checkpoint of the device graph to this directory and its reload")
+    ap.add_argument("--queries-100k", type=int, default=10000,
+                    help="Q=1 queries per path of the N=100,000 pass (0: no such pass)")
+    ap.add_argument("--cpu-queries-100k", type=int, default=10000,
+                    help="global queries the CPU oracle answers in the N=100,000 pass")
+    ap.add_argument("--no-recall-10k", action="store_true",
+                    help="skip the N=10,000 TEXT+AUDIO recall pass")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU; --gpus above 1 is not supported here "
@@ -814,11 +1020,21 @@ def main() -> int:
         log(f"cpu oracle (1 thread, {len(c1)} queries): p50 {pctl(c1, .5):.0f} us; host {model}, nproc {os.cpu_count()}")
     dq.free()
     mars_amd.destroy_query_context(ctx)
+    if not args.profile_only and args.dim == 768:
+        # the two smaller configurations of the same generator, each on its own graph
+        if args.queries_100k > 0:
+            evict = lambda: mars_amd.read_pattern(dg, mars_amd.READ_FRAGMENTS, reps=1)
+            res["config_100k"] = config_100k_pass(args, mars_amd, corpus, lib, check, evict, pctl)
+        if not args.no_recall_10k:
+            res["config_10k_recall"] = config_10k_recall_pass(args, mars_amd, corpus, pctl)
     mars_amd.free_device(dg)
     del c, full
     if host_rows:
         host_rows.free()
     print(json.dumps(res), flush=True)
+    if res.get("config_100k", {}).get("parity_checked", {}).get("mismatched", 0):
+        log("PARITY FAILURE at N=100,000")
+        return 3
     if res.get("parity_checked", {}).get("mismatched", 0):
         log(f"PARITY FAILURE: {res['parity_checked']['mismatched']} of {res['parity_checked']['queries']} GPU answers "
             f"differ from the oracle's")

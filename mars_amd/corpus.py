@@ -125,3 +125,28 @@ def nsn_edges(modalities: np.ndarray, k: int = 6, p: float = 0.15, phases: int =
     check(lib.mars_nsn_edges(n, _p(mods) if n else None, int(k), float(p), int(phases), _p(row), _p(col),
                              len(col), C.byref(ne)), "mars_nsn_edges")
     return row, col[: ne.value].copy()
+
+
+MOD_TEXT, MOD_AUDIO, MOD_IMAGE = 0, 1, 2
+
+
+def cross_modal_hit(ids, modalities: np.ndarray, episode_ids: np.ndarray, query_episode: int, top: int = 15) -> bool:
+    """episode_cross_modal_hit (demos/embodied_scene/bench_kids_sweep.cu:65-82): among the
+    first `top` result ids, the query's episode has a TEXT node and an AUDIO node."""
+    has = set()
+    for nid in list(ids)[:top]:
+        nid = int(nid)
+        if 0 <= nid < len(episode_ids) and int(episode_ids[nid]) == query_episode:
+            has.add(int(modalities[nid]))
+    return MOD_TEXT in has and MOD_AUDIO in has
+
+
+def cross_modal_recall(ids, modalities: np.ndarray, episode_ids: np.ndarray, query_episode: int,
+                       members: np.ndarray, top: int = 15) -> float:
+    """Fraction of the query episode's TEXT and AUDIO members (`members`: the episode's node
+    ids) found among the first `top` result ids."""
+    want = {int(m) for m in members if int(modalities[m]) in (MOD_TEXT, MOD_AUDIO)}
+    if not want:
+        return 1.0
+    got = {int(x) for x in list(ids)[:top]}
+    return len(want & got) / len(want)

@@ -38,10 +38,14 @@ constexpr int32_t kTargetWg = 512;
 constexpr int32_t kTargetWgF16 = 512;
 constexpr int32_t kTargetWgI8 = kScan8MaxLists;
 
+// Widths with an exact-rescoring kernel (k_cert_bfs<QF32<d / 64>>): the certified query
+// runs only at these; any other width is answered by the fp32 scan.
+bool cert_dim_supported(int32_t d) { return d == 256 || d == 384 || d == 512 || d == 768 || d == 1024; }
+
 // The certified query scans the int8 copy when there is one (d <= 1024: the exact
 // rescoring's QF32 layouts), else the fp16 copy.
 bool cert_uses_int8(const Graph& g) {
-    return g.emb8 && g.meta8 && g.nrm8 && scan8_dim_supported(g.d) && g.d <= 1024;
+    return g.emb8 && g.meta8 && g.nrm8 && scan8_dim_supported(g.d) && cert_dim_supported(g.d);
 }
 
 int ensure_device(int* dev) {
@@ -385,7 +389,7 @@ int query_impl(const mars_graph* gh, mars_ctx* ch, const float* h_q, const float
     const float lam = cfg->time_decay_lambda;
     const bool boost_on = g.ep_ids && cfg->query_episode_id >= 0 && cfg->episode_same_boost > 0.0f;
     const bool cert = !scoped && !fp16 && (c.flags & MARS_CTX_CERTIFIED) &&
-                      (cert_uses_int8(g) || (g.emb16 && g.nrm && g.d % 128 == 0 && g.d <= 1024)) &&
+                      cert_dim_supported(g.d) && (cert_uses_int8(g) || (g.emb16 && g.nrm)) &&
                       !boost_on && lam >= 0.0f && lam <= FLT_MAX && hops < 255;
     if (cert) {
         bool answered = false;
@@ -1570,7 +1574,7 @@ int mars_query_global_batch_knn(const mars_graph* gh, mars_ctx* ch, const float*
     std::vector<int32_t> q1;                    // queries the Q=1 path answers
     // A lone global query (no neighbour search) is cheaper on the Q=1 certified path: its
     // fp16 scan beats the MFMA kernel with one query lane of 64, and the results are the same.
-    const bool lone = batched && Q == 1 && knn_count == 0 && !fp16 && g.d % 128 == 0 && g.d <= 1024;
+    const bool lone = batched && Q == 1 && knn_count == 0 && !fp16 && cert_dim_supported(g.d);
     const int32_t Qg = (batched && !lone) ? Q : 0;   // global queries in the shared scan
     const int32_t Qt = Qg + knn_count;               // + k-NN queries (plain dot products)
     if (!batched) {

@@ -211,6 +211,7 @@ int dispatch_rows(const A& a, hipStream_t s) {
             case 6: return L<float, QF32<6>>::run(a, s);
             case 8: return L<float, QF32<8>>::run(a, s);
             case 12: return L<float, QF32<12>>::run(a, s);
+            case 16: return L<float, QF32<16>>::run(a, s);
             default: break;
         }
     }

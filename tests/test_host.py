@@ -204,3 +204,25 @@ def test_no_silent_cpu_path_without_gpu():
     desc, keep = _desc()
     h = C.c_void_p()
     assert _lib.lib.mars_graph_create(C.byref(desc), C.byref(h)) in (-2, -6)
+
+
+def test_cross_modal_metrics():
+    """hit@15 / recall@15 of the recall pass (bench_kids_sweep.cu:65-82's hit rule) on a
+    hand-made episode: members 10-19 (TEXT 10-12, AUDIO 13-15, IMAGE 16-19)."""
+    mods = np.array([2] * 10 + [0, 0, 0, 1, 1, 1, 2, 2, 2, 2] + [0, 1] * 5, np.int32)
+    ep = np.array([0] * 10 + [1] * 10 + [2] * 10, np.int32)
+    members = np.arange(10, 20)
+    # TEXT and AUDIO of episode 1, plus other episodes' TEXT / AUDIO (not counted)
+    ids = [16, 20, 21, 10, 13, 11]
+    assert corpus.cross_modal_hit(ids, mods, ep, 1)
+    assert corpus.cross_modal_recall(ids, mods, ep, 1, members) == 3 / 6
+    # only TEXT of the episode: no hit
+    assert not corpus.cross_modal_hit([10, 11, 21, 16], mods, ep, 1)
+    # the AUDIO node beyond the first `top` results does not count
+    assert not corpus.cross_modal_hit([10] + [0] * 14 + [13], mods, ep, 1)
+    assert corpus.cross_modal_hit([10] + [0] * 13 + [13], mods, ep, 1)
+    assert corpus.cross_modal_recall([10] + [0] * 14 + [13], mods, ep, 1, members) == 1 / 6
+    # the whole episode: hit and recall 1
+    assert corpus.cross_modal_recall(list(members), mods, ep, 1, members) == 1.0
+    # out-of-range ids are skipped
+    assert not corpus.cross_modal_hit([-1, 99, 10], mods, ep, 1)
