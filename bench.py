@@ -33,20 +33,33 @@ def log(*a):
     print("[bench]", *a, file=sys.stderr, flush=True)
 
 
+def source_digest(name: str) -> str:
+    """First 16 hex digits of the SHA-256 of a kernel source file of the package."""
+    import hashlib
+    return hashlib.sha256((ROOT / "mars_amd" / "csrc" / name).read_bytes()).hexdigest()[:16]
+
+
 def scan_traffic(n: int, d: int, profile: str = "k_scan_fp32_1M.md"):
-    """HBM bytes per k_scan launch measured with rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE,
-    scaled by a plain-copy calibration) for this workload, from the committed profile."""
+    """HBM bytes per scan launch measured with rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE,
+    scaled by a plain-copy calibration) for this workload, from the committed profile, and
+    where they come from. The profile names the kernel source it measured (file and
+    SHA-256 prefix): a source that changed since makes the figure stale, and then no
+    traffic is reported."""
     p = ROOT / "profiles" / profile
     if not p.exists():
-        return None
+        return None, f"no profile {profile}"
     kv = {}
     for line in p.read_text().splitlines():
         if ":" in line and not line.startswith(("#", " ", "|")):
             k, v = line.split(":", 1)
             kv[k.strip()] = v.split("(")[0].strip()
     if kv.get("workload") != f"N={n} D={d}":
-        return None
-    return int(kv["traffic_bytes_per_launch"])
+        return None, f"profiles/{profile} measured {kv.get('workload')}, not N={n} D={d}"
+    src = kv.get("kernel_source", "").split()
+    if len(src) != 2 or source_digest(src[0]) != src[1]:
+        return None, f"profiles/{profile} measured {' '.join(src) or 'an unnamed source'}; the source has changed since"
+    return int(kv["traffic_bytes_per_launch"]), f"profiles/{profile} (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE; " \
+                                                 f"kernel source {src[0]} {src[1]})"
 
 
 def checkpoint_pass(args, mars_amd, dg):
@@ -796,7 +809,11 @@ def main() -> int:
         (_, kern_c16, rest_c16), _ = timed(W, KT, C.pointer(g1), 1, True)
         ctx.timing = False
         ctx.certified = False
-        mars_amd.upload_int8_embeddings(dg)
+        t0 = time.perf_counter()
+        mars_amd.upload_int8_embeddings(dg)           # k_convert_i8 over all rows, synchronous
+        t_i8 = time.perf_counter() - t0
+        log(f"int8 copy rebuilt (k_convert_i8 over {N:,} rows, allocation included): {t_i8 * 1e3:.2f} ms")
+        out["int8_copy_build_ms"] = t_i8 * 1e3
         cert16 = dict(p50_us=pctl(lat_c16, .5), p99_us=pctl(lat_c16, .99), scan_kernel_mean_us=float(kern_c16.mean()),
                       seeds_bfs_results_mean_us=float(rest_c16.mean()),
                       scan_gbs=bytes_f16 / float(kern_c16.mean()) / 1e3, queries=min(S, 4000))
@@ -909,6 +926,7 @@ def main() -> int:
     if not args.profile_only and not args.no_maintenance:
         out["maintenance"] = maintenance_pass(mars_amd, dg, ctx, dq, W, S - W, D, gcfg, pctl)
 
+    traffic, traffic_src = scan_traffic(N, D, "k_scan_int8_1M.md" if cand == "int8" else "k_scan_fp16_1M.md")
     achieved = bytes_cert / float(kern_c.mean()) / 1e3      # GB/s of the certified path's candidate scan
     achieved32 = bytes_f32 / float(kern_g.mean()) / 1e3
     res = {
@@ -950,13 +968,14 @@ def main() -> int:
                             graph_replay=dict(p50_us=pctl(lat_gg, .5), p99_us=pctl(lat_gg, .99)),
                             scan_kernel_mean_us=float(kern_g.mean()), finalize_kernel_mean_us=float(bfs_g.mean()),
                             scan_gbs=achieved32, scan_frac=achieved32 / HBM_PEAK_GBS,
-                            scan_traffic=scan_traffic(N, D),
+                            scan_traffic=scan_traffic(N, D)[0],
                             finalize_phases_us=dict(seed_merge=float(ph[:, 0].mean()), bfs=float(ph[:, 1].mean()),
                                                     select=float(ph[:, 2].mean()))),
         **out,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": scan_traffic(N, D, "k_scan_int8_1M.md" if cand == "int8" else "k_scan_fp16_1M.md"),
+                     "traffic": traffic,
+                     "traffic_source": traffic_src,
                      "kernel": (f"k_scan8<{D // 64},false> (int8 MFMA, 16 keys per workgroup, 64 candidates, keys = "
                                 f"per-row upper bounds)"
                                 if cand == "int8" else f"k_scan<__half,QF16<{D // 128}>,false> (16 candidates per "

@@ -18,8 +18,10 @@
 //      top-K), gpu_ms_rerank is 0 (the decay is inside the scan), gpu_ms_topk the
 //      seed merge, gpu_ms_bfs the BFS and the sorted results;
 //    * DeviceMemoryGraph: d_row_offsets / d_col_indices are a packed copy of the
-//      edges, made again after they change; the queries read d_row_words and
-//      d_col_slots, where a row that grew by a streaming insert can sit apart;
+//      edges (set by upload_to_device and the upload_* calls, made again only when
+//      the edges changed); a streaming flush clears them instead of repacking all
+//      edges, and refresh_packed_csr() makes them again on demand. The queries read
+//      d_row_words and d_col_slots, where a row that grew by an insert can sit apart;
 //    * library errors print a message and exit, as CUDA_CHECK does (lines 52-60);
 //      malformed episode inputs are silent no-ops and an inactive episode scope
 //      falls back to Global, as in the reference (memory_cuda.cu:814-855, 1163-1171).
@@ -68,6 +70,9 @@ void upload_episode_ids(DeviceMemoryGraph& dg, const int32_t* host_episode_ids, 
 void upload_episode_csr(DeviceMemoryGraph& dg, const HostEpisodeCSR& csr);
 void upload_fp16_embeddings(DeviceMemoryGraph& dg);
 void free_fp16_embeddings(DeviceMemoryGraph& dg);
+// Extension: point d_row_offsets / d_col_indices at a packed copy of the current edges
+// (after a streaming flush cleared them).
+void refresh_packed_csr(DeviceMemoryGraph& dg);
 
 struct QueryResult {
     int32_t node_id;

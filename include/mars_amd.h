@@ -94,6 +94,10 @@ typedef struct mars_stats {
     int32_t used_fp16;          /* 1 if the fp16 corpus was scanned                       */
     int32_t seeds_certified;    /* MARS_CTX_CERTIFIED: 1 if the fp16 scan's seeds were certified
                                    (0: the fp32 scan answered the query)                     */
+    int32_t results_capped;     /* 1 if max_results_returned exceeded the context's result cap
+                                   min(max_nodes, max_k * 500) and more nodes were reached than
+                                   that cap: the call returned the cap's best results (the
+                                   reference keeps the first ones in visit order)          */
     double  wall_us;            /* host wall time of the call                             */
 } mars_stats;
 

@@ -92,6 +92,7 @@ class RetrievalStats:                              # memory_cuda.cuh:129-137 (+ 
     bfs_levels_run: int = 0
     used_fp16: int = 0
     seeds_certified: int = 0
+    results_capped: int = 0
     wall_us: float = 0.0
 
     def _fill(self, s: _lib.StatsC) -> None:

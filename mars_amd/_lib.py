@@ -65,6 +65,7 @@ class StatsC(C.Structure):
         ("bfs_levels_run", C.c_int32),
         ("used_fp16", C.c_int32),
         ("seeds_certified", C.c_int32),
+        ("results_capped", C.c_int32),
         ("wall_us", C.c_double),
     ]
 

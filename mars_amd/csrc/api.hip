@@ -374,6 +374,7 @@ int query_impl(const mars_graph* gh, mars_ctx* ch, const float* h_q, const float
     // results: max_results_returned (else K), at most the context's compaction cap
     // min(max_nodes, max_k * 500) (memory_cuda.cu:1059, 1421-1447)
     const int32_t rcap = std::min(cfg->max_results_returned > 0 ? cfg->max_results_returned : K, c.res_cap);
+    const bool capped = cfg->max_results_returned > c.res_cap;          // reported in stats
     MARS_TRY(use_device(c.device));
     hipStream_t s = c.stream;
     const bool timing = (c.flags & MARS_CTX_TIMING) != 0;
@@ -426,6 +427,7 @@ int query_impl(const mars_graph* gh, mars_ctx* ch, const float* h_q, const float
                 st.bfs_levels_run = h.levels;
                 st.used_fp16 = 1;
                 st.seeds_certified = 1;
+                st.results_capped = capped && h.visited > h.count ? 1 : 0;
                 st.wall_us = std::chrono::duration<double, std::micro>(std::chrono::steady_clock::now() - t0).count();
                 *stats = st;
             }
@@ -548,6 +550,7 @@ int query_impl(const mars_graph* gh, mars_ctx* ch, const float* h_q, const float
         st.visited = h.visited;
         st.bfs_levels_run = h.levels;
         st.used_fp16 = fp16 ? 1 : 0;
+        st.results_capped = capped && h.visited > h.count ? 1 : 0;
         st.wall_us = std::chrono::duration<double, std::micro>(std::chrono::steady_clock::now() - t0).count();
         *stats = st;
     }
@@ -636,8 +639,8 @@ using namespace mars;
 
 // The ctypes mirrors (mars_amd/_lib.py) depend on these layouts.
 static_assert(sizeof(mars_query_result) == 16, "mars_query_result layout");
-static_assert(sizeof(mars_stats) == 56 && offsetof(mars_stats, seeds_certified) == 44 &&
-                  offsetof(mars_stats, wall_us) == 48,
+static_assert(sizeof(mars_stats) == 64 && offsetof(mars_stats, seeds_certified) == 44 &&
+                  offsetof(mars_stats, results_capped) == 48 && offsetof(mars_stats, wall_us) == 56,
               "mars_stats layout");
 static_assert(sizeof(mars_insert_stats) == 48 && offsetof(mars_insert_stats, queryable_us) == 24,
               "mars_insert_stats layout");
@@ -701,7 +704,8 @@ int mars_init(int32_t device) {
     if (e != hipSuccess || count <= 0) return set_error(MARS_ERR_NODEVICE, "no HIP device");
     MARS_CHECK(device >= 0 && device < count, MARS_ERR_INVALID, "device %d of %d", device, count);
     MARS_HIP(hipSetDevice(device));
-    return ensure_device(nullptr);
+    MARS_TRY(ensure_device(nullptr));
+    return noalloc_prepare(device);
 }
 
 void mars_config_default(mars_retrieval_config* c) {
@@ -732,6 +736,7 @@ int mars_graph_create(const mars_graph_desc* d, mars_graph** out) {
     else MARS_CHECK(d->num_edges == 0 || (d->row_offsets && d->col_indices), MARS_ERR_INVALID, "CSR missing");
     int devid = 0;
     MARS_TRY(ensure_device(&devid));
+    MARS_TRY(noalloc_prepare(devid));      // mars_query_batch_static's scratch address
     auto* gh = new mars_graph();
     Graph& g = gh->g;
     g.device = devid;

@@ -392,11 +392,15 @@ __device__ inline void raise_row_norms(double s32, double s16, double sd, uint32
 
 // ---- the int8 copy (certified global query) -------------------------------------------
 // Row r is stored as bytes v_i in [-127, 127] with one scale s_r = fl(max_i |e_i| / 127),
-// standing for e^_i = s_r v_i. The int8 scan's dot of a row (a per-lane fmaf chain of
-// d/16 steps, the 16-lane reduction, then * s_r) and the fp32 scan's (d/16 steps, the
-// reduction) both lie within gamma_n |q| |x| of their exact values (x = e^, e), with
-// n = d/16 + 6 rounded operations per term at most, so
-//     |dot8 - dot32| <= |q| (|e^ - e| + gamma_n (|e^| + |e|)) = |q| c_r.
+// standing for e^_i = s_r v_i. The fp32 scan's dot of a row (per-lane fmaf chains of d/16
+// steps, then the 16-lane reduction) lies within gamma_n |q| |e| of q.e, with n = d/16 + 6
+// rounded operations per term at most. The int8 scan (k_scan8) splits the query into two
+// int8 parts, q = s_hi q_hi + s_lo q_lo + r2, and sums q_hi.v and q_lo.v exactly in int32 on
+// MFMA (|sum| <= 127 * 127 * d < 2^24 for d <= 1024, so the conversion to fp32 is exact as
+// well); the split's remainder r2 and the three fp32 roundings of s_r (s_hi A_hi + s_lo A_lo)
+// make up its per-query term tau. Hence
+//     |dot8 - dot32| <= |q| (|e^ - e| + gamma_n (|e^| + |e|)) + tau = |q| c_r + tau,
+// where the gamma_n |e^| term is slack the exact int32 sums no longer need.
 __device__ inline double i8_gamma(int32_t d) {
     const double nu = (double(d) / 16.0 + 6.0) * 0x1p-24;
     return nu / (1.0 - nu);

@@ -27,6 +27,10 @@ namespace mars {
 
 // ---- error reporting ---------------------------------------------------------
 int set_error(int code, const char* fmt, ...);
+
+// Takes the device address of mars_query_batch_static's scratch array on `dev` (the
+// current device) once; mars_init and mars_graph_create call it.
+int noalloc_prepare(int dev);
 #define MARS_HIP(call)                                                               \
     do {                                                                             \
         hipError_t e__ = (call);                                                     \

@@ -7,15 +7,18 @@
 //  k_batch_merge), with their scratch in one file-scope device array instead of
 //  context buffers: the queries' fp16 rows, the per-row-range partial keys and
 //  the merged keys. The device address of that array is taken once per device
-//  with hipGetSymbolAddress and kept; kernels receive that address, never the
-//  array's host-side name. Everything runs on the caller's stream and nothing
-//  waits for it, so the call can be captured. Every call on one GPU shares the
-//  array: calls that overlap on one GPU race. No slot needs clearing: the scan
-//  writes every partial key the merge reads, and the merge every key it emits.
+//  with hipGetSymbolAddress, at set-up (mars_init, and mars_graph_create on the
+//  graph's device), and kept; kernels receive that address, never the array's
+//  host-side name. A call makes no HIP API call but its kernel launches on the
+//  caller's stream, and nothing waits for them, so the call can be captured into
+//  a HIP graph. Every call on one GPU shares the array: calls that overlap on one
+//  GPU race. No slot needs clearing: the scan writes every partial key the merge
+//  reads, and the merge every key it emits.
 // ============================================================================
 #include "internal.hpp"
 
 #include <algorithm>
+#include <atomic>
 #include <cfloat>
 #include <mutex>
 
@@ -35,23 +38,33 @@ constexpr int kMaxDevices = 64;
 static __device__ __align__(256) unsigned char scratch[kStaticBytes];
 
 std::mutex g_scratch_mu;
-void* g_scratch_ptr[kMaxDevices] = {};
+std::atomic<void*> g_scratch_ptr[kMaxDevices] = {};
 
-// The array's device address on `dev` (current), taken on the first call there.
+// The array's device address on `dev`, set by noalloc_prepare.
 int static_scratch(int dev, unsigned char** out) {
     MARS_CHECK(dev >= 0 && dev < kMaxDevices, MARS_ERR_UNSUPPORTED, "device %d beyond %d", dev, kMaxDevices);
-    std::lock_guard<std::mutex> lock(g_scratch_mu);
-    if (!g_scratch_ptr[dev]) {
-        void* p = nullptr;
-        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-        if (e != hipSuccess || !p)
-            return set_error(MARS_ERR_HIP, "hipGetSymbolAddress(scratch) on device %d: %s", dev,
-                             hipGetErrorString(e));
-        g_scratch_ptr[dev] = p;
-    }
-    *out = static_cast<unsigned char*>(g_scratch_ptr[dev]);
+    void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+    MARS_CHECK(p != nullptr, MARS_ERR_INVALID, "static scratch of device %d not set up (mars_init)", dev);
+    *out = static_cast<unsigned char*>(p);
     return MARS_OK;
 }
+
+}  // namespace
+
+// The array's device address on `dev` (the current device), taken once.
+int noalloc_prepare(int dev) {
+    MARS_CHECK(dev >= 0 && dev < kMaxDevices, MARS_ERR_UNSUPPORTED, "device %d beyond %d", dev, kMaxDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[dev].load(std::memory_order_relaxed)) return MARS_OK;
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+        return set_error(MARS_ERR_HIP, "hipGetSymbolAddress(scratch) on device %d: %s", dev, hipGetErrorString(e));
+    g_scratch_ptr[dev].store(p, std::memory_order_release);
+    return MARS_OK;
+}
+
+namespace {
 
 // keys -> (id, score) pairs, as mars_query_batch converts them on the host
 __global__ __launch_bounds__(256) void k_keys_to_results(const uint64_t* __restrict__ keys, int32_t n,

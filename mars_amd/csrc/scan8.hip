@@ -7,7 +7,7 @@
 //  copy, a quarter of the fp32 rows) and each row carries its own bound c_r (from its
 //  quantisation residual and the two scans' rounding), so the scan ranks rows by an
 //  upper bound of the fp32 scan's fused score,
-//      U_r = fuse(dot8_r + |q| c_r)  >=  fuse(dot32_r),
+//      U_r = fuse(dot8_r + |q| c_r + tau)  >=  fuse(dot32_r),
 //  (fuse = dot * exp(-lambda age) is monotone in dot for the same row), and keeps the
 //  64 best keys of U. k_cert_bfs rescores those candidates exactly: when the K-th exact
 //  score beats the 64th candidate's U, no other row can reach the top K. Ranking by the
@@ -29,7 +29,8 @@
 //              bounds the rows a list dropped by the smallest 16th key. (Rows are dealt
 //              to the workgroups in blocks of 128 consecutive ids; on the benchmark corpus,
 //              16 per workgroup certify as often as 64 would.)
-//  k_convert_i8  one wave per row: scale, bytes, c_r and the maxima (quantize_row_i8).
+//  k_convert_i8  one wave per row, the row read once: scale, bytes, c_r (quantize_row_i8's
+//              arithmetic), and the maxima raised once per wave.
 //
 //  Reference analogue: none — the reference scores fp32 (cublasSgemv) or fp16 rows
 //  (src/memory_cuda.cu:1207-1215, :155-201); the results here are its fp32 path's.
@@ -43,10 +44,10 @@ namespace {
 
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 
-// 8 waves per workgroup, one tile of 16 rows per wave and step (d / 64 loads of 1 KB in
+// 4 waves per workgroup, one tile of 16 rows per wave and step (d / 64 loads of 1 KB in
 // flight, the next tile's issued before the current tile's scores are fused): 512
-// workgroups keep 4 waves on every SIMD, with room beside them for a wave of another
-// kernel (inserts, episode queries).
+// workgroups put 2 waves on every SIMD of 256 CUs, with room beside them for a wave of
+// another kernel (inserts, episode queries).
 constexpr int kScan8Waves = 4;
 constexpr int kScan8Ring = 2;
 constexpr int kScan8Threads = kScan8Waves * 64;
@@ -206,12 +207,77 @@ __global__ __launch_bounds__(kScan8Threads) void k_scan8(ScanArgs a) {
     }
 }
 
+// quantize_row_i8's arithmetic in one read of each row: one wave per row (grid-stride),
+// lane l holding elements [16 g, 16 g + 16) for g = l and g = l + 64 (d a multiple of 16,
+// at most 2048) as four 16-byte loads each; a group's 16 bytes are one 16-byte store into
+// the tiled copy. The wave keeps the largest c_r and |e| of its rows and raises nrm8 once
+// (an atomic per row on the same two words serialises the whole pass).
 __global__ __launch_bounds__(256) void k_convert_i8(const float* __restrict__ emb, int64_t r0, int64_t r1, int32_t d,
                                                     int8_t* __restrict__ emb8, float* __restrict__ meta8,
                                                     uint32_t* __restrict__ nrm8) {
-    const int wave = int(threadIdx.x >> 6);
-    for (int64_t row = r0 + int64_t(blockIdx.x) * 4 + wave; row < r1; row += int64_t(gridDim.x) * 4)
-        quantize_row_i8(emb + row * d, d, emb8, row, meta8 + 2 * row, nrm8);
+    const int wave = int(threadIdx.x >> 6), lane = lane_id();
+    const int ng = d >> 4;
+    uint32_t cmax = 0u, nmax = 0u;
+    for (int64_t row = r0 + int64_t(blockIdx.x) * 4 + wave; row < r1; row += int64_t(gridDim.x) * 4) {
+        f32x4 x[2][4];
+        float m = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int g = lane + 64 * j;
+            const f32x4* p = reinterpret_cast<const f32x4*>(emb + row * d + 16 * int64_t(g));
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                x[j][v] = g < ng ? __builtin_nontemporal_load(p + v) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                m = fmaxf(fmaxf(m, fabsf(x[j][v].x)), fabsf(x[j][v].y));
+                m = fmaxf(fmaxf(m, fabsf(x[j][v].z)), fabsf(x[j][v].w));
+            }
+        }
+        const float s = wave_max_f(m) / 127.0f;
+        int8_t* tile = emb8 + i8_offset(row, 0, d);
+        double s32 = 0.0, s8 = 0.0, sd = 0.0;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int g = lane + 64 * j;
+            if (g >= ng) continue;
+            uint32_t w[4];
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const float xs[4] = {x[j][v].x, x[j][v].y, x[j][v].z, x[j][v].w};
+                uint32_t word = 0u;
+#pragma unroll
+                for (int b = 0; b < 4; ++b) {
+                    // I8Row::put's arithmetic
+                    float t = s > 0.0f ? rintf(xs[b] / s) : 0.0f;
+                    t = fminf(fmaxf(t, -127.0f), 127.0f);
+                    const int vi = int(t);
+                    word |= uint32_t(uint8_t(int8_t(vi))) << (8 * b);
+                    const double eh = double(s) * double(vi);
+                    s32 += double(xs[b]) * double(xs[b]);
+                    s8 += eh * eh;
+                    const double df = eh - double(xs[b]);
+                    sd += df * df;
+                }
+                w[v] = word;
+            }
+            const int i0 = 16 * g;
+            *reinterpret_cast<u32x4*>(tile + ((i0 >> 6) << 10) + (((i0 & 63) >> 4) << 8)) = u32x4{w[0], w[1], w[2], w[3]};
+        }
+        s32 = wave_sum_f64(s32);
+        s8 = wave_sum_f64(s8);
+        sd = wave_sum_f64(sd);
+        const double c = (sqrt(sd) + i8_gamma(d) * (sqrt(s8) + sqrt(s32))) * (1.0 + 1e-9);
+        const uint32_t cb = up_bits(c), nb = up_bits(sqrt(s32));
+        if (lane == 0) {
+            meta8[2 * row] = s;
+            meta8[2 * row + 1] = __uint_as_float(cb);
+        }
+        cmax = cb > cmax ? cb : cmax;
+        nmax = nb > nmax ? nb : nmax;
+    }
+    if (lane == 0 && (cmax | nmax)) {
+        atomicMax(nrm8 + 0, cmax);
+        atomicMax(nrm8 + 1, nmax);
+    }
 }
 
 template <int NK>
@@ -250,6 +316,7 @@ int launch_scan8(const ScanArgs& a, hipStream_t s) {
 int launch_convert_i8(const float* emb, int64_t r0, int64_t r1, int32_t d, int8_t* emb8, float* meta8,
                       uint32_t* nrm8, hipStream_t s) {
     if (r1 <= r0) return MARS_OK;
+    MARS_CHECK(d % 16 == 0 && d <= 2048, MARS_ERR_UNSUPPORTED, "int8 copy: embedding_dim %d", d);
     const int64_t blocks = std::min<int64_t>((r1 - r0 + 3) / 4, 4096);
     MARS_LAUNCH(k_convert_i8, dim3(unsigned(blocks)), dim3(256), 0, s, emb, r0, r1, d, emb8, meta8, nrm8);
     return MARS_OK;

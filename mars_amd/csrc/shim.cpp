@@ -26,17 +26,19 @@ void die_on(int rc, const char* what) {
     std::exit(EXIT_FAILURE);
 }
 
-void refresh_view(DeviceMemoryGraph& d) {
+// packed: also point d_row_offsets / d_col_indices at the reference's packed CSR (a copy
+// the library makes again only when the edges changed since the last one); otherwise they
+// are cleared, and refresh_packed_csr() makes them on demand. The queries never read
+// them: they read the row words and their column slots.
+void refresh_view(DeviceMemoryGraph& d, bool packed = true) {
     mars_graph_view v{};
     die_on(mars_graph_get_view(d.handle, &v), "mars_graph_get_view");
     d.num_nodes = v.num_nodes;
     d.num_edges = v.num_edges;
     d.embedding_dim = v.embedding_dim;
-    // the reference's packed CSR (a copy, rebuilt when the edges changed); the queries
-    // read the row words and their column slots
     const int32_t* prow = nullptr;
     const int32_t* pcol = nullptr;
-    die_on(mars_graph_packed_csr(d.handle, &prow, &pcol), "mars_graph_packed_csr");
+    if (packed) die_on(mars_graph_packed_csr(d.handle, &prow, &pcol), "mars_graph_packed_csr");
     d.d_row_offsets = const_cast<int32_t*>(prow);
     d.d_col_indices = const_cast<int32_t*>(pcol);
     d.d_row_words = static_cast<int64_t*>(v.d_row_words);
@@ -150,6 +152,10 @@ int32_t maintain_graph(DeviceMemoryGraph& dg, int32_t min_hits, int32_t window_q
 
 void count_edge_hits(DeviceMemoryGraph& dg, QueryContext& ctx) {
     die_on(mars_edge_hits_count(dg.handle, ctx.handle), "count_edge_hits");
+}
+
+void refresh_packed_csr(DeviceMemoryGraph& dg) {
+    if (dg.handle) refresh_view(dg, true);
 }
 
 void free_device(DeviceMemoryGraph& d) {
@@ -341,7 +347,8 @@ FlushStats StreamingBuffer::flush(DeviceMemoryGraph& target) {
     die_on(mars_graph_insert(target.handle, n, rows.data(), mods.data(), ts.data(), with_eps ? eps.data() : nullptr,
                              cfg_.nsn_k, nullptr, &st),
            "StreamingBuffer::flush");
-    refresh_view(target);
+    // the packed CSR copy is not rebuilt per flush (an O(N + E) pass): refresh_packed_csr()
+    refresh_view(target, false);
     stats.nodes_committed = st.nodes_added;
     stats.edges_added = int32_t(std::min<int64_t>(st.edges_added, INT32_MAX));
     stats.flush_ms = float(st.linked_us / 1000.0);

@@ -133,6 +133,18 @@ static int stream_check(int32_t N, uint64_t seed) {
     std::printf("flush committed=%d edges_added=%d nodes=%d edges=%d staged=%d total=%lld\n", fs.nodes_committed,
                 fs.edges_added, dg.num_nodes, dg.num_edges - edges0, buf.staged_count(),
                 (long long)buf.total_flushed());
+    // the flush cleared the packed CSR copy; refresh_packed_csr makes it again, equal to
+    // the graph's edges as the library downloads them
+    const bool cleared = dg.d_row_offsets == nullptr && dg.d_col_indices == nullptr;
+    refresh_packed_csr(dg);
+    std::vector<int32_t> prow(size_t(dg.num_nodes) + 1), pcol(size_t(dg.num_edges));
+    std::vector<int32_t> wrow(prow.size()), wcol(pcol.size());
+    const bool same = dg.d_row_offsets && dg.d_col_indices &&
+                      mars_copy_to_host(prow.data(), dg.d_row_offsets, prow.size() * sizeof(int32_t)) == MARS_OK &&
+                      mars_copy_to_host(pcol.data(), dg.d_col_indices, pcol.size() * sizeof(int32_t)) == MARS_OK &&
+                      mars_graph_download(dg.handle, wrow.data(), wcol.data(), nullptr, nullptr) == MARS_OK &&
+                      prow == wrow && pcol == wcol;
+    std::printf("packed cleared=%d same=%d\n", cleared ? 1 : 0, same ? 1 : 0);
     QueryContext ctx = create_query_context(N + 10, D, 64);
     RetrievalConfig cfg;
     cfg.top_k = 10;

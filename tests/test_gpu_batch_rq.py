@@ -7,7 +7,8 @@ queries per workgroup in registers, 16-row tiles through LDS, a sampled score fl
 - bit for bit against k_batch_scan (batches of at most 64 queries), which computes the
   same MFMA products in the same order: the same queries scored in one batch (256, 128 or
   96 queries) and in batches of 32 give the same ids and scores;
-- with a corpus large enough that each row range is sampled for the score floor;
+- with a corpus large enough that each row range is sampled for the score floor, against
+  the oracle and bit for bit against batches of 32 (which take no floor);
 - the neighbour-search form (plain dot products, the node itself excluded) against the
   exact CPU k-NN.
 """
@@ -78,6 +79,33 @@ def test_rq_sampled_floor(rng):
         batch_check(dev, qn[:300], RetrievalConfig(top_k=16, time_decay_lambda=LAM, modality_filter=1), T_Q, emb)
     finally:
         dev.close()
+
+
+@pytest.mark.parametrize("q,k,filt,uniform", [(600, 10, -1, True), (300, 16, 1, False), (600, 5, 2, False)])
+def test_rq_sampled_floor_equals_scan_bit_for_bit(q, k, filt, uniform, rng):
+    """The sampled floor drops no row that belongs in a list: on 120K rows (each 256-query
+    group's ranges sampled for the floor), the batch's ids and score bits equal those of
+    the same queries scored in batches of 32 by k_batch_scan (no floor), with a modality
+    filter and with per-query times too."""
+    n, d = 120_000, 256
+    emb = rng.standard_normal((n, d)).astype(np.float32)
+    emb /= np.linalg.norm(emb, axis=1, keepdims=True)
+    mods = rng.integers(0, 3, size=n).astype(np.int32)
+    ts = rng.uniform(0, 600, size=n).astype(np.float32)
+    dev = Dev(emb, mods, ts, None, None, fp16=True)
+    qs = np.ascontiguousarray(emb[rng.choice(n, q, replace=False)])
+    tq = np.full(q, T_Q, np.float32) if uniform else rng.uniform(300, 600, q).astype(np.float32)
+    cfg = RetrievalConfig(top_k=k, time_decay_lambda=LAM, modality_filter=filt)
+    buf = mars_amd.DeviceBuffer.from_array(qs)
+    try:
+        ids, sc = mars_amd.query_batch(dev.dg, dev.ctx, buf.ptr, q, tq, cfg)                  # sampled floor
+        parts = [mars_amd.query_batch(dev.dg, dev.ctx, buf.ptr + j * d * 4, min(32, q - j), tq[j:j + 32], cfg)
+                 for j in range(0, q, 32)]                                                   # k_batch_scan
+    finally:
+        buf.free()
+        dev.close()
+    np.testing.assert_array_equal(ids, np.concatenate([p[0] for p in parts]))
+    np.testing.assert_array_equal(sc.view(np.uint32), np.concatenate([p[1] for p in parts]).view(np.uint32))
 
 
 def test_rq_sampled_floor_sparse_filter_and_neighbours(rng):

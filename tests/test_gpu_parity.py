@@ -134,14 +134,20 @@ def test_result_counts_up_to_the_compaction_cap(rng):
         res = check_global(dev, emb[7], cfg)
         assert len(res) == 20000
         _, st = dev.query(emb[7], cfg)
-        assert st.visited > 32000
+        assert st.visited > 32000 and st.results_capped == 0   # 20,000 asked, below the cap
         big = RetrievalConfig(top_k=8, bfs_max_hops=4, time_decay_lambda=LAM, max_results_returned=39000)
         res, st = dev.query(emb[7], big)
         assert len(res) == 32000                               # 64 * 500
+        assert st.results_capped == 1                          # the cap cut the results
         small_ctx = mars_amd.create_query_context(dev.n, dev.d, 8)   # cap 8 * 500; K = 8 on both
         try:
-            res8 = mars_amd.query_memory_fast(dev.dg, small_ctx, emb[7], T_Q, big)
-            assert len(res8) == 4000 and res8 == res[:4000]
+            st8 = mars_amd.RetrievalStats()
+            res8 = mars_amd.query_memory_fast(dev.dg, small_ctx, emb[7], T_Q, big, st8)
+            assert len(res8) == 4000 and res8 == res[:4000] and st8.results_capped == 1
+            # above the cap, but the visit set fits in it: nothing was cut
+            few = RetrievalConfig(top_k=8, bfs_max_hops=1, time_decay_lambda=LAM, max_results_returned=39000)
+            resf = mars_amd.query_memory_fast(dev.dg, small_ctx, emb[7], T_Q, few, st8)
+            assert st8.results_capped == 0 and len(resf) == st8.visited < 4000
         finally:
             mars_amd.destroy_query_context(small_ctx)
     finally:

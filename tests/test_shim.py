@@ -69,6 +69,8 @@ def test_shim_streaming_buffer_flush():
     assert int(kv["committed"]) == 10 and int(kv["nodes"]) == n + 10
     assert int(kv["edges_added"]) == int(kv["edges"]) > 10 * 9
     assert int(kv["staged"]) == 0 and int(kv["total"]) == 10
+    # the flush clears the packed CSR copy; refresh_packed_csr makes it equal to the edges
+    assert "packed cleared=1 same=1" in r.stdout.splitlines()
     line = next(ln for ln in r.stdout.splitlines() if ln.startswith("global"))
     head = line.split(" | ")[0].split()
     node = int(head[1])

@@ -61,3 +61,90 @@ def test_static_batch_matches_query_batch():
     finally:
         mars_amd.destroy_query_context(ctx)
         mars_amd.free_device(dg)
+
+
+def _hip():
+    """The HIP runtime libmars_amd.so links (the same library, so streams and graphs are
+    shared with it)."""
+    import ctypes as C
+    h = C.CDLL("libamdhip64.so.7")
+    vp = C.c_void_p
+    for name, args in (("hipStreamCreate", [C.POINTER(vp)]), ("hipStreamBeginCapture", [vp, C.c_int]),
+                       ("hipStreamEndCapture", [vp, C.POINTER(vp)]),
+                       ("hipGraphInstantiate", [C.POINTER(vp), vp, vp, vp, C.c_size_t]),
+                       ("hipGraphLaunch", [vp, vp]), ("hipStreamSynchronize", [vp]),
+                       ("hipGraphExecDestroy", [vp]), ("hipGraphDestroy", [vp]), ("hipStreamDestroy", [vp])):
+        getattr(h, name).argtypes = args
+        getattr(h, name).restype = C.c_int
+    return h
+
+
+def _free_bytes():
+    import ctypes as C
+    from mars_amd._lib import check, lib
+    free, total = C.c_size_t(), C.c_size_t()
+    check(lib.mars_device_memory(C.byref(free), C.byref(total)), "mars_device_memory")
+    return free.value
+
+
+def test_static_batch_captured_in_a_hip_graph():
+    """The call captured on a stream into a HIP graph, replayed three times with other
+    work and new query vectors between the replays: every replay equals query_batch on
+    the queries it read. Eager calls leave the device's free memory unchanged."""
+    import ctypes as C
+    mars_amd.init(0)
+    c = corpus.make_corpus(N, D, seed=48)
+    g = mars_amd.MemoryGraph(N, D, None, None, c.embeddings, c.modalities, c.timestamps)
+    dg = mars_amd.upload_to_device(g)
+    mars_amd.upload_fp16_embeddings(dg)
+    ctx = mars_amd.create_query_context(N, D, 64)
+    hip = _hip()
+    q, k = 96, 10
+    cfg = RetrievalConfig(top_k=k, time_decay_lambda=corpus.DECAY_LAMBDA)
+    sets = [c.embeddings[corpus.pick_queries(c.modalities, q, seed=900 + i)] for i in range(3)]
+    tq = np.full(q, corpus.QUERY_TIME, np.float32)
+    bq = mars_amd.DeviceBuffer.from_array(np.ascontiguousarray(sets[0]))
+    bt = mars_amd.DeviceBuffer.from_array(tq)
+    bi, bs = mars_amd.DeviceBuffer(q * k * 4), mars_amd.DeviceBuffer(q * k * 4)
+    s, graph, exe = C.c_void_p(), C.c_void_p(), C.c_void_p()
+    try:
+        # eager: no allocation (after one warm call that loads the kernels)
+        mars_amd.query_batch_static(dg, bq.ptr, q, bt.ptr, cfg, bi.ptr, bs.ptr, uniform_tq=True)
+        mars_amd.synchronize()
+        free0 = _free_bytes()
+        for _ in range(3):
+            mars_amd.query_batch_static(dg, bq.ptr, q, bt.ptr, cfg, bi.ptr, bs.ptr, uniform_tq=True)
+        mars_amd.synchronize()
+        assert _free_bytes() == free0
+        # capture
+        assert hip.hipStreamCreate(C.byref(s)) == 0
+        assert hip.hipStreamBeginCapture(s, 0) == 0                # hipStreamCaptureModeGlobal
+        mars_amd.query_batch_static(dg, bq.ptr, q, bt.ptr, cfg, bi.ptr, bs.ptr, uniform_tq=True, stream=s.value)
+        assert hip.hipStreamEndCapture(s, C.byref(graph)) == 0
+        assert hip.hipGraphInstantiate(C.byref(exe), graph, None, None, 0) == 0
+        for i, qs in enumerate(sets):
+            src = mars_amd.DeviceBuffer.from_array(np.ascontiguousarray(qs))
+            try:
+                from mars_amd._lib import check, lib
+                check(lib.mars_copy_device(C.c_void_p(bq.ptr), C.c_void_p(src.ptr), qs.nbytes), "mars_copy_device")
+                want_ids, want_sc = mars_amd.query_batch(dg, ctx, src.ptr, q, tq, cfg)   # eager work between
+            finally:
+                src.free()
+            assert hip.hipGraphLaunch(exe, s) == 0
+            assert hip.hipStreamSynchronize(s) == 0
+            got_ids = bi.to_array(np.int32, q * k).reshape(q, k)
+            got_sc = bs.to_array(np.float32, q * k).reshape(q, k)
+            np.testing.assert_array_equal(got_ids, want_ids, err_msg=f"replay {i}")
+            np.testing.assert_array_equal(got_sc.view(np.uint32), want_sc.view(np.uint32), err_msg=f"replay {i}")
+    finally:
+        if exe.value:
+            hip.hipGraphExecDestroy(exe)
+        if graph.value:
+            hip.hipGraphDestroy(graph)
+        if s.value:
+            hip.hipStreamSynchronize(s)
+            hip.hipStreamDestroy(s)
+        for b in (bq, bt, bi, bs):
+            b.free()
+        mars_amd.destroy_query_context(ctx)
+        mars_amd.free_device(dg)
