@@ -799,6 +799,31 @@ def main() -> int:
     log(f"global certified ({cand} scan, exact results): p50 {pctl(lat_c, .5):.1f} us p99 {pctl(lat_c, .99):.1f} us; "
         f"{S / wall_c:.0f} q/s; scan kernel mean {kern_c.mean():.1f} us ({bytes_cert / kern_c.mean() / 1e3:.0f} GB/s); "
         f"seeds + BFS + results {rest_c.mean():.1f} us; certified {n_cert}/{n_samp}")
+    if cand == "int8" and not args.profile_only:
+        # global queries in batches of 8 and 16 over one int8 pass (k_scan8m, certified seeds,
+        # batched BFS), the answers identical to the Q=1 path's
+        for B in (8, 16):
+            ctx.timing = True
+            rs = []
+            for r in range(33):
+                st = mars_amd.BatchStats()
+                mars_amd.query_global_batch(dg, ctx, dq.ptr + (W + r * B) % (nq - B + 1) * D * 4, B,
+                                            corpus.QUERY_TIME, gcfg, stats=st)
+                if r >= 3:
+                    rs.append((st.wall_us, st.gpu_ms_scan * 1e3, st.gpu_ms_seeds * 1e3, st.gpu_ms_bfs * 1e3,
+                               st.batched, st.candidate_rows))
+            ctx.timing = False
+            a = np.array(rs)
+            out[f"global_batch{B}_int8"] = dict(
+                p50_us=pctl(a[:, 0], .5), p99_us=pctl(a[:, 0], .99), queries_per_s=B / (pctl(a[:, 0], .5) / 1e6),
+                scan_kernel_mean_us=float(a[:, 1].mean()), certify_mean_us=float(a[:, 2].mean()),
+                bfs_results_mean_us=float(a[:, 3].mean()), batched=int(a[:, 4].sum()), queries=B * len(rs),
+                scan_vs_q1_scan=float(a[:, 1].mean()) / float(kern_c.mean()),
+                candidate_rows=int(a[0, 5]), kernel="k_scan8m (int8 MFMA, 8 queries per A operand)")
+            log(f"global batch of {B} (one int8 pass): p50 {pctl(a[:, 0], .5):.0f} us p99 {pctl(a[:, 0], .99):.0f} us; "
+                f"scan {a[:, 1].mean():.1f} us ({a[:, 1].mean() / float(kern_c.mean()):.2f}x the Q=1 scan), certify "
+                f"{a[:, 2].mean():.1f} us, BFS + results {a[:, 3].mean():.1f} us; {int(a[:, 4].sum())}/{B * len(rs)} "
+                f"batched")
     cert16 = None
     if cand == "int8" and not args.profile_only:
         # the same queries certified over the fp16 copy (the int8 copy set aside, then rebuilt)

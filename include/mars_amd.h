@@ -472,7 +472,10 @@ typedef struct mars_batch_stats {
     float   gpu_ms_bfs;         /* BFS, visit scores and results                          */
     float   gpu_ms_total;
     float   min_margin;         /* smallest certificate margin of a certified query        */
-    float   reserved;
+    int32_t candidate_rows;     /* rows the shared scan read: 8 = the int8 copy (up to 16 queries
+                                   and neighbour searches per pass, certified exact candidates),
+                                   16 = the fp16 MFMA scan, 24 = int8, then fp16 again for the
+                                   neighbour searches the int8 certificate did not cover     */
     double  wall_us;            /* host wall time of the call (Q=1 answers included)      */
     double  q1_us;              /* of which Q=1 answers                                   */
 } mars_batch_stats;

@@ -421,20 +421,22 @@ class BatchStats:
     gpu_ms_bfs: float = 0.0
     gpu_ms_total: float = 0.0
     min_margin: float = 0.0
+    candidate_rows: int = 0          # 8: int8 pass, 16: fp16 MFMA scan, 24: int8 then fp16 for the k-NN
     wall_us: float = 0.0
     q1_us: float = 0.0
 
     def _fill(self, c) -> None:
         for f in ("queries", "batched", "uncertified", "overflow", "whole_batch_q1", "n_live", "gpu_ms_scan",
-                  "gpu_ms_seeds", "gpu_ms_bfs", "gpu_ms_total", "min_margin", "wall_us", "q1_us"):
+                  "gpu_ms_seeds", "gpu_ms_bfs", "gpu_ms_total", "min_margin", "candidate_rows", "wall_us", "q1_us"):
             setattr(self, f, getattr(c, f))
 
 
 def query_global_batch(dg: DeviceMemoryGraph, ctx: QueryContext, d_queries_ptr: int, n_queries: int, t_q,
                        cfg: RetrievalConfig, cap: int = 64,
                        stats: Optional[BatchStats] = None) -> List[List[QueryResult]]:
-    """Q global queries in one call (shared fp16 MFMA scan, certified exact seeds, batched
-    BFS): query i's results are exactly query_memory_fast's for it (capped at cap)."""
+    """Q global queries in one call (one shared scan: the int8 copy for up to 16 queries when
+    the graph holds it, else the fp16 MFMA scan; certified exact seeds, batched BFS): query
+    i's results are exactly query_memory_fast's for it (capped at cap)."""
     tq = np.ascontiguousarray(np.broadcast_to(np.asarray(t_q, np.float32), (n_queries,)))
     out = (_lib.QueryResultC * (max(1, n_queries * cap)))()
     n_out = np.zeros(n_queries, np.int32)

@@ -132,7 +132,7 @@ class BatchStatsC(C.Structure):
         ("gpu_ms_bfs", C.c_float),
         ("gpu_ms_total", C.c_float),
         ("min_margin", C.c_float),
-        ("reserved", C.c_float),
+        ("candidate_rows", C.c_int32),
         ("wall_us", C.c_double),
         ("q1_us", C.c_double),
     ]

@@ -25,7 +25,7 @@ ARCH = "gfx950"
 # hipcc ignores the feature with a warning).
 NO_PK_FP32 = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 COMMON = ["-std=c++17", "-O3", "-fPIC", f"-I{ROOT / 'include'}", f"-I{CSRC}"]
-SOURCES = ["api.hip", "kernels.hip", "batch.hip", "batch_mm.hip", "batch_rq.hip", "multi.hip", "insert.hip", "tiled.hip", "maintain.hip", "noalloc.hip", "scan8.hip",
+SOURCES = ["api.hip", "kernels.hip", "batch.hip", "batch_mm.hip", "batch_rq.hip", "multi.hip", "insert.hip", "tiled.hip", "maintain.hip", "noalloc.hip", "scan8.hip", "scan8m.hip",
            "corpus.cpp", "formats.cpp", "nsn.cpp", "shim.cpp"]
 DRIVER_SRC = ROOT / "tests" / "cpp" / "shim_driver.cpp"
 DRIVER = ROOT / "tests" / "cpp" / "shim_driver"

@@ -175,6 +175,7 @@ int64_t edge_room(const Graph& g) {
 void multi_free(Ctx& c) {
     dfree(c.mknn);
     c.mknn_cap = 0;
+    dfree(c.m8part); dfree(c.m8qa); dfree(c.m8qp);
     dfree(c.mqn); dfree(c.mseed); dfree(c.mstat); dfree(c.minfo); dfree(c.mmargin);
     dfree(c.mvlist); dfree(c.mvhop); dfree(c.mvpar); dfree(c.mvro); dfree(c.mvfin); dfree(c.mvscore);
     c.mcap_q = 0;
@@ -589,7 +590,7 @@ int ensure_multi_scratch(Ctx& c, int32_t q, int32_t rcap) {
         c.mcap_q = 0;
         const size_t nv = size_t(q) * kMultiVisit;
         MARS_TRY(dmalloc(&c.mqn, size_t(q) * 4));
-        MARS_TRY(dmalloc(&c.mseed, std::max<size_t>(size_t(q) * kMultiCand, 64)));
+        MARS_TRY(dmalloc(&c.mseed, size_t(q) * 64));          // 64 per query (int8 certificate)
         MARS_TRY(dmalloc(&c.mstat, size_t(q)));
         MARS_TRY(dmalloc(&c.minfo, size_t(q) * 4));
         MARS_TRY(dmalloc(&c.mmargin, size_t(q)));
@@ -1382,7 +1383,10 @@ int mars_bench_serve(mars_graph* g, mars_ctx* cg, mars_ctx* ce, mars_serve_bench
             j = i + 1;
             while (j < b->n_global && j - i < mb && b->g_arrival_us[j] <= now) ++j;
         }
-        const int32_t cnt = l_wait ? std::min(n_pub - linked, b->max_link) : 0;
+        int32_t cnt = l_wait ? std::min(n_pub - linked, b->max_link) : 0;
+        // with the int8 copy, up to 16 queries and neighbour searches share one int8 pass:
+        // link at most what fits beside the global queries (the rest waits for the next call)
+        if (cnt > 0 && cert_uses_int8(g->g) && j - i < 8 * kScan8MMaxA) cnt = std::min(cnt, 8 * kScan8MMaxA - (j - i));
         if (mb == 1 && !deferred) {
             rc = query_impl(g, cg, nullptr, b->g_queries + int64_t(i) * D, b->t_q, b->gcfg, out.data(), 64,
                             nout.data(), nullptr);
@@ -1519,17 +1523,25 @@ int mars_query_batch(const mars_graph* gh, mars_ctx* ch, const float* dq, int32_
     return MARS_OK;
 }
 
-int mars_query_global_batch(const mars_graph* gh, mars_ctx* ch, const float* dq, int32_t Q, const float* h_tq,
-                            const mars_retrieval_config* cfg, mars_query_result* out, int32_t cap,
-                            int32_t* n_out, mars_batch_stats* stats) {
-    MARS_CHECK(Q > 0, MARS_ERR_INVALID, "bad arguments");
-    return mars_query_global_batch_knn(gh, ch, dq, Q, h_tq, cfg, out, cap, n_out, stats, 0, 0, 0, nullptr);
+namespace {
+
+// Scratch of the multi-query int8 pass (k_split8, k_scan8m, k_cert_multi8), sized once for
+// the most queries one pass takes.
+int ensure_scan8m_scratch(Ctx& c) {
+    if (c.m8part) return MARS_OK;
+    const int32_t qmax = 8 * kScan8MMaxA;
+    MARS_TRY(dmalloc(&c.m8part, size_t(qmax) * size_t(kScan8MPart)));
+    MARS_TRY(dmalloc(&c.m8qa, size_t(kScan8MMaxA) * size_t(c.d / 64) * 1024));
+    MARS_TRY(dmalloc(&c.m8qp, size_t(qmax) * 4));
+    return MARS_OK;
 }
 
-int mars_query_global_batch_knn(const mars_graph* gh, mars_ctx* ch, const float* dq, int32_t Q, const float* h_tq,
-                                const mars_retrieval_config* cfg, mars_query_result* out, int32_t cap,
-                                int32_t* n_out, mars_batch_stats* stats, int32_t knn_first, int32_t knn_count,
-                                int32_t knn_k, int32_t* out_knn) {
+// allow_int8 = false keeps the fp16 MFMA scan (the fallback of neighbour searches the int8
+// certificate did not cover).
+int global_batch_impl(const mars_graph* gh, mars_ctx* ch, const float* dq, int32_t Q, const float* h_tq,
+                      const mars_retrieval_config* cfg, mars_query_result* out, int32_t cap, int32_t* n_out,
+                      mars_batch_stats* stats, int32_t knn_first, int32_t knn_count, int32_t knn_k, int32_t* out_knn,
+                      bool allow_int8) {
     using clk = std::chrono::steady_clock;
     const auto t0 = clk::now();
     MARS_CHECK(gh && ch && Q >= 0 && knn_count >= 0 && Q + knn_count > 0, MARS_ERR_INVALID, "bad arguments");
@@ -1557,7 +1569,7 @@ int mars_query_global_batch_knn(const mars_graph* gh, mars_ctx* ch, const float*
                    "k-NN queries need the fp16 rows and embedding_dim in {256, 384, 512, 768}");
     }
     int32_t K = 0, hops = 0, rcap = 0;
-    bool fp16 = false, batched = false;
+    bool fp16 = false, glob_ok = false;
     float lambda = 0.0f;
     if (Q > 0) {
         MARS_CHECK(cfg->top_k > 0, MARS_ERR_INVALID, "top_k = %d", cfg->top_k);
@@ -1568,26 +1580,31 @@ int mars_query_global_batch_knn(const mars_graph* gh, mars_ctx* ch, const float*
         fp16 = (c.flags & MARS_CTX_USE_FP16) && g.emb16 != nullptr;
         const bool boost = g.ep_ids && cfg->query_episode_id >= 0 && cfg->episode_same_boost > 0.0f;
         lambda = cfg->time_decay_lambda;
-        batched = !scoped && g.emb16 && g.nrm && batch_dim_supported(g.d) && K <= kMultiCand && !boost &&
-                  lambda >= 0.0f && lambda <= FLT_MAX && hops < 255;
+        glob_ok = !scoped && K <= kMultiCand && !boost && lambda >= 0.0f && lambda <= FLT_MAX && hops < 255;
     }
+    // Up to 16 queries and neighbour searches share one pass over the int8 copy (half the
+    // fp16 rows' bytes) with certified exact candidates; larger batches take the fp16 MFMA
+    // scan, whose one pass serves any number of queries.
+    const int32_t na8 = ((glob_ok ? Q : 0) + knn_count + 7) / 8;
+    const bool use8 = allow_int8 && na8 >= 1 && na8 <= kScan8MMaxA && !fp16 && cert_uses_int8(g);
+    const bool batched = glob_ok && (use8 || (g.emb16 && g.nrm && batch_dim_supported(g.d)));
     MARS_TRY(use_device(c.device));
     mars_batch_stats st{};
     st.queries = Q;
     st.n_live = n_live;
     st.min_margin = FLT_MAX;
     std::vector<int32_t> q1;                    // queries the Q=1 path answers
-    // A lone global query (no neighbour search) is cheaper on the Q=1 certified path: its
-    // fp16 scan beats the MFMA kernel with one query lane of 64, and the results are the same.
+    // A lone global query (no neighbour search) is cheaper on the Q=1 certified path (one
+    // candidate scan and one kernel for the rest), and the results are the same.
     const bool lone = batched && Q == 1 && knn_count == 0 && !fp16 && cert_dim_supported(g.d);
     const int32_t Qg = (batched && !lone) ? Q : 0;   // global queries in the shared scan
     const int32_t Qt = Qg + knn_count;               // + k-NN queries (plain dot products)
+    bool knn_fallback = false;
     if (!batched) {
         st.whole_batch_q1 = Q > 0 ? 1 : 0;
         for (int32_t j = 0; j < Q; ++j) q1.push_back(j);
     }
     if (lone) {
-        const auto tl = clk::now();
         const uint32_t saved = c.flags;
         c.flags |= MARS_CTX_CERTIFIED;
         mars_stats s1{};
@@ -1595,19 +1612,15 @@ int mars_query_global_batch_knn(const mars_graph* gh, mars_ctx* ch, const float*
         c.flags = saved;
         MARS_TRY(rc);
         if (s1.seeds_certified) ++st.batched; else ++st.uncertified;
+        st.candidate_rows = cert_uses_int8(g) ? 8 : 16;
         st.q1_us = 0.0;
         st.wall_us = std::chrono::duration<double, std::micro>(clk::now() - t0).count();
-        (void)tl;
         if (stats) *stats = st;
         return MARS_OK;
     }
     if (Qt > 0) {
-        int32_t nrr = 0, nqb = 0;
-        int64_t rpr = 0;
-        batch_grid(n_live, Qt, &nrr, &nqb, &rpr);
-        const int32_t kp = batch_kpart(kMultiCand);
-        MARS_TRY(ensure_batch_scratch(c, Qt, int64_t(nqb) * nrr * 64 * kp));
-        if (Qg > 0) MARS_TRY(ensure_multi_scratch(c, Qg, rcap));
+        st.candidate_rows = use8 ? 8 : 16;
+        if (Qg > 0 || use8) MARS_TRY(ensure_multi_scratch(c, use8 ? Qt : Qg, std::max(rcap, 1)));
         if (knn_count > c.mknn_cap) {
             dfree(c.mknn);
             c.mknn_cap = 0;
@@ -1616,57 +1629,104 @@ int mars_query_global_batch_knn(const mars_graph* gh, mars_ctx* ch, const float*
         }
         hipStream_t s = c.stream;
         const bool timing = (c.flags & MARS_CTX_TIMING) != 0;
-        if (Qg > 0) {
-            MARS_HIP(hipMemcpyAsync(c.btq, h_tq, size_t(Qg) * sizeof(float), hipMemcpyHostToDevice, s));
-            MARS_TRY(launch_f32_to_f16_rows(dq, c.bq, int64_t(Qg) * g.d, s));
-            MARS_TRY(launch_query_norms(dq, c.bq, Qg, g.d, c.mqn, s));
+        int32_t seed_stride = kMultiCand;
+        std::vector<int32_t> knn_status(static_cast<size_t>(use8 ? knn_count : 0));
+        if (use8) {
+            MARS_TRY(ensure_scan8m_scratch(c));
+            MARS_TRY(ensure_batch_scratch(c, std::max(Qg, 1), 0));              // query times
+            if (Qg > 0) MARS_HIP(hipMemcpyAsync(c.btq, h_tq, size_t(Qg) * sizeof(float), hipMemcpyHostToDevice, s));
+            const float* qplain = g.emb + int64_t(knn_first) * g.d;
+            Split8Args sp{};
+            sp.q_glob = dq; sp.q_plain = qplain; sp.nq = Qt; sp.n_glob = Qg; sp.d = g.d; sp.na = na8;
+            sp.nrm8 = g.nrm8; sp.qa = c.m8qa; sp.qp = c.m8qp;
+            MARS_TRY(launch_split8(sp, s));
+            if (timing) MARS_HIP(hipEventRecord(c.ev[0], s));
+            int32_t rpw = 0, nwg = 0;
+            scan_grid(n_live, kTargetWgI8, &rpw, &nwg);
+            Scan8MArgs sa{};
+            sa.emb8 = g.emb8; sa.meta8 = g.meta8; sa.n = n_live; sa.d = g.d; sa.ts = g.ts; sa.mods = g.mods;
+            sa.qa = c.m8qa; sa.qp = c.m8qp; sa.tq = c.btq; sa.lambda = lambda;
+            sa.mod_filter = Qg > 0 ? cfg->modality_filter : -1; sa.nq = Qt; sa.n_glob = Qg;
+            sa.self_base = knn_first; sa.part = c.m8part; sa.num_wg = nwg;
+            MARS_TRY(launch_scan8m(sa, na8, s));
+            if (timing) MARS_HIP(hipEventRecord(c.ev[1], s));
+            CertMArgs ca{};
+            ca.part = c.m8part; ca.n_lists = nwg; ca.q = Qt; ca.n_glob = Qg; ca.q_glob = dq; ca.q_plain = qplain;
+            ca.d = g.d; ca.emb = g.emb; ca.ts = g.ts; ca.mods = g.mods; ca.tq = c.btq; ca.lambda = lambda;
+            ca.mod_filter = sa.mod_filter; ca.qp = c.m8qp; ca.nrm8 = g.nrm8; ca.k = std::max(K, 1);
+            ca.knn_k = std::max(knn_k, 1); ca.seeds = c.mseed; ca.status = c.mstat; ca.margin = c.mmargin;
+            ca.knn_out = c.mknn;
+            MARS_TRY(launch_cert_multi8(ca, s));
+            if (timing) MARS_HIP(hipEventRecord(c.ev[2], s));
+            seed_stride = 64;
+        } else {
+            int32_t nrr = 0, nqb = 0;
+            int64_t rpr = 0;
+            batch_grid(n_live, Qt, &nrr, &nqb, &rpr);
+            const int32_t kp = batch_kpart(kMultiCand);
+            MARS_TRY(ensure_batch_scratch(c, Qt, int64_t(nqb) * nrr * 64 * kp));
+            if (Qg > 0) {
+                MARS_HIP(hipMemcpyAsync(c.btq, h_tq, size_t(Qg) * sizeof(float), hipMemcpyHostToDevice, s));
+                MARS_TRY(launch_f32_to_f16_rows(dq, c.bq, int64_t(Qg) * g.d, s));
+                MARS_TRY(launch_query_norms(dq, c.bq, Qg, g.d, c.mqn, s));
+            }
+            if (knn_count > 0)     // the k-NN queries are the nodes' own fp16 rows
+                MARS_HIP(hipMemcpyAsync(c.bq + int64_t(Qg) * g.d, g.emb16 + int64_t(knn_first) * g.d,
+                                        size_t(knn_count) * size_t(g.d) * sizeof(__half), hipMemcpyDeviceToDevice, s));
+            if (timing) MARS_HIP(hipEventRecord(c.ev[0], s));
+            BatchArgs b{};
+            b.emb16 = g.emb16; b.n = n_live; b.d = g.d; b.qh = c.bq; b.q = Qt; b.tq = c.btq; b.ts = g.ts;
+            b.mods = g.mods; b.lambda = Qg > 0 ? lambda : 0.0f; b.mod_filter = Qg > 0 ? cfg->modality_filter : -1;
+            b.k = kMultiCand; b.q_plain = Qg; b.self_base = knn_count > 0 ? knn_first : -1; b.part = c.bpart;
+            b.rows_per_range = rpr; b.n_rranges = nrr; b.n_qblocks = nqb;
+            b.uniform_tq = (Qg == 0 || std::all_of(h_tq, h_tq + Qg, [&](float x) { return x == h_tq[0]; })) ? 1 : 0;
+            MARS_TRY(launch_batch_topk(b, kMultiCand, c.bout, s));
+            if (timing) MARS_HIP(hipEventRecord(c.ev[1], s));
+            if (knn_count > 0)
+                MARS_TRY(launch_knn_rerank(g.emb, knn_first, knn_count, g.d, c.bout + int64_t(Qg) * kMultiCand,
+                                           kMultiCand, knn_k, c.mknn, s));
+            if (Qg > 0) {
+                SeedArgs sa{};
+                sa.emb = fp16 ? static_cast<const void*>(g.emb16) : static_cast<const void*>(g.emb);
+                sa.fp16 = fp16 ? 1 : 0; sa.d = g.d; sa.ts = g.ts; sa.mods = g.mods; sa.queries = dq; sa.tq = c.btq;
+                sa.lambda = lambda; sa.mod_filter = cfg->modality_filter; sa.q = Qg; sa.k = K; sa.cand = c.bout;
+                sa.qn = c.mqn; sa.nrm = g.nrm; sa.seeds = c.mseed; sa.status = c.mstat; sa.margin = c.mmargin;
+                MARS_TRY(launch_multi_seed(sa, s));
+            }
+            if (timing) MARS_HIP(hipEventRecord(c.ev[2], s));
         }
-        if (knn_count > 0)     // the k-NN queries are the nodes' own fp16 rows
-            MARS_HIP(hipMemcpyAsync(c.bq + int64_t(Qg) * g.d, g.emb16 + int64_t(knn_first) * g.d,
-                                    size_t(knn_count) * size_t(g.d) * sizeof(__half), hipMemcpyDeviceToDevice, s));
-        if (timing) MARS_HIP(hipEventRecord(c.ev[0], s));
-        BatchArgs b{};
-        b.emb16 = g.emb16; b.n = n_live; b.d = g.d; b.qh = c.bq; b.q = Qt; b.tq = c.btq; b.ts = g.ts;
-        b.mods = g.mods; b.lambda = Qg > 0 ? lambda : 0.0f; b.mod_filter = Qg > 0 ? cfg->modality_filter : -1;
-        b.k = kMultiCand; b.q_plain = Qg; b.self_base = knn_count > 0 ? knn_first : -1; b.part = c.bpart;
-        b.rows_per_range = rpr; b.n_rranges = nrr; b.n_qblocks = nqb;
-        b.uniform_tq = (Qg == 0 || std::all_of(h_tq, h_tq + Qg, [&](float x) { return x == h_tq[0]; })) ? 1 : 0;
-        MARS_TRY(launch_batch_topk(b, kMultiCand, c.bout, s));
-        if (timing) MARS_HIP(hipEventRecord(c.ev[1], s));
-        if (knn_count > 0)
-            MARS_TRY(launch_knn_rerank(g.emb, knn_first, knn_count, g.d, c.bout + int64_t(Qg) * kMultiCand,
-                                       kMultiCand, knn_k, c.mknn, s));
         std::vector<float> margin(static_cast<size_t>(Qg));
         if (Qg > 0) {
-            SeedArgs sa{};
-            sa.emb = fp16 ? static_cast<const void*>(g.emb16) : static_cast<const void*>(g.emb);
-            sa.fp16 = fp16 ? 1 : 0; sa.d = g.d; sa.ts = g.ts; sa.mods = g.mods; sa.queries = dq; sa.tq = c.btq;
-            sa.lambda = lambda; sa.mod_filter = cfg->modality_filter; sa.q = Qg; sa.k = K; sa.cand = c.bout;
-            sa.qn = c.mqn; sa.nrm = g.nrm; sa.seeds = c.mseed; sa.status = c.mstat; sa.margin = c.mmargin;
-            MARS_TRY(launch_multi_seed(sa, s));
-            if (timing) MARS_HIP(hipEventRecord(c.ev[2], s));
             MultiArgs m{};
             m.ro = g.ro; m.col = g.col; m.mods = g.mods; m.n_live = n_live; m.hops = hops;
             m.hop_decay = cfg->bfs_score_decay; m.k = K; m.rcap = rcap; m.q = Qg; m.seeds = c.mseed;
-            m.seed_stride = kMultiCand;
+            m.seed_stride = seed_stride;
             m.status = c.mstat; m.info = c.minfo; m.vlist = c.mvlist; m.vhop = c.mvhop; m.vpar = c.mvpar;
             m.vro = c.mvro; m.vfin = c.mvfin; m.vscore = c.mvscore;
             m.res = static_cast<ResultHeader*>(c.d_mres);
             m.rec = reinterpret_cast<mars_query_result*>(m.res + Qg);
             MARS_TRY(launch_multi_bfs(m, s));
             VisitScoreArgs va{};
-            va.emb = sa.emb; va.fp16 = sa.fp16; va.d = g.d; va.ts = g.ts; va.mods = g.mods; va.queries = dq;
+            va.emb = fp16 ? static_cast<const void*>(g.emb16) : static_cast<const void*>(g.emb);
+            va.fp16 = fp16 ? 1 : 0; va.d = g.d; va.ts = g.ts; va.mods = g.mods; va.queries = dq;
             va.tq = c.btq; va.lambda = lambda; va.mod_filter = cfg->modality_filter; va.q = Qg;
             va.status = c.mstat; va.info = c.minfo; va.vlist = c.mvlist; va.vfin = c.mvfin;
             MARS_TRY(launch_visit_scores(va, s));
             MARS_TRY(launch_multi_select(m, s));
             if (timing) MARS_HIP(hipEventRecord(c.ev[3], s));
             MARS_HIP(hipMemcpyAsync(margin.data(), c.mmargin, size_t(Qg) * sizeof(float), hipMemcpyDeviceToHost, s));
+        } else if (timing) {
+            MARS_HIP(hipEventRecord(c.ev[3], s));
         }
-        if (knn_count > 0)
+        if (knn_count > 0) {
             MARS_HIP(hipMemcpyAsync(out_knn, c.mknn, size_t(knn_count) * size_t(knn_k) * sizeof(int32_t),
                                     hipMemcpyDeviceToHost, s));
+            if (use8)
+                MARS_HIP(hipMemcpyAsync(knn_status.data(), c.mstat + Qg, size_t(knn_count) * sizeof(int32_t),
+                                        hipMemcpyDeviceToHost, s));
+        }
         MARS_HIP(hipStreamSynchronize(s));
+        for (const int32_t x : knn_status) knn_fallback = knn_fallback || x != kMultiOk;
         if (Qg > 0) {
             const auto* hdr = static_cast<const ResultHeader*>(c.h_mres);
             const auto* rec = reinterpret_cast<const mars_query_result*>(hdr + Qg);
@@ -1685,18 +1745,26 @@ int mars_query_global_batch_knn(const mars_graph* gh, mars_ctx* ch, const float*
                 ++st.batched;
                 st.min_margin = std::min(st.min_margin, margin[size_t(j)]);
             }
-            if (timing) {
-                float ms = 0.0f;
-                MARS_HIP(hipEventElapsedTime(&ms, c.ev[0], c.ev[1]));
-                st.gpu_ms_scan = ms;
-                MARS_HIP(hipEventElapsedTime(&ms, c.ev[1], c.ev[2]));
-                st.gpu_ms_seeds = ms;
-                MARS_HIP(hipEventElapsedTime(&ms, c.ev[2], c.ev[3]));
-                st.gpu_ms_bfs = ms;
-                MARS_HIP(hipEventElapsedTime(&ms, c.ev[0], c.ev[3]));
-                st.gpu_ms_total = ms;
-            }
         }
+        if (timing) {
+            float ms = 0.0f;
+            MARS_HIP(hipEventElapsedTime(&ms, c.ev[0], c.ev[1]));
+            st.gpu_ms_scan = ms;
+            MARS_HIP(hipEventElapsedTime(&ms, c.ev[1], c.ev[2]));
+            st.gpu_ms_seeds = ms;
+            MARS_HIP(hipEventElapsedTime(&ms, c.ev[2], c.ev[3]));
+            st.gpu_ms_bfs = ms;
+            MARS_HIP(hipEventElapsedTime(&ms, c.ev[0], c.ev[3]));
+            st.gpu_ms_total = ms;
+        }
+    }
+    if (knn_fallback) {
+        // a neighbour search the int8 certificate did not cover: all of them again on the
+        // fp16 scan with exact rescoring
+        mars_batch_stats s2{};
+        MARS_TRY(global_batch_impl(gh, ch, nullptr, 0, nullptr, nullptr, nullptr, 0, nullptr, &s2, knn_first,
+                                   knn_count, knn_k, out_knn, false));
+        st.candidate_rows = 24;
     }
     const auto t1 = clk::now();
     for (const int32_t j : q1)
@@ -1707,6 +1775,23 @@ int mars_query_global_batch_knn(const mars_graph* gh, mars_ctx* ch, const float*
     st.wall_us = std::chrono::duration<double, std::micro>(t2 - t0).count();
     if (stats) *stats = st;
     return MARS_OK;
+}
+
+}  // namespace
+
+int mars_query_global_batch(const mars_graph* gh, mars_ctx* ch, const float* dq, int32_t Q, const float* h_tq,
+                            const mars_retrieval_config* cfg, mars_query_result* out, int32_t cap,
+                            int32_t* n_out, mars_batch_stats* stats) {
+    MARS_CHECK(Q > 0, MARS_ERR_INVALID, "bad arguments");
+    return global_batch_impl(gh, ch, dq, Q, h_tq, cfg, out, cap, n_out, stats, 0, 0, 0, nullptr, true);
+}
+
+int mars_query_global_batch_knn(const mars_graph* gh, mars_ctx* ch, const float* dq, int32_t Q, const float* h_tq,
+                                const mars_retrieval_config* cfg, mars_query_result* out, int32_t cap,
+                                int32_t* n_out, mars_batch_stats* stats, int32_t knn_first, int32_t knn_count,
+                                int32_t knn_k, int32_t* out_knn) {
+    return global_batch_impl(gh, ch, dq, Q, h_tq, cfg, out, cap, n_out, stats, knn_first, knn_count, knn_k, out_knn,
+                             true);
 }
 
 

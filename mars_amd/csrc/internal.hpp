@@ -272,6 +272,10 @@ struct Ctx {
     int32_t mcap_q = 0;
     int32_t* mknn = nullptr;       // neighbour lists of a shared scan's k-NN queries
     int32_t mknn_cap = 0;          // nodes
+    // multi-query int8 pass (allocated on first use, for 8 kScan8MMaxA queries)
+    uint64_t* m8part = nullptr;    // [q][kScan8MPart] workgroup lists
+    unsigned char* m8qa = nullptr; // A operands: kScan8MMaxA x d / 64 x 1 KB
+    float* m8qp = nullptr;         // [q][4] query split terms
     void* h_mres = nullptr;        // pinned, mapped: [q] ResultHeader then [q][rcap] results
     void* d_mres = nullptr;
     size_t mres_bytes = 0;
@@ -365,6 +369,41 @@ constexpr int32_t kScan8MaxLists = 512;    // int8 scan workgroups = lists k_cer
 constexpr int32_t kScan8List = 16;         // keys per workgroup list
 bool scan8_dim_supported(int32_t d);
 int launch_scan8(const ScanArgs& a, hipStream_t s);
+// The int8 scan for up to 8 kScan8MMaxA queries in one pass (scan8m.hip): query slot j
+// holds rows 2 (j % 8), 2 (j % 8) + 1 of A operand j / 8.
+constexpr int32_t kScan8MMaxA = 2;
+constexpr int64_t kScan8MPart = int64_t(kScan8MaxLists) * kScan8List;   // keys per query
+struct Split8Args {
+    const float* q_glob;     // [n_glob][d] global queries
+    const float* q_plain;    // [nq - n_glob][d] plain queries (a node's own fp32 row)
+    int32_t nq;
+    int32_t n_glob;
+    int32_t d;
+    int32_t na;              // A operands (slots 8 na)
+    const uint32_t* nrm8;
+    void* qa;                // out: [na][d / 64][64] x 16 bytes
+    float* qp;               // out: [8 na][4] s_hi, s_lo, tau, |q|
+};
+struct Scan8MArgs {
+    const void* emb8;
+    const float* meta8;
+    int64_t n;
+    int32_t d;
+    const float* ts;
+    const int32_t* mods;
+    const void* qa;
+    const float* qp;
+    const float* tq;         // [n_glob] query times
+    float lambda;
+    int32_t mod_filter;      // global queries
+    int32_t nq;
+    int32_t n_glob;          // queries [0, n_glob) global; the rest plain dots
+    int64_t self_base;       // plain query j skips row self_base + j - n_glob
+    uint64_t* part;          // [nq][kScan8MPart]: workgroup b's 16 best keys at [16 b ..]
+    int32_t num_wg;
+};
+int launch_split8(const Split8Args& a, hipStream_t s);
+int launch_scan8m(const Scan8MArgs& a, int na, hipStream_t s);
 // Quantizes rows [r0, r1) of emb into emb8 / meta8 and raises nrm8.
 int launch_convert_i8(const float* emb, int64_t r0, int64_t r1, int32_t d, int8_t* emb8, float* meta8,
                       uint32_t* nrm8, hipStream_t s);
@@ -614,6 +653,31 @@ struct CertArgs {
     uint32_t seq;
 };
 int launch_cert_bfs(const CertArgs& a, const struct MultiArgs& m, hipStream_t s);   // + BFS of query 0 of m
+// Certified seeds / neighbours of the queries of one k_scan8m pass (one workgroup each).
+struct CertMArgs {
+    const uint64_t* part;    // [q][kScan8MPart] (launch_scan8m)
+    int32_t n_lists;         // scan workgroups
+    int32_t q;
+    int32_t n_glob;          // queries [0, n_glob) global, the rest plain
+    const float* q_glob;
+    const float* q_plain;
+    int32_t d;
+    const float* emb;        // fp32 rows
+    const float* ts;
+    const int32_t* mods;
+    const float* tq;
+    float lambda;
+    int32_t mod_filter;
+    const float* qp;         // launch_split8's per-query terms (tau, |q|)
+    const uint32_t* nrm8;
+    int32_t k;               // seeds per global query (<= 64)
+    int32_t knn_k;           // neighbours per plain query (<= 64)
+    uint64_t* seeds;         // [n_glob][64]
+    int32_t* status;         // [q]
+    float* margin;           // [q]
+    int32_t* knn_out;        // [q - n_glob][knn_k] (device)
+};
+int launch_cert_multi8(const CertMArgs& a, hipStream_t s);
 int launch_multi_bfs(const MultiArgs& a, hipStream_t s);
 int launch_visit_scores(const VisitScoreArgs& a, hipStream_t s);
 int launch_multi_select(const MultiArgs& a, hipStream_t s);

@@ -783,6 +783,68 @@ __global__ __launch_bounds__(kFinThreads) void k_multi_select(MultiArgs m) {
     signal_done(m.done, m.seq);
 }
 
+// The c (<= 64) best keys of nl (<= kScan8MaxLists) ascending lists of kScan8List (16)
+// keys at part, one per int8 scan workgroup; wave 0 returns them (lane i: the i-th
+// smallest). The lists are read as 1 KB blocks of 8, one block per wave load instruction
+// (lane l: keys 2l, 2l + 1 of the block, i.e. keys 2 (l & 7), +1 of list 8b + l / 8), wave w
+// taking blocks w, w + 16, ...
+// cut = the c-th smallest of the lists' first keys: c lists hold a key <= cut, so the c
+// best keys are <= cut, and only those c lists hold keys <= cut: at most c * 16 keys
+// (with cut = kEmptyKey, fewer than c lists hold any), compacted into LDS, one per
+// thread for the final selection. s_lmin = the smallest 16th key: a row that a full list
+// dropped has a key above it (the certificate's bound takes it into account).
+__device__ uint64_t merge_lists8(FinShared& sh, const uint64_t* part, int nl, int c, uint64_t& s_lmin,
+                                 uint64_t& s_cut) {
+    const int tid = int(threadIdx.x), lane = lane_id(), wave = tid >> 6;
+    static_assert(kScan8List == 16 && kScan8MaxLists <= 8 * 4 * kFinWaves, "block layout");
+    static_assert(kScan8MaxLists + 64 * kScan8List <= kSortCap && 64 * kScan8List <= kFinThreads, "buffers");
+    uint64_t x[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int b = wave + i * kFinWaves;
+        const bool on = 8 * b + (lane >> 3) < nl;
+        const u64x2 v = on ? reinterpret_cast<const u64x2*>(part + int64_t(b) * 128)[lane]
+                           : u64x2{kEmptyKey, kEmptyKey};
+        x[2 * i] = v.x;
+        x[2 * i + 1] = v.y;
+    }
+    uint64_t* k1 = sh.u.sort.key;                    // the lists' first keys
+    uint64_t* buf = sh.u.sort.key + kScan8MaxLists;  // the keys <= cut
+    uint64_t l16 = kEmptyKey;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int li = 8 * (wave + i * kFinWaves) + (lane >> 3);
+        if ((lane & 7) == 0) k1[li] = li < nl ? x[2 * i] : kEmptyKey;
+        if ((lane & 7) == 7 && x[2 * i + 1] < l16) l16 = x[2 * i + 1];
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const uint64_t y = __shfl_xor(l16, o);
+        l16 = y < l16 ? y : l16;
+    }
+    if (tid == 0) { s_lmin = kEmptyKey; sh.s_misc[4] = 0; }
+    __syncthreads();
+    if (lane == 0) atomicMin(reinterpret_cast<unsigned long long*>(&s_lmin), (unsigned long long)l16);
+    uint64_t l1 = kEmptyKey, t1 = kEmptyKey;
+    wave_offer(l1, t1, tid < nl ? k1[tid] : kEmptyKey, lane, c);
+    l1 = tree_merge(sh, l1, c, (nl + 63) / 64);
+    if (wave == 0 && lane == c - 1) s_cut = l1;
+    __syncthreads();
+    const uint64_t cut = s_cut;
+    int cnt = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) cnt += (x[j] <= cut && x[j] != kEmptyKey) ? 1 : 0;
+    int at = cnt ? atomicAdd(&sh.s_misc[4], cnt) : 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+        if (x[j] <= cut && x[j] != kEmptyKey) buf[at++] = x[j];
+    __syncthreads();
+    const int m = sh.s_misc[4];                      // <= 64 * 16 = kFinThreads
+    uint64_t list = kEmptyKey, thr = kEmptyKey;
+    wave_offer(list, thr, tid < m ? buf[tid] : kEmptyKey, lane, c);
+    return tree_merge(sh, list, c, (m + 63) / 64);
+}
+
 // ---- certified Q=1 global query ---------------------------------------------------------
 // The candidate scan kept its c best keys per workgroup in part. Here they are merged to
 // the c best overall, rescored in the fp32 scan's arithmetic (QF32 dot, 16-lane
@@ -812,62 +874,8 @@ __global__ __launch_bounds__(kFinThreads) void k_cert_bfs(CertArgs a, MultiArgs 
     stamp_at(0);
     uint64_t list = kEmptyKey, thr = kEmptyKey;
     if (a.n_lists > 0) {
-        // A. the c (<= 64) best keys of n_lists (<= kScan8MaxLists) ascending lists of
-        // kScan8List (16) keys, one per scan workgroup. The lists are read as 1 KB blocks of 8,
-        // one block per wave load instruction (lane l: keys 2l, 2l + 1 of the block, i.e. keys
-        // 2 (l & 7), +1 of list 8b + l / 8), wave w taking blocks w, w + 16, ...
-        // cut = the c-th smallest of the lists' first keys: c lists hold a key <= cut, so the c
-        // best keys are <= cut, and only those c lists hold keys <= cut: at most c * 16 keys
-        // (with cut = kEmptyKey, fewer than c lists hold any), compacted into LDS, one per
-        // thread for the final selection. lmin = the smallest 16th key: a row that a full list
-        // dropped has a key above it (the certificate's bound takes it into account).
-        static_assert(kScan8List == 16 && kScan8MaxLists <= 8 * 4 * kFinWaves, "block layout");
-        static_assert(kScan8MaxLists + 64 * kScan8List <= kSortCap && 64 * kScan8List <= kFinThreads, "buffers");
-        const int nl = a.n_lists;
-        uint64_t x[8];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int b = wave + i * kFinWaves;
-            const bool on = 8 * b + (lane >> 3) < nl;
-            const u64x2 v = on ? reinterpret_cast<const u64x2*>(a.part + int64_t(b) * 128)[lane]
-                               : u64x2{kEmptyKey, kEmptyKey};
-            x[2 * i] = v.x;
-            x[2 * i + 1] = v.y;
-        }
-        uint64_t* k1 = sh.u.sort.key;                    // the lists' first keys
-        uint64_t* buf = sh.u.sort.key + kScan8MaxLists;  // the keys <= cut
-        uint64_t l16 = kEmptyKey;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int li = 8 * (wave + i * kFinWaves) + (lane >> 3);
-            if ((lane & 7) == 0) k1[li] = li < nl ? x[2 * i] : kEmptyKey;
-            if ((lane & 7) == 7 && x[2 * i + 1] < l16) l16 = x[2 * i + 1];
-        }
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) {
-            const uint64_t y = __shfl_xor(l16, o);
-            l16 = y < l16 ? y : l16;
-        }
-        if (tid == 0) { s_lmin = kEmptyKey; sh.s_misc[4] = 0; }
-        __syncthreads();
-        if (lane == 0) atomicMin(reinterpret_cast<unsigned long long*>(&s_lmin), (unsigned long long)l16);
-        uint64_t l1 = kEmptyKey, t1 = kEmptyKey;
-        wave_offer(l1, t1, tid < nl ? k1[tid] : kEmptyKey, lane, c);
-        l1 = tree_merge(sh, l1, c, (nl + 63) / 64);
-        if (wave == 0 && lane == c - 1) s_cut = l1;
-        __syncthreads();
-        const uint64_t cut = s_cut;
-        int cnt = 0;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) cnt += (x[j] <= cut && x[j] != kEmptyKey) ? 1 : 0;
-        int at = cnt ? atomicAdd(&sh.s_misc[4], cnt) : 0;
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-            if (x[j] <= cut && x[j] != kEmptyKey) buf[at++] = x[j];
-        __syncthreads();
-        const int m = sh.s_misc[4];                      // <= 64 * 16 = kFinThreads
-        wave_offer(list, thr, tid < m ? buf[tid] : kEmptyKey, lane, c);
-        list = tree_merge(sh, list, c, (m + 63) / 64);
+        // A. the c (<= 64) best keys of the scan workgroups' lists
+        list = merge_lists8(sh, a.part, a.n_lists, c, s_lmin, s_cut);
     } else {
         // A. the c best candidate keys (the finalize kernel's merge, 8 loads in flight per lane)
         const int n_part = int(*a.gcnt);
@@ -1115,6 +1123,86 @@ __global__ __launch_bounds__(kFinThreads) void k_cert_bfs(CertArgs a, MultiArgs 
     stamp_at(6);
     flush_stamps(s_st, 7, a.stamps);
     signal_done(a.done, a.seq);
+}
+
+// ---- certified seeds of up to 16 queries after k_scan8m -----------------------------
+// One workgroup per query j: the 64 best upper-bound keys of its scan lists (merge_lists8),
+// rescored exactly (QF32 dot and 16-lane reduction as the fp32 scan; global queries then
+// fuse_score with their time and the modality filter, plain queries keep the dot) and
+// sorted; the K best are certified when the K-th exact key's score beats the score of the
+// smallest key any row outside the candidates can hold (k_cert_bfs's int8 argument). A
+// global query's seeds go to seeds[64 j ..] (ascending keys, kEmptyKey padded); a plain
+// query's K = knn_k neighbour ids to knn_out[knn_k (j - n_glob) ..].
+template <typename QF>
+__global__ __launch_bounds__(kFinThreads) void k_cert_multi8(CertMArgs a) {
+    __shared__ FinShared sh;
+    __shared__ uint64_t s_cand[64];
+    __shared__ uint64_t s_exact[64];
+    __shared__ uint64_t s_lmin;
+    __shared__ uint64_t s_cut;
+    const int j = int(blockIdx.x);
+    const int tid = int(threadIdx.x), lane = lane_id(), wave = tid >> 6, g = tid >> 4, sub = tid & 15;
+    const bool plain = j >= a.n_glob;
+    constexpr int c = 64;
+    const uint64_t list = merge_lists8(sh, a.part + int64_t(j) * kScan8MPart, a.n_lists, c, s_lmin, s_cut);
+    const float* q = plain ? a.q_plain + int64_t(j - a.n_glob) * a.d : a.q_glob + int64_t(j) * a.d;
+    QF qf;
+    qf.load(q, sub);
+    if (wave == 0) s_cand[lane] = list;
+    __syncthreads();
+    const uint64_t ck = s_cand[g];
+    uint64_t key = kEmptyKey;
+    if (ck != kEmptyKey) {                       // uniform over the group
+        const int32_t id = key_id(ck);
+        const float dot = row16_sum(qf.dot(a.emb + int64_t(id) * a.d, sub));
+        float sc = dot;
+        if (!plain) {
+            const QueryTerms t{a.tq[j], a.lambda, a.mod_filter, -1, 0.0f};
+            sc = fuse_score(dot, a.ts[id], (a.mod_filter >= 0) ? a.mods[id] : 0, -1, t);
+        }
+        key = make_key(sc, uint32_t(id));
+    }
+    if (sub == 0) s_exact[g] = key;
+    __syncthreads();
+    if (wave != 0) return;
+    const uint64_t x = wave_sort64(s_exact[lane], lane);
+    const uint64_t c_last = __shfl(s_cand[lane], c - 1);
+    const int K = plain ? a.knn_k : a.k;
+    const int kk = K < c ? K : c;
+    const uint64_t kth = __shfl(x, kk - 1);
+    bool ok = false;
+    float margin = __builtin_inff();
+    // the bounds must be finite: the row bound maxima and this query's terms
+    const double u = 0x1p-24;
+    const double cm = double(__uint_as_float(a.nrm8[0])), en = double(__uint_as_float(a.nrm8[1]));
+    const double qn = double(a.qp[4 * j + 3]), tau = double(a.qp[4 * j + 2]);
+    const double eps = (cm * qn + 4.0 * u * (en + cm) * qn) * 1.01 + tau + 1e-30 * double(a.d);
+    const uint64_t bnd = s_lmin < c_last ? s_lmin : c_last;
+    if (K <= c) {
+        if (bnd == kEmptyKey) {
+            ok = true;                           // every row with a key was a candidate
+        } else if (eps < 1e30) {                 // also false for NaN bounds
+            const float s8 = key_score(bnd), s32 = key_score(kth);
+            if (s8 == -FLT_MAX) {
+                ok = en * qn * 2.0 < double(FLT_MAX);       // the bound key is a filtered row
+            } else {
+                const double mg = double(s32) - double(s8);
+                ok = mg > 0.0;
+                margin = float(mg);
+            }
+        } else {
+            margin = -__builtin_inff();
+        }
+    }
+    if (plain) {
+        if (lane < kk) a.knn_out[int64_t(j - a.n_glob) * a.knn_k + lane] = (ok && x != kEmptyKey) ? key_id(x) : -1;
+    } else {
+        a.seeds[int64_t(j) * 64 + lane] = (ok && lane < kk) ? x : kEmptyKey;
+    }
+    if (lane == 0) {
+        a.status[j] = ok ? kMultiOk : kMultiUncertified;
+        a.margin[j] = margin;
+    }
 }
 
 // NCH > 0 (d = 64 NCH, NCH <= 12): a member row's NCH 16-byte loads are all issued
@@ -1427,6 +1515,19 @@ int launch_cert_bfs(const CertArgs& a, const MultiArgs& m, hipStream_t s) {
         }
     }
     return set_error(MARS_ERR_UNSUPPORTED, "certified query: embedding_dim %d unsupported", a.d);
+}
+
+int launch_cert_multi8(const CertMArgs& a, hipStream_t s) {
+    MARS_CHECK(a.q >= 1 && a.n_lists >= 1 && a.n_lists <= kScan8MaxLists && a.k <= 64 && a.knn_k <= 64,
+               MARS_ERR_INVALID, "multi-query certificate: %d queries, %d lists", a.q, a.n_lists);
+    switch (a.d) {
+        case 256: MARS_LAUNCH(k_cert_multi8<QF32<4>>, dim3(unsigned(a.q)), dim3(kFinThreads), 0, s, a); return MARS_OK;
+        case 512: MARS_LAUNCH(k_cert_multi8<QF32<8>>, dim3(unsigned(a.q)), dim3(kFinThreads), 0, s, a); return MARS_OK;
+        case 768: MARS_LAUNCH(k_cert_multi8<QF32<12>>, dim3(unsigned(a.q)), dim3(kFinThreads), 0, s, a); return MARS_OK;
+        case 1024: MARS_LAUNCH(k_cert_multi8<QF32<16>>, dim3(unsigned(a.q)), dim3(kFinThreads), 0, s, a); return MARS_OK;
+        default: break;
+    }
+    return set_error(MARS_ERR_UNSUPPORTED, "multi-query certificate: embedding_dim %d", a.d);
 }
 
 int launch_multi_bfs(const MultiArgs& a, hipStream_t s) {

@@ -53,7 +53,7 @@ def test_struct_layouts():
     assert C.sizeof(_lib.TiledResultC) == 12                      # TiledQueryResult
     assert C.sizeof(_lib.TiledConfigC) == 20
     assert C.sizeof(_lib.InsertStatsC) == 48
-    assert C.sizeof(_lib.StatsC) == 56 and _lib.StatsC.wall_us.offset == 48
+    assert C.sizeof(_lib.StatsC) == 64 and _lib.StatsC.wall_us.offset == 56
     assert _lib.InsertStatsC.queryable_us.offset == 24
     assert C.sizeof(_lib.StreamBenchC) == 128 and _lib.StreamBenchC.knn_k.offset == 88
     assert C.sizeof(_lib.BatchStatsC) == 64 and _lib.BatchStatsC.wall_us.offset == 48
