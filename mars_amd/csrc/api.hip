@@ -38,15 +38,6 @@ constexpr int32_t kTargetWg = 512;
 constexpr int32_t kTargetWgF16 = 512;
 constexpr int32_t kTargetWgI8 = kScan8MaxLists;
 
-// Widths with an exact-rescoring kernel (k_cert_bfs<QF32<d / 64>>): the certified query
-// runs only at these; any other width is answered by the fp32 scan.
-bool cert_dim_supported(int32_t d) { return d == 256 || d == 384 || d == 512 || d == 768 || d == 1024; }
-
-// The certified query scans the int8 copy when there is one (d <= 1024: the exact
-// rescoring's QF32 layouts), else the fp16 copy.
-bool cert_uses_int8(const Graph& g) {
-    return g.emb8 && g.meta8 && g.nrm8 && scan8_dim_supported(g.d) && cert_dim_supported(g.d);
-}
 
 int ensure_device(int* dev) {
     int d = 0;

@@ -230,9 +230,61 @@ double us_since(std::chrono::steady_clock::time_point t0) {
     return std::chrono::duration<double, std::micro>(std::chrono::steady_clock::now() - t0).count();
 }
 
-// k nearest neighbours of nodes [first, first + nq) among [0, n): batched fp16 scan
-// (no decay, no filter, self excluded) + exact fp32 rescoring of 16 candidates.
+// Up to 16 nodes over the int8 copy: one k_scan8m pass (plain dots, self excluded), then
+// k_cert_multi8's certified exact neighbours into g.ins_nbrs. *done = false when a node's
+// certificate did not hold (the caller then runs the fp16 search for all of them).
+int insert_knn_int8(Graph& g, int64_t first, int32_t nq, int64_t n, int32_t k, hipStream_t s, bool* done) {
+    *done = false;
+    const int32_t qmax = 8 * kScan8MMaxA;
+    if (!g.ins8_part) {
+        MARS_TRY(dmalloc(&g.ins8_part, size_t(qmax) * size_t(kScan8MPart)));
+        MARS_TRY(dmalloc(&g.ins8_qa, size_t(kScan8MMaxA) * size_t(g.d / 64) * 1024));
+        MARS_TRY(dmalloc(&g.ins8_qp, size_t(qmax) * 4));
+        MARS_TRY(dmalloc(&g.ins8_stat, size_t(qmax)));
+        MARS_TRY(dmalloc(&g.ins8_margin, size_t(qmax)));
+    }
+    if (nq > g.ins_cap_q) {
+        dfree(g.ins_nbrs);
+        g.ins_cap_q = 0;
+        MARS_TRY(dmalloc(&g.ins_nbrs, size_t(nq) * 16));
+        g.ins_cap_q = nq;
+    }
+    const float* rows = g.emb + first * g.d;
+    const int32_t na = (nq + 7) / 8;
+    Split8Args sp{};
+    sp.q_glob = nullptr; sp.q_plain = rows; sp.nq = nq; sp.n_glob = 0; sp.d = g.d; sp.na = na; sp.nrm8 = g.nrm8;
+    sp.qa = g.ins8_qa; sp.qp = g.ins8_qp;
+    MARS_TRY(launch_split8(sp, s));
+    int32_t rpw = 0, nwg = 0;
+    scan_grid(n, kScan8MaxLists, &rpw, &nwg);
+    Scan8MArgs sa{};
+    sa.emb8 = g.emb8; sa.meta8 = g.meta8; sa.n = n; sa.d = g.d; sa.ts = g.ts; sa.mods = g.mods; sa.qa = g.ins8_qa;
+    sa.qp = g.ins8_qp; sa.tq = nullptr; sa.lambda = 0.0f; sa.mod_filter = -1; sa.nq = nq; sa.n_glob = 0;
+    sa.self_base = first; sa.part = g.ins8_part; sa.num_wg = nwg;
+    MARS_TRY(launch_scan8m(sa, na, s));
+    CertMArgs ca{};
+    ca.part = g.ins8_part; ca.n_lists = nwg; ca.q = nq; ca.n_glob = 0; ca.q_glob = nullptr; ca.q_plain = rows;
+    ca.d = g.d; ca.emb = g.emb; ca.ts = g.ts; ca.mods = g.mods; ca.tq = nullptr; ca.lambda = 0.0f;
+    ca.mod_filter = -1; ca.qp = g.ins8_qp; ca.nrm8 = g.nrm8; ca.k = 1; ca.knn_k = k; ca.seeds = nullptr;
+    ca.status = g.ins8_stat; ca.margin = g.ins8_margin; ca.knn_out = g.ins_nbrs;
+    MARS_TRY(launch_cert_multi8(ca, s));
+    int32_t stat[8 * kScan8MMaxA];
+    MARS_HIP(hipMemcpyAsync(stat, g.ins8_stat, size_t(nq) * sizeof(int32_t), hipMemcpyDeviceToHost, s));
+    MARS_HIP(hipStreamSynchronize(s));
+    *done = std::all_of(stat, stat + nq, [](int32_t x) { return x == kMultiOk; });
+    return MARS_OK;
+}
+
+// k nearest neighbours of nodes [first, first + nq) among [0, n): with the int8 copy and
+// at most 16 nodes, one int8 pass with certified exact neighbours; otherwise (or when a
+// certificate failed) a batched fp16 scan (no decay, no filter, self excluded) + exact
+// fp32 rescoring of 16 candidates.
 int insert_knn(Graph& g, int64_t first, int32_t nq, int64_t n, int32_t k, hipStream_t s) {
+    if (nq >= 1 && nq <= 8 * kScan8MMaxA && k <= 16 && cert_uses_int8(g)) {
+        bool done = false;
+        MARS_TRY(insert_knn_int8(g, first, nq, n, k, s, &done));
+        if (done) return MARS_OK;
+    }
     int32_t nrr = 0, nqb = 0;
     int64_t rpr = 0, part_keys = 0;
     const int32_t ranges = n <= kInsertKnnNarrowRows ? kInsertKnnRanges : 256;
@@ -479,6 +531,7 @@ int graph_insert_free(Graph& g) {
     g.ins_dev = nullptr;
     g.ins_dev_bytes = 0;
     dfree(g.ins_part); dfree(g.ins_cand); dfree(g.ins_nbrs); dfree(g.ins_tq);
+    dfree(g.ins8_part); dfree(g.ins8_qa); dfree(g.ins8_qp); dfree(g.ins8_stat); dfree(g.ins8_margin);
     g.ins_part_cap = 0;
     g.ins_cap_q = 0;
     for (auto& e : g.ins_ev) {

@@ -174,6 +174,12 @@ struct Graph {
     float* ins_tq = nullptr;             // zero query times (no decay)
     int32_t ins_cap_q = 0;
     hipEvent_t ins_ev[2] = {nullptr, nullptr};
+    // the neighbour search of up to 16 new nodes over the int8 copy (one k_scan8m pass)
+    uint64_t* ins8_part = nullptr;       // [16][kScan8MPart]
+    unsigned char* ins8_qa = nullptr;    // A operands
+    float* ins8_qp = nullptr;            // [16][4]
+    int32_t* ins8_stat = nullptr;        // [16] certificate status
+    float* ins8_margin = nullptr;        // [16]
     // importance and edge-hit counters (allocated on request, under the graph mutex)
     float* imp = nullptr;                // cap_n: importance of each node
     int32_t* hits = nullptr;             // cap_e: BFS hits per col slot; slots no row uses hold 0
@@ -404,6 +410,14 @@ struct Scan8MArgs {
 };
 int launch_split8(const Split8Args& a, hipStream_t s);
 int launch_scan8m(const Scan8MArgs& a, int na, hipStream_t s);
+// Widths with an exact-rescoring kernel (k_cert_bfs / k_cert_multi8 over QF32<d / 64>): the
+// certified paths run only at these; any other width is answered by the fp32 scan.
+inline bool cert_dim_supported(int32_t d) { return d == 256 || d == 384 || d == 512 || d == 768 || d == 1024; }
+// The certified paths scan the int8 copy when there is one (d <= 1024: the exact
+// rescoring's QF32 layouts), else the fp16 copy.
+inline bool cert_uses_int8(const Graph& g) {
+    return g.emb8 && g.meta8 && g.nrm8 && scan8_dim_supported(g.d) && cert_dim_supported(g.d);
+}
 // Quantizes rows [r0, r1) of emb into emb8 / meta8 and raises nrm8.
 int launch_convert_i8(const float* emb, int64_t r0, int64_t r1, int32_t d, int8_t* emb8, float* meta8,
                       uint32_t* nrm8, hipStream_t s);

@@ -116,3 +116,28 @@ def test_int8_batch_widths(d):
             check_knn_exact(c.embeddings, 100, knn, 8)
     finally:
         dev.close()
+
+
+def test_insert_knn_over_int8(corpus_10k):
+    """An insert of up to 16 nodes finds their neighbours with one int8 pass: the lists
+    are the exact k-NN among all rows (near-ties aside) and equal the batched neighbour
+    search's over the same rows."""
+    c = corpus.make_corpus(8020, 768, seed=91)
+    base = 8000
+    g = corpus.nsn_graph(corpus.Corpus(c.embeddings[:base], c.modalities[:base], c.timestamps[:base],
+                                       c.episode_ids[:base], 91))
+    dev = Dev(g.embeddings, g.modalities, g.timestamps, g.row_offsets, g.col_indices, g.episode_ids, cap_nodes=8020)
+    mars_amd.upload_int8_embeddings(dev.dg)
+    try:
+        st, got = mars_amd.insert_nodes(dev.dg, c.embeddings[base:base + 10], c.modalities[base:base + 10],
+                                        c.timestamps[base:base + 10], c.episode_ids[base:base + 10], knn_k=8,
+                                        return_knn=True)
+        assert st.nodes_added == 10
+        check_knn_exact(c.embeddings[:base + 10], base, got, 8)
+        bst = BatchStats()
+        _, knn = mars_amd.query_global_batch_knn(dev.dg, dev.ctx, 0, 0, T_Q, RetrievalConfig(), base, 10, 8,
+                                                 stats=bst)
+        assert bst.candidate_rows == 8
+        np.testing.assert_array_equal(knn, got)
+    finally:
+        dev.close()
