@@ -88,15 +88,23 @@ __global__ __launch_bounds__(256) void k_scan(ScanArgs a) {
 constexpr int kFinThreads = 1024;
 constexpr int kFinWaves = kFinThreads / 64;
 
+// Inclusive prefix sum across the wave on DPP: row_shr 1, 2, 4, 8 within each 16-lane row
+// (lanes shifted in from outside the row read 0), then row_bcast:15 carries row 0's and row
+// 2's totals into rows 1 and 3, and row_bcast:31 the first two rows' total into rows 2, 3.
+__device__ inline int wave_incl_scan(int v) {
+    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, true);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, true);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, true);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, true);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false);
+    return v;
+}
+
 // Exclusive prefix sum across the block; *total gets the block sum.
 __device__ inline int block_excl_scan(int v, int* s_wave, int* total) {
     const int lane = lane_id(), wave = int(threadIdx.x >> 6);
-    int incl = v;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const int y = __shfl_up(incl, unsigned(o));
-        if (lane >= o) incl += y;
-    }
+    const int incl = wave_incl_scan(v);
     if (lane == 63) s_wave[wave] = incl;
     __syncthreads();
     int off = 0, tot = 0;
@@ -161,6 +169,7 @@ struct FinShared {
     } u;
     uint64_t lists[kFinWaves][64];
     int64_t ro_cache[kRoCache];          // row words of visit positions < kRoCache (also in vro)
+    int32_t seed_id[64];                 // the seeds' node ids (visit positions 0 .. ns - 1)
     int s_wave[kFinWaves];
     int s_misc[8];
 };
@@ -277,7 +286,7 @@ __device__ int bfs_lds(FinShared& sh, const FinalizeArgs& a, int ns, int* levels
     if (tid == 0) { sh.s_misc[4] = 0; sh.s_misc[5] = 0; }
     __syncthreads();
     if (tid < ns) {
-        const int slot = hash_find_or_insert(sh, ld_coherent(a.vlist + tid));
+        const int slot = hash_find_or_insert(sh, sh.seed_id[tid]);
         if (slot >= 0) sh.u.bfs.hval[slot] = uint32_t(tid);          // hop 0, position tid
     }
     __syncthreads();
@@ -608,6 +617,7 @@ __global__ __launch_bounds__(kFinThreads) void k_finalize(FinalizeArgs a) {
             a.vhop[lane] = 0;
             a.vscore[lane] = sc;
             a.vro[lane] = sh.ro_cache[lane] = a.ro[id];
+            sh.seed_id[lane] = id;
         }
         if (lane == 0) sh.s_misc[0] = ns;
     }
@@ -690,6 +700,7 @@ __device__ int multi_bfs_query(FinShared& sh, const MultiArgs& m, int j, int* le
             a.vpar[lane] = -1;
             a.vscore[lane] = key_score(key);
             a.vro[lane] = sh.ro_cache[lane] = a.ro[id];
+            sh.seed_id[lane] = id;
         }
         if (lane == 0) sh.s_misc[0] = ns;
     }
@@ -817,10 +828,13 @@ __device__ uint64_t merge_lists8(FinShared& sh, const uint64_t* part, int nl, in
         if ((lane & 7) == 0) k1[li] = li < nl ? x[2 * i] : kEmptyKey;
         if ((lane & 7) == 7 && x[2 * i + 1] < l16) l16 = x[2 * i + 1];
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const uint64_t y = __shfl_xor(l16, o);
-        l16 = y < l16 ? y : l16;
+    {
+        uint64_t y = xor_lane64<32>(l16); l16 = y < l16 ? y : l16;
+        y = xor_lane64<16>(l16); l16 = y < l16 ? y : l16;
+        y = xor_lane64<8>(l16); l16 = y < l16 ? y : l16;
+        y = xor_lane64<4>(l16); l16 = y < l16 ? y : l16;
+        y = xor_lane64<2>(l16); l16 = y < l16 ? y : l16;
+        y = xor_lane64<1>(l16); l16 = y < l16 ? y : l16;
     }
     if (tid == 0) { s_lmin = kEmptyKey; sh.s_misc[4] = 0; }
     __syncthreads();
@@ -1025,6 +1039,7 @@ __global__ __launch_bounds__(kFinThreads) void k_cert_bfs(CertArgs a, MultiArgs 
             v.vscore[lane] = key_score(seedkey);
             v.vdv[lane] = 0.0f;
             v.vro[lane] = sh.ro_cache[lane] = v.ro[id];
+            sh.seed_id[lane] = id;
         }
         if (lane == 0) { sh.s_misc[0] = nsd; sh.s_misc[7] = 0; }
     }
@@ -1044,17 +1059,32 @@ __global__ __launch_bounds__(kFinThreads) void k_cert_bfs(CertArgs a, MultiArgs 
     if (wave == 0 && lane == rc - 1) sh.s_misc[5] = int(__float_as_uint(key_score(best)));
     __syncthreads();
     const double cut = double(__uint_as_float(uint32_t(sh.s_misc[5])));
+    // positions p = tid + j kFinThreads (V <= kMultiVisit): each thread's visit data is
+    // loaded once; parents and exact BFS scores live by position in the freed frontier arrays
+    // (rstart + eoff: kMultiVisit words), marks and the marked list in the freed hash
+    constexpr int kPer = kMultiVisit / kFinThreads;
+    static_assert(kHashLimit + kFinThreads <= kMultiVisit && kMultiVisit <= 2 * kFrontierChunk + 1, "positions");
     float* dv = reinterpret_cast<float*>(&sh.u.bfs.rstart[0]);      // exact BFS scores by position
-    // mark the candidates and their ancestors (flags in the freed hash keys)
+    int32_t* par_l = &sh.u.bfs.rstart[0];                            // parents by position (until dv)
     uint32_t* flag = sh.u.bfs.hkey;
     int32_t* rlist = reinterpret_cast<int32_t*>(sh.u.bfs.hval);
-    for (int p = tid; p < V; p += kFinThreads) flag[p] = 0u;
-    __syncthreads();
-    for (int p = tid; p < V; p += kFinThreads) {
-        if (double(ld_coherent(v.vscore + p)) + double(ld_coherent(v.vdv + p)) >= cut) {
-            for (int x = p; x >= 0; x = ld_coherent(v.vpar + x)) flag[x] = 1u;
+    // mark the candidates and their ancestors
+    bool mk[kPer];
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+        const int p = tid + j * kFinThreads;
+        mk[j] = false;
+        if (p < V) {
+            mk[j] = double(ld_coherent(v.vscore + p)) + double(ld_coherent(v.vdv + p)) >= cut;
+            par_l[p] = ld_coherent(v.vpar + p);
+            flag[p] = 0u;
         }
     }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < kPer; ++j)
+        if (mk[j])
+            for (int x = tid + j * kFinThreads; x >= 0; x = par_l[x]) flag[x] = 1u;
     __syncthreads();
     // compact the marked positions (ascending)
     int r = 0;
@@ -1085,34 +1115,49 @@ __global__ __launch_bounds__(kFinThreads) void k_cert_bfs(CertArgs a, MultiArgs 
     __threadfence_block();
     __syncthreads();
     stamp_at(5);
+    // the marked nodes (i = tid + j kFinThreads < r): position, hop, parent, id and the score
+    // their exact BFS score starts from, loaded once
+    int32_t mp[kPer], mh[kPer], mpar[kPer], mid[kPer];
+    float mval[kPer];
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+        const int i = tid + j * kFinThreads;
+        mh[j] = -1; mp[j] = 0; mpar[j] = -1; mid[j] = 0; mval[j] = 0.0f;
+        if (i < r) {
+            const int p = rlist[i];
+            mp[j] = p;
+            mh[j] = ld_coherent(v.vhop + p);
+            mpar[j] = par_l[p];
+            mid[j] = ld_coherent(v.vlist + p);
+            mval[j] = p < ns ? ld_coherent(v.vscore + p) : ld_coherent(m.vfin + p);
+        }
+    }
+    __syncthreads();                                                 // par_l read: dv may overwrite it
     // exact BFS scores over the marked set, level by level (parents are marked too)
     for (int h = 0; h <= levels; ++h) {
-        for (int i = tid; i < r; i += kFinThreads) {
-            const int p = rlist[i];
-            if (ld_coherent(v.vhop + p) != h) continue;
-            dv[p] = (h == 0) ? ld_coherent(v.vscore + p)
-                             : fmaxf(dv[ld_coherent(v.vpar + p)] * dlt, ld_coherent(m.vfin + p) * 0.8f);
-        }
+#pragma unroll
+        for (int j = 0; j < kPer; ++j)
+            if (mh[j] == h) dv[mp[j]] = (h == 0) ? mval[j] : fmaxf(dv[mpar[j]] * dlt, mval[j] * 0.8f);
         __syncthreads();
     }
     // the rc best exact keys among the marked nodes, and their hops
     best = kEmptyKey;
     bthr = kEmptyKey;
-    for (int i0 = wave * 64; i0 < r; i0 += kFinThreads) {
-        const int i = i0 + lane;
-        wave_offer(best, bthr, i < r ? make_key(dv[rlist[i]], uint32_t(ld_coherent(v.vlist + rlist[i]))) : kEmptyKey, lane, rc);
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+        if (j * kFinThreads + wave * 64 >= r) break;                 // uniform over the wave
+        wave_offer(best, bthr, mh[j] >= 0 ? make_key(dv[mp[j]], uint32_t(mid[j])) : kEmptyKey, lane, rc);
     }
     best = tree_merge(sh, best, rc);
     // each result's hop from the one marked position that holds its node
     if (wave == 0) s_exact[lane] = best;
     __syncthreads();
     int32_t* s_hop = reinterpret_cast<int32_t*>(sh.lists[1]);        // free after the merge
-    for (int i = tid; i < r; i += kFinThreads) {
-        const int p = rlist[i];
-        const int32_t id = ld_coherent(v.vlist + p);
-        for (int j = 0; j < rc; ++j)
-            if (key_id(s_exact[j]) == id) s_hop[j] = ld_coherent(v.vhop + p);
-    }
+#pragma unroll
+    for (int j = 0; j < kPer; ++j)
+        if (mh[j] >= 0)
+            for (int x = 0; x < rc; ++x)
+                if (key_id(s_exact[x]) == mid[j]) s_hop[x] = mh[j];
     __syncthreads();
     if (wave == 0 && lane < rc) write_result(v, lane, best, s_hop[lane]);
     if (tid == 0) {
