@@ -342,11 +342,24 @@ int certified_query(const Graph& g, Ctx& c, const float* q, float t_q, const mar
     return MARS_OK;
 }
 
+int global_batch_impl(const mars_graph* gh, mars_ctx* ch, const float* dq, int32_t Q, const float* h_tq,
+                      const mars_retrieval_config* cfg, mars_query_result* out, int32_t cap, int32_t* n_out,
+                      mars_batch_stats* stats, int32_t knn_first, int32_t knn_count, int32_t knn_k, int32_t* out_knn,
+                      bool allow_int8, bool q1_route = false);
+
+// A lone certified query over an int8 copy of at least this many rows takes the multi-query
+// int8 pass (k_split8, k_scan8m, k_cert_multi8) and the batched BFS: its scan streams the
+// copy faster than k_scan8 (the query split done once, no per-row estimate stores: 1.455
+// against 1.596 ms at 13M rows), which outweighs the longer chain after it (about 8 us more
+// at 1M rows, where k_scan8 and the one-kernel interval BFS stay ahead). Same results.
+constexpr int32_t kCertRouteRows = 2000000;
+
 // n_pin >= 0: answer over the first n_pin nodes (a batch that already read the node
-// count), else over the nodes published when the query starts.
+// count), else over the nodes published when the query starts. allow_route = false keeps a
+// certified query off the multi-query int8 pass (that pass's own fallback).
 int query_impl(const mars_graph* gh, mars_ctx* ch, const float* h_q, const float* d_q, float t_q,
                const mars_retrieval_config* cfg, mars_query_result* out, int32_t cap, int32_t* n_out,
-               mars_stats* stats, int32_t n_pin = -1) {
+               mars_stats* stats, int32_t n_pin = -1, bool allow_route = true) {
     const auto t0 = std::chrono::steady_clock::now();
     MARS_CHECK(gh && ch && cfg && n_out && (h_q || d_q), MARS_ERR_INVALID, "null argument");
     MARS_CHECK(cap >= 0 && (cap == 0 || out), MARS_ERR_INVALID, "bad output buffer");
@@ -384,6 +397,42 @@ int query_impl(const mars_graph* gh, mars_ctx* ch, const float* h_q, const float
     const bool cert = !scoped && !fp16 && (c.flags & MARS_CTX_CERTIFIED) &&
                       cert_dim_supported(g.d) && (cert_uses_int8(g) || (g.emb16 && g.nrm)) &&
                       !boost_on && lam >= 0.0f && lam <= FLT_MAX && hops < 255;
+    if (cert && allow_route && !use_graph && cert_uses_int8(g) && n_live >= kCertRouteRows && K <= kMultiCand &&
+        n_pin < 0) {
+        mars_batch_stats bst{};
+        MARS_TRY(global_batch_impl(gh, ch, q, 1, &t_q, cfg, out, cap, n_out, &bst, 0, 0, 0, nullptr, true, true));
+        c.last_certified = 0;                 // no phase stamps on this path
+        c.last_visited = 0;
+        c.last_n = 0;
+        int32_t visited = 0, levels = 0;
+        if (bst.batched == 1) {
+            const ResultHeader h = static_cast<const ResultHeader*>(c.h_mres)[0];
+            visited = h.visited;
+            levels = h.levels;
+            c.hit_vlist = c.mvlist;           // BFS levels for edge-hit counting
+            c.hit_vhop = c.mvhop;
+            c.hit_n = h.visited;
+            c.last_k = h.n_seeds;
+        }
+        if (stats) {
+            mars_stats st{};
+            st.gpu_ms_similarity = bst.gpu_ms_scan;
+            st.gpu_ms_topk = bst.gpu_ms_seeds;
+            st.gpu_ms_bfs = bst.gpu_ms_bfs;
+            st.gpu_ms_total = bst.gpu_ms_total;
+            st.nodes_scanned = n_live;
+            st.bfs_waves = cfg->bfs_max_hops;
+            st.scope_fallback = (cfg->retrieval_scope == MARS_SCOPE_EPISODE_SCOPED) ? 1 : 0;
+            st.visited = visited;
+            st.bfs_levels_run = levels;
+            st.used_fp16 = 1;
+            st.seeds_certified = bst.batched;
+            st.results_capped = capped && visited > *n_out ? 1 : 0;
+            st.wall_us = std::chrono::duration<double, std::micro>(std::chrono::steady_clock::now() - t0).count();
+            *stats = st;
+        }
+        return MARS_OK;
+    }
     if (cert) {
         bool answered = false;
         ResultHeader h{};
@@ -1514,6 +1563,7 @@ int mars_query_batch(const mars_graph* gh, mars_ctx* ch, const float* dq, int32_
     return MARS_OK;
 }
 
+namespace mars {
 namespace {
 
 // Scratch of the multi-query int8 pass (k_split8, k_scan8m, k_cert_multi8), sized once for
@@ -1532,15 +1582,17 @@ int ensure_scan8m_scratch(Ctx& c) {
 int global_batch_impl(const mars_graph* gh, mars_ctx* ch, const float* dq, int32_t Q, const float* h_tq,
                       const mars_retrieval_config* cfg, mars_query_result* out, int32_t cap, int32_t* n_out,
                       mars_batch_stats* stats, int32_t knn_first, int32_t knn_count, int32_t knn_k, int32_t* out_knn,
-                      bool allow_int8) {
+                      bool allow_int8, bool q1_route) {
     using clk = std::chrono::steady_clock;
     const auto t0 = clk::now();
     MARS_CHECK(gh && ch && Q >= 0 && knn_count >= 0 && Q + knn_count > 0, MARS_ERR_INVALID, "bad arguments");
-    // a batch leaves no single query's BFS levels for edge-hit counting
+    // a batch leaves no single query's BFS levels for edge-hit counting (a routed Q=1 query
+    // sets them itself)
     struct HitReset {
         Ctx& c;
-        ~HitReset() { c.hit_n = 0; }
-    } hit_reset{ch->c};
+        bool on;
+        ~HitReset() { if (on) c.hit_n = 0; }
+    } hit_reset{ch->c, !q1_route};
     MARS_CHECK(Q == 0 || (dq && h_tq && cfg && n_out && cap >= 0 && (cap == 0 || out)), MARS_ERR_INVALID,
                "bad query arguments");
     const Graph& g = gh->g;
@@ -1587,7 +1639,7 @@ int global_batch_impl(const mars_graph* gh, mars_ctx* ch, const float* dq, int32
     std::vector<int32_t> q1;                    // queries the Q=1 path answers
     // A lone global query (no neighbour search) is cheaper on the Q=1 certified path (one
     // candidate scan and one kernel for the rest), and the results are the same.
-    const bool lone = batched && Q == 1 && knn_count == 0 && !fp16 && cert_dim_supported(g.d);
+    const bool lone = batched && Q == 1 && knn_count == 0 && !fp16 && cert_dim_supported(g.d) && !q1_route;
     const int32_t Qg = (batched && !lone) ? Q : 0;   // global queries in the shared scan
     const int32_t Qt = Qg + knn_count;               // + k-NN queries (plain dot products)
     bool knn_fallback = false;
@@ -1622,10 +1674,14 @@ int global_batch_impl(const mars_graph* gh, mars_ctx* ch, const float* dq, int32
         const bool timing = (c.flags & MARS_CTX_TIMING) != 0;
         int32_t seed_stride = kMultiCand;
         std::vector<int32_t> knn_status(static_cast<size_t>(use8 ? knn_count : 0));
+        // one query time for every global query: passed by value (no copy)
+        const bool uniform = Qg == 0 || std::all_of(h_tq, h_tq + Qg, [&](float x) { return x == h_tq[0]; });
+        const float tq0 = Qg > 0 ? h_tq[0] : 0.0f;
         if (use8) {
             MARS_TRY(ensure_scan8m_scratch(c));
             MARS_TRY(ensure_batch_scratch(c, std::max(Qg, 1), 0));              // query times
-            if (Qg > 0) MARS_HIP(hipMemcpyAsync(c.btq, h_tq, size_t(Qg) * sizeof(float), hipMemcpyHostToDevice, s));
+            if (!uniform) MARS_HIP(hipMemcpyAsync(c.btq, h_tq, size_t(Qg) * sizeof(float), hipMemcpyHostToDevice, s));
+            const float* tqd = uniform ? nullptr : c.btq;
             const float* qplain = g.emb + int64_t(knn_first) * g.d;
             Split8Args sp{};
             sp.q_glob = dq; sp.q_plain = qplain; sp.nq = Qt; sp.n_glob = Qg; sp.d = g.d; sp.na = na8;
@@ -1636,14 +1692,14 @@ int global_batch_impl(const mars_graph* gh, mars_ctx* ch, const float* dq, int32
             scan_grid(n_live, kTargetWgI8, &rpw, &nwg);
             Scan8MArgs sa{};
             sa.emb8 = g.emb8; sa.meta8 = g.meta8; sa.n = n_live; sa.d = g.d; sa.ts = g.ts; sa.mods = g.mods;
-            sa.qa = c.m8qa; sa.qp = c.m8qp; sa.tq = c.btq; sa.lambda = lambda;
+            sa.qa = c.m8qa; sa.qp = c.m8qp; sa.tq = tqd; sa.tq_value = tq0; sa.lambda = lambda;
             sa.mod_filter = Qg > 0 ? cfg->modality_filter : -1; sa.nq = Qt; sa.n_glob = Qg;
             sa.self_base = knn_first; sa.part = c.m8part; sa.num_wg = nwg;
             MARS_TRY(launch_scan8m(sa, na8, s));
             if (timing) MARS_HIP(hipEventRecord(c.ev[1], s));
             CertMArgs ca{};
             ca.part = c.m8part; ca.n_lists = nwg; ca.q = Qt; ca.n_glob = Qg; ca.q_glob = dq; ca.q_plain = qplain;
-            ca.d = g.d; ca.emb = g.emb; ca.ts = g.ts; ca.mods = g.mods; ca.tq = c.btq; ca.lambda = lambda;
+            ca.d = g.d; ca.emb = g.emb; ca.ts = g.ts; ca.mods = g.mods; ca.tq = tqd; ca.tq_value = tq0; ca.lambda = lambda;
             ca.mod_filter = sa.mod_filter; ca.qp = c.m8qp; ca.nrm8 = g.nrm8; ca.k = std::max(K, 1);
             ca.knn_k = std::max(knn_k, 1); ca.seeds = c.mseed; ca.status = c.mstat; ca.margin = c.mmargin;
             ca.knn_out = c.mknn;
@@ -1700,12 +1756,18 @@ int global_batch_impl(const mars_graph* gh, mars_ctx* ch, const float* dq, int32
             VisitScoreArgs va{};
             va.emb = fp16 ? static_cast<const void*>(g.emb16) : static_cast<const void*>(g.emb);
             va.fp16 = fp16 ? 1 : 0; va.d = g.d; va.ts = g.ts; va.mods = g.mods; va.queries = dq;
-            va.tq = c.btq; va.lambda = lambda; va.mod_filter = cfg->modality_filter; va.q = Qg;
+            va.tq = (use8 && uniform) ? nullptr : c.btq; va.t_q_value = tq0; va.lambda = lambda;
+            va.mod_filter = cfg->modality_filter; va.q = Qg;
             va.status = c.mstat; va.info = c.minfo; va.vlist = c.mvlist; va.vfin = c.mvfin;
             MARS_TRY(launch_visit_scores(va, s));
+            if (q1_route && !timing) {                  // the last kernel stores the completion word
+                m.done = c.d_done;
+                m.seq = next_seq(c);
+            }
             MARS_TRY(launch_multi_select(m, s));
             if (timing) MARS_HIP(hipEventRecord(c.ev[3], s));
-            MARS_HIP(hipMemcpyAsync(margin.data(), c.mmargin, size_t(Qg) * sizeof(float), hipMemcpyDeviceToHost, s));
+            if (!q1_route)
+                MARS_HIP(hipMemcpyAsync(margin.data(), c.mmargin, size_t(Qg) * sizeof(float), hipMemcpyDeviceToHost, s));
         } else if (timing) {
             MARS_HIP(hipEventRecord(c.ev[3], s));
         }
@@ -1716,7 +1778,8 @@ int global_batch_impl(const mars_graph* gh, mars_ctx* ch, const float* dq, int32
                 MARS_HIP(hipMemcpyAsync(knn_status.data(), c.mstat + Qg, size_t(knn_count) * sizeof(int32_t),
                                         hipMemcpyDeviceToHost, s));
         }
-        MARS_HIP(hipStreamSynchronize(s));
+        if (q1_route && !timing && Qg == 1) MARS_TRY(wait_done(c, c.seq, s));
+        else MARS_HIP(hipStreamSynchronize(s));
         for (const int32_t x : knn_status) knn_fallback = knn_fallback || x != kMultiOk;
         if (Qg > 0) {
             const auto* hdr = static_cast<const ResultHeader*>(c.h_mres);
@@ -1754,13 +1817,13 @@ int global_batch_impl(const mars_graph* gh, mars_ctx* ch, const float* dq, int32
         // fp16 scan with exact rescoring
         mars_batch_stats s2{};
         MARS_TRY(global_batch_impl(gh, ch, nullptr, 0, nullptr, nullptr, nullptr, 0, nullptr, &s2, knn_first,
-                                   knn_count, knn_k, out_knn, false));
+                                   knn_count, knn_k, out_knn, false, false));
         st.candidate_rows = 24;
     }
     const auto t1 = clk::now();
     for (const int32_t j : q1)
         MARS_TRY(query_impl(gh, ch, nullptr, dq + int64_t(j) * g.d, h_tq[j], cfg, cap ? out + int64_t(j) * cap : nullptr,
-                            cap, &n_out[j], nullptr, n_live));
+                            cap, &n_out[j], nullptr, n_live, false));
     const auto t2 = clk::now();
     st.q1_us = std::chrono::duration<double, std::micro>(t2 - t1).count();
     st.wall_us = std::chrono::duration<double, std::micro>(t2 - t0).count();
@@ -1769,6 +1832,7 @@ int global_batch_impl(const mars_graph* gh, mars_ctx* ch, const float* dq, int32
 }
 
 }  // namespace
+}  // namespace mars
 
 int mars_query_global_batch(const mars_graph* gh, mars_ctx* ch, const float* dq, int32_t Q, const float* h_tq,
                             const mars_retrieval_config* cfg, mars_query_result* out, int32_t cap,

@@ -399,7 +399,8 @@ struct Scan8MArgs {
     const int32_t* mods;
     const void* qa;
     const float* qp;
-    const float* tq;         // [n_glob] query times
+    const float* tq;         // [n_glob] query times, or null: every global query at tq_value
+    float tq_value;
     float lambda;
     int32_t mod_filter;      // global queries
     int32_t nq;
@@ -679,7 +680,8 @@ struct CertMArgs {
     const float* emb;        // fp32 rows
     const float* ts;
     const int32_t* mods;
-    const float* tq;
+    const float* tq;         // or null: every global query at tq_value
+    float tq_value;
     float lambda;
     int32_t mod_filter;
     const float* qp;         // launch_split8's per-query terms (tau, |q|)

@@ -1202,7 +1202,7 @@ __global__ __launch_bounds__(kFinThreads) void k_cert_multi8(CertMArgs a) {
         const float dot = row16_sum(qf.dot(a.emb + int64_t(id) * a.d, sub));
         float sc = dot;
         if (!plain) {
-            const QueryTerms t{a.tq[j], a.lambda, a.mod_filter, -1, 0.0f};
+            const QueryTerms t{a.tq ? a.tq[j] : a.tq_value, a.lambda, a.mod_filter, -1, 0.0f};
             sc = fuse_score(dot, a.ts[id], (a.mod_filter >= 0) ? a.mods[id] : 0, -1, t);
         }
         key = make_key(sc, uint32_t(id));

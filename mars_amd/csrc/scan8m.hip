@@ -195,7 +195,7 @@ __global__ __launch_bounds__(kThreads) void k_scan8m(Scan8MArgs a) {
         shi[x] = p.x; slo[x] = p.y; tau[x] = p.z; qn[x] = p.w;
         qon[x] = j < a.nq;
         plain[x] = j >= a.n_glob;
-        tq[x] = (qon[x] && !plain[x]) ? a.tq[j] : 0.0f;
+        tq[x] = (qon[x] && !plain[x]) ? (a.tq ? a.tq[j] : a.tq_value) : 0.0f;
         self[x] = plain[x] ? a.self_base + (j - a.n_glob) : -1;
     }
     __syncthreads();
