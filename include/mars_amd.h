@@ -187,8 +187,16 @@ int mars_graph_set_csr(mars_graph* g, int32_t num_edges, const int32_t* row_offs
  * id): an fp16 MFMA scan keeps 16 candidates per node, exact fp32 rescoring keeps
  * k <= 16. Needs the fp16 copy. nbrs: host, num_nodes * k ids. Builds the k-NN part
  * of the NSN graph at corpus sizes a CPU cannot (analogue of the tiled kNN build of
- * src/cmng_build.cu:135-245). */
+ * src/cmng_build.cu:135-245). Each node's list is certified exact when its k-th exact
+ * score beats the 16th candidate's fp16 score by more than the fp16 scan's error bound
+ * (from the fp16 copy's row-norm maxima); the lists the certificate does not cover are
+ * found again by exact fp32 scans (mars_graph_knn_report counts both). */
 int mars_graph_knn(mars_graph* g, int32_t k, int32_t* nbrs);
+/* Counts of the last k-NN builder call on g (mars_graph_knn, _blocked, _blocks, _range):
+ * the nodes whose lists the certificate did not cover, and of those the nodes found again
+ * by exact scans (all-pairs builds; a build within blocks only counts them). No reference
+ * counterpart: the reference's builders report nothing of the kind. */
+int mars_graph_knn_report(const mars_graph* g, int64_t* uncertified, int64_t* rescanned);
 /* The same within blocks: each node's k nearest among the nodes of its block of
  * block_rows consecutive ids (block_rows >= num_nodes: mars_graph_knn). For corpora
  * where the exact all-pairs search is too long to build (13M rows: ~2.6e17 FLOP). */

@@ -461,19 +461,37 @@ def graph_knn_range(dg: DeviceMemoryGraph, k: int, first: int, count: int) -> np
     return out
 
 
+def graph_knn_report(dg: DeviceMemoryGraph):
+    """(uncertified, rescanned) of the last k-NN builder call: nodes whose lists the
+    certificate did not cover, and of those the ones found again by exact scans."""
+    u, r = C.c_int64(), C.c_int64()
+    check(lib.mars_graph_knn_report(dg.handle, C.byref(u), C.byref(r)), "mars_graph_knn_report")
+    return int(u.value), int(r.value)
+
+
 def graph_knn(dg: DeviceMemoryGraph, k: int = 8, block_rows: int = 0, progress=None,
               piece: int = 1 << 20) -> np.ndarray:
-    """k nearest neighbours of every node (fp16 MFMA candidates + exact fp32 rescoring);
+    """k nearest neighbours of every node (fp16 MFMA candidates + exact fp32 rescoring,
+    certified; nodes the certificate misses are scanned again exactly in all-pairs builds);
     block_rows > 0: among the nodes of each block of block_rows consecutive ids
     (progress(done, total) is called after each block when given); block_rows = 0 with a
-    progress callback: all pairs, in pieces of `piece` query nodes, progress after each."""
+    progress callback: all pairs, in pieces of `piece` query nodes, progress after each.
+    dg.knn_report gets the (uncertified, rescanned) node counts of the whole build."""
     out = np.empty((dg.num_nodes, k), np.int32)
+    rep = [0, 0]
+
+    def add():
+        u, r = graph_knn_report(dg)
+        rep[0] += u
+        rep[1] += r
+
     if block_rows <= 0 and progress is not None:
         n = dg.num_nodes
         total = (n + piece - 1) // piece
         for b in range(total):
             lo = b * piece
             out[lo:lo + piece] = graph_knn_range(dg, k, lo, min(piece, n - lo))
+            add()
             progress(b + 1, total)
     elif block_rows > 0 and progress is not None:
         nb = (dg.num_nodes + block_rows - 1) // block_rows
@@ -481,11 +499,15 @@ def graph_knn(dg: DeviceMemoryGraph, k: int = 8, block_rows: int = 0, progress=N
             lo = b * block_rows
             check(lib.mars_graph_knn_blocks(dg.handle, int(k), int(block_rows), b, 1, _ptr(out[lo:])),
                   "mars_graph_knn_blocks")
+            add()
             progress(b + 1, nb)
     elif block_rows > 0:
         check(lib.mars_graph_knn_blocked(dg.handle, int(k), int(block_rows), _ptr(out)), "mars_graph_knn_blocked")
+        add()
     else:
         check(lib.mars_graph_knn(dg.handle, int(k), _ptr(out)), "mars_graph_knn")
+        add()
+    dg.knn_report = tuple(rep)
     return out
 
 

@@ -238,6 +238,7 @@ SIGNATURES = {
     "mars_graph_knn_blocked": (C.c_int, [VP, I32, I32, VP]),
     "mars_graph_knn_blocks": (C.c_int, [VP, I32, I32, I32, I32, VP]),
     "mars_graph_knn_range": (C.c_int, [VP, I32, I32, I32, VP]),
+    "mars_graph_knn_report": (C.c_int, [VP, C.POINTER(C.c_int64), C.POINTER(C.c_int64)]),
     "mars_graph_read_ceiling": (C.c_int, [VP, I32, I32, C.POINTER(C.c_double)]),
     "mars_graph_read_pattern": (C.c_int, [VP, I32, I32, C.POINTER(C.c_double)]),
     "mars_fnv1a64": (C.c_int, [VP, I64, C.POINTER(C.c_uint64)]),

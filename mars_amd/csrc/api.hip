@@ -1890,6 +1890,54 @@ int mars_graph_read_pattern(const mars_graph* gh, int32_t pattern, int32_t reps,
     }, gbps);
 }
 
+namespace {
+
+// The k-NN lists of the nodes the builder's certificate did not cover (cert[i] == 0 for
+// node first + i), found again by exact fp32 scans over all rows (the global query path with
+// no decay, no BFS and k + 1 seeds, the node itself dropped). Records the counts.
+int knn_rescan_uncertified(mars_graph* gh, int32_t k, int64_t first, const std::vector<int32_t>& cert,
+                           int32_t* nbrs, bool rescan) {
+    Graph& g = gh->g;
+    std::vector<int64_t> todo;
+    for (size_t i = 0; i < cert.size(); ++i)
+        if (!cert[i]) todo.push_back(first + int64_t(i));
+    g.knn_uncertified = int64_t(todo.size());
+    g.knn_rescanned = 0;
+    if (todo.empty() || !rescan) return MARS_OK;
+    mars_ctx* ctx = nullptr;
+    MARS_TRY(mars_ctx_create(g.cap_n, g.d, 32, 0, &ctx));
+    mars_retrieval_config cfg;
+    mars_config_default(&cfg);
+    cfg.top_k = k + 1;
+    cfg.bfs_max_hops = 0;
+    cfg.time_decay_lambda = 0.0f;
+    cfg.max_results_returned = k + 1;
+    std::vector<mars_query_result> res(static_cast<size_t>(k) + 1);
+    int rc = MARS_OK;
+    for (const int64_t node : todo) {
+        int32_t nr = 0;
+        rc = query_impl(gh, ctx, nullptr, g.emb + node * g.d, 0.0f, &cfg, res.data(), k + 1, &nr, nullptr);
+        if (rc != MARS_OK) break;
+        int32_t* row = nbrs + (node - first) * k;
+        int32_t w = 0;
+        for (int32_t j = 0; j < std::min(nr, k + 1) && w < k; ++j)
+            if (res[size_t(j)].node_id != node) row[w++] = res[size_t(j)].node_id;
+        for (; w < k; ++w) row[w] = -1;
+        ++g.knn_rescanned;
+    }
+    (void)mars_ctx_destroy(ctx);
+    return rc;
+}
+
+}  // namespace
+
+int mars_graph_knn_report(const mars_graph* gh, int64_t* uncertified, int64_t* rescanned) {
+    MARS_CHECK(gh && uncertified && rescanned, MARS_ERR_INVALID, "null argument");
+    *uncertified = gh->g.knn_uncertified;
+    *rescanned = gh->g.knn_rescanned;
+    return MARS_OK;
+}
+
 int mars_graph_knn_blocked(mars_graph* gh, int32_t k, int32_t block_rows, int32_t* nbrs) {
     MARS_CHECK(gh && block_rows > 0, MARS_ERR_INVALID, "k-NN: bad arguments (block_rows=%d)", block_rows);
     const int64_t n = gh->g.n;
@@ -1917,16 +1965,22 @@ int mars_graph_knn_blocks(mars_graph* gh, int32_t k, int32_t block_rows, int32_t
     int64_t rpr = 0;
     batch_grid(B, kChunk, &nrr, &nqb, &rpr);         // the largest block sizes the scratch
     float* tq = nullptr; uint64_t* part = nullptr; uint64_t* cand = nullptr; int32_t* dn = nullptr;
+    int32_t* cert = nullptr;
     hipStream_t s = nullptr;
     int rc = MARS_OK;
-    auto cleanup = [&]() { dfree(tq); dfree(part); dfree(cand); dfree(dn); if (s) (void)hipStreamDestroy(s); };
+    auto cleanup = [&]() {
+        dfree(tq); dfree(part); dfree(cand); dfree(dn); dfree(cert);
+        if (s) (void)hipStreamDestroy(s);
+    };
     if ((rc = dmalloc(&tq, kChunk)) || (rc = dmalloc(&part, size_t(nqb) * nrr * 64 * kCand)) ||
-        (rc = dmalloc(&cand, size_t(kChunk) * kCand)) || (rc = dmalloc(&dn, size_t(hi - lo) * k))) {
+        (rc = dmalloc(&cand, size_t(kChunk) * kCand)) || (rc = dmalloc(&dn, size_t(hi - lo) * k)) ||
+        (rc = dmalloc(&cert, size_t(hi - lo)))) {
         cleanup();
         return rc;
     }
     hipError_t e = hipStreamCreateWithFlags(&s, hipStreamNonBlocking);
     if (e == hipSuccess) e = hipMemsetAsync(tq, 0, kChunk * sizeof(float), s);
+    if (e == hipSuccess) e = hipMemsetAsync(cert, 0, size_t(hi - lo) * sizeof(int32_t), s);
     if (e != hipSuccess) { cleanup(); return set_error(MARS_ERR_HIP, "k-NN setup: %s", hipGetErrorString(e)); }
     // block [r0, r1): rows, queries and candidate ids relative to r0
     for (int64_t r0 = lo; r0 < hi && rc == MARS_OK; r0 += B) {
@@ -1941,12 +1995,15 @@ int mars_graph_knn_blocks(mars_graph* gh, int32_t k, int32_t block_rows, int32_t
             a.rows_per_range = rpr; a.n_rranges = nrr; a.n_qblocks = (q + 63) / 64;
             rc = launch_batch_topk(a, kCand, cand, s);
             if (rc == MARS_OK)
-                rc = launch_knn_rerank(g.emb + r0 * g.d, q0, q, g.d, cand, kCand, k, dn + (r0 - lo + q0) * k, s);
+                rc = launch_knn_rerank(g.emb + r0 * g.d, q0, q, g.d, cand, kCand, k, dn + (r0 - lo + q0) * k, s,
+                                       g.nrm, g.nrm ? cert + (r0 - lo + q0) : nullptr);
         }
     }
+    std::vector<int32_t> hcert(size_t(hi - lo), 0);
     if (rc == MARS_OK) {
         e = hipStreamSynchronize(s);
         if (e == hipSuccess) e = hipMemcpy(nbrs, dn, size_t(hi - lo) * k * sizeof(int32_t), hipMemcpyDeviceToHost);
+        if (e == hipSuccess) e = hipMemcpy(hcert.data(), cert, hcert.size() * sizeof(int32_t), hipMemcpyDeviceToHost);
         if (e != hipSuccess) rc = set_error(MARS_ERR_HIP, "k-NN: %s", hipGetErrorString(e));
     }
     cleanup();
@@ -1957,6 +2014,9 @@ int mars_graph_knn_blocks(mars_graph* gh, int32_t k, int32_t block_rows, int32_t
                 if (nbrs[(i - lo) * k + j] >= 0) nbrs[(i - lo) * k + j] += off;
         }
     }
+    // all pairs: the nodes the certificate missed are scanned again exactly; within blocks
+    // they are only counted (an exact scan would search beyond the block)
+    if (rc == MARS_OK) rc = knn_rescan_uncertified(gh, k, lo, hcert, nbrs, B >= g.n);
     return rc;
 }
 
@@ -1978,16 +2038,22 @@ int mars_graph_knn_range(mars_graph* gh, int32_t k, int32_t first, int32_t count
     int64_t rpr = 0;
     batch_grid(n, kChunk, &nrr, &nqb, &rpr);
     float* tq = nullptr; uint64_t* part = nullptr; uint64_t* cand = nullptr; int32_t* dn = nullptr;
+    int32_t* cert = nullptr;
     hipStream_t s = nullptr;
     int rc = MARS_OK;
-    auto cleanup = [&]() { dfree(tq); dfree(part); dfree(cand); dfree(dn); if (s) (void)hipStreamDestroy(s); };
+    auto cleanup = [&]() {
+        dfree(tq); dfree(part); dfree(cand); dfree(dn); dfree(cert);
+        if (s) (void)hipStreamDestroy(s);
+    };
     if ((rc = dmalloc(&tq, kChunk)) || (rc = dmalloc(&part, size_t(nqb) * nrr * 64 * kCand)) ||
-        (rc = dmalloc(&cand, size_t(kChunk) * kCand)) || (rc = dmalloc(&dn, size_t(count) * k))) {
+        (rc = dmalloc(&cand, size_t(kChunk) * kCand)) || (rc = dmalloc(&dn, size_t(count) * k)) ||
+        (rc = dmalloc(&cert, size_t(count)))) {
         cleanup();
         return rc;
     }
     hipError_t e = hipStreamCreateWithFlags(&s, hipStreamNonBlocking);
     if (e == hipSuccess) e = hipMemsetAsync(tq, 0, kChunk * sizeof(float), s);
+    if (e == hipSuccess) e = hipMemsetAsync(cert, 0, size_t(count) * sizeof(int32_t), s);
     if (e != hipSuccess) { cleanup(); return set_error(MARS_ERR_HIP, "k-NN range setup: %s", hipGetErrorString(e)); }
     // queries [q0, q0 + q) against every node; the query's own id is excluded
     for (int64_t q0 = first; q0 < int64_t(first) + count && rc == MARS_OK; q0 += kChunk) {
@@ -1998,14 +2064,19 @@ int mars_graph_knn_range(mars_graph* gh, int32_t k, int32_t first, int32_t count
         a.part = part; a.uniform_tq = 1;
         a.rows_per_range = rpr; a.n_rranges = nrr; a.n_qblocks = (q + 63) / 64;
         rc = launch_batch_topk(a, kCand, cand, s);
-        if (rc == MARS_OK) rc = launch_knn_rerank(g.emb, q0, q, g.d, cand, kCand, k, dn + (q0 - first) * k, s);
+        if (rc == MARS_OK)
+            rc = launch_knn_rerank(g.emb, q0, q, g.d, cand, kCand, k, dn + (q0 - first) * k, s, g.nrm,
+                                   g.nrm ? cert + (q0 - first) : nullptr);
     }
+    std::vector<int32_t> hcert(static_cast<size_t>(count), 0);
     if (rc == MARS_OK) {
         e = hipStreamSynchronize(s);
         if (e == hipSuccess) e = hipMemcpy(nbrs, dn, size_t(count) * k * sizeof(int32_t), hipMemcpyDeviceToHost);
+        if (e == hipSuccess) e = hipMemcpy(hcert.data(), cert, hcert.size() * sizeof(int32_t), hipMemcpyDeviceToHost);
         if (e != hipSuccess) rc = set_error(MARS_ERR_HIP, "k-NN range: %s", hipGetErrorString(e));
     }
     cleanup();
+    if (rc == MARS_OK) rc = knn_rescan_uncertified(gh, k, first, hcert, nbrs, true);
     return rc;
 }
 

@@ -269,9 +269,21 @@ __global__ __launch_bounds__(64) void k_batch_merge(const uint64_t* __restrict__
 
 // Exact fp32 rescoring of kc candidates per node; keeps k_out by (score desc, id asc).
 // Nodes q0 .. q0+nq-1; cand / nbrs are indexed from q0.
+// With nrm (the fp16 copy's row-norm maxima) and cert: cert[node] = 1 when the lists are
+// certified exact. Every row outside the candidates has an fp16 score at most the kc-th
+// candidate's, and its fp32 score (this kernel's arithmetic) exceeds its fp16 score by at
+// most
+//     eps = |e16| |ftz(e16) - e| + |e| |ftz(e16) - e|      (both fp16 roundings)
+//           + g_mfma |e16|^2 + g_fp32 |e|^2 + u (|e16|^2 (1 + g_mfma) + |e|^2 (1 + g_fp32))
+// (row maxima for the query row too; g_mfma = 2 d u / (1 - d u), doubled for the MFMA's
+// unspecified order; g_fp32 = n u / (1 - n u) with n = d / 16 + 4 for this kernel's
+// per-lane chains and 16-lane reduction), so a k_out-th exact score above (kc-th fp16 score
+// + eps) leaves no row outside the candidates that could enter the list. Fewer than kc
+// candidates: every other row was one.
 __global__ __launch_bounds__(256) void k_knn_rerank(const float* __restrict__ emb, int64_t q0, int64_t nq,
                                                     int32_t d, const uint64_t* __restrict__ cand, int32_t kc,
-                                                    int32_t k_out, int32_t* __restrict__ nbrs) {
+                                                    int32_t k_out, int32_t* __restrict__ nbrs,
+                                                    const uint32_t* __restrict__ nrm, int32_t* __restrict__ cert) {
     const int lane = int(threadIdx.x & 63u);
     const int sub = lane & 15;
     const int64_t node = (int64_t(blockIdx.x) * blockDim.x + threadIdx.x) >> 4;
@@ -301,6 +313,21 @@ __global__ __launch_bounds__(256) void k_knn_rerank(const float* __restrict__ em
             keys[j + 1] = v;
         }
         for (int c = 0; c < k_out; ++c) nbrs[node * k_out + c] = (keys[c] != kEmptyKey) ? key_id(keys[c]) : -1;
+        if (cert) {
+            const uint64_t last = cand[node * kc + kc - 1];
+            bool ok = last == kEmptyKey;
+            if (!ok && nrm && keys[k_out - 1] != kEmptyKey) {
+                const double e32 = double(__uint_as_float(nrm[0]));
+                const double e16 = double(__uint_as_float(nrm[1]));
+                const double de = double(__uint_as_float(nrm[2]));
+                const double u = 0x1p-24, nm = double(d), nf = double(d) / 16.0 + 4.0;
+                const double g_mfma = 2.0 * nm * u / (1.0 - nm * u), g_f32 = nf * u / (1.0 - nf * u);
+                const double eps = (e16 * de + e32 * de + g_mfma * e16 * e16 + g_f32 * e32 * e32 +
+                                    u * (e16 * e16 * (1.0 + g_mfma) + e32 * e32 * (1.0 + g_f32))) * 1.01 + 1e-30 * nm;
+                ok = eps < 1e30 && double(key_score(keys[k_out - 1])) > double(key_score(last)) + eps;
+            }
+            cert[node] = ok ? 1 : 0;
+        }
     }
 }
 
@@ -375,10 +402,10 @@ int launch_batch_topk(BatchArgs a, int32_t k_out, uint64_t* out, hipStream_t s, 
 }
 
 int launch_knn_rerank(const float* emb, int64_t q0, int64_t nq, int32_t d, const uint64_t* cand, int32_t kc,
-                      int32_t k_out, int32_t* nbrs, hipStream_t s) {
+                      int32_t k_out, int32_t* nbrs, hipStream_t s, const uint32_t* nrm, int32_t* cert) {
     const int64_t threads = nq * 16;
     MARS_LAUNCH(k_knn_rerank, dim3(unsigned((threads + 255) / 256)), dim3(256), 0, s, emb, q0, nq, d, cand, kc,
-                       k_out, nbrs);
+                k_out, nbrs, nrm, cert);
     return MARS_OK;
 }
 

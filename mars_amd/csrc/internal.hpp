@@ -174,6 +174,10 @@ struct Graph {
     float* ins_tq = nullptr;             // zero query times (no decay)
     int32_t ins_cap_q = 0;
     hipEvent_t ins_ev[2] = {nullptr, nullptr};
+    // the last k-NN builder call: nodes whose lists the certificate did not cover, and of
+    // those, how many were found again by exact scans
+    int64_t knn_uncertified = 0;
+    int64_t knn_rescanned = 0;
     // the neighbour search of up to 16 new nodes over the int8 copy (one k_scan8m pass)
     uint64_t* ins8_part = nullptr;       // [16][kScan8MPart]
     unsigned char* ins8_qa = nullptr;    // A operands
@@ -555,8 +559,10 @@ constexpr int64_t kSampleRowsMin = 32;
 constexpr int64_t kSampleRowsMax = 1024;
 // `scanned` (optional) is recorded after the full pass, before the final merge.
 int launch_batch_topk(BatchArgs a, int32_t k_out, uint64_t* out, hipStream_t s, hipEvent_t scanned = nullptr);
+// nrm and cert given: cert[node] = 1 when the node's lists are certified exact (k_knn_rerank)
 int launch_knn_rerank(const float* emb, int64_t q0, int64_t nq, int32_t d, const uint64_t* cand, int32_t kc,
-                      int32_t k_out, int32_t* nbrs, hipStream_t s);
+                      int32_t k_out, int32_t* nbrs, hipStream_t s, const uint32_t* nrm = nullptr,
+                      int32_t* cert = nullptr);
 int launch_f32_to_f16_rows(const float* in, __half* out, int64_t count, hipStream_t s);
 
 // ---- batched global queries (multi.hip; BFS / select kernels in kernels.hip) -----------
