@@ -57,6 +57,11 @@ constexpr int32_t kKnnCand = 16;            // fp16 candidates rescored per new 
 // full-width search takes about 4 ms), and a longer one would only delay the writer.
 constexpr int32_t kInsertKnnRanges = 64;
 constexpr int64_t kInsertKnnNarrowRows = 2000000;
+// Up to that size the narrow fp16 search runs first, its lists certified as the k-NN
+// builders' are, and the int8 pass only for the nodes of a failed certificate: the int8
+// pass at full width links in 0.29 ms at 1M rows but lifts the global p99 of concurrent
+// queries from 199 to 304 us, and at 32 workgroups still to 235-257 us. Above it the int8
+// pass runs first, at full width.
 
 // Step 1 of an insert: the staged block (rows | modalities | times | episode ids |
 // episode members | episode offsets) is scattered into the graph; each new row is also
@@ -275,16 +280,11 @@ int insert_knn_int8(Graph& g, int64_t first, int32_t nq, int64_t n, int32_t k, h
     return MARS_OK;
 }
 
-// k nearest neighbours of nodes [first, first + nq) among [0, n): with the int8 copy and
-// at most 16 nodes, one int8 pass with certified exact neighbours; otherwise (or when a
-// certificate failed) a batched fp16 scan (no decay, no filter, self excluded) + exact
-// fp32 rescoring of 16 candidates.
-int insert_knn(Graph& g, int64_t first, int32_t nq, int64_t n, int32_t k, hipStream_t s) {
-    if (nq >= 1 && nq <= 8 * kScan8MMaxA && k <= 16 && cert_uses_int8(g)) {
-        bool done = false;
-        MARS_TRY(insert_knn_int8(g, first, nq, n, k, s, &done));
-        if (done) return MARS_OK;
-    }
+// The fp16 search: a batched fp16 scan (no decay, no filter, self excluded) + exact fp32
+// rescoring of 16 candidates per node into g.ins_nbrs. cert given: cert[i] = 1 when node
+// first + i's list is certified exact (its k-th exact score beats the 16th candidate's
+// fp16 score by the fp16 error bound).
+int insert_knn_fp16(Graph& g, int64_t first, int32_t nq, int64_t n, int32_t k, hipStream_t s, int32_t* cert) {
     int32_t nrr = 0, nqb = 0;
     int64_t rpr = 0, part_keys = 0;
     const int32_t ranges = n <= kInsertKnnNarrowRows ? kInsertKnnRanges : 256;
@@ -319,9 +319,35 @@ int insert_knn(Graph& g, int64_t first, int32_t nq, int64_t n, int32_t k, hipStr
         a.q_plain = 0; a.self_base = first + c0; a.part = g.ins_part; a.rows_per_range = rpr; a.n_rranges = nrr;
         a.n_qblocks = nqb; a.uniform_tq = 1;
         MARS_TRY(launch_batch_topk(a, kKnnCand, g.ins_cand, s));
-        MARS_TRY(launch_knn_rerank(g.emb, first + c0, q, g.d, g.ins_cand, kKnnCand, k, g.ins_nbrs + int64_t(c0) * k, s));
+        MARS_TRY(launch_knn_rerank(g.emb, first + c0, q, g.d, g.ins_cand, kKnnCand, k, g.ins_nbrs + int64_t(c0) * k, s,
+                                   cert ? g.nrm : nullptr, cert ? cert + c0 : nullptr));
     }
     return MARS_OK;
+}
+
+// k nearest neighbours of nodes [first, first + nq) among [0, n) into g.ins_nbrs. For at
+// most 16 nodes over the int8 copy the result is certified exact: up to
+// kInsertKnnNarrowRows rows the narrow fp16 search first and the int8 pass only when a
+// list failed its certificate, above it the int8 pass first; when the int8 certificate
+// fails too (or for more nodes, or without the int8 copy) the fp16 search's lists stand.
+int insert_knn(Graph& g, int64_t first, int32_t nq, int64_t n, int32_t k, hipStream_t s) {
+    const bool int8_ok = nq >= 1 && nq <= 8 * kScan8MMaxA && k <= 16 && cert_uses_int8(g);
+    bool done = false;
+    if (int8_ok && n > kInsertKnnNarrowRows) {
+        MARS_TRY(insert_knn_int8(g, first, nq, n, k, s, &done));
+        if (done) return MARS_OK;
+        return insert_knn_fp16(g, first, nq, n, k, s, nullptr);
+    }
+    if (!int8_ok || !g.nrm) return insert_knn_fp16(g, first, nq, n, k, s, nullptr);
+    if (!g.ins_cert) MARS_TRY(dmalloc(&g.ins_cert, size_t(8 * kScan8MMaxA)));
+    MARS_TRY(insert_knn_fp16(g, first, nq, n, k, s, g.ins_cert));
+    int32_t cert[8 * kScan8MMaxA];
+    MARS_HIP(hipMemcpyAsync(cert, g.ins_cert, size_t(nq) * sizeof(int32_t), hipMemcpyDeviceToHost, s));
+    MARS_HIP(hipStreamSynchronize(s));
+    if (std::all_of(cert, cert + nq, [](int32_t x) { return x != 0; })) return MARS_OK;
+    MARS_TRY(insert_knn_int8(g, first, nq, n, k, s, &done));
+    if (done) return MARS_OK;
+    return insert_knn_fp16(g, first, nq, n, k, s, nullptr);
 }
 
 // Copies rows out of col: spec holds n x {start, len, out offset}; one wave per row.
@@ -531,7 +557,7 @@ int graph_insert_free(Graph& g) {
     g.ins_dev = nullptr;
     g.ins_dev_bytes = 0;
     dfree(g.ins_part); dfree(g.ins_cand); dfree(g.ins_nbrs); dfree(g.ins_tq);
-    dfree(g.ins8_part); dfree(g.ins8_qa); dfree(g.ins8_qp); dfree(g.ins8_stat); dfree(g.ins8_margin);
+    dfree(g.ins8_part); dfree(g.ins8_qa); dfree(g.ins8_qp); dfree(g.ins8_stat); dfree(g.ins8_margin); dfree(g.ins_cert);
     g.ins_part_cap = 0;
     g.ins_cap_q = 0;
     for (auto& e : g.ins_ev) {

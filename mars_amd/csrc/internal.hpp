@@ -184,6 +184,7 @@ struct Graph {
     float* ins8_qp = nullptr;            // [16][4]
     int32_t* ins8_stat = nullptr;        // [16] certificate status
     float* ins8_margin = nullptr;        // [16]
+    int32_t* ins_cert = nullptr;         // [16] fp16 k-NN certificate flags
     // importance and edge-hit counters (allocated on request, under the graph mutex)
     float* imp = nullptr;                // cap_n: importance of each node
     int32_t* hits = nullptr;             // cap_e: BFS hits per col slot; slots no row uses hold 0
