@@ -40,6 +40,7 @@ constexpr int kRWaves = 4;     // one per SIMD; each holds QT 16-query MFMA tile
 constexpr int kRThreads = kRWaves * 64;
 constexpr int kRRows = 16;     // corpus rows per tile
 constexpr int kRBuf = 5;       // tile buffers: tiles i + 1 .. i + 4 load while tile i computes
+constexpr int kRqSparse = 4;   // at most this many lanes with one pair each: the pairs one at a time
 
 template <int NS, int QT>
 struct RqLds {
@@ -155,7 +156,13 @@ void k_batch_rq(BatchArgs a) {
     const bool uni = a.uniform_tq != 0;
     const float tq0 = a.tq[0];
     const bool plain = myq >= a.q_plain;          // neighbour search: dot product only
-    const int64_t self_id = (a.self_base >= 0 && qvalid && plain) ? a.self_base + (myq - a.q_plain) : -1;
+    // the query's own row (a neighbour search of a corpus row), relative to the range: -1
+    // when it is not in this range (one 32-bit register: the queries need the rest)
+    int32_t self_rel = -1;
+    if (a.self_base >= 0 && qvalid && plain) {
+        const int64_t self_id = a.self_base + (myq - a.q_plain);
+        if (self_id >= r0 && self_id < r1) self_rel = int32_t(self_id - r0);
+    }
     uint64_t list[K];
 #pragma unroll
     for (int j = 0; j < K; ++j) list[j] = kEmptyKey;
@@ -164,7 +171,9 @@ void k_batch_rq(BatchArgs a) {
         const uint64_t fk = a.floor_keys[int64_t(myq) * a.floor_k + a.floor_k - 1];
         if (fk != kEmptyKey) own = ord32(key_score(fk));
     }
-    if (lane < WQ) sh.floorv[wave][lane] = own != 0u ? ord32_inv(own) : -INFINITY;   // read after the loop's first barrier
+    // per query: the floor its rows must reach (read after the loop's first barrier); past
+    // the batch +inf, so no row reaches it
+    if (lane < WQ) sh.floorv[wave][lane] = !qvalid ? INFINITY : own != 0u ? ord32_inv(own) : -INFINITY;
     const bool prefilter = uni || a.lambda >= 0.0f;
 
     // B-fragment slots: k-step ks reads piece 4 ks + kg of row m, i.e. slot
@@ -235,13 +244,14 @@ void k_batch_rq(BatchArgs a) {
             const bool keep_m = a.mod_filter < 0 || smod == a.mod_filter;
             const float w_m = !uni ? sts : (a.lambda != 0.0f ? expf(-a.lambda * fmaxf(0.0f, tq0 - sts)) : 1.0f);
             const int nr = int((r1 - t0) < kRRows ? (r1 - t0) : kRRows);
-            // Pre-filter in the MFMA layout (C[query qt*16 + 4*kg + v][row m]): the tile
-            // goes through the selection only if some score reaches its query's floor. With
-            // one query time the score is the selection's own (x * w_m); otherwise x, or 0
-            // for x < 0, bounds x * w for any weight in (0, 1]. NaN passes.
-            bool any = true;
+            // Pre-filter in the MFMA layout (C[query qt*16 + 4*kg + v][row m]): bit 4 qt + v
+            // of hb is set when this lane's row reaches query qt*16 + 4*kg + v's floor (from
+            // the sampled pass; +inf past the batch). With one query time the score is the
+            // selection's own (x * w_m); otherwise x, or 0 for x < 0, bounds x * w for any
+            // weight in (0, 1]. NaN passes.
+            uint32_t hb = 0xFFFFu;
             if (prefilter) {
-                bool hit = false;
+                hb = 0u;
 #pragma unroll
                 for (int qt = 0; qt < QT; ++qt) {
                     const f32x4 fl = *reinterpret_cast<const f32x4*>(&sh.floorv[wave][qt * 16 + 4 * kg]);
@@ -251,49 +261,63 @@ void k_batch_rq(BatchArgs a) {
                         float sv = uni ? x * w_m : (x < 0.0f ? 0.0f : x);
                         sv = keep_m ? sv : -FLT_MAX;
                         sv = (wq0 + qt * 16 + 4 * kg + v >= a.q_plain) ? x : sv;
-                        hit = hit || !(sv < fl[v]);
+                        hb = !(sv < fl[v]) ? (hb | (1u << (4 * qt + v))) : hb;
                     }
                 }
-                any = __ballot(hit && m < nr) != 0;
             }
+            hb = m < nr ? hb : 0u;
+            const uint64_t hl = __ballot(hb != 0u);
+            const bool any = hl != 0u;
+            // sparse: a few lanes, one pair each; each pair's query lane then offers that
+            // one row, instead of testing all 16
+            const bool sparse = prefilter && __popcll(hl) <= kRqSparse && __ballot((hb & (hb - 1u)) != 0u) == 0;
+            // The fused score of row j for this lane's query: dot * w (k_batch_scan's
+            // arithmetic), filtered rows -FLT_MAX, neighbour searches the plain dot.
+            // (Branch-free per lane: the uni / lambda tests are wave-uniform.)
+            auto fuse = [&](float x, float wj, bool keep) {
+                float sv = x;
+                if (uni) sv = x * wj;
+                else if (a.lambda != 0.0f) sv = x * expf(-a.lambda * fmaxf(0.0f, tq - wj));
+                sv = keep ? sv : -FLT_MAX;
+                return plain ? x : sv;
+            };
             if (any) {
                 if (lane < kRRows) sh.wrow[wave][lane] = w_m;
                 const uint32_t keepm = uint32_t(__ballot(keep_m && lane < kRRows));
-                // C[query = qt*16 + 4*kg + v][row = m]
+                uint32_t pass = 0u;                  // rows of this lane's query to offer
+                // the tile, transposed: C[query = qt*16 + 4*kg + v][row = m]
 #pragma unroll
                 for (int qt = 0; qt < QT; ++qt)
 #pragma unroll
                     for (int v = 0; v < 4; ++v) sh.stage[wave][m][qt * 16 + 4 * kg + v] = acc[qt][v];
-                float w[kRRows];                     // wave-uniform (read in uniform control flow)
-#pragma unroll
-                for (int j = 0; j < kRRows; ++j)
-                    w[j] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w_m), j));
-                rq_wave_lds_sync();
-                // The fused score of row j for this lane's query: dot * w (k_batch_scan's
-                // arithmetic), filtered rows -FLT_MAX, neighbour searches the plain dot.
-                // (Branch-free per lane: the uni / lambda tests are wave-uniform.)
-                auto fuse = [&](float x, float wj, bool keep) {
-                    float sv = x;
-                    if (uni) sv = x * wj;
-                    else if (a.lambda != 0.0f) sv = x * expf(-a.lambda * fmaxf(0.0f, tq - wj));
-                    sv = keep ? sv : -FLT_MAX;
-                    return plain ? x : sv;
-                };
-                if (qvalid) {
-                    // The rows that may enter the list: not below its K-th score (a float test
-                    // that never rejects a row the key test below accepts; NaN passes to it).
-                    const float bound_f = own != 0u ? ord32_inv(own) : -INFINITY;
-                    uint32_t pass = 0u;
-#pragma unroll
-                    for (int j = 0; j < kRRows; ++j) {
-                        const float sv = fuse(sh.stage[wave][j][lane], w[j], (keepm >> j) & 1u);
-                        pass |= uint32_t(!(sv < bound_f)) << j;
+                if (sparse) {
+                    // each pair's row to the lane of its query (bit b: query (b / 4)*16 + 4*kg + b % 4)
+                    const int bt = hb != 0u ? __builtin_ctz(hb) : 0;
+                    for (uint64_t ln = hl; ln != 0; ln &= ln - 1) {
+                        const int L = __builtin_ctzll(ln);
+                        const int b1 = __builtin_amdgcn_readlane(bt, L);
+                        if (lane == (b1 >> 2) * 16 + 4 * (L >> 4) + (b1 & 3)) pass |= 1u << (L & 15);
                     }
-                    pass &= 0xFFFFu >> (kRRows - nr);
-                    if (self_id >= t0 && self_id < t0 + kRRows) pass &= ~(1u << int(self_id - t0));
-                    // one passing row per lane and round (a round costs what one insertion
-                    // does; most tiles need one or none), its score again from the stage (the
-                    // same operations, so the same bits)
+                }
+                rq_wave_lds_sync();
+                if (qvalid) {
+                    const float bound_f = own != 0u ? ord32_inv(own) : -INFINITY;
+                    if (!sparse) {
+                        // The rows that may enter the list: not below its K-th score (a float
+                        // test that never rejects a row the key test below accepts; NaN passes).
+#pragma unroll
+                        for (int j = 0; j < kRRows; ++j) {
+                            const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w_m), j));
+                            const float sv = fuse(sh.stage[wave][j][lane], wj, (keepm >> j) & 1u);
+                            pass |= uint32_t(!(sv < bound_f)) << j;
+                        }
+                        pass &= 0xFFFFu >> (kRRows - nr);
+                    }
+                    const int32_t self_t = self_rel - int32_t(t0 - r0);
+                    if (self_t >= 0 && self_t < kRRows) pass &= ~(1u << self_t);
+                    // one row per lane and round (a round costs what one insertion does; most
+                    // tiles need one or none), its fused score from the stage (the same
+                    // operations, so the same bits)
                     while (pass) {
                         const int j = __builtin_ctz(pass);
                         pass &= pass - 1u;
