@@ -64,9 +64,9 @@ def test_rq_equals_scan_bit_for_bit(q, k, filt, uniform, rng):
 
 
 def test_rq_sampled_floor(rng):
-    """120K rows, 600 queries (three 256-query groups over 80 row ranges of 1,504 rows):
-    each range's first thirty-second (32 rows) is scored first and sets the queries' floors."""
-    n, d = 120_000, 256
+    """200K rows, 600 queries (three 256-query groups over 80 row ranges of 2,512 rows):
+    each range's first sixty-fourth (32 rows) is scored first and sets the queries' floors."""
+    n, d = 200_000, 256
     emb = rng.standard_normal((n, d)).astype(np.float32)
     emb /= np.linalg.norm(emb, axis=1, keepdims=True)
     mods = rng.integers(0, 3, size=n).astype(np.int32)
@@ -83,11 +83,11 @@ def test_rq_sampled_floor(rng):
 
 @pytest.mark.parametrize("q,k,filt,uniform", [(600, 10, -1, True), (300, 16, 1, False), (600, 5, 2, False)])
 def test_rq_sampled_floor_equals_scan_bit_for_bit(q, k, filt, uniform, rng):
-    """The sampled floor drops no row that belongs in a list: on 120K rows (each 256-query
+    """The sampled floor drops no row that belongs in a list: on 200K rows (each 256-query
     group's ranges sampled for the floor), the batch's ids and score bits equal those of
     the same queries scored in batches of 32 by k_batch_scan (no floor), with a modality
     filter and with per-query times too."""
-    n, d = 120_000, 256
+    n, d = 200_000, 256
     emb = rng.standard_normal((n, d)).astype(np.float32)
     emb /= np.linalg.norm(emb, axis=1, keepdims=True)
     mods = rng.integers(0, 3, size=n).astype(np.int32)
@@ -109,11 +109,11 @@ def test_rq_sampled_floor_equals_scan_bit_for_bit(q, k, filt, uniform, rng):
 
 
 def test_rq_sampled_floor_sparse_filter_and_neighbours(rng):
-    """140K rows, 300 queries (two 256-query groups over 128 row ranges of 1,104 rows,
+    """280K rows, 300 queries (two 256-query groups over 128 row ranges of 2,192 rows,
     sampled): a modality filter that keeps 1 row in 2,000 (the sampled rows hold fewer than
     K of them, so the floors are -FLT_MAX scores), and the neighbour-search form (plain dot
     products, self excluded) over the same sampled ranges."""
-    n, d = 140_000, 256
+    n, d = 280_000, 256
     emb = rng.standard_normal((n, d)).astype(np.float32)
     emb /= np.linalg.norm(emb, axis=1, keepdims=True)
     mods = (rng.random(n) < 0.0005).astype(np.int32)
