@@ -222,49 +222,46 @@ __global__ __launch_bounds__(kBWaves * 64) void k_batch_scan(BatchArgs a) {
     }
 }
 
-// One wave per query: merge n_rranges lists of K keys into the best k_out.
-__global__ __launch_bounds__(64) void k_batch_merge(const uint64_t* __restrict__ part, int32_t n_rranges,
-                                                    int32_t kpart, int32_t q, int32_t k_out,
-                                                    uint64_t* __restrict__ out) {
-    const int lane = int(threadIdx.x);
+// One workgroup of eight waves per query: merge n_rranges lists of K keys into the best
+// k_out. Each wave takes every eighth round of 8 x 64 keys (loads in flight together; a
+// chunk with many keys under the wave's bound is sorted and merged in registers, one with
+// a few inserts them one by one), then wave 0 merges the eight lists. (One wave per
+// query, inserting every key under its bound one at a time: 21 us for 256 queries of
+// 4,096 keys; this form: 13 us.)
+constexpr int kMergeWaves = 8;
+__global__ __launch_bounds__(kMergeWaves * 64) void k_batch_merge(const uint64_t* __restrict__ part, int32_t n_rranges,
+                                                                  int32_t kpart, int32_t q, int32_t k_out,
+                                                                  uint64_t* __restrict__ out) {
+    __shared__ uint64_t s_l[kMergeWaves][64];
+    const int lane = int(threadIdx.x & 63u), wave = int(threadIdx.x >> 6);
     const int qi = int(blockIdx.x);
-    if (qi >= q) return;
+    if (qi >= q) return;                               // the whole workgroup
     const int qb = qi / kBQ, j = qi % kBQ;
     uint64_t list = kEmptyKey, thr = kEmptyKey;
     const int total = n_rranges * kpart;
-    // eight 64-key chunks loaded at a time (their loads in flight together)
+    const int kshift = kpart == 8 ? 3 : 4;             // kpart is 8 or 16 (batch_kpart)
     constexpr int kMergeLd = 8;
-    for (int base = 0; base < total; base += 64 * kMergeLd) {
+    for (int base = wave * 64 * kMergeLd; base < total; base += kMergeWaves * 64 * kMergeLd) {
         uint64_t xs[kMergeLd];
 #pragma unroll
         for (int c = 0; c < kMergeLd; ++c) {
             const int t = base + c * 64 + lane;
             xs[c] = kEmptyKey;
             if (t < total) {
-                const int r = t / kpart, s = t % kpart;
+                const int r = t >> kshift, s = t & (kpart - 1);
                 xs[c] = part[((int64_t(qb) * n_rranges + r) * kBQ + j) * kpart + s];
             }
         }
 #pragma unroll
-        for (int c = 0; c < kMergeLd; ++c) {
-            const uint64_t x = xs[c];
-            uint64_t msk = __ballot(x < thr);
-            while (msk) {
-                const int src = __ffsll((unsigned long long)msk) - 1;
-                msk &= msk - 1;
-                const uint64_t y = __shfl(x, src);
-                if (y < thr) {
-                    const uint64_t below = __ballot(list < y);
-                    const int pos = __popcll(below);
-                    const uint64_t up = __shfl_up(list, 1u);
-                    const uint64_t v = (lane < pos) ? list : ((lane == pos) ? y : up);
-                    list = (lane < k_out) ? v : kEmptyKey;
-                    thr = __shfl(list, k_out - 1);
-                }
-            }
-        }
+        for (int c = 0; c < kMergeLd; ++c) wave_offer(list, thr, xs[c], lane, k_out);
     }
-    if (lane < k_out) out[int64_t(qi) * k_out + lane] = list;
+    s_l[wave][lane] = list;
+    __syncthreads();
+    if (wave == 0) {
+#pragma unroll
+        for (int w = 1; w < kMergeWaves; ++w) list = wave_merge64(list, s_l[w][lane], lane, k_out);
+        if (lane < k_out) out[int64_t(qi) * k_out + lane] = list;
+    }
 }
 
 // Exact fp32 rescoring of kc candidates per node; keeps k_out by (score desc, id asc).
@@ -373,7 +370,8 @@ int launch_batch_scan(const BatchArgs& a, hipStream_t s) {
 
 int launch_batch_merge(const uint64_t* part, int32_t n_rranges, int32_t kpart, int32_t q, int32_t k_out,
                        uint64_t* out, hipStream_t s) {
-    MARS_LAUNCH(k_batch_merge, dim3(unsigned(q)), dim3(64), 0, s, part, n_rranges, kpart, q, k_out, out);
+    MARS_CHECK(kpart == 8 || kpart == 16, MARS_ERR_INVALID, "batched merge: %d keys per range", kpart);
+    MARS_LAUNCH(k_batch_merge, dim3(unsigned(q)), dim3(kMergeWaves * 64), 0, s, part, n_rranges, kpart, q, k_out, out);
     return MARS_OK;
 }
 
