@@ -141,3 +141,34 @@ def test_insert_knn_over_int8(corpus_10k):
         np.testing.assert_array_equal(knn, got)
     finally:
         dev.close()
+
+
+def test_insert_knn_ties_fall_back():
+    """Nodes whose neighbours tie: 25 rows of the corpus are one vector, and two of the
+    inserted nodes are that vector too, so the 8th and 16th best scores of their lists are
+    equal and the fp16 search cannot certify them. The insert then takes the int8 pass (64
+    candidates, past the ties) or, where its certificate fails too, the fp16 lists: either
+    way the exact k-NN up to the ties (eight of the copies), the other nodes' lists exact,
+    a node never its own neighbour."""
+    c = corpus.make_corpus(8008, 768, seed=93)
+    base = 8000
+    emb = c.embeddings.copy()
+    dup = emb[17].copy()
+    copies = np.arange(100, 100 + 24 * 300, 300)
+    emb[copies] = dup
+    emb[base:base + 2] = dup
+    g = corpus.nsn_graph(corpus.Corpus(emb[:base], c.modalities[:base], c.timestamps[:base],
+                                       c.episode_ids[:base], 93))
+    dev = Dev(g.embeddings, g.modalities, g.timestamps, g.row_offsets, g.col_indices, g.episode_ids, cap_nodes=8008)
+    mars_amd.upload_int8_embeddings(dev.dg)
+    try:
+        st, got = mars_amd.insert_nodes(dev.dg, emb[base:base + 8], c.modalities[base:base + 8],
+                                        c.timestamps[base:base + 8], c.episode_ids[base:base + 8], knn_k=8,
+                                        return_knn=True)
+        assert st.nodes_added == 8
+        check_knn_exact(emb[:base + 8], base, got, 8)
+        for i in (0, 1):                      # the copies: eight of the tied rows
+            allowed = (set(copies.tolist()) | {17, base, base + 1}) - {base + i}
+            assert set(got[i].tolist()) <= allowed, got[i]
+    finally:
+        dev.close()
