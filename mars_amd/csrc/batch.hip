@@ -385,7 +385,7 @@ int launch_batch_topk(BatchArgs a, int32_t k_out, uint64_t* out, hipStream_t s, 
     // The floor pays where a range is long: without it a query inserts about
     // K (1 + ln(rows / K)) rows per range (every new best of the rows seen so far), with
     // it about rows x K / sampled rows.
-    if (batch_uses_rq(a.q) && a.rows_per_range >= kSampleDiv * kSampleRowsMin) {
+    if ((batch_uses_rq(a.q) || batch_uses_gemm(a.q)) && a.rows_per_range >= kSampleDiv * kSampleRowsMin) {
         BatchArgs b = a;
         b.rows_per_range = std::min<int64_t>(kSampleRowsMax, a.rows_per_range / kSampleDiv / 16 * 16);
         b.range_stride = a.rows_per_range;

@@ -17,10 +17,16 @@
 //  Buffer b holds a stage's corpus pieces in the first 64 KiB of LDS and its query
 //  pieces in the next, so every fragment read is one base register plus an immediate.
 //
-//  Selection: after a tile, the raw accumulators go through the free stage buffer 32
-//  rows at a time ([query][row], 16-byte writes and reads), and thread t, the owner of
-//  query q0 + t, fuses its scores (decay, filter) and keeps its best K keys in
-//  registers. Output: K keys per (query, row range) in the layout k_batch_merge reads.
+//  Selection: thread t, the owner of query q0 + t, keeps its best K keys in registers.
+//  Once every list is full, the owners publish a threshold per query (their K-th score;
+//  a fused score f = dot x w with w in [0, 1] can reach it only if the raw dot does),
+//  and after a tile each lane offers the (query, row) pairs of its accumulators at or
+//  above their query's threshold into 16 slots per query in the free stage buffer; the
+//  owners then fuse and insert their few candidates (the slot selection). A tile where
+//  some query gets more than 16 candidates, and every tile before the thresholds, goes
+//  the full way instead: the raw accumulators pass through the free stage buffer 32
+//  rows at a time ([query][row], 16-byte writes and reads) and the owners test all of
+//  their scores. Output: K keys per (query, row range) in the layout k_batch_merge reads.
 // ============================================================================
 #include "device.hpp"
 
@@ -37,6 +43,8 @@ constexpr int kMThreads = 256;
 constexpr int kMChunk = 32;     // rows per staged chunk of the first tile
 constexpr int kPartQ = 64;      // queries per block of the partial-key layout
 constexpr int kMDma = 4;        // load instructions per wave and operand per stage
+constexpr int kMSlots = 8;      // candidate slots per query and tile (the slot selection)
+constexpr int kMRec = 64;       // per wave and tile: 16-dot records of lanes that reach a threshold
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
@@ -47,13 +55,28 @@ struct MmLds {
     u32x4 q[kMB][kMQ * 4];      // 4 x 16 KiB: 256 queries x 4 pieces per stage
     float w[kMR];               // row decay weight (one query time) or row timestamp
     uint32_t keepm[kMR / kMChunk];   // bit j of word c: row 32 c + j passes the modality filter
+    float thr[kMQ];             // per query: raw dot products below it cannot enter its list
+    uint32_t cnt[kMQ];          // per query: candidates offered in this tile
+    uint32_t rhdr[kMThreads / 64][kMRec];  // per record: query << 8 | first row of the lane's 16
+    uint32_t wfast[kMThreads / 64];  // per wave: every query it owns has a threshold
+    uint32_t wover[kMThreads / 64];  // per wave: a query of its half got more than kMSlots
 };
 static_assert(sizeof(u32x4) * kMR * 4 == size_t(kMQ / 2) * kMChunk * sizeof(float), "half the queries per operand");
+static_assert(sizeof(u32x4) * kMQ * 4 == size_t(kMQ) * kMSlots * 8, "the slots fill the query half of a stage buffer");
+static_assert(sizeof(u32x4) * kMR * 4 == size_t(kMThreads / 64) * kMRec * 64, "the records fill its corpus half");
 static_assert(kMThreads / 64 * kMDma * 64 == kMR * 4, "the waves' loads cover a stage");
 
 // s_waitcnt immediates (gfx9 encoding: vmcnt[3:0] and [15:14], expcnt[6:4], lgkmcnt[11:8])
 constexpr int wait_vm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 constexpr int kWaitLgkm0 = 15 | (3 << 14) | (7 << 4);
+
+// A pointer the wave holds in SGPRs (the same in every lane), so that loads take the
+// scalar-base plus 32-bit vector-offset form.
+__device__ inline const char* uniform_ptr(const char* p) {
+    const uint64_t u = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane(uint32_t(u)), hi = __builtin_amdgcn_readfirstlane(uint32_t(u >> 32));
+    return reinterpret_cast<const char*>((uint64_t(hi) << 32) | lo);
+}
 
 // Workgroup barrier without the memory fence of __syncthreads (which waits for every
 // load in flight, the stage prefetches included): callers wait for what they need first.
@@ -87,28 +110,31 @@ void k_batch_mm(BatchArgs a) {
     // the last tile load a clamped tile nobody reads), so the wait counts stay exact.
     const int srow = (wave * kMDma) * 16 + (lane >> 2);            // + 16 j
     const int spiece = (lane & 3) ^ ((srow >> 1) & 3);             // the same for every j
-    int qrow[kMDma];
+    // Addresses: a uniform base (the tile's first row; the query array) plus a 32-bit
+    // byte offset per lane (within 256 rows, within the batch's queries).
+    uint32_t qoff[kMDma];
 #pragma unroll
     for (int j = 0; j < kMDma; ++j) {
         const int q = q0 + srow + 16 * j;
-        qrow[j] = q < a.q ? q : a.q - 1;
+        qoff[j] = uint32_t(q < a.q ? q : a.q - 1) * uint32_t(d * 2) + uint32_t(spiece * 16);
     }
     // stage st of tile `tile` (clamped: stages past the last tile load the last one again)
     auto issue_stage = [&](int tile, int st) {
         const int b = st & (kMB - 1);              // NS % kMB == 0: a stage's buffer is st % kMB
         tile = tile < int(ntiles) ? tile : int(ntiles) - 1;
-        const int koff = st * kMK + spiece * 8;
-        const int64_t tbase = r0 + int64_t(tile) * kMR + srow;
+        const int64_t trow = r0 + int64_t(tile) * kMR;
+        const char* const tb = uniform_ptr(reinterpret_cast<const char*>(a.emb16 + trow * d) + st * kMK * 2);
+        const char* const qb = uniform_ptr(reinterpret_cast<const char*>(a.qh) + st * kMK * 2);
+        const uint32_t last = uint32_t(r1 - 1 - trow < kMR - 1 ? r1 - 1 - trow : kMR - 1);   // rows past r1 - 1 clamp
 #pragma unroll
         for (int j = 0; j < kMDma; ++j) {
-            int64_t row = tbase + 16 * j;
-            row = row < r1 ? row : r1 - 1;
-            __builtin_amdgcn_global_load_lds(a.emb16 + row * d + koff, &sh.e[b][(wave * kMDma + j) * 64], 16, 0, 0);
+            const uint32_t rl = uint32_t(srow + 16 * j) < last ? uint32_t(srow + 16 * j) : last;
+            __builtin_amdgcn_global_load_lds(tb + (rl * uint32_t(d * 2) + uint32_t(spiece * 16)),
+                                             &sh.e[b][(wave * kMDma + j) * 64], 16, 0, 0);
         }
 #pragma unroll
         for (int j = 0; j < kMDma; ++j)
-            __builtin_amdgcn_global_load_lds(a.qh + int64_t(qrow[j]) * d + koff, &sh.q[b][(wave * kMDma + j) * 64],
-                                             16, 0, 0);
+            __builtin_amdgcn_global_load_lds(qb + qoff[j], &sh.q[b][(wave * kMDma + j) * 64], 16, 0, 0);
     };
 
     uint64_t list[K];                              // query q0 + tid
@@ -118,6 +144,13 @@ void k_batch_mm(BatchArgs a) {
     const bool my_plain = my_q >= a.q_plain;
     const int64_t my_self = (a.self_base >= 0 && my_plain) ? a.self_base + (my_q - a.q_plain) : -1;
     const float my_tq = my_q < a.q ? a.tq[my_q] : 0.0f;
+    // the sampled score floor (a lower bound of the query's final floor_k-th best score): no
+    // row below it can be among the query's results, so none is kept
+    float my_floor = -INFINITY;
+    if (a.floor_keys != nullptr && my_q < a.q) {
+        const uint64_t fk = a.floor_keys[int64_t(my_q) * a.floor_k + a.floor_k - 1];
+        if (fk != kEmptyKey) my_floor = key_score(fk);
+    }
 
     // row attributes (timestamp, modality) of the next tile, one tile ahead
     const float tq0 = a.tq[0];
@@ -189,6 +222,32 @@ void k_batch_mm(BatchArgs a) {
     float* const wbase = wq ? stg_hi : stg_lo;                      // this wave's 128 queries
     const float* const obase = (tid < 128 ? stg_lo : stg_hi) + (tid & 127) * kMChunk;
     const int oswz = (tid >> 1) & 7;
+    // decay weights expf(-lambda max(0, dt)) lie in [0, 1] (up to expf's error) for a
+    // finite lambda >= 0
+    const bool weights_ok = a.lambda >= 0.0f && a.lambda < INFINITY;
+    // The owner's threshold for the next tile: the larger of its floor and, once its list is
+    // full, its K-th score s; a row below it cannot enter the list. Neighbour searches
+    // compare the dot itself. Fused scores f = fl(dot x w), filtered rows -FLT_MAX: with
+    // decay weights w <= 1 + 2^-22 (expf of a non-positive argument, within a few ulps of
+    // its value in [0, 1]) and s > 0, a dot below s (1 - 2^-20) gives f < s, so the
+    // threshold is s (1 - 2^-20). Without a threshold (no floor, list not full; or fused
+    // scores with s <= 0) the wave's tiles go the full way. Queries past the batch offer
+    // nothing.
+    auto publish = [&]() {
+        float th = INFINITY;
+        bool ok = true;
+        if (my_q < a.q) {
+            th = fmaxf(list[K - 1] != kEmptyKey ? key_score(list[K - 1]) : -INFINITY, my_floor);
+            ok = th > -INFINITY && (my_plain || (weights_ok && th > 0.0f));
+            if (!my_plain) th *= 1.0f - 0x1p-20f;
+        }
+        int ut = tid;
+        asm volatile("" : "+v"(ut));
+        sh.thr[ut] = th;
+        sh.cnt[ut] = 0u;
+        const uint64_t bad = __ballot(!ok);
+        if (lane == 0) sh.wfast[wave] = bad == 0u ? 1u : 0u;
+    };
     // acc[rt][qt][v] = C[row wr*128 + rt*32 + 8*(v/4) + 4*lh + v%4][query wq*128 + qt*32 + lm]:
     // v = 4 g .. 4 g + 3 are rows 4 (2 g + lh) .. + 3 of the chunk, one 16-byte slot
     auto stage_rows = [&](const f32x16 (&ac)[4]) {
@@ -237,8 +296,8 @@ void k_batch_mm(BatchArgs a) {
 #pragma unroll
             for (int j = 0; j < kMChunk; ++j) sc[j] = x[j];
         }
-        // rows at or above the K-th score held (NaN passes to the key test)
-        const float bound = list[K - 1] != kEmptyKey ? key_score(list[K - 1]) : -INFINITY;
+        // rows at or above the K-th score held and the floor (NaN passes to the key test)
+        const float bound = fmaxf(list[K - 1] != kEmptyKey ? key_score(list[K - 1]) : -INFINITY, my_floor);
         uint32_t pass = 0u;
 #pragma unroll
         for (int j = 0; j < kMChunk; ++j) {
@@ -259,6 +318,7 @@ void k_batch_mm(BatchArgs a) {
         }
     };
 
+    publish();                                     // the first tile's thresholds (floors)
     for (int64_t t = 0; t < ntiles; ++t) {
         const int64_t t0 = r0 + t * kMR;
         {
@@ -290,21 +350,129 @@ void k_batch_mm(BatchArgs a) {
         // every wave is done with buffer kMB - 1 (the tile's last stage): the selection's
         // LDS until the deferred load of the next tile's stage kMB - 1 refills it
         lds_barrier();
-        // 32 rows at a time: the two waves holding them stage their raw scores, then the
-        // owner of each query fuses its 32 scores and keeps its best K. Row half h is a loop,
-        // not unrolled (the code then stays in the instruction cache); the four 32-row tiles
-        // of a half are unrolled, so each stages a fixed accumulator. (The order of the rows
-        // does not change the result: the list keeps the K least keys of a total order.)
-#pragma unroll 1
-        for (int h = 0; h < 2; ++h) {
+        // (The order in which rows are offered does not change the result: the list keeps
+        // the K least keys of a total order.)
+        bool full_way = (sh.wfast[0] & sh.wfast[1] & sh.wfast[2] & sh.wfast[3]) == 0u;
+        if (!full_way) {
+            // Slot selection, in three steps.
+            // 1. Each lane tests its 16 dots of each 32 x 32 block at once: their maximum
+            //    against the query's threshold, and x * 0, NaN exactly for a NaN or infinite
+            //    dot (offered, as the full way offers NaN). A lane that reaches it appends
+            //    the block's 16 dots to its wave's records (ballot compaction).
+            // 2. The wave's lanes take one record each and offer every dot not below the
+            //    threshold: a slot index from the query's counter, then (row, dot).
+            // 3. The owners fuse and insert their candidates.
+            // More than kMRec records in a wave or kMSlots candidates for a query: the tile
+            // goes the full way. The lane index is laundered so that the addresses and rows
+            // derived from it are computed here rather than held across the tile loop.
+            int ut = tid;
+            asm volatile("" : "+v"(ut));
+            const int ul = ut & 63, ulm = ut & 31;
+            u32x4* const rec = &sh.e[kMB - 1][wave * 4 * kMRec];
+            uint2* const slots = reinterpret_cast<uint2*>(&sh.q[kMB - 1][0]);
+            const uint32_t rowb = uint32_t(wr * 128 + 4 * (ul >> 5));
+            uint32_t nrec = 0;                                          // uniform
+            auto offer_block = [&](const f32x16& xv, int rt, int qt) {
+                const int ql = wq * 128 + qt * 32 + ulm;
+                const float th = sh.thr[ql];
+                // the maximum (NaN ignored) and the sum (NaN if a dot is NaN), as trees
+                const float m = fmaxf(fmaxf(fmaxf(fmaxf(xv[0], xv[1]), xv[2]), fmaxf(fmaxf(xv[3], xv[4]), xv[5])),
+                                      fmaxf(fmaxf(fmaxf(xv[6], xv[7]), xv[8]), fmaxf(fmaxf(xv[9], xv[10]), xv[11])));
+                const float m2 = fmaxf(fmaxf(fmaxf(xv[12], xv[13]), xv[14]), xv[15]);
+                const float s0 = (xv[0] + xv[1]) + (xv[2] + xv[3]), s1 = (xv[4] + xv[5]) + (xv[6] + xv[7]);
+                const float s2 = (xv[8] + xv[9]) + (xv[10] + xv[11]), s3 = (xv[12] + xv[13]) + (xv[14] + xv[15]);
+                const float sum = (s0 + s1) + (s2 + s3);
+                const bool hit = !(fmaxf(m, m2) < th) || sum != sum;
+                const uint64_t hb = __ballot(hit);
+                if (hb != 0u) {
+                    const uint32_t idx = nrec + __builtin_amdgcn_mbcnt_hi(uint32_t(hb >> 32), __builtin_amdgcn_mbcnt_lo(uint32_t(hb), 0u));
+                    if (hit && idx < uint32_t(kMRec)) {
 #pragma unroll
-            for (int rt = 0; rt < 4; ++rt) {
-                if (wr == h) stage_rows(acc[rt]);
-                lds_barrier();
-                if (my_q < a.q) select_chunk(4 * h + rt, t0);
+                        for (int c = 0; c < 4; ++c)
+                            rec[c * kMRec + idx] = __builtin_bit_cast(u32x4, float4{xv[4 * c], xv[4 * c + 1], xv[4 * c + 2], xv[4 * c + 3]});
+                        sh.rhdr[wave][idx] = (uint32_t(ql) << 8) | (rowb + uint32_t(rt * 32));
+                    }
+                    nrec += uint32_t(__popcll(hb));
+                }
+            };
+            // two blocks at a time: a rolled loop (one copy of the offer code), the blocks'
+            // accumulators picked by a uniform switch
+#pragma unroll 1
+            for (int h = 0; h < 8; ++h) {
+                f32x16 x0, x1;
+                switch (h) {
+                    case 0: x0 = acc[0][0]; x1 = acc[0][1]; break;
+                    case 1: x0 = acc[0][2]; x1 = acc[0][3]; break;
+                    case 2: x0 = acc[1][0]; x1 = acc[1][1]; break;
+                    case 3: x0 = acc[1][2]; x1 = acc[1][3]; break;
+                    case 4: x0 = acc[2][0]; x1 = acc[2][1]; break;
+                    case 5: x0 = acc[2][2]; x1 = acc[2][3]; break;
+                    case 6: x0 = acc[3][0]; x1 = acc[3][1]; break;
+                    default: x0 = acc[3][2]; x1 = acc[3][3]; break;
+                }
+                offer_block(x0, h >> 1, 2 * (h & 1));
+                offer_block(x1, h >> 1, 2 * (h & 1) + 1);
+            }
+            bool over = nrec > uint32_t(kMRec);
+            if (!over && uint32_t(ul) < nrec) {
+                const uint32_t hdr = sh.rhdr[wave][ul];
+                const uint32_t q = hdr >> 8, rb = hdr & 255u;
+                const float th = sh.thr[q];
+                float xv[16];
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const float4 f4 = __builtin_bit_cast(float4, rec[c * kMRec + ul]);
+                    xv[4 * c] = f4.x; xv[4 * c + 1] = f4.y; xv[4 * c + 2] = f4.z; xv[4 * c + 3] = f4.w;
+                }
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    if (!(xv[v] < th)) {
+                        const uint32_t i = atomicAdd(&sh.cnt[q], 1u);
+                        if (i < uint32_t(kMSlots))
+                            slots[q * kMSlots + ((i + q) & (kMSlots - 1))] = uint2{rb + uint32_t(8 * (v >> 2) + (v & 3)), __float_as_uint(xv[v])};
+                        else
+                            over = true;
+                    }
+                }
+            }
+            const uint64_t ob = __ballot(over);
+            if (lane == 0) sh.wover[wave] = ob != 0u ? 1u : 0u;
+            lds_barrier();
+            full_way = (sh.wover[0] | sh.wover[1] | sh.wover[2] | sh.wover[3]) != 0u;
+            if (!full_way) {
+                if (my_q < a.q) {
+                    const uint32_t n = sh.cnt[ut];
+                    for (uint32_t i = 0; i < n; ++i) {
+                        const uint2 sl = slots[ut * kMSlots + ((i + uint32_t(ut)) & (kMSlots - 1))];
+                        const int j = int(sl.x);
+                        const int64_t row = t0 + j;
+                        if (row >= r1 || row == my_self) continue;
+                        const float f = fuse_row(__uint_as_float(sl.y), sh.w[j], (sh.keepm[j >> 5] >> (j & 31)) & 1u);
+                        const uint64_t key = make_key(f, uint32_t(row));
+                        if (key < list[K - 1]) reg_insert<K>(list, key);
+                    }
+                }
+                // every owner has read its slots before the stage load below refills them
                 lds_barrier();
             }
         }
+        if (full_way) {
+            // 32 rows at a time: the two waves holding them stage their raw scores, then the
+            // owner of each query fuses its 32 scores and keeps its best K. Row half h is a
+            // loop, not unrolled (the code then stays in the instruction cache); the four
+            // 32-row tiles of a half are unrolled, so each stages a fixed accumulator.
+#pragma unroll 1
+            for (int h = 0; h < 2; ++h) {
+#pragma unroll
+                for (int rt = 0; rt < 4; ++rt) {
+                    if (wr == h) stage_rows(acc[rt]);
+                    lds_barrier();
+                    if (my_q < a.q) select_chunk(4 * h + rt, t0);
+                    lds_barrier();
+                }
+            }
+        }
+        publish();                             // the next tile's thresholds
         issue_stage(int(t) + 1, kMB - 1);      // into the buffer the selection used
     }
     // the last stages' loads (past the last tile) must land before the workgroup ends
@@ -339,7 +507,8 @@ int launch_mm_k(const BatchArgs& a, hipStream_t s) {
 int launch_batch_mm(const BatchArgs& a, hipStream_t s) {
     MARS_CHECK(a.k >= 1 && a.k <= 16, MARS_ERR_UNSUPPORTED, "batched scoring keeps at most 16 per query (asked %d)",
                a.k);
-    MARS_CHECK(a.floor_keys == nullptr, MARS_ERR_INVALID, "k_batch_mm takes no score floor");
+    MARS_CHECK(a.floor_keys == nullptr || (a.floor_k >= 1 && a.floor_k <= 16), MARS_ERR_INVALID,
+               "batched scoring: floor of %d keys per query", a.floor_k);
     return a.k <= 8 ? launch_mm_k<8>(a, s) : launch_mm_k<16>(a, s);
 }
 

@@ -16,8 +16,8 @@ import oracle
 from mars_amd import RetrievalConfig, RetrievalScope, corpus
 
 from conftest import RTOL_F16_VS_F32, RTOL_F32
-from parity import (FLT_MAX, LAM, T_Q, Dev, batch_check, check_episode, check_episode_results, check_global,
-                    check_results_exact, check_scores, episode_cfg, ocfg, random_graph)
+from parity import (FLT_MAX, LAM, T_Q, Dev, batch_check, check_batch_topk, check_episode, check_episode_results,
+                    check_global, check_results_exact, check_scores, episode_cfg, ocfg, random_graph)
 
 pytestmark = pytest.mark.gpu
 
@@ -270,6 +270,34 @@ def test_batch_tiled_widths(d, k, filt, uniform, rng):
         qn = rng.choice(n, 1030, replace=False)
         tq = np.float32(T_Q) if uniform else rng.uniform(300, 600, 1030).astype(np.float32)
         batch_check(dev, qn, RetrievalConfig(top_k=k, time_decay_lambda=LAM, modality_filter=filt), tq, emb)
+    finally:
+        dev.close()
+
+
+@pytest.mark.parametrize("n,k,filt,uniform,lam", [(60_000, 10, -1, True, LAM), (60_000, 16, 1, False, LAM),
+                                                   (110_000, 4, -1, False, 0.0), (110_000, 8, 2, True, LAM),
+                                                   (110_000, 16, -1, False, LAM)])
+def test_batch_tiled_long_ranges(n, k, filt, uniform, lam, rng):
+    """k_batch_mm over long row ranges (1,030 queries): 60,000 rows, ranges of five 256-row
+    tiles, thresholds from the owners' lists after the first tile; 110,000 rows, ranges of
+    2,304 rows, long enough for the sampled pass whose floors give thresholds from the
+    first tile. Most tiles go through the candidate slots, the others (a query with more
+    candidates than slots) the full way; decay per query and per batch, no decay, filters.
+    A quarter of the queries and the six of the last, partial query tile are checked
+    against the oracle's top-K."""
+    d, q = 256, 1030
+    emb, mods, ts, row, col, _ = random_graph(rng, n, d)
+    dev = Dev(emb, mods, ts, row, col, fp16=True)
+    try:
+        qs = emb[rng.choice(n, q, replace=False)]
+        tq = np.full(q, T_Q, np.float32) if uniform else rng.uniform(300, 600, q).astype(np.float32)
+        cfg = RetrievalConfig(top_k=k, time_decay_lambda=lam, modality_filter=filt)
+        buf = mars_amd.DeviceBuffer.from_array(qs)
+        try:
+            ids, sc = mars_amd.query_batch(dev.dg, dev.ctx, buf.ptr, q, tq if not uniform else np.float32(T_Q), cfg)
+        finally:
+            buf.free()
+        check_batch_topk(dev.og, qs, tq, cfg, ids, sc, n, check_rows=list(range(0, 1024, 4)) + list(range(1024, q)))
     finally:
         dev.close()
 
