@@ -372,28 +372,27 @@ void k_batch_mm(BatchArgs a) {
             uint2* const slots = reinterpret_cast<uint2*>(&sh.q[kMB - 1][0]);
             const uint32_t rowb = uint32_t(wr * 128 + 4 * (ul >> 5));
             uint32_t nrec = 0;                                          // uniform
-            auto offer_block = [&](const f32x16& xv, int rt, int qt) {
-                const int ql = wq * 128 + qt * 32 + ulm;
-                const float th = sh.thr[ql];
-                // the maximum (NaN ignored) and the sum (NaN if a dot is NaN), as trees
+            // whether a lane's 16 dots of a block can reach threshold th: their maximum (NaN
+            // ignored) is not below it, or their sum is NaN (a NaN dot), as trees
+            auto block_hit = [](const f32x16& xv, float th) {
                 const float m = fmaxf(fmaxf(fmaxf(fmaxf(xv[0], xv[1]), xv[2]), fmaxf(fmaxf(xv[3], xv[4]), xv[5])),
                                       fmaxf(fmaxf(fmaxf(xv[6], xv[7]), xv[8]), fmaxf(fmaxf(xv[9], xv[10]), xv[11])));
                 const float m2 = fmaxf(fmaxf(fmaxf(xv[12], xv[13]), xv[14]), xv[15]);
                 const float s0 = (xv[0] + xv[1]) + (xv[2] + xv[3]), s1 = (xv[4] + xv[5]) + (xv[6] + xv[7]);
                 const float s2 = (xv[8] + xv[9]) + (xv[10] + xv[11]), s3 = (xv[12] + xv[13]) + (xv[14] + xv[15]);
                 const float sum = (s0 + s1) + (s2 + s3);
-                const bool hit = !(fmaxf(m, m2) < th) || sum != sum;
-                const uint64_t hb = __ballot(hit);
-                if (hb != 0u) {
-                    const uint32_t idx = nrec + __builtin_amdgcn_mbcnt_hi(uint32_t(hb >> 32), __builtin_amdgcn_mbcnt_lo(uint32_t(hb), 0u));
-                    if (hit && idx < uint32_t(kMRec)) {
+                return !(fmaxf(m, m2) < th) || sum != sum;
+            };
+            // append the block of the lanes that hit to the wave's records
+            auto put_records = [&](const f32x16& xv, bool hit, uint64_t hb, int ql, int rt) {
+                const uint32_t idx = nrec + __builtin_amdgcn_mbcnt_hi(uint32_t(hb >> 32), __builtin_amdgcn_mbcnt_lo(uint32_t(hb), 0u));
+                if (hit && idx < uint32_t(kMRec)) {
 #pragma unroll
-                        for (int c = 0; c < 4; ++c)
-                            rec[c * kMRec + idx] = __builtin_bit_cast(u32x4, float4{xv[4 * c], xv[4 * c + 1], xv[4 * c + 2], xv[4 * c + 3]});
-                        sh.rhdr[wave][idx] = (uint32_t(ql) << 8) | (rowb + uint32_t(rt * 32));
-                    }
-                    nrec += uint32_t(__popcll(hb));
+                    for (int c = 0; c < 4; ++c)
+                        rec[c * kMRec + idx] = __builtin_bit_cast(u32x4, float4{xv[4 * c], xv[4 * c + 1], xv[4 * c + 2], xv[4 * c + 3]});
+                    sh.rhdr[wave][idx] = (uint32_t(ql) << 8) | (rowb + uint32_t(rt * 32));
                 }
+                nrec += uint32_t(__popcll(hb));
             };
             // two blocks at a time: a rolled loop (one copy of the offer code), the blocks'
             // accumulators picked by a uniform switch
@@ -410,8 +409,15 @@ void k_batch_mm(BatchArgs a) {
                     case 6: x0 = acc[3][0]; x1 = acc[3][1]; break;
                     default: x0 = acc[3][2]; x1 = acc[3][3]; break;
                 }
-                offer_block(x0, h >> 1, 2 * (h & 1));
-                offer_block(x1, h >> 1, 2 * (h & 1) + 1);
+                // both blocks' tests first (independent, so their instructions interleave)
+                const int ql0 = wq * 128 + (h & 1) * 64 + ulm, ql1 = ql0 + 32;
+                const float th0 = sh.thr[ql0], th1 = sh.thr[ql1];
+                const bool hit0 = block_hit(x0, th0), hit1 = block_hit(x1, th1);
+                const uint64_t hb0 = __ballot(hit0), hb1 = __ballot(hit1);
+                if ((hb0 | hb1) != 0u) {
+                    put_records(x0, hit0, hb0, ql0, h >> 1);
+                    put_records(x1, hit1, hb1, ql1, h >> 1);
+                }
             }
             bool over = nrec > uint32_t(kMRec);
             if (!over && uint32_t(ul) < nrec) {
@@ -424,15 +430,20 @@ void k_batch_mm(BatchArgs a) {
                     const float4 f4 = __builtin_bit_cast(float4, rec[c * kMRec + ul]);
                     xv[4 * c] = f4.x; xv[4 * c + 1] = f4.y; xv[4 * c + 2] = f4.z; xv[4 * c + 3] = f4.w;
                 }
+                // the record's dots not below the threshold: one slot reservation for all
+                // of them, then each dot read back from the record by its index
+                uint32_t hits = 0;
 #pragma unroll
-                for (int v = 0; v < 16; ++v) {
-                    if (!(xv[v] < th)) {
-                        const uint32_t i = atomicAdd(&sh.cnt[q], 1u);
-                        if (i < uint32_t(kMSlots))
-                            slots[q * kMSlots + ((i + q) & (kMSlots - 1))] = uint2{rb + uint32_t(8 * (v >> 2) + (v & 3)), __float_as_uint(xv[v])};
-                        else
-                            over = true;
-                    }
+                for (int v = 0; v < 16; ++v) hits |= uint32_t(!(xv[v] < th)) << v;
+                const uint32_t n = uint32_t(__popc(hits));
+                uint32_t i = n != 0u ? atomicAdd(&sh.cnt[q], n) : 0u;
+                if (i + n > uint32_t(kMSlots)) over = true;
+                const uint32_t* const rw = reinterpret_cast<const uint32_t*>(rec);
+                for (; hits != 0u && i < uint32_t(kMSlots); ++i) {
+                    const uint32_t v = uint32_t(__builtin_ctz(hits));
+                    hits &= hits - 1u;
+                    slots[q * kMSlots + ((i + q) & (kMSlots - 1))] =
+                        uint2{rb + 8u * (v >> 2) + (v & 3u), rw[((v >> 2) * kMRec + ul) * 4 + (v & 3u)]};
                 }
             }
             const uint64_t ob = __ballot(over);
