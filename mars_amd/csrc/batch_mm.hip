@@ -104,12 +104,12 @@ void k_batch_mm(BatchArgs a) {
 
     // Stage loads go straight from global memory to LDS (global_load_lds_dwordx4): load
     // j of a wave fills 64 consecutive 16-byte slots, s = (wave * kMDma + j) * 64 + lane,
-    // i.e. slot s & 3 of row s >> 2, which holds piece (s & 3) ^ ((row >> 1) & 3) of the
-    // row's 32 k. The fragment reads of 8 consecutive rows then hit 8 distinct 16-byte
-    // bank groups. Every stage issues the same loads (rows clamped into range; stages past
+    // i.e. slot s & 3 of row s >> 2, which holds piece (s & 3) ^ ((row >> 2) & 3) of the
+    // row's 32 k. The fragment reads of 16 consecutive rows (a 16-lane group of a 16-byte
+    // read) then hit the 16 distinct 16-byte bank groups of the 256-byte LDS row. Every stage issues the same loads (rows clamped into range; stages past
     // the last tile load a clamped tile nobody reads), so the wait counts stay exact.
     const int srow = (wave * kMDma) * 16 + (lane >> 2);            // + 16 j
-    const int spiece = (lane & 3) ^ ((srow >> 1) & 3);             // the same for every j
+    const int spiece = (lane & 3) ^ ((srow >> 2) & 3);             // the same for every j
     // Addresses: a uniform base (the tile's first row; the query array) plus a 32-bit
     // byte offset per lane (within 256 rows, within the batch's queries).
     uint32_t qoff[kMDma];
@@ -174,7 +174,7 @@ void k_batch_mm(BatchArgs a) {
     f32x16 acc[4][4];
     f16x8 fa0[4], fb0[4], fa1[4], fb1[4];          // fragments of k-step 0 / 1 of a stage
     auto read_frags = [&](int b, int kk, f16x8 (&af)[4], f16x8 (&bf)[4]) {
-        const int pc = (2 * kk + lh) ^ ((lm >> 1) & 3);        // swizzled slot of this lane's piece
+        const int pc = (2 * kk + lh) ^ ((lm >> 2) & 3);        // swizzled slot of this lane's piece
 #pragma unroll
         for (int x = 0; x < 4; ++x) {
             af[x] = __builtin_bit_cast(f16x8, sh.e[b][(wr * 128 + x * 32 + lm) * 4 + pc]);
