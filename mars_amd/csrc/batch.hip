@@ -14,7 +14,7 @@
 //                query; the workgroup index puts all query blocks of a row range
 //                on the same XCD (id % 8 == r % 8) so they share its L2.
 //  k_batch_merge One wave per query merges the per-row-range keys.
-//  k_knn_rerank  Exact fp32 rescoring of k-NN candidates (16-lane group per node).
+//  k_knn_rerank  Exact fp32 rescoring of k-NN candidates (one wave per node).
 //
 //  Reference analogue: wmma_mma_similarity_kernel / wmma_similarity_kernel
 //  (src/wmma_similarity.cu:55-138), which score one query and are never called.
@@ -229,6 +229,7 @@ __global__ __launch_bounds__(kBWaves * 64) void k_batch_scan(BatchArgs a) {
 // query, inserting every key under its bound one at a time: 21 us for 256 queries of
 // 4,096 keys; this form: 13 us.)
 constexpr int kMergeWaves = 8;
+constexpr int kRerankPieces = 3;  // k_knn_rerank: 16-byte pieces per lane and row (d <= 768)
 __global__ __launch_bounds__(kMergeWaves * 64) void k_batch_merge(const uint64_t* __restrict__ part, int32_t n_rranges,
                                                                   int32_t kpart, int32_t q, int32_t k_out,
                                                                   uint64_t* __restrict__ out) {
@@ -273,8 +274,8 @@ __global__ __launch_bounds__(kMergeWaves * 64) void k_batch_merge(const uint64_t
 //     eps = |e16| |ftz(e16) - e| + |e| |ftz(e16) - e|      (both fp16 roundings)
 //           + g_mfma |e16|^2 + g_fp32 |e|^2 + u (|e16|^2 (1 + g_mfma) + |e|^2 (1 + g_fp32))
 // (row maxima for the query row too; g_mfma = 2 d u / (1 - d u), doubled for the MFMA's
-// unspecified order; g_fp32 = n u / (1 - n u) with n = d / 16 + 4 for this kernel's
-// per-lane chains and 16-lane reduction), so a k_out-th exact score above (kc-th fp16 score
+// unspecified order; g_fp32 = n u / (1 - n u) with n = 4 ceil(d / 256) + 6 for this
+// kernel's per-lane chains and 64-lane butterfly), so a k_out-th exact score above (kc-th fp16 score
 // + eps) leaves no row outside the candidates that could enter the list. Fewer than kc
 // candidates: every other row was one.
 __global__ __launch_bounds__(256) void k_knn_rerank(const float* __restrict__ emb, int64_t q0, int64_t nq,
@@ -282,27 +283,51 @@ __global__ __launch_bounds__(256) void k_knn_rerank(const float* __restrict__ em
                                                     int32_t k_out, int32_t* __restrict__ nbrs,
                                                     const uint32_t* __restrict__ nrm, int32_t* __restrict__ cert) {
     const int lane = int(threadIdx.x & 63u);
-    const int sub = lane & 15;
-    const int64_t node = (int64_t(blockIdx.x) * blockDim.x + threadIdx.x) >> 4;
-    if (node >= nq) return;                     // whole 16-lane group exits together
+    const int64_t node = int64_t(blockIdx.x) * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    if (node >= nq) return;                      // whole wave
+    // lane l holds elements 4 l + 256 j .. + 3 of the node's row (d <= 768: j < 3)
+    const int nj = (d + 255) >> 8;
     const float* x = emb + (q0 + node) * d;
-    uint64_t keys[16];
-    for (int c = 0; c < 16; ++c) keys[c] = kEmptyKey;
-    for (int c = 0; c < kc && c < 16; ++c) {
-        const uint64_t ck = cand[node * kc + c];
-        const int32_t id = key_id(ck);
-        float acc = 0.0f;
-        if (ck != kEmptyKey) {
-            const float* y = emb + int64_t(id) * d;
-            for (int i = sub; i < d; i += 16) acc = fmaf(x[i], y[i], acc);
-        }
-        acc += __shfl_xor(acc, 8, 16);
-        acc += __shfl_xor(acc, 4, 16);
-        acc += __shfl_xor(acc, 2, 16);
-        acc += __shfl_xor(acc, 1, 16);
-        keys[c] = (ck != kEmptyKey) ? make_key(acc, uint32_t(id)) : kEmptyKey;
+    f32x4 xr[kRerankPieces];
+#pragma unroll
+    for (int j = 0; j < kRerankPieces; ++j) {
+        const int i = 256 * j + 4 * lane;
+        xr[j] = (j < nj && i < d) ? *reinterpret_cast<const f32x4*>(x + i) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     }
-    if (sub == 0) {
+    uint64_t keys[16];
+#pragma unroll
+    for (int c = 0; c < 16; ++c) keys[c] = kEmptyKey;
+    const int nc = kc < 16 ? kc : 16;
+    // four candidates at a time: their rows read in 1 KB pieces, one fmaf chain per lane and
+    // candidate, then a butterfly over the wave (lane 0's association is the one kept)
+    for (int c0 = 0; c0 < nc; c0 += 4) {
+        uint64_t ck[4];
+        float acc[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            ck[u] = c0 + u < nc ? cand[node * kc + c0 + u] : kEmptyKey;
+            const float* y = ck[u] != kEmptyKey ? emb + int64_t(key_id(ck[u])) * d : x;
+            acc[u] = 0.0f;
+#pragma unroll
+            for (int j = 0; j < kRerankPieces; ++j) {
+                const int i = 256 * j + 4 * lane;
+                if (j < nj && i < d) {
+                    const f32x4 yv = *reinterpret_cast<const f32x4*>(y + i);
+                    acc[u] = fmaf(xr[j].x, yv.x, acc[u]);
+                    acc[u] = fmaf(xr[j].y, yv.y, acc[u]);
+                    acc[u] = fmaf(xr[j].z, yv.z, acc[u]);
+                    acc[u] = fmaf(xr[j].w, yv.w, acc[u]);
+                }
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+#pragma unroll
+            for (int m = 32; m >= 1; m >>= 1) acc[u] += __shfl_xor(acc[u], m);
+            if (c0 + u < nc) keys[c0 + u] = ck[u] != kEmptyKey ? make_key(acc[u], uint32_t(key_id(ck[u]))) : kEmptyKey;
+        }
+    }
+    if (lane == 0) {
         for (int i = 1; i < 16; ++i) {           // insertion sort of 16 keys
             const uint64_t v = keys[i];
             int j = i - 1;
@@ -317,7 +342,7 @@ __global__ __launch_bounds__(256) void k_knn_rerank(const float* __restrict__ em
                 const double e32 = double(__uint_as_float(nrm[0]));
                 const double e16 = double(__uint_as_float(nrm[1]));
                 const double de = double(__uint_as_float(nrm[2]));
-                const double u = 0x1p-24, nm = double(d), nf = double(d) / 16.0 + 4.0;
+                const double u = 0x1p-24, nm = double(d), nf = double(4 * nj + 6);
                 const double g_mfma = 2.0 * nm * u / (1.0 - nm * u), g_f32 = nf * u / (1.0 - nf * u);
                 const double eps = (e16 * de + e32 * de + g_mfma * e16 * e16 + g_f32 * e32 * e32 +
                                     u * (e16 * e16 * (1.0 + g_mfma) + e32 * e32 * (1.0 + g_f32))) * 1.01 + 1e-30 * nm;
@@ -401,7 +426,9 @@ int launch_batch_topk(BatchArgs a, int32_t k_out, uint64_t* out, hipStream_t s, 
 
 int launch_knn_rerank(const float* emb, int64_t q0, int64_t nq, int32_t d, const uint64_t* cand, int32_t kc,
                       int32_t k_out, int32_t* nbrs, hipStream_t s, const uint32_t* nrm, int32_t* cert) {
-    const int64_t threads = nq * 16;
+    MARS_CHECK(d >= 4 && d <= 256 * kRerankPieces && d % 4 == 0, MARS_ERR_UNSUPPORTED,
+               "k-NN rescoring: embedding_dim %d not a multiple of 4 up to %d", d, 256 * kRerankPieces);
+    const int64_t threads = nq * 64;
     MARS_LAUNCH(k_knn_rerank, dim3(unsigned((threads + 255) / 256)), dim3(256), 0, s, emb, q0, nq, d, cand, kc,
                 k_out, nbrs, nrm, cert);
     return MARS_OK;
