@@ -364,3 +364,46 @@ def test_int8_certificate_names_the_fp32_top_k():
         else:
             uncertified += 1
     assert certified >= 20 and uncertified >= 1, (certified, uncertified)
+
+
+def rerank_dot(x, y):
+    """k_knn_rerank's fp32 dot (batch.hip): lane l sums elements 4 l + 256 j .. + 3 in one fmaf
+    chain (j ascending), then lane 0's view of the 64-lane xor butterfly (32, 16, .., 1).
+    fmaf is taken as one rounding of the float64 value a * b + c."""
+    d = x.size
+    lanes = np.zeros(64, F32)
+    for lane in range(64):
+        acc = F32(0)
+        for j in range((d + 255) // 256):
+            i = 256 * j + 4 * lane
+            if i < d:
+                for c in range(4):
+                    acc = F32(np.float64(x[i + c]) * np.float64(y[i + c]) + np.float64(acc))
+        lanes[lane] = acc
+    for m in (32, 16, 8, 4, 2, 1):
+        lanes = (lanes + lanes[np.arange(64) ^ m]).astype(F32)
+    return lanes[0]
+
+
+def test_rerank_dot_within_its_error_bound():
+    """The k-NN certificate charges the rescoring gamma_n |x||y| with n = 4 ceil(d/256) + 6
+    (the longest per-lane fmaf chain plus the six butterfly levels); the emulated kernel
+    arithmetic stays within gamma_n sum |x_i y_i| on rows built for cancellation, at every
+    supported width (384 leaves the upper 32 lanes with one 4-term piece)."""
+    rng = np.random.default_rng(11)
+    for d in (256, 384, 512, 768):
+        n = 4 * ((d + 255) // 256) + 6
+        g = n * U / (1 - n * U)
+        worst = 0.0
+        for t in range(40):
+            x = rng.standard_normal(d).astype(F32)
+            y = rng.standard_normal(d).astype(F32)
+            if t % 2:
+                y = (x * F32(1 + 1e-3) + rng.standard_normal(d).astype(F32) * F32(1e-4)).astype(F32)
+                y[::2] *= F32(-1)                    # large terms of both signs: heavy cancellation
+            exact = float(np.dot(x.astype(np.float64), y.astype(np.float64)))
+            got = float(rerank_dot(x, y))
+            scale = float(np.abs(x.astype(np.float64) * y.astype(np.float64)).sum())
+            assert abs(got - exact) <= g * scale, (d, t, got, exact)
+            worst = max(worst, abs(got - exact) / (g * scale))
+        assert worst > 0.0                           # the emulation rounds somewhere
