@@ -902,7 +902,7 @@ def main() -> int:
                                          scan_kernel_mean_us=bkm, tflops=flops / bkm / 1e6,
                                          mfma_util=flops / bkm / 1e6 / 2500.0,
                                          hbm_gbs=bytes_f16 / bkm / 1e3, hbm_frac=bytes_f16 / bkm / 1e3 / HBM_PEAK_GBS,
-                                         kernel="k_batch_scan" if B <= 128 else ("k_batch_rq" if B < 1024 else "k_batch_mm"))
+                                         kernel="k_batch_scan" if B <= 64 else "k_batch_rq")
             log(f"batch Q={B}: p50 {pctl(bl, .5):.0f} us; scan {bkm:.0f} us = {flops / bkm / 1e6:.0f} TFLOP/s "
                 f"({flops / bkm / 1e6 / 25:.1f}% of 2.5 PF), {bytes_f16 / bkm / 1e3:.0f} GB/s")
         out["episode"] = dict(p50_us=pctl(lat_e, .5), p99_us=pctl(lat_e, .99), qps=S / wall_e,

@@ -602,11 +602,11 @@ int query_impl(const mars_graph* gh, mars_ctx* ch, const float* h_q, const float
 
 // Row ranges x query blocks for the batched scan: one 512-thread workgroup per CU
 // (256 CUs), all query blocks of a row range on one XCD.
-void batch_grid(int64_t n, int32_t q, int32_t* n_rranges, int32_t* n_qblocks, int64_t* rows_per_range,
+void batch_grid(int64_t n, int32_t q, bool plain, int32_t* n_rranges, int32_t* n_qblocks, int64_t* rows_per_range,
                 int32_t max_ranges) {
-    // n_qblocks counts 64-query blocks (the layout of the partial keys) for both kernels
+    // n_qblocks counts 64-query blocks (the layout of the partial keys) for every kernel
     const int32_t qblocks = (q + 63) / 64;
-    const bool gemm = batch_uses_gemm(q), rq = batch_uses_rq(q);
+    const bool gemm = batch_uses_gemm(q, plain), rq = batch_uses_rq(q, plain);
     const int32_t wgq = gemm ? 256 : (rq ? 64 * batch_rq_tiles(q) : 64);   // queries per workgroup
     const int32_t tiles = (q + wgq - 1) / wgq;                             // workgroups per row range
     const int64_t align = gemm ? 256 : 16;                            // rows per tile
@@ -1522,7 +1522,7 @@ int mars_query_batch(const mars_graph* gh, mars_ctx* ch, const float* dq, int32_
     const int32_t n_live = __atomic_load_n(&g.n, __ATOMIC_ACQUIRE);
     int32_t nrr = 0, nqb = 0;
     int64_t rpr = 0;
-    batch_grid(n_live, Q, &nrr, &nqb, &rpr);
+    batch_grid(n_live, Q, false, &nrr, &nqb, &rpr);
     const int32_t kp = batch_kpart(K);
     MARS_TRY(ensure_batch_scratch(c, Q, int64_t(nqb) * nrr * 64 * kp));
     hipStream_t s = c.stream;
@@ -1709,7 +1709,7 @@ int global_batch_impl(const mars_graph* gh, mars_ctx* ch, const float* dq, int32
         } else {
             int32_t nrr = 0, nqb = 0;
             int64_t rpr = 0;
-            batch_grid(n_live, Qt, &nrr, &nqb, &rpr);
+            batch_grid(n_live, Qt, Qg == 0, &nrr, &nqb, &rpr);   // the k-NN queries alone: plain
             const int32_t kp = batch_kpart(kMultiCand);
             MARS_TRY(ensure_batch_scratch(c, Qt, int64_t(nqb) * nrr * 64 * kp));
             if (Qg > 0) {
@@ -1963,7 +1963,7 @@ int mars_graph_knn_blocks(mars_graph* gh, int32_t k, int32_t block_rows, int32_t
     if (hi <= lo) return MARS_OK;
     int32_t nrr = 0, nqb = 0;
     int64_t rpr = 0;
-    batch_grid(B, kChunk, &nrr, &nqb, &rpr);         // the largest block sizes the scratch
+    batch_grid(B, kChunk, true, &nrr, &nqb, &rpr);   // the largest block sizes the scratch
     float* tq = nullptr; uint64_t* part = nullptr; uint64_t* cand = nullptr; int32_t* dn = nullptr;
     int32_t* cert = nullptr;
     hipStream_t s = nullptr;
@@ -1985,7 +1985,7 @@ int mars_graph_knn_blocks(mars_graph* gh, int32_t k, int32_t block_rows, int32_t
     // block [r0, r1): rows, queries and candidate ids relative to r0
     for (int64_t r0 = lo; r0 < hi && rc == MARS_OK; r0 += B) {
         const int64_t nb = std::min<int64_t>(B, g.n - r0);
-        batch_grid(nb, kChunk, &nrr, &nqb, &rpr);
+        batch_grid(nb, kChunk, true, &nrr, &nqb, &rpr);
         for (int64_t q0 = 0; q0 < nb && rc == MARS_OK; q0 += kChunk) {
             const int32_t q = int32_t(std::min<int64_t>(kChunk, nb - q0));
             BatchArgs a{};
@@ -2036,7 +2036,7 @@ int mars_graph_knn_range(mars_graph* gh, int32_t k, int32_t first, int32_t count
     const int64_t n = g.n;
     int32_t nrr = 0, nqb = 0;
     int64_t rpr = 0;
-    batch_grid(n, kChunk, &nrr, &nqb, &rpr);
+    batch_grid(n, kChunk, true, &nrr, &nqb, &rpr);
     float* tq = nullptr; uint64_t* part = nullptr; uint64_t* cand = nullptr; int32_t* dn = nullptr;
     int32_t* cert = nullptr;
     hipStream_t s = nullptr;

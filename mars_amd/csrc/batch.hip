@@ -367,8 +367,9 @@ int launch_batch_t(const BatchArgs& a, hipStream_t s) {
 
 template <int K>
 int launch_batch_k(const BatchArgs& a, hipStream_t s) {
-    if (batch_uses_rq(a.q)) return launch_batch_rq(a, s);
-    if (batch_uses_gemm(a.q)) return launch_batch_mm(a, s);
+    const bool plain = a.q_plain == 0;
+    if (batch_uses_rq(a.q, plain)) return launch_batch_rq(a, s);
+    if (batch_uses_gemm(a.q, plain)) return launch_batch_mm(a, s);
     MARS_CHECK(a.floor_keys == nullptr, MARS_ERR_INVALID, "k_batch_scan takes no score floor");
     switch (a.d / 32) {
         case 8: return launch_batch_t<8, K>(a, s);
@@ -382,8 +383,8 @@ int launch_batch_k(const BatchArgs& a, hipStream_t s) {
 }  // namespace
 
 bool batch_dim_supported(int32_t d) { return d == 256 || d == 384 || d == 512 || d == 768; }
-bool batch_uses_gemm(int32_t q) { return q >= kGemmMinQ; }
-bool batch_uses_rq(int32_t q) { return q > kRqMaxScanQ && q < kGemmMinQ; }
+bool batch_uses_gemm(int32_t q, bool plain) { return plain && q >= kGemmMinQ; }
+bool batch_uses_rq(int32_t q, bool plain) { return q > kRqMaxScanQ && !batch_uses_gemm(q, plain); }
 int batch_rq_tiles(int32_t q) { return q <= 128 ? 2 : 4; }
 int batch_kpart(int32_t k) { return k <= 8 ? 8 : 16; }
 
@@ -410,7 +411,7 @@ int launch_batch_topk(BatchArgs a, int32_t k_out, uint64_t* out, hipStream_t s, 
     // The floor pays where a range is long: without it a query inserts about
     // K (1 + ln(rows / K)) rows per range (every new best of the rows seen so far), with
     // it about rows x K / sampled rows.
-    if ((batch_uses_rq(a.q) || batch_uses_gemm(a.q)) && a.rows_per_range >= kSampleDiv * kSampleRowsMin) {
+    if (a.q > kRqMaxScanQ && a.rows_per_range >= kSampleDiv * kSampleRowsMin) {
         BatchArgs b = a;
         b.rows_per_range = std::min<int64_t>(kSampleRowsMax, a.rows_per_range / kSampleDiv / 16 * 16);
         b.range_stride = a.rows_per_range;

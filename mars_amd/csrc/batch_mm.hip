@@ -1,6 +1,7 @@
 // ============================================================================
-//  batch_mm.hip — k_batch_mm: batched scoring for Q >= kGemmMinQ queries, the
-//  shared corpus pass of large query batches and of the k-NN graph builder.
+//  batch_mm.hip — k_batch_mm: the neighbour searches of the k-NN builders, batches of
+//  Q >= kGemmMinQ queries that are corpus rows (the score is the plain dot product and
+//  the query's own row is excluded).
 //
 //  C = E_tile x Q_tile^T for 256 corpus rows x 256 queries per tile on
 //  v_mfma_f32_32x32x16_f16 (fp16 operands, fp32 accumulation). Four waves, one per
@@ -18,15 +19,14 @@
 //  pieces in the next, so every fragment read is one base register plus an immediate.
 //
 //  Selection: thread t, the owner of query q0 + t, keeps its best K keys in registers.
-//  Once every list is full, the owners publish a threshold per query (their K-th score;
-//  a fused score f = dot x w with w in [0, 1] can reach it only if the raw dot does),
-//  and after a tile each lane offers the (query, row) pairs of its accumulators at or
-//  above their query's threshold into 16 slots per query in the free stage buffer; the
-//  owners then fuse and insert their few candidates (the slot selection). A tile where
-//  some query gets more than 16 candidates, and every tile before the thresholds, goes
-//  the full way instead: the raw accumulators pass through the free stage buffer 32
-//  rows at a time ([query][row], 16-byte writes and reads) and the owners test all of
-//  their scores. Output: K keys per (query, row range) in the layout k_batch_merge reads.
+//  Before each tile the owners publish a threshold per query (the larger of its sampled
+//  floor and, once its list is full, its K-th score); after the tile each lane tests its
+//  accumulators against it and offers the few (query, row) pairs that reach it into 8
+//  slots per query in the free stage buffer, and the owners insert those (the slot
+//  selection). A tile where a query has no threshold or more candidates than slots goes
+//  the full way instead: the raw accumulators pass through the free stage buffer 32 rows
+//  at a time ([query][row], 16-byte writes and reads) and the owners test all of their
+//  scores. Output: K keys per (query, row range) in the layout k_batch_merge reads.
 // ============================================================================
 #include "device.hpp"
 
@@ -53,8 +53,6 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 struct MmLds {
     u32x4 e[kMB][kMR * 4];      // 4 x 16 KiB: 256 rows x 4 pieces per stage
     u32x4 q[kMB][kMQ * 4];      // 4 x 16 KiB: 256 queries x 4 pieces per stage
-    float w[kMR];               // row decay weight (one query time) or row timestamp
-    uint32_t keepm[kMR / kMChunk];   // bit j of word c: row 32 c + j passes the modality filter
     float thr[kMQ];             // per query: raw dot products below it cannot enter its list
     uint32_t cnt[kMQ];          // per query: candidates offered in this tile
     uint32_t rhdr[kMThreads / 64][kMRec];  // per record: query << 8 | first row of the lane's 16
@@ -100,7 +98,6 @@ void k_batch_mm(BatchArgs a) {
     const int64_t r0 = int64_t(r_id) * (a.range_stride > 0 ? a.range_stride : a.rows_per_range);
     const int64_t r1 = (a.n < r0 + a.rows_per_range) ? a.n : r0 + a.rows_per_range;
     const int64_t ntiles = r1 > r0 ? (r1 - r0 + kMR - 1) / kMR : 0;
-    const bool uni = a.uniform_tq != 0;
 
     // Stage loads go straight from global memory to LDS (global_load_lds_dwordx4): load
     // j of a wave fills 64 consecutive 16-byte slots, s = (wave * kMDma + j) * 64 + lane,
@@ -141,9 +138,7 @@ void k_batch_mm(BatchArgs a) {
 #pragma unroll
     for (int j = 0; j < K; ++j) list[j] = kEmptyKey;
     const int my_q = q0 + tid;
-    const bool my_plain = my_q >= a.q_plain;
-    const int64_t my_self = (a.self_base >= 0 && my_plain) ? a.self_base + (my_q - a.q_plain) : -1;
-    const float my_tq = my_q < a.q ? a.tq[my_q] : 0.0f;
+    const int64_t my_self = a.self_base >= 0 ? a.self_base + my_q : -1;   // the query's own row
     // the sampled score floor (a lower bound of the query's final floor_k-th best score): no
     // row below it can be among the query's results, so none is kept
     float my_floor = -INFINITY;
@@ -152,19 +147,7 @@ void k_batch_mm(BatchArgs a) {
         if (fk != kEmptyKey) my_floor = key_score(fk);
     }
 
-    // row attributes (timestamp, modality) of the next tile, one tile ahead
-    const float tq0 = a.tq[0];
-    float p_ts = 0.0f;
-    int32_t p_mod = 0;
-    auto load_attr = [&](int64_t tile) {
-        tile = tile < ntiles ? tile : ntiles - 1;
-        int64_t row = r0 + tile * kMR + tid;
-        row = row < r1 ? row : r1 - 1;
-        p_ts = a.ts[row];
-        p_mod = a.mods[row];
-    };
     if (ntiles > 0) {
-        load_attr(0);
         issue_stage(0, 0);
         issue_stage(0, 1);
         issue_stage(0, 2);
@@ -222,24 +205,15 @@ void k_batch_mm(BatchArgs a) {
     float* const wbase = wq ? stg_hi : stg_lo;                      // this wave's 128 queries
     const float* const obase = (tid < 128 ? stg_lo : stg_hi) + (tid & 127) * kMChunk;
     const int oswz = (tid >> 1) & 7;
-    // decay weights expf(-lambda max(0, dt)) lie in [0, 1] (up to expf's error) for a
-    // finite lambda >= 0
-    const bool weights_ok = a.lambda >= 0.0f && a.lambda < INFINITY;
     // The owner's threshold for the next tile: the larger of its floor and, once its list is
-    // full, its K-th score s; a row below it cannot enter the list. Neighbour searches
-    // compare the dot itself. Fused scores f = fl(dot x w), filtered rows -FLT_MAX: with
-    // decay weights w <= 1 + 2^-22 (expf of a non-positive argument, within a few ulps of
-    // its value in [0, 1]) and s > 0, a dot below s (1 - 2^-20) gives f < s, so the
-    // threshold is s (1 - 2^-20). Without a threshold (no floor, list not full; or fused
-    // scores with s <= 0) the wave's tiles go the full way. Queries past the batch offer
-    // nothing.
+    // full, its K-th score; a dot below it cannot enter the list. Without either the wave's
+    // tiles go the full way. Queries past the batch offer nothing.
     auto publish = [&]() {
         float th = INFINITY;
         bool ok = true;
         if (my_q < a.q) {
             th = fmaxf(list[K - 1] != kEmptyKey ? key_score(list[K - 1]) : -INFINITY, my_floor);
-            ok = th > -INFINITY && (my_plain || (weights_ok && th > 0.0f));
-            if (!my_plain) th *= 1.0f - 0x1p-20f;
+            ok = th > -INFINITY;
         }
         int ut = tid;
         asm volatile("" : "+v"(ut));
@@ -261,59 +235,27 @@ void k_batch_mm(BatchArgs a) {
                     float4{ac[qt][4 * g], ac[qt][4 * g + 1], ac[qt][4 * g + 2], ac[qt][4 * g + 3]};
         }
     };
-    // The fused score: dot * w in the reference's order, filtered rows -FLT_MAX, neighbour
-    // searches (plain queries) the plain dot product. fuse_row is the single-row form of
-    // the chunk loop in select_chunk: the same operations, so the same bits.
-    auto fuse_row = [&](float x, float wv, uint32_t keep) {
-        float f;
-        if (uni) f = x * wv;
-        else if (a.lambda != 0.0f) f = x * expf(-a.lambda * fmaxf(0.0f, my_tq - wv));
-        else f = x;
-        f = keep ? f : -FLT_MAX;
-        return my_plain ? x : f;
-    };
-    // The owner's pass over chunk c of the tile at row t0: its 32 raw scores, the rows'
-    // weights and filter bits, then the rows that can enter its list.
+    // The owner's pass over chunk c of the tile at row t0: its 32 dots, then the rows that
+    // can enter its list.
     auto select_chunk = [&](int c, int64_t t0) {
-        float x[kMChunk], wv[kMChunk];
-        const float* const wc = sh.w + c * kMChunk;
+        float x[kMChunk];
 #pragma unroll
         for (int s4 = 0; s4 < kMChunk / 4; ++s4) {
             const float4 v4 = *reinterpret_cast<const float4*>(obase + (s4 ^ oswz) * 4);
-            const float4 w4 = *reinterpret_cast<const float4*>(wc + 4 * s4);
             x[4 * s4] = v4.x; x[4 * s4 + 1] = v4.y; x[4 * s4 + 2] = v4.z; x[4 * s4 + 3] = v4.w;
-            wv[4 * s4] = w4.x; wv[4 * s4 + 1] = w4.y; wv[4 * s4 + 2] = w4.z; wv[4 * s4 + 3] = w4.w;
-        }
-        const uint32_t km = sh.keepm[c];
-        float sc[kMChunk];
-        if (uni) {
-#pragma unroll
-            for (int j = 0; j < kMChunk; ++j) sc[j] = x[j] * wv[j];
-        } else if (a.lambda != 0.0f) {
-#pragma unroll
-            for (int j = 0; j < kMChunk; ++j) sc[j] = x[j] * expf(-a.lambda * fmaxf(0.0f, my_tq - wv[j]));
-        } else {
-#pragma unroll
-            for (int j = 0; j < kMChunk; ++j) sc[j] = x[j];
         }
         // rows at or above the K-th score held and the floor (NaN passes to the key test)
         const float bound = fmaxf(list[K - 1] != kEmptyKey ? key_score(list[K - 1]) : -INFINITY, my_floor);
         uint32_t pass = 0u;
 #pragma unroll
-        for (int j = 0; j < kMChunk; ++j) {
-            float f = ((km >> j) & 1u) ? sc[j] : -FLT_MAX;
-            f = my_plain ? x[j] : f;
-            pass |= uint32_t(!(f < bound)) << j;
-        }
+        for (int j = 0; j < kMChunk; ++j) pass |= uint32_t(!(x[j] < bound)) << j;
         const int64_t rbase = t0 + c * kMChunk;
         if (rbase + kMChunk > r1) pass &= (r1 > rbase) ? (0xFFFFFFFFu >> (kMChunk - int(r1 - rbase))) : 0u;
         if (my_self >= rbase && my_self < rbase + kMChunk) pass &= ~(1u << int(my_self - rbase));
         while (pass) {
             const int j = __builtin_ctz(pass);
             pass &= pass - 1u;
-            // row j's score again, from its raw score in the staging
-            const float v = fuse_row(obase[((j >> 2) ^ oswz) * 4 + (j & 3)], wc[j], (km >> j) & 1u);
-            const uint64_t key = make_key(v, uint32_t(rbase + j));
+            const uint64_t key = make_key(obase[((j >> 2) ^ oswz) * 4 + (j & 3)], uint32_t(rbase + j));
             if (key < list[K - 1]) reg_insert<K>(list, key);
         }
     };
@@ -321,15 +263,6 @@ void k_batch_mm(BatchArgs a) {
     publish();                                     // the first tile's thresholds (floors)
     for (int64_t t = 0; t < ntiles; ++t) {
         const int64_t t0 = r0 + t * kMR;
-        {
-            const uint64_t km = __ballot((a.mod_filter < 0 || p_mod == a.mod_filter) ? 1 : 0);
-            if (lane == 0) {
-                sh.keepm[2 * wave] = uint32_t(km);
-                sh.keepm[2 * wave + 1] = uint32_t(km >> 32);
-            }
-        }
-        sh.w[tid] = !uni ? p_ts : (a.lambda != 0.0f ? expf(-a.lambda * fmaxf(0.0f, tq0 - p_ts)) : 1.0f);
-        load_attr(t + 1);
 #pragma unroll
         for (int rt = 0; rt < 4; ++rt)
 #pragma unroll
@@ -356,12 +289,12 @@ void k_batch_mm(BatchArgs a) {
         if (!full_way) {
             // Slot selection, in three steps.
             // 1. Each lane tests its 16 dots of each 32 x 32 block at once: their maximum
-            //    against the query's threshold, and x * 0, NaN exactly for a NaN or infinite
-            //    dot (offered, as the full way offers NaN). A lane that reaches it appends
+            //    (NaN ignored) against the query's threshold, and their sum, NaN when a dot
+            //    is NaN (offered, as the full way offers NaN). A lane that reaches it appends
             //    the block's 16 dots to its wave's records (ballot compaction).
             // 2. The wave's lanes take one record each and offer every dot not below the
             //    threshold: a slot index from the query's counter, then (row, dot).
-            // 3. The owners fuse and insert their candidates.
+            // 3. The owners insert their candidates.
             // More than kMRec records in a wave or kMSlots candidates for a query: the tile
             // goes the full way. The lane index is laundered so that the addresses and rows
             // derived from it are computed here rather than held across the tile loop.
@@ -458,8 +391,7 @@ void k_batch_mm(BatchArgs a) {
                         const int j = int(sl.x);
                         const int64_t row = t0 + j;
                         if (row >= r1 || row == my_self) continue;
-                        const float f = fuse_row(__uint_as_float(sl.y), sh.w[j], (sh.keepm[j >> 5] >> (j & 31)) & 1u);
-                        const uint64_t key = make_key(f, uint32_t(row));
+                        const uint64_t key = make_key(__uint_as_float(sl.y), uint32_t(row));
                         if (key < list[K - 1]) reg_insert<K>(list, key);
                     }
                 }
@@ -516,11 +448,13 @@ int launch_mm_k(const BatchArgs& a, hipStream_t s) {
 }  // namespace
 
 int launch_batch_mm(const BatchArgs& a, hipStream_t s) {
-    MARS_CHECK(a.k >= 1 && a.k <= 16, MARS_ERR_UNSUPPORTED, "batched scoring keeps at most 16 per query (asked %d)",
-               a.k);
+    // the k-NN builders keep 16 candidates per query and row range (batch_kpart(k) = 16)
+    MARS_CHECK(a.k > 8 && a.k <= 16, MARS_ERR_UNSUPPORTED, "k_batch_mm keeps 16 keys per query (asked %d)", a.k);
+    MARS_CHECK(a.q_plain == 0, MARS_ERR_INVALID, "k_batch_mm scores neighbour searches only (%d of %d queries fused)",
+               a.q_plain, a.q);
     MARS_CHECK(a.floor_keys == nullptr || (a.floor_k >= 1 && a.floor_k <= 16), MARS_ERR_INVALID,
                "batched scoring: floor of %d keys per query", a.floor_k);
-    return a.k <= 8 ? launch_mm_k<8>(a, s) : launch_mm_k<16>(a, s);
+    return launch_mm_k<16>(a, s);
 }
 
 }  // namespace mars

@@ -290,7 +290,7 @@ int insert_knn_fp16(Graph& g, int64_t first, int32_t nq, int64_t n, int32_t k, h
     const int32_t ranges = n <= kInsertKnnNarrowRows ? kInsertKnnRanges : 256;
     for (int32_t q : {std::min(nq, kInsertChunk), nq % kInsertChunk}) {   // full and last chunk
         if (q == 0) continue;
-        batch_grid(n, q, &nrr, &nqb, &rpr, ranges);
+        batch_grid(n, q, true, &nrr, &nqb, &rpr, ranges);
         part_keys = std::max<int64_t>(part_keys, int64_t(nrr) * nqb * 64 * kKnnCand);
     }
     if (part_keys > g.ins_part_cap) {
@@ -312,7 +312,7 @@ int insert_knn_fp16(Graph& g, int64_t first, int32_t nq, int64_t n, int32_t k, h
     }
     for (int32_t c0 = 0; c0 < nq; c0 += kInsertChunk) {
         const int32_t q = std::min(kInsertChunk, nq - c0);
-        batch_grid(n, q, &nrr, &nqb, &rpr, ranges);
+        batch_grid(n, q, true, &nrr, &nqb, &rpr, ranges);
         BatchArgs a{};
         a.emb16 = g.emb16; a.n = n; a.d = g.d; a.qh = g.emb16 + (first + c0) * g.d; a.q = q; a.tq = g.ins_tq;
         a.ts = g.ts; a.mods = g.mods; a.lambda = 0.0f; a.mod_filter = -1; a.k = kKnnCand;

@@ -83,9 +83,10 @@ void dfree(T*& p) {
     p = nullptr;
 }
 
-// Row ranges x query blocks of the batched scan (defined in api.hip).
-// max_ranges caps the row ranges (workgroups per 64-query block).
-void batch_grid(int64_t n, int32_t q, int32_t* n_rranges, int32_t* n_qblocks, int64_t* rows_per_range,
+// Row ranges x query blocks of the batched scan (defined in api.hip). plain: every query
+// is a neighbour search (BatchArgs::q_plain == 0), which picks the kernel as in
+// batch_uses_gemm. max_ranges caps the row ranges (workgroups per 64-query block).
+void batch_grid(int64_t n, int32_t q, bool plain, int32_t* n_rranges, int32_t* n_qblocks, int64_t* rows_per_range,
                 int32_t max_ranges = 256);
 
 constexpr int kMaxK = 64;              // seeds per query (wave-held list), as MAX_TOP_K
@@ -527,21 +528,26 @@ struct BatchArgs {
     int32_t uniform_tq;      // all query times equal: one decay weight per row
 };
 bool batch_dim_supported(int32_t d);
-// Three kernels score a batch, by its size (1M rows, d = 768, one MI355X):
+// Three kernels score a batch, by its size and kind (1M rows, d = 768, one MI355X):
 //   Q <= kRqMaxScanQ              k_batch_scan: 64-query blocks, rows streamed into
 //                                 registers (Q = 64: 313 us);
-//   kRqMaxScanQ < Q < kGemmMinQ   k_batch_rq (batch_rq.hip): the queries held in registers
+//   Q > kRqMaxScanQ               k_batch_rq (batch_rq.hip): the queries held in registers
 //                                 (128 or 256 per workgroup, batch_rq_tiles x 16 per wave),
 //                                 16-row tiles streamed through LDS, a sampled score floor
-//                                 (Q = 256: 628 us, 774 us with the scan);
-//   Q >= kGemmMinQ                k_batch_mm: 256-query x 256-row LDS tiles (the k-NN
-//                                 builder's 1024-query chunks).
+//                                 (Q = 256: 549 us; Q = 1024: 1.80 ms);
+//   neighbour searches, Q >= kGemmMinQ
+//                                 k_batch_mm: 256-query x 256-row LDS tiles, thresholds from
+//                                 the sampled floor (the k-NN builders' 1024-query chunks:
+//                                 1.90 ms, against 2.86 ms through k_batch_rq). With decayed
+//                                 scores its raw-dot thresholds pass far more rows than reach
+//                                 the lists, and k_batch_rq is faster (Q = 1024: 1.80 against
+//                                 2.50 ms).
 // (With 64 queries per workgroup k_batch_rq measured slower than the scan: 445 against
 // 408 us on a random 1M corpus.)
 constexpr int32_t kGemmMinQ = 1024;
 constexpr int32_t kRqMaxScanQ = 64;
-bool batch_uses_gemm(int32_t q);
-bool batch_uses_rq(int32_t q);
+bool batch_uses_gemm(int32_t q, bool plain);
+bool batch_uses_rq(int32_t q, bool plain);
 int batch_rq_tiles(int32_t q);   // 16-query MFMA tiles per k_batch_rq wave: 2 or 4
 int launch_batch_rq(const BatchArgs& a, hipStream_t s);
 int batch_kpart(int32_t k);  // keys per (query, row range) the scan writes

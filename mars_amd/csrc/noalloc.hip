@@ -101,7 +101,7 @@ extern "C" int mars_query_batch_static(const mars_graph* gh, const float* d_quer
     MARS_CHECK(n_live > 0, MARS_ERR_INVALID, "empty graph");
     int32_t nrr = 0, nqb = 0;
     int64_t rpr = 0;
-    batch_grid(n_live, Q, &nrr, &nqb, &rpr);
+    batch_grid(n_live, Q, false, &nrr, &nqb, &rpr);
     const int32_t kp = batch_kpart(K);
     const int64_t part_keys = int64_t(nqb) * nrr * 64 * kp;
     MARS_CHECK(part_keys <= int64_t(kStaticPartKeys), MARS_ERR_CAPACITY,

@@ -2,8 +2,9 @@
 
 Bars:
   * every list of an all-pairs build is exact: the k-NN of 2,000 sampled nodes of the
-    100K benchmark corpus equal the fp64 oracle's up to near-ties (1e-5), and the report
-    says that every node the certificate missed was scanned again exactly;
+    100K benchmark corpus (and 1,000 of a 150K one, whose row ranges take the sampled
+    floors) equal the fp64 oracle's up to near-ties (1e-5), and the report says that every
+    node the certificate missed was scanned again exactly;
   * rows whose neighbours tie (80 copies of one row) miss the certificate, are scanned
     again, and their lists hold copies of the row (score 1, the node itself excluded);
   * a build within blocks counts the nodes the certificate missed and scans none again;
@@ -53,6 +54,22 @@ def test_all_pairs_100k_exact():
         got2 = mars_amd.graph_knn(dg, 8, progress=lambda *_: None, piece=30_000)
         np.testing.assert_array_equal(got2, got)
         assert dg.knn_report == (u, r)
+    finally:
+        mars_amd.free_device(dg)
+
+
+def test_all_pairs_150k_with_floors_exact():
+    """150,000 nodes: row ranges of 2,560 rows, long enough for the sampled pass, so
+    k_batch_mm's thresholds start from its floors; 1,000 sampled nodes against the fp64
+    oracle, up to near-ties, and every list the certificate missed scanned again."""
+    c = corpus.make_corpus(150_000, D, seed=2027, threads=16)
+    dg = device_graph(c.embeddings, c.modalities, c.timestamps)
+    try:
+        got = mars_amd.graph_knn(dg, 8)
+        u, r = dg.knn_report
+        assert r == u and u <= 1500
+        nodes = np.random.default_rng(6).choice(150_000, 1000, replace=False)
+        check_lists(c.embeddings, nodes, got[nodes])
     finally:
         mars_amd.free_device(dg)
 

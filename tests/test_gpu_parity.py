@@ -260,9 +260,9 @@ def test_batch_parity_shapes(dev10k, corpus_10k, q, k, filt, rng):
 @pytest.mark.parametrize("d,k,filt,uniform", [(256, 5, -1, False), (384, 16, 1, True), (512, 8, 2, False),
                                                (768, 3, -1, True)])
 def test_batch_tiled_widths(d, k, filt, uniform, rng):
-    """1,030 queries run the 256-query x 256-row tiled kernel (k_batch_mm): every supported
-    width, both list sizes (K <= 8 and K <= 16), ragged row tiles (2,600 rows), filters and
-    per-query times, against the oracle's top-K."""
+    """1,030 queries (k_batch_rq, five groups of 256 queries per row range, the last with six):
+    every supported width, both list sizes (K <= 8 and K <= 16), ragged row tiles (2,600
+    rows), filters and per-query times, against the oracle's top-K."""
     n = 2600
     emb, mods, ts, row, col, _ = random_graph(rng, n, d)
     dev = Dev(emb, mods, ts, row, col, fp16=True)
@@ -278,13 +278,10 @@ def test_batch_tiled_widths(d, k, filt, uniform, rng):
                                                    (110_000, 4, -1, False, 0.0), (110_000, 8, 2, True, LAM),
                                                    (110_000, 16, -1, False, LAM)])
 def test_batch_tiled_long_ranges(n, k, filt, uniform, lam, rng):
-    """k_batch_mm over long row ranges (1,030 queries): 60,000 rows, ranges of five 256-row
-    tiles, thresholds from the owners' lists after the first tile; 110,000 rows, ranges of
-    2,304 rows, long enough for the sampled pass whose floors give thresholds from the
-    first tile. Most tiles go through the candidate slots, the others (a query with more
-    candidates than slots) the full way; decay per query and per batch, no decay, filters.
-    A quarter of the queries and the six of the last, partial query tile are checked
-    against the oracle's top-K."""
+    """Batches of 1,030 fused-score queries over long row ranges (k_batch_rq): 60,000 rows
+    without the sampled pass, 110,000 rows with it (its floors drop rows from the first
+    tile on); decay per query and per batch, no decay, filters. A quarter of the queries
+    and the six of the last, partial query group are checked against the oracle's top-K."""
     d, q = 256, 1030
     emb, mods, ts, row, col, _ = random_graph(rng, n, d)
     dev = Dev(emb, mods, ts, row, col, fp16=True)
@@ -302,10 +299,12 @@ def test_batch_tiled_long_ranges(n, k, filt, uniform, lam, rng):
         dev.close()
 
 
-def test_knn_tiled_width_384(rng):
-    """The k-NN builder (plain dot products, the node itself excluded) at width 384
-    against the exact CPU k-NN; differing neighbours must be near-ties with the 8th."""
-    n, d = 1500, 384
+@pytest.mark.parametrize("d", [256, 384, 512])
+def test_knn_tiled_widths(d, rng):
+    """The k-NN builder (plain dot products, the node itself excluded) at the other widths
+    against the exact CPU k-NN: the first 1,024 nodes through k_batch_mm, the other 476
+    through k_batch_rq; differing neighbours must be near-ties with the 8th."""
+    n = 1500
     emb, mods, ts, _, _, _ = random_graph(rng, n, d)
     dev = Dev(emb, mods, ts, None, None, fp16=True)
     try:
