@@ -668,11 +668,12 @@ def main() -> int:
         knn = mars_amd.graph_knn(dg, args.knn_k, args.knn_block,
                                  knn_progress if (args.knn_block or big) else None)
         knn_unc, knn_res = getattr(dg, "knn_report", (0, 0))
+        knn_s = time.time() - t
         log(f"{args.knn_k}-NN on the GPU" + (f" (blocks of {args.knn_block} ids)" if args.knn_block else "") +
-            f": {time.time() - t:.1f}s; {N - knn_unc:,} of {N:,} lists certified exact, {knn_res:,} scanned again")
+            f": {knn_s:.1f}s; {N - knn_unc:,} of {N:,} lists certified exact, {knn_res:,} scanned again")
     else:
         knn = np.empty((N, 0), np.int32)
-        knn_unc, knn_res = 0, 0
+        knn_unc, knn_res, knn_s = 0, 0, 0.0
         log("NSN graph without k-NN edges (intra-episode pairs only)")
     t = time.time()
     corpus.nsn_graph(c, knn)
@@ -978,6 +979,7 @@ def main() -> int:
                    "num_nodes": N, "dim": D, "top_k": K, "bfs_hops": 2, "decay_lambda": corpus.DECAY_LAMBDA,
                    "corpus_seed": args.seed, "query_seed": args.query_seed, "num_edges": int(len(c.col_indices)),
                    "knn_lists_uncertified": knn_unc, "knn_lists_scanned_again": knn_res,
+                   "knn_build_s": round(knn_s, 3),
                    "nsn_graph": (f"intra-episode pairs + {args.knn_k}-NN" +
                                  (f" within blocks of {args.knn_block} ids" if args.knn_block else "")
                                  if args.knn_k > 0 else "intra-episode pairs only (k-NN edges omitted)")},
