@@ -30,8 +30,6 @@
 // ============================================================================
 #include "device.hpp"
 
-#include <cfloat>
-
 namespace mars {
 namespace {
 
@@ -40,7 +38,7 @@ constexpr int kMR = 256;        // rows per tile
 constexpr int kMK = 32;         // k per LDS stage
 constexpr int kMB = 4;          // LDS stage buffers: stages g + 1 .. g + 3 load while g computes
 constexpr int kMThreads = 256;
-constexpr int kMChunk = 32;     // rows per staged chunk of the first tile
+constexpr int kMChunk = 32;     // rows per staged chunk of the full-way selection
 constexpr int kPartQ = 64;      // queries per block of the partial-key layout
 constexpr int kMDma = 4;        // load instructions per wave and operand per stage
 constexpr int kMSlots = 8;      // candidate slots per query and tile (the slot selection)
@@ -103,8 +101,9 @@ void k_batch_mm(BatchArgs a) {
     // j of a wave fills 64 consecutive 16-byte slots, s = (wave * kMDma + j) * 64 + lane,
     // i.e. slot s & 3 of row s >> 2, which holds piece (s & 3) ^ ((row >> 2) & 3) of the
     // row's 32 k. The fragment reads of 16 consecutive rows (a 16-lane group of a 16-byte
-    // read) then hit the 16 distinct 16-byte bank groups of the 256-byte LDS row. Every stage issues the same loads (rows clamped into range; stages past
-    // the last tile load a clamped tile nobody reads), so the wait counts stay exact.
+    // read) then hit the 16 distinct 16-byte bank groups of the 256-byte LDS row. Every
+    // stage issues the same loads (rows clamped into range; stages past the last tile load
+    // a clamped tile nobody reads), so the wait counts stay exact.
     const int srow = (wave * kMDma) * 16 + (lane >> 2);            // + 16 j
     const int spiece = (lane & 3) ^ ((srow >> 2) & 3);             // the same for every j
     // Addresses: a uniform base (the tile's first row; the query array) plus a 32-bit
