@@ -11,20 +11,20 @@
 //  is read from L2 once per 256 rows.
 //
 //  Operands reach LDS in k-stages of 32 straight from global memory
-//  (global_load_lds_dwordx4, no staging registers), four stage buffers deep: while
-//  stage g computes, stages g + 1 .. g + 3 are in flight. The stage pipeline waits for
-//  its own loads by count (s_waitcnt vmcnt) and meets at plain s_barriers: the
-//  __syncthreads fence would wait for every load in flight, the prefetches included.
-//  Buffer b holds a stage's corpus pieces in the first 64 KiB of LDS and its query
-//  pieces in the next, so every fragment read is one base register plus an immediate.
+//  (global_load_lds_dwordx4, no staging registers) through two rings: five corpus stage
+//  buffers and four query stage buffers. Once stage g's fragments are in registers its
+//  buffers refill, so the rows of stages g + 1 .. g + 5 and the queries of g + 1 .. g + 4
+//  are in flight while stage g's MFMAs run. The stage pipeline waits for its own loads
+//  by count (s_waitcnt vmcnt) and meets at plain s_barriers: the __syncthreads fence
+//  would wait for every load in flight, the prefetches included.
 //
 //  Selection: thread t, the owner of query q0 + t, keeps its best K keys in registers.
 //  Before each tile the owners publish a threshold per query (the larger of its sampled
 //  floor and, once its list is full, its K-th score); after the tile each lane tests its
 //  accumulators against it and offers the few (query, row) pairs that reach it into 8
-//  slots per query in the free stage buffer, and the owners insert those (the slot
+//  slots per query in the tile's last stage buffers, and the owners insert those (the slot
 //  selection). A tile where a query has no threshold or more candidates than slots goes
-//  the full way instead: the raw accumulators pass through the free stage buffer 32 rows
+//  the full way instead: the raw accumulators pass through those buffers 32 rows
 //  at a time ([query][row], 16-byte writes and reads) and the owners test all of their
 //  scores. Output: K keys per (query, row range) in the layout k_batch_merge reads.
 // ============================================================================
@@ -36,7 +36,8 @@ namespace {
 constexpr int kMQ = 256;        // queries per workgroup
 constexpr int kMR = 256;        // rows per tile
 constexpr int kMK = 32;         // k per LDS stage
-constexpr int kMB = 4;          // LDS stage buffers: stages g + 1 .. g + 3 load while g computes
+constexpr int kMBC = 5;         // corpus stage buffers (a ring over the tile loop's stages)
+constexpr int kMBQ = 4;         // query stage buffers
 constexpr int kMThreads = 256;
 constexpr int kMChunk = 32;     // rows per staged chunk of the full-way selection
 constexpr int kPartQ = 64;      // queries per block of the partial-key layout
@@ -46,11 +47,13 @@ constexpr int kMRec = 64;       // per wave and tile: 16-dot records of lanes th
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-// All corpus stages in the first 64 KiB and all query stages in the next, so every
-// fragment read is one base register plus an immediate offset.
+// The corpus stages in the first 80 KiB, the query stages in the next 64 KiB. The rows
+// come from HBM (shared with the three other query tiles of the row range through L2) and
+// get one more stage in flight than the L2-resident queries. (Same-box traces of the 1M
+// k-NN chunks: full pass 1870 us with four buffers of each, 1828 us with this split.)
 struct MmLds {
-    u32x4 e[kMB][kMR * 4];      // 4 x 16 KiB: 256 rows x 4 pieces per stage
-    u32x4 q[kMB][kMQ * 4];      // 4 x 16 KiB: 256 queries x 4 pieces per stage
+    u32x4 e[kMBC][kMR * 4];     // 5 x 16 KiB: 256 rows x 4 pieces per stage
+    u32x4 q[kMBQ][kMQ * 4];     // 4 x 16 KiB: 256 queries x 4 pieces per stage
     float thr[kMQ];             // per query: raw dot products below it cannot enter its list
     uint32_t cnt[kMQ];          // per query: candidates offered in this tile
     uint32_t rhdr[kMThreads / 64][kMRec];  // per record: query << 8 | first row of the lane's 16
@@ -84,7 +87,7 @@ __device__ inline void lds_barrier() {
 template <int NS, int K>
 __global__ __launch_bounds__(kMThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void k_batch_mm(BatchArgs a) {
-    static_assert(NS % kMB == 0, "stages are taken kMB at a time");
+    static_assert(NS > kMBC, "a tile has more stages than the corpus ring");
     __shared__ __attribute__((aligned(16))) MmLds sh;
     const int tid = int(threadIdx.x), lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -114,23 +117,27 @@ void k_batch_mm(BatchArgs a) {
         const int q = q0 + srow + 16 * j;
         qoff[j] = uint32_t(q < a.q ? q : a.q - 1) * uint32_t(d * 2) + uint32_t(spiece * 16);
     }
-    // stage st of tile `tile` (clamped: stages past the last tile load the last one again)
-    auto issue_stage = [&](int tile, int st) {
-        const int b = st & (kMB - 1);              // NS % kMB == 0: a stage's buffer is st % kMB
+    // The loads of stage st of tile `tile` (st >= NS: stage st - NS of the next tile; tiles
+    // past the last load the last one again) into query buffer bq / corpus buffer bc.
+    auto issue_q = [&](int tile, int st, int bq) {
+        if (st >= NS) { ++tile; st -= NS; }
+        const char* const qb = uniform_ptr(reinterpret_cast<const char*>(a.qh) + st * kMK * 2);
+#pragma unroll
+        for (int j = 0; j < kMDma; ++j)
+            __builtin_amdgcn_global_load_lds(qb + qoff[j], &sh.q[bq][(wave * kMDma + j) * 64], 16, 0, 0);
+    };
+    auto issue_c = [&](int tile, int st, int bc) {
+        if (st >= NS) { ++tile; st -= NS; }
         tile = tile < int(ntiles) ? tile : int(ntiles) - 1;
         const int64_t trow = r0 + int64_t(tile) * kMR;
         const char* const tb = uniform_ptr(reinterpret_cast<const char*>(a.emb16 + trow * d) + st * kMK * 2);
-        const char* const qb = uniform_ptr(reinterpret_cast<const char*>(a.qh) + st * kMK * 2);
         const uint32_t last = uint32_t(r1 - 1 - trow < kMR - 1 ? r1 - 1 - trow : kMR - 1);   // rows past r1 - 1 clamp
 #pragma unroll
         for (int j = 0; j < kMDma; ++j) {
             const uint32_t rl = uint32_t(srow + 16 * j) < last ? uint32_t(srow + 16 * j) : last;
             __builtin_amdgcn_global_load_lds(tb + (rl * uint32_t(d * 2) + uint32_t(spiece * 16)),
-                                             &sh.e[b][(wave * kMDma + j) * 64], 16, 0, 0);
+                                             &sh.e[bc][(wave * kMDma + j) * 64], 16, 0, 0);
         }
-#pragma unroll
-        for (int j = 0; j < kMDma; ++j)
-            __builtin_amdgcn_global_load_lds(qb + qoff[j], &sh.q[b][(wave * kMDma + j) * 64], 16, 0, 0);
     };
 
     uint64_t list[K];                              // query q0 + tid
@@ -146,21 +153,32 @@ void k_batch_mm(BatchArgs a) {
         if (fk != kEmptyKey) my_floor = key_score(fk);
     }
 
+    // Every stage issues its loads in one order, the queries kMBQ stages ahead, then the rows
+    // kMBC stages ahead, so the wait counts below are exact in the steady state (and only
+    // stricter in the first stages of the first tile).
     if (ntiles > 0) {
-        issue_stage(0, 0);
-        issue_stage(0, 1);
-        issue_stage(0, 2);
-        issue_stage(0, 3);
+#pragma unroll
+        for (int st = 0; st < kMBQ; ++st) {
+            issue_q(0, st, st);
+            issue_c(0, st, st);
+        }
+#pragma unroll
+        for (int st = kMBQ; st < kMBC; ++st) issue_c(0, st, st);
     }
+    // loads issued after stage g + 1's queries, when stage g waits for them: the rows of
+    // stage g + 2 (issued with them), then two stages of loads
+    constexpr int kStageWait = kMDma * (1 + 2 * (kMBQ - 2));
+    // at a tile's first stage: also the deferred loads issued after the selection
+    constexpr int kTileWait = kMDma * (1 + 2 * (kMBQ - 1));
 
     f32x16 acc[4][4];
     f16x8 fa0[4], fb0[4], fa1[4], fb1[4];          // fragments of k-step 0 / 1 of a stage
-    auto read_frags = [&](int b, int kk, f16x8 (&af)[4], f16x8 (&bf)[4]) {
+    auto read_frags = [&](int bc, int bq, int kk, f16x8 (&af)[4], f16x8 (&bf)[4]) {
         const int pc = (2 * kk + lh) ^ ((lm >> 2) & 3);        // swizzled slot of this lane's piece
 #pragma unroll
         for (int x = 0; x < 4; ++x) {
-            af[x] = __builtin_bit_cast(f16x8, sh.e[b][(wr * 128 + x * 32 + lm) * 4 + pc]);
-            bf[x] = __builtin_bit_cast(f16x8, sh.q[b][(wq * 128 + x * 32 + lm) * 4 + pc]);
+            af[x] = __builtin_bit_cast(f16x8, sh.e[bc][(wr * 128 + x * 32 + lm) * 4 + pc]);
+            bf[x] = __builtin_bit_cast(f16x8, sh.q[bq][(wq * 128 + x * 32 + lm) * 4 + pc]);
         }
     };
     auto mma = [&](const f16x8 (&af)[4], const f16x8 (&bf)[4]) {
@@ -170,39 +188,16 @@ void k_batch_mm(BatchArgs a) {
             for (int qt = 0; qt < 4; ++qt)
                 acc[rt][qt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[rt], bf[qt], acc[rt][qt], 0, 0, 0);
     };
-    // Stage st of tile t (buffer st % kMB), with its k-step-0 fragments already read:
-    //   read k-step 1; MFMAs of k-step 0 (the reads land meanwhile);
-    //   wait for the loads of stage st + 1 (stages st + 2, st + 3 may stay in flight) and
-    //   meet: every wave's loads of st + 1 landed, every wave is done reading stage st;
-    //   refill this buffer with stage st + 4 (the tile's last stage leaves that to after
-    //   the selection, which needs the buffer); read k-step 0 of stage st + 1;
-    //   MFMAs of k-step 1 (the reads land meanwhile).
-    // Every stage issues one stage of loads, so the wait counts stay exact.
-    // (sched_barrier keeps each block of reads ahead of the MFMAs it overlaps: the
-    // scheduler would otherwise sink the reads next to their uses)
-    auto run_stage = [&](int t, int st, int b) {
-        read_frags(b, 1, fa1, fb1);
-        __builtin_amdgcn_sched_barrier(0);
-        mma(fa0, fb0);
-        if (st + 1 < NS) {
-            __builtin_amdgcn_s_waitcnt(wait_vm(2 * 2 * kMDma));
-            lds_barrier();
-            if (st + 4 < NS) issue_stage(t, st + 4);
-            else issue_stage(t + 1, st + 4 - NS);
-            read_frags((b + 1) & (kMB - 1), 0, fa0, fb0);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-        mma(fa1, fb1);
-    };
 
     // Selection staging: a chunk's raw scores as [query][row] fp32, queries 0 .. 127 in the
-    // corpus half of the free stage buffer and 128 .. 255 in its query half. Query q's 32
+    // tile's last corpus stage buffer and 128 .. 255 in its last query stage buffer. Query q's 32
     // rows are eight 16-byte slots; rows 4 s .. 4 s + 3 sit in slot s ^ ((q >> 1) & 7), so
     // the 16-byte writes and reads of 16 consecutive queries hit 16 distinct bank groups.
-    float* const stg_lo = reinterpret_cast<float*>(&sh.e[kMB - 1][0]);
-    float* const stg_hi = reinterpret_cast<float*>(&sh.q[kMB - 1][0]);
-    float* const wbase = wq ? stg_hi : stg_lo;                      // this wave's 128 queries
-    const float* const obase = (tid < 128 ? stg_lo : stg_hi) + (tid & 127) * kMChunk;
+    // (the last stage's buffers of each tile: set before its selection)
+    float* stg_lo = nullptr;
+    float* stg_hi = nullptr;
+    float* wbase = nullptr;                                         // this wave's 128 queries
+    const float* obase = nullptr;
     const int oswz = (tid >> 1) & 7;
     // The owner's threshold for the next tile: the larger of its floor and, once its list is
     // full, its K-th score; a dot below it cannot enter the list. Without either the wave's
@@ -268,20 +263,44 @@ void k_batch_mm(BatchArgs a) {
             for (int qt = 0; qt < 4; ++qt)
 #pragma unroll
                 for (int v = 0; v < 16; ++v) acc[rt][qt][v] = 0.0f;
-        // stage 0's loads (stages 1 .. 3 may stay in flight), then its k-step-0 fragments
-        __builtin_amdgcn_s_waitcnt(wait_vm(3 * 2 * kMDma));
+        // stage 0's buffers (global stage t NS), its loads, then its k-step-0 fragments
+        int bc = int((t * NS) % kMBC), bq = int((t * NS) % kMBQ);
+        __builtin_amdgcn_s_waitcnt(wait_vm(kTileWait));
         lds_barrier();
-        read_frags(0, 0, fa0, fb0);
-#pragma unroll 1
-        for (int st = 0; st < NS; st += kMB) {
-            run_stage(int(t), st, 0);
-            run_stage(int(t), st + 1, 1);
-            run_stage(int(t), st + 2, 2);
-            run_stage(int(t), st + 3, 3);
+        read_frags(bc, bq, 0, fa0, fb0);
+        // Stage st, with its k-step-0 fragments already read:
+        //   read k-step 1; MFMAs of k-step 0 (the reads land meanwhile);
+        //   wait for stage st + 1's loads and meet: every wave's loads of st + 1 landed,
+        //   every wave is done reading stage st; refill stage st's buffers with the queries
+        //   of stage st + kMBQ and the rows of stage st + kMBC (the tile's last stage leaves
+        //   that to after the selection, which needs the buffers); read k-step 0 of st + 1;
+        //   MFMAs of k-step 1 (the reads land meanwhile).
+        // (sched_barrier keeps each block of reads ahead of the MFMAs it overlaps: the
+        // scheduler would otherwise sink the reads next to their uses)
+#pragma unroll 2
+        for (int st = 0; st < NS; ++st) {
+            read_frags(bc, bq, 1, fa1, fb1);
+            __builtin_amdgcn_sched_barrier(0);
+            mma(fa0, fb0);
+            if (st + 1 < NS) {
+                __builtin_amdgcn_s_waitcnt(wait_vm(kStageWait));
+                lds_barrier();
+                issue_q(int(t), st + kMBQ, bq);
+                issue_c(int(t), st + kMBC, bc);
+                bc = bc + 1 == kMBC ? 0 : bc + 1;
+                bq = (bq + 1) & (kMBQ - 1);
+                read_frags(bc, bq, 0, fa0, fb0);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            mma(fa1, fb1);
         }
-        // every wave is done with buffer kMB - 1 (the tile's last stage): the selection's
-        // LDS until the deferred load of the next tile's stage kMB - 1 refills it
+        // every wave is done with the tile's last stage's buffers (bc, bq): the selection's
+        // LDS until the deferred loads refill them
         lds_barrier();
+        stg_lo = reinterpret_cast<float*>(&sh.e[bc][0]);
+        stg_hi = reinterpret_cast<float*>(&sh.q[bq][0]);
+        wbase = wq ? stg_hi : stg_lo;
+        obase = (tid < 128 ? stg_lo : stg_hi) + (tid & 127) * kMChunk;
         // (The order in which rows are offered does not change the result: the list keeps
         // the K least keys of a total order.)
         bool full_way = (sh.wfast[0] & sh.wfast[1] & sh.wfast[2] & sh.wfast[3]) == 0u;
@@ -300,8 +319,8 @@ void k_batch_mm(BatchArgs a) {
             int ut = tid;
             asm volatile("" : "+v"(ut));
             const int ul = ut & 63, ulm = ut & 31;
-            u32x4* const rec = &sh.e[kMB - 1][wave * 4 * kMRec];
-            uint2* const slots = reinterpret_cast<uint2*>(&sh.q[kMB - 1][0]);
+            u32x4* const rec = &sh.e[bc][wave * 4 * kMRec];
+            uint2* const slots = reinterpret_cast<uint2*>(&sh.q[bq][0]);
             const uint32_t rowb = uint32_t(wr * 128 + 4 * (ul >> 5));
             uint32_t nrec = 0;                                          // uniform
             // whether a lane's 16 dots of a block can reach threshold th: their maximum (NaN
@@ -415,7 +434,9 @@ void k_batch_mm(BatchArgs a) {
             }
         }
         publish();                             // the next tile's thresholds
-        issue_stage(int(t) + 1, kMB - 1);      // into the buffer the selection used
+        // the deferred loads, into the buffers the selection used
+        issue_q(int(t), NS - 1 + kMBQ, bq);
+        issue_c(int(t), NS - 1 + kMBC, bc);
     }
     // the last stages' loads (past the last tile) must land before the workgroup ends
     __builtin_amdgcn_s_waitcnt(wait_vm(0));
