@@ -415,6 +415,7 @@ int launch_batch_topk(BatchArgs a, int32_t k_out, uint64_t* out, hipStream_t s, 
         BatchArgs b = a;
         b.rows_per_range = std::min<int64_t>(kSampleRowsMax, a.rows_per_range / kSampleDiv / 16 * 16);
         b.range_stride = a.rows_per_range;
+        b.sample_pass = 1;
         MARS_TRY(launch_batch_scan(b, s));
         MARS_TRY(launch_batch_merge(a.part, a.n_rranges, kp, a.q, k_out, out, s));
         a.floor_keys = out;

@@ -27,6 +27,8 @@
 //  the full way instead: the raw accumulators pass through those buffers 32 rows
 //  at a time ([query][row], 16-byte writes and reads) and the owners test all of their
 //  scores. Output: K keys per (query, row range) in the layout k_batch_merge reads.
+//  The sampled pass that gives the floors keeps no lists: per query and range it writes
+//  the largest dot of each of the 16 row blocks a query's dots fall into (see gmx).
 // ============================================================================
 #include "device.hpp"
 
@@ -254,6 +256,64 @@ void k_batch_mm(BatchArgs a) {
         }
     };
 
+    // The sampled pass (its keys serve only as floors): each lane keeps, per block of the
+    // accumulator layout, the largest dot of its 16 rows of that block over the tiles (rows
+    // past the range and the query's own row left out). A query's 16 maxima per range are
+    // 16 distinct dots of its sampled rows, so their k-th best is at most the k-th best of
+    // those rows: a floor as sound as the best-K lists would give, and far cheaper (no
+    // insertions). gmx[qt * 4 + rt]: block (rt, qt).
+    const bool sample = a.sample_pass != 0;
+    float gmx[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) gmx[i] = -INFINITY;
+    auto sample_tile = [&](int64_t t0) {
+        int ut = tid;
+        asm volatile("" : "+v"(ut));
+        const int ulm = ut & 31, ulh = (ut >> 5) & 1;
+#pragma unroll 1
+        for (int h = 0; h < 8; ++h) {
+            f32x16 x0, x1;
+            switch (h) {
+                case 0: x0 = acc[0][0]; x1 = acc[0][1]; break;
+                case 1: x0 = acc[0][2]; x1 = acc[0][3]; break;
+                case 2: x0 = acc[1][0]; x1 = acc[1][1]; break;
+                case 3: x0 = acc[1][2]; x1 = acc[1][3]; break;
+                case 4: x0 = acc[2][0]; x1 = acc[2][1]; break;
+                case 5: x0 = acc[2][2]; x1 = acc[2][3]; break;
+                case 6: x0 = acc[3][0]; x1 = acc[3][1]; break;
+                default: x0 = acc[3][2]; x1 = acc[3][3]; break;
+            }
+            // dot v of the lane's block is row rb + 8 (v >> 2) + (v & 3)
+            const int64_t rb = t0 + wr * 128 + (h >> 1) * 32 + 4 * ulh;
+            const int64_t lim64 = r1 - rb;
+            const int lim = lim64 < 0 ? 0 : (lim64 > 32 ? 32 : int(lim64));   // offsets below it are in range
+            const int ql0 = wq * 128 + (h & 1) * 64 + ulm;
+            int s0 = -1, s1 = -1;                                             // the queries' own rows
+            if (a.self_base >= 0) {
+                const int64_t o0 = a.self_base + q0 + ql0 - rb, o1 = o0 + 32;
+                s0 = (o0 >= 0 && o0 < 32) ? int(o0) : -1;
+                s1 = (o1 >= 0 && o1 < 32) ? int(o1) : -1;
+            }
+            float m0 = -INFINITY, m1 = -INFINITY;
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int o = 8 * (v >> 2) + (v & 3);
+                m0 = (o < lim && o != s0) ? fmaxf(m0, x0[v]) : m0;
+                m1 = (o < lim && o != s1) ? fmaxf(m1, x1[v]) : m1;
+            }
+            switch (h) {
+                case 0: gmx[0] = fmaxf(gmx[0], m0); gmx[4] = fmaxf(gmx[4], m1); break;
+                case 1: gmx[8] = fmaxf(gmx[8], m0); gmx[12] = fmaxf(gmx[12], m1); break;
+                case 2: gmx[1] = fmaxf(gmx[1], m0); gmx[5] = fmaxf(gmx[5], m1); break;
+                case 3: gmx[9] = fmaxf(gmx[9], m0); gmx[13] = fmaxf(gmx[13], m1); break;
+                case 4: gmx[2] = fmaxf(gmx[2], m0); gmx[6] = fmaxf(gmx[6], m1); break;
+                case 5: gmx[10] = fmaxf(gmx[10], m0); gmx[14] = fmaxf(gmx[14], m1); break;
+                case 6: gmx[3] = fmaxf(gmx[3], m0); gmx[7] = fmaxf(gmx[7], m1); break;
+                default: gmx[11] = fmaxf(gmx[11], m0); gmx[15] = fmaxf(gmx[15], m1); break;
+            }
+        }
+    };
+
     publish();                                     // the first tile's thresholds (floors)
     for (int64_t t = 0; t < ntiles; ++t) {
         const int64_t t0 = r0 + t * kMR;
@@ -303,8 +363,10 @@ void k_batch_mm(BatchArgs a) {
         obase = (tid < 128 ? stg_lo : stg_hi) + (tid & 127) * kMChunk;
         // (The order in which rows are offered does not change the result: the list keeps
         // the K least keys of a total order.)
-        bool full_way = (sh.wfast[0] & sh.wfast[1] & sh.wfast[2] & sh.wfast[3]) == 0u;
-        if (!full_way) {
+        bool full_way = false;
+        if (sample) sample_tile(t0);
+        else full_way = (sh.wfast[0] & sh.wfast[1] & sh.wfast[2] & sh.wfast[3]) == 0u;
+        if (!sample && !full_way) {
             // Slot selection, in three steps.
             // 1. Each lane tests its 16 dots of each 32 x 32 block at once: their maximum
             //    (NaN ignored) against the query's threshold, and their sum, NaN when a dot
@@ -433,14 +495,29 @@ void k_batch_mm(BatchArgs a) {
                 }
             }
         }
-        publish();                             // the next tile's thresholds
+        if (!sample) publish();                // the next tile's thresholds
         // the deferred loads, into the buffers the selection used
         issue_q(int(t), NS - 1 + kMBQ, bq);
         issue_c(int(t), NS - 1 + kMBC, bc);
     }
     // the last stages' loads (past the last tile) must land before the workgroup ends
     __builtin_amdgcn_s_waitcnt(wait_vm(0));
-    if (my_q < a.q) {
+    if (sample) {
+        // query wq 128 + qt 32 + lm gets block (rt, qt)'s maximum in slot wr 8 + lh 4 + rt,
+        // keyed with the block's first row (distinct per slot and range; only the score is used)
+        static_assert(K == 16, "16 block maxima per query and range");
+#pragma unroll
+        for (int qt = 0; qt < 4; ++qt) {
+            const int qg = q0 + wq * 128 + qt * 32 + lm;
+            if (qg < a.q) {
+                uint64_t* out = a.part + ((int64_t(qg / kPartQ) * a.n_rranges + r_id) * kPartQ + (qg % kPartQ)) * K +
+                                wr * 8 + lh * 4;
+#pragma unroll
+                for (int rt = 0; rt < 4; ++rt)
+                    out[rt] = make_key(gmx[qt * 4 + rt], uint32_t(r0 + wr * 128 + rt * 32 + 4 * lh));
+            }
+        }
+    } else if (my_q < a.q) {
         uint64_t* out = a.part + ((int64_t(my_q / kPartQ) * a.n_rranges + r_id) * kPartQ + (my_q % kPartQ)) * K;
 #pragma unroll
         for (int j = 0; j < K; ++j) out[j] = list[j];

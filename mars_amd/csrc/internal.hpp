@@ -526,6 +526,8 @@ struct BatchArgs {
     int32_t n_rranges;
     int32_t n_qblocks;
     int32_t uniform_tq;      // all query times equal: one decay weight per row
+    int32_t sample_pass;     // the sampled pass of launch_batch_topk: its keys serve only as
+                             // floors (k_batch_mm then keeps group maxima, not the best K)
 };
 bool batch_dim_supported(int32_t d);
 // Three kernels score a batch, by its size and kind (1M rows, d = 768, one MI355X):

@@ -74,6 +74,26 @@ def test_all_pairs_150k_with_floors_exact():
         mars_amd.free_device(dg)
 
 
+def test_knn_range_2_2m_multi_tile_floors_exact():
+    """2,200,000 nodes: row ranges of 34,560 rows, whose sampled pass covers 528 rows
+    (three tiles, the last one partial), so k_batch_mm's floors come from block maxima kept
+    over several tiles. The 2,048 query nodes start at range 28's first row, so 528 of them
+    have their own row among the sampled rows. 100 of them against the fp64 oracle, up to
+    near-ties."""
+    n = 2_200_000
+    c = corpus.make_corpus(n, D, seed=2028, threads=16)
+    dg = device_graph(c.embeddings, c.modalities, c.timestamps)
+    try:
+        first = 28 * 34_560
+        got = mars_amd.graph_knn_range(dg, 8, first, 2048)
+        u, r = mars_amd.graph_knn_report(dg)
+        assert r == u and u <= 20
+        idx = np.sort(np.concatenate([np.arange(0, 528, 11), np.random.default_rng(7).choice(np.arange(528, 2048), 52, replace=False)]))
+        check_lists(c.embeddings, first + idx, got[idx])
+    finally:
+        mars_amd.free_device(dg)
+
+
 def test_tied_rows_are_scanned_again():
     c = corpus.make_corpus(6000, D, seed=17)
     emb = c.embeddings.copy()
